@@ -1,0 +1,117 @@
+/*
+ * tsfast_hip.h - C ABI of libtsfast_hip.so, the MI355X (gfx950) scan-family kernels behind
+ * tsfast's scan dispatch layer.
+ *
+ * Conventions (shared by every entry point):
+ *   - sizes are int64_t; tensors are raw device pointers to contiguous row-major buffers in the
+ *     layouts named below; optional tensors are NULL when absent;
+ *   - outputs and workspaces are allocated by the caller (the Python shim allocates them with
+ *     torch.empty on the caller's device); the library never allocates device memory;
+ *   - `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream); every
+ *     launch is asynchronous on that stream, with no host synchronisation, so calls can be
+ *     captured in a HIP graph;
+ *   - the return value is a status: TSF_OK (0) on success, a negative TSF_ERR_* code otherwise;
+ *     tsfast_hip_status_string() names it (for TSF_ERR_HIP, with the HIP runtime's message).
+ *
+ * Complex tensors are interleaved (re, im) float pairs, i.e. torch.view_as_real layout.
+ * bf16 tensors are raw 16-bit bfloat16 words (torch.bfloat16 storage).
+ */
+#ifndef TSFAST_HIP_H
+#define TSFAST_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSF_OK 0
+#define TSF_ERR_ARG (-1)         /* a size or pointer argument is invalid */
+#define TSF_ERR_WORKSPACE (-2)   /* workspace missing or smaller than the *_workspace_bytes query */
+#define TSF_ERR_UNSUPPORTED (-3) /* shape outside what the kernels are built for (e.g. N > 64) */
+#define TSF_ERR_HIP (-4)         /* a HIP runtime call or kernel launch failed */
+
+#define TSF_DTYPE_F32 0
+#define TSF_DTYPE_BF16 1
+
+const char* tsfast_hip_status_string(int status);
+/* Library version, for the Python loader's sanity check. */
+int tsfast_hip_version(void);
+
+/* ------------------------------------------------------------------------------------------
+ * Constant-coefficient diagonal scan  x_t = lam * x_{t-1} + v_t  and its adjoint.
+ * Replaces the backend contract of tsfast/models/_core/scan_backends/diagonal_triton.py:255-305
+ * (forward(lam, v, x0) / backward(g, lam, out, x0)), reached from the tsfast::scan_diagonal ops
+ * (tsfast/models/_core/scan.py:100-154).
+ * Layout: lam [M, N], v/out/g/gv [M, L, N], x0/gx0/glam [M, N]; float32 or complex64.
+ */
+int64_t tsfast_hip_diag_workspace_bytes(int64_t M, int64_t L, int64_t N, int is_complex);
+int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const void* lam, const void* v,
+                        const void* x0, void* out, void* workspace, int64_t workspace_bytes, void* stream);
+/* glam = sum_t G_t conj(x_{t-1}), gv = G, gx0 = conj(lam) G_0 (gx0 required iff x0 given). */
+int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const void* g, const void* lam,
+                        const void* out, const void* x0, void* gv, void* glam, void* gx0, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Time-varying (selective) diagonal scan  x_t = a_t * x_{t-1} + v_t  and its adjoint, float32.
+ * Replaces tsfast/models/_core/scan_backends/selective_triton.py:112-160 (forward / backward),
+ * reached from the tsfast::scan_selective ops (tsfast/models/_core/scan.py:157-215).
+ * Layout: a/v/out/g/gv/glam [M, L, N], x0/gx0 [M, N].
+ */
+int64_t tsfast_hip_sel_workspace_bytes(int64_t M, int64_t L, int64_t N);
+int tsfast_hip_sel_fwd(int64_t M, int64_t L, int64_t N, const float* a, const float* v, const float* x0, float* out,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+/* glam_t = G_t x_{t-1}, gv = G, gx0 = a_0 G_0 (gx0 required iff x0 given). */
+int tsfast_hip_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const float* a, const float* out,
+                       const float* x0, float* glam, float* gv, float* gx0, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Fused Mamba selective SSM (softplus discretisation, exp(delta A), input injection, recurrence,
+ * C contraction, D skip, SiLU gate):
+ *   h_t = exp(softplus(draw_t) A) h_{t-1} + softplus(draw_t) u_t B_t
+ *   out_t = (h_t . C_t + Dp u_t) * z_t * sigmoid(z_t)
+ * Replaces the kernels behind tsfast/models/architectures/mamba/mamba_triton.py:286-489
+ * (tsfast::mamba_scan / mamba_scan_train / mamba_scan_bwd) and the C ABI of
+ * tsfast/models/architectures/mamba/backend_c.py:105-245 (mamba_fwd / mamba_bwd).
+ * Layout: draw/u/z/out/gout/gdraw/gu/gz [B, L, D] and Bt/Ct/gBt/gCt [B, L, N] in io_dtype
+ * (TSF_DTYPE_F32 or TSF_DTYPE_BF16); A/gA [D, N], Dp/gDp [D], h0/h_last/ghlast/gh0 [B, D, N]
+ * always float32 (the state is float32 in both regimes). 1 <= N <= 64.
+ * chk [B, NC, D, N] float32 with NC = ceil(L / tsfast_hip_mamba_chk_interval(N)): slot k holds
+ * the state after step (k + 1) * interval - 1. chk == NULL selects the inference kernel, which
+ * writes no checkpoints.
+ */
+int64_t tsfast_hip_mamba_chk_interval(int64_t N);
+int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtype, const void* draw, const float* A,
+                         const void* Bt, const void* Ct, const void* u, const void* z, const float* Dp,
+                         const float* h0, void* out, float* h_last, float* chk, void* stream);
+/* Backward from the forward's checkpoints. ghlast may be NULL (zero upstream state gradient);
+ * gh0 is written iff h0 is given. gA/gDp are the full parameter gradients (summed over the batch). */
+int64_t tsfast_hip_mamba_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t N);
+int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtype, const void* draw, const float* A,
+                         const void* Bt, const void* Ct, const void* u, const void* z, const float* Dp,
+                         const float* h0, const float* chk, const void* gout, const float* ghlast, void* gdraw,
+                         float* gA, void* gBt, void* gCt, void* gu, void* gz, float* gDp, float* gh0, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * dynoNet all-pole IIR scan  y_t = w_t - sum_{i=1..na} a_i y_{t-i},  float32, 1 <= na <= 16.
+ * Replaces the generated kernels of tsfast/models/architectures/dynonet/allpole_triton.py:59-233
+ * (tsfast::dynonet_allpole / dynonet_allpole_bwd, including the host-side y0 head taps at :202-213).
+ * Layout: a [lanes, na], w/y/g/gw [lanes, L] (time contiguous), y0/gy0 [lanes, na] newest first
+ * (y0[j] = y_{-1-j}).
+ */
+int64_t tsfast_hip_allpole_workspace_bytes(int64_t lanes, int64_t L, int64_t na);
+int tsfast_hip_allpole_fwd(int64_t lanes, int64_t L, int64_t na, const float* a, const float* w, const float* y0,
+                           float* y, void* workspace, int64_t workspace_bytes, void* stream);
+/* ga = d loss / d a (full gradient, y0 taps included), gw = G, gy0 written iff y0 given. */
+int tsfast_hip_allpole_bwd(int64_t lanes, int64_t L, int64_t na, const float* g, const float* a, const float* y,
+                           const float* y0, float* gw, float* ga, float* gy0, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSFAST_HIP_H */

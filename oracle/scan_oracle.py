@@ -1,0 +1,249 @@
+"""fp64 sequential oracle for tsfast's scan family — TEST INFRASTRUCTURE ONLY.
+
+This module is the checker, never the thing measured or shipped: only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg may import it. The product path
+(``tsfast_amd``) never calls into ``oracle/``.
+
+Each function restates the reference algorithm as a per-time-step loop in float64 (complex128
+for complex lanes), vectorised over lanes with numpy, following the cited reference lines.
+Backward functions are the closed-form adjoints the reference derives; they take the upstream
+gradient in torch's convention (conjugate Wirtinger for complex tensors), so they equal
+``torch.autograd.grad`` through the forward loop.
+
+Pinning (see tests/test_oracle.py): every function here is checked against an independent
+route — brute-force closed-form sums, ``scipy.signal.lfilter``, a textbook selective-scan
+written as einsums, the companion-matrix doubling scan, and torch float64 autograd through
+sequential loops — plus special cases (constant coefficients reduce the selective scan to the
+diagonal one, delta -> 0 makes Mamba the identity map on the state, N = 1 reduces it to a
+scalar recurrence).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "rel_err",
+    "diag_forward",
+    "diag_backward",
+    "selective_forward",
+    "selective_backward",
+    "softplus",
+    "mamba_forward",
+    "mamba_backward",
+    "allpole_forward",
+    "allpole_backward",
+]
+
+
+def rel_err(a, b) -> float:
+    """``max|a - b| / max|b|`` — the reference tests' metric (tests/test_scan.py:13-14)."""
+    a = np.asarray(a)
+    b = np.asarray(b)
+    if b.size == 0:
+        return 0.0
+    return float(np.max(np.abs(a - b)) / (np.max(np.abs(b)) + 1e-30))
+
+
+def _hi(x):
+    x = np.asarray(x)
+    return x.astype(np.complex128) if np.iscomplexobj(x) else x.astype(np.float64)
+
+
+# --------------------------------------------------------------------------- diagonal scans
+def diag_forward(lam, v, x0=None):
+    """``x_t = lam * x_{t-1} + v_t`` on lanes: lam [M, N], v [M, L, N], x0 [M, N] or None.
+
+    Follows tsfast/models/_core/scan.py:316-328 (the sequential loop), semantics of the
+    ``tsfast::scan_diagonal`` op (:100-115).
+    """
+    lam, v = _hi(lam), _hi(v)
+    M, L, N = v.shape
+    dt = np.result_type(lam, v)
+    x = np.zeros((M, N), dt) if x0 is None else _hi(x0).astype(dt)
+    out = np.empty((M, L, N), dt)
+    for t in range(L):
+        x = lam * x + v[:, t]
+        out[:, t] = x
+    return out
+
+
+def diag_backward(g, lam, out, x0=None):
+    """Adjoint of :func:`diag_forward`: ``G_t = g_t + conj(lam) G_{t+1}``;
+    ``glam = sum_t G_t conj(x_{t-1})``, ``gv = G``, ``gx0 = conj(lam) G_0``
+    (tsfast/models/_core/scan.py:10-15, 118-140)."""
+    g, lam, out = _hi(g), _hi(lam), _hi(out)
+    M, L, N = out.shape
+    dt = np.result_type(g, lam, out)
+    lc = np.conj(lam)
+    G = np.zeros((M, N), dt)
+    gv = np.empty((M, L, N), dt)
+    glam = np.zeros((M, N), dt)
+    for t in range(L - 1, -1, -1):
+        G = g[:, t] + lc * G
+        gv[:, t] = G
+        xprev = out[:, t - 1] if t > 0 else (np.zeros((M, N), dt) if x0 is None else _hi(x0))
+        glam = glam + G * np.conj(xprev)
+    gx0 = None if x0 is None else lc * (gv[:, 0] if L > 0 else np.zeros((M, N), dt))
+    return glam, gv, gx0
+
+
+def selective_forward(a, v, x0=None):
+    """``x_t = a_t * x_{t-1} + v_t``: a, v [M, L, N] (tsfast/models/_core/scan.py:157-168, 316-328)."""
+    a, v = _hi(a), _hi(v)
+    M, L, N = v.shape
+    dt = np.result_type(a, v)
+    x = np.zeros((M, N), dt) if x0 is None else _hi(x0).astype(dt)
+    out = np.empty((M, L, N), dt)
+    for t in range(L):
+        x = a[:, t] * x + v[:, t]
+        out[:, t] = x
+    return out
+
+
+def selective_backward(g, a, out, x0=None):
+    """Adjoint: ``G_t = g_t + conj(a_{t+1}) G_{t+1}``; ``glam_t = G_t conj(x_{t-1})``, ``gv = G``,
+    ``gx0 = conj(a_0) G_0`` (tsfast/models/_core/scan.py:176-195)."""
+    g, a, out = _hi(g), _hi(a), _hi(out)
+    M, L, N = out.shape
+    dt = np.result_type(g, a, out)
+    G = np.zeros((M, N), dt)
+    gv = np.empty((M, L, N), dt)
+    glam = np.empty((M, L, N), dt)
+    for t in range(L - 1, -1, -1):
+        an = np.conj(a[:, t + 1]) if t + 1 < L else np.zeros((M, N), dt)
+        G = g[:, t] + an * G
+        gv[:, t] = G
+        xprev = out[:, t - 1] if t > 0 else (np.zeros((M, N), dt) if x0 is None else _hi(x0))
+        glam[:, t] = G * np.conj(xprev)
+    gx0 = None if x0 is None else np.conj(a[:, 0]) * gv[:, 0]
+    return glam, gv, gx0
+
+
+# --------------------------------------------------------------------------- Mamba
+def softplus(x):
+    """torch.nn.functional.softplus with threshold 20 (mamba_triton.py:75-78)."""
+    x = np.asarray(x, np.float64)
+    return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+
+
+def _sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def mamba_forward(draw, A, Bt, Ct, u, z, Dp, h0=None, return_states=False):
+    """Fused Mamba SSM forward (mamba_triton.py:85-157; backend_c.py:105-144):
+
+    ``delta = softplus(draw)``, ``h_t = exp(delta_t A) h_{t-1} + delta_t u_t B_t``,
+    ``out_t = (sum_n h_t C_t + Dp u_t) * z_t * sigmoid(z_t)``.
+    Shapes: draw/u/z [B, L, D], A [D, N], Bt/Ct [B, L, N], Dp [D], h0 [B, D, N].
+    Returns ``(out [B, L, D], h_last [B, D, N])`` (and all states ``[B, L, D, N]`` if asked).
+    """
+    draw, A, Bt, Ct, u, z, Dp = map(_hi, (draw, A, Bt, Ct, u, z, Dp))
+    Bsz, L, D = draw.shape
+    N = A.shape[-1]
+    h = np.zeros((Bsz, D, N)) if h0 is None else _hi(h0).copy()
+    delta = softplus(draw)
+    out = np.empty((Bsz, L, D))
+    hs = np.empty((Bsz, L, D, N)) if return_states else None
+    for t in range(L):
+        lam = np.exp(delta[:, t, :, None] * A[None])
+        h = lam * h + (delta[:, t] * u[:, t])[:, :, None] * Bt[:, t, None, :]
+        y = np.einsum("bdn,bn->bd", h, Ct[:, t]) + Dp * u[:, t]
+        out[:, t] = y * z[:, t] * _sigmoid(z[:, t])
+        if hs is not None:
+            hs[:, t] = h
+    if return_states:
+        return out, h, hs
+    return out, h
+
+
+def mamba_backward(gout, ghlast, draw, A, Bt, Ct, u, z, Dp, h0=None):
+    """Closed-form adjoint of :func:`mamba_forward` (mamba_triton.py:163-286; backend_c.py:149-245).
+
+    With ``gy = gout z sigmoid(z)`` and ``G_t = gy_t C_t + lam_{t+1} G_{t+1}`` (``lam_L = 1``, so
+    ``ghlast`` enters ``G_{L-1}``) and ``P_t = lam_t h_{t-1}``:
+    ``gz = gout y sigmoid(z) (1 + z (1 - sigmoid(z)))``, ``gA = sum G P delta``,
+    ``gdelta = sum_n G (A P + u B)``, ``gdraw = gdelta sigmoid(draw)``,
+    ``gu = delta sum_n G B + gy Dp``, ``gBt = sum_d G delta u``, ``gCt = sum_d gy h``,
+    ``gDp = sum gy u``, ``gh0 = lam_0 G_0``.
+    Returns ``(gdraw, gA, gBt, gCt, gu, gz, gDp, gh0)`` (gh0 None when h0 is None).
+    """
+    draw, A, Bt, Ct, u, z, Dp, gout = map(_hi, (draw, A, Bt, Ct, u, z, Dp, gout))
+    Bsz, L, D = draw.shape
+    N = A.shape[-1]
+    _, _, hs = mamba_forward(draw, A, Bt, Ct, u, z, Dp, h0, return_states=True)
+    delta = softplus(draw)
+    sig = _sigmoid(z)
+    y = np.einsum("bldn,bln->bld", hs, Ct) + Dp * u
+    gy = gout * z * sig
+    gz = gout * y * sig * (1.0 + z * (1.0 - sig))
+    G = np.zeros((Bsz, D, N)) if ghlast is None else _hi(ghlast).copy()
+    gdraw = np.empty((Bsz, L, D))
+    gu = np.empty((Bsz, L, D))
+    gBt = np.empty((Bsz, L, N))
+    gCt = np.empty((Bsz, L, N))
+    gA = np.zeros((D, N))
+    h_init = np.zeros((Bsz, D, N)) if h0 is None else _hi(h0)
+    for t in range(L - 1, -1, -1):
+        if t + 1 < L:
+            G = np.exp(delta[:, t + 1, :, None] * A[None]) * G
+        G = G + gy[:, t, :, None] * Ct[:, t, None, :]
+        hprev = hs[:, t - 1] if t > 0 else h_init
+        P = np.exp(delta[:, t, :, None] * A[None]) * hprev
+        gA += np.sum(G * P * delta[:, t, :, None], axis=0)
+        gdelta = np.sum(G * (A[None] * P + u[:, t, :, None] * Bt[:, t, None, :]), axis=2)
+        gdraw[:, t] = gdelta * _sigmoid(draw[:, t])
+        gu[:, t] = delta[:, t] * np.sum(G * Bt[:, t, None, :], axis=2) + gy[:, t] * Dp
+        gBt[:, t] = np.sum(G * (delta[:, t] * u[:, t])[:, :, None], axis=1)
+        gCt[:, t] = np.sum(gy[:, t, :, None] * hs[:, t], axis=1)
+    gDp = np.sum(gy * u, axis=(0, 1))
+    gh0 = None
+    if h0 is not None:
+        gh0 = (np.exp(delta[:, 0, :, None] * A[None]) * G) if L > 0 else G
+    return gdraw, gA, gBt, gCt, gu, gz, gDp, gh0
+
+
+# --------------------------------------------------------------------------- all-pole
+def allpole_forward(a, w, y0=None):
+    """``y_t = w_t - sum_{i=1..na} a_i y_{t-i}`` per lane: a [lanes, na], w [lanes, L],
+    y0 [lanes, na] newest first (``y0[j] = y_{-1-j}``) (allpole_triton.py:1-31, 80-96)."""
+    a, w = _hi(a), _hi(w)
+    lanes, L = w.shape
+    na = a.shape[-1]
+    s = np.zeros((lanes, na)) if y0 is None else _hi(y0).copy()  # s[:, k] = y_{t-1-k}
+    y = np.empty((lanes, L))
+    for t in range(L):
+        yt = w[:, t] - np.sum(a * s, axis=1)
+        y[:, t] = yt
+        s = np.concatenate([yt[:, None], s[:, :-1]], axis=1)
+    return y
+
+
+def allpole_backward(g, a, y, y0=None):
+    """Adjoint (allpole_triton.py:19-27, 101-122, 191-213): ``G_t = g_t - sum_i a_i G_{t+i}``,
+    ``gw = G``, ``ga_i = -sum_{t>=0} G_t y_{t-i}`` with ``y_{-k} = y0[k-1]``,
+    ``gy0_j = -sum_{i=j+1..na} a_i G_{i-1-j}``. Returns ``(ga, gw, gy0)``."""
+    g, a, y = _hi(g), _hi(a), _hi(y)
+    lanes, L = y.shape
+    na = a.shape[-1]
+    Gpad = np.zeros((lanes, L + na))
+    for t in range(L - 1, -1, -1):
+        Gpad[:, t] = g[:, t] - np.sum(a * Gpad[:, t + 1 : t + 1 + na], axis=1)
+    gw = Gpad[:, :L].copy()
+    # y extended to the left by y0: yext[:, na + t] = y_t, yext[:, na - 1 - j] = y0[j]
+    yext = np.zeros((lanes, na + L))
+    yext[:, na:] = y
+    if y0 is not None:
+        yext[:, :na] = _hi(y0)[:, ::-1]
+    ga = np.zeros((lanes, na))
+    for i in range(1, na + 1):
+        # sum_t G_t y_{t-i}, t = 0..L-1, y_{t-i} = yext[:, na + t - i]
+        ga[:, i - 1] = -np.sum(gw * yext[:, na - i : na - i + L], axis=1)
+    gy0 = None
+    if y0 is not None:
+        gy0 = np.zeros((lanes, na))
+        for j in range(na):
+            for i in range(j + 1, na + 1):
+                gy0[:, j] -= a[:, i - 1] * Gpad[:, i - 1 - j]
+    return ga, gw, gy0

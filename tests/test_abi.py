@@ -1,0 +1,60 @@
+"""The C ABI: libtsfast_hip.so loads on the CPU host and exports every symbol include/tsfast_hip.h
+declares, and the size/status queries behave (no kernel is launched here)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from tsfast_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "tsfast_hip.h").read_text()
+    return sorted(set(re.findall(r"\b(tsfast_hip_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.available():
+        pytest.skip("libtsfast_hip.so not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_loader_signatures_cover_the_header():
+    assert sorted(_lib._SIGNATURES) == _declared()
+
+
+def test_status_strings(lib):
+    assert lib.tsfast_hip_status_string(0) == b"ok"
+    assert b"workspace" in lib.tsfast_hip_status_string(-2)
+    assert lib.tsfast_hip_version() >= 1
+
+
+def test_size_queries(lib):
+    assert lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 0) > 0
+    assert lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 1) == 2 * lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 0)
+    assert lib.tsfast_hip_mamba_chk_interval(16) >= 1
+    assert lib.tsfast_hip_mamba_workspace_bytes(16, 4096, 1536, 16) > 0
+    assert lib.tsfast_hip_mamba_workspace_bytes(1, 1, 1, 65) == -1  # N above 64
+    assert lib.tsfast_hip_allpole_workspace_bytes(4096, 16384, 3) > 0
+    assert lib.tsfast_hip_allpole_workspace_bytes(4, 16, 17) == -1  # na above 16
+
+
+def test_argument_errors_before_any_launch(lib):
+    # negative sizes and unsupported orders are rejected on the host, before touching a device
+    assert lib.tsfast_hip_diag_fwd(-1, 1, 1, 0, None, None, None, None, None, 0, None) == -1
+    assert lib.tsfast_hip_allpole_fwd(4, 16, 17, None, None, None, None, None, 0, None) == -3
+    assert lib.tsfast_hip_mamba_fwd(1, 1, 1, 65, 0, *([None] * 12)) == -3
+    # empty problems are a no-op
+    assert lib.tsfast_hip_diag_fwd(0, 5, 3, 0, None, None, None, None, None, 0, None) == 0

@@ -1,0 +1,56 @@
+"""The CPU-baseline port (oracle/cpu_baseline.cpp) computes the same thing as the fp64 oracle,
+so the bench's CPU column times the right work."""
+
+import numpy as np
+import pytest
+
+from oracle import cpu_baseline as CB
+from oracle import scan_oracle as O
+
+
+@pytest.fixture(scope="module")
+def lib():
+    try:
+        return CB.load(prefer_native=False)
+    except Exception as e:  # pragma: no cover - no compiler
+        pytest.skip(f"cpu baseline unavailable: {e}")
+
+
+@pytest.mark.parametrize("B,L,D,N,with_h0", [(2, 50, 20, 16, True), (1, 33, 9, 4, False), (2, 17, 8, 12, True)])
+def test_mamba_port_matches_oracle(lib, B, L, D, N, with_h0):
+    rng = np.random.default_rng(B + L + D + N)
+    args = dict(
+        draw=rng.normal(-1, 1, (B, L, D)), A=-np.exp(rng.normal(0, 0.5, (D, N))), Bt=rng.standard_normal((B, L, N)),
+        Ct=rng.standard_normal((B, L, N)), u=rng.standard_normal((B, L, D)), z=rng.standard_normal((B, L, D)),
+        Dp=rng.standard_normal(D),
+    )
+    args = {k: v.astype(np.float32).astype(np.float64) for k, v in args.items()}
+    h0 = rng.standard_normal((B, D, N)).astype(np.float32).astype(np.float64) if with_h0 else None
+    gout = rng.standard_normal((B, L, D)).astype(np.float32).astype(np.float64)
+    ghl = rng.standard_normal((B, D, N)).astype(np.float32).astype(np.float64) if with_h0 else None
+    order = ("draw", "A", "Bt", "Ct", "u", "z", "Dp")
+    got = CB.mamba_fwd_bwd(*(args[k] for k in order), gout, h0=h0, ghlast=ghl)
+    out, hl = O.mamba_forward(*(args[k] for k in order), h0)
+    want = O.mamba_backward(gout, ghl, *(args[k] for k in order), h0)
+    assert O.rel_err(got[0], out) < 1e-4 and O.rel_err(got[1], hl) < 1e-4
+    for a, b in zip(got[2:], want):
+        if b is not None:
+            assert O.rel_err(a, b) < 1e-4
+
+
+@pytest.mark.parametrize("cplx", [False, True])
+def test_diag_port_matches_oracle(lib, cplx):
+    rng = np.random.default_rng(3)
+    M, L, N = 3, 70, 100
+    lam = rng.uniform(0.9, 0.999, (M, N))
+    v, g, x0 = rng.standard_normal((M, L, N)), rng.standard_normal((M, L, N)), rng.standard_normal((M, N))
+    if cplx:
+        lam = lam * np.exp(1j * rng.uniform(0, np.pi / 10, (M, N)))
+        v, g, x0 = v + 1j * rng.standard_normal(v.shape), g + 1j * rng.standard_normal(g.shape), x0 + 1j
+    dt = np.complex64 if cplx else np.float32
+    lam, v, g, x0 = (a.astype(dt) for a in (lam, v, g, x0))
+    out, glam, gv, gx0 = CB.diag_fwd_bwd(lam, v, g, x0)
+    want = O.diag_forward(lam, v, x0)
+    wl, wv, wx = O.diag_backward(g, lam, want, x0)
+    assert O.rel_err(out, want) < 1e-5
+    assert O.rel_err(glam, wl) < 1e-4 and O.rel_err(gv, wv) < 1e-5 and O.rel_err(gx0, wx) < 1e-5

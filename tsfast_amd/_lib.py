@@ -1,0 +1,108 @@
+"""ctypes loader for libtsfast_hip.so and the marshalling shared by the backend shims.
+
+The library is built in-tree by ``tsfast_amd.build`` (``python -m tsfast_amd.build``). Loading
+is lazy (first kernel call) and failures raise: there is no silent fallback from a backend
+module once it has been selected — a missing or unloadable library is a ``RuntimeError``
+naming the path and the loader's reason.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(os.environ.get("TSFAST_HIP_LIB", Path(__file__).resolve().parent / "libtsfast_hip.so"))
+
+_lib: ctypes.CDLL | None = None
+_lock = threading.Lock()
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_ptr = ctypes.c_void_p
+
+# Entry points and their argument types (mirrors include/tsfast_hip.h).
+_SIGNATURES: dict[str, tuple[list, object]] = {
+    "tsfast_hip_version": ([], _int),
+    "tsfast_hip_status_string": ([_int], ctypes.c_char_p),
+    "tsfast_hip_diag_workspace_bytes": ([_i64, _i64, _i64, _int], _i64),
+    "tsfast_hip_diag_fwd": ([_i64, _i64, _i64, _int] + [_ptr] * 5 + [_i64, _ptr], _int),
+    "tsfast_hip_diag_bwd": ([_i64, _i64, _i64, _int] + [_ptr] * 8 + [_i64, _ptr], _int),
+    "tsfast_hip_sel_workspace_bytes": ([_i64, _i64, _i64], _i64),
+    "tsfast_hip_sel_fwd": ([_i64, _i64, _i64] + [_ptr] * 5 + [_i64, _ptr], _int),
+    "tsfast_hip_sel_bwd": ([_i64, _i64, _i64] + [_ptr] * 8 + [_i64, _ptr], _int),
+    "tsfast_hip_mamba_chk_interval": ([_i64], _i64),
+    "tsfast_hip_mamba_workspace_bytes": ([_i64, _i64, _i64, _i64], _i64),
+    "tsfast_hip_mamba_fwd": ([_i64, _i64, _i64, _i64, _int] + [_ptr] * 11 + [_ptr], _int),
+    "tsfast_hip_mamba_bwd": ([_i64, _i64, _i64, _i64, _int] + [_ptr] * 19 + [_i64, _ptr], _int),
+    "tsfast_hip_allpole_workspace_bytes": ([_i64, _i64, _i64], _i64),
+    "tsfast_hip_allpole_fwd": ([_i64, _i64, _i64] + [_ptr] * 5 + [_i64, _ptr], _int),
+    "tsfast_hip_allpole_bwd": ([_i64, _i64, _i64] + [_ptr] * 8 + [_i64, _ptr], _int),
+}
+
+TSF_DTYPE_F32 = 0
+TSF_DTYPE_BF16 = 1
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raises RuntimeError if it is missing or broken."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"libtsfast_hip.so not found at {LIB_PATH}; build it with `python -m tsfast_amd.build`"
+                )
+            try:
+                lib = ctypes.CDLL(str(LIB_PATH))
+            except OSError as e:
+                raise RuntimeError(f"failed to load {LIB_PATH}: {e}") from e
+            for name, (argtypes, restype) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = argtypes
+                fn.restype = restype
+            _lib = lib
+    return _lib
+
+
+def available() -> bool:
+    """True when the library file exists (does not load it)."""
+    return LIB_PATH.exists()
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().tsfast_hip_status_string(status).decode()
+        raise RuntimeError(f"{what} failed (status {status}): {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    """Raw device pointer of a tensor (None passes NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """The current HIP stream of the tensor's device, as an integer handle."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require(t: torch.Tensor | None, name: str, dtypes: tuple, device: torch.device) -> None:
+    """Screen a tensor handed to a raw-pointer kernel: dtype, device and density."""
+    if t is None:
+        return
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name}: dtype {t.dtype} not in {dtypes}")
+    if t.device != device:
+        raise TypeError(f"{name}: on {t.device}, expected {device}")
+    if not t.is_contiguous():
+        raise TypeError(f"{name}: must be contiguous")
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Scratch buffer for partial results (uninitialised; the kernels write before reading)."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

@@ -1,0 +1,133 @@
+// Shared device helpers for the tsfast scan kernels (gfx950 / CDNA4, wave64).
+//
+// Everything here is plain HIP: float / float2 arithmetic, bf16 <-> f32 conversion with
+// round-to-nearest-even (the rounding torch uses for .to(torch.bfloat16)), and the
+// transcendental building blocks the Mamba kernels need. No host code lives here.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define TSF_DEV __device__ __forceinline__
+
+namespace tsf {
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ------------------------------------------------------------------ bf16 storage
+// bf16 values travel as raw uint16_t; the kernels compute in fp32.
+struct bf16 {
+  uint16_t bits;
+};
+
+TSF_DEV float to_f32(float x) { return x; }
+TSF_DEV float to_f32(bf16 x) { return __uint_as_float(static_cast<uint32_t>(x.bits) << 16); }
+
+template <typename T>
+TSF_DEV T from_f32(float x);
+template <>
+TSF_DEV float from_f32<float>(float x) { return x; }
+template <>
+TSF_DEV bf16 from_f32<bf16>(float x) {
+  uint32_t u = __float_as_uint(x);
+  bf16 r;
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+    r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN, sign kept
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);
+    r.bits = static_cast<uint16_t>(u >> 16);
+  }
+  return r;
+}
+
+// ------------------------------------------------------------------ complex (interleaved re/im)
+TSF_DEV float2 cmul(float2 a, float2 b) { return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x); }
+// a * conj(b)
+TSF_DEV float2 cmul_conj(float2 a, float2 b) { return make_float2(a.x * b.x + a.y * b.y, a.y * b.x - a.x * b.y); }
+TSF_DEV float2 cconj(float2 a) { return make_float2(a.x, -a.y); }
+TSF_DEV float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+// a * x + b
+TSF_DEV float2 cfma(float2 a, float2 x, float2 b) {
+  return make_float2(fmaf(a.x, x.x, fmaf(-a.y, x.y, b.x)), fmaf(a.x, x.y, fmaf(a.y, x.x, b.y)));
+}
+
+// Scalar traits so one kernel body serves float (real) and float2 (complex) lanes.
+template <typename T>
+struct Num;
+template <>
+struct Num<float> {
+  TSF_DEV static float zero() { return 0.0f; }
+  TSF_DEV static float one() { return 1.0f; }
+  TSF_DEV static float mul(float a, float b) { return a * b; }
+  TSF_DEV static float fma(float a, float x, float b) { return fmaf(a, x, b); }
+  TSF_DEV static float add(float a, float b) { return a + b; }
+  TSF_DEV static float conj(float a) { return a; }
+  TSF_DEV static float mul_conj(float a, float b) { return a * b; }
+};
+template <>
+struct Num<float2> {
+  TSF_DEV static float2 zero() { return make_float2(0.0f, 0.0f); }
+  TSF_DEV static float2 one() { return make_float2(1.0f, 0.0f); }
+  TSF_DEV static float2 mul(float2 a, float2 b) { return cmul(a, b); }
+  TSF_DEV static float2 fma(float2 a, float2 x, float2 b) { return cfma(a, x, b); }
+  TSF_DEV static float2 add(float2 a, float2 b) { return cadd(a, b); }
+  TSF_DEV static float2 conj(float2 a) { return cconj(a); }
+  TSF_DEV static float2 mul_conj(float2 a, float2 b) { return cmul_conj(a, b); }
+};
+
+// x^k for an integer k >= 0 by binary powering (log2(k) squarings; exact for k = 0).
+template <typename T>
+TSF_DEV T ipow(T x, int64_t k) {
+  T r = Num<T>::one();
+  while (k > 0) {
+    if (k & 1) r = Num<T>::mul(r, x);
+    x = Num<T>::mul(x, x);
+    k >>= 1;
+  }
+  return r;
+}
+
+// ------------------------------------------------------------------ Mamba scalar maps
+// 2^x on the hardware transcendental unit (v_exp_f32); the kernels pre-scale A by log2(e).
+TSF_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// softplus with torch.nn.functional.softplus's threshold: x for x > 20, else log(1 + e^x).
+TSF_DEV float softplus(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }
+
+TSF_DEV float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// ------------------------------------------------------------------ wave reductions
+// Reduce-scatter of K values (K a power of two, K <= 64) held by every lane of a wave64:
+// on return v[0] of lane l holds the sum over all 64 lanes of value index (l >> (6 - log2 K)).
+// Each halving level exchanges half of the remaining values with the partner lane, so the
+// whole reduction costs K - 1 exchanges instead of 6 * K for independent butterflies.
+template <int K>
+TSF_DEV void wave_reduce_scatter(float* v, int lane) {
+  static_assert(K >= 1 && K <= 64 && (K & (K - 1)) == 0, "K must be a power of two <= 64");
+  int k = K;
+#pragma unroll
+  for (int mask = 32; mask >= 1; mask >>= 1) {
+    if (k > 1) {
+      const bool upper = (lane & mask) != 0;
+      const int half = k >> 1;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        if (i < half) {
+          const float send = upper ? v[i] : v[i + half];
+          const float keep = upper ? v[i + half] : v[i];
+          v[i] = keep + __shfl_xor(send, mask, kWave);
+        }
+      }
+      k = half;
+    } else {
+      v[0] += __shfl_xor(v[0], mask, kWave);
+    }
+  }
+}
+
+}  // namespace tsf
+
+// Host side: status of the launches just enqueued (records the HIP error for the status string).
+int tsf_record_hip_error(hipError_t e);
+inline int tsf_launch_status() { return tsf_record_hip_error(hipGetLastError()); }

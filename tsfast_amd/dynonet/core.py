@@ -1,0 +1,120 @@
+"""dynoNet all-pole section with its fused-kernel dispatch, and the companion-matrix scan.
+
+Mirrors ``tsfast/models/architectures/dynonet/core.py``: ``linear_recurrence`` (the log-doubling
+scan ``x_t = A x_{t-1} + v_t`` with its analytic matrix adjoint, ``:23-127``) and the all-pole
+branch of ``LinearDynamicalOperator.forward`` (``:221-248``): the fused backend when one serves
+the inputs (``_fused_allpole``, ``:91-100``; here the ``"hip"`` family for ``"cuda"`` tensors),
+else ``linear_recurrence`` over the companion matrices.
+"""
+
+from __future__ import annotations
+
+__all__ = ["linear_recurrence", "allpole", "companion"]
+
+import torch
+import torch.nn.functional as F
+
+from ..dispatch import resolve
+from . import allpole_hip
+
+_ALLPOLE_BACKENDS = {"hip": allpole_hip}
+
+
+def _doubling_matrix_scan(A: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """``x_t = A x_{t-1} + v_t`` from a zero state: doubling span, one batched matmul per level."""
+    L = v.shape[-2]
+    x = v.clone() if L <= 1 else v
+    span, P = 1, A
+    while span < L:
+        shifted = F.pad(x[..., :-span, :], (0, 0, span, 0))
+        x = x + shifted @ P.transpose(-1, -2)
+        P = P @ P
+        span <<= 1
+    return x
+
+
+def _prev(x: torch.Tensor, x0: torch.Tensor | None) -> torch.Tensor:
+    head = torch.zeros_like(x[..., :1, :]) if x0 is None else x0.unsqueeze(-2).expand_as(x[..., :1, :])
+    return torch.cat((head, x[..., :-1, :]), dim=-2)
+
+
+@torch.library.custom_op("tsfast_hip::linear_recurrence", mutates_args=())
+def _linear_recurrence_op(A: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> torch.Tensor:
+    if x0 is not None:
+        v = torch.cat((v[..., :1, :] + x0.unsqueeze(-2) @ A.transpose(-1, -2), v[..., 1:, :]), dim=-2)
+    return _doubling_matrix_scan(A, v)
+
+
+@_linear_recurrence_op.register_fake
+def _(A, v, x0):
+    return torch.empty_like(v)
+
+
+@torch.library.custom_op("tsfast_hip::linear_recurrence_bwd", mutates_args=())
+def _linear_recurrence_bwd_op(
+    g: torch.Tensor, A: torch.Tensor, out: torch.Tensor, x0: torch.Tensor | None
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    # adjoint G_t = A^T G_{t+1} + g_t: the same scan with A transposed, run time-reversed
+    G = _doubling_matrix_scan(A.transpose(-1, -2), g.flip(-2)).flip(-2)
+    grad_A = G.transpose(-1, -2) @ _prev(out, x0)
+    grad_x0 = (G[..., :1, :] @ A).squeeze(-2) if x0 is not None else A.new_empty(0)
+    return grad_A, G, grad_x0
+
+
+@_linear_recurrence_bwd_op.register_fake
+def _(g, A, out, x0):
+    gx0 = torch.empty_like(x0) if x0 is not None else A.new_empty(0)
+    return torch.empty_like(A), torch.empty_like(g), gx0
+
+
+def _linrec_setup(ctx, inputs, output):
+    A, v, x0 = inputs
+    ctx.save_for_backward(A, output, x0)
+
+
+def _linrec_backward(ctx, g):
+    A, out, x0 = ctx.saved_tensors
+    grad_A, grad_v, grad_x0 = _linear_recurrence_bwd_op(g, A, out, x0)
+    return grad_A, grad_v, (grad_x0 if x0 is not None else None)
+
+
+_linear_recurrence_op.register_autograd(_linrec_backward, setup_context=_linrec_setup)
+
+
+def linear_recurrence(A: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None = None) -> torch.Tensor:
+    """``x_t = A x_{t-1} + v_t`` with constant ``A [..., n, n]`` by log-doubling (``core.py:103-127``)."""
+    bshape = torch.broadcast_shapes(A.shape[:-2], v.shape[:-2], () if x0 is None else x0.shape[:-1])
+    A_b = A.broadcast_to(bshape + A.shape[-2:])
+    v_b = v.broadcast_to(bshape + v.shape[-2:])
+    x0_b = None if x0 is None else x0.broadcast_to(bshape + x0.shape[-1:])
+    return _linear_recurrence_op(A_b, v_b, x0_b)
+
+
+def companion(a: torch.Tensor) -> torch.Tensor:
+    """Companion matrices ``[..., na, na]`` of monic denominators ``1 + a_1 q^-1 + ... + a_na q^-na``:
+    first row ``-a``, then the unit shift (``LinearDynamicalOperator._companion``, ``core.py:186-190``)."""
+    na = a.shape[-1]
+    shift = torch.eye(na, dtype=a.dtype, device=a.device)[:-1].expand(*a.shape[:-1], na - 1, na)
+    return torch.cat((-a.unsqueeze(-2), shift), dim=-2)
+
+
+def _fused_allpole(a, w, y0):
+    """Dispatch the fused all-pole kernel; None means run the matrix doubling scan."""
+    order = ("hip",) if w.device.type == "cuda" else ()
+    mod = resolve("dynonet.allpole", _ALLPOLE_BACKENDS, order, (a, w, y0))
+    return None if mod is None else mod.run(a, w, y0)
+
+
+def allpole(a: torch.Tensor, w: torch.Tensor, y0: torch.Tensor | None = None) -> torch.Tensor:
+    """``y_t = w_t - sum_i a_i y_{t-i}`` over lanes ``w [..., L]`` with ``a [..., na]``, ``y0 [..., na]``.
+
+    The fused kernel when one serves the inputs, else the companion-matrix doubling scan
+    (the reference CPU path): the companion state is a shift register of past outputs, so
+    ``y`` is its first component.
+    """
+    y = _fused_allpole(a, w, y0)
+    if y is not None:
+        return y
+    na = a.shape[-1]
+    x = linear_recurrence(companion(a), F.pad(w.unsqueeze(-1), (0, na - 1)), y0)
+    return x[..., 0]

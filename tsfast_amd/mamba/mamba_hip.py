@@ -1,0 +1,250 @@
+"""Fused HIP backend for the Mamba selective SSM section (softplus discretisation, exp(delta A),
+input injection, recurrence, C contraction, D skip and SiLU gate in one kernel).
+
+Drop-in for the ``mamba.ssm`` registry of ``tsfast/models/architectures/mamba/core.py:22-23``
+(the role of ``mamba_triton.py:286-534``): ``supports(draw, A, Bt, Ct, u, z, Dp, h0)`` and
+``run(...) -> (out [B, L, D], h_last [B, D, N])``, differentiable in all eight inputs through
+the ``tsfast_hip::mamba_scan`` / ``mamba_scan_train`` / ``mamba_scan_bwd`` custom ops.
+
+Two I/O regimes: float32 everywhere (tsfast's regime), or bfloat16 sequence tensors
+(draw, u, z, Bt, Ct and their gradients) with float32 parameters (A, Dp) and float32 state
+(h0, h_last, the checkpoints). The state never leaves registers in fp32 arithmetic; only the
+training forward stores one fp32 checkpoint per channel every ``chk_interval(N)`` steps
+(``tsfast_hip_mamba_chk_interval``), from which the backward recomputes.
+"""
+
+from __future__ import annotations
+
+__all__ = ["supports", "run", "chk_interval"]
+
+import torch
+
+from .. import _lib
+
+_IO_DTYPES = {torch.float32: _lib.TSF_DTYPE_F32, torch.bfloat16: _lib.TSF_DTYPE_BF16}
+_MAX_N = 64
+
+
+def chk_interval(N: int) -> int:
+    """Checkpoint interval (steps) the kernels use for state size N."""
+    return int(_lib.load().tsfast_hip_mamba_chk_interval(N))
+
+
+def supports(draw, A, Bt, Ct, u, z, Dp, h0) -> str | None:
+    """Reason the fused HIP kernel cannot handle these tensors, or None if it can."""
+    seq = {"draw": draw, "Bt": Bt, "Ct": Ct, "u": u, "z": z}
+    params = {"A": A, "Dp": Dp}
+    if h0 is not None:
+        params["h0"] = h0
+    for name, t in {**seq, **params}.items():
+        if t.device.type != "cuda":
+            return f"{name} on {t.device.type}, hip backend is GPU-only"
+        if t.device != draw.device:
+            return f"{name} on {t.device}, expected {draw.device}"
+    if draw.dtype not in _IO_DTYPES:
+        return f"sequence dtype {draw.dtype} unsupported (need float32 or bfloat16)"
+    for name, t in seq.items():
+        if t.dtype != draw.dtype:
+            return f"{name} dtype {t.dtype} != draw dtype {draw.dtype}"
+    for name, t in params.items():
+        if t.dtype != torch.float32:
+            return f"needs float32 {name}, got {t.dtype}"
+    if draw.dim() != 3:
+        return f"draw must be [B, L, D], got {draw.dim()} dims"
+    B, L, D = draw.shape
+    if A.dim() != 2:
+        return f"A must be [D, N], got {tuple(A.shape)}"
+    N = A.shape[-1]
+    if tuple(A.shape) != (D, N):
+        return f"A.shape {tuple(A.shape)} incompatible with draw {tuple(draw.shape)}"
+    if not 1 <= N <= _MAX_N:
+        return f"state size N={N} outside [1, {_MAX_N}]"
+    if B > 65535:
+        return f"batch {B} above the 65535 grid limit"
+    if tuple(u.shape) != (B, L, D) or tuple(z.shape) != (B, L, D):
+        return f"u/z shapes {tuple(u.shape)}/{tuple(z.shape)} != {(B, L, D)}"
+    if tuple(Bt.shape) != (B, L, N) or tuple(Ct.shape) != (B, L, N):
+        return f"Bt/Ct shapes {tuple(Bt.shape)}/{tuple(Ct.shape)} != {(B, L, N)}"
+    if tuple(Dp.shape) != (D,):
+        return f"Dp.shape {tuple(Dp.shape)} != {(D,)}"
+    if h0 is not None and tuple(h0.shape) != (B, D, N):
+        return f"h0.shape {tuple(h0.shape)} != {(B, D, N)}"
+    return None
+
+
+def _contig(*ts):
+    return [t.contiguous() if t is not None else None for t in ts]
+
+
+def _check_inputs(draw, A, Bt, Ct, u, z, Dp, h0):
+    io = (draw.dtype,)
+    dev = draw.device
+    for name, t in (("draw", draw), ("Bt", Bt), ("Ct", Ct), ("u", u), ("z", z)):
+        _lib.require(t, name, io, dev)
+    for name, t in (("A", A), ("Dp", Dp), ("h0", h0)):
+        _lib.require(t, name, (torch.float32,), dev)
+
+
+def _forward(draw, A, Bt, Ct, u, z, Dp, h0, store_chk: bool):
+    lib = _lib.load()
+    _check_inputs(draw, A, Bt, Ct, u, z, Dp, h0)
+    B, L, D = draw.shape
+    N = A.shape[-1]
+    out = torch.empty_like(draw)
+    h_last = torch.empty(B, D, N, device=draw.device, dtype=torch.float32)
+    chk = None
+    if store_chk:
+        nc = -(-L // chk_interval(N))
+        chk = torch.empty(B, nc, D, N, device=draw.device, dtype=torch.float32)
+    _lib.check(
+        lib.tsfast_hip_mamba_fwd(
+            B, L, D, N, _IO_DTYPES[draw.dtype], *map(_lib.ptr, (draw, A, Bt, Ct, u, z, Dp, h0, out, h_last, chk)),
+            _lib.stream_of(draw),
+        ),
+        "tsfast_hip_mamba_fwd",
+    )
+    return out, h_last, chk
+
+
+@torch.library.custom_op("tsfast_hip::mamba_scan", mutates_args=())
+def _scan_op(
+    draw: torch.Tensor,
+    A: torch.Tensor,
+    Bt: torch.Tensor,
+    Ct: torch.Tensor,
+    u: torch.Tensor,
+    z: torch.Tensor,
+    Dp: torch.Tensor,
+    h0: torch.Tensor | None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    draw, A, Bt, Ct, u, z, Dp, h0 = _contig(draw, A, Bt, Ct, u, z, Dp, h0)
+    out, h_last, _ = _forward(draw, A, Bt, Ct, u, z, Dp, h0, store_chk=False)
+    return out, h_last
+
+
+@torch.library.custom_op("tsfast_hip::mamba_scan_train", mutates_args=())
+def _scan_train_op(
+    draw: torch.Tensor,
+    A: torch.Tensor,
+    Bt: torch.Tensor,
+    Ct: torch.Tensor,
+    u: torch.Tensor,
+    z: torch.Tensor,
+    Dp: torch.Tensor,
+    h0: torch.Tensor | None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    draw, A, Bt, Ct, u, z, Dp, h0 = _contig(draw, A, Bt, Ct, u, z, Dp, h0)
+    out, h_last, chk = _forward(draw, A, Bt, Ct, u, z, Dp, h0, store_chk=True)
+    return out, h_last, chk
+
+
+def _fake_outs(draw, A, with_chk: bool):
+    B, L, D = draw.shape
+    N = A.shape[-1]
+    out = torch.empty_like(draw)
+    h_last = draw.new_empty(B, D, N, dtype=torch.float32)
+    if not with_chk:
+        return out, h_last
+    return out, h_last, draw.new_empty(B, -(-L // chk_interval(N)), D, N, dtype=torch.float32)
+
+
+@_scan_op.register_fake
+def _(draw, A, Bt, Ct, u, z, Dp, h0):
+    return _fake_outs(draw, A, with_chk=False)
+
+
+@_scan_train_op.register_fake
+def _(draw, A, Bt, Ct, u, z, Dp, h0):
+    return _fake_outs(draw, A, with_chk=True)
+
+
+@torch.library.custom_op("tsfast_hip::mamba_scan_bwd", mutates_args=())
+def _scan_bwd_op(
+    gout: torch.Tensor,
+    ghlast: torch.Tensor | None,
+    chk: torch.Tensor,
+    draw: torch.Tensor,
+    A: torch.Tensor,
+    Bt: torch.Tensor,
+    Ct: torch.Tensor,
+    u: torch.Tensor,
+    z: torch.Tensor,
+    Dp: torch.Tensor,
+    h0: torch.Tensor | None,
+) -> tuple[
+    torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor
+]:
+    lib = _lib.load()
+    gout, ghlast, chk, draw, A, Bt, Ct, u, z, Dp, h0 = _contig(gout, ghlast, chk, draw, A, Bt, Ct, u, z, Dp, h0)
+    _check_inputs(draw, A, Bt, Ct, u, z, Dp, h0)
+    _lib.require(gout, "gout", (draw.dtype,), draw.device)
+    _lib.require(ghlast, "ghlast", (torch.float32,), draw.device)
+    _lib.require(chk, "chk", (torch.float32,), draw.device)
+    B, L, D = draw.shape
+    N = A.shape[-1]
+    gdraw = torch.empty_like(draw)
+    gu = torch.empty_like(draw)
+    gz = torch.empty_like(draw)
+    gBt = torch.empty_like(Bt)
+    gCt = torch.empty_like(Ct)
+    gA = torch.empty(D, N, device=draw.device, dtype=torch.float32)
+    gDp = torch.empty(D, device=draw.device, dtype=torch.float32)
+    gh0 = torch.empty(B, D, N, device=draw.device, dtype=torch.float32) if h0 is not None else None
+    nbytes = lib.tsfast_hip_mamba_workspace_bytes(B, L, D, N)
+    ws = _lib.workspace(nbytes, draw.device)
+    _lib.check(
+        lib.tsfast_hip_mamba_bwd(
+            B, L, D, N, _IO_DTYPES[draw.dtype],
+            *map(_lib.ptr, (draw, A, Bt, Ct, u, z, Dp, h0, chk, gout, ghlast, gdraw, gA, gBt, gCt, gu, gz, gDp, gh0, ws)),
+            nbytes, _lib.stream_of(draw),
+        ),
+        "tsfast_hip_mamba_bwd",
+    )
+    return gdraw, gA, gBt, gCt, gu, gz, gDp, (gh0 if gh0 is not None else draw.new_empty(0, dtype=torch.float32))
+
+
+@_scan_bwd_op.register_fake
+def _(gout, ghlast, chk, draw, A, Bt, Ct, u, z, Dp, h0):
+    B, L, D = draw.shape
+    N = A.shape[-1]
+    f32 = torch.float32
+    return (
+        torch.empty_like(draw),
+        draw.new_empty(D, N, dtype=f32),
+        torch.empty_like(Bt),
+        torch.empty_like(Ct),
+        torch.empty_like(draw),
+        torch.empty_like(draw),
+        draw.new_empty(D, dtype=f32),
+        (draw.new_empty(B, D, N, dtype=f32) if h0 is not None else draw.new_empty(0, dtype=f32)),
+    )
+
+
+def _scan_setup(ctx, inputs, output):
+    draw, A, Bt, Ct, u, z, Dp, h0 = inputs
+    ctx.save_for_backward(draw, A, Bt, Ct, u, z, Dp, h0, output[2])
+
+
+def _scan_backward(ctx, gout, ghlast, gchk):
+    draw, A, Bt, Ct, u, z, Dp, h0, chk = ctx.saved_tensors
+    if gout is None:
+        gout = torch.zeros_like(draw)
+    gdraw, gA, gBt, gCt, gu, gz, gDp, gh0 = _scan_bwd_op(gout, ghlast, chk, draw, A, Bt, Ct, u, z, Dp, h0)
+    return gdraw, gA, gBt, gCt, gu, gz, gDp, (gh0 if h0 is not None else None)
+
+
+_scan_train_op.register_autograd(_scan_backward, setup_context=_scan_setup)
+
+
+def run(draw, A, Bt, Ct, u, z, Dp, h0):
+    """Fused Mamba SSM: ``h_t = exp(softplus(draw_t) A) h_{t-1} + softplus(draw_t) u_t B_t``,
+    ``out_t = (h_t . C_t + Dp u_t) * silu(z_t)``.
+
+    Returns ``(out [B, L, D], h_last [B, D, N] float32)``; differentiable in all inputs. Without
+    grad the inference op (no checkpoints) runs. (Contract of ``mamba_triton.py:523-534``.)
+    """
+    inputs = (draw, A, Bt, Ct, u, z, Dp) + ((h0,) if h0 is not None else ())
+    if not torch.is_grad_enabled() or not any(t.requires_grad for t in inputs):
+        return _scan_op(draw, A, Bt, Ct, u, z, Dp, h0)
+    out, h_last, _chk = _scan_train_op(draw, A, Bt, Ct, u, z, Dp, h0)
+    return out, h_last
