@@ -58,3 +58,22 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.tsfast_hip_mamba_fwd(1, 1, 1, 65, 0, *([None] * 12)) == -3
     # empty problems are a no-op
     assert lib.tsfast_hip_diag_fwd(0, 5, 3, 0, None, None, None, None, None, 0, None) == 0
+
+
+def _declared_arity():
+    text = (ROOT / "include" / "tsfast_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(tsfast_hip_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_loader_arity_matches_header():
+    """ctypes argtypes must have exactly the header's parameter count (a short list shifts the
+    stream handle into the wrong slot)."""
+    arity = _declared_arity()
+    assert sorted(arity) == _declared()
+    for name, (argtypes, _) in _lib._SIGNATURES.items():
+        assert len(argtypes) == arity[name], name

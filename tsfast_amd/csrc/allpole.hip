@@ -8,6 +8,10 @@
 // (y0[j] = y_{-1-j}). The recurrence order NA is a template parameter (1..16), so the delay
 // line s_0..s_{NA-1} (s_k = y_{t-1-k}) lives in registers and a step is NA FMAs.
 //
+// Arithmetic: fp32 in and out, fp64 inside (delay line, transfer matrices, carries, grad
+// accumulators). High-order direct-form filters amplify fp32 rounding badly (order 16 with
+// poles near 0.98 loses ~3 digits), and the scan is HBM-bound, so the wider state is free.
+//
 // Parallel structure: time is cut into chunks of T_c steps and every (lane, chunk) pair is a
 // thread. The state entering a chunk is the last NA outputs before it. A chunk maps its
 // entering state s to  M s + e,  with M = C^{T_c} the companion matrix raised to the chunk
@@ -42,17 +46,17 @@ int64_t allpole_chunk(int64_t lanes, int64_t L, int64_t na) {
 // 1. M = C^{T_c} for the companion matrix C of lane `lane`: row 0 is (-a_1 .. -a_NA), row k is
 //    the unit shift e_{k-1}. Stored row-major per lane.
 template <int NA>
-__global__ void __launch_bounds__(256) allpole_transfer(const float* __restrict__ a, float* __restrict__ Mout,
+__global__ void __launch_bounds__(256) allpole_transfer(const float* __restrict__ a, double* __restrict__ Mout,
                                                         int64_t lanes, int64_t T_c) {
   const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (lane >= lanes) return;
-  float P[NA][NA], R[NA][NA], T[NA][NA];
+  double P[NA][NA], R[NA][NA], T[NA][NA];
 #pragma unroll
   for (int r = 0; r < NA; ++r)
 #pragma unroll
     for (int c = 0; c < NA; ++c) {
-      P[r][c] = (r == 0) ? -a[lane * NA + c] : (c == r - 1 ? 1.0f : 0.0f);
-      R[r][c] = (r == c) ? 1.0f : 0.0f;
+      P[r][c] = (r == 0) ? -(double)a[lane * NA + c] : (c == r - 1 ? 1.0 : 0.0);
+      R[r][c] = (r == c) ? 1.0 : 0.0;
     }
   int64_t k = T_c;
   while (k > 0) {
@@ -61,9 +65,9 @@ __global__ void __launch_bounds__(256) allpole_transfer(const float* __restrict_
       for (int r = 0; r < NA; ++r)
 #pragma unroll
         for (int c = 0; c < NA; ++c) {
-          float s = 0.0f;
+          double s = 0.0;
 #pragma unroll
-          for (int j = 0; j < NA; ++j) s = fmaf(R[r][j], P[j][c], s);
+          for (int j = 0; j < NA; ++j) s = fma(R[r][j], P[j][c], s);
           T[r][c] = s;
         }
 #pragma unroll
@@ -77,9 +81,9 @@ __global__ void __launch_bounds__(256) allpole_transfer(const float* __restrict_
       for (int r = 0; r < NA; ++r)
 #pragma unroll
         for (int c = 0; c < NA; ++c) {
-          float s = 0.0f;
+          double s = 0.0;
 #pragma unroll
-          for (int j = 0; j < NA; ++j) s = fmaf(P[r][j], P[j][c], s);
+          for (int j = 0; j < NA; ++j) s = fma(P[r][j], P[j][c], s);
           T[r][c] = s;
         }
 #pragma unroll
@@ -96,10 +100,10 @@ __global__ void __launch_bounds__(256) allpole_transfer(const float* __restrict_
 
 // One filter step on the register delay line: returns the new output and shifts it in.
 template <int NA>
-TSF_DEV float step(const float (&av)[NA], float (&s)[NA], float x) {
-  float acc = x;
+TSF_DEV double step(const double (&av)[NA], double (&s)[NA], double x) {
+  double acc = x;
 #pragma unroll
-  for (int k = 0; k < NA; ++k) acc = fmaf(-av[k], s[k], acc);
+  for (int k = 0; k < NA; ++k) acc = fma(-av[k], s[k], acc);
 #pragma unroll
   for (int k = NA - 1; k > 0; --k) s[k] = s[k - 1];
   s[0] = acc;
@@ -109,46 +113,46 @@ TSF_DEV float step(const float (&av)[NA], float (&s)[NA], float x) {
 // 2. forward chunk ends from a zero entering state, chunks 0 .. nchunk-2.
 template <int NA>
 __global__ void __launch_bounds__(256) allpole_fwd_chunk_end(const float* __restrict__ a, const float* __restrict__ w,
-                                                             float* __restrict__ e, int64_t lanes, int64_t L,
+                                                             double* __restrict__ e, int64_t lanes, int64_t L,
                                                              int64_t T_c, int64_t nchunk) {
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int64_t lane = gid % lanes, c = gid / lanes;
   if (c >= nchunk - 1) return;
-  float av[NA], s[NA];
+  double av[NA], s[NA];
 #pragma unroll
   for (int k = 0; k < NA; ++k) {
-    av[k] = a[lane * NA + k];
-    s[k] = 0.0f;
+    av[k] = (double)a[lane * NA + k];
+    s[k] = 0.0;
   }
   const float* wp = w + lane * L + c * T_c;
-  for (int64_t i = 0; i < T_c; ++i) step<NA>(av, s, wp[i]);
+  for (int64_t i = 0; i < T_c; ++i) step<NA>(av, s, (double)wp[i]);
 #pragma unroll
   for (int k = 0; k < NA; ++k) e[(c * lanes + lane) * NA + k] = s[k];
 }
 
 // 3. forward carries: entering state of every chunk, sequential over chunks per lane.
 template <int NA>
-__global__ void __launch_bounds__(256) allpole_fwd_carry(const float* __restrict__ M, const float* __restrict__ e,
-                                                         const float* __restrict__ y0, float* __restrict__ S,
+__global__ void __launch_bounds__(256) allpole_fwd_carry(const double* __restrict__ M, const double* __restrict__ e,
+                                                         const float* __restrict__ y0, double* __restrict__ S,
                                                          int64_t lanes, int64_t nchunk) {
   const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (lane >= lanes) return;
-  float m[NA][NA], s[NA], t[NA];
+  double m[NA][NA], s[NA], t[NA];
 #pragma unroll
   for (int r = 0; r < NA; ++r)
 #pragma unroll
     for (int c = 0; c < NA; ++c) m[r][c] = M[(lane * NA + r) * NA + c];
 #pragma unroll
-  for (int k = 0; k < NA; ++k) s[k] = y0 ? y0[lane * NA + k] : 0.0f;
+  for (int k = 0; k < NA; ++k) s[k] = y0 ? (double)y0[lane * NA + k] : 0.0;
   for (int64_t c = 0; c < nchunk; ++c) {
 #pragma unroll
     for (int k = 0; k < NA; ++k) S[(c * lanes + lane) * NA + k] = s[k];
     if (c + 1 < nchunk) {
 #pragma unroll
       for (int r = 0; r < NA; ++r) {
-        float acc = e[(c * lanes + lane) * NA + r];
+        double acc = e[(c * lanes + lane) * NA + r];
 #pragma unroll
-        for (int j = 0; j < NA; ++j) acc = fmaf(m[r][j], s[j], acc);
+        for (int j = 0; j < NA; ++j) acc = fma(m[r][j], s[j], acc);
         t[r] = acc;
       }
 #pragma unroll
@@ -160,43 +164,43 @@ __global__ void __launch_bounds__(256) allpole_fwd_carry(const float* __restrict
 // 4. forward apply.
 template <int NA>
 __global__ void __launch_bounds__(256) allpole_fwd_apply(const float* __restrict__ a, const float* __restrict__ w,
-                                                         const float* __restrict__ S, float* __restrict__ y,
+                                                         const double* __restrict__ S, float* __restrict__ y,
                                                          int64_t lanes, int64_t L, int64_t T_c, int64_t nchunk) {
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int64_t lane = gid % lanes, c = gid / lanes;
   if (c >= nchunk) return;
-  float av[NA], s[NA];
+  double av[NA], s[NA];
 #pragma unroll
   for (int k = 0; k < NA; ++k) {
-    av[k] = a[lane * NA + k];
+    av[k] = (double)a[lane * NA + k];
     s[k] = S[(c * lanes + lane) * NA + k];
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const float* wp = w + lane * L + t0;
   float* yp = y + lane * L + t0;
-  for (int64_t i = 0; i < len; ++i) yp[i] = step<NA>(av, s, wp[i]);
+  for (int64_t i = 0; i < len; ++i) yp[i] = (float)step<NA>(av, s, (double)wp[i]);
 }
 
 // Backward 2. reverse chunk exits (G_{t0}, G_{t0+1}, ...) with zero entering state, chunks >= 1.
 template <int NA>
 __global__ void __launch_bounds__(256) allpole_bwd_chunk_start(const float* __restrict__ a,
-                                                               const float* __restrict__ g, float* __restrict__ f,
+                                                               const float* __restrict__ g, double* __restrict__ f,
                                                                int64_t lanes, int64_t L, int64_t T_c,
                                                                int64_t nchunk) {
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int64_t lane = gid % lanes, c = gid / lanes + 1;
   if (c >= nchunk) return;
-  float av[NA], s[NA];
+  double av[NA], s[NA];
 #pragma unroll
   for (int k = 0; k < NA; ++k) {
-    av[k] = a[lane * NA + k];
-    s[k] = 0.0f;
+    av[k] = (double)a[lane * NA + k];
+    s[k] = 0.0;
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const float* gp = g + lane * L + t0;
-  for (int64_t i = len - 1; i >= 0; --i) step<NA>(av, s, gp[i]);
+  for (int64_t i = len - 1; i >= 0; --i) step<NA>(av, s, (double)gp[i]);
 #pragma unroll
   for (int k = 0; k < NA; ++k) f[(c * lanes + lane) * NA + k] = s[k];
 }
@@ -204,17 +208,17 @@ __global__ void __launch_bounds__(256) allpole_bwd_chunk_start(const float* __re
 // Backward 3. entering (from the right) states of every chunk: R_last = 0, R_{last-1} = f_last,
 // R_c = M R_{c+1} + f_{c+1}.
 template <int NA>
-__global__ void __launch_bounds__(256) allpole_bwd_carry(const float* __restrict__ M, const float* __restrict__ f,
-                                                         float* __restrict__ R, int64_t lanes, int64_t nchunk) {
+__global__ void __launch_bounds__(256) allpole_bwd_carry(const double* __restrict__ M, const double* __restrict__ f,
+                                                         double* __restrict__ R, int64_t lanes, int64_t nchunk) {
   const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (lane >= lanes) return;
-  float m[NA][NA], s[NA], t[NA];
+  double m[NA][NA], s[NA], t[NA];
 #pragma unroll
   for (int r = 0; r < NA; ++r)
 #pragma unroll
     for (int c = 0; c < NA; ++c) m[r][c] = M[(lane * NA + r) * NA + c];
 #pragma unroll
-  for (int k = 0; k < NA; ++k) s[k] = 0.0f;
+  for (int k = 0; k < NA; ++k) s[k] = 0.0;
   for (int64_t c = nchunk - 1; c >= 0; --c) {
 #pragma unroll
     for (int k = 0; k < NA; ++k) R[(c * lanes + lane) * NA + k] = s[k];
@@ -223,10 +227,10 @@ __global__ void __launch_bounds__(256) allpole_bwd_carry(const float* __restrict
       const bool last = (c == nchunk - 1);  // its entering state is zero, M is irrelevant
 #pragma unroll
       for (int r = 0; r < NA; ++r) {
-        float acc = f[(c * lanes + lane) * NA + r];
+        double acc = f[(c * lanes + lane) * NA + r];
         if (!last) {
 #pragma unroll
-          for (int j = 0; j < NA; ++j) acc = fmaf(m[r][j], s[j], acc);
+          for (int j = 0; j < NA; ++j) acc = fma(m[r][j], s[j], acc);
         }
         t[r] = acc;
       }
@@ -239,18 +243,18 @@ __global__ void __launch_bounds__(256) allpole_bwd_carry(const float* __restrict
 // Backward 4. reverse apply: G_t, gw = G, and grad_a partials sum_u G_{u+1+k} y_u per chunk.
 template <int NA>
 __global__ void __launch_bounds__(256) allpole_bwd_apply(const float* __restrict__ a, const float* __restrict__ g,
-                                                         const float* __restrict__ y, const float* __restrict__ R,
-                                                         float* __restrict__ gw, float* __restrict__ ga_part,
+                                                         const float* __restrict__ y, const double* __restrict__ R,
+                                                         float* __restrict__ gw, double* __restrict__ ga_part,
                                                          int64_t lanes, int64_t L, int64_t T_c, int64_t nchunk) {
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int64_t lane = gid % lanes, c = gid / lanes;
   if (c >= nchunk) return;
-  float av[NA], s[NA], ga[NA];
+  double av[NA], s[NA], ga[NA];
 #pragma unroll
   for (int k = 0; k < NA; ++k) {
-    av[k] = a[lane * NA + k];
+    av[k] = (double)a[lane * NA + k];
     s[k] = R[(c * lanes + lane) * NA + k];
-    ga[k] = 0.0f;
+    ga[k] = 0.0;
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
@@ -258,10 +262,10 @@ __global__ void __launch_bounds__(256) allpole_bwd_apply(const float* __restrict
   const float* yp = y + lane * L + t0;
   float* gwp = gw + lane * L + t0;
   for (int64_t i = len - 1; i >= 0; --i) {
-    const float yu = yp[i];
+    const double yu = yp[i];
 #pragma unroll
-    for (int k = 0; k < NA; ++k) ga[k] = fmaf(s[k], yu, ga[k]);  // s_k = G_{u+1+k} before the step
-    gwp[i] = step<NA>(av, s, gp[i]);
+    for (int k = 0; k < NA; ++k) ga[k] = fma(s[k], yu, ga[k]);  // s_k = G_{u+1+k} before the step
+    gwp[i] = (float)step<NA>(av, s, (double)gp[i]);
   }
 #pragma unroll
   for (int k = 0; k < NA; ++k) ga_part[(c * lanes + lane) * NA + k] = ga[k];
@@ -271,32 +275,32 @@ __global__ void __launch_bounds__(256) allpole_bwd_apply(const float* __restrict
 template <int NA>
 __global__ void __launch_bounds__(256) allpole_bwd_finish(const float* __restrict__ a, const float* __restrict__ gw,
                                                           const float* __restrict__ y0,
-                                                          const float* __restrict__ ga_part, float* __restrict__ ga,
+                                                          const double* __restrict__ ga_part, float* __restrict__ ga,
                                                           float* __restrict__ gy0, int64_t lanes, int64_t L,
                                                           int64_t nchunk) {
   const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (lane >= lanes) return;
-  float Gh[NA];  // G_0 .. G_{NA-1}, zero past the end of the sequence
+  double Gh[NA];  // G_0 .. G_{NA-1}, zero past the end of the sequence
 #pragma unroll
-  for (int k = 0; k < NA; ++k) Gh[k] = (k < L) ? gw[lane * L + k] : 0.0f;
+  for (int k = 0; k < NA; ++k) Gh[k] = (k < L) ? (double)gw[lane * L + k] : 0.0;
 #pragma unroll
   for (int k = 0; k < NA; ++k) {
-    float acc = 0.0f;
+    double acc = 0.0;
     for (int64_t c = 0; c < nchunk; ++c) acc += ga_part[(c * lanes + lane) * NA + k];
     if (y0) {
       // a_i (i = k + 1) also multiplied y_{t-i} = y0[i-t-1] for t < i
 #pragma unroll
-      for (int j = 1; j <= k + 1; ++j) acc = fmaf(Gh[k + 1 - j], y0[lane * NA + j - 1], acc);
+      for (int j = 1; j <= k + 1; ++j) acc = fma(Gh[k + 1 - j], (double)y0[lane * NA + j - 1], acc);
     }
-    ga[lane * NA + k] = -acc;
+    ga[lane * NA + k] = (float)(-acc);
   }
   if (y0 && gy0) {
 #pragma unroll
     for (int j = 0; j < NA; ++j) {
-      float acc = 0.0f;
+      double acc = 0.0;
 #pragma unroll
-      for (int i = j + 1; i <= NA; ++i) acc = fmaf(a[lane * NA + i - 1], Gh[i - 1 - j], acc);
-      gy0[lane * NA + j] = -acc;
+      for (int i = j + 1; i <= NA; ++i) acc = fma((double)a[lane * NA + i - 1], Gh[i - 1 - j], acc);
+      gy0[lane * NA + j] = (float)(-acc);
     }
   }
 }
@@ -310,7 +314,7 @@ Plan plan(int64_t lanes, int64_t L, int64_t na) {
   Plan p;
   p.T_c = allpole_chunk(lanes, L, na);
   p.nchunk = (L + p.T_c - 1) / p.T_c;
-  const size_t f = 4;
+  const size_t f = 8;  // fp64 transfer matrices, carries and partials
   p.off_M = 0;
   p.off_e = p.off_M + f * lanes * na * na;
   p.off_S = p.off_e + f * p.nchunk * lanes * na;
@@ -323,9 +327,9 @@ template <int NA>
 int fwd_impl(int64_t lanes, int64_t L, const float* a, const float* w, const float* y0, float* y, char* ws,
              hipStream_t s) {
   const Plan p = plan(lanes, L, NA);
-  float* M = reinterpret_cast<float*>(ws + p.off_M);
-  float* e = reinterpret_cast<float*>(ws + p.off_e);
-  float* S = reinterpret_cast<float*>(ws + p.off_S);
+  double* M = reinterpret_cast<double*>(ws + p.off_M);
+  double* e = reinterpret_cast<double*>(ws + p.off_e);
+  double* S = reinterpret_cast<double*>(ws + p.off_S);
   hipLaunchKernelGGL((allpole_transfer<NA>), grid_for(lanes), dim3(256), 0, s, a, M, lanes, p.T_c);
   if (p.nchunk > 1)
     hipLaunchKernelGGL((allpole_fwd_chunk_end<NA>), grid_for(lanes * (p.nchunk - 1)), dim3(256), 0, s, a, w, e, lanes,
@@ -340,10 +344,10 @@ template <int NA>
 int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* a, const float* y, const float* y0, float* gw,
              float* ga, float* gy0, char* ws, hipStream_t s) {
   const Plan p = plan(lanes, L, NA);
-  float* M = reinterpret_cast<float*>(ws + p.off_M);
-  float* f = reinterpret_cast<float*>(ws + p.off_e);
-  float* R = reinterpret_cast<float*>(ws + p.off_S);
-  float* part = reinterpret_cast<float*>(ws + p.off_part);
+  double* M = reinterpret_cast<double*>(ws + p.off_M);
+  double* f = reinterpret_cast<double*>(ws + p.off_e);
+  double* R = reinterpret_cast<double*>(ws + p.off_S);
+  double* part = reinterpret_cast<double*>(ws + p.off_part);
   if (L > 0) {
     hipLaunchKernelGGL((allpole_transfer<NA>), grid_for(lanes), dim3(256), 0, s, a, M, lanes, p.T_c);
     if (p.nchunk > 1)

@@ -76,6 +76,50 @@ struct Num<float2> {
   TSF_DEV static float2 mul_conj(float2 a, float2 b) { return cmul_conj(a, b); }
 };
 
+template <>
+struct Num<double> {
+  TSF_DEV static double zero() { return 0.0; }
+  TSF_DEV static double one() { return 1.0; }
+  TSF_DEV static double mul(double a, double b) { return a * b; }
+  TSF_DEV static double fma(double a, double x, double b) { return ::fma(a, x, b); }
+  TSF_DEV static double add(double a, double b) { return a + b; }
+  TSF_DEV static double conj(double a) { return a; }
+  TSF_DEV static double mul_conj(double a, double b) { return a * b; }
+};
+template <>
+struct Num<double2> {
+  TSF_DEV static double2 zero() { return make_double2(0.0, 0.0); }
+  TSF_DEV static double2 one() { return make_double2(1.0, 0.0); }
+  TSF_DEV static double2 mul(double2 a, double2 b) {
+    return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+  }
+  TSF_DEV static double2 fma(double2 a, double2 x, double2 b) {
+    return make_double2(::fma(a.x, x.x, ::fma(-a.y, x.y, b.x)), ::fma(a.x, x.y, ::fma(a.y, x.x, b.y)));
+  }
+  TSF_DEV static double2 add(double2 a, double2 b) { return make_double2(a.x + b.x, a.y + b.y); }
+  TSF_DEV static double2 conj(double2 a) { return make_double2(a.x, -a.y); }
+  TSF_DEV static double2 mul_conj(double2 a, double2 b) {
+    return make_double2(a.x * b.x + a.y * b.y, a.y * b.x - a.x * b.y);
+  }
+};
+
+// fp32 storage type -> fp64 compute type (the scans are HBM-bound, so carrying the state in
+// double costs no time and keeps long / slowly-decaying recurrences at fp32 output accuracy).
+template <typename T>
+struct Wide;
+template <>
+struct Wide<float> {
+  using type = double;
+  TSF_DEV static double up(float x) { return (double)x; }
+  TSF_DEV static float down(double x) { return (float)x; }
+};
+template <>
+struct Wide<float2> {
+  using type = double2;
+  TSF_DEV static double2 up(float2 x) { return make_double2((double)x.x, (double)x.y); }
+  TSF_DEV static float2 down(double2 x) { return make_float2((float)x.x, (float)x.y); }
+};
+
 // x^k for an integer k >= 0 by binary powering (log2(k) squarings; exact for k = 0).
 template <typename T>
 TSF_DEV T ipow(T x, int64_t k) {

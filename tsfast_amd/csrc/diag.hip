@@ -23,49 +23,55 @@ using namespace tsf;
 
 namespace {
 
+// All kernels load fp32 (or complex64) and carry the recurrence in fp64 (complex128): W below.
 // ---------------------------------------------------------------- constant coefficient, forward
 template <typename T>
 __global__ void __launch_bounds__(256) diag_fwd_chunk_end(const T* __restrict__ lam, const T* __restrict__ v,
-                                                          T* __restrict__ carry, int64_t M, int64_t L, int64_t N,
-                                                          int64_t T_c, int64_t nchunk) {
+                                                          typename Wide<T>::type* __restrict__ carry, int64_t M,
+                                                          int64_t L, int64_t N, int64_t T_c, int64_t nchunk) {
+  using W = typename Wide<T>::type;
   const int64_t lanes = M * N;
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int64_t lane = gid % lanes;
   const int64_t c = gid / lanes;  // chunks 0 .. nchunk-2 (the last chunk's end is never needed)
   if (c >= nchunk - 1) return;
   const int64_t m = lane / N, n = lane % N;
-  const T a = lam[lane];
+  const W a = Wide<T>::up(lam[lane]);
   const T* vp = v + (m * L + c * T_c) * N + n;
-  T x = Num<T>::zero();
-  for (int64_t i = 0; i < T_c; ++i) x = Num<T>::fma(a, x, vp[i * N]);
+  W x = Num<W>::zero();
+#pragma unroll 8
+  for (int64_t i = 0; i < T_c; ++i) x = Num<W>::fma(a, x, Wide<T>::up(vp[i * N]));
   carry[c * lanes + lane] = x;
 }
 
 template <typename T>
 __global__ void __launch_bounds__(256) diag_fwd_apply(const T* __restrict__ lam, const T* __restrict__ v,
-                                                      const T* __restrict__ x0, const T* __restrict__ carry,
+                                                      const T* __restrict__ x0,
+                                                      const typename Wide<T>::type* __restrict__ carry,
                                                       T* __restrict__ out, int64_t M, int64_t L, int64_t N,
                                                       int64_t T_c, int64_t nchunk) {
+  using W = typename Wide<T>::type;
   const int64_t lanes = M * N;
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int64_t lane = gid % lanes;
   const int64_t c = gid / lanes;
   if (c >= nchunk) return;
   const int64_t m = lane / N, n = lane % N;
-  const T a = lam[lane];
+  const W a = Wide<T>::up(lam[lane]);
   // state entering chunk c: x0 carried through the full-length chunks before it
-  T x = x0 ? x0[lane] : Num<T>::zero();
+  W x = x0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
   if (c > 0) {
-    const T P = ipow(a, T_c);
-    for (int64_t j = 0; j < c; ++j) x = Num<T>::fma(P, x, carry[j * lanes + lane]);
+    const W P = ipow(a, T_c);
+    for (int64_t j = 0; j < c; ++j) x = Num<W>::fma(P, x, carry[j * lanes + lane]);
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const T* vp = v + (m * L + t0) * N + n;
   T* op = out + (m * L + t0) * N + n;
+#pragma unroll 8
   for (int64_t i = 0; i < len; ++i) {
-    x = Num<T>::fma(a, x, vp[i * N]);
-    op[i * N] = x;
+    x = Num<W>::fma(a, x, Wide<T>::up(vp[i * N]));
+    op[i * N] = Wide<T>::down(x);
   }
 }
 
@@ -73,80 +79,86 @@ __global__ void __launch_bounds__(256) diag_fwd_apply(const T* __restrict__ lam,
 // Reverse chunk summaries: G at the chunk's first step with no gradient entering from the right.
 template <typename T>
 __global__ void __launch_bounds__(256) diag_bwd_chunk_start(const T* __restrict__ lam, const T* __restrict__ g,
-                                                            T* __restrict__ carry, int64_t M, int64_t L, int64_t N,
-                                                            int64_t T_c, int64_t nchunk) {
+                                                            typename Wide<T>::type* __restrict__ carry, int64_t M,
+                                                            int64_t L, int64_t N, int64_t T_c, int64_t nchunk) {
+  using W = typename Wide<T>::type;
   const int64_t lanes = M * N;
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int64_t lane = gid % lanes;
   const int64_t c = gid / lanes + 1;  // chunks 1 .. nchunk-1 (chunk 0's start feeds nobody)
   if (c >= nchunk) return;
   const int64_t m = lane / N, n = lane % N;
-  const T ac = Num<T>::conj(lam[lane]);
+  const W ac = Num<W>::conj(Wide<T>::up(lam[lane]));
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const T* gp = g + (m * L + t0) * N + n;
-  T G = Num<T>::zero();
-  for (int64_t i = len - 1; i >= 0; --i) G = Num<T>::fma(ac, G, gp[i * N]);
+  W G = Num<W>::zero();
+#pragma unroll 8
+  for (int64_t i = len - 1; i >= 0; --i) G = Num<W>::fma(ac, G, Wide<T>::up(gp[i * N]));
   carry[c * lanes + lane] = G;
 }
 
 template <typename T>
 __global__ void __launch_bounds__(256) diag_bwd_apply(const T* __restrict__ lam, const T* __restrict__ g,
                                                       const T* __restrict__ out, const T* __restrict__ x0,
-                                                      const T* __restrict__ carry, T* __restrict__ gv,
-                                                      T* __restrict__ glam_part, T* __restrict__ gx0, int64_t M,
-                                                      int64_t L, int64_t N, int64_t T_c, int64_t nchunk) {
+                                                      const typename Wide<T>::type* __restrict__ carry,
+                                                      T* __restrict__ gv, typename Wide<T>::type* __restrict__ glam_part,
+                                                      T* __restrict__ gx0, int64_t M, int64_t L, int64_t N,
+                                                      int64_t T_c, int64_t nchunk) {
+  using W = typename Wide<T>::type;
   const int64_t lanes = M * N;
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int64_t lane = gid % lanes;
   const int64_t c = gid / lanes;
   if (c >= nchunk) return;
   const int64_t m = lane / N, n = lane % N;
-  const T ac = Num<T>::conj(lam[lane]);
+  const W ac = Num<W>::conj(Wide<T>::up(lam[lane]));
   // G at the first step of chunk c+1: fold the chunk summaries from the right end inwards.
   // Every chunk but the last has full length, and the last one receives no gradient.
-  T R = Num<T>::zero();
+  W R = Num<W>::zero();
   if (c + 1 < nchunk) {
-    const T P = ipow(ac, T_c);
+    const W P = ipow(ac, T_c);
     R = carry[(nchunk - 1) * lanes + lane];
-    for (int64_t j = nchunk - 2; j > c; --j) R = Num<T>::fma(P, R, carry[j * lanes + lane]);
+    for (int64_t j = nchunk - 2; j > c; --j) R = Num<W>::fma(P, R, carry[j * lanes + lane]);
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const T* gp = g + (m * L + t0) * N + n;
   const T* xp = out + (m * L + t0) * N + n;
   T* gvp = gv + (m * L + t0) * N + n;
-  T G = R;
-  T acc = Num<T>::zero();
+  W G = R;
+  W acc = Num<W>::zero();
+#pragma unroll 8
   for (int64_t i = len - 1; i >= 0; --i) {
-    G = Num<T>::fma(ac, G, gp[i * N]);
-    gvp[i * N] = G;
-    T xprev;
+    G = Num<W>::fma(ac, G, Wide<T>::up(gp[i * N]));
+    gvp[i * N] = Wide<T>::down(G);
+    W xprev;
     if (t0 + i > 0)
-      xprev = xp[(i - 1) * N];
+      xprev = Wide<T>::up(xp[(i - 1) * N]);
     else
-      xprev = x0 ? x0[lane] : Num<T>::zero();
-    acc = Num<T>::add(acc, Num<T>::mul_conj(G, xprev));
+      xprev = x0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
+    acc = Num<W>::add(acc, Num<W>::mul_conj(G, xprev));
   }
   glam_part[c * lanes + lane] = acc;
-  if (c == 0 && gx0) gx0[lane] = Num<T>::mul(ac, G);
+  if (c == 0 && gx0) gx0[lane] = Wide<T>::down(Num<W>::mul(ac, G));
 }
 
 // Sum of per-chunk partials in a fixed order (deterministic run to run).
 template <typename T>
-__global__ void __launch_bounds__(256) sum_chunks(const T* __restrict__ part, T* __restrict__ dst, int64_t lanes,
-                                                  int64_t nchunk) {
+__global__ void __launch_bounds__(256) sum_chunks(const typename Wide<T>::type* __restrict__ part,
+                                                  T* __restrict__ dst, int64_t lanes, int64_t nchunk) {
+  using W = typename Wide<T>::type;
   const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (lane >= lanes) return;
-  T s = Num<T>::zero();
-  for (int64_t c = 0; c < nchunk; ++c) s = Num<T>::add(s, part[c * lanes + lane]);
-  dst[lane] = s;
+  W s = Num<W>::zero();
+  for (int64_t c = 0; c < nchunk; ++c) s = Num<W>::add(s, part[c * lanes + lane]);
+  dst[lane] = Wide<T>::down(s);
 }
 
 // ---------------------------------------------------------------- time-varying coefficient (real)
 // Pass-1 summary of a forward chunk: (product of its coefficients, end state from zero).
 __global__ void __launch_bounds__(256) sel_fwd_chunk_end(const float* __restrict__ a, const float* __restrict__ v,
-                                                         float2* __restrict__ carry, int64_t M, int64_t L, int64_t N,
+                                                         double2* __restrict__ carry, int64_t M, int64_t L, int64_t N,
                                                          int64_t T_c, int64_t nchunk) {
   const int64_t lanes = M * N;
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -155,17 +167,18 @@ __global__ void __launch_bounds__(256) sel_fwd_chunk_end(const float* __restrict
   if (c >= nchunk - 1) return;
   const int64_t m = lane / N, n = lane % N;
   const int64_t off = (m * L + c * T_c) * N + n;
-  float P = 1.0f, x = 0.0f;
+  double P = 1.0, x = 0.0;
+#pragma unroll 8
   for (int64_t i = 0; i < T_c; ++i) {
-    const float at = a[off + i * N];
-    x = fmaf(at, x, v[off + i * N]);
+    const double at = a[off + i * N];
+    x = fma(at, x, (double)v[off + i * N]);
     P *= at;
   }
-  carry[c * lanes + lane] = make_float2(P, x);
+  carry[c * lanes + lane] = make_double2(P, x);
 }
 
 __global__ void __launch_bounds__(256) sel_fwd_apply(const float* __restrict__ a, const float* __restrict__ v,
-                                                     const float* __restrict__ x0, const float2* __restrict__ carry,
+                                                     const float* __restrict__ x0, const double2* __restrict__ carry,
                                                      float* __restrict__ out, int64_t M, int64_t L, int64_t N,
                                                      int64_t T_c, int64_t nchunk) {
   const int64_t lanes = M * N;
@@ -174,17 +187,18 @@ __global__ void __launch_bounds__(256) sel_fwd_apply(const float* __restrict__ a
   const int64_t c = gid / lanes;
   if (c >= nchunk) return;
   const int64_t m = lane / N, n = lane % N;
-  float x = x0 ? x0[lane] : 0.0f;
+  double x = x0 ? (double)x0[lane] : 0.0;
   for (int64_t j = 0; j < c; ++j) {
-    const float2 pe = carry[j * lanes + lane];
-    x = fmaf(pe.x, x, pe.y);
+    const double2 pe = carry[j * lanes + lane];
+    x = fma(pe.x, x, pe.y);
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const int64_t off = (m * L + t0) * N + n;
+#pragma unroll 8
   for (int64_t i = 0; i < len; ++i) {
-    x = fmaf(a[off + i * N], x, v[off + i * N]);
-    out[off + i * N] = x;
+    x = fma((double)a[off + i * N], x, (double)v[off + i * N]);
+    out[off + i * N] = (float)x;
   }
 }
 
@@ -192,8 +206,8 @@ __global__ void __launch_bounds__(256) sel_fwd_apply(const float* __restrict__ a
 // multiplier of the entering gradient, prod_{s=t0+1..t1} a_s (a_{t1} is the next chunk's first
 // coefficient; the last chunk has no entering gradient, so its multiplier is never used).
 __global__ void __launch_bounds__(256) sel_bwd_chunk_start(const float* __restrict__ a, const float* __restrict__ g,
-                                                           float2* __restrict__ carry, int64_t M, int64_t L, int64_t N,
-                                                           int64_t T_c, int64_t nchunk) {
+                                                           double2* __restrict__ carry, int64_t M, int64_t L,
+                                                           int64_t N, int64_t T_c, int64_t nchunk) {
   const int64_t lanes = M * N;
   const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int64_t lane = gid % lanes;
@@ -203,21 +217,21 @@ __global__ void __launch_bounds__(256) sel_bwd_chunk_start(const float* __restri
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const int64_t off = (m * L + t0) * N + n;
-  float G = 0.0f, P = 1.0f;
+  double G = 0.0, P = 1.0;
   for (int64_t i = len - 1; i >= 0; --i) {
     // G_t = g_t + a_{t+1} G_{t+1}; inside the chunk a_{t+1} is at i+1
-    const float an = (i + 1 < len) ? a[off + (i + 1) * N] : 1.0f;
-    G = fmaf(an, G, g[off + i * N]);
-    if (i + 1 < len) P *= an;
+    const double an = (i + 1 < len) ? (double)a[off + (i + 1) * N] : 1.0;
+    G = fma(an, G, (double)g[off + i * N]);
+    P *= an;
   }
-  // entering gradient enters through a_{t1} (first coefficient of the next chunk)
+  // the entering gradient passes through a_{t1}, the next chunk's first coefficient
   if (t0 + len < L) P *= a[off + len * N];
-  carry[c * lanes + lane] = make_float2(P, G);
+  carry[c * lanes + lane] = make_double2(P, G);
 }
 
 __global__ void __launch_bounds__(256) sel_bwd_apply(const float* __restrict__ a, const float* __restrict__ g,
                                                      const float* __restrict__ out, const float* __restrict__ x0,
-                                                     const float2* __restrict__ carry, float* __restrict__ glam,
+                                                     const double2* __restrict__ carry, float* __restrict__ glam,
                                                      float* __restrict__ gv, float* __restrict__ gx0, int64_t M,
                                                      int64_t L, int64_t N, int64_t T_c, int64_t nchunk) {
   const int64_t lanes = M * N;
@@ -227,28 +241,28 @@ __global__ void __launch_bounds__(256) sel_bwd_apply(const float* __restrict__ a
   if (c >= nchunk) return;
   const int64_t m = lane / N, n = lane % N;
   // G_{t1} (first step of chunk c+1), folded from the right end
-  float R = 0.0f;
+  double R = 0.0;
   if (c + 1 < nchunk) {
     R = carry[(nchunk - 1) * lanes + lane].y;
     for (int64_t j = nchunk - 2; j > c; --j) {
-      const float2 pe = carry[j * lanes + lane];
+      const double2 pe = carry[j * lanes + lane];
       // pe.x multiplies G at the first step of chunk j+1
-      R = fmaf(pe.x, R, pe.y);
+      R = fma(pe.x, R, pe.y);
     }
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const int64_t off = (m * L + t0) * N + n;
-  float G = R;
+  double G = R;
   for (int64_t i = len - 1; i >= 0; --i) {
     const int64_t t = t0 + i;
-    const float an = (t + 1 < L) ? a[off + (i + 1) * N] : 1.0f;
-    G = fmaf(an, G, g[off + i * N]);
-    gv[off + i * N] = G;
-    const float xprev = (t > 0) ? out[off + (i - 1) * N] : (x0 ? x0[lane] : 0.0f);
-    glam[off + i * N] = G * xprev;
+    const double an = (t + 1 < L) ? (double)a[off + (i + 1) * N] : 1.0;
+    G = fma(an, G, (double)g[off + i * N]);
+    gv[off + i * N] = (float)G;
+    const double xprev = (t > 0) ? (double)out[off + (i - 1) * N] : (x0 ? (double)x0[lane] : 0.0);
+    glam[off + i * N] = (float)(G * xprev);
   }
-  if (c == 0 && gx0) gx0[lane] = a[off] * G;
+  if (c == 0 && gx0) gx0[lane] = (float)((double)a[off] * G);
 }
 
 // Chunk length: enough (lane, chunk) threads to cover the device several times over, but
@@ -272,8 +286,8 @@ int64_t tsfast_hip_diag_workspace_bytes(int64_t M, int64_t L, int64_t N, int is_
   const int64_t lanes = M * N;
   const int64_t T_c = pick_chunk(lanes, L);
   const int64_t nchunk = (L + T_c - 1) / T_c;
-  // carries [nchunk, lanes] plus glam partials [nchunk, lanes] (complex elements when complex)
-  return 2 * nchunk * lanes * (is_complex ? 8 : 4);
+  // fp64 carries [nchunk, lanes] plus fp64 glam partials [nchunk, lanes] (complex128 when complex)
+  return 2 * nchunk * lanes * (is_complex ? 16 : 8);
 }
 
 int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const void* lam, const void* v,
@@ -287,14 +301,14 @@ int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   const int64_t T_c = pick_chunk(lanes, L);
   const int64_t nchunk = (L + T_c - 1) / T_c;
   if (is_complex) {
-    auto* c = static_cast<float2*>(workspace);
+    auto* c = static_cast<double2*>(workspace);
     if (nchunk > 1)
       hipLaunchKernelGGL(diag_fwd_chunk_end<float2>, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s,
                          (const float2*)lam, (const float2*)v, c, M, L, N, T_c, nchunk);
     hipLaunchKernelGGL(diag_fwd_apply<float2>, grid_for(lanes * nchunk), dim3(256), 0, s, (const float2*)lam,
                        (const float2*)v, (const float2*)x0, c, (float2*)out, M, L, N, T_c, nchunk);
   } else {
-    auto* c = static_cast<float*>(workspace);
+    auto* c = static_cast<double*>(workspace);
     if (nchunk > 1)
       hipLaunchKernelGGL(diag_fwd_chunk_end<float>, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s,
                          (const float*)lam, (const float*)v, c, M, L, N, T_c, nchunk);
@@ -308,11 +322,10 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
                         const void* out, const void* x0, void* gv, void* glam, void* gx0, void* workspace,
                         int64_t workspace_bytes, void* stream) {
   if (M < 0 || L < 0 || N < 0) return TSF_ERR_ARG;
-  if (!g || !lam || !out || !gv || !glam) return TSF_ERR_ARG;
-  if (x0 && !gx0) return TSF_ERR_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t lanes = M * N;
   if (lanes == 0) return TSF_OK;
+  if (!lam || !glam || (x0 && !gx0)) return TSF_ERR_ARG;
   if (L == 0) {
     // empty sequence: every gradient is zero
     const size_t esz = is_complex ? 8 : 4;
@@ -320,11 +333,12 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
     if (gx0 && hipMemsetAsync(gx0, 0, lanes * esz, s) != hipSuccess) return TSF_ERR_HIP;
     return TSF_OK;
   }
+  if (!g || !out || !gv) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
   const int64_t T_c = pick_chunk(lanes, L);
   const int64_t nchunk = (L + T_c - 1) / T_c;
   if (is_complex) {
-    auto* c = static_cast<float2*>(workspace);
+    auto* c = static_cast<double2*>(workspace);
     auto* part = c + nchunk * lanes;
     if (nchunk > 1)
       hipLaunchKernelGGL(diag_bwd_chunk_start<float2>, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s,
@@ -334,7 +348,7 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
                        L, N, T_c, nchunk);
     hipLaunchKernelGGL(sum_chunks<float2>, grid_for(lanes), dim3(256), 0, s, part, (float2*)glam, lanes, nchunk);
   } else {
-    auto* c = static_cast<float*>(workspace);
+    auto* c = static_cast<double*>(workspace);
     auto* part = c + nchunk * lanes;
     if (nchunk > 1)
       hipLaunchKernelGGL(diag_bwd_chunk_start<float>, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s,
@@ -351,7 +365,7 @@ int64_t tsfast_hip_sel_workspace_bytes(int64_t M, int64_t L, int64_t N) {
   const int64_t lanes = M * N;
   const int64_t T_c = pick_chunk(lanes, L);
   const int64_t nchunk = (L + T_c - 1) / T_c;
-  return nchunk * lanes * 8;  // (product, state) pairs
+  return nchunk * lanes * 16;  // fp64 (product, state) pairs
 }
 
 int tsfast_hip_sel_fwd(int64_t M, int64_t L, int64_t N, const float* a, const float* v, const float* x0, float* out,
@@ -364,7 +378,7 @@ int tsfast_hip_sel_fwd(int64_t M, int64_t L, int64_t N, const float* a, const fl
   const int64_t lanes = M * N;
   const int64_t T_c = pick_chunk(lanes, L);
   const int64_t nchunk = (L + T_c - 1) / T_c;
-  auto* c = static_cast<float2*>(workspace);
+  auto* c = static_cast<double2*>(workspace);
   if (nchunk > 1)
     hipLaunchKernelGGL(sel_fwd_chunk_end, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s, a, v, c, M, L, N, T_c,
                        nchunk);
@@ -376,19 +390,19 @@ int tsfast_hip_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const fl
                        const float* x0, float* glam, float* gv, float* gx0, void* workspace, int64_t workspace_bytes,
                        void* stream) {
   if (M < 0 || L < 0 || N < 0) return TSF_ERR_ARG;
-  if (!g || !a || !out || !gv || !glam) return TSF_ERR_ARG;
-  if (x0 && !gx0) return TSF_ERR_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t lanes = M * N;
   if (lanes == 0) return TSF_OK;
+  if (x0 && !gx0) return TSF_ERR_ARG;
   if (L == 0) {
     if (gx0 && hipMemsetAsync(gx0, 0, lanes * 4, s) != hipSuccess) return TSF_ERR_HIP;
     return TSF_OK;
   }
+  if (!g || !a || !out || !gv || !glam) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_sel_workspace_bytes(M, L, N) || !workspace) return TSF_ERR_WORKSPACE;
   const int64_t T_c = pick_chunk(lanes, L);
   const int64_t nchunk = (L + T_c - 1) / T_c;
-  auto* c = static_cast<float2*>(workspace);
+  auto* c = static_cast<double2*>(workspace);
   if (nchunk > 1)
     hipLaunchKernelGGL(sel_bwd_chunk_start, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s, a, g, c, M, L, N, T_c,
                        nchunk);

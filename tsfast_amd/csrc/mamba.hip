@@ -393,7 +393,8 @@ int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
   const int ns = ns_for(N);
   if (ns == 0) return TSF_ERR_UNSUPPORTED;
   if (B == 0 || D == 0) return TSF_OK;
-  if (!draw || !A || !Bt || !Ct || !u || !z || !Dp || !out || !h_last) return TSF_ERR_ARG;
+  if (!A || !Dp || !h_last) return TSF_ERR_ARG;
+  if (L > 0 && (!draw || !Bt || !Ct || !u || !z || !out)) return TSF_ERR_ARG;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (io_dtype == TSF_DTYPE_F32) {
     TSF_DISPATCH_NS(ns, fwd_f32, B, L, D, N, draw, A, Bt, Ct, u, z, Dp, h0, out, h_last, chk, s)
@@ -412,8 +413,8 @@ int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
   if (B > 65535) return TSF_ERR_UNSUPPORTED;
   const int ns = ns_for(N);
   if (ns == 0) return TSF_ERR_UNSUPPORTED;
-  if (!draw || !A || !Bt || !Ct || !u || !z || !Dp || !gout || !gdraw || !gA || !gBt || !gCt || !gu || !gz || !gDp)
-    return TSF_ERR_ARG;
+  if (!A || !Dp || !gA || !gDp) return TSF_ERR_ARG;
+  if (L > 0 && (!draw || !Bt || !Ct || !u || !z || !gout || !gdraw || !gBt || !gCt || !gu || !gz)) return TSF_ERR_ARG;
   if (h0 && !gh0) return TSF_ERR_ARG;
   if (L > 0 && !chk && L > chk_interval_for(ns)) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_mamba_workspace_bytes(B, L, D, N) || !workspace) return TSF_ERR_WORKSPACE;
