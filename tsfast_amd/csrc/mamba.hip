@@ -7,28 +7,34 @@
 // Reference semantics: tsfast/models/architectures/mamba/mamba_triton.py:85-286 (kernels) and
 // :286-489 (ops), mamba/backend_c.py:105-245 (CPU kernels, same algebra).
 //
-// Thread layout: one lane per (batch b, channel d), holding all N states of that channel in
-// VGPRs; a wave covers 64 consecutive channels of one batch row, so every per-step load of
-// draw/u/z (and store of out) is one coalesced 64-element row segment, and the per-step B_t/C_t
-// rows are wave-uniform. The [B, L, D, N] state never touches HBM: the training forward writes
-// one fp32 checkpoint per channel every CHK steps, and the backward walks the checkpoints in
-// reverse, recomputes the chunk's states into registers, and runs the adjoint
-//   G_t = gy_t C_t + lam_{t+1} G_{t+1}
-// in the same pass. lam_t h_{t-1} is recovered as h_t - delta_t u_t B_t, so states before the
-// chunk are never needed. grad B_t / grad C_t are reduced over the wave's 64 channels with a
-// register reduce-scatter and written as per-wave partials that a second kernel sums in a fixed
-// order (no atomics: deterministic).
+// The scan is VALU-bound on gfx950 (one exp and ~5 (fwd) / ~15 (bwd) fp32 ops per state element
+// against 2-5 bytes of HBM traffic per element), so the layout minimises per-element VALU work
+// and keeps every SIMD busy:
+//
+//  * Workgroup = one batch row b x a tile of DT=32 channels, all N states, walking the whole
+//    sequence. NG lanes share a channel, each holding NPT = NS/NG states in VGPRs (NG = 8 for
+//    N >= 8), so the grid B * D/32 (768 workgroups of 4 waves at config 3) puts three
+//    workgroups on every CU with no tail.
+//  * Time advances in chunks of CHK steps. Per-(t, d) scalar work (softplus, sigmoid, gates,
+//    the D skip) is done once per (t, d) by an "owner" thread and staged through LDS, with
+//    coalesced 32-channel row loads/stores; each lane then runs only the per-state recurrence.
+//  * Sums over states (y = h.C in the forward; sum A Q, sum G B, sum h C in the backward) are
+//    pre-reduced between the two adjacent lanes of a state pair with one DPP swap and finished
+//    by the owner thread from LDS.
+//  * The backward recomputes each chunk's states from the forward's fp32 checkpoint into
+//    registers (lam_t and h_t for the chunk), then runs the adjoint
+//        G_t = gy_t C_t + lam_{t+1} G_{t+1}
+//    backwards through the chunk, so exp is evaluated once per element per pass.
+//  * grad B_t / grad C_t (sums over channels) are reduced over the 32 channels of the tile in
+//    LDS and written as fp32 partials [D/32, B, L, 2*NS]; a second kernel sums the partials in a
+//    fixed order (no atomics: deterministic run to run).
+// The next chunk's inputs are loaded into registers while the current chunk computes.
 #include "common.h"
 #include "tsfast_hip.h"
 
 using namespace tsf;
 
 namespace {
-
-template <int NS>
-constexpr int chk_for() {
-  return NS <= 16 ? 16 : (NS == 32 ? 8 : 4);
-}
 
 int ns_for(int64_t N) {
   if (N <= 4) return 4;
@@ -39,103 +45,245 @@ int ns_for(int64_t N) {
   return 0;
 }
 
+template <int NS>
+struct MCfg {
+  static constexpr int NG = NS >= 8 ? 8 : NS;  // lanes per channel
+  static constexpr int NPT = NS / NG;          // states per lane
+  static constexpr int DT = 32;                // channels per workgroup
+  static constexpr int TH = DT * NG;           // threads per workgroup
+  static constexpr int NPAIR = NG / 2;         // state-pair partial slots per channel
+  // checkpoint interval = backward recompute chunk (lam_t and h_t of a chunk live in VGPRs)
+  static constexpr int CHK = NPT <= 2 ? 16 : (NPT == 4 ? 8 : 4);
+  static constexpr int TB = CHK < 8 ? CHK : 8;  // backward flush sub-block
+  static constexpr int ITEMS = (CHK * DT + TH - 1) / TH;  // owned (t, d) items per thread per chunk
+  static constexpr int BCI = (CHK * NS + TH - 1) / TH;    // B/C tile elements per thread
+};
+
+// Swap with the neighbouring lane (lane ^ 1) through DPP: one VALU op, no LDS round trip.
+TSF_DEV float swap_lane1(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1 /* quad_perm [1,0,3,2] */, 0xF, 0xF, false));
+}
+
+TSF_DEV float fast_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+template <typename TIO>
+TSF_DEV TIO io_zero();
+template <>
+TSF_DEV float io_zero<float>() {
+  return 0.0f;
+}
+template <>
+TSF_DEV bf16 io_zero<bf16>() {
+  bf16 zr;
+  zr.bits = 0;
+  return zr;
+}
+
 // ------------------------------------------------------------------------------------ forward
 template <typename TIO, int NS>
-__global__ void __launch_bounds__(64) mamba_fwd_kernel(const TIO* __restrict__ draw, const float* __restrict__ A,
-                                                       const TIO* __restrict__ Bt, const TIO* __restrict__ Ct,
-                                                       const TIO* __restrict__ u, const TIO* __restrict__ z,
-                                                       const float* __restrict__ Dp, const float* __restrict__ h0,
-                                                       TIO* __restrict__ out, float* __restrict__ h_last,
-                                                       float* __restrict__ chk, int64_t L, int64_t D, int N,
-                                                       int64_t NC) {
-  constexpr int CHK = chk_for<NS>();
-  const int lane = threadIdx.x;
-  const int64_t d = (int64_t)blockIdx.x * 64 + lane;
+__global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
+    const TIO* __restrict__ draw, const float* __restrict__ A, const TIO* __restrict__ Bt,
+    const TIO* __restrict__ Ct, const TIO* __restrict__ u, const TIO* __restrict__ z, const float* __restrict__ Dp,
+    const float* __restrict__ h0, TIO* __restrict__ out, float* __restrict__ h_last, float* __restrict__ chk,
+    int64_t L, int64_t D, int N, int64_t NC) {
+  using C = MCfg<NS>;
+  constexpr int NPT = C::NPT, DT = C::DT, TH = C::TH, CHK = C::CHK, IT = C::ITEMS, BCI = C::BCI;
+  constexpr int NPAIR = C::NPAIR;
+  __shared__ float2 s_sc[CHK][DT];       // (delta, delta * u)
+  __shared__ float2 s_bc[CHK][NS];       // (B, C)
+  __shared__ float s_y[CHK][NPAIR][DT];  // y partial per state pair
+
+  const int tid = threadIdx.x;
   const int64_t b = blockIdx.y;
+  const int64_t d0 = (int64_t)blockIdx.x * DT;
+  // recurrence mapping: adjacent lanes hold the two halves of a state pair
+  const int pr = tid & 1;
+  const int dl = (tid >> 1) & (DT - 1);
+  const int ng = 2 * (tid / (2 * DT)) + pr;
+  const int n0 = ng * NPT;
+  const int64_t d = d0 + dl;
   const bool act = d < D;
+  // owner mapping: item k of this thread is (t = idx / DT, channel d0 + idx % DT), idx = tid + k * TH
+  const int od = tid % DT;
+  const int64_t odg = d0 + od;
+  const bool oact = odg < D;
 
-  float Av[NS], h[NS];
+  float A2[NPT], h[NPT];
 #pragma unroll
-  for (int n = 0; n < NS; ++n) {
-    Av[n] = (act && n < N) ? A[d * N + n] : 0.0f;
-    h[n] = (act && h0 && n < N) ? h0[(b * D + d) * N + n] : 0.0f;
+  for (int j = 0; j < NPT; ++j) {
+    const int n = n0 + j;
+    A2[j] = (act && n < N) ? A[d * N + n] * kLog2e : 0.0f;
+    h[j] = (act && h0 && n < N) ? h0[(b * D + d) * N + n] : 0.0f;
   }
-  const float dp = act ? Dp[d] : 0.0f;
-  const TIO* Bb = Bt + b * L * N;
-  const TIO* Cb = Ct + b * L * N;
+  const float dp_o = oact ? Dp[odg] : 0.0f;
 
-  for (int64_t t = 0; t < L; ++t) {
-    const int64_t idx = (b * L + t) * D + d;
-    const float dr = act ? to_f32(draw[idx]) : 0.0f;
-    const float uu = act ? to_f32(u[idx]) : 0.0f;
-    const float zz = act ? to_f32(z[idx]) : 0.0f;
-    const float delta = act ? softplus(dr) : 0.0f;
-    const float dl2 = delta * kLog2e;
-    const float du = delta * uu;
-    float acc = 0.0f;
+  TIO r_dr[IT], r_u[IT], r_z[IT], r_b[BCI], r_c[BCI];
+  auto load_chunk = [&](int64_t t0) {
 #pragma unroll
-    for (int n = 0; n < NS; ++n) {
-      const float bt = n < N ? to_f32(Bb[t * N + n]) : 0.0f;
-      const float ct = n < N ? to_f32(Cb[t * N + n]) : 0.0f;
-      const float lam = fast_exp2(dl2 * Av[n]);
-      h[n] = fmaf(lam, h[n], du * bt);
-      acc = fmaf(h[n], ct, acc);
+    for (int k = 0; k < IT; ++k) {
+      const int idx = tid + k * TH;
+      const int t = idx / DT;
+      const bool v = idx < CHK * DT && oact && t0 + t < L;
+      const int64_t g = (b * L + t0 + t) * D + odg;
+      r_dr[k] = v ? draw[g] : io_zero<TIO>();
+      r_u[k] = v ? u[g] : io_zero<TIO>();
+      r_z[k] = v ? z[g] : io_zero<TIO>();
     }
-    if (act) out[idx] = from_f32<TIO>((acc + dp * uu) * zz * sigmoid(zz));
-    if (chk && ((t + 1) % CHK) == 0 && act) {
-      const int64_t slot = (t + 1) / CHK - 1;
+#pragma unroll
+    for (int k = 0; k < BCI; ++k) {
+      const int idx = tid + k * TH;
+      const int t = idx / NS, n = idx % NS;
+      const bool v = idx < CHK * NS && n < N && t0 + t < L;
+      const int64_t g = (b * L + t0 + t) * N + n;
+      r_b[k] = v ? Bt[g] : io_zero<TIO>();
+      r_c[k] = v ? Ct[g] : io_zero<TIO>();
+    }
+  };
+  load_chunk(0);
+
+  float o_u[IT], o_z[IT];
+  for (int64_t t0 = 0; t0 < L; t0 += CHK) {
+    const int len = (int)((L - t0) < CHK ? (L - t0) : CHK);
+    // phase 1: owner scalars and the B/C tile into LDS
+#pragma unroll
+    for (int k = 0; k < IT; ++k) {
+      const int idx = tid + k * TH;
+      if (idx < CHK * DT) {
+        const float dr = to_f32(r_dr[k]);
+        o_u[k] = to_f32(r_u[k]);
+        o_z[k] = to_f32(r_z[k]);
+        const float delta = oact ? softplus(dr) : 0.0f;
+        s_sc[idx / DT][idx % DT] = make_float2(delta, delta * o_u[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < BCI; ++k) {
+      const int idx = tid + k * TH;
+      if (idx < CHK * NS) s_bc[idx / NS][idx % NS] = make_float2(to_f32(r_b[k]), to_f32(r_c[k]));
+    }
+    if (t0 + CHK < L) load_chunk(t0 + CHK);  // prefetch: lands while this chunk computes
+    __syncthreads();
+    // phase 2: the recurrence, NPT states per lane
+#pragma unroll
+    for (int i = 0; i < CHK; ++i) {
+      if (i < len) {
+        const float2 s = s_sc[i][dl];
+        float y = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+          const float2 bcv = s_bc[i][n0 + j];
+          const float lam = fast_exp2(s.x * A2[j]);
+          h[j] = fmaf(lam, h[j], s.y * bcv.x);
+          y = fmaf(h[j], bcv.y, y);
+        }
+        y += swap_lane1(y);
+        if (pr == 0) s_y[i][ng >> 1][dl] = y;
+      }
+    }
+    if (chk && len == CHK && act) {
+      const int64_t slot = t0 / CHK;
       float* cp = chk + ((b * NC + slot) * D + d) * N;
 #pragma unroll
-      for (int n = 0; n < NS; ++n)
-        if (n < N) cp[n] = h[n];
+      for (int j = 0; j < NPT; ++j)
+        if (n0 + j < N) cp[n0 + j] = h[j];
+    }
+    __syncthreads();
+    // phase 3: owners finish y, apply the D skip and the SiLU gate, store the output row
+#pragma unroll
+    for (int k = 0; k < IT; ++k) {
+      const int idx = tid + k * TH;
+      const int t = idx / DT;
+      if (idx < CHK * DT && t < len && oact) {
+        float y = 0.0f;
+#pragma unroll
+        for (int p = 0; p < NPAIR; ++p) y += s_y[t][p][od];
+        const float zz = o_z[k];
+        out[(b * L + t0 + t) * D + odg] = from_f32<TIO>((y + dp_o * o_u[k]) * zz * fast_sigmoid(zz));
+      }
     }
   }
   if (act) {
 #pragma unroll
-    for (int n = 0; n < NS; ++n)
-      if (n < N) h_last[(b * D + d) * N + n] = h[n];
+    for (int j = 0; j < NPT; ++j)
+      if (n0 + j < N) h_last[(b * D + d) * N + n0 + j] = h[j];
   }
 }
 
 // ------------------------------------------------------------------------------------ backward
 template <typename TIO, int NS>
-__global__ void __launch_bounds__(64) mamba_bwd_kernel(
+__global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     const TIO* __restrict__ draw, const float* __restrict__ A, const TIO* __restrict__ Bt,
     const TIO* __restrict__ Ct, const TIO* __restrict__ u, const TIO* __restrict__ z, const float* __restrict__ Dp,
     const float* __restrict__ h0, const float* __restrict__ chk, const TIO* __restrict__ gout,
     const float* __restrict__ ghlast, TIO* __restrict__ gdraw, TIO* __restrict__ gu, TIO* __restrict__ gz,
     float* __restrict__ gA_part, float* __restrict__ gDp_part, float* __restrict__ gBC_part, float* __restrict__ gh0,
     int64_t B, int64_t L, int64_t D, int N, int64_t NC) {
-  constexpr int CHK = chk_for<NS>();
-  constexpr int KR = (2 * NS) < 64 ? 2 * NS : 64;  // values per reduce-scatter call
-  constexpr int NRED = (2 * NS) / KR;               // calls per step
-  constexpr int GROUP = 64 / KR;                    // lanes holding each reduced value
-  const int lane = threadIdx.x;
-  const int64_t d = (int64_t)blockIdx.x * 64 + lane;
+  using C = MCfg<NS>;
+  constexpr int NPT = C::NPT, DT = C::DT, TH = C::TH, CHK = C::CHK, TB = C::TB, IT = C::ITEMS;
+  constexpr int BCI = C::BCI, NPAIR = C::NPAIR, NSB = CHK / TB;
+  constexpr int W2 = 2 * NS;  // grad B / grad C columns
+  constexpr int SWZ = (W2 < DT ? W2 : DT) - 1;  // column XOR swizzle (keeps the index inside the row)
+  __shared__ float s_dl[CHK][DT], s_du[CHK][DT], s_gy[CHK][DT];
+  __shared__ float2 s_bc[CHK][NS];
+  __shared__ float s_np[TB][3][NPAIR][DT];  // (sum A Q, sum G B, sum h C) per state pair
+  __shared__ float s_dp[TB][DT][W2];        // per-channel (G du, gy h), columns XOR-swizzled by channel
+
+  const int tid = threadIdx.x;
   const int64_t b = blockIdx.y;
+  const int64_t tile = blockIdx.x;
+  const int64_t d0 = tile * DT;
+  const int pr = tid & 1;
+  const int dl = (tid >> 1) & (DT - 1);
+  const int ng = 2 * (tid / (2 * DT)) + pr;
+  const int n0 = ng * NPT;
+  const int64_t d = d0 + dl;
   const bool act = d < D;
+  const int od = tid % DT;
+  const int64_t odg = d0 + od;
+  const bool oact = odg < D;
 
-  float Av[NS], G[NS], gA[NS];
+  float A2[NPT], Av[NPT], G[NPT], gA[NPT], lam_next[NPT];
 #pragma unroll
-  for (int n = 0; n < NS; ++n) {
-    Av[n] = (act && n < N) ? A[d * N + n] : 0.0f;
-    G[n] = (act && ghlast && n < N) ? ghlast[(b * D + d) * N + n] : 0.0f;
-    gA[n] = 0.0f;
+  for (int j = 0; j < NPT; ++j) {
+    const int n = n0 + j;
+    const bool v = act && n < N;
+    Av[j] = v ? A[d * N + n] : 0.0f;
+    A2[j] = Av[j] * kLog2e;
+    G[j] = (v && ghlast) ? ghlast[(b * D + d) * N + n] : 0.0f;
+    gA[j] = 0.0f;
+    lam_next[j] = 1.0f;  // no step after the last one
   }
-  const float dp = act ? Dp[d] : 0.0f;
+  const float dp_o = oact ? Dp[odg] : 0.0f;
   float gdp = 0.0f;
-  const TIO* Bb = Bt + b * L * N;
-  const TIO* Cb = Ct + b * L * N;
-  float* part = gBC_part + ((int64_t)blockIdx.x * B + b) * L * (2 * NS);
 
-  float hb[CHK][NS];
-  float db[CHK];
-  for (int64_t c = NC - 1; c >= 0; --c) {
+  TIO r_dr[IT], r_u[IT], r_z[IT], r_go[IT], r_b[BCI], r_c[BCI];
+  float r_hs[NPT];
+  auto load_chunk = [&](int64_t c) {
     const int64_t t0 = c * CHK;
-    const int len = (int)((L - t0) < CHK ? (L - t0) : CHK);
-    float hs[NS];
 #pragma unroll
-    for (int n = 0; n < NS; ++n) {
+    for (int k = 0; k < IT; ++k) {
+      const int idx = tid + k * TH;
+      const int t = idx / DT;
+      const bool v = idx < CHK * DT && oact && t0 + t < L;
+      const int64_t g = (b * L + t0 + t) * D + odg;
+      r_dr[k] = v ? draw[g] : io_zero<TIO>();
+      r_u[k] = v ? u[g] : io_zero<TIO>();
+      r_z[k] = v ? z[g] : io_zero<TIO>();
+      r_go[k] = v ? gout[g] : io_zero<TIO>();
+    }
+#pragma unroll
+    for (int k = 0; k < BCI; ++k) {
+      const int idx = tid + k * TH;
+      const int t = idx / NS, n = idx % NS;
+      const bool v = idx < CHK * NS && n < N && t0 + t < L;
+      const int64_t g = (b * L + t0 + t) * N + n;
+      r_b[k] = v ? Bt[g] : io_zero<TIO>();
+      r_c[k] = v ? Ct[g] : io_zero<TIO>();
+    }
+    // state entering the chunk: checkpoint slot c-1, or h0 for the first chunk
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int n = n0 + j;
       float v0 = 0.0f;
       if (act && n < N) {
         if (c > 0)
@@ -143,115 +291,181 @@ __global__ void __launch_bounds__(64) mamba_bwd_kernel(
         else if (h0)
           v0 = h0[(b * D + d) * N + n];
       }
-      hs[n] = v0;
+      r_hs[j] = v0;
     }
-    // recompute the chunk's states from its checkpoint
+  };
+  if (NC > 0) load_chunk(NC - 1);
+
+  float lamb[CHK][NPT], hb[CHK][NPT];
+  float o_dl[IT], o_u[IT], o_z[IT], o_sg[IT], o_go[IT], o_gy[IT], o_sd[IT];
+  for (int64_t c = NC - 1; c >= 0; --c) {
+    const int64_t t0 = c * CHK;
+    const int len = (int)((L - t0) < CHK ? (L - t0) : CHK);
+    // phase 1: owner scalars into LDS
 #pragma unroll
-    for (int i = 0; i < CHK; ++i) {
-      if (i < len) {
-        const int64_t t = t0 + i;
-        const int64_t idx = (b * L + t) * D + d;
-        const float delta = act ? softplus(to_f32(draw[idx])) : 0.0f;
-        const float uu = act ? to_f32(u[idx]) : 0.0f;
-        const float dl2 = delta * kLog2e;
-        const float du = delta * uu;
-        db[i] = delta;
+    for (int k = 0; k < IT; ++k) {
+      const int idx = tid + k * TH;
+      if (idx < CHK * DT) {
+        const float dr = to_f32(r_dr[k]);
+        const float uu = to_f32(r_u[k]), zz = to_f32(r_z[k]), go = to_f32(r_go[k]);
+        const float delta = oact ? softplus(dr) : 0.0f;
+        const float sg = fast_sigmoid(zz);
+        const float gy = go * zz * sg;
+        o_dl[k] = delta;
+        o_u[k] = uu;
+        o_z[k] = zz;
+        o_sg[k] = sg;
+        o_go[k] = go;
+        o_gy[k] = gy;
+        o_sd[k] = fast_sigmoid(dr);  // d softplus / d draw
+        s_dl[idx / DT][idx % DT] = delta;
+        s_du[idx / DT][idx % DT] = delta * uu;
+        s_gy[idx / DT][idx % DT] = gy;
+      }
+    }
 #pragma unroll
-        for (int n = 0; n < NS; ++n) {
-          const float bt = n < N ? to_f32(Bb[t * N + n]) : 0.0f;
-          hs[n] = fmaf(fast_exp2(dl2 * Av[n]), hs[n], du * bt);
-          hb[i][n] = hs[n];
+    for (int k = 0; k < BCI; ++k) {
+      const int idx = tid + k * TH;
+      if (idx < CHK * NS) s_bc[idx / NS][idx % NS] = make_float2(to_f32(r_b[k]), to_f32(r_c[k]));
+    }
+    float hst[NPT];
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) hst[j] = r_hs[j];
+    if (c > 0) load_chunk(c - 1);  // prefetch the previous chunk while this one computes
+    __syncthreads();
+
+    // recompute this chunk's states: lam_t and h_t into registers
+    {
+      float hs[NPT];
+#pragma unroll
+      for (int j = 0; j < NPT; ++j) hs[j] = hst[j];
+#pragma unroll
+      for (int i = 0; i < CHK; ++i) {
+        if (i < len) {
+          const float dlt = s_dl[i][dl], du = s_du[i][dl];
+#pragma unroll
+          for (int j = 0; j < NPT; ++j) {
+            const float lam = fast_exp2(dlt * A2[j]);
+            lamb[i][j] = lam;
+            hs[j] = fmaf(lam, hs[j], du * s_bc[i][n0 + j].x);
+            hb[i][j] = hs[j];
+          }
         }
       }
     }
-    // adjoint sweep, backwards through the chunk
-#pragma unroll
-    for (int ii = 0; ii < CHK; ++ii) {
-      const int i = CHK - 1 - ii;
-      if (i < len) {
-        const int64_t t = t0 + i;
-        const int64_t idx = (b * L + t) * D + d;
-        const float delta = db[i];
-        const float dr = act ? to_f32(draw[idx]) : 0.0f;
-        const float uu = act ? to_f32(u[idx]) : 0.0f;
-        const float zz = act ? to_f32(z[idx]) : 0.0f;
-        const float go = act ? to_f32(gout[idx]) : 0.0f;
-        const bool has_next = (t + 1) < L;
-        float dn = 0.0f;  // delta_{t+1}
-        if (i + 1 < len)
-          dn = db[i + 1];
-        else if (has_next && act)
-          dn = softplus(to_f32(draw[idx + D]));
-        const float dn2 = dn * kLog2e;
 
-        float y = dp * uu;
+    // adjoint sweep, backwards through the chunk in sub-blocks of TB steps
 #pragma unroll
-        for (int n = 0; n < NS; ++n) {
-          const float ct = n < N ? to_f32(Cb[t * N + n]) : 0.0f;
-          y = fmaf(hb[i][n], ct, y);
-        }
-        const float sig = sigmoid(zz);
-        const float gy = go * zz * sig;
-        const float gzv = go * y * sig * (1.0f + zz * (1.0f - sig));
-        gdp = fmaf(gy, uu, gdp);
-        const float du = delta * uu;
-
-        float gdelta = 0.0f, gus = 0.0f;
-        float red[2 * NS];
+    for (int sb = NSB - 1; sb >= 0; --sb) {
 #pragma unroll
-        for (int n = 0; n < NS; ++n) {
-          const float bt = n < N ? to_f32(Bb[t * N + n]) : 0.0f;
-          const float ct = n < N ? to_f32(Cb[t * N + n]) : 0.0f;
-          const float an = has_next ? fast_exp2(dn2 * Av[n]) : 1.0f;
-          G[n] = fmaf(an, G[n], gy * ct);
-          const float lamh = hb[i][n] - du * bt;  // lam_t h_{t-1}
-          const float Q = G[n] * lamh;
-          gA[n] = fmaf(delta, Q, gA[n]);
-          gdelta = fmaf(Av[n], Q, gdelta);
-          gus = fmaf(G[n], bt, gus);
-          red[n] = G[n] * du;
-          red[NS + n] = gy * hb[i][n];
-        }
-        gdelta = fmaf(uu, gus, gdelta);
-        if (act) {
-          gdraw[idx] = from_f32<TIO>(gdelta * sigmoid(dr));
-          gu[idx] = from_f32<TIO>(fmaf(delta, gus, gy * dp));
-          gz[idx] = from_f32<TIO>(gzv);
-        }
+      for (int ii = TB - 1; ii >= 0; --ii) {
+        const int i = sb * TB + ii;
+        if (i < len) {
+          const float dlt = s_dl[i][dl], du = s_du[i][dl], gy = s_gy[i][dl];
+          float aq = 0.0f, gb = 0.0f, hc = 0.0f;
 #pragma unroll
-        for (int r = 0; r < NRED; ++r) {
-          wave_reduce_scatter<KR>(red + r * KR, lane);
-          if ((lane % GROUP) == 0) part[t * (2 * NS) + r * KR + lane / GROUP] = red[r * KR];
+          for (int j = 0; j < NPT; ++j) {
+            const float2 bcv = s_bc[i][n0 + j];
+            const float an = (i + 1 < len) ? lamb[(i + 1) % CHK][j] : lam_next[j];
+            G[j] = fmaf(an, G[j], gy * bcv.y);
+            const float hprev = (i > 0) ? hb[(i + CHK - 1) % CHK][j] : hst[j];
+            const float Q = G[j] * (lamb[i][j] * hprev);  // G_t * lam_t h_{t-1}
+            gA[j] = fmaf(dlt, Q, gA[j]);
+            aq = fmaf(Av[j], Q, aq);
+            gb = fmaf(G[j], bcv.x, gb);
+            hc = fmaf(hb[i][j], bcv.y, hc);
+            const int col = n0 + j;
+            s_dp[ii][dl][col ^ (dl & SWZ)] = G[j] * du;
+            s_dp[ii][dl][(NS + col) ^ (dl & SWZ)] = gy * hb[i][j];
+          }
+          aq += swap_lane1(aq);
+          gb += swap_lane1(gb);
+          hc += swap_lane1(hc);
+          if (pr == 0) {
+            s_np[ii][0][ng >> 1][dl] = aq;
+            s_np[ii][1][ng >> 1][dl] = gb;
+            s_np[ii][2][ng >> 1][dl] = hc;
+          }
         }
       }
+      __syncthreads();
+      // owners: finish the per-(t, d) gradients of this sub-block
+#pragma unroll
+      for (int k = 0; k < IT; ++k) {
+        const int idx = tid + k * TH;
+        const int t = idx / DT;
+        if (idx < CHK * DT && t >= sb * TB && t < sb * TB + TB && t < len && oact) {
+          const int ii = t - sb * TB;
+          float aq = 0.0f, gb = 0.0f, hc = 0.0f;
+#pragma unroll
+          for (int p = 0; p < NPAIR; ++p) {
+            aq += s_np[ii][0][p][od];
+            gb += s_np[ii][1][p][od];
+            hc += s_np[ii][2][p][od];
+          }
+          const float uu = o_u[k], zz = o_z[k], sg = o_sg[k];
+          const float y = fmaf(dp_o, uu, hc);
+          const float gzv = o_go[k] * y * sg * (1.0f + zz * (1.0f - sg));
+          const float gdelta = fmaf(uu, gb, aq);
+          const int64_t g = (b * L + t0 + t) * D + odg;
+          gdraw[g] = from_f32<TIO>(gdelta * o_sd[k]);
+          gu[g] = from_f32<TIO>(fmaf(o_dl[k], gb, o_gy[k] * dp_o));
+          gz[g] = from_f32<TIO>(gzv);
+          gdp = fmaf(o_gy[k], uu, gdp);
+        }
+      }
+      // grad B_t / grad C_t: sum the tile's channels for each (t, column)
+      for (int idx = tid; idx < TB * W2; idx += TH) {
+        const int ii = idx / W2, col = idx % W2;
+        const int t = sb * TB + ii;
+        if (t < len) {
+          float s = 0.0f;
+#pragma unroll 8
+          for (int dd = 0; dd < DT; ++dd) s += s_dp[ii][dd][col ^ (dd & SWZ)];
+          gBC_part[((tile * B + b) * L + t0 + t) * W2 + col] = s;
+        }
+      }
+      __syncthreads();
     }
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) lam_next[j] = lamb[0][j];
   }
+
   if (act) {
 #pragma unroll
-    for (int n = 0; n < NS; ++n)
-      if (n < N) gA_part[(b * D + d) * N + n] = gA[n];
-    gDp_part[b * D + d] = gdp;
-    if (gh0) {
-      // an empty sequence passes the state through unchanged (gh0 = ghlast)
-      const float d0 = L > 0 ? softplus(to_f32(draw[b * L * D + d])) * kLog2e : 0.0f;
+    for (int j = 0; j < NPT; ++j)
+      if (n0 + j < N) gA_part[(b * D + d) * N + n0 + j] = gA[j];
+  }
+  // gh0 = lam_0 G_0 (lam_next now holds lam_0; an empty sequence passes the state through)
+  if (gh0 && act) {
 #pragma unroll
-      for (int n = 0; n < NS; ++n)
-        if (n < N) gh0[(b * D + d) * N + n] = fast_exp2(d0 * Av[n]) * G[n];
-    }
+    for (int j = 0; j < NPT; ++j)
+      if (n0 + j < N) gh0[(b * D + d) * N + n0 + j] = lam_next[j] * G[j];
+  }
+  // gDp: every owner thread of channel od holds a partial; sum them through LDS
+  __syncthreads();
+  float* red = &s_dp[0][0][0];
+  static_assert(TB * DT * W2 >= TH, "reduction scratch too small");
+  red[tid] = gdp;
+  __syncthreads();
+  if (tid < DT && oact) {
+    float s = 0.0f;
+    for (int k = tid; k < TH; k += DT) s += red[k];
+    gDp_part[b * D + odg] = s;
   }
 }
 
-// gBt/gCt: sum the per-wave partials [nDB, B, L, 2*NS] over the channel blocks.
+// gBt/gCt: sum the per-tile partials [nT, B, L, 2*NS] over the channel tiles, in order.
 template <typename TIO>
 __global__ void __launch_bounds__(256) mamba_reduce_bc(const float* __restrict__ part, TIO* __restrict__ gBt,
-                                                       TIO* __restrict__ gCt, int64_t nDB, int64_t BL, int N,
+                                                       TIO* __restrict__ gCt, int64_t nT, int64_t BL, int N,
                                                        int NS) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // over BL * N
   if (i >= BL * N) return;
   const int64_t row = i / N;
   const int n = (int)(i % N);
   float sb = 0.0f, sc = 0.0f;
-  for (int64_t k = 0; k < nDB; ++k) {
+  for (int64_t k = 0; k < nT; ++k) {
     const float* p = part + (k * BL + row) * (2 * NS);
     sb += p[n];
     sc += p[NS + n];
@@ -274,12 +488,19 @@ template <typename TIO, int NS>
 int launch_fwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, const float* A, const void* Bt,
                const void* Ct, const void* u, const void* z, const float* Dp, const float* h0, void* out,
                float* h_last, float* chk, hipStream_t s) {
-  constexpr int CHK = chk_for<NS>();
-  const int64_t NC = (L + CHK - 1) / CHK;
-  dim3 grid((unsigned)((D + 63) / 64), (unsigned)B);
-  hipLaunchKernelGGL((mamba_fwd_kernel<TIO, NS>), grid, dim3(64), 0, s, (const TIO*)draw, A, (const TIO*)Bt,
+  using C = MCfg<NS>;
+  const int64_t NC = (L + C::CHK - 1) / C::CHK;
+  dim3 grid((unsigned)((D + C::DT - 1) / C::DT), (unsigned)B);
+  hipLaunchKernelGGL((mamba_fwd_kernel<TIO, NS>), grid, dim3(C::TH), 0, s, (const TIO*)draw, A, (const TIO*)Bt,
                      (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, (TIO*)out, h_last, chk, L, D, (int)N, NC);
   return tsf_launch_status();
+}
+
+template <int NS>
+int64_t bwd_workspace_floats(int64_t B, int64_t L, int64_t D, int64_t N) {
+  using C = MCfg<NS>;
+  const int64_t nT = (D + C::DT - 1) / C::DT;
+  return nT * B * L * 2 * NS + B * D * N + B * D;
 }
 
 template <typename TIO, int NS>
@@ -287,21 +508,21 @@ int launch_bwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
                const void* Ct, const void* u, const void* z, const float* Dp, const float* h0, const float* chk,
                const void* gout, const float* ghlast, void* gdraw, float* gA, void* gBt, void* gCt, void* gu, void* gz,
                float* gDp, float* gh0, void* workspace, hipStream_t s) {
-  constexpr int CHK = chk_for<NS>();
-  const int64_t NC = (L + CHK - 1) / CHK;
-  const int64_t nDB = (D + 63) / 64;
+  using C = MCfg<NS>;
+  const int64_t NC = (L + C::CHK - 1) / C::CHK;
+  const int64_t nT = (D + C::DT - 1) / C::DT;
   float* gBC_part = static_cast<float*>(workspace);
-  float* gA_part = gBC_part + nDB * B * L * 2 * NS;
+  float* gA_part = gBC_part + nT * B * L * 2 * NS;
   float* gDp_part = gA_part + B * D * N;
-  dim3 grid((unsigned)nDB, (unsigned)B);
+  dim3 grid((unsigned)nT, (unsigned)B);
   if (B > 0 && D > 0)
-    hipLaunchKernelGGL((mamba_bwd_kernel<TIO, NS>), grid, dim3(64), 0, s, (const TIO*)draw, A, (const TIO*)Bt,
+    hipLaunchKernelGGL((mamba_bwd_kernel<TIO, NS>), grid, dim3(C::TH), 0, s, (const TIO*)draw, A, (const TIO*)Bt,
                        (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, chk, (const TIO*)gout, ghlast,
                        (TIO*)gdraw, (TIO*)gu, (TIO*)gz, gA_part, gDp_part, gBC_part, gh0, B, L, D, (int)N, NC);
   const int64_t BLN = B * L * N;
   if (BLN > 0)
     hipLaunchKernelGGL((mamba_reduce_bc<TIO>), dim3((unsigned)((BLN + 255) / 256)), dim3(256), 0, s, gBC_part,
-                       (TIO*)gBt, (TIO*)gCt, nDB, B * L, (int)N, NS);
+                       (TIO*)gBt, (TIO*)gCt, nT, B * L, (int)N, NS);
   if (D > 0) {
     hipLaunchKernelGGL(mamba_reduce_batch, dim3((unsigned)((D * N + 255) / 256)), dim3(256), 0, s, gA_part, gA, B,
                        D * N);
@@ -310,20 +531,20 @@ int launch_bwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
   return tsf_launch_status();
 }
 
-#define TSF_DISPATCH_NS(NSV, FN, ...)            \
-  switch (NSV) {                                 \
-    case 4:                                      \
-      return FN<4>(__VA_ARGS__);                 \
-    case 8:                                      \
-      return FN<8>(__VA_ARGS__);                 \
-    case 16:                                     \
-      return FN<16>(__VA_ARGS__);                \
-    case 32:                                     \
-      return FN<32>(__VA_ARGS__);                \
-    case 64:                                     \
-      return FN<64>(__VA_ARGS__);                \
-    default:                                     \
-      return TSF_ERR_UNSUPPORTED;                \
+#define TSF_DISPATCH_NS(NSV, FN, ...) \
+  switch (NSV) {                      \
+    case 4:                           \
+      return FN<4>(__VA_ARGS__);      \
+    case 8:                           \
+      return FN<8>(__VA_ARGS__);      \
+    case 16:                          \
+      return FN<16>(__VA_ARGS__);     \
+    case 32:                          \
+      return FN<32>(__VA_ARGS__);     \
+    case 64:                          \
+      return FN<64>(__VA_ARGS__);     \
+    default:                          \
+      return TSF_ERR_UNSUPPORTED;     \
   }
 
 template <int NS>
@@ -358,17 +579,34 @@ int bwd_bf16(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, const
 int chk_interval_for(int ns) {
   switch (ns) {
     case 4:
-      return chk_for<4>();
+      return MCfg<4>::CHK;
     case 8:
-      return chk_for<8>();
+      return MCfg<8>::CHK;
     case 16:
-      return chk_for<16>();
+      return MCfg<16>::CHK;
     case 32:
-      return chk_for<32>();
+      return MCfg<32>::CHK;
     case 64:
-      return chk_for<64>();
+      return MCfg<64>::CHK;
     default:
       return 0;
+  }
+}
+
+int64_t workspace_floats(int ns, int64_t B, int64_t L, int64_t D, int64_t N) {
+  switch (ns) {
+    case 4:
+      return bwd_workspace_floats<4>(B, L, D, N);
+    case 8:
+      return bwd_workspace_floats<8>(B, L, D, N);
+    case 16:
+      return bwd_workspace_floats<16>(B, L, D, N);
+    case 32:
+      return bwd_workspace_floats<32>(B, L, D, N);
+    case 64:
+      return bwd_workspace_floats<64>(B, L, D, N);
+    default:
+      return -1;
   }
 }
 
@@ -380,9 +618,8 @@ int64_t tsfast_hip_mamba_chk_interval(int64_t N) { return chk_interval_for(ns_fo
 
 int64_t tsfast_hip_mamba_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t N) {
   const int ns = ns_for(N);
-  if (ns == 0) return -1;
-  const int64_t nDB = (D + 63) / 64;
-  return 4 * (nDB * B * L * 2 * ns + B * D * N + B * D);
+  if (ns == 0 || N < 1) return -1;
+  return 4 * workspace_floats(ns, B, L, D, N);
 }
 
 int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtype, const void* draw, const float* A,
@@ -416,7 +653,7 @@ int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
   if (!A || !Dp || !gA || !gDp) return TSF_ERR_ARG;
   if (L > 0 && (!draw || !Bt || !Ct || !u || !z || !gout || !gdraw || !gBt || !gCt || !gu || !gz)) return TSF_ERR_ARG;
   if (h0 && !gh0) return TSF_ERR_ARG;
-  if (L > 0 && !chk && L > chk_interval_for(ns)) return TSF_ERR_ARG;
+  if (L > chk_interval_for(ns) && !chk) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_mamba_workspace_bytes(B, L, D, N) || !workspace) return TSF_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (io_dtype == TSF_DTYPE_F32) {
