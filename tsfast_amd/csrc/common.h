@@ -136,10 +136,35 @@ TSF_DEV T ipow(T x, int64_t k) {
 // 2^x on the hardware transcendental unit (v_exp_f32); the kernels pre-scale A by log2(e).
 TSF_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+constexpr float kLn2 = 0.6931471805599453f;
+
 // softplus with torch.nn.functional.softplus's threshold: x for x > 20, else log(1 + e^x).
 TSF_DEV float softplus(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }
 
 TSF_DEV float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// log(1 + e^x) on the transcendental unit: e = e^x, u = 1 + e rounded, and
+// log1p(e) = e * log(u) / (u - 1), exact to a few ulp because the rounding error of u cancels
+// between numerator and denominator (Goldberg, "What every computer scientist should know
+// about floating-point arithmetic", 1991, theorem 4). Returns e and u for the caller (the
+// derivative of softplus is e / u).
+struct SoftplusParts {
+  float value, e, u;
+};
+TSF_DEV SoftplusParts softplus_parts(float x) {
+  const float e = __builtin_amdgcn_exp2f(fminf(x, 20.0f) * kLog2e);
+  const float u = 1.0f + e;
+  const float dm = u - 1.0f;
+  const float lg = __builtin_amdgcn_logf(u) * kLn2;
+  const float lp = dm == 0.0f ? e : lg * (e * __builtin_amdgcn_rcpf(dm));
+  SoftplusParts r;
+  r.value = x > 20.0f ? x : lp;
+  r.e = e;
+  r.u = u;
+  return r;
+}
+TSF_DEV float softplus_fast(float x) { return softplus_parts(x).value; }
+TSF_DEV float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e)); }
 
 // ------------------------------------------------------------------ wave reductions
 // Reduce-scatter of K values (K a power of two, K <= 64) held by every lane of a wave64:

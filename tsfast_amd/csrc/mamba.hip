@@ -29,6 +29,8 @@
 //    LDS and written as fp32 partials [D/32, B, L, 2*NS]; a second kernel sums the partials in a
 //    fixed order (no atomics: deterministic run to run).
 // The next chunk's inputs are loaded into registers while the current chunk computes.
+#include <type_traits>
+
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -53,18 +55,19 @@ struct MCfg {
   static constexpr int TH = DT * NG;           // threads per workgroup
   static constexpr int NPAIR = NG / 2;         // state-pair partial slots per channel
   // checkpoint interval = backward recompute chunk (lam_t and h_t of a chunk live in VGPRs)
-  static constexpr int CHK = NPT <= 2 ? 16 : (NPT == 4 ? 8 : 4);
+  static constexpr int CHK = NPT <= 2 ? 8 : (NPT == 4 ? 8 : 4);
+  static constexpr int TF = NPT <= 2 ? 32 : 2 * CHK;  // forward steps per LDS round
   static constexpr int TB = CHK < 8 ? CHK : 8;  // backward flush sub-block
-  static constexpr int ITEMS = (CHK * DT + TH - 1) / TH;  // owned (t, d) items per thread per chunk
-  static constexpr int BCI = (CHK * NS + TH - 1) / TH;    // B/C tile elements per thread
+  static constexpr int IT_F = (TF * DT + TH - 1) / TH;   // owned (t, d) items per thread, forward
+  static constexpr int IT_B = (CHK * DT + TH - 1) / TH;  // owned (t, d) items per thread, backward
+  static constexpr int BC_F = (TF * NS + TH - 1) / TH;   // B/C tile elements per thread, forward
+  static constexpr int BC_B = (CHK * NS + TH - 1) / TH;  // B/C tile elements per thread, backward
 };
 
 // Swap with the neighbouring lane (lane ^ 1) through DPP: one VALU op, no LDS round trip.
 TSF_DEV float swap_lane1(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1 /* quad_perm [1,0,3,2] */, 0xF, 0xF, false));
 }
-
-TSF_DEV float fast_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 template <typename TIO>
 TSF_DEV TIO io_zero();
@@ -79,6 +82,9 @@ TSF_DEV bf16 io_zero<bf16>() {
   return zr;
 }
 
+template <bool V>
+using Bool = std::integral_constant<bool, V>;
+
 // ------------------------------------------------------------------------------------ forward
 template <typename TIO, int NS>
 __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
@@ -87,11 +93,11 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     const float* __restrict__ h0, TIO* __restrict__ out, float* __restrict__ h_last, float* __restrict__ chk,
     int64_t L, int64_t D, int N, int64_t NC) {
   using C = MCfg<NS>;
-  constexpr int NPT = C::NPT, DT = C::DT, TH = C::TH, CHK = C::CHK, IT = C::ITEMS, BCI = C::BCI;
-  constexpr int NPAIR = C::NPAIR;
-  __shared__ float2 s_sc[CHK][DT];       // (delta, delta * u)
-  __shared__ float2 s_bc[CHK][NS];       // (B, C)
-  __shared__ float s_y[CHK][NPAIR][DT];  // y partial per state pair
+  constexpr int NPT = C::NPT, NG = C::NG, DT = C::DT, TH = C::TH, CHK = C::CHK, TF = C::TF;
+  constexpr int IT = C::IT_F, BCI = C::BC_F, NPAIR = C::NPAIR;
+  __shared__ float2 s_sc[TF][DT];       // (delta, delta * u)
+  __shared__ float2 s_bc[TF][NS];       // (B, C)
+  __shared__ float s_y[TF][NPAIR][DT];  // y partial per state pair
 
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.y;
@@ -103,10 +109,12 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   const int n0 = ng * NPT;
   const int64_t d = d0 + dl;
   const bool act = d < D;
-  // owner mapping: item k of this thread is (t = idx / DT, channel d0 + idx % DT), idx = tid + k * TH
+  // owner mapping: item k of this thread is (t = tid / DT + k * NG, channel d0 + tid % DT)
   const int od = tid % DT;
-  const int64_t odg = d0 + od;
-  const bool oact = odg < D;
+  const bool oact = d0 + od < D;
+  // workgroup-uniform bases and 32-bit per-thread offsets (the host bounds L*D and L*N)
+  const int64_t rowD = b * L * D + d0, rowN = b * L * N;
+  const uint32_t Du = (uint32_t)D, Nu = (uint32_t)N;
 
   float A2[NPT], h[NPT];
 #pragma unroll
@@ -115,58 +123,72 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     A2[j] = (act && n < N) ? A[d * N + n] * kLog2e : 0.0f;
     h[j] = (act && h0 && n < N) ? h0[(b * D + d) * N + n] : 0.0f;
   }
-  const float dp_o = oact ? Dp[odg] : 0.0f;
+  const float dp_o = oact ? Dp[d0 + od] : 0.0f;
 
   TIO r_dr[IT], r_u[IT], r_z[IT], r_b[BCI], r_c[BCI];
-  auto load_chunk = [&](int64_t t0) {
+  auto load_chunk = [&](uint32_t t0, auto full) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full)::value;
 #pragma unroll
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
-      const int t = idx / DT;
-      const bool v = idx < CHK * DT && oact && t0 + t < L;
-      const int64_t g = (b * L + t0 + t) * D + odg;
-      r_dr[k] = v ? draw[g] : io_zero<TIO>();
-      r_u[k] = v ? u[g] : io_zero<TIO>();
-      r_z[k] = v ? z[g] : io_zero<TIO>();
+      const uint32_t t = (uint32_t)(idx / DT);
+      bool v = idx < TF * DT && oact;
+      if (!FULL) v = v && (int64_t)(t0 + t) < L;
+      const uint32_t o = (t0 + t) * Du + (uint32_t)od;
+      r_dr[k] = v ? draw[rowD + o] : io_zero<TIO>();
+      r_u[k] = v ? u[rowD + o] : io_zero<TIO>();
+      r_z[k] = v ? z[rowD + o] : io_zero<TIO>();
     }
 #pragma unroll
     for (int k = 0; k < BCI; ++k) {
       const int idx = tid + k * TH;
-      const int t = idx / NS, n = idx % NS;
-      const bool v = idx < CHK * NS && n < N && t0 + t < L;
-      const int64_t g = (b * L + t0 + t) * N + n;
-      r_b[k] = v ? Bt[g] : io_zero<TIO>();
-      r_c[k] = v ? Ct[g] : io_zero<TIO>();
+      const uint32_t t = (uint32_t)(idx / NS), n = (uint32_t)(idx % NS);
+      bool v = idx < TF * NS && (int)n < N;
+      if (!FULL) v = v && (int64_t)(t0 + t) < L;
+      const uint32_t o = (t0 + t) * Nu + n;
+      r_b[k] = v ? Bt[rowN + o] : io_zero<TIO>();
+      r_c[k] = v ? Ct[rowN + o] : io_zero<TIO>();
     }
   };
-  load_chunk(0);
+  if (L > 0) {
+    if (TF <= L)
+      load_chunk(0u, Bool<true>());
+    else
+      load_chunk(0u, Bool<false>());
+  }
 
   float o_u[IT], o_z[IT];
-  for (int64_t t0 = 0; t0 < L; t0 += CHK) {
-    const int len = (int)((L - t0) < CHK ? (L - t0) : CHK);
+  auto chunk = [&](uint32_t t0, int len, auto full) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full)::value;
     // phase 1: owner scalars and the B/C tile into LDS
 #pragma unroll
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
-      if (idx < CHK * DT) {
-        const float dr = to_f32(r_dr[k]);
+      if (idx < TF * DT) {
         o_u[k] = to_f32(r_u[k]);
         o_z[k] = to_f32(r_z[k]);
-        const float delta = oact ? softplus(dr) : 0.0f;
+        const float delta = oact ? softplus_fast(to_f32(r_dr[k])) : 0.0f;
         s_sc[idx / DT][idx % DT] = make_float2(delta, delta * o_u[k]);
       }
     }
 #pragma unroll
     for (int k = 0; k < BCI; ++k) {
       const int idx = tid + k * TH;
-      if (idx < CHK * NS) s_bc[idx / NS][idx % NS] = make_float2(to_f32(r_b[k]), to_f32(r_c[k]));
+      if (idx < TF * NS) s_bc[idx / NS][idx % NS] = make_float2(to_f32(r_b[k]), to_f32(r_c[k]));
     }
-    if (t0 + CHK < L) load_chunk(t0 + CHK);  // prefetch: lands while this chunk computes
+    // prefetch the next round while this one computes
+    const uint32_t t1 = t0 + TF;
+    if ((int64_t)t1 < L) {
+      if ((int64_t)t1 + TF <= L)
+        load_chunk(t1, Bool<true>());
+      else
+        load_chunk(t1, Bool<false>());
+    }
     __syncthreads();
     // phase 2: the recurrence, NPT states per lane
 #pragma unroll
-    for (int i = 0; i < CHK; ++i) {
-      if (i < len) {
+    for (int i = 0; i < TF; ++i) {
+      if (FULL || i < len) {
         const float2 s = s_sc[i][dl];
         float y = 0.0f;
 #pragma unroll
@@ -178,14 +200,15 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         }
         y += swap_lane1(y);
         if (pr == 0) s_y[i][ng >> 1][dl] = y;
-      }
-    }
-    if (chk && len == CHK && act) {
-      const int64_t slot = t0 / CHK;
-      float* cp = chk + ((b * NC + slot) * D + d) * N;
+        // checkpoint slot k holds the state after step (k + 1) * CHK - 1
+        if ((i % CHK) == CHK - 1 && chk && act) {
+          const int64_t slot = ((int64_t)t0 + i) / CHK;
+          float* cp = chk + ((b * NC + slot) * D + d) * N + n0;
 #pragma unroll
-      for (int j = 0; j < NPT; ++j)
-        if (n0 + j < N) cp[n0 + j] = h[j];
+          for (int j = 0; j < NPT; ++j)
+            if (n0 + j < N) cp[j] = h[j];
+        }
+      }
     }
     __syncthreads();
     // phase 3: owners finish y, apply the D skip and the SiLU gate, store the output row
@@ -193,15 +216,23 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
       const int t = idx / DT;
-      if (idx < CHK * DT && t < len && oact) {
+      if (idx < TF * DT && (FULL || t < len) && oact) {
         float y = 0.0f;
 #pragma unroll
         for (int p = 0; p < NPAIR; ++p) y += s_y[t][p][od];
         const float zz = o_z[k];
-        out[(b * L + t0 + t) * D + odg] = from_f32<TIO>((y + dp_o * o_u[k]) * zz * fast_sigmoid(zz));
+        const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
+        out[rowD + o] = from_f32<TIO>(fmaf(dp_o, o_u[k], y) * zz * sigmoid_fast(zz));
       }
     }
+  };
+  for (int64_t t0 = 0; t0 < L; t0 += TF) {
+    if (t0 + TF <= L)
+      chunk((uint32_t)t0, TF, Bool<true>());
+    else
+      chunk((uint32_t)t0, (int)(L - t0), Bool<false>());
   }
+  (void)NG;
   if (act) {
 #pragma unroll
     for (int j = 0; j < NPT; ++j)
@@ -219,14 +250,14 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     float* __restrict__ gA_part, float* __restrict__ gDp_part, float* __restrict__ gBC_part, float* __restrict__ gh0,
     int64_t B, int64_t L, int64_t D, int N, int64_t NC) {
   using C = MCfg<NS>;
-  constexpr int NPT = C::NPT, DT = C::DT, TH = C::TH, CHK = C::CHK, TB = C::TB, IT = C::ITEMS;
-  constexpr int BCI = C::BCI, NPAIR = C::NPAIR, NSB = CHK / TB;
+  constexpr int NPT = C::NPT, DT = C::DT, TH = C::TH, CHK = C::CHK, TB = C::TB, IT = C::IT_B;
+  constexpr int BCI = C::BC_B, NPAIR = C::NPAIR, NSB = CHK / TB;
   constexpr int W2 = 2 * NS;  // grad B / grad C columns
-  constexpr int SWZ = (W2 < DT ? W2 : DT) - 1;  // column XOR swizzle (keeps the index inside the row)
+  static_assert(DT == 32, "the channel-sum read pattern assumes 32 channels per row");
   __shared__ float s_dl[CHK][DT], s_du[CHK][DT], s_gy[CHK][DT];
   __shared__ float2 s_bc[CHK][NS];
   __shared__ float s_np[TB][3][NPAIR][DT];  // (sum A Q, sum G B, sum h C) per state pair
-  __shared__ float s_dp[TB][DT][W2];        // per-channel (G du, gy h), columns XOR-swizzled by channel
+  __shared__ float s_dp[TB][W2][DT];        // per (step, column): the 32 channels' (G du | gy h)
 
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.y;
@@ -239,8 +270,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   const int64_t d = d0 + dl;
   const bool act = d < D;
   const int od = tid % DT;
-  const int64_t odg = d0 + od;
-  const bool oact = odg < D;
+  const bool oact = d0 + od < D;
+  const int64_t rowD = b * L * D + d0, rowN = b * L * N;
+  const uint32_t Du = (uint32_t)D, Nu = (uint32_t)N;
 
   float A2[NPT], Av[NPT], G[NPT], gA[NPT], lam_next[NPT];
 #pragma unroll
@@ -253,32 +285,35 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     gA[j] = 0.0f;
     lam_next[j] = 1.0f;  // no step after the last one
   }
-  const float dp_o = oact ? Dp[odg] : 0.0f;
+  const float dp_o = oact ? Dp[d0 + od] : 0.0f;
   float gdp = 0.0f;
 
   TIO r_dr[IT], r_u[IT], r_z[IT], r_go[IT], r_b[BCI], r_c[BCI];
   float r_hs[NPT];
-  auto load_chunk = [&](int64_t c) {
-    const int64_t t0 = c * CHK;
+  auto load_chunk = [&](int64_t c, auto full) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full)::value;
+    const uint32_t t0 = (uint32_t)(c * CHK);
 #pragma unroll
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
-      const int t = idx / DT;
-      const bool v = idx < CHK * DT && oact && t0 + t < L;
-      const int64_t g = (b * L + t0 + t) * D + odg;
-      r_dr[k] = v ? draw[g] : io_zero<TIO>();
-      r_u[k] = v ? u[g] : io_zero<TIO>();
-      r_z[k] = v ? z[g] : io_zero<TIO>();
-      r_go[k] = v ? gout[g] : io_zero<TIO>();
+      const uint32_t t = (uint32_t)(idx / DT);
+      bool v = idx < CHK * DT && oact;
+      if (!FULL) v = v && (int64_t)(t0 + t) < L;
+      const uint32_t o = (t0 + t) * Du + (uint32_t)od;
+      r_dr[k] = v ? draw[rowD + o] : io_zero<TIO>();
+      r_u[k] = v ? u[rowD + o] : io_zero<TIO>();
+      r_z[k] = v ? z[rowD + o] : io_zero<TIO>();
+      r_go[k] = v ? gout[rowD + o] : io_zero<TIO>();
     }
 #pragma unroll
     for (int k = 0; k < BCI; ++k) {
       const int idx = tid + k * TH;
-      const int t = idx / NS, n = idx % NS;
-      const bool v = idx < CHK * NS && n < N && t0 + t < L;
-      const int64_t g = (b * L + t0 + t) * N + n;
-      r_b[k] = v ? Bt[g] : io_zero<TIO>();
-      r_c[k] = v ? Ct[g] : io_zero<TIO>();
+      const uint32_t t = (uint32_t)(idx / NS), n = (uint32_t)(idx % NS);
+      bool v = idx < CHK * NS && (int)n < N;
+      if (!FULL) v = v && (int64_t)(t0 + t) < L;
+      const uint32_t o = (t0 + t) * Nu + n;
+      r_b[k] = v ? Bt[rowN + o] : io_zero<TIO>();
+      r_c[k] = v ? Ct[rowN + o] : io_zero<TIO>();
     }
     // state entering the chunk: checkpoint slot c-1, or h0 for the first chunk
 #pragma unroll
@@ -294,33 +329,36 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       r_hs[j] = v0;
     }
   };
-  if (NC > 0) load_chunk(NC - 1);
+  auto load_any = [&](int64_t c) __attribute__((always_inline)) {
+    if ((c + 1) * CHK <= L)
+      load_chunk(c, Bool<true>());
+    else
+      load_chunk(c, Bool<false>());
+  };
+  if (NC > 0) load_any(NC - 1);
 
   float lamb[CHK][NPT], hb[CHK][NPT];
-  float o_dl[IT], o_u[IT], o_z[IT], o_sg[IT], o_go[IT], o_gy[IT], o_sd[IT];
-  for (int64_t c = NC - 1; c >= 0; --c) {
-    const int64_t t0 = c * CHK;
-    const int len = (int)((L - t0) < CHK ? (L - t0) : CHK);
+  float o_u[IT], o_z[IT], o_sg[IT], o_go[IT], o_sd[IT];
+  auto chunk = [&](int64_t c, int len, auto full) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full)::value;
+    const uint32_t t0 = (uint32_t)(c * CHK);
     // phase 1: owner scalars into LDS
 #pragma unroll
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
       if (idx < CHK * DT) {
-        const float dr = to_f32(r_dr[k]);
         const float uu = to_f32(r_u[k]), zz = to_f32(r_z[k]), go = to_f32(r_go[k]);
-        const float delta = oact ? softplus(dr) : 0.0f;
-        const float sg = fast_sigmoid(zz);
-        const float gy = go * zz * sg;
-        o_dl[k] = delta;
+        const SoftplusParts sp = softplus_parts(to_f32(r_dr[k]));
+        const float delta = oact ? sp.value : 0.0f;
+        const float sg = sigmoid_fast(zz);
         o_u[k] = uu;
         o_z[k] = zz;
         o_sg[k] = sg;
         o_go[k] = go;
-        o_gy[k] = gy;
-        o_sd[k] = fast_sigmoid(dr);  // d softplus / d draw
+        o_sd[k] = sp.e * __builtin_amdgcn_rcpf(sp.u);  // d softplus / d draw = sigmoid(draw)
         s_dl[idx / DT][idx % DT] = delta;
         s_du[idx / DT][idx % DT] = delta * uu;
-        s_gy[idx / DT][idx % DT] = gy;
+        s_gy[idx / DT][idx % DT] = go * zz * sg;
       }
     }
 #pragma unroll
@@ -331,7 +369,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     float hst[NPT];
 #pragma unroll
     for (int j = 0; j < NPT; ++j) hst[j] = r_hs[j];
-    if (c > 0) load_chunk(c - 1);  // prefetch the previous chunk while this one computes
+    if (c > 0) load_chunk(c - 1, Bool<true>());  // every chunk before the last is full
     __syncthreads();
 
     // recompute this chunk's states: lam_t and h_t into registers
@@ -341,7 +379,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       for (int j = 0; j < NPT; ++j) hs[j] = hst[j];
 #pragma unroll
       for (int i = 0; i < CHK; ++i) {
-        if (i < len) {
+        if (FULL || i < len) {
           const float dlt = s_dl[i][dl], du = s_du[i][dl];
 #pragma unroll
           for (int j = 0; j < NPT; ++j) {
@@ -351,6 +389,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
             hb[i][j] = hs[j];
           }
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
 
@@ -360,13 +399,17 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
 #pragma unroll
       for (int ii = TB - 1; ii >= 0; --ii) {
         const int i = sb * TB + ii;
-        if (i < len) {
+        if (FULL || i < len) {
           const float dlt = s_dl[i][dl], du = s_du[i][dl], gy = s_gy[i][dl];
           float aq = 0.0f, gb = 0.0f, hc = 0.0f;
 #pragma unroll
           for (int j = 0; j < NPT; ++j) {
             const float2 bcv = s_bc[i][n0 + j];
-            const float an = (i + 1 < len) ? lamb[(i + 1) % CHK][j] : lam_next[j];
+            float an;
+            if (i + 1 < CHK)
+              an = (FULL || i + 1 < len) ? lamb[(i + 1) % CHK][j] : lam_next[j];
+            else
+              an = lam_next[j];
             G[j] = fmaf(an, G[j], gy * bcv.y);
             const float hprev = (i > 0) ? hb[(i + CHK - 1) % CHK][j] : hst[j];
             const float Q = G[j] * (lamb[i][j] * hprev);  // G_t * lam_t h_{t-1}
@@ -374,9 +417,10 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
             aq = fmaf(Av[j], Q, aq);
             gb = fmaf(G[j], bcv.x, gb);
             hc = fmaf(hb[i][j], bcv.y, hc);
-            const int col = n0 + j;
-            s_dp[ii][dl][col ^ (dl & SWZ)] = G[j] * du;
-            s_dp[ii][dl][(NS + col) ^ (dl & SWZ)] = gy * hb[i][j];
+            // the two lanes of a pair write rows two apart: flip bit 4 of the channel slot for
+            // odd pairs so they land in different banks (the channel order is summed over anyway)
+            s_dp[ii][n0 + j][dl ^ (pr << 4)] = G[j] * du;
+            s_dp[ii][NS + n0 + j][dl ^ (pr << 4)] = gy * hb[i][j];
           }
           aq += swap_lane1(aq);
           gb += swap_lane1(gb);
@@ -394,7 +438,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       for (int k = 0; k < IT; ++k) {
         const int idx = tid + k * TH;
         const int t = idx / DT;
-        if (idx < CHK * DT && t >= sb * TB && t < sb * TB + TB && t < len && oact) {
+        if (idx < CHK * DT && t >= sb * TB && t < sb * TB + TB && (FULL || t < len) && oact) {
           const int ii = t - sb * TB;
           float aq = 0.0f, gb = 0.0f, hc = 0.0f;
 #pragma unroll
@@ -403,25 +447,30 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
             gb += s_np[ii][1][p][od];
             hc += s_np[ii][2][p][od];
           }
-          const float uu = o_u[k], zz = o_z[k], sg = o_sg[k];
+          const float uu = o_u[k], zz = o_z[k], sg = o_sg[k], gy = s_gy[t][od];
           const float y = fmaf(dp_o, uu, hc);
           const float gzv = o_go[k] * y * sg * (1.0f + zz * (1.0f - sg));
           const float gdelta = fmaf(uu, gb, aq);
-          const int64_t g = (b * L + t0 + t) * D + odg;
-          gdraw[g] = from_f32<TIO>(gdelta * o_sd[k]);
-          gu[g] = from_f32<TIO>(fmaf(o_dl[k], gb, o_gy[k] * dp_o));
-          gz[g] = from_f32<TIO>(gzv);
-          gdp = fmaf(o_gy[k], uu, gdp);
+          const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
+          gdraw[rowD + o] = from_f32<TIO>(gdelta * o_sd[k]);
+          gu[rowD + o] = from_f32<TIO>(fmaf(s_dl[t][od], gb, gy * dp_o));
+          gz[rowD + o] = from_f32<TIO>(gzv);
+          gdp = fmaf(gy, uu, gdp);
         }
       }
-      // grad B_t / grad C_t: sum the tile's channels for each (t, column)
+      // grad B_t / grad C_t: sum the tile's 32 channels for each (t, column); each thread
+      // reads its row as eight float4s, starting at a column-dependent quarter to spread banks
       for (int idx = tid; idx < TB * W2; idx += TH) {
         const int ii = idx / W2, col = idx % W2;
         const int t = sb * TB + ii;
-        if (t < len) {
+        if (FULL || t < len) {
+          const float4* row = reinterpret_cast<const float4*>(&s_dp[ii][col][0]);
           float s = 0.0f;
-#pragma unroll 8
-          for (int dd = 0; dd < DT; ++dd) s += s_dp[ii][dd][col ^ (dd & SWZ)];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float4 v = row[(q + col) & 7];
+            s += (v.x + v.y) + (v.z + v.w);
+          }
           gBC_part[((tile * B + b) * L + t0 + t) * W2 + col] = s;
         }
       }
@@ -429,6 +478,11 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     }
 #pragma unroll
     for (int j = 0; j < NPT; ++j) lam_next[j] = lamb[0][j];
+  };
+  for (int64_t c = NC - 1; c >= 0; --c) {
+    const int64_t t0 = c * CHK;
+    // one code path for every chunk: the guard-free variant needs ~120 more VGPRs
+    chunk(c, (int)((L - t0) < CHK ? (L - t0) : CHK), Bool<false>());
   }
 
   if (act) {
@@ -445,13 +499,13 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   // gDp: every owner thread of channel od holds a partial; sum them through LDS
   __syncthreads();
   float* red = &s_dp[0][0][0];
-  static_assert(TB * DT * W2 >= TH, "reduction scratch too small");
+  static_assert(TB * W2 * DT >= TH, "reduction scratch too small");
   red[tid] = gdp;
   __syncthreads();
   if (tid < DT && oact) {
     float s = 0.0f;
     for (int k = tid; k < TH; k += DT) s += red[k];
-    gDp_part[b * D + odg] = s;
+    gDp_part[b * D + d0 + tid] = s;
   }
 }
 
@@ -576,6 +630,12 @@ int bwd_bf16(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, const
                               gz, gDp, gh0, ws, s);
 }
 
+// The kernels index one batch row with 32-bit element offsets (t * D + d, t * N + n).
+bool offsets_fit(int64_t L, int64_t D, int64_t N) {
+  const int64_t lim = (int64_t)1 << 31;
+  return (L + 64) * D < lim && (L + 64) * N < lim;
+}
+
 int chk_interval_for(int ns) {
   switch (ns) {
     case 4:
@@ -632,6 +692,7 @@ int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
   if (B == 0 || D == 0) return TSF_OK;
   if (!A || !Dp || !h_last) return TSF_ERR_ARG;
   if (L > 0 && (!draw || !Bt || !Ct || !u || !z || !out)) return TSF_ERR_ARG;
+  if (!offsets_fit(L, D, N)) return TSF_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (io_dtype == TSF_DTYPE_F32) {
     TSF_DISPATCH_NS(ns, fwd_f32, B, L, D, N, draw, A, Bt, Ct, u, z, Dp, h0, out, h_last, chk, s)
@@ -655,6 +716,7 @@ int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
   if (h0 && !gh0) return TSF_ERR_ARG;
   if (L > chk_interval_for(ns) && !chk) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_mamba_workspace_bytes(B, L, D, N) || !workspace) return TSF_ERR_WORKSPACE;
+  if (!offsets_fit(L, D, N)) return TSF_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (io_dtype == TSF_DTYPE_F32) {
     TSF_DISPATCH_NS(ns, bwd_f32, B, L, D, N, draw, A, Bt, Ct, u, z, Dp, h0, chk, gout, ghlast, gdraw, gA, gBt, gCt,
