@@ -78,9 +78,11 @@ int tsfast_hip_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const fl
  * Layout: draw/u/z/out/gout/gdraw/gu/gz [B, L, D] and Bt/Ct/gBt/gCt [B, L, N] in io_dtype
  * (TSF_DTYPE_F32 or TSF_DTYPE_BF16); A/gA [D, N], Dp/gDp [D], h0/h_last/ghlast/gh0 [B, D, N]
  * always float32 (the state is float32 in both regimes). 1 <= N <= 64.
- * chk [B, NC, D, N] float32 with NC = ceil(L / tsfast_hip_mamba_chk_interval(N)): slot k holds
- * the state after step (k + 1) * interval - 1. chk == NULL selects the inference kernel, which
- * writes no checkpoints.
+ * chk [B, NC, N, D] float32 with NC = ceil(L / tsfast_hip_mamba_chk_interval(N)): slot k holds
+ * the state after step (k + 1) * interval - 1 (channel-contiguous, so checkpoint traffic is
+ * coalesced). chk == NULL selects the inference kernel, which writes no checkpoints.
+ * One batch row must fit 32-bit element offsets: (L + 64) * D and (L + 64) * N below 2^31,
+ * else TSF_ERR_UNSUPPORTED.
  */
 int64_t tsfast_hip_mamba_chk_interval(int64_t N);
 int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtype, const void* draw, const float* A,

@@ -125,6 +125,14 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   }
   const float dp_o = oact ? Dp[d0 + od] : 0.0f;
 
+  // workgroup-uniform row bases: loads use SGPR base + 32-bit VGPR offset addressing
+  const TIO* __restrict__ drw = draw + rowD;
+  const TIO* __restrict__ urw = u + rowD;
+  const TIO* __restrict__ zrw = z + rowD;
+  TIO* __restrict__ orw = out + rowD;
+  const TIO* __restrict__ brw = Bt + rowN;
+  const TIO* __restrict__ crw = Ct + rowN;
+
   TIO r_dr[IT], r_u[IT], r_z[IT], r_b[BCI], r_c[BCI];
   auto load_chunk = [&](uint32_t t0, auto full) __attribute__((always_inline)) {
     constexpr bool FULL = decltype(full)::value;
@@ -135,9 +143,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       bool v = idx < TF * DT && oact;
       if (!FULL) v = v && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Du + (uint32_t)od;
-      r_dr[k] = v ? draw[rowD + o] : io_zero<TIO>();
-      r_u[k] = v ? u[rowD + o] : io_zero<TIO>();
-      r_z[k] = v ? z[rowD + o] : io_zero<TIO>();
+      r_dr[k] = v ? drw[o] : io_zero<TIO>();
+      r_u[k] = v ? urw[o] : io_zero<TIO>();
+      r_z[k] = v ? zrw[o] : io_zero<TIO>();
     }
 #pragma unroll
     for (int k = 0; k < BCI; ++k) {
@@ -146,8 +154,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       bool v = idx < TF * NS && (int)n < N;
       if (!FULL) v = v && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Nu + n;
-      r_b[k] = v ? Bt[rowN + o] : io_zero<TIO>();
-      r_c[k] = v ? Ct[rowN + o] : io_zero<TIO>();
+      r_b[k] = v ? brw[o] : io_zero<TIO>();
+      r_c[k] = v ? crw[o] : io_zero<TIO>();
     }
   };
   if (L > 0) {
@@ -158,8 +166,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   }
 
   float o_u[IT], o_z[IT];
-  auto chunk = [&](uint32_t t0, int len, auto full) __attribute__((always_inline)) {
-    constexpr bool FULL = decltype(full)::value;
+  // Steps past the end of the sequence run as identity steps (delta = 0: lam = 1, no input),
+  // so the recurrence needs no per-step guard; only stores check the length.
+  auto chunk = [&](uint32_t t0, int len) __attribute__((always_inline)) {
     // phase 1: owner scalars and the B/C tile into LDS
 #pragma unroll
     for (int k = 0; k < IT; ++k) {
@@ -167,7 +176,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       if (idx < TF * DT) {
         o_u[k] = to_f32(r_u[k]);
         o_z[k] = to_f32(r_z[k]);
-        const float delta = oact ? softplus_fast(to_f32(r_dr[k])) : 0.0f;
+        const bool live = oact && idx / DT < len;
+        const float delta = live ? softplus_fast(to_f32(r_dr[k])) : 0.0f;
         s_sc[idx / DT][idx % DT] = make_float2(delta, delta * o_u[k]);
       }
     }
@@ -188,26 +198,24 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     // phase 2: the recurrence, NPT states per lane
 #pragma unroll
     for (int i = 0; i < TF; ++i) {
-      if (FULL || i < len) {
-        const float2 s = s_sc[i][dl];
-        float y = 0.0f;
+      const float2 s = s_sc[i][dl];
+      float y = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NPT; ++j) {
-          const float2 bcv = s_bc[i][n0 + j];
-          const float lam = fast_exp2(s.x * A2[j]);
-          h[j] = fmaf(lam, h[j], s.y * bcv.x);
-          y = fmaf(h[j], bcv.y, y);
-        }
-        y += swap_lane1(y);
-        if (pr == 0) s_y[i][ng >> 1][dl] = y;
-        // checkpoint slot k holds the state after step (k + 1) * CHK - 1
-        if ((i % CHK) == CHK - 1 && chk && act) {
-          const int64_t slot = ((int64_t)t0 + i) / CHK;
-          float* cp = chk + ((b * NC + slot) * D + d) * N + n0;
+      for (int j = 0; j < NPT; ++j) {
+        const float2 bcv = s_bc[i][n0 + j];
+        const float lam = fast_exp2(s.x * A2[j]);
+        h[j] = fmaf(lam, h[j], s.y * bcv.x);
+        y = fmaf(h[j], bcv.y, y);
+      }
+      y += swap_lane1(y);
+      if (pr == 0) s_y[i][ng >> 1][dl] = y;
+      // checkpoint slot k holds the state after step (k + 1) * CHK - 1 (layout [B, NC, N, D])
+      if ((i % CHK) == CHK - 1 && chk && act && i < len) {
+        const int64_t slot = ((int64_t)t0 + i) / CHK;
+        float* cp = chk + ((b * NC + slot) * N + n0) * D + d;
 #pragma unroll
-          for (int j = 0; j < NPT; ++j)
-            if (n0 + j < N) cp[j] = h[j];
-        }
+        for (int j = 0; j < NPT; ++j)
+          if (n0 + j < N) cp[(int64_t)j * D] = h[j];
       }
     }
     __syncthreads();
@@ -216,22 +224,17 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
       const int t = idx / DT;
-      if (idx < TF * DT && (FULL || t < len) && oact) {
+      if (idx < TF * DT && t < len && oact) {
         float y = 0.0f;
 #pragma unroll
         for (int p = 0; p < NPAIR; ++p) y += s_y[t][p][od];
         const float zz = o_z[k];
         const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
-        out[rowD + o] = from_f32<TIO>(fmaf(dp_o, o_u[k], y) * zz * sigmoid_fast(zz));
+        orw[o] = from_f32<TIO>(fmaf(dp_o, o_u[k], y) * zz * sigmoid_fast(zz));
       }
     }
   };
-  for (int64_t t0 = 0; t0 < L; t0 += TF) {
-    if (t0 + TF <= L)
-      chunk((uint32_t)t0, TF, Bool<true>());
-    else
-      chunk((uint32_t)t0, (int)(L - t0), Bool<false>());
-  }
+  for (int64_t t0 = 0; t0 < L; t0 += TF) chunk((uint32_t)t0, (int)((L - t0) < TF ? (L - t0) : TF));
   (void)NG;
   if (act) {
 #pragma unroll
@@ -288,6 +291,16 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   const float dp_o = oact ? Dp[d0 + od] : 0.0f;
   float gdp = 0.0f;
 
+  const TIO* __restrict__ drw = draw + rowD;
+  const TIO* __restrict__ urw = u + rowD;
+  const TIO* __restrict__ zrw = z + rowD;
+  const TIO* __restrict__ grw = gout + rowD;
+  TIO* __restrict__ gdrw = gdraw + rowD;
+  TIO* __restrict__ gurw = gu + rowD;
+  TIO* __restrict__ gzrw = gz + rowD;
+  const TIO* __restrict__ brw = Bt + rowN;
+  const TIO* __restrict__ crw = Ct + rowN;
+
   TIO r_dr[IT], r_u[IT], r_z[IT], r_go[IT], r_b[BCI], r_c[BCI];
   float r_hs[NPT];
   auto load_chunk = [&](int64_t c, auto full) __attribute__((always_inline)) {
@@ -300,10 +313,10 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       bool v = idx < CHK * DT && oact;
       if (!FULL) v = v && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Du + (uint32_t)od;
-      r_dr[k] = v ? draw[rowD + o] : io_zero<TIO>();
-      r_u[k] = v ? u[rowD + o] : io_zero<TIO>();
-      r_z[k] = v ? z[rowD + o] : io_zero<TIO>();
-      r_go[k] = v ? gout[rowD + o] : io_zero<TIO>();
+      r_dr[k] = v ? drw[o] : io_zero<TIO>();
+      r_u[k] = v ? urw[o] : io_zero<TIO>();
+      r_z[k] = v ? zrw[o] : io_zero<TIO>();
+      r_go[k] = v ? grw[o] : io_zero<TIO>();
     }
 #pragma unroll
     for (int k = 0; k < BCI; ++k) {
@@ -312,8 +325,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       bool v = idx < CHK * NS && (int)n < N;
       if (!FULL) v = v && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Nu + n;
-      r_b[k] = v ? Bt[rowN + o] : io_zero<TIO>();
-      r_c[k] = v ? Ct[rowN + o] : io_zero<TIO>();
+      r_b[k] = v ? brw[o] : io_zero<TIO>();
+      r_c[k] = v ? crw[o] : io_zero<TIO>();
     }
     // state entering the chunk: checkpoint slot c-1, or h0 for the first chunk
 #pragma unroll
@@ -322,7 +335,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       float v0 = 0.0f;
       if (act && n < N) {
         if (c > 0)
-          v0 = chk[((b * NC + c - 1) * D + d) * N + n];
+          v0 = chk[((b * NC + c - 1) * N + n) * D + d];
         else if (h0)
           v0 = h0[(b * D + d) * N + n];
       }
@@ -339,8 +352,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
 
   float lamb[CHK][NPT], hb[CHK][NPT];
   float o_u[IT], o_z[IT], o_sg[IT], o_go[IT], o_sd[IT];
-  auto chunk = [&](int64_t c, int len, auto full) __attribute__((always_inline)) {
-    constexpr bool FULL = decltype(full)::value;
+  // Steps past the end of the sequence run as identity steps (delta = 0, gy = 0: lam = 1, no
+  // input, no injected gradient), so the sweeps need no per-step guard; only stores check len.
+  auto chunk = [&](int64_t c, int len) __attribute__((always_inline)) {
     const uint32_t t0 = (uint32_t)(c * CHK);
     // phase 1: owner scalars into LDS
 #pragma unroll
@@ -349,7 +363,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       if (idx < CHK * DT) {
         const float uu = to_f32(r_u[k]), zz = to_f32(r_z[k]), go = to_f32(r_go[k]);
         const SoftplusParts sp = softplus_parts(to_f32(r_dr[k]));
-        const float delta = oact ? sp.value : 0.0f;
+        const float delta = (oact && idx / DT < len) ? sp.value : 0.0f;
         const float sg = sigmoid_fast(zz);
         o_u[k] = uu;
         o_z[k] = zz;
@@ -379,17 +393,14 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       for (int j = 0; j < NPT; ++j) hs[j] = hst[j];
 #pragma unroll
       for (int i = 0; i < CHK; ++i) {
-        if (FULL || i < len) {
-          const float dlt = s_dl[i][dl], du = s_du[i][dl];
+        const float dlt = s_dl[i][dl], du = s_du[i][dl];
 #pragma unroll
-          for (int j = 0; j < NPT; ++j) {
-            const float lam = fast_exp2(dlt * A2[j]);
-            lamb[i][j] = lam;
-            hs[j] = fmaf(lam, hs[j], du * s_bc[i][n0 + j].x);
-            hb[i][j] = hs[j];
-          }
+        for (int j = 0; j < NPT; ++j) {
+          const float lam = fast_exp2(dlt * A2[j]);
+          lamb[i][j] = lam;
+          hs[j] = fmaf(lam, hs[j], du * s_bc[i][n0 + j].x);
+          hb[i][j] = hs[j];
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
 
@@ -399,17 +410,13 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
 #pragma unroll
       for (int ii = TB - 1; ii >= 0; --ii) {
         const int i = sb * TB + ii;
-        if (FULL || i < len) {
+        {
           const float dlt = s_dl[i][dl], du = s_du[i][dl], gy = s_gy[i][dl];
           float aq = 0.0f, gb = 0.0f, hc = 0.0f;
 #pragma unroll
           for (int j = 0; j < NPT; ++j) {
             const float2 bcv = s_bc[i][n0 + j];
-            float an;
-            if (i + 1 < CHK)
-              an = (FULL || i + 1 < len) ? lamb[(i + 1) % CHK][j] : lam_next[j];
-            else
-              an = lam_next[j];
+            const float an = (i + 1 < CHK) ? lamb[(i + 1) % CHK][j] : lam_next[j];
             G[j] = fmaf(an, G[j], gy * bcv.y);
             const float hprev = (i > 0) ? hb[(i + CHK - 1) % CHK][j] : hst[j];
             const float Q = G[j] * (lamb[i][j] * hprev);  // G_t * lam_t h_{t-1}
@@ -438,7 +445,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       for (int k = 0; k < IT; ++k) {
         const int idx = tid + k * TH;
         const int t = idx / DT;
-        if (idx < CHK * DT && t >= sb * TB && t < sb * TB + TB && (FULL || t < len) && oact) {
+        if (idx < CHK * DT && t >= sb * TB && t < sb * TB + TB && t < len && oact) {
           const int ii = t - sb * TB;
           float aq = 0.0f, gb = 0.0f, hc = 0.0f;
 #pragma unroll
@@ -452,9 +459,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
           const float gzv = o_go[k] * y * sg * (1.0f + zz * (1.0f - sg));
           const float gdelta = fmaf(uu, gb, aq);
           const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
-          gdraw[rowD + o] = from_f32<TIO>(gdelta * o_sd[k]);
-          gu[rowD + o] = from_f32<TIO>(fmaf(s_dl[t][od], gb, gy * dp_o));
-          gz[rowD + o] = from_f32<TIO>(gzv);
+          gdrw[o] = from_f32<TIO>(gdelta * o_sd[k]);
+          gurw[o] = from_f32<TIO>(fmaf(s_dl[t][od], gb, gy * dp_o));
+          gzrw[o] = from_f32<TIO>(gzv);
           gdp = fmaf(gy, uu, gdp);
         }
       }
@@ -463,7 +470,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       for (int idx = tid; idx < TB * W2; idx += TH) {
         const int ii = idx / W2, col = idx % W2;
         const int t = sb * TB + ii;
-        if (FULL || t < len) {
+        if (t < len) {
           const float4* row = reinterpret_cast<const float4*>(&s_dp[ii][col][0]);
           float s = 0.0f;
 #pragma unroll
@@ -481,8 +488,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   };
   for (int64_t c = NC - 1; c >= 0; --c) {
     const int64_t t0 = c * CHK;
-    // one code path for every chunk: the guard-free variant needs ~120 more VGPRs
-    chunk(c, (int)((L - t0) < CHK ? (L - t0) : CHK), Bool<false>());
+    chunk(c, (int)((L - t0) < CHK ? (L - t0) : CHK));
   }
 
   if (act) {

@@ -95,7 +95,7 @@ def _forward(draw, A, Bt, Ct, u, z, Dp, h0, store_chk: bool):
     chk = None
     if store_chk:
         nc = -(-L // chk_interval(N))
-        chk = torch.empty(B, nc, D, N, device=draw.device, dtype=torch.float32)
+        chk = torch.empty(B, nc, N, D, device=draw.device, dtype=torch.float32)
     _lib.check(
         lib.tsfast_hip_mamba_fwd(
             B, L, D, N, _IO_DTYPES[draw.dtype], *map(_lib.ptr, (draw, A, Bt, Ct, u, z, Dp, h0, out, h_last, chk)),
@@ -145,7 +145,7 @@ def _fake_outs(draw, A, with_chk: bool):
     h_last = draw.new_empty(B, D, N, dtype=torch.float32)
     if not with_chk:
         return out, h_last
-    return out, h_last, draw.new_empty(B, -(-L // chk_interval(N)), D, N, dtype=torch.float32)
+    return out, h_last, draw.new_empty(B, -(-L // chk_interval(N)), N, D, dtype=torch.float32)
 
 
 @_scan_op.register_fake
