@@ -1,9 +1,10 @@
-"""Benchmark: fused Mamba selective scan forward + backward on one MI355X.
+"""Benchmark of the scan family on one MI355X; default = the headline metric.
 
-Workload: B=16, L=4096, D=1536, N=16, bf16 I/O (draw, u, z, Bt, Ct,
-out and their gradients) with fp32 state, fp32 A/Dp. A = -exp(log(arange(1, 17))) broadcast over
-D; delta = softplus(draw), draw ~ N(-4, 1); Bt, Ct, u, z, Dp ~ N(0, 1); h0 = None; upstream
-gradient gout ~ N(0, 1), ghlast = None. Synthetic data, inputs resident in HBM before timing.
+Default workload: fused Mamba selective scan, B=16, L=4096, D=1536,
+N=16, bf16 I/O (draw, u, z, Bt, Ct, out and their gradients) with fp32 state and fp32 A/Dp.
+A = -exp(log(arange(1, 17))) broadcast over D; delta = softplus(draw), draw ~ N(-4, 1);
+Bt, Ct, u, z, Dp ~ N(0, 1); h0 = None; upstream gradient gout ~ N(0, 1), ghlast = None.
+Synthetic data, inputs resident in HBM before timing.
 
 One step = the training forward (tsfast_hip::mamba_scan_train: output, h_last and the state
 checkpoints) followed by the backward (tsfast_hip::mamba_scan_bwd: all eight gradients). W warmup
@@ -11,17 +12,24 @@ steps, then K timed steps between two device synchronisations. ``value`` is the 
 algorithmic HBM bandwidth of the whole step (compulsory bytes of the op's inputs, outputs and
 gradients, once each) in GB/s; ``ms_per_step`` is fwd+bwd milliseconds.
 
-The CPU column times the C++/OpenMP port of the reference CPU kernels
-(oracle/cpu_baseline.cpp, following mamba/backend_c.py) on a bounded sample of the same
-workload: one batch row (B=1) of config 3, fp32 (the reference CPU regime).
+``--config 1|2|4|5`` runs the other BASELINE configs the same way (diagonal scan real / complex,
+dynoNet all-pole, TBPTT diagonal scan as 64 chunks with the state carried); these are for the
+design notes, the driver's line is config 3.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--io bf16|fp32] [--no-cpu]
+The CPU column times the reference CPU path on a bounded sample of the same workload, on the
+host's cores: the C++/OpenMP port of the reference CPU kernels (oracle/cpu_baseline.cpp, after
+mamba/backend_c.py and scan_backends/diagonal_c.py) for configs 1, 2, 3, 5, and the
+companion-matrix doubling scan (tsfast_amd.dynonet.linear_recurrence on CPU, the reference CPU
+path of dynonet/core.py:23-88) for config 4.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 3] [--io bf16|fp32] [--no-cpu]
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -33,10 +41,11 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "fwd+bwd ms + achieved HBM GB/s (% peak), selective scan B16 L4096 D1536 N16"
 HBM_PEAK_GBS = 8000.0
-CFG = dict(B=16, L=4096, D=1536, N=16)
+CFG3 = dict(B=16, L=4096, D=1536, N=16)
 
 
-def algorithmic_bytes(B, L, D, N, io_bytes):
+# --------------------------------------------------------------------------- algorithmic bytes
+def mamba_bytes(B, L, D, N, io_bytes):
     """Compulsory bytes, once each: (fwd, bwd)."""
     bld, bln = B * L * D, B * L * N
     params = D * N * 4 + D * 4
@@ -45,7 +54,13 @@ def algorithmic_bytes(B, L, D, N, io_bytes):
     return fwd, bwd
 
 
-def make_inputs(B, L, D, N, io_dtype, device, seed=2):
+def scan_bytes(elems, esz, lanes, lane_esz):
+    """Diagonal / all-pole scan: fwd reads v, writes out; bwd reads g and out, writes gv (+ per-lane terms)."""
+    return 2 * elems * esz + lanes * lane_esz, 3 * elems * esz + 2 * lanes * lane_esz
+
+
+# --------------------------------------------------------------------------- inputs
+def mamba_inputs(B, L, D, N, io_dtype, device, seed=2):
     import torch
 
     g = torch.Generator().manual_seed(seed)
@@ -65,43 +80,278 @@ def make_inputs(B, L, D, N, io_dtype, device, seed=2):
     return {k: v.to(device) for k, v in t.items()}
 
 
-def cpu_baseline(io_dtype, budget_s=20.0):
-    """Time the reference-port CPU kernels on one batch row of config 3 (fp32 regime)."""
+def diag_inputs(cfg, device):
+    """Configs 1, 2, 5 in the lane layout (lam [M, N], v/g [M, L, N])."""
+    import torch
+
+    g = torch.Generator().manual_seed(cfg - 1)
+    if cfg == 1:
+        lam = torch.rand(32, 64, generator=g) * 0.099 + 0.9
+        v = torch.randn(32, 1000, 64, generator=g)
+        gv = torch.randn(32, 1000, 64, generator=g)
+    elif cfg == 2:
+        from tsfast_amd.scan import complex_in_proj, real_out_proj
+
+        H, n = 32, 256
+        lam1 = torch.polar(torch.rand(n, generator=g) * 0.099 + 0.9, torch.rand(n, generator=g) * (math.pi / 10))
+        lam = lam1.expand(64, n).contiguous()
+        u = torch.randn(64, 4096, H, generator=g)
+        B_re = torch.randn(n, H, generator=g) / math.sqrt(2 * H)
+        B_im = torch.randn(n, H, generator=g) / math.sqrt(2 * H)
+        v = complex_in_proj(u, B_re, B_im).contiguous()
+        C_re = torch.randn(H, n, generator=g) / math.sqrt(n)
+        C_im = torch.randn(H, n, generator=g) / math.sqrt(n)
+        # g_h = d(sum(gy * Re(h C^T)))/dh for gy ~ N(0,1): the readout's adjoint, computed once
+        h = torch.zeros_like(v, requires_grad=True)
+        gy = torch.randn(64, 4096, H, generator=g)
+        (real_out_proj(h, C_re, C_im) * gy).sum().backward()
+        gv = h.grad.contiguous()
+    else:  # 5: one 4096-step chunk shape; the runner loops 64 chunks
+        lam = torch.rand(8, 128, generator=g) * 0.0099 + 0.99
+        v = torch.randn(8, 64 * 4096, 128, generator=g)
+        gv = torch.randn(8, 64 * 4096, 128, generator=g)
+    return lam.to(device), v.to(device), gv.to(device)
+
+
+def allpole_inputs(device, P=64, B=64, L=16384, na=3):
+    """Config 4: per pair, poles p, conj(p), r with |p|, |r| ~ U(0.5, 0.98); a = poly(poles)[1:]."""
     import numpy as np
     import torch
 
-    from oracle import cpu_baseline as CB
+    rng = np.random.default_rng(3)
+    rows = []
+    for _ in range(P):
+        rp = rng.uniform(0.5, 0.98)
+        th = rng.uniform(0, math.pi)
+        rr = rng.uniform(0.5, 0.98) * (1 if rng.random() < 0.5 else -1)
+        rows.append(np.real(np.poly([rp * np.exp(1j * th), rp * np.exp(-1j * th), rr]))[1:])
+    a = torch.tensor(np.array(rows), dtype=torch.float32)
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(B, P, L, generator=g)
+    gout = torch.randn(B, P, L, generator=g)
+    a_lane = a.expand(B, P, na).reshape(B * P, na).contiguous()
+    return a_lane.to(device), w.reshape(B * P, L).to(device), gout.reshape(B * P, L).to(device)
 
-    lib = CB.load(prefer_native=True)
-    threads = os.cpu_count() or 1
-    lib.cpu_set_threads(threads)
-    B, L, D, N = 1, CFG["L"], CFG["D"], CFG["N"]
-    x = make_inputs(B, L, D, N, io_dtype, "cpu")
-    a = {k: v.float().numpy() for k, v in x.items()}
-    args = [a[k] for k in ("draw", "A", "Bt", "Ct", "u", "z", "Dp")]
+
+# --------------------------------------------------------------------------- timing
+def time_steps(step, steps, warmup):
+    """W untimed steps, then K timed steps between device synchronisations; step(ev) records
+    events at phase boundaries. Returns (ms per step, [mean ms per phase])."""
+    import torch
+
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    events = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ev = []
+        step(ev)
+        events.append(ev)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    phases = []
+    if events and events[0]:
+        for p in range(len(events[0]) - 1):
+            phases.append(statistics.mean(e[p].elapsed_time(e[p + 1]) for e in events))
+    return (t1 - t0) * 1e3 / steps, phases
+
+
+def mark(ev):
+    """Record an event on the current stream (the one every kernel here is launched on)."""
+    import torch
+
+    if ev is not None:
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        ev.append(e)
+
+
+def cpu_time(fn, budget_s=20.0, reps=5):
+    fn()  # warmup
     times = []
     t_start = time.perf_counter()
-    CB.mamba_fwd_bwd(*args, a["gout"])  # warmup
-    while len(times) < 5 and (time.perf_counter() - t_start) < budget_s:
+    while len(times) < reps and (time.perf_counter() - t_start) < budget_s:
         t0 = time.perf_counter()
-        CB.mamba_fwd_bwd(*args, a["gout"])
+        fn()
         times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    fwd_b, bwd_b = algorithmic_bytes(B, L, D, N, 2 if io_dtype == torch.bfloat16 else 4)
-    del np
-    return {
-        "value": round((fwd_b + bwd_b) / med / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (
-            f"one batch row (B=1, L={L}, D={D}, N={N}) of config 3, fp32 (reference CPU regime, "
-            f"oracle/cpu_baseline.cpp after mamba/backend_c.py), fwd+bwd median of {len(times)} runs "
-            f"= {med * 1e3:.1f} ms; full config 3 would take ~{med * CFG['B'] * 1e3:.0f} ms; "
-            f"build {CB.lib_path().name}"
-        ),
-        "ms_per_step_sample": round(med * 1e3, 3),
-    }
+    return statistics.median(times), len(times)
+
+
+# --------------------------------------------------------------------------- workloads
+def run_mamba(args, line):
+    import torch
+
+    from tsfast_amd.mamba import mamba_hip
+
+    io_dtype = torch.bfloat16 if args.io == "bf16" else torch.float32
+    B, L, D, N = CFG3["B"], CFG3["L"], CFG3["D"], CFG3["N"]
+    x = mamba_inputs(B, L, D, N, io_dtype, "cuda")
+    fargs = [x[k] for k in ("draw", "A", "Bt", "Ct", "u", "z", "Dp")] + [None]
+
+    def step(ev):
+        mark(ev)
+        out, h_last, chk = mamba_hip._scan_train_op(*fargs)
+        mark(ev)
+        mamba_hip._scan_bwd_op(x["gout"], None, chk, *fargs)
+        mark(ev)
+
+    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
+    fwd_b, bwd_b = mamba_bytes(B, L, D, N, 2 if io_dtype == torch.bfloat16 else 4)
+    line.update(
+        config={
+            "workload": "fused Mamba selective scan, train forward (checkpoints) + backward, BASELINE config 3",
+            "B": B, "L": L, "D": D, "N": N, "io_dtype": args.io, "state_dtype": "f32",
+        },
+        fwd_ms=round(fwd_ms, 4),
+        bwd_ms=round(bwd_ms, 4),
+    )
+    kernels = {"fwd": ("mamba_fwd_kernel", fwd_ms, fwd_b),
+               "bwd": ("mamba_bwd_kernel + its partial reductions (one ABI call)", bwd_ms, bwd_b)}
+    cpu = None
+    if not args.no_cpu:
+        def cpu_leg():
+            from oracle import cpu_baseline as CB
+
+            lib = CB.load(prefer_native=True)
+            threads = os.cpu_count() or 1
+            lib.cpu_set_threads(threads)
+            xs = mamba_inputs(1, L, D, N, io_dtype, "cpu")
+            a = {k: v.float().numpy() for k, v in xs.items()}
+            margs = [a[k] for k in ("draw", "A", "Bt", "Ct", "u", "z", "Dp")]
+            med, n = cpu_time(lambda: CB.mamba_fwd_bwd(*margs, a["gout"]))
+            sf, sb = mamba_bytes(1, L, D, N, 2 if io_dtype == torch.bfloat16 else 4)
+            return {
+                "value": round((sf + sb) / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": (f"one batch row (B=1, L={L}, D={D}, N={N}) of config 3, fp32 (reference CPU regime, "
+                           f"oracle/cpu_baseline.cpp after mamba/backend_c.py), fwd+bwd median of {n} runs = "
+                           f"{med * 1e3:.1f} ms; full config 3 would take ~{med * B * 1e3:.0f} ms; "
+                           f"build {CB.lib_path().name}"),
+                "ms_per_step_sample": round(med * 1e3, 3),
+            }
+        cpu = cpu_leg
+    return ms, fwd_b + bwd_b, kernels, cpu
+
+
+def run_diag(args, line):
+    from tsfast_amd.scan_backends import diagonal_hip
+
+    cfg = args.config
+    lam, v, gv = diag_inputs(cfg, "cuda")
+    cplx = v.is_complex()
+    esz = 8 if cplx else 4
+    if cfg == 5:
+        T, C = 4096, 64
+        chunks_v = [v[:, k * T : (k + 1) * T].contiguous() for k in range(C)]
+        chunks_g = [gv[:, k * T : (k + 1) * T].contiguous() for k in range(C)]
+
+        def step(ev):
+            mark(ev)
+            x0 = None
+            outs = []
+            for k in range(C):
+                o = diagonal_hip.forward(lam, chunks_v[k], x0)
+                outs.append((o, x0))
+                x0 = o[:, -1].contiguous()
+            mark(ev)
+            for k in range(C - 1, -1, -1):
+                o, xin = outs[k]
+                diagonal_hip.backward(chunks_g[k], lam, o, xin)
+            mark(ev)
+
+        fwd_b, bwd_b = scan_bytes(v.numel(), esz, lam.numel() * C, esz)
+        workload = "TBPTT real diagonal scan, 64 chunks x 4096 with x0 carry, fwd+bwd, BASELINE config 5"
+    else:
+        def step(ev):
+            mark(ev)
+            o = diagonal_hip.forward(lam, v, None)
+            mark(ev)
+            diagonal_hip.backward(gv, lam, o, None)
+            mark(ev)
+
+        fwd_b, bwd_b = scan_bytes(v.numel(), esz, lam.numel(), esz)
+        workload = ("real diagonal scan fwd+bwd, BASELINE config 1" if cfg == 1
+                    else "complex64 diagonal scan fwd+bwd (scan only; projections outside), BASELINE config 2")
+    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
+    M, L, N = v.shape
+    line.update(config={"workload": workload, "M": M, "L": L, "N": N, "io_dtype": "complex64" if cplx else "f32"},
+                fwd_ms=round(fwd_ms, 4), bwd_ms=round(bwd_ms, 4))
+    line["dtype"] = "c128" if cplx else "f64"  # fp32/complex64 I/O, fp64 state inside
+    kernels = {"fwd": ("diag fwd (chunk summaries + re-scan)", fwd_ms, fwd_b),
+               "bwd": ("diag bwd (chunk summaries + re-scan + lane sums)", bwd_ms, bwd_b)}
+    cpu = None
+    if not args.no_cpu:
+        def cpu_leg():
+            from oracle import cpu_baseline as CB
+
+            lib = CB.load(prefer_native=True)
+            threads = os.cpu_count() or 1
+            lib.cpu_set_threads(threads)
+            rows = {1: M, 2: 4, 5: M}[cfg]
+            Ls = {1: L, 2: L, 5: 4 * 4096}[cfg]
+            lam_c, v_c, g_c = (t.cpu().numpy() for t in (lam[:rows], v[:rows, :Ls], gv[:rows, :Ls]))
+            med, n = cpu_time(lambda: CB.diag_fwd_bwd(lam_c, v_c, g_c, None))
+            sf, sb = scan_bytes(rows * Ls * N, esz, rows * N, esz)
+            return {
+                "value": round((sf + sb) / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": (f"rows={rows}, L={Ls}, N={N} of config {cfg} (oracle/cpu_baseline.cpp after "
+                           f"scan_backends/diagonal_c.py, single pass per (row, 64-lane block)), fwd+bwd median "
+                           f"of {n} runs = {med * 1e3:.2f} ms"),
+            }
+        cpu = cpu_leg
+    return ms, fwd_b + bwd_b, kernels, cpu
+
+
+def run_allpole(args, line):
+    from tsfast_amd.dynonet import allpole_hip
+
+    a, w, gout = allpole_inputs("cuda")
+    lanes, L = w.shape
+
+    def step(ev):
+        mark(ev)
+        y = allpole_hip._allpole_op(a, w, None)
+        mark(ev)
+        allpole_hip._allpole_bwd_op(gout, a, y, None)
+        mark(ev)
+
+    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
+    fwd_b, bwd_b = scan_bytes(w.numel(), 4, lanes, 12)
+    line.update(config={"workload": "dynoNet all-pole IIR scan fwd+bwd, na=3, BASELINE config 4",
+                        "lanes": lanes, "L": L, "na": 3}, fwd_ms=round(fwd_ms, 4), bwd_ms=round(bwd_ms, 4))
+    line["dtype"] = "f64"  # fp32 I/O, fp64 recurrence inside
+    kernels = {"fwd": ("allpole fwd (transfer + chunk ends + carries + apply)", fwd_ms, fwd_b),
+               "bwd": ("allpole bwd", bwd_ms, bwd_b)}
+    cpu = None
+    if not args.no_cpu:
+        def cpu_leg():
+            import torch
+            import torch.nn.functional as F
+
+            from tsfast_amd.dynonet.core import companion, linear_recurrence
+
+            threads = os.cpu_count() or 1
+            torch.set_num_threads(threads)
+            rows = 64
+            a_c = a[:rows].cpu()
+            w_c = w[:rows].cpu()
+            g_c = gout[:rows].cpu()
+            Cm = companion(a_c)
+
+            def fb():
+                v = F.pad(w_c.unsqueeze(-1), (0, 2)).requires_grad_()
+                x = linear_recurrence(Cm, v, None)
+                x[..., 0].backward(g_c)
+
+            med, n = cpu_time(fb)
+            sf, sb = scan_bytes(rows * L, 4, rows, 12)
+            return {
+                "value": round((sf + sb) / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": (f"{rows} of {lanes} lanes, L={L}: companion-matrix doubling scan on CPU (the reference "
+                           f"CPU path, dynonet/core.py:23-88), fwd+bwd median of {n} runs = {med * 1e3:.1f} ms"),
+            }
+        cpu = cpu_leg
+    return ms, fwd_b + bwd_b, kernels, cpu
 
 
 def main():
@@ -109,8 +359,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--io", choices=("bf16", "fp32"), default="bf16")
+    ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5))
+    ap.add_argument("--io", choices=("bf16", "fp32"), default="bf16", help="config 3 I/O dtype")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    ap.add_argument(
+        "--copy-calibration",
+        action="store_true",
+        help="only run a plain 512 MiB elementwise copy (to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)",
+    )
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
@@ -122,80 +378,55 @@ def main():
 
     import torch
 
-    from tsfast_amd import _lib
-    from tsfast_amd.mamba import mamba_hip
-
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_calibration:
+        # an elementwise kernel (plain vector loads/stores), not the runtime's blit copy
+        src = torch.ones(128 << 20, dtype=torch.float32, device="cuda")  # 512 MiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "copies": 5}), flush=True)
+        return
+
+    from tsfast_amd import _lib
+
     _lib.load()
-    dev = torch.device("cuda", 0)
-    io_dtype = torch.bfloat16 if args.io == "bf16" else torch.float32
-    B, L, D, N = CFG["B"], CFG["L"], CFG["D"], CFG["N"]
-    x = make_inputs(B, L, D, N, io_dtype, dev)
-    fargs = [x[k] for k in ("draw", "A", "Bt", "Ct", "u", "z", "Dp")] + [None]
-
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record()
-        out, h_last, chk = mamba_hip._scan_train_op(*fargs)
-        if ev is not None:
-            ev[1].record()
-        grads = mamba_hip._scan_bwd_op(x["gout"], None, chk, *fargs)
-        if ev is not None:
-            ev[2].record()
-        return out, grads
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        step(events[k])
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms = (t1 - t0) * 1e3 / args.steps
-    fwd_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
-    bwd_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in events)
-    io_bytes = 2 if io_dtype == torch.bfloat16 else 4
-    fwd_b, bwd_b = algorithmic_bytes(B, L, D, N, io_bytes)
-    gbs = (fwd_b + bwd_b) / (ms * 1e-3) / 1e9
-    dom = "bwd" if bwd_ms >= fwd_ms else "fwd"
-    dom_ms, dom_b = (bwd_ms, bwd_b) if dom == "bwd" else (fwd_ms, fwd_b)
-    achieved = dom_b / (dom_ms * 1e-3) / 1e9
     line = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
+        "metric": METRIC if args.config == 3 else f"fwd+bwd ms + achieved HBM GB/s, BASELINE config {args.config}",
+        "value": None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {
-            "workload": "fused Mamba selective scan, train forward (checkpoints) + backward, BASELINE config 3",
-            "B": B, "L": L, "D": D, "N": N, "io_dtype": args.io, "state_dtype": "f32",
-        },
-        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "fwd_ms": round(fwd_ms, 4),
-        "bwd_ms": round(bwd_ms, 4),
-        "algorithmic_bytes": {"fwd": fwd_b, "bwd": bwd_b},
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "mamba_fwd_kernel" if dom == "fwd" else "mamba_bwd_kernel + its partial reductions (one ABI call)",
-            "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-        },
     }
-    if not args.no_cpu:
+    runner = {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config]
+    ms, total_bytes, kernels, cpu = runner(args, line)
+    gbs = total_bytes / (ms * 1e-3) / 1e9
+    line["value"] = round(gbs, 2)
+    line["ms_per_step"] = round(ms, 4)
+    line["pct_hbm_peak"] = round(100 * gbs / HBM_PEAK_GBS, 2)
+    line["algorithmic_bytes"] = {k: v[2] for k, v in kernels.items()}
+    name, dom_ms, dom_b = max(kernels.values(), key=lambda k: k[1])
+    achieved = dom_b / (dom_ms * 1e-3) / 1e9
+    line["roofline"] = {
+        "bound": "hbm",
+        "kernel": name,
+        "achieved": round(achieved, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": None,
+    }
+    if cpu is not None:
         try:
-            line["cpu_baseline"] = cpu_baseline(io_dtype)
+            line["cpu_baseline"] = cpu()
         except Exception as e:  # noqa: BLE001 - reported, not fatal to the GPU number
             line["cpu_baseline"] = {"value": None, "error": repr(e)}
     print(json.dumps(line), flush=True)
