@@ -36,11 +36,44 @@ inline dim3 grid_for(int64_t threads) { return dim3((unsigned)((threads + 255) /
 
 int64_t allpole_chunk(int64_t lanes, int64_t L, int64_t na) {
   if (L < 1) return 1;
-  const int64_t target_threads = 256 * 1024 * 2;
+  // one wave per (64-lane group, chunk): aim for ~4096 waves, chunks of at least 64 steps
+  const int64_t groups = (lanes + 63) / 64;
+  const int64_t target_waves = 4096;
   int64_t T_c = L;
-  const int64_t min_len = na > 32 ? na : 32;
-  while (T_c / 2 >= min_len && lanes * ((L + T_c - 1) / T_c) < target_threads) T_c = (T_c + 1) / 2;
+  const int64_t min_len = na > 64 ? na : 64;
+  while (T_c / 2 >= min_len && groups * ((L + T_c - 1) / T_c) < target_waves) T_c = (T_c + 1) / 2;
   return T_c;
+}
+
+// Streaming kernels: one wave owns 64 consecutive lanes x one time chunk. Time-contiguous rows
+// are moved through a [64 x 33] LDS tile: the wave loads/stores 32-step row segments with
+// coalesced 128-byte accesses, and each lane then walks its own row from LDS (the padding keeps
+// the column walk conflict-free). The recurrence itself runs in fp64 registers.
+constexpr int kTile = 64;   // lanes per wave (tile rows)
+constexpr int kTileT = 32;  // time steps per tile (tile columns)
+
+// rows [l0, l0+64) x columns [c0, c0+ncol) of a [lanes, L] matrix <-> tile (zero outside).
+// Each access instruction moves two rows: lanes 0-31 one row, lanes 32-63 the next, 128-byte
+// contiguous segments.
+TSF_DEV void tile_load(float (*tile)[kTileT + 1], const float* __restrict__ src, int64_t lanes, int64_t L,
+                       int64_t l0, int64_t c0, int ncol) {
+  const int col = threadIdx.x & (kTileT - 1), half = threadIdx.x >> 5;
+#pragma unroll 8
+  for (int r2 = 0; r2 < kTile / 2; ++r2) {
+    const int r = 2 * r2 + half;
+    const int64_t lane = l0 + r;
+    tile[r][col] = (lane < lanes && col < ncol) ? src[lane * L + c0 + col] : 0.0f;
+  }
+}
+TSF_DEV void tile_store(float (*tile)[kTileT + 1], float* __restrict__ dst, int64_t lanes, int64_t L, int64_t l0,
+                        int64_t c0, int ncol) {
+  const int col = threadIdx.x & (kTileT - 1), half = threadIdx.x >> 5;
+#pragma unroll 8
+  for (int r2 = 0; r2 < kTile / 2; ++r2) {
+    const int r = 2 * r2 + half;
+    const int64_t lane = l0 + r;
+    if (lane < lanes && col < ncol) dst[lane * L + c0 + col] = tile[r][col];
+  }
 }
 
 // 1. M = C^{T_c} for the companion matrix C of lane `lane`: row 0 is (-a_1 .. -a_NA), row k is
@@ -99,11 +132,13 @@ __global__ void __launch_bounds__(256) allpole_transfer(const float* __restrict_
 }
 
 // One filter step on the register delay line: returns the new output and shifts it in.
+// The oldest taps are accumulated first so that only the last FMA (with y_{t-1}) sits on the
+// step-to-step dependency chain.
 template <int NA>
 TSF_DEV double step(const double (&av)[NA], double (&s)[NA], double x) {
   double acc = x;
 #pragma unroll
-  for (int k = 0; k < NA; ++k) acc = fma(-av[k], s[k], acc);
+  for (int k = NA - 1; k >= 0; --k) acc = fma(-av[k], s[k], acc);
 #pragma unroll
   for (int k = NA - 1; k > 0; --k) s[k] = s[k - 1];
   s[0] = acc;
@@ -112,22 +147,33 @@ TSF_DEV double step(const double (&av)[NA], double (&s)[NA], double x) {
 
 // 2. forward chunk ends from a zero entering state, chunks 0 .. nchunk-2.
 template <int NA>
-__global__ void __launch_bounds__(256) allpole_fwd_chunk_end(const float* __restrict__ a, const float* __restrict__ w,
-                                                             double* __restrict__ e, int64_t lanes, int64_t L,
-                                                             int64_t T_c, int64_t nchunk) {
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes, c = gid / lanes;
-  if (c >= nchunk - 1) return;
+__global__ void __launch_bounds__(kTile) allpole_fwd_chunk_end(const float* __restrict__ a,
+                                                               const float* __restrict__ w, double* __restrict__ e,
+                                                               int64_t lanes, int64_t L, int64_t T_c,
+                                                               int64_t nchunk) {
+  __shared__ float tile[kTile][kTileT + 1];
+  const int tid = threadIdx.x;
+  const int64_t l0 = (int64_t)blockIdx.x * kTile, c = blockIdx.y;
+  const int64_t lane = l0 + tid;
+  const bool act = lane < lanes;
   double av[NA], s[NA];
 #pragma unroll
   for (int k = 0; k < NA; ++k) {
-    av[k] = (double)a[lane * NA + k];
+    av[k] = act ? (double)a[lane * NA + k] : 0.0;
     s[k] = 0.0;
   }
-  const float* wp = w + lane * L + c * T_c;
-  for (int64_t i = 0; i < T_c; ++i) step<NA>(av, s, (double)wp[i]);
+  const int64_t t0 = c * T_c;
+  for (int64_t tt = 0; tt < T_c; tt += kTileT) {
+    const int n = (int)((T_c - tt) < kTileT ? (T_c - tt) : kTileT);
+    tile_load(tile, w, lanes, L, l0, t0 + tt, n);
+    __syncthreads();
+    for (int k = 0; k < n; ++k) step<NA>(av, s, (double)tile[tid][k]);
+    __syncthreads();
+  }
+  if (act) {
 #pragma unroll
-  for (int k = 0; k < NA; ++k) e[(c * lanes + lane) * NA + k] = s[k];
+    for (int k = 0; k < NA; ++k) e[(c * lanes + lane) * NA + k] = s[k];
+  }
 }
 
 // 3. forward carries: entering state of every chunk, sequential over chunks per lane.
@@ -163,46 +209,64 @@ __global__ void __launch_bounds__(256) allpole_fwd_carry(const double* __restric
 
 // 4. forward apply.
 template <int NA>
-__global__ void __launch_bounds__(256) allpole_fwd_apply(const float* __restrict__ a, const float* __restrict__ w,
-                                                         const double* __restrict__ S, float* __restrict__ y,
-                                                         int64_t lanes, int64_t L, int64_t T_c, int64_t nchunk) {
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes, c = gid / lanes;
-  if (c >= nchunk) return;
+__global__ void __launch_bounds__(kTile) allpole_fwd_apply(const float* __restrict__ a, const float* __restrict__ w,
+                                                           const double* __restrict__ S, float* __restrict__ y,
+                                                           int64_t lanes, int64_t L, int64_t T_c, int64_t nchunk) {
+  __shared__ float tile[kTile][kTileT + 1];
+  const int tid = threadIdx.x;
+  const int64_t l0 = (int64_t)blockIdx.x * kTile, c = blockIdx.y;
+  const int64_t lane = l0 + tid;
+  const bool act = lane < lanes;
   double av[NA], s[NA];
 #pragma unroll
   for (int k = 0; k < NA; ++k) {
-    av[k] = (double)a[lane * NA + k];
-    s[k] = S[(c * lanes + lane) * NA + k];
+    av[k] = act ? (double)a[lane * NA + k] : 0.0;
+    s[k] = act ? S[(c * lanes + lane) * NA + k] : 0.0;
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
-  const float* wp = w + lane * L + t0;
-  float* yp = y + lane * L + t0;
-  for (int64_t i = 0; i < len; ++i) yp[i] = (float)step<NA>(av, s, (double)wp[i]);
+  for (int64_t tt = 0; tt < len; tt += kTileT) {
+    const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
+    tile_load(tile, w, lanes, L, l0, t0 + tt, n);
+    __syncthreads();
+    for (int k = 0; k < n; ++k) tile[tid][k] = (float)step<NA>(av, s, (double)tile[tid][k]);
+    __syncthreads();
+    tile_store(tile, y, lanes, L, l0, t0 + tt, n);
+    __syncthreads();
+  }
 }
 
 // Backward 2. reverse chunk exits (G_{t0}, G_{t0+1}, ...) with zero entering state, chunks >= 1.
 template <int NA>
-__global__ void __launch_bounds__(256) allpole_bwd_chunk_start(const float* __restrict__ a,
-                                                               const float* __restrict__ g, double* __restrict__ f,
-                                                               int64_t lanes, int64_t L, int64_t T_c,
-                                                               int64_t nchunk) {
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes, c = gid / lanes + 1;
-  if (c >= nchunk) return;
+__global__ void __launch_bounds__(kTile) allpole_bwd_chunk_start(const float* __restrict__ a,
+                                                                 const float* __restrict__ g, double* __restrict__ f,
+                                                                 int64_t lanes, int64_t L, int64_t T_c,
+                                                                 int64_t nchunk) {
+  __shared__ float tile[kTile][kTileT + 1];
+  const int tid = threadIdx.x;
+  const int64_t l0 = (int64_t)blockIdx.x * kTile, c = (int64_t)blockIdx.y + 1;
+  const int64_t lane = l0 + tid;
+  const bool act = lane < lanes;
   double av[NA], s[NA];
 #pragma unroll
   for (int k = 0; k < NA; ++k) {
-    av[k] = (double)a[lane * NA + k];
+    av[k] = act ? (double)a[lane * NA + k] : 0.0;
     s[k] = 0.0;
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
-  const float* gp = g + lane * L + t0;
-  for (int64_t i = len - 1; i >= 0; --i) step<NA>(av, s, (double)gp[i]);
+  const int64_t last = ((len - 1) / kTileT) * kTileT;
+  for (int64_t tt = last; tt >= 0; tt -= kTileT) {
+    const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
+    tile_load(tile, g, lanes, L, l0, t0 + tt, n);
+    __syncthreads();
+    for (int k = n - 1; k >= 0; --k) step<NA>(av, s, (double)tile[tid][k]);
+    __syncthreads();
+  }
+  if (act) {
 #pragma unroll
-  for (int k = 0; k < NA; ++k) f[(c * lanes + lane) * NA + k] = s[k];
+    for (int k = 0; k < NA; ++k) f[(c * lanes + lane) * NA + k] = s[k];
+  }
 }
 
 // Backward 3. entering (from the right) states of every chunk: R_last = 0, R_{last-1} = f_last,
@@ -242,33 +306,45 @@ __global__ void __launch_bounds__(256) allpole_bwd_carry(const double* __restric
 
 // Backward 4. reverse apply: G_t, gw = G, and grad_a partials sum_u G_{u+1+k} y_u per chunk.
 template <int NA>
-__global__ void __launch_bounds__(256) allpole_bwd_apply(const float* __restrict__ a, const float* __restrict__ g,
-                                                         const float* __restrict__ y, const double* __restrict__ R,
-                                                         float* __restrict__ gw, double* __restrict__ ga_part,
-                                                         int64_t lanes, int64_t L, int64_t T_c, int64_t nchunk) {
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes, c = gid / lanes;
-  if (c >= nchunk) return;
+__global__ void __launch_bounds__(kTile) allpole_bwd_apply(const float* __restrict__ a, const float* __restrict__ g,
+                                                           const float* __restrict__ y, const double* __restrict__ R,
+                                                           float* __restrict__ gw, double* __restrict__ ga_part,
+                                                           int64_t lanes, int64_t L, int64_t T_c, int64_t nchunk) {
+  __shared__ float tg[kTile][kTileT + 1];
+  __shared__ float ty[kTile][kTileT + 1];
+  const int tid = threadIdx.x;
+  const int64_t l0 = (int64_t)blockIdx.x * kTile, c = blockIdx.y;
+  const int64_t lane = l0 + tid;
+  const bool act = lane < lanes;
   double av[NA], s[NA], ga[NA];
 #pragma unroll
   for (int k = 0; k < NA; ++k) {
-    av[k] = (double)a[lane * NA + k];
-    s[k] = R[(c * lanes + lane) * NA + k];
+    av[k] = act ? (double)a[lane * NA + k] : 0.0;
+    s[k] = act ? R[(c * lanes + lane) * NA + k] : 0.0;
     ga[k] = 0.0;
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
-  const float* gp = g + lane * L + t0;
-  const float* yp = y + lane * L + t0;
-  float* gwp = gw + lane * L + t0;
-  for (int64_t i = len - 1; i >= 0; --i) {
-    const double yu = yp[i];
+  const int64_t last = ((len - 1) / kTileT) * kTileT;
+  for (int64_t tt = last; tt >= 0; tt -= kTileT) {
+    const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
+    tile_load(tg, g, lanes, L, l0, t0 + tt, n);
+    tile_load(ty, y, lanes, L, l0, t0 + tt, n);
+    __syncthreads();
+    for (int k = n - 1; k >= 0; --k) {
+      const double yu = ty[tid][k];
 #pragma unroll
-    for (int k = 0; k < NA; ++k) ga[k] = fma(s[k], yu, ga[k]);  // s_k = G_{u+1+k} before the step
-    gwp[i] = (float)step<NA>(av, s, (double)gp[i]);
+      for (int q = 0; q < NA; ++q) ga[q] = fma(s[q], yu, ga[q]);  // s_q = G_{u+1+q} before the step
+      tg[tid][k] = (float)step<NA>(av, s, (double)tg[tid][k]);
+    }
+    __syncthreads();
+    tile_store(tg, gw, lanes, L, l0, t0 + tt, n);
+    __syncthreads();
   }
+  if (act) {
 #pragma unroll
-  for (int k = 0; k < NA; ++k) ga_part[(c * lanes + lane) * NA + k] = ga[k];
+    for (int k = 0; k < NA; ++k) ga_part[(c * lanes + lane) * NA + k] = ga[k];
+  }
 }
 
 // Backward 5. per lane: grad_a = -(sum of chunk partials + y0 head taps), grad_y0.
@@ -331,12 +407,13 @@ int fwd_impl(int64_t lanes, int64_t L, const float* a, const float* w, const flo
   double* e = reinterpret_cast<double*>(ws + p.off_e);
   double* S = reinterpret_cast<double*>(ws + p.off_S);
   hipLaunchKernelGGL((allpole_transfer<NA>), grid_for(lanes), dim3(256), 0, s, a, M, lanes, p.T_c);
+  const unsigned groups = (unsigned)((lanes + kTile - 1) / kTile);
   if (p.nchunk > 1)
-    hipLaunchKernelGGL((allpole_fwd_chunk_end<NA>), grid_for(lanes * (p.nchunk - 1)), dim3(256), 0, s, a, w, e, lanes,
-                       L, p.T_c, p.nchunk);
+    hipLaunchKernelGGL((allpole_fwd_chunk_end<NA>), dim3(groups, (unsigned)(p.nchunk - 1)), dim3(kTile), 0, s, a, w, e,
+                       lanes, L, p.T_c, p.nchunk);
   hipLaunchKernelGGL((allpole_fwd_carry<NA>), grid_for(lanes), dim3(256), 0, s, M, e, y0, S, lanes, p.nchunk);
-  hipLaunchKernelGGL((allpole_fwd_apply<NA>), grid_for(lanes * p.nchunk), dim3(256), 0, s, a, w, S, y, lanes, L,
-                     p.T_c, p.nchunk);
+  hipLaunchKernelGGL((allpole_fwd_apply<NA>), dim3(groups, (unsigned)p.nchunk), dim3(kTile), 0, s, a, w, S, y, lanes,
+                     L, p.T_c, p.nchunk);
   return tsf_launch_status();
 }
 
@@ -350,12 +427,13 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* a, const flo
   double* part = reinterpret_cast<double*>(ws + p.off_part);
   if (L > 0) {
     hipLaunchKernelGGL((allpole_transfer<NA>), grid_for(lanes), dim3(256), 0, s, a, M, lanes, p.T_c);
+    const unsigned groups = (unsigned)((lanes + kTile - 1) / kTile);
     if (p.nchunk > 1)
-      hipLaunchKernelGGL((allpole_bwd_chunk_start<NA>), grid_for(lanes * (p.nchunk - 1)), dim3(256), 0, s, a, g, f,
-                         lanes, L, p.T_c, p.nchunk);
+      hipLaunchKernelGGL((allpole_bwd_chunk_start<NA>), dim3(groups, (unsigned)(p.nchunk - 1)), dim3(kTile), 0, s, a,
+                         g, f, lanes, L, p.T_c, p.nchunk);
     hipLaunchKernelGGL((allpole_bwd_carry<NA>), grid_for(lanes), dim3(256), 0, s, M, f, R, lanes, p.nchunk);
-    hipLaunchKernelGGL((allpole_bwd_apply<NA>), grid_for(lanes * p.nchunk), dim3(256), 0, s, a, g, y, R, gw, part,
-                       lanes, L, p.T_c, p.nchunk);
+    hipLaunchKernelGGL((allpole_bwd_apply<NA>), dim3(groups, (unsigned)p.nchunk), dim3(kTile), 0, s, a, g, y, R, gw,
+                       part, lanes, L, p.T_c, p.nchunk);
   }
   hipLaunchKernelGGL((allpole_bwd_finish<NA>), grid_for(lanes), dim3(256), 0, s, a, gw, y0, part, ga, gy0, lanes, L,
                      p.nchunk);
