@@ -54,16 +54,25 @@ constexpr int kTileT = 32;  // time steps per tile (tile columns)
 
 // rows [l0, l0+64) x columns [c0, c0+ncol) of a [lanes, L] matrix <-> tile (zero outside).
 // Each access instruction moves two rows: lanes 0-31 one row, lanes 32-63 the next, 128-byte
-// contiguous segments.
-TSF_DEV void tile_load(float (*tile)[kTileT + 1], const float* __restrict__ src, int64_t lanes, int64_t L,
-                       int64_t l0, int64_t c0, int ncol) {
+// contiguous segments. Loads go to registers first (tile_fetch: all 32 issued back to back, so
+// a whole tile is in flight at once) and into LDS afterwards (tile_put), which lets the next
+// tile's loads overlap the current tile's recurrence.
+struct TileRegs {
+  float v[kTile / 2];
+};
+TSF_DEV void tile_fetch(TileRegs& rg, const float* __restrict__ src, int64_t lanes, int64_t L, int64_t l0, int64_t c0,
+                        int ncol) {
   const int col = threadIdx.x & (kTileT - 1), half = threadIdx.x >> 5;
-#pragma unroll 8
+#pragma unroll
   for (int r2 = 0; r2 < kTile / 2; ++r2) {
-    const int r = 2 * r2 + half;
-    const int64_t lane = l0 + r;
-    tile[r][col] = (lane < lanes && col < ncol) ? src[lane * L + c0 + col] : 0.0f;
+    const int64_t lane = l0 + 2 * r2 + half;
+    rg.v[r2] = (lane < lanes && col < ncol) ? src[lane * L + c0 + col] : 0.0f;
   }
+}
+TSF_DEV void tile_put(const TileRegs& rg, float (*tile)[kTileT + 1]) {
+  const int col = threadIdx.x & (kTileT - 1), half = threadIdx.x >> 5;
+#pragma unroll
+  for (int r2 = 0; r2 < kTile / 2; ++r2) tile[2 * r2 + half][col] = rg.v[r2];
 }
 TSF_DEV void tile_store(float (*tile)[kTileT + 1], float* __restrict__ dst, int64_t lanes, int64_t L, int64_t l0,
                         int64_t c0, int ncol) {
@@ -163,11 +172,20 @@ __global__ void __launch_bounds__(kTile) allpole_fwd_chunk_end(const float* __re
     s[k] = 0.0;
   }
   const int64_t t0 = c * T_c;
+  TileRegs rg;
+  tile_fetch(rg, w, lanes, L, l0, t0, (int)(T_c < kTileT ? T_c : kTileT));
   for (int64_t tt = 0; tt < T_c; tt += kTileT) {
     const int n = (int)((T_c - tt) < kTileT ? (T_c - tt) : kTileT);
-    tile_load(tile, w, lanes, L, l0, t0 + tt, n);
+    tile_put(rg, tile);
     __syncthreads();
-    for (int k = 0; k < n; ++k) step<NA>(av, s, (double)tile[tid][k]);
+    if (tt + kTileT < T_c)
+      tile_fetch(rg, w, lanes, L, l0, t0 + tt + kTileT, (int)((T_c - tt - kTileT) < kTileT ? (T_c - tt - kTileT) : kTileT));
+    if (n == kTileT) {
+#pragma unroll
+      for (int k = 0; k < kTileT; ++k) step<NA>(av, s, (double)tile[tid][k]);
+    } else {
+      for (int k = 0; k < n; ++k) step<NA>(av, s, (double)tile[tid][k]);
+    }
     __syncthreads();
   }
   if (act) {
@@ -225,11 +243,20 @@ __global__ void __launch_bounds__(kTile) allpole_fwd_apply(const float* __restri
   }
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
+  TileRegs rg;
+  tile_fetch(rg, w, lanes, L, l0, t0, (int)(len < kTileT ? len : kTileT));
   for (int64_t tt = 0; tt < len; tt += kTileT) {
     const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
-    tile_load(tile, w, lanes, L, l0, t0 + tt, n);
+    tile_put(rg, tile);
     __syncthreads();
-    for (int k = 0; k < n; ++k) tile[tid][k] = (float)step<NA>(av, s, (double)tile[tid][k]);
+    if (tt + kTileT < len)
+      tile_fetch(rg, w, lanes, L, l0, t0 + tt + kTileT, (int)((len - tt - kTileT) < kTileT ? (len - tt - kTileT) : kTileT));
+    if (n == kTileT) {
+#pragma unroll
+      for (int k = 0; k < kTileT; ++k) tile[tid][k] = (float)step<NA>(av, s, (double)tile[tid][k]);
+    } else {
+      for (int k = 0; k < n; ++k) tile[tid][k] = (float)step<NA>(av, s, (double)tile[tid][k]);
+    }
     __syncthreads();
     tile_store(tile, y, lanes, L, l0, t0 + tt, n);
     __syncthreads();
@@ -256,11 +283,19 @@ __global__ void __launch_bounds__(kTile) allpole_bwd_chunk_start(const float* __
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const int64_t last = ((len - 1) / kTileT) * kTileT;
+  TileRegs rg;
+  tile_fetch(rg, g, lanes, L, l0, t0 + last, (int)((len - last) < kTileT ? (len - last) : kTileT));
   for (int64_t tt = last; tt >= 0; tt -= kTileT) {
     const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
-    tile_load(tile, g, lanes, L, l0, t0 + tt, n);
+    tile_put(rg, tile);
     __syncthreads();
-    for (int k = n - 1; k >= 0; --k) step<NA>(av, s, (double)tile[tid][k]);
+    if (tt > 0) tile_fetch(rg, g, lanes, L, l0, t0 + tt - kTileT, kTileT);
+    if (n == kTileT) {
+#pragma unroll
+      for (int k = kTileT - 1; k >= 0; --k) step<NA>(av, s, (double)tile[tid][k]);
+    } else {
+      for (int k = n - 1; k >= 0; --k) step<NA>(av, s, (double)tile[tid][k]);
+    }
     __syncthreads();
   }
   if (act) {
@@ -326,16 +361,32 @@ __global__ void __launch_bounds__(kTile) allpole_bwd_apply(const float* __restri
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const int64_t last = ((len - 1) / kTileT) * kTileT;
+  TileRegs rgg, rgy;
+  {
+    const int n0 = (int)((len - last) < kTileT ? (len - last) : kTileT);
+    tile_fetch(rgg, g, lanes, L, l0, t0 + last, n0);
+    tile_fetch(rgy, y, lanes, L, l0, t0 + last, n0);
+  }
   for (int64_t tt = last; tt >= 0; tt -= kTileT) {
     const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
-    tile_load(tg, g, lanes, L, l0, t0 + tt, n);
-    tile_load(ty, y, lanes, L, l0, t0 + tt, n);
+    tile_put(rgg, tg);
+    tile_put(rgy, ty);
     __syncthreads();
-    for (int k = n - 1; k >= 0; --k) {
+    if (tt > 0) {
+      tile_fetch(rgg, g, lanes, L, l0, t0 + tt - kTileT, kTileT);
+      tile_fetch(rgy, y, lanes, L, l0, t0 + tt - kTileT, kTileT);
+    }
+    auto bstep = [&](int k) __attribute__((always_inline)) {
       const double yu = ty[tid][k];
 #pragma unroll
       for (int q = 0; q < NA; ++q) ga[q] = fma(s[q], yu, ga[q]);  // s_q = G_{u+1+q} before the step
       tg[tid][k] = (float)step<NA>(av, s, (double)tg[tid][k]);
+    };
+    if (n == kTileT) {
+#pragma unroll
+      for (int k = kTileT - 1; k >= 0; --k) bstep(k);
+    } else {
+      for (int k = n - 1; k >= 0; --k) bstep(k);
     }
     __syncthreads();
     tile_store(tg, gw, lanes, L, l0, t0 + tt, n);
