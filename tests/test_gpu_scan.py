@@ -29,6 +29,7 @@ _DIAG_SHAPES = [
     ((2, 300, 100), (100,)),
     ((32, 1000, 64), (32, 64)),  # config 1
     ((4, 4096, 256), (256,)),  # config 2, batch reduced
+    ((16, 2048, 256), (256,)),  # enough lanes for the 32-step real chunk tiles
 ]
 
 

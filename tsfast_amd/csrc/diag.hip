@@ -6,16 +6,13 @@
 // Reference semantics: tsfast/models/_core/scan.py:100-215 (ops), :52-80 (doubling scans),
 // scan_backends/diagonal_triton.py:82-228 and selective_triton.py:48-109 (kernels).
 //
-// Parallel structure (chunked two-pass scan, no inter-workgroup waiting):
-//   pass 1  one thread per (lane, time chunk) runs the chunk from a zero state and records the
-//           chunk's end state (and, for time-varying coefficients, the product of its
-//           coefficients) in a small carry buffer [nchunk, lanes].
-//   pass 2  one thread per (lane, time chunk) composes the carries of the chunks before it
-//           (Horner over at most nchunk small affine maps), then re-runs its chunk from the
-//           true start state and streams the result out.
-// Consecutive threads own consecutive lanes, so every per-step load/store is a coalesced row
-// segment along N. The chunk count is picked on the host so that lanes x chunks fills the
-// 256 CUs; the re-read of the input in pass 2 is the price of needing no global barrier.
+// Both are chunked two-pass scans with no inter-workgroup waiting: chunk summaries from a zero
+// state first, then a re-scan of every chunk from its true start state, the carries composed in
+// fp64 (complex128). Consecutive threads own consecutive lanes, so every per-step load/store is a
+// coalesced row segment along N; the re-read of the input in pass 2 is the price of needing no
+// global barrier. The constant-coefficient kernels keep a chunk in registers and combine chunk
+// summaries inside a workgroup through LDS (tiling described at those kernels); the time-varying
+// kernels run one thread per (lane, time chunk).
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -24,136 +21,342 @@ using namespace tsf;
 namespace {
 
 // All kernels load fp32 (or complex64) and carry the recurrence in fp64 (complex128): W below.
-// ---------------------------------------------------------------- constant coefficient, forward
-template <typename T>
-__global__ void __launch_bounds__(256) diag_fwd_chunk_end(const T* __restrict__ lam, const T* __restrict__ v,
-                                                          typename Wide<T>::type* __restrict__ carry, int64_t M,
-                                                          int64_t L, int64_t N, int64_t T_c, int64_t nchunk) {
-  using W = typename Wide<T>::type;
-  const int64_t lanes = M * N;
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes;
-  const int64_t c = gid / lanes;  // chunks 0 .. nchunk-2 (the last chunk's end is never needed)
-  if (c >= nchunk - 1) return;
-  const int64_t m = lane / N, n = lane % N;
-  const W a = Wide<T>::up(lam[lane]);
-  const T* vp = v + (m * L + c * T_c) * N + n;
-  W x = Num<W>::zero();
-#pragma unroll 8
-  for (int64_t i = 0; i < T_c; ++i) x = Num<W>::fma(a, x, Wide<T>::up(vp[i * N]));
-  carry[c * lanes + lane] = x;
-}
 
-template <typename T>
-__global__ void __launch_bounds__(256) diag_fwd_apply(const T* __restrict__ lam, const T* __restrict__ v,
-                                                      const T* __restrict__ x0,
-                                                      const typename Wide<T>::type* __restrict__ carry,
-                                                      T* __restrict__ out, int64_t M, int64_t L, int64_t N,
-                                                      int64_t T_c, int64_t nchunk) {
+// ---------------------------------------------------------------- constant coefficient
+// Tiling. A workgroup of K waves (K <= 16) owns 64 consecutive lanes (thread lid of every wave
+// owns lane group * 64 + lid) and one super-chunk of K * TC consecutive steps; wave k owns the
+// k-th chunk of TC steps. A thread keeps its chunk's TC inputs in registers, scans them from a
+// zero state, the K chunk summaries meet in LDS, and the thread re-runs its chunk from its true
+// start state. Super-chunk summaries (one per lane and super-chunk) go through HBM:
+//   summary  end state of every super-chunk but the last from a zero start, E [nsuper, lanes]
+//   carry    (long sequences only) in-place scan of E into true super-chunk start states
+//   apply    fold of E before the super-chunk (or the carried start), then the chunk scan.
+// The backward mirrors this from the right end with conj(lam), and reduces the glam partials of
+// the K chunks in LDS and of the super-chunks in a fixed-order sum (deterministic).
+constexpr int kMaxWaves = 16;
+
+template <typename T, int TC>
+__global__ void __launch_bounds__(1024) diag_fwd_summary(const T* __restrict__ lam, const T* __restrict__ v,
+                                                         typename Wide<T>::type* __restrict__ E, int64_t lanes,
+                                                         int64_t L, int64_t N, int64_t groups, int K) {
   using W = typename Wide<T>::type;
-  const int64_t lanes = M * N;
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes;
-  const int64_t c = gid / lanes;
-  if (c >= nchunk) return;
-  const int64_t m = lane / N, n = lane % N;
-  const W a = Wide<T>::up(lam[lane]);
-  // state entering chunk c: x0 carried through the full-length chunks before it
-  W x = x0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
-  if (c > 0) {
-    const W P = ipow(a, T_c);
-    for (int64_t j = 0; j < c; ++j) x = Num<W>::fma(P, x, carry[j * lanes + lane]);
+  __shared__ W s_e[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t g = blockIdx.x % groups, sc = blockIdx.x / groups;  // super-chunks 0 .. nsuper-2
+  const int64_t lane = g * 64 + lid;
+  const bool live = lane < lanes;
+  W a = Num<W>::zero(), e = Num<W>::zero();
+  if (live) {
+    a = Wide<T>::up(lam[lane]);
+    const int64_t m = lane / N, n = lane - m * N;
+    // every chunk of a super-chunk before the last is full
+    const T* vp = v + (m * L + sc * K * TC + (int64_t)k * TC) * N + n;
+    T vb[TC];
+#pragma unroll
+    for (int i = 0; i < TC; ++i) vb[i] = vp[i * N];
+#pragma unroll
+    for (int i = 0; i < TC; ++i) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
   }
-  const int64_t t0 = c * T_c;
-  const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
-  const T* vp = v + (m * L + t0) * N + n;
-  T* op = out + (m * L + t0) * N + n;
-#pragma unroll 8
-  for (int64_t i = 0; i < len; ++i) {
-    x = Num<W>::fma(a, x, Wide<T>::up(vp[i * N]));
-    op[i * N] = Wide<T>::down(x);
+  s_e[k][lid] = e;
+  __syncthreads();
+  if (k == 0 && live) {
+    const W P = ipow(a, TC);
+    W s = s_e[0][lid];
+    for (int j = 1; j < K; ++j) s = Num<W>::fma(P, s, s_e[j][lid]);
+    E[sc * lanes + lane] = s;
   }
 }
 
-// ---------------------------------------------------------------- constant coefficient, backward
-// Reverse chunk summaries: G at the chunk's first step with no gradient entering from the right.
+// In-place inclusive scan s_r = c * s_{r-1} + S[r] over n summaries per lane, with s_{-1} = init
+// (NULL: zero). Summary r of lane `lane` sits at S[(first + dir * r) * lanes + lane]; c is the
+// per-super-chunk multiplier lam^SL (conj(lam)^SL when `conjugate`). One workgroup per 64-lane
+// group; wave k scans the k-th of 16 contiguous segments, and the segment results meet in LDS.
 template <typename T>
-__global__ void __launch_bounds__(256) diag_bwd_chunk_start(const T* __restrict__ lam, const T* __restrict__ g,
-                                                            typename Wide<T>::type* __restrict__ carry, int64_t M,
-                                                            int64_t L, int64_t N, int64_t T_c, int64_t nchunk) {
+__global__ void __launch_bounds__(1024) diag_carry(const T* __restrict__ lam, const T* __restrict__ init,
+                                                   typename Wide<T>::type* __restrict__ S, int64_t lanes, int64_t n,
+                                                   int64_t first, int64_t dir, int64_t SL, int conjugate) {
   using W = typename Wide<T>::type;
-  const int64_t lanes = M * N;
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes;
-  const int64_t c = gid / lanes + 1;  // chunks 1 .. nchunk-1 (chunk 0's start feeds nobody)
-  if (c >= nchunk) return;
-  const int64_t m = lane / N, n = lane % N;
-  const W ac = Num<W>::conj(Wide<T>::up(lam[lane]));
-  const int64_t t0 = c * T_c;
-  const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
-  const T* gp = g + (m * L + t0) * N + n;
-  W G = Num<W>::zero();
+  __shared__ W s_p[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t lane = blockIdx.x * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t seg = (n + kMaxWaves - 1) / kMaxWaves;
+  const int64_t r0 = k * seg, r1 = (r0 + seg < n) ? r0 + seg : n;
+  W c = Num<W>::zero(), p = Num<W>::zero();
+  if (live) {
+    W a = Wide<T>::up(lam[lane]);
+    if (conjugate) a = Num<W>::conj(a);
+    c = ipow(a, SL);
 #pragma unroll 8
-  for (int64_t i = len - 1; i >= 0; --i) G = Num<W>::fma(ac, G, Wide<T>::up(gp[i * N]));
-  carry[c * lanes + lane] = G;
+    for (int64_t r = r0; r < r1; ++r) p = Num<W>::fma(c, p, S[(first + dir * r) * lanes + lane]);
+  }
+  s_p[k][lid] = p;
+  __syncthreads();
+  if (live && r0 < r1) {
+    W s = init ? Wide<T>::up(init[lane]) : Num<W>::zero();
+    const W cs = ipow(c, seg);  // every segment before a non-empty one is full
+    for (int j = 0; j < k; ++j) s = Num<W>::fma(cs, s, s_p[j][lid]);
+#pragma unroll 8
+    for (int64_t r = r0; r < r1; ++r) {
+      W* q = S + (first + dir * r) * lanes + lane;
+      s = Num<W>::fma(c, s, *q);
+      *q = s;
+    }
+  }
 }
 
-template <typename T>
-__global__ void __launch_bounds__(256) diag_bwd_apply(const T* __restrict__ lam, const T* __restrict__ g,
-                                                      const T* __restrict__ out, const T* __restrict__ x0,
-                                                      const typename Wide<T>::type* __restrict__ carry,
-                                                      T* __restrict__ gv, typename Wide<T>::type* __restrict__ glam_part,
-                                                      T* __restrict__ gx0, int64_t M, int64_t L, int64_t N,
-                                                      int64_t T_c, int64_t nchunk) {
+template <typename T, int TC>
+__global__ void __launch_bounds__(1024) diag_fwd_apply(const T* __restrict__ lam, const T* __restrict__ v,
+                                                       const T* __restrict__ x0,
+                                                       const typename Wide<T>::type* __restrict__ E,
+                                                       T* __restrict__ out, int64_t lanes, int64_t L, int64_t N,
+                                                       int64_t groups, int K, int starts_ready) {
   using W = typename Wide<T>::type;
-  const int64_t lanes = M * N;
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes;
-  const int64_t c = gid / lanes;
-  if (c >= nchunk) return;
-  const int64_t m = lane / N, n = lane % N;
-  const W ac = Num<W>::conj(Wide<T>::up(lam[lane]));
-  // G at the first step of chunk c+1: fold the chunk summaries from the right end inwards.
-  // Every chunk but the last has full length, and the last one receives no gradient.
-  W R = Num<W>::zero();
-  if (c + 1 < nchunk) {
-    const W P = ipow(ac, T_c);
-    R = carry[(nchunk - 1) * lanes + lane];
-    for (int64_t j = nchunk - 2; j > c; --j) R = Num<W>::fma(P, R, carry[j * lanes + lane]);
+  __shared__ W s_e[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t g = blockIdx.x % groups, sc = blockIdx.x / groups;
+  const int64_t lane = g * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t SL = (int64_t)K * TC;
+  const int64_t t0 = sc * SL + (int64_t)k * TC;
+  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+  W a = Num<W>::zero(), e = Num<W>::zero();
+  T vb[TC];
+  int64_t base = 0;
+  if (live) {
+    a = Wide<T>::up(lam[lane]);
+    const int64_t m = lane / N, n = lane - m * N;
+    base = (m * L + t0) * N + n;
+    const T* vp = v + base;
+    if (len == TC) {
+#pragma unroll
+      for (int i = 0; i < TC; ++i) vb[i] = vp[i * N];
+#pragma unroll
+      for (int i = 0; i < TC; ++i) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < TC; ++i)
+        if (i < len) vb[i] = vp[i * N];
+#pragma unroll
+      for (int i = 0; i < TC; ++i)
+        if (i < len) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
+    }
   }
-  const int64_t t0 = c * T_c;
-  const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
-  const T* gp = g + (m * L + t0) * N + n;
-  const T* xp = out + (m * L + t0) * N + n;
-  T* gvp = gv + (m * L + t0) * N + n;
-  W G = R;
+  s_e[k][lid] = e;
+  __syncthreads();
+  if (!live || len == 0) return;  // no barrier follows
+  // state entering the super-chunk
+  W s = x0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
+  if (sc > 0) {
+    if (starts_ready) {
+      s = E[(sc - 1) * lanes + lane];
+    } else {
+      const W Q = ipow(a, SL);
+#pragma unroll 8
+      for (int64_t j = 0; j < sc; ++j) s = Num<W>::fma(Q, s, E[j * lanes + lane]);
+    }
+  }
+  // state entering chunk k
+  if (k > 0) {
+    const W P = ipow(a, TC);
+    for (int j = 0; j < k; ++j) s = Num<W>::fma(P, s, s_e[j][lid]);
+  }
+  T* op = out + base;
+  if (len == TC) {
+#pragma unroll
+    for (int i = 0; i < TC; ++i) {
+      s = Num<W>::fma(a, s, Wide<T>::up(vb[i]));
+      op[i * N] = Wide<T>::down(s);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TC; ++i)
+      if (i < len) {
+        s = Num<W>::fma(a, s, Wide<T>::up(vb[i]));
+        op[i * N] = Wide<T>::down(s);
+      }
+  }
+}
+
+// Reverse summary of super-chunk sc >= 1: G at its first step with no gradient entering from the
+// right, F [nsuper, lanes] (slot 0 unused). Chunks past the end of the sequence are empty and
+// contribute zero, so the full-chunk multiplier conj(lam)^TC is right for every fold.
+template <typename T, int TC>
+__global__ void __launch_bounds__(1024) diag_bwd_summary(const T* __restrict__ lam, const T* __restrict__ g,
+                                                         typename Wide<T>::type* __restrict__ F, int64_t lanes,
+                                                         int64_t L, int64_t N, int64_t groups, int K) {
+  using W = typename Wide<T>::type;
+  __shared__ W s_f[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t gr = blockIdx.x % groups, sc = blockIdx.x / groups + 1;  // super-chunks 1 .. nsuper-1
+  const int64_t lane = gr * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t t0 = sc * K * TC + (int64_t)k * TC;
+  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+  W ac = Num<W>::zero(), f = Num<W>::zero();
+  if (live) {
+    ac = Num<W>::conj(Wide<T>::up(lam[lane]));
+    const int64_t m = lane / N, n = lane - m * N;
+    const T* gp = g + (m * L + t0) * N + n;
+    T gb[TC];
+    if (len == TC) {
+#pragma unroll
+      for (int i = 0; i < TC; ++i) gb[i] = gp[i * N];
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < TC; ++i)
+        if (i < len) gb[i] = gp[i * N];
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i)
+        if (i < len) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
+    }
+  }
+  s_f[k][lid] = f;
+  __syncthreads();
+  if (k == 0 && live) {
+    const W P = ipow(ac, TC);
+    W s = s_f[K - 1][lid];
+    for (int j = K - 2; j >= 0; --j) s = Num<W>::fma(P, s, s_f[j][lid]);
+    F[sc * lanes + lane] = s;
+  }
+}
+
+template <typename T, int TC>
+__global__ void __launch_bounds__(1024) diag_bwd_apply(const T* __restrict__ lam, const T* __restrict__ g,
+                                                       const T* __restrict__ out, const T* __restrict__ x0,
+                                                       const typename Wide<T>::type* __restrict__ F,
+                                                       T* __restrict__ gv, typename Wide<T>::type* __restrict__ part,
+                                                       T* __restrict__ glam, T* __restrict__ gx0, int64_t lanes,
+                                                       int64_t L, int64_t N, int64_t groups, int K, int64_t nsuper,
+                                                       int starts_ready) {
+  using W = typename Wide<T>::type;
+  __shared__ W s_f[kMaxWaves][64];
+  __shared__ W s_acc[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t gr = blockIdx.x % groups, sc = blockIdx.x / groups;
+  const int64_t lane = gr * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t SL = (int64_t)K * TC;
+  const int64_t t0 = sc * SL + (int64_t)k * TC;
+  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+  W ac = Num<W>::zero(), f = Num<W>::zero();
+  T gb[TC], xb[TC];  // g_t and x_{t-1} of the chunk's steps
+  int64_t base = 0;
+  if (live) {
+    ac = Num<W>::conj(Wide<T>::up(lam[lane]));
+    const int64_t m = lane / N, n = lane - m * N;
+    base = (m * L + t0) * N + n;
+    const T* gp = g + base;
+    const T* xp = out + base;
+    if (len == TC && t0 > 0) {
+#pragma unroll
+      for (int i = 0; i < TC; ++i) {
+        gb[i] = gp[i * N];
+        xb[i] = xp[(i - 1) * N];
+      }
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
+    } else if (len > 0) {
+      const T xinit = x0 ? x0[lane] : T{};  // x_{-1}: the initial state (zero without x0)
+#pragma unroll
+      for (int i = 0; i < TC; ++i)
+        if (i < len) {
+          gb[i] = gp[i * N];
+          xb[i] = (t0 + i > 0) ? xp[(i - 1) * N] : xinit;
+        }
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i)
+        if (i < len) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
+    }
+  }
+  s_f[k][lid] = f;
+  __syncthreads();
   W acc = Num<W>::zero();
+  if (live && len > 0) {
+    // G entering the super-chunk from the right: G at the first step of super-chunk sc + 1
+    W R = Num<W>::zero();
+    if (sc + 1 < nsuper) {
+      if (starts_ready) {
+        R = F[(sc + 1) * lanes + lane];
+      } else {
+        const W Q = ipow(ac, SL);
+        R = F[(nsuper - 1) * lanes + lane];
 #pragma unroll 8
-  for (int64_t i = len - 1; i >= 0; --i) {
-    G = Num<W>::fma(ac, G, Wide<T>::up(gp[i * N]));
-    gvp[i * N] = Wide<T>::down(G);
-    W xprev;
-    if (t0 + i > 0)
-      xprev = Wide<T>::up(xp[(i - 1) * N]);
-    else
-      xprev = x0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
-    acc = Num<W>::add(acc, Num<W>::mul_conj(G, xprev));
+        for (int64_t j = nsuper - 2; j > sc; --j) R = Num<W>::fma(Q, R, F[j * lanes + lane]);
+      }
+    }
+    // G entering chunk k from the right
+    if (k + 1 < K) {
+      const W P = ipow(ac, TC);
+      for (int j = K - 1; j > k; --j) R = Num<W>::fma(P, R, s_f[j][lid]);
+    }
+    W G = R;
+    T* gvp = gv + base;
+    if (len == TC) {
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i) {
+        G = Num<W>::fma(ac, G, Wide<T>::up(gb[i]));
+        gvp[i * N] = Wide<T>::down(G);
+        acc = Num<W>::add(acc, Num<W>::mul_conj(G, Wide<T>::up(xb[i])));
+      }
+    } else {
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i)
+        if (i < len) {
+          G = Num<W>::fma(ac, G, Wide<T>::up(gb[i]));
+          gvp[i * N] = Wide<T>::down(G);
+          acc = Num<W>::add(acc, Num<W>::mul_conj(G, Wide<T>::up(xb[i])));
+        }
+    }
+    if (t0 == 0 && gx0) gx0[lane] = Wide<T>::down(Num<W>::mul(ac, G));
   }
-  glam_part[c * lanes + lane] = acc;
-  if (c == 0 && gx0) gx0[lane] = Wide<T>::down(Num<W>::mul(ac, G));
+  s_acc[k][lid] = acc;
+  __syncthreads();
+  if (k == 0 && live) {
+    W s = s_acc[0][lid];
+    for (int j = 1; j < K; ++j) s = Num<W>::add(s, s_acc[j][lid]);
+    if (nsuper == 1)
+      glam[lane] = Wide<T>::down(s);
+    else
+      part[sc * lanes + lane] = s;
+  }
 }
 
-// Sum of per-chunk partials in a fixed order (deterministic run to run).
+// glam = sum over super-chunks of the partials, in a fixed order (deterministic run to run):
+// wave k adds the k-th of 16 contiguous segments, wave 0 adds the 16 segment sums in order.
 template <typename T>
-__global__ void __launch_bounds__(256) sum_chunks(const typename Wide<T>::type* __restrict__ part,
-                                                  T* __restrict__ dst, int64_t lanes, int64_t nchunk) {
+__global__ void __launch_bounds__(1024) diag_sum_parts(const typename Wide<T>::type* __restrict__ part,
+                                                       T* __restrict__ dst, int64_t lanes, int64_t n) {
   using W = typename Wide<T>::type;
-  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (lane >= lanes) return;
+  __shared__ W s_p[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t lane = blockIdx.x * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t seg = (n + kMaxWaves - 1) / kMaxWaves;
+  const int64_t r0 = k * seg, r1 = (r0 + seg < n) ? r0 + seg : n;
   W s = Num<W>::zero();
-  for (int64_t c = 0; c < nchunk; ++c) s = Num<W>::add(s, part[c * lanes + lane]);
-  dst[lane] = Wide<T>::down(s);
+  if (live) {
+#pragma unroll 8
+    for (int64_t r = r0; r < r1; ++r) s = Num<W>::add(s, part[r * lanes + lane]);
+  }
+  s_p[k][lid] = s;
+  __syncthreads();
+  if (k == 0 && live) {
+    W t = s_p[0][lid];
+    for (int j = 1; j < kMaxWaves; ++j) t = Num<W>::add(t, s_p[j][lid]);
+    dst[lane] = Wide<T>::down(t);
+  }
 }
+
+// Zero fill (gradients of an empty sequence); a kernel rather than a memset node, so that a
+// captured graph replays it reliably.
+__global__ void __launch_bounds__(256) zero_fill(float* __restrict__ p, int64_t n) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
 
 // ---------------------------------------------------------------- time-varying coefficient (real)
 // Pass-1 summary of a forward chunk: (product of its coefficients, end state from zero).
@@ -278,16 +481,96 @@ int64_t pick_chunk(int64_t lanes, int64_t L) {
 
 inline dim3 grid_for(int64_t threads) { return dim3((unsigned)((threads + 255) / 256)); }
 
+// Tile shape of the constant-coefficient kernels for one call. TC (steps per chunk) is a
+// template parameter: 16 or 32 for real lanes, 16 for complex ones (their backward keeps 2 x TC
+// complex values per thread in registers, within the 128 VGPRs a 1024-thread workgroup allows).
+// Every thread issues all TC loads of its chunk at once, so the bytes in flight do not depend on
+// TC; the wave count (lanes / 64 x L / TC) does, and real lanes drop to TC = 16 when 32 would
+// leave fewer than kDiagWaveTarget waves. K (chunks per workgroup) starts at 16, which keeps
+// the super-chunk count and the summary folds small, and halves down to 4 only while the grid
+// holds fewer than kDiagWgTarget workgroups. The carry kernel replaces the per-thread fold of
+// super-chunk summaries once there are more than kDiagFoldMax of them.
+#ifndef TSF_DIAG_WG_TARGET
+#define TSF_DIAG_WG_TARGET 256
+#endif
+#ifndef TSF_DIAG_WAVE_TARGET
+#define TSF_DIAG_WAVE_TARGET 4096
+#endif
+#ifndef TSF_DIAG_FOLD_MAX
+#define TSF_DIAG_FOLD_MAX 16
+#endif
+constexpr int64_t kDiagWgTarget = TSF_DIAG_WG_TARGET;
+constexpr int64_t kDiagWaveTarget = TSF_DIAG_WAVE_TARGET;
+constexpr int64_t kDiagFoldMax = TSF_DIAG_FOLD_MAX;
+
+struct DiagTile {
+  int64_t lanes = 0, groups = 0, nsuper = 0, SL = 0;
+  int TC = 0, K = 0;
+  bool carry_kernel = false;
+};
+
+DiagTile diag_tile(int64_t lanes, int64_t L, bool cplx) {
+  DiagTile t;
+  t.lanes = lanes;
+  if (lanes < 1 || L < 1) return t;
+  t.groups = (lanes + 63) / 64;
+  t.TC = (cplx || t.groups * ((L + 31) / 32) < kDiagWaveTarget) ? 16 : 32;
+  t.K = kMaxWaves;
+  auto wgs = [&](int K) { return t.groups * ((L + (int64_t)t.TC * K - 1) / ((int64_t)t.TC * K)); };
+  while (t.K > 4 && wgs(t.K) < kDiagWgTarget) t.K /= 2;
+  const int64_t chunks = (L + t.TC - 1) / t.TC;
+  if (t.K > chunks) t.K = (int)chunks;  // no waves past the end of a short sequence
+  t.SL = (int64_t)t.TC * t.K;
+  t.nsuper = (L + t.SL - 1) / t.SL;
+  t.carry_kernel = t.nsuper - 1 > kDiagFoldMax;
+  return t;
+}
+
+inline bool grid_fits(const DiagTile& t) { return t.groups * t.nsuper <= INT32_MAX; }
+
+template <typename T, int TC>
+void diag_fwd_launch(const DiagTile& t, const T* lam, const T* v, const T* x0, T* out, typename Wide<T>::type* E,
+                     int64_t L, int64_t N, hipStream_t s) {
+  const dim3 blk(64 * t.K);
+  if (t.nsuper > 1) {
+    hipLaunchKernelGGL((diag_fwd_summary<T, TC>), dim3((unsigned)(t.groups * (t.nsuper - 1))), blk, 0, s, lam, v, E,
+                       t.lanes, L, N, t.groups, t.K);
+    if (t.carry_kernel)
+      hipLaunchKernelGGL(diag_carry<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, lam, x0, E, t.lanes,
+                         t.nsuper - 1, (int64_t)0, (int64_t)1, t.SL, 0);
+  }
+  hipLaunchKernelGGL((diag_fwd_apply<T, TC>), dim3((unsigned)(t.groups * t.nsuper)), blk, 0, s, lam, v, x0,
+                     (const typename Wide<T>::type*)E, out, t.lanes, L, N, t.groups, t.K, (int)t.carry_kernel);
+}
+
+template <typename T, int TC>
+void diag_bwd_launch(const DiagTile& t, const T* g, const T* lam, const T* out, const T* x0, T* gv, T* glam, T* gx0,
+                     typename Wide<T>::type* F, typename Wide<T>::type* part, int64_t L, int64_t N, hipStream_t s) {
+  const dim3 blk(64 * t.K);
+  if (t.nsuper > 1) {
+    hipLaunchKernelGGL((diag_bwd_summary<T, TC>), dim3((unsigned)(t.groups * (t.nsuper - 1))), blk, 0, s, lam, g, F,
+                       t.lanes, L, N, t.groups, t.K);
+    if (t.carry_kernel)
+      hipLaunchKernelGGL(diag_carry<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, lam, (const T*)nullptr,
+                         F, t.lanes, t.nsuper - 1, t.nsuper - 1, (int64_t)-1, t.SL, 1);
+  }
+  hipLaunchKernelGGL((diag_bwd_apply<T, TC>), dim3((unsigned)(t.groups * t.nsuper)), blk, 0, s, lam, g, out, x0,
+                     (const typename Wide<T>::type*)F, gv, part, glam, gx0, t.lanes, L, N, t.groups, t.K, t.nsuper,
+                     (int)t.carry_kernel);
+  if (t.nsuper > 1)
+    hipLaunchKernelGGL(diag_sum_parts<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s,
+                       (const typename Wide<T>::type*)part, glam, t.lanes, t.nsuper);
+}
+
 }  // namespace
 
 extern "C" {
 
 int64_t tsfast_hip_diag_workspace_bytes(int64_t M, int64_t L, int64_t N, int is_complex) {
-  const int64_t lanes = M * N;
-  const int64_t T_c = pick_chunk(lanes, L);
-  const int64_t nchunk = (L + T_c - 1) / T_c;
-  // fp64 carries [nchunk, lanes] plus fp64 glam partials [nchunk, lanes] (complex128 when complex)
-  return 2 * nchunk * lanes * (is_complex ? 16 : 8);
+  const DiagTile t = diag_tile(M * N, L, is_complex != 0);
+  // fp64 super-chunk summaries [nsuper, lanes] plus fp64 glam partials [nsuper, lanes]
+  // (complex128 when complex)
+  return 2 * t.nsuper * t.lanes * (is_complex ? 16 : 8);
 }
 
 int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const void* lam, const void* v,
@@ -296,25 +579,18 @@ int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   if (M == 0 || L == 0 || N == 0) return TSF_OK;
   if (!lam || !v || !out) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
+  const DiagTile t = diag_tile(M * N, L, is_complex != 0);
+  if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t lanes = M * N;
-  const int64_t T_c = pick_chunk(lanes, L);
-  const int64_t nchunk = (L + T_c - 1) / T_c;
-  if (is_complex) {
-    auto* c = static_cast<double2*>(workspace);
-    if (nchunk > 1)
-      hipLaunchKernelGGL(diag_fwd_chunk_end<float2>, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s,
-                         (const float2*)lam, (const float2*)v, c, M, L, N, T_c, nchunk);
-    hipLaunchKernelGGL(diag_fwd_apply<float2>, grid_for(lanes * nchunk), dim3(256), 0, s, (const float2*)lam,
-                       (const float2*)v, (const float2*)x0, c, (float2*)out, M, L, N, T_c, nchunk);
-  } else {
-    auto* c = static_cast<double*>(workspace);
-    if (nchunk > 1)
-      hipLaunchKernelGGL(diag_fwd_chunk_end<float>, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s,
-                         (const float*)lam, (const float*)v, c, M, L, N, T_c, nchunk);
-    hipLaunchKernelGGL(diag_fwd_apply<float>, grid_for(lanes * nchunk), dim3(256), 0, s, (const float*)lam,
-                       (const float*)v, (const float*)x0, c, (float*)out, M, L, N, T_c, nchunk);
-  }
+  if (is_complex)
+    diag_fwd_launch<float2, 16>(t, (const float2*)lam, (const float2*)v, (const float2*)x0, (float2*)out,
+                                static_cast<double2*>(workspace), L, N, s);
+  else if (t.TC == 32)
+    diag_fwd_launch<float, 32>(t, (const float*)lam, (const float*)v, (const float*)x0, (float*)out,
+                               static_cast<double*>(workspace), L, N, s);
+  else
+    diag_fwd_launch<float, 16>(t, (const float*)lam, (const float*)v, (const float*)x0, (float*)out,
+                               static_cast<double*>(workspace), L, N, s);
   return tsf_launch_status();
 }
 
@@ -328,35 +604,27 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   if (!lam || !glam || (x0 && !gx0)) return TSF_ERR_ARG;
   if (L == 0) {
     // empty sequence: every gradient is zero
-    const size_t esz = is_complex ? 8 : 4;
-    if (hipMemsetAsync(glam, 0, lanes * esz, s) != hipSuccess) return TSF_ERR_HIP;
-    if (gx0 && hipMemsetAsync(gx0, 0, lanes * esz, s) != hipSuccess) return TSF_ERR_HIP;
-    return TSF_OK;
+    const int64_t nf = lanes * (is_complex ? 2 : 1);
+    hipLaunchKernelGGL(zero_fill, grid_for(nf), dim3(256), 0, s, (float*)glam, nf);
+    if (gx0) hipLaunchKernelGGL(zero_fill, grid_for(nf), dim3(256), 0, s, (float*)gx0, nf);
+    return tsf_launch_status();
   }
   if (!g || !out || !gv) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
-  const int64_t T_c = pick_chunk(lanes, L);
-  const int64_t nchunk = (L + T_c - 1) / T_c;
+  const DiagTile t = diag_tile(lanes, L, is_complex != 0);
+  if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
   if (is_complex) {
-    auto* c = static_cast<double2*>(workspace);
-    auto* part = c + nchunk * lanes;
-    if (nchunk > 1)
-      hipLaunchKernelGGL(diag_bwd_chunk_start<float2>, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s,
-                         (const float2*)lam, (const float2*)g, c, M, L, N, T_c, nchunk);
-    hipLaunchKernelGGL(diag_bwd_apply<float2>, grid_for(lanes * nchunk), dim3(256), 0, s, (const float2*)lam,
-                       (const float2*)g, (const float2*)out, (const float2*)x0, c, (float2*)gv, part, (float2*)gx0, M,
-                       L, N, T_c, nchunk);
-    hipLaunchKernelGGL(sum_chunks<float2>, grid_for(lanes), dim3(256), 0, s, part, (float2*)glam, lanes, nchunk);
+    auto* F = static_cast<double2*>(workspace);
+    diag_bwd_launch<float2, 16>(t, (const float2*)g, (const float2*)lam, (const float2*)out, (const float2*)x0,
+                                (float2*)gv, (float2*)glam, (float2*)gx0, F, F + t.nsuper * lanes, L, N, s);
   } else {
-    auto* c = static_cast<double*>(workspace);
-    auto* part = c + nchunk * lanes;
-    if (nchunk > 1)
-      hipLaunchKernelGGL(diag_bwd_chunk_start<float>, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s,
-                         (const float*)lam, (const float*)g, c, M, L, N, T_c, nchunk);
-    hipLaunchKernelGGL(diag_bwd_apply<float>, grid_for(lanes * nchunk), dim3(256), 0, s, (const float*)lam,
-                       (const float*)g, (const float*)out, (const float*)x0, c, (float*)gv, part, (float*)gx0, M, L,
-                       N, T_c, nchunk);
-    hipLaunchKernelGGL(sum_chunks<float>, grid_for(lanes), dim3(256), 0, s, part, (float*)glam, lanes, nchunk);
+    auto* F = static_cast<double*>(workspace);
+    if (t.TC == 32)
+      diag_bwd_launch<float, 32>(t, (const float*)g, (const float*)lam, (const float*)out, (const float*)x0,
+                                 (float*)gv, (float*)glam, (float*)gx0, F, F + t.nsuper * lanes, L, N, s);
+    else
+      diag_bwd_launch<float, 16>(t, (const float*)g, (const float*)lam, (const float*)out, (const float*)x0,
+                                 (float*)gv, (float*)glam, (float*)gx0, F, F + t.nsuper * lanes, L, N, s);
   }
   return tsf_launch_status();
 }
@@ -395,8 +663,8 @@ int tsfast_hip_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const fl
   if (lanes == 0) return TSF_OK;
   if (x0 && !gx0) return TSF_ERR_ARG;
   if (L == 0) {
-    if (gx0 && hipMemsetAsync(gx0, 0, lanes * 4, s) != hipSuccess) return TSF_ERR_HIP;
-    return TSF_OK;
+    if (gx0) hipLaunchKernelGGL(zero_fill, grid_for(lanes), dim3(256), 0, s, gx0, lanes);
+    return tsf_launch_status();
   }
   if (!g || !a || !out || !gv || !glam) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_sel_workspace_bytes(M, L, N) || !workspace) return TSF_ERR_WORKSPACE;
