@@ -81,8 +81,9 @@ int tsfast_hip_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const fl
  * chk [B, NC, N, D] float32 with NC = ceil(L / tsfast_hip_mamba_chk_interval(N)): slot k holds
  * the state after step (k + 1) * interval - 1 (channel-contiguous, so checkpoint traffic is
  * coalesced). chk == NULL selects the inference kernel, which writes no checkpoints.
- * One batch row must fit 32-bit element offsets: (L + 64) * D and (L + 64) * N below 2^31,
- * else TSF_ERR_UNSUPPORTED.
+ * The kernels address one batch row with 32-bit byte offsets: (L + 64) * D, (L + 64) * 2 * N'
+ * (N' = N rounded up to 4, 8, 16, 32 or 64) and NC * N * D must stay below 2^30, else
+ * TSF_ERR_UNSUPPORTED.
  */
 int64_t tsfast_hip_mamba_chk_interval(int64_t N);
 int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtype, const void* draw, const float* A,

@@ -28,17 +28,24 @@ template <typename T>
 TSF_DEV T from_f32(float x);
 template <>
 TSF_DEV float from_f32<float>(float x) { return x; }
+// Round to nearest even with NaN kept quiet: the fptrunc lowers to gfx950's v_cvt_pk_bf16_f32.
 template <>
 TSF_DEV bf16 from_f32<bf16>(float x) {
-  uint32_t u = __float_as_uint(x);
   bf16 r;
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
-    r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN, sign kept
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);
-    r.bits = static_cast<uint16_t>(u >> 16);
-  }
+  r.bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
   return r;
+}
+
+// Row access by a 32-bit element index: the byte offset is formed in 32 bits, so the access
+// is an SGPR base plus a VGPR byte offset (the global load/store "saddr" form) with no 64-bit
+// address arithmetic. The caller guarantees that idx * sizeof(T) fits in 32 bits.
+template <typename T>
+TSF_DEV T ld32(const T* __restrict__ base, uint32_t idx) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + idx * (uint32_t)sizeof(T));
+}
+template <typename T>
+TSF_DEV void st32(T* __restrict__ base, uint32_t idx, T v) {
+  *reinterpret_cast<T*>(reinterpret_cast<char*>(base) + idx * (uint32_t)sizeof(T)) = v;
 }
 
 // ------------------------------------------------------------------ complex (interleaved re/im)

@@ -132,6 +132,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   TIO* __restrict__ orw = out + rowD;
   const TIO* __restrict__ brw = Bt + rowN;
   const TIO* __restrict__ crw = Ct + rowN;
+  // checkpoints of this batch row and channel tile: [NC, N, D] from channel d0
+  float* __restrict__ chkb = chk ? chk + b * NC * N * D + d0 : nullptr;
 
   TIO r_dr[IT], r_u[IT], r_z[IT], r_b[BCI], r_c[BCI];
   auto load_chunk = [&](uint32_t t0, auto full) __attribute__((always_inline)) {
@@ -143,9 +145,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       bool v = idx < TF * DT && oact;
       if (!FULL) v = v && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Du + (uint32_t)od;
-      r_dr[k] = v ? drw[o] : io_zero<TIO>();
-      r_u[k] = v ? urw[o] : io_zero<TIO>();
-      r_z[k] = v ? zrw[o] : io_zero<TIO>();
+      r_dr[k] = v ? ld32(drw, o) : io_zero<TIO>();
+      r_u[k] = v ? ld32(urw, o) : io_zero<TIO>();
+      r_z[k] = v ? ld32(zrw, o) : io_zero<TIO>();
     }
 #pragma unroll
     for (int k = 0; k < BCI; ++k) {
@@ -154,8 +156,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       bool v = idx < TF * NS && (int)n < N;
       if (!FULL) v = v && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Nu + n;
-      r_b[k] = v ? brw[o] : io_zero<TIO>();
-      r_c[k] = v ? crw[o] : io_zero<TIO>();
+      r_b[k] = v ? ld32(brw, o) : io_zero<TIO>();
+      r_c[k] = v ? ld32(crw, o) : io_zero<TIO>();
     }
   };
   if (L > 0) {
@@ -195,27 +197,40 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         load_chunk(t1, Bool<false>());
     }
     __syncthreads();
-    // phase 2: the recurrence, NPT states per lane
+    // phase 2: the recurrence, NPT states per lane. LDS operands are read kRd steps ahead of
+    // their use, and the step body has no branch (both lanes of a pair store the same pair sum
+    // to the same slot), so the reads of later steps overlap the arithmetic of earlier ones.
+    constexpr int kRd = NPT <= 2 ? 4 : 2;
+    static_assert(TF % kRd == 0 && CHK % kRd == 0, "read batches must not straddle checkpoints");
 #pragma unroll
-    for (int i = 0; i < TF; ++i) {
-      const float2 s = s_sc[i][dl];
-      float y = 0.0f;
+    for (int i0 = 0; i0 < TF; i0 += kRd) {
+      float2 sv[kRd], bcv[kRd][NPT];
 #pragma unroll
-      for (int j = 0; j < NPT; ++j) {
-        const float2 bcv = s_bc[i][n0 + j];
-        const float lam = fast_exp2(s.x * A2[j]);
-        h[j] = fmaf(lam, h[j], s.y * bcv.x);
-        y = fmaf(h[j], bcv.y, y);
+      for (int r = 0; r < kRd; ++r) {
+        sv[r] = s_sc[i0 + r][dl];
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) bcv[r][j] = s_bc[i0 + r][n0 + j];
       }
-      y += swap_lane1(y);
-      if (pr == 0) s_y[i][ng >> 1][dl] = y;
+#pragma unroll
+      for (int r = 0; r < kRd; ++r) {
+        const int i = i0 + r;
+        float y = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NPT; ++j) {
+          const float lam = fast_exp2(sv[r].x * A2[j]);
+          h[j] = fmaf(lam, h[j], sv[r].y * bcv[r][j].x);
+          y = fmaf(h[j], bcv[r][j].y, y);
+        }
+        y += swap_lane1(y);
+        s_y[i][ng >> 1][dl] = y;
+      }
       // checkpoint slot k holds the state after step (k + 1) * CHK - 1 (layout [B, NC, N, D])
-      if ((i % CHK) == CHK - 1 && chk && act && i < len) {
-        const int64_t slot = ((int64_t)t0 + i) / CHK;
-        float* cp = chk + ((b * NC + slot) * N + n0) * D + d;
+      const int ie = i0 + kRd - 1;
+      if ((ie % CHK) == CHK - 1 && chk && act && ie < len) {
+        const uint32_t slot = (t0 + (uint32_t)ie) / CHK;
 #pragma unroll
         for (int j = 0; j < NPT; ++j)
-          if (n0 + j < N) cp[(int64_t)j * D] = h[j];
+          if (n0 + j < N) st32(chkb, (slot * Nu + (uint32_t)(n0 + j)) * Du + (uint32_t)dl, h[j]);
       }
     }
     __syncthreads();
@@ -230,7 +245,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         for (int p = 0; p < NPAIR; ++p) y += s_y[t][p][od];
         const float zz = o_z[k];
         const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
-        orw[o] = from_f32<TIO>(fmaf(dp_o, o_u[k], y) * zz * sigmoid_fast(zz));
+        st32(orw, o, from_f32<TIO>(fmaf(dp_o, o_u[k], y) * zz * sigmoid_fast(zz)));
       }
     }
   };
@@ -260,7 +275,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   __shared__ float s_dl[CHK][DT], s_du[CHK][DT], s_gy[CHK][DT];
   __shared__ float2 s_bc[CHK][NS];
   __shared__ float s_np[TB][3][NPAIR][DT];  // (sum A Q, sum G B, sum h C) per state pair
-  __shared__ float s_dp[TB][W2][DT];        // per (step, column): the 32 channels' (G du | gy h)
+  __shared__ __align__(16) float s_dp[TB][W2][DT];  // per (step, column): the 32 channels' (G du | gy h)
 
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.y;
@@ -300,6 +315,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   TIO* __restrict__ gzrw = gz + rowD;
   const TIO* __restrict__ brw = Bt + rowN;
   const TIO* __restrict__ crw = Ct + rowN;
+  const float* __restrict__ chkb = chk + b * NC * N * D + d0;  // [NC, N, D] from channel d0
+  float* __restrict__ gbcb = gBC_part + (tile * B + b) * L * (2 * NS);  // [L, 2*NS] partials
 
   TIO r_dr[IT], r_u[IT], r_z[IT], r_go[IT], r_b[BCI], r_c[BCI];
   float r_hs[NPT];
@@ -313,10 +330,10 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       bool v = idx < CHK * DT && oact;
       if (!FULL) v = v && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Du + (uint32_t)od;
-      r_dr[k] = v ? drw[o] : io_zero<TIO>();
-      r_u[k] = v ? urw[o] : io_zero<TIO>();
-      r_z[k] = v ? zrw[o] : io_zero<TIO>();
-      r_go[k] = v ? grw[o] : io_zero<TIO>();
+      r_dr[k] = v ? ld32(drw, o) : io_zero<TIO>();
+      r_u[k] = v ? ld32(urw, o) : io_zero<TIO>();
+      r_z[k] = v ? ld32(zrw, o) : io_zero<TIO>();
+      r_go[k] = v ? ld32(grw, o) : io_zero<TIO>();
     }
 #pragma unroll
     for (int k = 0; k < BCI; ++k) {
@@ -325,8 +342,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       bool v = idx < CHK * NS && (int)n < N;
       if (!FULL) v = v && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Nu + n;
-      r_b[k] = v ? brw[o] : io_zero<TIO>();
-      r_c[k] = v ? crw[o] : io_zero<TIO>();
+      r_b[k] = v ? ld32(brw, o) : io_zero<TIO>();
+      r_c[k] = v ? ld32(crw, o) : io_zero<TIO>();
     }
     // state entering the chunk: checkpoint slot c-1, or h0 for the first chunk
 #pragma unroll
@@ -335,7 +352,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       float v0 = 0.0f;
       if (act && n < N) {
         if (c > 0)
-          v0 = chk[((b * NC + c - 1) * N + n) * D + d];
+          v0 = ld32(chkb, ((uint32_t)(c - 1) * Nu + (uint32_t)n) * Du + (uint32_t)dl);
         else if (h0)
           v0 = h0[(b * D + d) * N + n];
       }
@@ -350,7 +367,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   };
   if (NC > 0) load_any(NC - 1);
 
-  float lamb[CHK][NPT], hb[CHK][NPT];
+  float lamb[CHK][NPT], lhb[CHK][NPT], hb[CHK][NPT];
   float o_u[IT], o_z[IT], o_sg[IT], o_go[IT], o_sd[IT];
   // Steps past the end of the sequence run as identity steps (delta = 0, gy = 0: lam = 1, no
   // input, no injected gradient), so the sweeps need no per-step guard; only stores check len.
@@ -386,7 +403,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     if (c > 0) load_chunk(c - 1, Bool<true>());  // every chunk before the last is full
     __syncthreads();
 
-    // recompute this chunk's states: lam_t and h_t into registers
+    // recompute this chunk's states into registers: lam_t, lam_t h_{t-1} and h_t
     {
       float hs[NPT];
 #pragma unroll
@@ -398,7 +415,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
         for (int j = 0; j < NPT; ++j) {
           const float lam = fast_exp2(dlt * A2[j]);
           lamb[i][j] = lam;
-          hs[j] = fmaf(lam, hs[j], du * s_bc[i][n0 + j].x);
+          lhb[i][j] = lam * hs[j];
+          hs[j] = fmaf(du, s_bc[i][n0 + j].x, lhb[i][j]);
           hb[i][j] = hs[j];
         }
       }
@@ -418,8 +436,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
             const float2 bcv = s_bc[i][n0 + j];
             const float an = (i + 1 < CHK) ? lamb[(i + 1) % CHK][j] : lam_next[j];
             G[j] = fmaf(an, G[j], gy * bcv.y);
-            const float hprev = (i > 0) ? hb[(i + CHK - 1) % CHK][j] : hst[j];
-            const float Q = G[j] * (lamb[i][j] * hprev);  // G_t * lam_t h_{t-1}
+            const float Q = G[j] * lhb[i][j];  // G_t * lam_t h_{t-1}
             gA[j] = fmaf(dlt, Q, gA[j]);
             aq = fmaf(Av[j], Q, aq);
             gb = fmaf(G[j], bcv.x, gb);
@@ -432,11 +449,11 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
           aq += swap_lane1(aq);
           gb += swap_lane1(gb);
           hc += swap_lane1(hc);
-          if (pr == 0) {
-            s_np[ii][0][ng >> 1][dl] = aq;
-            s_np[ii][1][ng >> 1][dl] = gb;
-            s_np[ii][2][ng >> 1][dl] = hc;
-          }
+          // both lanes of a pair hold the pair sums and store them to the same slot: a
+          // branch-free step body lets the compiler hoist later steps' LDS reads
+          s_np[ii][0][ng >> 1][dl] = aq;
+          s_np[ii][1][ng >> 1][dl] = gb;
+          s_np[ii][2][ng >> 1][dl] = hc;
         }
       }
       __syncthreads();
@@ -459,14 +476,15 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
           const float gzv = o_go[k] * y * sg * (1.0f + zz * (1.0f - sg));
           const float gdelta = fmaf(uu, gb, aq);
           const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
-          gdrw[o] = from_f32<TIO>(gdelta * o_sd[k]);
-          gurw[o] = from_f32<TIO>(fmaf(s_dl[t][od], gb, gy * dp_o));
-          gzrw[o] = from_f32<TIO>(gzv);
+          st32(gdrw, o, from_f32<TIO>(gdelta * o_sd[k]));
+          st32(gurw, o, from_f32<TIO>(fmaf(s_dl[t][od], gb, gy * dp_o)));
+          st32(gzrw, o, from_f32<TIO>(gzv));
           gdp = fmaf(gy, uu, gdp);
         }
       }
       // grad B_t / grad C_t: sum the tile's 32 channels for each (t, column); each thread
-      // reads its row as eight float4s, starting at a column-dependent quarter to spread banks
+      // reads its row as eight float4s, starting at a column-dependent eighth so that the 16
+      // lanes of one b128 pass (16 consecutive columns, rows 128 B apart) hit distinct banks
       for (int idx = tid; idx < TB * W2; idx += TH) {
         const int ii = idx / W2, col = idx % W2;
         const int t = sb * TB + ii;
@@ -475,10 +493,10 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
           float s = 0.0f;
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
-            const float4 v = row[(q + col) & 7];
+            const float4 v = row[(q + (col >> 1)) & 7];
             s += (v.x + v.y) + (v.z + v.w);
           }
-          gBC_part[((tile * B + b) * L + t0 + t) * W2 + col] = s;
+          st32(gbcb, (t0 + (uint32_t)t) * (uint32_t)W2 + (uint32_t)col, s);
         }
       }
       __syncthreads();
@@ -637,9 +655,13 @@ int bwd_bf16(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, const
 }
 
 // The kernels index one batch row with 32-bit element offsets (t * D + d, t * N + n).
-bool offsets_fit(int64_t L, int64_t D, int64_t N) {
-  const int64_t lim = (int64_t)1 << 31;
-  return (L + 64) * D < lim && (L + 64) * N < lim;
+// Per-row accesses use 32-bit byte offsets from a per-workgroup base: one batch row of every
+// [B, L, *] tensor (fp32 at most, the last chunk's identity steps included), one batch row of
+// the checkpoints [NC, N, D] and of the grad-B/C partials [L, 2*NS] must stay below 4 GiB.
+bool offsets_fit(int64_t L, int64_t D, int64_t N, int64_t chk_interval) {
+  const int64_t lim = ((int64_t)1 << 32) / 4;  // fp32 elements
+  const int64_t nc = (L + chk_interval - 1) / chk_interval;
+  return (L + 64) * D < lim && (L + 64) * 2 * ns_for(N) < lim && nc * N * D < lim;
 }
 
 int chk_interval_for(int ns) {
@@ -698,7 +720,7 @@ int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
   if (B == 0 || D == 0) return TSF_OK;
   if (!A || !Dp || !h_last) return TSF_ERR_ARG;
   if (L > 0 && (!draw || !Bt || !Ct || !u || !z || !out)) return TSF_ERR_ARG;
-  if (!offsets_fit(L, D, N)) return TSF_ERR_UNSUPPORTED;
+  if (!offsets_fit(L, D, N, chk_interval_for(ns))) return TSF_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (io_dtype == TSF_DTYPE_F32) {
     TSF_DISPATCH_NS(ns, fwd_f32, B, L, D, N, draw, A, Bt, Ct, u, z, Dp, h0, out, h_last, chk, s)
@@ -722,7 +744,7 @@ int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
   if (h0 && !gh0) return TSF_ERR_ARG;
   if (L > chk_interval_for(ns) && !chk) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_mamba_workspace_bytes(B, L, D, N) || !workspace) return TSF_ERR_WORKSPACE;
-  if (!offsets_fit(L, D, N)) return TSF_ERR_UNSUPPORTED;
+  if (!offsets_fit(L, D, N, chk_interval_for(ns))) return TSF_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (io_dtype == TSF_DTYPE_F32) {
     TSF_DISPATCH_NS(ns, bwd_f32, B, L, D, N, draw, A, Bt, Ct, u, z, Dp, h0, chk, gout, ghlast, gdraw, gA, gBt, gCt,
