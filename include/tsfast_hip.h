@@ -78,19 +78,25 @@ int tsfast_hip_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const fl
  * Layout: draw/u/z/out/gout/gdraw/gu/gz [B, L, D] and Bt/Ct/gBt/gCt [B, L, N] in io_dtype
  * (TSF_DTYPE_F32 or TSF_DTYPE_BF16); A/gA [D, N], Dp/gDp [D], h0/h_last/ghlast/gh0 [B, D, N]
  * always float32 (the state is float32 in both regimes). 1 <= N <= 64.
- * chk [B, NC, N, D] float32 with NC = ceil(L / tsfast_hip_mamba_chk_interval(N)): slot k holds
- * the state after step (k + 1) * interval - 1 (channel-contiguous, so checkpoint traffic is
- * coalesced). chk == NULL selects the inference kernel, which writes no checkpoints.
+ * chk is the training forward's saved state, [B, S] float32 words with
+ * S = tsfast_hip_mamba_saved_floats(L, D, N, io_dtype) per batch row: the float32 checkpoints
+ * [NC, N, D] with NC = ceil(L / tsfast_hip_mamba_chk_interval(N)) (slot k = the state after step
+ * (k + 1) * interval - 1, channel-contiguous so that checkpoint traffic is coalesced), then
+ * y [L, D] = sum_n h_t C_t + Dp u_t in io_dtype, the output before the gate (the backward's gate
+ * gradient reads it instead of recomputing sum_n h_t C_t). chk == NULL selects the inference
+ * kernel, which saves nothing.
  * The kernels address one batch row with 32-bit byte offsets: (L + 64) * D, (L + 64) * 2 * N'
- * (N' = N rounded up to 4, 8, 16, 32 or 64) and NC * N * D must stay below 2^30, else
+ * (N' = N rounded up to 4, 8, 16, 32 or 64) and NC * N * D + L * D must stay below 2^30, else
  * TSF_ERR_UNSUPPORTED.
  */
 int64_t tsfast_hip_mamba_chk_interval(int64_t N);
+int64_t tsfast_hip_mamba_saved_floats(int64_t L, int64_t D, int64_t N, int io_dtype);
 int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtype, const void* draw, const float* A,
                          const void* Bt, const void* Ct, const void* u, const void* z, const float* Dp,
                          const float* h0, void* out, float* h_last, float* chk, void* stream);
-/* Backward from the forward's checkpoints. ghlast may be NULL (zero upstream state gradient);
- * gh0 is written iff h0 is given. gA/gDp are the full parameter gradients (summed over the batch). */
+/* Backward from the forward's saved state chk (required when L > 0). ghlast may be NULL (zero
+ * upstream state gradient); gh0 is written iff h0 is given. gA/gDp are the full parameter
+ * gradients (summed over the batch). */
 int64_t tsfast_hip_mamba_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t N);
 int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtype, const void* draw, const float* A,
                          const void* Bt, const void* Ct, const void* u, const void* z, const float* Dp,

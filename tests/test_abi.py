@@ -45,6 +45,11 @@ def test_size_queries(lib):
     assert lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 0) > 0
     assert lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 1) == 2 * lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 0)
     assert lib.tsfast_hip_mamba_chk_interval(16) >= 1
+    k = lib.tsfast_hip_mamba_chk_interval(16)
+    # per batch row: fp32 checkpoints [ceil(L/k), N, D], then y [L, D] in the I/O type
+    assert lib.tsfast_hip_mamba_saved_floats(45, 40, 16, 0) == -(-45 // k) * 16 * 40 + 45 * 40
+    assert lib.tsfast_hip_mamba_saved_floats(45, 40, 16, 1) == -(-45 // k) * 16 * 40 + (45 * 40 * 2 + 3) // 4
+    assert lib.tsfast_hip_mamba_saved_floats(45, 40, 65, 0) == -1
     assert lib.tsfast_hip_mamba_workspace_bytes(16, 4096, 1536, 16) > 0
     assert lib.tsfast_hip_mamba_workspace_bytes(1, 1, 1, 65) == -1  # N above 64
     assert lib.tsfast_hip_allpole_workspace_bytes(4096, 16384, 3) > 0

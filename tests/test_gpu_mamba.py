@@ -111,7 +111,28 @@ def test_mamba_inference_equals_train_forward(gpu):
         a_out, a_h = mamba_hip.run(*args)
     b_out, b_h, chk = mamba_hip._scan_train_op(*args)
     assert torch.equal(a_out, b_out) and torch.equal(a_h, b_h)
-    assert chk.shape[1] == -(-45 // mamba_hip.chk_interval(16))
+    assert chk.shape == (2, mamba_hip.saved_floats(45, 40, 16, torch.float32))
+
+
+def test_mamba_saved_state_layout(gpu):
+    """The training forward's saved state, per batch row: checkpoint slot k = the state after
+    step (k + 1) * interval - 1 as [N, D], then y = sum_n h C + Dp u as [L, D] (fp64 oracle)."""
+    B, L, D, N = 2, 45, 40, 16
+    t, _, _ = _make(B, L, D, N, seed=13, io_dtype=torch.float32)
+    args = [t[k].to(gpu) if t[k] is not None else None for k in _NAMES]
+    _, _, saved = mamba_hip._scan_train_op(*args)
+    k = mamba_hip.chk_interval(N)
+    nc = -(-L // k)
+    saved = saved.cpu().numpy().astype(np.float64)
+    chk = saved[:, : nc * N * D].reshape(B, nc, N, D)
+    y = saved[:, nc * N * D :].reshape(B, L, D)
+    np_t = {n: _np64(v) for n, v in t.items()}
+    _, _, states = O.mamba_forward(*[np_t[n] for n in _NAMES], return_states=True)  # [B, L, D, N]
+    full = L // k  # slots whose step exists
+    want_chk = states[:, k - 1 :: k][:, :full].transpose(0, 1, 3, 2)  # [B, full, N, D]
+    assert O.rel_err(chk[:, :full], want_chk) < 1e-5
+    want_y = np.einsum("bldn,bln->bld", states, np_t["Ct"]) + np_t["Dp"] * np_t["u"]
+    assert O.rel_err(y, want_y) < 1e-5
 
 
 def test_mamba_chunked_state_equivalence(gpu):

@@ -35,6 +35,7 @@ _SIGNATURES: dict[str, tuple[list, object]] = {
     "tsfast_hip_sel_fwd": ([_i64, _i64, _i64] + [_ptr] * 5 + [_i64, _ptr], _int),
     "tsfast_hip_sel_bwd": ([_i64, _i64, _i64] + [_ptr] * 8 + [_i64, _ptr], _int),
     "tsfast_hip_mamba_chk_interval": ([_i64], _i64),
+    "tsfast_hip_mamba_saved_floats": ([_i64, _i64, _i64, _int], _i64),
     "tsfast_hip_mamba_workspace_bytes": ([_i64, _i64, _i64, _i64], _i64),
     "tsfast_hip_mamba_fwd": ([_i64, _i64, _i64, _i64, _int] + [_ptr] * 11 + [_ptr], _int),
     "tsfast_hip_mamba_bwd": ([_i64, _i64, _i64, _i64, _int] + [_ptr] * 20 + [_i64, _ptr], _int),

@@ -9,6 +9,7 @@
 #include <stdint.h>
 
 #define TSF_DEV __device__ __forceinline__
+#define TSF_HOST_DEV __host__ __device__ __forceinline__
 
 namespace tsf {
 

@@ -61,7 +61,6 @@ struct MCfg {
   static constexpr int IT_F = (TF * DT + TH - 1) / TH;   // owned (t, d) items per thread, forward
   static constexpr int IT_B = (CHK * DT + TH - 1) / TH;  // owned (t, d) items per thread, backward
   static constexpr int BC_F = (TF * NS + TH - 1) / TH;   // B/C tile elements per thread, forward
-  static constexpr int BC_B = (CHK * NS + TH - 1) / TH;  // B/C tile elements per thread, backward
 };
 
 // Swap with the neighbouring lane (lane ^ 1) through DPP: one VALU op, no LDS round trip.
@@ -84,6 +83,13 @@ TSF_DEV bf16 io_zero<bf16>() {
 
 template <bool V>
 using Bool = std::integral_constant<bool, V>;
+
+// Floats of training-forward saved state per batch row: fp32 checkpoints [NC, N, D], then the
+// pre-gate output y [L, D] in the I/O type (padded to whole floats).
+template <typename TIO>
+TSF_HOST_DEV int64_t saved_row_floats(int64_t L, int64_t D, int64_t N, int64_t NC) {
+  return NC * N * D + (L * D * (int64_t)sizeof(TIO) + 3) / 4;
+}
 
 // ------------------------------------------------------------------------------------ forward
 template <typename TIO, int NS>
@@ -132,8 +138,10 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   TIO* __restrict__ orw = out + rowD;
   const TIO* __restrict__ brw = Bt + rowN;
   const TIO* __restrict__ crw = Ct + rowN;
-  // checkpoints of this batch row and channel tile: [NC, N, D] from channel d0
-  float* __restrict__ chkb = chk ? chk + b * NC * N * D + d0 : nullptr;
+  // saved state of this batch row (training only): checkpoints [NC, N, D], then y [L, D]
+  float* __restrict__ svb = chk ? chk + b * saved_row_floats<TIO>(L, D, N, NC) : nullptr;
+  float* __restrict__ chkb = chk ? svb + d0 : nullptr;
+  TIO* __restrict__ yrw = chk ? reinterpret_cast<TIO*>(svb + NC * N * D) + d0 : nullptr;
 
   TIO r_dr[IT], r_u[IT], r_z[IT], r_b[BCI], r_c[BCI];
   auto load_chunk = [&](uint32_t t0, auto full) __attribute__((always_inline)) {
@@ -245,7 +253,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         for (int p = 0; p < NPAIR; ++p) y += s_y[t][p][od];
         const float zz = o_z[k];
         const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
-        st32(orw, o, from_f32<TIO>(fmaf(dp_o, o_u[k], y) * zz * sigmoid_fast(zz)));
+        const float yv = fmaf(dp_o, o_u[k], y);
+        st32(orw, o, from_f32<TIO>(yv * zz * sigmoid_fast(zz)));
+        if (yrw) st32(yrw, o, from_f32<TIO>(yv));  // the backward's gate gradient needs y before the gate
       }
     }
   };
@@ -259,32 +269,65 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
 }
 
 // ------------------------------------------------------------------------------------ backward
+// Lane layout: the workgroup's TH threads form 2*NG rows of 16 lanes (a DPP row). Row r holds
+// state group ng = r / 2 for channels dl = 16 * (r % 2) + (lane in row), and a lane's NPT states
+// are n = j * NG + ng. B_t and C_t of a row's states are the same for its 16 lanes, so each
+// chunk's B/C tile sits in VGPRs spread over the row (slot s = i * NPT + j in lane s % 16 of
+// register s / 16) and reaches every lane through a DPP row broadcast (row_newbcast) folded into
+// the consuming multiply; no LDS round trip. Consecutive state groups sit in adjacent rows of the
+// channel-sum scratch, so every per-step LDS store of a wave is 64 consecutive floats.
+template <int K>
+TSF_DEV float row_bcast_k(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + K, 0xF, 0xF, true));
+}
+// lane k (0..15) of this lane's DPP row; k must fold to a constant at compile time
+TSF_DEV float row_bcast(float x, int k) {
+  switch (k) {
+    case 0: return row_bcast_k<0>(x);
+    case 1: return row_bcast_k<1>(x);
+    case 2: return row_bcast_k<2>(x);
+    case 3: return row_bcast_k<3>(x);
+    case 4: return row_bcast_k<4>(x);
+    case 5: return row_bcast_k<5>(x);
+    case 6: return row_bcast_k<6>(x);
+    case 7: return row_bcast_k<7>(x);
+    case 8: return row_bcast_k<8>(x);
+    case 9: return row_bcast_k<9>(x);
+    case 10: return row_bcast_k<10>(x);
+    case 11: return row_bcast_k<11>(x);
+    case 12: return row_bcast_k<12>(x);
+    case 13: return row_bcast_k<13>(x);
+    case 14: return row_bcast_k<14>(x);
+    default: return row_bcast_k<15>(x);
+  }
+}
+
 template <typename TIO, int NS>
 __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     const TIO* __restrict__ draw, const float* __restrict__ A, const TIO* __restrict__ Bt,
     const TIO* __restrict__ Ct, const TIO* __restrict__ u, const TIO* __restrict__ z, const float* __restrict__ Dp,
-    const float* __restrict__ h0, const float* __restrict__ chk, const TIO* __restrict__ gout,
+    const float* __restrict__ h0, const float* __restrict__ saved, const TIO* __restrict__ gout,
     const float* __restrict__ ghlast, TIO* __restrict__ gdraw, TIO* __restrict__ gu, TIO* __restrict__ gz,
     float* __restrict__ gA_part, float* __restrict__ gDp_part, float* __restrict__ gBC_part, float* __restrict__ gh0,
     int64_t B, int64_t L, int64_t D, int N, int64_t NC) {
   using C = MCfg<NS>;
-  constexpr int NPT = C::NPT, DT = C::DT, TH = C::TH, CHK = C::CHK, TB = C::TB, IT = C::IT_B;
-  constexpr int BCI = C::BC_B, NPAIR = C::NPAIR, NSB = CHK / TB;
-  constexpr int W2 = 2 * NS;  // grad B / grad C columns
-  static_assert(DT == 32, "the channel-sum read pattern assumes 32 channels per row");
-  __shared__ float s_dl[CHK][DT], s_du[CHK][DT], s_gy[CHK][DT];
-  __shared__ float2 s_bc[CHK][NS];
-  __shared__ float s_np[TB][3][NPAIR][DT];  // (sum A Q, sum G B, sum h C) per state pair
+  constexpr int NPT = C::NPT, NG = C::NG, DT = C::DT, TH = C::TH, CHK = C::CHK, TB = C::TB, IT = C::IT_B;
+  constexpr int NSB = CHK / TB;
+  constexpr int W2 = 2 * NS;                   // grad B / grad C columns
+  constexpr int NSL = CHK * NPT;               // B/C broadcast slots per chunk and row
+  constexpr int NBV = (NSL + 15) / 16;         // VGPRs per B (and per C) tile
+  static_assert(DT == 32 && TH == 32 * NG, "two 16-lane rows per state group cover the 32 channels");
+  __shared__ float4 s_sc[CHK][DT];                  // (delta, delta * u, gy, -) per (t, d)
+  __shared__ float s_np[TB][2][NG][DT];             // (sum_n A Q, sum_n G B) per state group
   __shared__ __align__(16) float s_dp[TB][W2][DT];  // per (step, column): the 32 channels' (G du | gy h)
 
   const int tid = threadIdx.x;
   const int64_t b = blockIdx.y;
   const int64_t tile = blockIdx.x;
   const int64_t d0 = tile * DT;
-  const int pr = tid & 1;
-  const int dl = (tid >> 1) & (DT - 1);
-  const int ng = 2 * (tid / (2 * DT)) + pr;
-  const int n0 = ng * NPT;
+  const int rw = tid >> 4, lk = tid & 15;
+  const int ng = rw >> 1;
+  const int dl = lk | ((rw & 1) << 4);
   const int64_t d = d0 + dl;
   const bool act = d < D;
   const int od = tid % DT;
@@ -295,7 +338,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   float A2[NPT], Av[NPT], G[NPT], gA[NPT], lam_next[NPT];
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
-    const int n = n0 + j;
+    const int n = j * NG + ng;
     const bool v = act && n < N;
     Av[j] = v ? A[d * N + n] : 0.0f;
     A2[j] = Av[j] * kLog2e;
@@ -315,10 +358,13 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   TIO* __restrict__ gzrw = gz + rowD;
   const TIO* __restrict__ brw = Bt + rowN;
   const TIO* __restrict__ crw = Ct + rowN;
-  const float* __restrict__ chkb = chk + b * NC * N * D + d0;  // [NC, N, D] from channel d0
+  // saved state of this batch row: checkpoints [NC, N, D] then pre-gate outputs y [L, D]
+  const float* __restrict__ svb = saved + b * saved_row_floats<TIO>(L, D, N, NC);
+  const float* __restrict__ chkb = svb + d0;
+  const TIO* __restrict__ yrw = reinterpret_cast<const TIO*>(svb + NC * N * D) + d0;
   float* __restrict__ gbcb = gBC_part + (tile * B + b) * L * (2 * NS);  // [L, 2*NS] partials
 
-  TIO r_dr[IT], r_u[IT], r_z[IT], r_go[IT], r_b[BCI], r_c[BCI];
+  TIO r_dr[IT], r_u[IT], r_z[IT], r_go[IT], r_y[IT], r_bv[NBV], r_cv[NBV];
   float r_hs[NPT];
   auto load_chunk = [&](int64_t c, auto full) __attribute__((always_inline)) {
     constexpr bool FULL = decltype(full)::value;
@@ -334,21 +380,24 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       r_u[k] = v ? ld32(urw, o) : io_zero<TIO>();
       r_z[k] = v ? ld32(zrw, o) : io_zero<TIO>();
       r_go[k] = v ? ld32(grw, o) : io_zero<TIO>();
+      r_y[k] = v ? ld32(yrw, o) : io_zero<TIO>();
     }
+    // B/C broadcast slots of this lane: slot s = i * NPT + j -> (step t0 + i, state j * NG + ng)
 #pragma unroll
-    for (int k = 0; k < BCI; ++k) {
-      const int idx = tid + k * TH;
-      const uint32_t t = (uint32_t)(idx / NS), n = (uint32_t)(idx % NS);
-      bool v = idx < CHK * NS && (int)n < N;
-      if (!FULL) v = v && (int64_t)(t0 + t) < L;
-      const uint32_t o = (t0 + t) * Nu + n;
-      r_b[k] = v ? ld32(brw, o) : io_zero<TIO>();
-      r_c[k] = v ? ld32(crw, o) : io_zero<TIO>();
+    for (int v = 0; v < NBV; ++v) {
+      const int s = v * 16 + lk;
+      const uint32_t t = (uint32_t)(s / NPT);
+      const int n = (s % NPT) * NG + ng;
+      bool ok = s < NSL && n < N;
+      if (!FULL) ok = ok && (int64_t)(t0 + t) < L;
+      const uint32_t o = (t0 + t) * Nu + (uint32_t)n;
+      r_bv[v] = ok ? ld32(brw, o) : io_zero<TIO>();
+      r_cv[v] = ok ? ld32(crw, o) : io_zero<TIO>();
     }
     // state entering the chunk: checkpoint slot c-1, or h0 for the first chunk
 #pragma unroll
     for (int j = 0; j < NPT; ++j) {
-      const int n = n0 + j;
+      const int n = j * NG + ng;
       float v0 = 0.0f;
       if (act && n < N) {
         if (c > 0)
@@ -368,7 +417,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   if (NC > 0) load_any(NC - 1);
 
   float lamb[CHK][NPT], lhb[CHK][NPT], hb[CHK][NPT];
-  float o_u[IT], o_z[IT], o_sg[IT], o_go[IT], o_sd[IT];
+  float o_u[IT], o_z[IT], o_sg[IT], o_go[IT], o_sd[IT], o_y[IT];
   // Steps past the end of the sequence run as identity steps (delta = 0, gy = 0: lam = 1, no
   // input, no injected gradient), so the sweeps need no per-step guard; only stores check len.
   auto chunk = [&](int64_t c, int len) __attribute__((always_inline)) {
@@ -386,18 +435,17 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
         o_z[k] = zz;
         o_sg[k] = sg;
         o_go[k] = go;
+        o_y[k] = to_f32(r_y[k]);
         o_sd[k] = sp.e * __builtin_amdgcn_rcpf(sp.u);  // d softplus / d draw = sigmoid(draw)
-        s_dl[idx / DT][idx % DT] = delta;
-        s_du[idx / DT][idx % DT] = delta * uu;
-        s_gy[idx / DT][idx % DT] = go * zz * sg;
+        s_sc[idx / DT][idx % DT] = make_float4(delta, delta * uu, go * zz * sg, 0.0f);
       }
     }
+    float bv[NBV], cv[NBV], hst[NPT];
 #pragma unroll
-    for (int k = 0; k < BCI; ++k) {
-      const int idx = tid + k * TH;
-      if (idx < CHK * NS) s_bc[idx / NS][idx % NS] = make_float2(to_f32(r_b[k]), to_f32(r_c[k]));
+    for (int v = 0; v < NBV; ++v) {
+      bv[v] = to_f32(r_bv[v]);
+      cv[v] = to_f32(r_cv[v]);
     }
-    float hst[NPT];
 #pragma unroll
     for (int j = 0; j < NPT; ++j) hst[j] = r_hs[j];
     if (c > 0) load_chunk(c - 1, Bool<true>());  // every chunk before the last is full
@@ -410,13 +458,14 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       for (int j = 0; j < NPT; ++j) hs[j] = hst[j];
 #pragma unroll
       for (int i = 0; i < CHK; ++i) {
-        const float dlt = s_dl[i][dl], du = s_du[i][dl];
+        const float4 sc = s_sc[i][dl];
 #pragma unroll
         for (int j = 0; j < NPT; ++j) {
-          const float lam = fast_exp2(dlt * A2[j]);
+          const int s = i * NPT + j;
+          const float lam = fast_exp2(sc.x * A2[j]);
           lamb[i][j] = lam;
           lhb[i][j] = lam * hs[j];
-          hs[j] = fmaf(du, s_bc[i][n0 + j].x, lhb[i][j]);
+          hs[j] = lhb[i][j] + row_bcast(bv[s / 16], s % 16) * sc.y;
           hb[i][j] = hs[j];
         }
       }
@@ -428,33 +477,22 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
 #pragma unroll
       for (int ii = TB - 1; ii >= 0; --ii) {
         const int i = sb * TB + ii;
-        {
-          const float dlt = s_dl[i][dl], du = s_du[i][dl], gy = s_gy[i][dl];
-          float aq = 0.0f, gb = 0.0f, hc = 0.0f;
+        const float4 sc = s_sc[i][dl];  // (delta, delta * u, gy)
+        float aq = 0.0f, gb = 0.0f;
 #pragma unroll
-          for (int j = 0; j < NPT; ++j) {
-            const float2 bcv = s_bc[i][n0 + j];
-            const float an = (i + 1 < CHK) ? lamb[(i + 1) % CHK][j] : lam_next[j];
-            G[j] = fmaf(an, G[j], gy * bcv.y);
-            const float Q = G[j] * lhb[i][j];  // G_t * lam_t h_{t-1}
-            gA[j] = fmaf(dlt, Q, gA[j]);
-            aq = fmaf(Av[j], Q, aq);
-            gb = fmaf(G[j], bcv.x, gb);
-            hc = fmaf(hb[i][j], bcv.y, hc);
-            // the two lanes of a pair write rows two apart: flip bit 4 of the channel slot for
-            // odd pairs so they land in different banks (the channel order is summed over anyway)
-            s_dp[ii][n0 + j][dl ^ (pr << 4)] = G[j] * du;
-            s_dp[ii][NS + n0 + j][dl ^ (pr << 4)] = gy * hb[i][j];
-          }
-          aq += swap_lane1(aq);
-          gb += swap_lane1(gb);
-          hc += swap_lane1(hc);
-          // both lanes of a pair hold the pair sums and store them to the same slot: a
-          // branch-free step body lets the compiler hoist later steps' LDS reads
-          s_np[ii][0][ng >> 1][dl] = aq;
-          s_np[ii][1][ng >> 1][dl] = gb;
-          s_np[ii][2][ng >> 1][dl] = hc;
+        for (int j = 0; j < NPT; ++j) {
+          const int s = i * NPT + j;
+          const float an = (i + 1 < CHK) ? lamb[(i + 1) % CHK][j] : lam_next[j];
+          G[j] = fmaf(an, G[j], row_bcast(cv[s / 16], s % 16) * sc.z);
+          const float Q = G[j] * lhb[i][j];  // G_t * lam_t h_{t-1}
+          gA[j] = fmaf(sc.x, Q, gA[j]);
+          aq = fmaf(Av[j], Q, aq);
+          gb = fmaf(row_bcast(bv[s / 16], s % 16), G[j], gb);
+          s_dp[ii][j * NG + ng][dl] = G[j] * sc.y;
+          s_dp[ii][NS + j * NG + ng][dl] = sc.z * hb[i][j];
         }
+        s_np[ii][0][ng][dl] = aq;
+        s_np[ii][1][ng][dl] = gb;
       }
       __syncthreads();
       // owners: finish the per-(t, d) gradients of this sub-block
@@ -464,22 +502,21 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
         const int t = idx / DT;
         if (idx < CHK * DT && t >= sb * TB && t < sb * TB + TB && t < len && oact) {
           const int ii = t - sb * TB;
-          float aq = 0.0f, gb = 0.0f, hc = 0.0f;
+          float aq = 0.0f, gb = 0.0f;
 #pragma unroll
-          for (int p = 0; p < NPAIR; ++p) {
-            aq += s_np[ii][0][p][od];
-            gb += s_np[ii][1][p][od];
-            hc += s_np[ii][2][p][od];
+          for (int g = 0; g < NG; ++g) {
+            aq += s_np[ii][0][g][od];
+            gb += s_np[ii][1][g][od];
           }
-          const float uu = o_u[k], zz = o_z[k], sg = o_sg[k], gy = s_gy[t][od];
-          const float y = fmaf(dp_o, uu, hc);
-          const float gzv = o_go[k] * y * sg * (1.0f + zz * (1.0f - sg));
+          const float4 sc = s_sc[t][od];
+          const float uu = o_u[k], zz = o_z[k], sg = o_sg[k];
+          const float gzv = o_go[k] * o_y[k] * sg * (1.0f + zz * (1.0f - sg));
           const float gdelta = fmaf(uu, gb, aq);
           const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
           st32(gdrw, o, from_f32<TIO>(gdelta * o_sd[k]));
-          st32(gurw, o, from_f32<TIO>(fmaf(s_dl[t][od], gb, gy * dp_o)));
+          st32(gurw, o, from_f32<TIO>(fmaf(sc.x, gb, sc.z * dp_o)));
           st32(gzrw, o, from_f32<TIO>(gzv));
-          gdp = fmaf(gy, uu, gdp);
+          gdp = fmaf(sc.z, uu, gdp);
         }
       }
       // grad B_t / grad C_t: sum the tile's 32 channels for each (t, column); each thread
@@ -512,13 +549,13 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   if (act) {
 #pragma unroll
     for (int j = 0; j < NPT; ++j)
-      if (n0 + j < N) gA_part[(b * D + d) * N + n0 + j] = gA[j];
+      if (j * NG + ng < N) gA_part[(b * D + d) * N + j * NG + ng] = gA[j];
   }
   // gh0 = lam_0 G_0 (lam_next now holds lam_0; an empty sequence passes the state through)
   if (gh0 && act) {
 #pragma unroll
     for (int j = 0; j < NPT; ++j)
-      if (n0 + j < N) gh0[(b * D + d) * N + n0 + j] = lam_next[j] * G[j];
+      if (j * NG + ng < N) gh0[(b * D + d) * N + j * NG + ng] = lam_next[j] * G[j];
   }
   // gDp: every owner thread of channel od holds a partial; sum them through LDS
   __syncthreads();
@@ -657,11 +694,12 @@ int bwd_bf16(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, const
 // The kernels index one batch row with 32-bit element offsets (t * D + d, t * N + n).
 // Per-row accesses use 32-bit byte offsets from a per-workgroup base: one batch row of every
 // [B, L, *] tensor (fp32 at most, the last chunk's identity steps included), one batch row of
-// the checkpoints [NC, N, D] and of the grad-B/C partials [L, 2*NS] must stay below 4 GiB.
+// the saved state (checkpoints [NC, N, D] and y [L, D]) and of the grad-B/C partials [L, 2*NS]
+// must stay below 4 GiB.
 bool offsets_fit(int64_t L, int64_t D, int64_t N, int64_t chk_interval) {
   const int64_t lim = ((int64_t)1 << 32) / 4;  // fp32 elements
   const int64_t nc = (L + chk_interval - 1) / chk_interval;
-  return (L + 64) * D < lim && (L + 64) * 2 * ns_for(N) < lim && nc * N * D < lim;
+  return (L + 64) * D < lim && (L + 64) * 2 * ns_for(N) < lim && nc * N * D + L * D < lim;
 }
 
 int chk_interval_for(int ns) {
@@ -704,6 +742,15 @@ extern "C" {
 
 int64_t tsfast_hip_mamba_chk_interval(int64_t N) { return chk_interval_for(ns_for(N)); }
 
+int64_t tsfast_hip_mamba_saved_floats(int64_t L, int64_t D, int64_t N, int io_dtype) {
+  const int ns = ns_for(N);
+  if (ns == 0 || N < 1 || L < 0 || D < 0) return -1;
+  const int64_t nc = (L + chk_interval_for(ns) - 1) / chk_interval_for(ns);
+  if (io_dtype == TSF_DTYPE_F32) return saved_row_floats<float>(L, D, N, nc);
+  if (io_dtype == TSF_DTYPE_BF16) return saved_row_floats<bf16>(L, D, N, nc);
+  return -1;
+}
+
 int64_t tsfast_hip_mamba_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t N) {
   const int ns = ns_for(N);
   if (ns == 0 || N < 1) return -1;
@@ -742,7 +789,7 @@ int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
   if (!A || !Dp || !gA || !gDp) return TSF_ERR_ARG;
   if (L > 0 && (!draw || !Bt || !Ct || !u || !z || !gout || !gdraw || !gBt || !gCt || !gu || !gz)) return TSF_ERR_ARG;
   if (h0 && !gh0) return TSF_ERR_ARG;
-  if (L > chk_interval_for(ns) && !chk) return TSF_ERR_ARG;
+  if (L > 0 && !chk) return TSF_ERR_ARG;  // the saved state holds y as well as checkpoints
   if (workspace_bytes < tsfast_hip_mamba_workspace_bytes(B, L, D, N) || !workspace) return TSF_ERR_WORKSPACE;
   if (!offsets_fit(L, D, N, chk_interval_for(ns))) return TSF_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);

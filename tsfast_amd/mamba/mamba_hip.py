@@ -9,13 +9,16 @@ the ``tsfast_hip::mamba_scan`` / ``mamba_scan_train`` / ``mamba_scan_bwd`` custo
 Two I/O regimes: float32 everywhere (tsfast's regime), or bfloat16 sequence tensors
 (draw, u, z, Bt, Ct and their gradients) with float32 parameters (A, Dp) and float32 state
 (h0, h_last, the checkpoints). The state never leaves registers in fp32 arithmetic; only the
-training forward stores one fp32 checkpoint per channel every ``chk_interval(N)`` steps
-(``tsfast_hip_mamba_chk_interval``), from which the backward recomputes.
+training forward saves state for the backward: one fp32 checkpoint per channel every
+``chk_interval(N)`` steps (``tsfast_hip_mamba_chk_interval``), from which the backward
+recomputes, and the output before the gate (in the I/O dtype). The saved tensor is
+[B, saved_floats(L, D, N, dtype)] float32 words (per batch row: checkpoints [NC, N, D], then
+y [L, D]).
 """
 
 from __future__ import annotations
 
-__all__ = ["supports", "run", "chk_interval"]
+__all__ = ["supports", "run", "chk_interval", "saved_floats"]
 
 import torch
 
@@ -28,6 +31,12 @@ _MAX_N = 64
 def chk_interval(N: int) -> int:
     """Checkpoint interval (steps) the kernels use for state size N."""
     return int(_lib.load().tsfast_hip_mamba_chk_interval(N))
+
+
+def saved_floats(L: int, D: int, N: int, dtype: torch.dtype = torch.float32) -> int:
+    """float32 words of training-forward saved state per batch row for I/O dtype ``dtype``:
+    fp32 checkpoints [NC, N, D], then the pre-gate output y [L, D] in ``dtype``."""
+    return int(_lib.load().tsfast_hip_mamba_saved_floats(L, D, N, _IO_DTYPES[dtype]))
 
 
 def supports(draw, A, Bt, Ct, u, z, Dp, h0) -> str | None:
@@ -94,8 +103,7 @@ def _forward(draw, A, Bt, Ct, u, z, Dp, h0, store_chk: bool):
     h_last = torch.empty(B, D, N, device=draw.device, dtype=torch.float32)
     chk = None
     if store_chk:
-        nc = -(-L // chk_interval(N))
-        chk = torch.empty(B, nc, N, D, device=draw.device, dtype=torch.float32)
+        chk = torch.empty(B, saved_floats(L, D, N, draw.dtype), device=draw.device, dtype=torch.float32)
     _lib.check(
         lib.tsfast_hip_mamba_fwd(
             B, L, D, N, _IO_DTYPES[draw.dtype], *map(_lib.ptr, (draw, A, Bt, Ct, u, z, Dp, h0, out, h_last, chk)),
@@ -145,7 +153,7 @@ def _fake_outs(draw, A, with_chk: bool):
     h_last = draw.new_empty(B, D, N, dtype=torch.float32)
     if not with_chk:
         return out, h_last
-    return out, h_last, draw.new_empty(B, -(-L // chk_interval(N)), N, D, dtype=torch.float32)
+    return out, h_last, draw.new_empty(B, saved_floats(L, D, N, draw.dtype), dtype=torch.float32)
 
 
 @_scan_op.register_fake
