@@ -84,11 +84,29 @@ TSF_DEV bf16 io_zero<bf16>() {
 template <bool V>
 using Bool = std::integral_constant<bool, V>;
 
+// Streaming store for the training forward's saved state, which is read back only by the
+// backward (non-temporal: it is not kept in the caches on the way out).
+TSF_DEV void nt_store(float* p, float v) { __builtin_nontemporal_store(v, p); }
+TSF_DEV void nt_store(bf16* p, bf16 v) { __builtin_nontemporal_store(v.bits, &p->bits); }
+
 // Floats of training-forward saved state per batch row: fp32 checkpoints [NC, N, D], then the
 // pre-gate output y [L, D] in the I/O type (padded to whole floats).
 template <typename TIO>
 TSF_HOST_DEV int64_t saved_row_floats(int64_t L, int64_t D, int64_t N, int64_t NC) {
   return NC * N * D + (L * D * (int64_t)sizeof(TIO) + 3) / 4;
+}
+
+// Workgroups go to the 8 XCDs (each with its own L2) round-robin by linear id. Renumber them so
+// that every XCD receives a contiguous range of (channel tile, batch row) pairs: neighbouring
+// channel tiles share the 128-byte lines of each bf16 [B, L, D] row (one tile's row segment is
+// 64 bytes), and on one XCD the second read of a line hits that XCD's L2 instead of HBM.
+constexpr unsigned kXcds = 8;
+TSF_DEV void xcd_remap(int64_t& tile, int64_t& row) {
+  const unsigned gx = gridDim.x, total = gridDim.x * gridDim.y;
+  unsigned lin = blockIdx.x + blockIdx.y * gx;
+  if (total % kXcds == 0) lin = (lin % kXcds) * (total / kXcds) + lin / kXcds;
+  tile = lin % gx;
+  row = lin / gx;
 }
 
 // ------------------------------------------------------------------------------------ forward
@@ -106,8 +124,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   __shared__ float s_y[TF][NPAIR][DT];  // y partial per state pair
 
   const int tid = threadIdx.x;
-  const int64_t b = blockIdx.y;
-  const int64_t d0 = (int64_t)blockIdx.x * DT;
+  int64_t tile, b;
+  xcd_remap(tile, b);
+  const int64_t d0 = tile * DT;
   // recurrence mapping: adjacent lanes hold the two halves of a state pair
   const int pr = tid & 1;
   const int dl = (tid >> 1) & (DT - 1);
@@ -238,7 +257,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         const uint32_t slot = (t0 + (uint32_t)ie) / CHK;
 #pragma unroll
         for (int j = 0; j < NPT; ++j)
-          if (n0 + j < N) st32(chkb, (slot * Nu + (uint32_t)(n0 + j)) * Du + (uint32_t)dl, h[j]);
+          if (n0 + j < N) nt_store(chkb + ((slot * Nu + (uint32_t)(n0 + j)) * Du + (uint32_t)dl), h[j]);
       }
     }
     __syncthreads();
@@ -255,7 +274,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
         const float yv = fmaf(dp_o, o_u[k], y);
         st32(orw, o, from_f32<TIO>(yv * zz * sigmoid_fast(zz)));
-        if (yrw) st32(yrw, o, from_f32<TIO>(yv));  // the backward's gate gradient needs y before the gate
+        if (yrw) nt_store(yrw + o, from_f32<TIO>(yv));  // the backward's gate gradient needs y before the gate
       }
     }
   };
@@ -322,8 +341,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   __shared__ __align__(16) float s_dp[TB][W2][DT];  // per (step, column): the 32 channels' (G du | gy h)
 
   const int tid = threadIdx.x;
-  const int64_t b = blockIdx.y;
-  const int64_t tile = blockIdx.x;
+  int64_t tile, b;
+  xcd_remap(tile, b);
   const int64_t d0 = tile * DT;
   const int rw = tid >> 4, lk = tid & 15;
   const int ng = rw >> 1;
