@@ -43,6 +43,18 @@ METRIC = "fwd+bwd ms + achieved HBM GB/s (% peak), selective scan B16 L4096 D153
 HBM_PEAK_GBS = 8000.0
 CFG3 = dict(B=16, L=4096, D=1536, N=16)
 
+# HBM bytes per call measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on the default bench
+# workload, each scaled by the same counter on a 512 MiB elementwise copy (FETCH x 2.0, WRITE
+# x 1.0): (config, I/O dtype) -> {phase: (bytes, source)}. Counters cannot be read from inside
+# this process, so the figures come from the committed summary and must be re-measured when the
+# kernels change.
+MEASURED_TRAFFIC = {
+    (3, "bf16"): {
+        "fwd": (2_083_282_000, "profiles/mamba_scan_config3_traffic.md"),
+        "bwd": (3_736_450_000, "profiles/mamba_scan_config3_traffic.md"),
+    },
+}
+
 
 # --------------------------------------------------------------------------- algorithmic bytes
 def mamba_bytes(B, L, D, N, io_bytes):
@@ -413,8 +425,10 @@ def main():
     line["ms_per_step"] = round(ms, 4)
     line["pct_hbm_peak"] = round(100 * gbs / HBM_PEAK_GBS, 2)
     line["algorithmic_bytes"] = {k: v[2] for k, v in kernels.items()}
-    name, dom_ms, dom_b = max(kernels.values(), key=lambda k: k[1])
+    phase = max(kernels, key=lambda k: kernels[k][1])
+    name, dom_ms, dom_b = kernels[phase]
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
+    measured = MEASURED_TRAFFIC.get((args.config, args.io if args.config == 3 else "f32"), {}).get(phase)
     line["roofline"] = {
         "bound": "hbm",
         "kernel": name,
@@ -422,8 +436,12 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": measured[0] if measured else None,
     }
+    if measured:
+        line["roofline"]["traffic_unit"] = "bytes per call"
+        line["roofline"]["traffic_source"] = measured[1]
+        line["roofline"]["algorithmic_bytes"] = dom_b
     if cpu is not None:
         try:
             line["cpu_baseline"] = cpu()

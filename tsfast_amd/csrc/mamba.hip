@@ -7,24 +7,27 @@
 // Reference semantics: tsfast/models/architectures/mamba/mamba_triton.py:85-286 (kernels) and
 // :286-489 (ops), mamba/backend_c.py:105-245 (CPU kernels, same algebra).
 //
-// The scan is VALU-bound on gfx950 (one exp and ~5 (fwd) / ~15 (bwd) fp32 ops per state element
+// The scan is VALU-bound on gfx950 (one exp and ~4 (fwd) / ~13 (bwd) fp32 ops per state element
 // against 2-5 bytes of HBM traffic per element), so the layout minimises per-element VALU work
-// and keeps every SIMD busy:
+// and LDS traffic and keeps every SIMD busy:
 //
 //  * Workgroup = one batch row b x a tile of DT=32 channels, all N states, walking the whole
 //    sequence. NG lanes share a channel, each holding NPT = NS/NG states in VGPRs (NG = 8 for
 //    N >= 8), so the grid B * D/32 (768 workgroups of 4 waves at config 3) puts three
-//    workgroups on every CU with no tail.
-//  * Time advances in chunks of CHK steps. Per-(t, d) scalar work (softplus, sigmoid, gates,
-//    the D skip) is done once per (t, d) by an "owner" thread and staged through LDS, with
-//    coalesced 32-channel row loads/stores; each lane then runs only the per-state recurrence.
-//  * Sums over states (y = h.C in the forward; sum A Q, sum G B, sum h C in the backward) are
-//    pre-reduced between the two adjacent lanes of a state pair with one DPP swap and finished
-//    by the owner thread from LDS.
-//  * The backward recomputes each chunk's states from the forward's fp32 checkpoint into
-//    registers (lam_t and h_t for the chunk), then runs the adjoint
+//    workgroups on every CU with no tail; workgroups are renumbered so that each XCD works on a
+//    contiguous range of tiles (neighbouring tiles share L2 lines).
+//  * Time advances in chunks. Per-(t, d) scalar work (softplus, sigmoid, gates, the D skip) is
+//    done once per (t, d) by an "owner" thread and staged through LDS, with coalesced 32-channel
+//    row loads/stores; each lane then runs only the per-state recurrence.
+//  * Forward: sums over states (y = h.C) are pre-reduced between the two adjacent lanes of a
+//    state pair with one DPP swap and finished by the owner thread from LDS.
+//  * Backward: each 16-lane DPP row holds one state group; the chunk's B_t/C_t values live in
+//    VGPRs spread over the row and reach the lanes through DPP row broadcasts. It recomputes
+//    each chunk's states from the forward's fp32 checkpoint into registers (lam_t, lam_t h_{t-1}
+//    and h_t for the chunk), then runs the adjoint
 //        G_t = gy_t C_t + lam_{t+1} G_{t+1}
-//    backwards through the chunk, so exp is evaluated once per element per pass.
+//    backwards through the chunk, so exp is evaluated once per element per pass; the gate
+//    gradient reads the forward's saved pre-gate output y instead of recomputing sum_n h C.
 //  * grad B_t / grad C_t (sums over channels) are reduced over the 32 channels of the tile in
 //    LDS and written as fp32 partials [D/32, B, L, 2*NS]; a second kernel sums the partials in a
 //    fixed order (no atomics: deterministic run to run).
