@@ -314,6 +314,74 @@ def run_diag(args, line):
     return ms, fwd_b + bwd_b, kernels, cpu
 
 
+def run_conv(args, line):
+    """The fused Mamba causal depthwise conv + SiLU (the scope table's next row, not a BASELINE
+    config) at config 3's shape: x is the in_proj chunk view of a [B, L, 2D] tensor, K = 4."""
+    import torch
+
+    from tsfast_amd.mamba import conv_hip
+
+    io_dtype = torch.bfloat16 if args.io == "bf16" else torch.float32
+    esz = 2 if io_dtype == torch.bfloat16 else 4
+    B, L, D, K = CFG3["B"], CFG3["L"], CFG3["D"], 4
+    g = torch.Generator().manual_seed(5)
+    xz = torch.randn(B, L, 2 * D, generator=g).to("cuda", io_dtype)
+    x = xz[..., :D]
+    tail = torch.randn(B, D, K - 1, generator=g).to("cuda", io_dtype)
+    w = (torch.randn(D, K, generator=g) * 0.5).cuda()
+    b = torch.randn(D, generator=g).cuda()
+    gy = torch.randn(B, L, D, generator=g).to("cuda", io_dtype)
+
+    def step(ev):
+        mark(ev)
+        conv_hip._conv_silu_op(x, tail, w, b)
+        mark(ev)
+        conv_hip._conv_silu_bwd_op(gy, x, tail, w, b)
+        mark(ev)
+
+    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
+    bld = B * L * D
+    params = D * K * 4 + D * 4
+    fwd_b = 2 * bld * esz + B * D * (K - 1) * esz + params
+    bwd_b = 3 * bld * esz + 2 * B * D * (K - 1) * esz + 2 * params
+    line.update(
+        config={"workload": "fused Mamba causal depthwise conv + SiLU fwd+bwd at config 3's shape (next row)",
+                "B": B, "L": L, "D": D, "K": K, "io_dtype": args.io, "x": "strided in_proj chunk view"},
+        fwd_ms=round(fwd_ms, 4),
+        bwd_ms=round(bwd_ms, 4),
+    )
+    line["metric"] = "fwd+bwd ms + achieved HBM GB/s, fused Mamba conv+SiLU at B16 L4096 D1536 K4"
+    kernels = {"fwd": ("conv_silu_fwd_kernel", fwd_ms, fwd_b),
+               "bwd": ("conv_silu_bwd_kernel + conv_reduce_params (one ABI call)", bwd_ms, bwd_b)}
+    cpu = None
+    if not args.no_cpu:
+        def cpu_leg():
+            from tsfast_amd.mamba.core import _causal_depthwise_silu
+
+            threads = os.cpu_count() or 1
+            torch.set_num_threads(threads)
+            rows = 2
+            xc = xz[:rows].float().cpu()[..., :D].requires_grad_()
+            tc = tail[:rows].float().cpu().requires_grad_()
+            wc = w.cpu()[:, None, :].requires_grad_()
+            bc = b.cpu().requires_grad_()
+            gc = gy[:rows].float().cpu()
+
+            def fb():
+                _causal_depthwise_silu(xc, tc, wc, bc).backward(gc)
+
+            med, n = cpu_time(fb)
+            sf = 2 * rows * L * D * 4 + 3 * rows * L * D * 4
+            return {
+                "value": round(sf / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": (f"{rows} of {B} batch rows, fp32: the reference's eager CPU conv path "
+                           f"(shifted multiply-adds + SiLU, mamba/core.py:38-58) in torch with autograd, fwd+bwd "
+                           f"median of {n} runs = {med * 1e3:.2f} ms"),
+            }
+        cpu = cpu_leg
+    return ms, fwd_b + bwd_b, kernels, cpu
+
+
 def run_allpole(args, line):
     from tsfast_amd.dynonet import allpole_hip
 
@@ -372,7 +440,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5))
-    ap.add_argument("--io", choices=("bf16", "fp32"), default="bf16", help="config 3 I/O dtype")
+    ap.add_argument("--io", choices=("bf16", "fp32"), default="bf16", help="config 3 / --conv I/O dtype")
+    ap.add_argument("--conv", action="store_true",
+                    help="measure the fused Mamba conv+SiLU at config 3's shape instead of a BASELINE config")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument(
         "--copy-calibration",
@@ -418,7 +488,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
     }
-    runner = {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config]
+    runner = run_conv if args.conv else {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config]
     ms, total_bytes, kernels, cpu = runner(args, line)
     gbs = total_bytes / (ms * 1e-3) / 1e9
     line["value"] = round(gbs, 2)
@@ -428,7 +498,7 @@ def main():
     phase = max(kernels, key=lambda k: kernels[k][1])
     name, dom_ms, dom_b = kernels[phase]
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
-    measured = MEASURED_TRAFFIC.get((args.config, args.io if args.config == 3 else "f32"), {}).get(phase)
+    measured = None if args.conv else MEASURED_TRAFFIC.get((args.config, args.io if args.config == 3 else "f32"), {}).get(phase)
     line["roofline"] = {
         "bound": "hbm",
         "kernel": name,

@@ -119,6 +119,28 @@ int tsfast_hip_allpole_bwd(int64_t lanes, int64_t L, int64_t na, const float* g,
                            const float* y0, float* gw, float* ga, float* gy0, void* workspace,
                            int64_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Fused causal depthwise convolution + SiLU (the Mamba conv section):
+ *   out_t = silu(bias + sum_{k<K} w_k xbuf_{t-(K-1)+k}),  xbuf = cat(tail, x) along time,
+ * per channel, 2 <= K <= 8. Replaces tsfast/models/architectures/mamba/conv_triton.py:59-263
+ * (tsfast::mamba_conv_silu / mamba_conv_silu_bwd, the tail gradient of :241-250 included).
+ * Layout: x [B, L, D] in io_dtype read through element strides (sxb, sxl, sxd) (the in_proj
+ * chunk view needs no copy); tail/gtail [B, D, K-1] in io_dtype (NULL tail = zero left
+ * context; gtail may be NULL); weight/gw [D, K] and bias/gb [D] float32 (bias NULL = none);
+ * out, gy, gx [B, L, D] contiguous in io_dtype. B <= 65535; strides >= 0. One batch row of x
+ * ((L + 8) * sxl + (D + 8) * sxd elements) and of the outputs ((L + 8) * D) must stay below
+ * 4 GiB, else TSF_ERR_UNSUPPORTED.
+ */
+int tsfast_hip_conv_silu_fwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_dtype, const void* x, int64_t sxb,
+                             int64_t sxl, int64_t sxd, const void* tail, const float* weight, const float* bias,
+                             void* out, void* stream);
+/* Backward; gw/gb are the full parameter gradients (summed over batch and time). */
+int64_t tsfast_hip_conv_silu_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t K);
+int tsfast_hip_conv_silu_bwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_dtype, const void* x, int64_t sxb,
+                             int64_t sxl, int64_t sxd, const void* tail, const float* weight, const float* bias,
+                             const void* gy, void* gx, void* gtail, float* gw, float* gb, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

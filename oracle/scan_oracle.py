@@ -33,6 +33,8 @@ __all__ = [
     "mamba_backward",
     "allpole_forward",
     "allpole_backward",
+    "conv_silu_forward",
+    "conv_silu_backward",
 ]
 
 
@@ -247,3 +249,45 @@ def allpole_backward(g, a, y, y0=None):
             for i in range(j + 1, na + 1):
                 gy0[:, j] -= a[:, i - 1] * Gpad[:, i - 1 - j]
     return ga, gw, gy0
+
+
+# --------------------------------------------------------------------------- causal depthwise conv + SiLU
+def _conv_pre(x, tail, w, bias):
+    """Pre-activation ``p_t = bias + sum_k w_k xbuf_{t-(K-1)+k}`` with ``xbuf = cat(tail, x)``
+    along time, as the shifted multiply-adds of mamba/core.py:38-58 (``_causal_depthwise_silu``).
+    x [B, L, D], tail [B, D, K-1], w [D, K], bias [D] or None. Returns (p [B, L, D], xbuf)."""
+    x, tail, w = _hi(x), _hi(tail), _hi(w)
+    Bsz, L, D = x.shape
+    K = w.shape[-1]
+    buf = np.concatenate([np.transpose(tail, (0, 2, 1)), x], axis=1)  # [B, K-1+L, D]
+    p = np.zeros((Bsz, L, D)) if bias is None else np.broadcast_to(_hi(bias), (Bsz, L, D)).copy()
+    for k in range(K):
+        p += w[:, k] * buf[:, k : k + L]
+    return p, buf
+
+
+def conv_silu_forward(x, tail, w, bias=None):
+    """``silu(p)`` (mamba/core.py:38-58; conv_triton.py:59-118)."""
+    p, _ = _conv_pre(x, tail, w, bias)
+    return p * _sigmoid(p)
+
+
+def conv_silu_backward(gy, x, tail, w, bias=None):
+    """Adjoint (conv_triton.py:120-263): ``gpre = gy silu'(p)``, ``gx_t = sum_k w_k
+    gpre_{t+K-1-k}``, ``gw_k = sum_{b,t} gpre_t xbuf_{t-(K-1)+k}``, ``gb = sum gpre``,
+    ``gtail_j = sum_{t<=j} gpre_t w_{j-t}`` (the loop at :244-248).
+    Returns ``(gx, gtail, gw, gb)`` (gb None when bias is None)."""
+    gy, w = _hi(gy), _hi(w)
+    p, buf = _conv_pre(x, tail, w, bias)
+    Bsz, L, D = p.shape
+    K = w.shape[-1]
+    sg = _sigmoid(p)
+    gpre = gy * sg * (1.0 + p * (1.0 - sg))
+    gbuf = np.zeros((Bsz, K - 1 + L, D))  # gradient of every xbuf position
+    for k in range(K):
+        gbuf[:, k : k + L] += w[:, k] * gpre
+    gx = gbuf[:, K - 1 :]
+    gtail = np.transpose(gbuf[:, : K - 1], (0, 2, 1))
+    gw = np.stack([np.sum(gpre * buf[:, k : k + L], axis=(0, 1)) for k in range(K)], axis=1)
+    gb = None if bias is None else np.sum(gpre, axis=(0, 1))
+    return gx, gtail, gw, gb

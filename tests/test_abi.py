@@ -54,6 +54,8 @@ def test_size_queries(lib):
     assert lib.tsfast_hip_mamba_workspace_bytes(1, 1, 1, 65) == -1  # N above 64
     assert lib.tsfast_hip_allpole_workspace_bytes(4096, 16384, 3) > 0
     assert lib.tsfast_hip_allpole_workspace_bytes(4, 16, 17) == -1  # na above 16
+    assert lib.tsfast_hip_conv_silu_workspace_bytes(16, 4096, 1536, 4) > 0
+    assert lib.tsfast_hip_conv_silu_workspace_bytes(1, 8, 4, 9) == -1  # kernel width above 8
 
 
 def test_argument_errors_before_any_launch(lib):
@@ -61,6 +63,8 @@ def test_argument_errors_before_any_launch(lib):
     assert lib.tsfast_hip_diag_fwd(-1, 1, 1, 0, None, None, None, None, None, 0, None) == -1
     assert lib.tsfast_hip_allpole_fwd(4, 16, 17, None, None, None, None, None, 0, None) == -3
     assert lib.tsfast_hip_mamba_fwd(1, 1, 1, 65, 0, *([None] * 12)) == -3
+    assert lib.tsfast_hip_conv_silu_fwd(1, 8, 4, 1, 0, *([None, 0, 0, 0] + [None] * 5)) == -1  # K < 2
+    assert lib.tsfast_hip_conv_silu_fwd(1, 8, 4, 9, 0, *([None, 0, 0, 0] + [None] * 5)) == -3  # K > 8
     # empty problems are a no-op
     assert lib.tsfast_hip_diag_fwd(0, 5, 3, 0, None, None, None, None, None, 0, None) == 0
 

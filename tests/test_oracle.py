@@ -389,3 +389,76 @@ def test_allpole_check_rejects_forward(mutant):
 
 def test_allpole_check_rejects_backward():
     assert not check_allpole(O.allpole_forward, _allpole_no_head_taps)
+
+
+# ------------------------------------------------------------------------ causal depthwise conv + SiLU
+def _torch_conv_silu(x, tail, w, bias):
+    """F.conv1d (cross-correlation, groups = D) over cat(tail, x) along time, then SiLU."""
+    xb = torch.cat((tail, x.transpose(1, 2)), dim=-1)  # [B, D, K-1+L]
+    p = torch.nn.functional.conv1d(xb, w[:, None, :], bias, groups=w.shape[0])
+    return torch.nn.functional.silu(p).transpose(1, 2)
+
+
+def check_conv(fwd, bwd):
+    rng = _rng(7)
+    for Bsz, L, D, K, with_bias in ((2, 9, 5, 4, True), (1, 2, 3, 4, True), (3, 1, 2, 2, False), (2, 13, 4, 8, True)):
+        x = rng.standard_normal((Bsz, L, D))
+        tail = rng.standard_normal((Bsz, D, K - 1))
+        w = rng.standard_normal((D, K)) * 0.5
+        bias = rng.standard_normal(D) if with_bias else None
+        gy = rng.standard_normal((Bsz, L, D))
+        args = (x, tail, w, bias)
+        want = _torch_conv_silu(*[None if a is None else torch.tensor(a) for a in args]).numpy()
+        if O.rel_err(fwd(*args), want) > TOL:
+            return False
+        gw_ = _vjp(_torch_conv_silu, args, gy)
+        got = bwd(gy, *args)
+        for g_got, g_want in zip(got, gw_):
+            if (g_got is None) != (g_want is None):
+                return False
+            if g_got is not None and O.rel_err(g_got, g_want) > TOL:
+                return False
+        # zero tail: the reference test's form, conv1d with K-1 zero padding cut to L steps
+        # (tests/test_mamba.py:60)
+        z = np.zeros_like(tail)
+        pad = torch.nn.functional.conv1d(
+            torch.tensor(x).transpose(1, 2), torch.tensor(w)[:, None, :], None if bias is None else torch.tensor(bias),
+            padding=K - 1, groups=D,
+        )[..., :L]
+        if O.rel_err(fwd(x, z, w, bias), torch.nn.functional.silu(pad).transpose(1, 2).numpy()) > TOL:
+            return False
+    return True
+
+
+def test_conv_silu_conv1d_and_autograd():
+    assert check_conv(O.conv_silu_forward, O.conv_silu_backward)
+
+
+def _conv_flipped_taps(x, tail, w, bias=None):
+    return O.conv_silu_forward(x, tail, np.asarray(w)[:, ::-1], bias)
+
+
+def _conv_tail_reversed(x, tail, w, bias=None):
+    return O.conv_silu_forward(x, np.asarray(tail)[..., ::-1], w, bias)
+
+
+def _conv_no_silu_prime(gy, x, tail, w, bias=None):
+    # gradient of p instead of silu(p): drops the silu' factor
+    p, _ = O._conv_pre(x, tail, w, bias)
+    s = 1.0 / (1.0 + np.exp(-p))
+    return O.conv_silu_backward(np.asarray(gy) / (1.0 + p * (1.0 - s)), x, tail, w, bias)
+
+
+def _conv_tail_grad_zero(gy, x, tail, w, bias=None):
+    gx, gtail, gw, gb = O.conv_silu_backward(gy, x, tail, w, bias)
+    return gx, np.zeros_like(gtail), gw, gb
+
+
+@pytest.mark.parametrize("mutant", [_conv_flipped_taps, _conv_tail_reversed])
+def test_conv_check_rejects_forward(mutant):
+    assert not check_conv(mutant, O.conv_silu_backward)
+
+
+@pytest.mark.parametrize("mutant", [_conv_no_silu_prime, _conv_tail_grad_zero])
+def test_conv_check_rejects_backward(mutant):
+    assert not check_conv(O.conv_silu_forward, mutant)

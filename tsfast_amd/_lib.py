@@ -42,6 +42,12 @@ _SIGNATURES: dict[str, tuple[list, object]] = {
     "tsfast_hip_allpole_workspace_bytes": ([_i64, _i64, _i64], _i64),
     "tsfast_hip_allpole_fwd": ([_i64, _i64, _i64] + [_ptr] * 5 + [_i64, _ptr], _int),
     "tsfast_hip_allpole_bwd": ([_i64, _i64, _i64] + [_ptr] * 8 + [_i64, _ptr], _int),
+    "tsfast_hip_conv_silu_workspace_bytes": ([_i64, _i64, _i64, _i64], _i64),
+    "tsfast_hip_conv_silu_fwd": ([_i64, _i64, _i64, _i64, _int, _ptr, _i64, _i64, _i64] + [_ptr] * 5, _int),
+    "tsfast_hip_conv_silu_bwd": (
+        [_i64, _i64, _i64, _i64, _int, _ptr, _i64, _i64, _i64] + [_ptr] * 9 + [_i64, _ptr],
+        _int,
+    ),
 }
 
 TSF_DTYPE_F32 = 0

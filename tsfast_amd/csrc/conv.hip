@@ -1,0 +1,464 @@
+// Fused causal depthwise convolution + SiLU (the Mamba conv section), forward and backward:
+//
+//   p_t  = bias + sum_{k<K} w_k xbuf_{t-(K-1)+k},   xbuf_s = x_s (s >= 0), tail_{K-1+s} (s < 0)
+//   out_t = p_t sigmoid(p_t)
+//
+// per channel d, over x [B, L, D] read through arbitrary element strides (the reference passes
+// the strided in_proj chunk view), tail [B, D, K-1] the carried causal left context.
+// Reference semantics: tsfast/models/architectures/mamba/conv_triton.py:59-263 (kernels and
+// ops, tail gradient at :241-250) and the eager path mamba/core.py:38-58.
+//
+// No recurrence: each thread owns VEC consecutive channels and a run of kRun consecutive steps,
+// keeps the K-1 step causal window in registers, and streams x once (plus a K-1 step halo per
+// run); consecutive threads own consecutive channel groups, so every per-step access of a wave
+// is one coalesced row segment. Memory-bound: fwd reads x and writes out, bwd reads x and gy and
+// writes gx. The backward recomputes p (cheaper than storing it), forms gx from the K shifted
+// pre-activation gradients, and reduces grad-w / grad-bias in registers over a thread's runs,
+// in LDS over a workgroup, and over (batch, run block) in a second kernel, in a fixed order
+// (deterministic).
+#include "common.h"
+#include "tsfast_hip.h"
+
+using namespace tsf;
+
+namespace {
+
+constexpr int kRun = 16;   // forward steps per thread
+constexpr int kCgWg = 64;  // channel groups per workgroup (one wave wide)
+constexpr int kRunsWg = 4; // runs per workgroup (one per wave)
+
+template <typename TIO>
+TSF_DEV TIO zero_io();
+template <>
+TSF_DEV float zero_io<float>() {
+  return 0.0f;
+}
+template <>
+TSF_DEV bf16 zero_io<bf16>() {
+  bf16 r;
+  r.bits = 0;
+  return r;
+}
+
+// VEC consecutive channels of one row: one vector access when the row is contiguous.
+template <typename TIO, int VEC>
+struct alignas(sizeof(TIO) * VEC) Vec {
+  TIO v[VEC];
+};
+
+// VEC channels at element offset o of a row base (32-bit byte offsets from a workgroup-uniform
+// base: the SGPR-base + VGPR-offset address form, no 64-bit arithmetic per access).
+template <typename TIO, int VEC>
+TSF_DEV void load_vec(float (&dst)[VEC], const TIO* base, uint32_t o) {
+  if (VEC > 1) {
+    const Vec<TIO, VEC> r = ld32(reinterpret_cast<const Vec<TIO, VEC>*>(base), o / VEC);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) dst[c] = to_f32(r.v[c]);
+  } else {
+    dst[0] = to_f32(ld32(base, o));
+  }
+}
+
+template <typename TIO, int VEC>
+TSF_DEV void store_vec(TIO* base, uint32_t o, const float (&src)[VEC]) {
+  if (VEC > 1) {
+    Vec<TIO, VEC> r;
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) r.v[c] = from_f32<TIO>(src[c]);
+    st32(reinterpret_cast<Vec<TIO, VEC>*>(base), o / VEC, r);
+  } else {
+    st32(base, o, from_f32<TIO>(src[0]));
+  }
+}
+
+TSF_DEV float silu_f(float p) { return p * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-p * kLog2e)); }
+
+// Thread coordinates: channel group cg (VEC channels from d0 = cg * VEC), run r, batch row b.
+struct Coord {
+  int64_t b, run, d0;
+  bool live;
+};
+template <int VEC>
+TSF_DEV Coord coord(int64_t D, int64_t runs) {
+  const int64_t cgs = (D + VEC - 1) / VEC;
+  const int64_t cg = (int64_t)blockIdx.x * kCgWg + (threadIdx.x % kCgWg);
+  const int64_t run = (int64_t)blockIdx.y * kRunsWg + threadIdx.x / kCgWg;
+  Coord c;
+  c.b = blockIdx.z;
+  c.run = run;
+  c.d0 = cg * VEC;
+  c.live = cg < cgs && run < runs;
+  return c;
+}
+
+// xbuf_s for VEC channels (s may be negative: the carried tail); zero outside [-(K-1), L).
+// xrow = x + b * sxb (uniform per workgroup); the vector path has sxd == 1.
+template <typename TIO, int VEC, int K>
+TSF_DEV void load_xbuf(float (&dst)[VEC], const TIO* __restrict__ xrow, const TIO* __restrict__ tail, int64_t b,
+                       int64_t s, int64_t d0, int64_t L, int64_t D, int64_t sxl, int64_t sxd) {
+  if (s >= 0 && s < L) {
+    load_vec<TIO, VEC>(dst, xrow, (uint32_t)(s * sxl + d0 * sxd));
+  } else if (s < 0 && s >= -(K - 1)) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) dst[c] = tail ? to_f32(tail[(b * D + d0 + c) * (K - 1) + (K - 1 + s)]) : 0.0f;
+  } else {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) dst[c] = 0.0f;
+  }
+}
+
+// ------------------------------------------------------------------------------------ forward
+template <typename TIO, int K, int VEC>
+__global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_fwd_kernel(
+    const TIO* __restrict__ x, const TIO* __restrict__ tail, const float* __restrict__ w,
+    const float* __restrict__ bias, TIO* __restrict__ out, int64_t L, int64_t D, int64_t sxb, int64_t sxl,
+    int64_t sxd, int64_t runs) {
+  const Coord c = coord<VEC>(D, runs);
+  if (!c.live) return;
+  float wk[K][VEC], bv[VEC];
+#pragma unroll
+  for (int ch = 0; ch < VEC; ++ch) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) wk[k][ch] = w[(c.d0 + ch) * K + k];
+    bv[ch] = bias ? bias[c.d0 + ch] : 0.0f;
+  }
+  const int64_t t0 = c.run * kRun;
+  // the run's inputs with its K-1 step causal halo, all loads issued before the arithmetic
+  const TIO* xrow = x + c.b * sxb;
+  float xb[kRun + K - 1][VEC];
+#pragma unroll
+  for (int i = 0; i < kRun + K - 1; ++i)
+    load_xbuf<TIO, VEC, K>(xb[i], xrow, tail, c.b, t0 - (K - 1) + i, c.d0, L, D, sxl, sxd);
+  TIO* orow = out + c.b * L * D;
+#pragma unroll
+  for (int i = 0; i < kRun; ++i) {
+    if (t0 + i >= L) break;
+    float o[VEC];
+#pragma unroll
+    for (int ch = 0; ch < VEC; ++ch) {
+      float p = bv[ch];
+#pragma unroll
+      for (int k = 0; k < K; ++k) p = fmaf(wk[k][ch], xb[i + k][ch], p);
+      o[ch] = silu_f(p);
+    }
+    store_vec<TIO, VEC>(orow, (uint32_t)((t0 + i) * D + c.d0), o);
+  }
+}
+
+// ----------------------------------------------------------------------------------- backward
+// gpre_t = gy_t silu'(p_t); gx_t = sum_k w_k gpre_{t+K-1-k}; grad w_k = sum_t gpre_t
+// xbuf_{t-(K-1)+k}; grad bias = sum_t gpre_t; grad tail_j = sum_{t<=j} gpre_t w_{j-t}.
+// A backward thread walks kRpt consecutive runs, accumulating its parameter partials in
+// registers; the workgroup's kRunsWg threads per channel group meet in LDS, and the result is
+// one partial row per (batch, run block): part [B, G, D, K+1] (K taps, then the bias term).
+constexpr int kRpt = 4;
+constexpr int kRunB = 8;  // backward steps per run: its register tiles hold x and gy with halos
+
+template <typename TIO, int K, int VEC>
+__global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_bwd_kernel(
+    const TIO* __restrict__ x, const TIO* __restrict__ tail, const float* __restrict__ w,
+    const float* __restrict__ bias, const TIO* __restrict__ gy, TIO* __restrict__ gx, TIO* __restrict__ gtail,
+    float* __restrict__ part, int64_t L, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd, int64_t runs) {
+  constexpr int KP = K + 1;
+  constexpr int NP = kRunB + K - 1;  // steps whose gpre a run needs: t0 .. t0+kRunB+K-2
+  __shared__ float s_part[kRunsWg][KP][kCgWg * VEC];
+  const int wv = threadIdx.x / kCgWg, ln = threadIdx.x % kCgWg;
+  const int64_t cg = (int64_t)blockIdx.x * kCgWg + ln;
+  const int64_t b = blockIdx.z;
+  const int64_t d0 = cg * VEC;
+  const int64_t run0 = ((int64_t)blockIdx.y * kRunsWg + wv) * kRpt;
+  const TIO* xrow = x + b * sxb;
+  const TIO* gyrow = gy + b * L * D;
+  TIO* gxrow = gx + b * L * D;
+  float acc[KP][VEC];
+#pragma unroll
+  for (int k = 0; k < KP; ++k)
+#pragma unroll
+    for (int ch = 0; ch < VEC; ++ch) acc[k][ch] = 0.0f;
+
+  if (cg < (D + VEC - 1) / VEC) {
+    float wk[K][VEC], bv[VEC];
+#pragma unroll
+    for (int ch = 0; ch < VEC; ++ch) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) wk[k][ch] = w[(d0 + ch) * K + k];
+      bv[ch] = bias ? bias[d0 + ch] : 0.0f;
+    }
+#pragma unroll 1
+    for (int r = 0; r < kRpt; ++r) {
+      const int64_t t0 = (run0 + r) * kRunB;
+      if (t0 >= L) break;
+      // xbuf from t0-(K-1) to t0+kRunB+K-2 and gy from t0 to t0+kRunB+K-2, loads issued first
+      float xb[NP + K - 1][VEC], gp[NP][VEC];
+#pragma unroll
+      for (int i = 0; i < NP + K - 1; ++i)
+        load_xbuf<TIO, VEC, K>(xb[i], xrow, tail, b, t0 - (K - 1) + i, d0, L, D, sxl, sxd);
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        if (t0 + i < L) {
+          load_vec<TIO, VEC>(gp[i], gyrow, (uint32_t)((t0 + i) * D + d0));
+        } else {
+#pragma unroll
+          for (int ch = 0; ch < VEC; ++ch) gp[i][ch] = 0.0f;  // rows past the end carry no gradient
+        }
+      }
+      // gpre in place of gy
+#pragma unroll
+      for (int i = 0; i < NP; ++i)
+#pragma unroll
+        for (int ch = 0; ch < VEC; ++ch) {
+          float p = bv[ch];
+#pragma unroll
+          for (int k = 0; k < K; ++k) p = fmaf(wk[k][ch], xb[i + k][ch], p);
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-p * kLog2e));
+          gp[i][ch] *= sg * fmaf(p, 1.0f - sg, 1.0f);
+        }
+#pragma unroll
+      for (int i = 0; i < kRunB; ++i) {
+        if (t0 + i >= L) break;
+        float g[VEC];
+#pragma unroll
+        for (int ch = 0; ch < VEC; ++ch) {
+          float s = 0.0f;
+#pragma unroll
+          for (int k = 0; k < K; ++k) s = fmaf(wk[k][ch], gp[i + K - 1 - k][ch], s);
+          g[ch] = s;
+          // parameter partials over this run's own steps
+#pragma unroll
+          for (int k = 0; k < K; ++k) acc[k][ch] = fmaf(gp[i][ch], xb[i + k][ch], acc[k][ch]);
+          acc[K][ch] += gp[i][ch];
+        }
+        store_vec<TIO, VEC>(gxrow, (uint32_t)((t0 + i) * D + d0), g);
+      }
+      // the carried tail feeds the first K-1 outputs
+      if (t0 == 0 && gtail) {
+#pragma unroll
+        for (int ch = 0; ch < VEC; ++ch)
+#pragma unroll
+          for (int j = 0; j < K - 1; ++j) {
+            float s = 0.0f;
+#pragma unroll
+            for (int t = 0; t <= j; ++t) s = fmaf(gp[t][ch], wk[j - t][ch], s);  // gp = 0 past L
+            gtail[(b * D + d0 + ch) * (K - 1) + j] = from_f32<TIO>(s);
+          }
+      }
+    }
+  }
+  // reduce the workgroup's threads of each channel group in LDS (fixed order)
+#pragma unroll
+  for (int k = 0; k < KP; ++k)
+#pragma unroll
+    for (int ch = 0; ch < VEC; ++ch) s_part[wv][k][ln * VEC + ch] = acc[k][ch];
+  __syncthreads();
+  const int64_t groups = gridDim.y;
+  for (int idx = threadIdx.x; idx < KP * kCgWg * VEC; idx += kCgWg * kRunsWg) {
+    const int k = idx / (kCgWg * VEC), dd = idx % (kCgWg * VEC);
+    const int64_t d = (int64_t)blockIdx.x * kCgWg * VEC + dd;
+    if (d < D) {
+      float s = 0.0f;
+#pragma unroll
+      for (int r = 0; r < kRunsWg; ++r) s += s_part[r][k][dd];
+      part[((int64_t)blockIdx.z * groups + blockIdx.y) * D * KP + d * KP + k] = s;
+    }
+  }
+}
+
+// grad w [D, K] and grad bias [D]: sum the partials [P, D, K+1] over P in a fixed order. A
+// workgroup owns 64 consecutive outputs; its kRedWaves waves sum contiguous segments of the
+// P rows (independent loads in flight), and wave 0 adds the segment sums in order.
+constexpr int kRedWaves = 16;
+__global__ void __launch_bounds__(64 * kRedWaves) conv_reduce_params(const float* __restrict__ part,
+                                                                    float* __restrict__ gw, float* __restrict__ gb,
+                                                                    int64_t P, int64_t D, int K) {
+  __shared__ float s_seg[kRedWaves][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t n = D * (K + 1);
+  const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t seg = (P + kRedWaves - 1) / kRedWaves;
+  const int64_t p0 = wv * seg, p1 = (p0 + seg < P) ? p0 + seg : P;
+  float s = 0.0f;
+  if (i < n) {
+#pragma unroll 8
+    for (int64_t p = p0; p < p1; ++p) s += part[p * n + i];
+  }
+  s_seg[wv][lane] = s;
+  __syncthreads();
+  if (wv == 0 && i < n) {
+    float t = s_seg[0][lane];
+    for (int j = 1; j < kRedWaves; ++j) t += s_seg[j][lane];
+    const int64_t d = i / (K + 1);
+    const int k = (int)(i % (K + 1));
+    if (k < K)
+      gw[d * K + k] = t;
+    else if (gb)
+      gb[d] = t;
+  }
+}
+
+__global__ void __launch_bounds__(256) conv_zero_f32(float* __restrict__ p, int64_t n) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+struct ConvPlan {
+  int64_t runs, cg_blocks, run_groups;
+};
+// run_groups: runs per workgroup row of the grid (kRunsWg for the forward, kRunsWg * kRpt for
+// the backward, whose threads walk kRpt runs each)
+ConvPlan conv_plan(int64_t L, int64_t D, int vec, int run_len, int runs_per_group) {
+  ConvPlan p;
+  p.runs = (L + run_len - 1) / run_len;
+  p.cg_blocks = ((D + vec - 1) / vec + kCgWg - 1) / kCgWg;
+  p.run_groups = (p.runs + runs_per_group - 1) / runs_per_group;
+  return p;
+}
+
+// Vector width 4 (both passes) when every row of x and of the contiguous outputs is a 16-byte-aligned run of
+// whole channel groups; the tail, weights and bias are read per channel either way.
+template <typename TIO>
+int vec_for(const void* x, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd, const void* y) {
+  const uintptr_t a = (uintptr_t)x | (uintptr_t)y;
+  const bool ok = sxd == 1 && D % 4 == 0 && sxl % 4 == 0 && sxb % 4 == 0 && a % (4 * sizeof(TIO)) == 0;
+  return ok ? 4 : 1;
+}
+
+template <typename TIO, int K, int VEC>
+void launch_fwd(int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
+                const void* tail, const float* w, const float* bias, void* out, hipStream_t s) {
+  const ConvPlan p = conv_plan(L, D, VEC, kRun, kRunsWg);
+  dim3 grid((unsigned)p.cg_blocks, (unsigned)p.run_groups, (unsigned)B);
+  hipLaunchKernelGGL((conv_silu_fwd_kernel<TIO, K, VEC>), grid, dim3(kCgWg * kRunsWg), 0, s, (const TIO*)x,
+                     (const TIO*)tail, w, bias, (TIO*)out, L, D, sxb, sxl, sxd, p.runs);
+}
+
+template <typename TIO, int K, int VEC>
+void launch_bwd(int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
+                const void* tail, const float* w, const float* bias, const void* gy, void* gx, void* gtail,
+                float* gw, float* gb, float* part, hipStream_t s) {
+  const ConvPlan p = conv_plan(L, D, VEC, kRunB, kRunsWg * kRpt);
+  dim3 grid((unsigned)p.cg_blocks, (unsigned)p.run_groups, (unsigned)B);
+  hipLaunchKernelGGL((conv_silu_bwd_kernel<TIO, K, VEC>), grid, dim3(kCgWg * kRunsWg), 0, s, (const TIO*)x,
+                     (const TIO*)tail, w, bias, (const TIO*)gy, (TIO*)gx, (TIO*)gtail, part, L, D, sxb, sxl, sxd,
+                     p.runs);
+  const int64_t n = D * (K + 1);
+  hipLaunchKernelGGL(conv_reduce_params, dim3((unsigned)((n + 63) / 64)), dim3(64 * kRedWaves), 0, s,
+                     (const float*)part, gw, gb, B * p.run_groups, D, K);
+}
+
+template <typename TIO, int K>
+void fwd_k(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
+           const void* tail, const float* w, const float* bias, void* out, hipStream_t s) {
+  if (vec == 4)
+    launch_fwd<TIO, K, 4>(B, L, D, x, sxb, sxl, sxd, tail, w, bias, out, s);
+  else
+    launch_fwd<TIO, K, 1>(B, L, D, x, sxb, sxl, sxd, tail, w, bias, out, s);
+}
+
+template <typename TIO, int K>
+void bwd_k(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
+           const void* tail, const float* w, const float* bias, const void* gy, void* gx, void* gtail, float* gw,
+           float* gb, float* part, hipStream_t s) {
+  if (vec == 4)
+    launch_bwd<TIO, K, 4>(B, L, D, x, sxb, sxl, sxd, tail, w, bias, gy, gx, gtail, gw, gb, part, s);
+  else
+    launch_bwd<TIO, K, 1>(B, L, D, x, sxb, sxl, sxd, tail, w, bias, gy, gx, gtail, gw, gb, part, s);
+}
+
+#define TSF_CONV_K_SWITCH(K, CALL) \
+  switch (K) {                     \
+    case 2: CALL(2); break;        \
+    case 3: CALL(3); break;        \
+    case 4: CALL(4); break;        \
+    case 5: CALL(5); break;        \
+    case 6: CALL(6); break;        \
+    case 7: CALL(7); break;        \
+    case 8: CALL(8); break;        \
+    default: return TSF_ERR_UNSUPPORTED; \
+  }
+
+// TSF_OK when the sizes are valid and supported, else the status to return
+int conv_args_status(int64_t B, int64_t L, int64_t D, int64_t K) {
+  if (B < 0 || L < 0 || D < 0 || K < 2) return TSF_ERR_ARG;
+  if (K > 8 || B > 65535) return TSF_ERR_UNSUPPORTED;
+  return TSF_OK;
+}
+
+// The kernels address one batch row of x and of the [B, L, D] outputs with 32-bit byte offsets.
+int conv_layout_status(int64_t L, int64_t D, int64_t sxl, int64_t sxd, int64_t esz) {
+  if (sxl < 0 || sxd < 0) return TSF_ERR_ARG;
+  const int64_t lim = (int64_t)1 << 32;
+  const bool ok = ((L + 8) * sxl + (D + 8) * sxd) * esz < lim && (L + 8) * D * esz < lim;
+  return ok ? TSF_OK : TSF_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t tsfast_hip_conv_silu_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t K) {
+  if (conv_args_status(B, L, D, K) != TSF_OK) return -1;
+  const ConvPlan p = conv_plan(L, D, 1, kRunB, kRunsWg * kRpt);
+  return B * p.run_groups * D * (K + 1) * 4;
+}
+
+int tsfast_hip_conv_silu_fwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_dtype, const void* x, int64_t sxb,
+                             int64_t sxl, int64_t sxd, const void* tail, const float* weight, const float* bias,
+                             void* out, void* stream) {
+  if (const int st = conv_args_status(B, L, D, K)) return st;
+  if (B == 0 || L == 0 || D == 0) return TSF_OK;
+  if (!x || !weight || !out) return TSF_ERR_ARG;
+  if (const int st = conv_layout_status(L, D, sxl, sxd, io_dtype == TSF_DTYPE_BF16 ? 2 : 4)) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (io_dtype == TSF_DTYPE_F32) {
+    const int vec = vec_for<float>(x, D, sxb, sxl, sxd, out);
+#define CALL(KK) fwd_k<float, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, out, s)
+    TSF_CONV_K_SWITCH(K, CALL)
+#undef CALL
+  } else if (io_dtype == TSF_DTYPE_BF16) {
+    const int vec = vec_for<bf16>(x, D, sxb, sxl, sxd, out);
+#define CALL(KK) fwd_k<bf16, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, out, s)
+    TSF_CONV_K_SWITCH(K, CALL)
+#undef CALL
+  } else {
+    return TSF_ERR_ARG;
+  }
+  return tsf_launch_status();
+}
+
+int tsfast_hip_conv_silu_bwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_dtype, const void* x, int64_t sxb,
+                             int64_t sxl, int64_t sxd, const void* tail, const float* weight, const float* bias,
+                             const void* gy, void* gx, void* gtail, float* gw, float* gb, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+  if (const int st = conv_args_status(B, L, D, K)) return st;
+  if (D == 0) return TSF_OK;
+  if (!weight || !gw || (bias && !gb)) return TSF_ERR_ARG;
+  if (B > 0 && L > 0 && (!x || !gy || !gx)) return TSF_ERR_ARG;
+  if (workspace_bytes < tsfast_hip_conv_silu_workspace_bytes(B, L, D, K) || (!workspace && B * L > 0))
+    return TSF_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B == 0 || L == 0) {
+    // empty sequence: parameter gradients are zero, the tail receives no gradient
+    const int64_t n = D * K;
+    hipLaunchKernelGGL(conv_zero_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, gw, n);
+    if (gb) hipLaunchKernelGGL(conv_zero_f32, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, s, gb, D);
+    return tsf_launch_status();
+  }
+  if (const int st = conv_layout_status(L, D, sxl, sxd, io_dtype == TSF_DTYPE_BF16 ? 2 : 4)) return st;
+  float* part = static_cast<float*>(workspace);
+  if (io_dtype == TSF_DTYPE_F32) {
+    const int vec = vec_for<float>(x, D, sxb, sxl, sxd, gy) == 4 && ((uintptr_t)gx % 16 == 0) ? 4 : 1;
+#define CALL(KK) bwd_k<float, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, gy, gx, gtail, gw, gb, part, s)
+    TSF_CONV_K_SWITCH(K, CALL)
+#undef CALL
+  } else if (io_dtype == TSF_DTYPE_BF16) {
+    const int vec = vec_for<bf16>(x, D, sxb, sxl, sxd, gy) == 4 && ((uintptr_t)gx % 8 == 0) ? 4 : 1;
+#define CALL(KK) bwd_k<bf16, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, gy, gx, gtail, gw, gb, part, s)
+    TSF_CONV_K_SWITCH(K, CALL)
+#undef CALL
+  } else {
+    return TSF_ERR_ARG;
+  }
+  return tsf_launch_status();
+}
+
+}  // extern "C"
