@@ -87,6 +87,29 @@ TSF_DEV bf16 io_zero<bf16>() {
 template <bool V>
 using Bool = std::integral_constant<bool, V>;
 
+// Wave issue priority (s_setprio takes an immediate, 0..3).
+TSF_DEV void set_wave_priority(unsigned p) {
+  switch (p) {
+    case 0: __builtin_amdgcn_s_setprio(0); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    default: __builtin_amdgcn_s_setprio(3); break;
+  }
+}
+
+// Compute units of the current device (queried once per device).
+unsigned device_cus() {
+  static unsigned cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = (unsigned)n;
+  }
+  return cache[dev];
+}
+
 // Streaming store for the training forward's saved state, which is read back only by the
 // backward (non-temporal: it is not kept in the caches on the way out).
 TSF_DEV void nt_store(float* p, float v) { __builtin_nontemporal_store(v, p); }
@@ -118,7 +141,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     const TIO* __restrict__ draw, const float* __restrict__ A, const TIO* __restrict__ Bt,
     const TIO* __restrict__ Ct, const TIO* __restrict__ u, const TIO* __restrict__ z, const float* __restrict__ Dp,
     const float* __restrict__ h0, TIO* __restrict__ out, float* __restrict__ h_last, float* __restrict__ chk,
-    int64_t L, int64_t D, int N, int64_t NC) {
+    int64_t L, int64_t D, int N, int64_t NC, unsigned cus) {
   using C = MCfg<NS>;
   constexpr int NPT = C::NPT, NG = C::NG, DT = C::DT, TH = C::TH, CHK = C::CHK, TF = C::TF;
   constexpr int IT = C::IT_F, BCI = C::BC_F, NPAIR = C::NPAIR;
@@ -281,7 +304,14 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       }
     }
   };
-  for (int64_t t0 = 0; t0 < L; t0 += TF) chunk((uint32_t)t0, (int)((L - t0) < TF ? (L - t0) : TF));
+  // Workgroups sharing a CU (slot = dispatch round) are issued oldest-first, so the first one
+  // races ahead and the last ones finish alone; rotating the issue priority among the slots
+  // every four rounds evens their progress and shortens the tail.
+  const unsigned slot = (blockIdx.x + blockIdx.y * gridDim.x) / cus;
+  for (int64_t t0 = 0; t0 < L; t0 += TF) {
+    if (((t0 / TF) & 3) == 0) set_wave_priority((slot + (unsigned)(t0 / TF / 4)) % 3);
+    chunk((uint32_t)t0, (int)((L - t0) < TF ? (L - t0) : TF));
+  }
   (void)NG;
   if (act) {
 #pragma unroll
@@ -629,7 +659,8 @@ int launch_fwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
   const int64_t NC = (L + C::CHK - 1) / C::CHK;
   dim3 grid((unsigned)((D + C::DT - 1) / C::DT), (unsigned)B);
   hipLaunchKernelGGL((mamba_fwd_kernel<TIO, NS>), grid, dim3(C::TH), 0, s, (const TIO*)draw, A, (const TIO*)Bt,
-                     (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, (TIO*)out, h_last, chk, L, D, (int)N, NC);
+                     (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, (TIO*)out, h_last, chk, L, D, (int)N, NC,
+                     device_cus());
   return tsf_launch_status();
 }
 
