@@ -382,6 +382,61 @@ def run_conv(args, line):
     return ms, fwd_b + bwd_b, kernels, cpu
 
 
+def run_selective(args, line):
+    """The time-varying (selective) diagonal scan, fp32, in the Mamba generic-fallback layout
+    [B, L, D*N] (scope-table rows a6/a7; not a BASELINE config): B16 L4096, 2048 lanes per row."""
+    import torch
+
+    from tsfast_amd.scan_backends import selective_hip
+
+    g = torch.Generator().manual_seed(6)
+    M, L, N = 16, 4096, 2048
+    a = (torch.rand(M, L, N, generator=g) * 0.5 + 0.49).cuda()
+    v = torch.randn(M, L, N, generator=g).cuda()
+    gv_up = torch.randn(M, L, N, generator=g).cuda()
+
+    def step(ev):
+        mark(ev)
+        o = selective_hip.forward(a, v, None)
+        mark(ev)
+        selective_hip.backward(gv_up, a, o, None)
+        mark(ev)
+
+    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
+    e = M * L * N
+    fwd_b, bwd_b = 3 * e * 4, 5 * e * 4  # fwd: a, v -> out; bwd: g, a, out -> glam, gv
+    line.update(
+        config={"workload": "selective diagonal scan fwd+bwd, fp32, [B, L, lanes] = [16, 4096, 2048] (rows a6/a7)",
+                "M": M, "L": L, "N": N, "io_dtype": "f32"},
+        fwd_ms=round(fwd_ms, 4),
+        bwd_ms=round(bwd_ms, 4),
+    )
+    line["metric"] = "fwd+bwd ms + achieved HBM GB/s, selective scan [16, 4096, 2048] fp32"
+    line["dtype"] = "f64"  # fp32 I/O, fp64 state inside
+    kernels = {"fwd": ("sel fwd (chunk maps + re-scan)", fwd_ms, fwd_b),
+               "bwd": ("sel bwd (chunk maps + re-scan)", bwd_ms, bwd_b)}
+    cpu = None
+    if not args.no_cpu:
+        def cpu_leg():
+            from oracle import cpu_baseline as CB
+
+            lib = CB.load(prefer_native=True)
+            threads = os.cpu_count() or 1
+            lib.cpu_set_threads(threads)
+            rows = 2
+            a_c, v_c, g_c = (t[:rows].cpu().numpy() for t in (a, v, gv_up))
+            med, n = cpu_time(lambda: CB.sel_fwd_bwd(a_c, v_c, g_c, None))
+            eb = rows * L * N * 4
+            return {
+                "value": round(8 * eb / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": (f"rows={rows} of {M}, L={L}, N={N} (oracle/cpu_baseline.cpp after "
+                           f"scan_backends/selective_c.py, sequential per (row, 64-lane block)), fwd+bwd median "
+                           f"of {n} runs = {med * 1e3:.2f} ms"),
+            }
+        cpu = cpu_leg
+    return ms, fwd_b + bwd_b, kernels, cpu
+
+
 def run_allpole(args, line):
     from tsfast_amd.dynonet import allpole_hip
 
@@ -441,6 +496,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5))
     ap.add_argument("--io", choices=("bf16", "fp32"), default="bf16", help="config 3 / --conv I/O dtype")
+    ap.add_argument("--selective", action="store_true",
+                    help="measure the selective (time-varying) diagonal scan instead of a BASELINE config")
     ap.add_argument("--conv", action="store_true",
                     help="measure the fused Mamba conv+SiLU at config 3's shape instead of a BASELINE config")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
@@ -488,7 +545,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
     }
-    runner = run_conv if args.conv else {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config]
+    runner = run_conv if args.conv else run_selective if args.selective else {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config]
     ms, total_bytes, kernels, cpu = runner(args, line)
     gbs = total_bytes / (ms * 1e-3) / 1e9
     line["value"] = round(gbs, 2)
@@ -498,7 +555,7 @@ def main():
     phase = max(kernels, key=lambda k: kernels[k][1])
     name, dom_ms, dom_b = kernels[phase]
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
-    measured = None if args.conv else MEASURED_TRAFFIC.get((args.config, args.io if args.config == 3 else "f32"), {}).get(phase)
+    measured = None if (args.conv or args.selective) else MEASURED_TRAFFIC.get((args.config, args.io if args.config == 3 else "f32"), {}).get(phase)
     line["roofline"] = {
         "bound": "hbm",
         "kernel": name,

@@ -261,6 +261,49 @@ void diag_bwd_impl(int64_t M, int64_t L, int64_t N, int cplx, const float* g, co
   }
 }
 
+// Time-varying diagonal scan (scan_backends/selective_c.py:45-121): one task per (row, 64-lane
+// tile) keeps the tile's state resident and streams over L; the inner lane loop vectorises.
+void sel_fwd_impl(int64_t M, int64_t L, int64_t N, const float* a, const float* v, const float* x0, float* out) {
+  const int64_t nt = (N + 63) / 64;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M * nt; ++i) {
+    const int64_t m = i / nt, n0 = (i % nt) * 64;
+    const int nw = (int)std::min<int64_t>(64, N - n0);
+    float x[64];
+    for (int j = 0; j < nw; ++j) x[j] = x0 ? x0[m * N + n0 + j] : 0.0f;
+    for (int64_t t = 0; t < L; ++t) {
+      const int64_t p = (m * L + t) * N + n0;
+      for (int j = 0; j < nw; ++j) {
+        x[j] = a[p + j] * x[j] + v[p + j];
+        out[p + j] = x[j];
+      }
+    }
+  }
+}
+
+void sel_bwd_impl(int64_t M, int64_t L, int64_t N, const float* g, const float* a, const float* out,
+                  const float* x0, float* glam, float* gv, float* gx0) {
+  const int64_t nt = (N + 63) / 64;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M * nt; ++i) {
+    const int64_t m = i / nt, n0 = (i % nt) * 64;
+    const int nw = (int)std::min<int64_t>(64, N - n0);
+    float G[64];
+    for (int j = 0; j < nw; ++j) G[j] = 0.0f;
+    for (int64_t t = L - 1; t >= 0; --t) {
+      const int64_t p = (m * L + t) * N + n0;
+      for (int j = 0; j < nw; ++j) {
+        G[j] = g[p + j] + (t + 1 < L ? a[p + N + j] * G[j] : 0.0f);
+        gv[p + j] = G[j];
+        const float xp = t > 0 ? out[p - N + j] : (x0 ? x0[m * N + n0 + j] : 0.0f);
+        glam[p + j] = G[j] * xp;
+      }
+      if (t == 0 && gx0)
+        for (int j = 0; j < nw; ++j) gx0[m * N + n0 + j] = a[p + j] * G[j];
+    }
+  }
+}
+
 }  // namespace
 
 #define TSF_CPU_NS(X) X(1) X(2) X(3) X(4) X(8) X(12) X(16) X(32) X(64)
@@ -312,6 +355,17 @@ int cpu_diag_fwd(int64_t M, int64_t L, int64_t N, int cplx, const float* lam, co
 int cpu_diag_bwd(int64_t M, int64_t L, int64_t N, int cplx, const float* g, const float* lam, const float* out,
                  const float* x0, float* gv, float* glam, float* gx0) {
   diag_bwd_impl(M, L, N, cplx, g, lam, out, x0, gv, glam, gx0);
+  return 0;
+}
+
+int cpu_sel_fwd(int64_t M, int64_t L, int64_t N, const float* a, const float* v, const float* x0, float* out) {
+  sel_fwd_impl(M, L, N, a, v, x0, out);
+  return 0;
+}
+
+int cpu_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const float* a, const float* out, const float* x0,
+                float* glam, float* gv, float* gx0) {
+  sel_bwd_impl(M, L, N, g, a, out, x0, glam, gv, gx0);
   return 0;
 }
 

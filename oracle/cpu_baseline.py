@@ -71,7 +71,10 @@ def load(prefer_native: bool = True) -> ctypes.CDLL:
     lib.cpu_mamba_bwd.argtypes = [i64] * 4 + [ptr] * 19
     lib.cpu_diag_fwd.argtypes = [i64, i64, i64, i32] + [ptr] * 4
     lib.cpu_diag_bwd.argtypes = [i64, i64, i64, i32] + [ptr] * 7
-    for name in ("cpu_mamba_fwd", "cpu_mamba_bwd", "cpu_diag_fwd", "cpu_diag_bwd", "cpu_num_threads",
+    lib.cpu_sel_fwd.argtypes = [i64, i64, i64] + [ptr] * 4
+    lib.cpu_sel_bwd.argtypes = [i64, i64, i64] + [ptr] * 7
+    for name in ("cpu_mamba_fwd", "cpu_mamba_bwd", "cpu_diag_fwd", "cpu_diag_bwd", "cpu_sel_fwd", "cpu_sel_bwd",
+                 "cpu_num_threads",
                  "cpu_mamba_chk", "cpu_mamba_bd"):
         getattr(lib, name).restype = i32
     lib.cpu_set_threads.argtypes = [i32]
@@ -130,4 +133,18 @@ def diag_fwd_bwd(lam, v, g, x0=None):
     glam = np.empty_like(lam)
     gx0 = np.empty_like(lam) if x0 is not None else None
     lib.cpu_diag_bwd(M, L, N, cplx, _p(g), _p(lam), _p(out), _p(x0), _p(gv), _p(glam), _p(gx0))
+    return out, glam, gv, gx0
+
+
+def sel_fwd_bwd(a, v, g, x0=None):
+    """Time-varying diagonal scan forward + backward (float32 numpy arrays [M, L, N])."""
+    lib = load()
+    a, v, g = (np.ascontiguousarray(t, dtype=np.float32) for t in (a, v, g))
+    x0 = None if x0 is None else np.ascontiguousarray(x0, dtype=np.float32)
+    M, L, N = v.shape
+    out = np.empty_like(v)
+    lib.cpu_sel_fwd(M, L, N, _p(a), _p(v), _p(x0), _p(out))
+    glam, gv = np.empty_like(v), np.empty_like(v)
+    gx0 = np.empty_like(x0) if x0 is not None else None
+    lib.cpu_sel_bwd(M, L, N, _p(g), _p(a), _p(out), _p(x0), _p(glam), _p(gv), _p(gx0))
     return out, glam, gv, gx0

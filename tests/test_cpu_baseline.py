@@ -54,3 +54,16 @@ def test_diag_port_matches_oracle(lib, cplx):
     wl, wv, wx = O.diag_backward(g, lam, want, x0)
     assert O.rel_err(out, want) < 1e-5
     assert O.rel_err(glam, wl) < 1e-4 and O.rel_err(gv, wv) < 1e-5 and O.rel_err(gx0, wx) < 1e-5
+
+
+def test_selective_port_matches_oracle(lib):
+    rng = np.random.default_rng(4)
+    M, L, N = 3, 70, 100
+    a = rng.uniform(0.05, 0.95, (M, L, N)).astype(np.float32)
+    v, g = rng.standard_normal((M, L, N)).astype(np.float32), rng.standard_normal((M, L, N)).astype(np.float32)
+    x0 = rng.standard_normal((M, N)).astype(np.float32)
+    out, glam, gv, gx0 = CB.sel_fwd_bwd(a, v, g, x0)
+    want = O.selective_forward(a, v, x0)
+    wl, wv, wx = O.selective_backward(g, a, want, x0)
+    assert O.rel_err(out, want) < 1e-5
+    assert O.rel_err(glam, wl) < 1e-5 and O.rel_err(gv, wv) < 1e-5 and O.rel_err(gx0, wx) < 1e-5

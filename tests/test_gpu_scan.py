@@ -95,7 +95,11 @@ def test_diag_inference_equals_grad_path(gpu):
     assert torch.equal(a, b.detach())
 
 
-@pytest.mark.parametrize("shape", [(2, 7, 3), (4, 257, 8), (2, 1, 3), (3, 5000, 40), (8, 1024, 128)])
+# (1, 3000, 24): more than 16 super-chunks (cooperative carry kernel); (16, 2048, 512): 32-step
+# forward chunks
+@pytest.mark.parametrize(
+    "shape", [(2, 7, 3), (4, 257, 8), (2, 1, 3), (3, 5000, 40), (8, 1024, 128), (1, 3000, 24), (16, 2048, 512)]
+)
 @pytest.mark.parametrize("with_x0", [True, False])
 def test_selective_matches_oracle(gpu, shape, with_x0):
     g = torch.Generator().manual_seed(sum(shape))

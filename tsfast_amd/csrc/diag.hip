@@ -10,9 +10,9 @@
 // state first, then a re-scan of every chunk from its true start state, the carries composed in
 // fp64 (complex128). Consecutive threads own consecutive lanes, so every per-step load/store is a
 // coalesced row segment along N; the re-read of the input in pass 2 is the price of needing no
-// global barrier. The constant-coefficient kernels keep a chunk in registers and combine chunk
-// summaries inside a workgroup through LDS (tiling described at those kernels); the time-varying
-// kernels run one thread per (lane, time chunk).
+// global barrier. Both keep a chunk in registers and combine chunk summaries inside a workgroup
+// through LDS (tiling described at the constant-coefficient kernels); the time-varying kernels
+// carry (product of coefficients, state) affine maps where the constant ones carry states.
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -359,124 +359,285 @@ __global__ void __launch_bounds__(256) zero_fill(float* __restrict__ p, int64_t 
 
 
 // ---------------------------------------------------------------- time-varying coefficient (real)
-// Pass-1 summary of a forward chunk: (product of its coefficients, end state from zero).
-__global__ void __launch_bounds__(256) sel_fwd_chunk_end(const float* __restrict__ a, const float* __restrict__ v,
-                                                         double2* __restrict__ carry, int64_t M, int64_t L, int64_t N,
-                                                         int64_t T_c, int64_t nchunk) {
-  const int64_t lanes = M * N;
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes;
-  const int64_t c = gid / lanes;
-  if (c >= nchunk - 1) return;
-  const int64_t m = lane / N, n = lane % N;
-  const int64_t off = (m * L + c * T_c) * N + n;
-  double P = 1.0, x = 0.0;
-#pragma unroll 8
-  for (int64_t i = 0; i < T_c; ++i) {
-    const double at = a[off + i * N];
-    x = fma(at, x, (double)v[off + i * N]);
-    P *= at;
-  }
-  carry[c * lanes + lane] = make_double2(P, x);
+// Same tiling as the constant-coefficient kernels; a chunk's summary is the affine map
+// s -> P s + e with P the product of its coefficients, stored as double2 (P, e), composed in
+// LDS across the K chunks of a super-chunk and through HBM across super-chunks.
+TSF_DEV double2 compose(double2 first, double2 then) {  // apply `first`, then `then`
+  return make_double2(then.x * first.x, fma(then.x, first.y, then.y));
 }
 
-__global__ void __launch_bounds__(256) sel_fwd_apply(const float* __restrict__ a, const float* __restrict__ v,
-                                                     const float* __restrict__ x0, const double2* __restrict__ carry,
-                                                     float* __restrict__ out, int64_t M, int64_t L, int64_t N,
-                                                     int64_t T_c, int64_t nchunk) {
-  const int64_t lanes = M * N;
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes;
-  const int64_t c = gid / lanes;
-  if (c >= nchunk) return;
-  const int64_t m = lane / N, n = lane % N;
-  double x = x0 ? (double)x0[lane] : 0.0;
-  for (int64_t j = 0; j < c; ++j) {
-    const double2 pe = carry[j * lanes + lane];
-    x = fma(pe.x, x, pe.y);
-  }
-  const int64_t t0 = c * T_c;
-  const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
-  const int64_t off = (m * L + t0) * N + n;
-#pragma unroll 8
-  for (int64_t i = 0; i < len; ++i) {
-    x = fma((double)a[off + i * N], x, (double)v[off + i * N]);
-    out[off + i * N] = (float)x;
-  }
-}
-
-// Reverse summary of chunk c >= 1: G at its first step with zero entering gradient, and the
-// multiplier of the entering gradient, prod_{s=t0+1..t1} a_s (a_{t1} is the next chunk's first
-// coefficient; the last chunk has no entering gradient, so its multiplier is never used).
-__global__ void __launch_bounds__(256) sel_bwd_chunk_start(const float* __restrict__ a, const float* __restrict__ g,
-                                                           double2* __restrict__ carry, int64_t M, int64_t L,
-                                                           int64_t N, int64_t T_c, int64_t nchunk) {
-  const int64_t lanes = M * N;
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes;
-  const int64_t c = gid / lanes + 1;
-  if (c >= nchunk) return;
-  const int64_t m = lane / N, n = lane % N;
-  const int64_t t0 = c * T_c;
-  const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
-  const int64_t off = (m * L + t0) * N + n;
-  double G = 0.0, P = 1.0;
-  for (int64_t i = len - 1; i >= 0; --i) {
-    // G_t = g_t + a_{t+1} G_{t+1}; inside the chunk a_{t+1} is at i+1
-    const double an = (i + 1 < len) ? (double)a[off + (i + 1) * N] : 1.0;
-    G = fma(an, G, (double)g[off + i * N]);
-    P *= an;
-  }
-  // the entering gradient passes through a_{t1}, the next chunk's first coefficient
-  if (t0 + len < L) P *= a[off + len * N];
-  carry[c * lanes + lane] = make_double2(P, G);
-}
-
-__global__ void __launch_bounds__(256) sel_bwd_apply(const float* __restrict__ a, const float* __restrict__ g,
-                                                     const float* __restrict__ out, const float* __restrict__ x0,
-                                                     const double2* __restrict__ carry, float* __restrict__ glam,
-                                                     float* __restrict__ gv, float* __restrict__ gx0, int64_t M,
-                                                     int64_t L, int64_t N, int64_t T_c, int64_t nchunk) {
-  const int64_t lanes = M * N;
-  const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  const int64_t lane = gid % lanes;
-  const int64_t c = gid / lanes;
-  if (c >= nchunk) return;
-  const int64_t m = lane / N, n = lane % N;
-  // G_{t1} (first step of chunk c+1), folded from the right end
-  double R = 0.0;
-  if (c + 1 < nchunk) {
-    R = carry[(nchunk - 1) * lanes + lane].y;
-    for (int64_t j = nchunk - 2; j > c; --j) {
-      const double2 pe = carry[j * lanes + lane];
-      // pe.x multiplies G at the first step of chunk j+1
-      R = fma(pe.x, R, pe.y);
+template <int TC>
+__global__ void __launch_bounds__(1024) sel_fwd_summary(const float* __restrict__ a, const float* __restrict__ v,
+                                                        double2* __restrict__ E, int64_t lanes, int64_t L, int64_t N,
+                                                        int64_t groups, int K) {
+  __shared__ double2 s_e[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t g = blockIdx.x % groups, sc = blockIdx.x / groups;  // super-chunks 0 .. nsuper-2
+  const int64_t lane = g * 64 + lid;
+  const bool live = lane < lanes;
+  double P = 1.0, e = 0.0;
+  if (live) {
+    const int64_t m = lane / N, n = lane - m * N;
+    const int64_t base = (m * L + sc * K * TC + (int64_t)k * TC) * N + n;  // full chunks only
+    float ab[TC], vb[TC];
+#pragma unroll
+    for (int i = 0; i < TC; ++i) {
+      ab[i] = a[base + i * N];
+      vb[i] = v[base + i * N];
+    }
+#pragma unroll
+    for (int i = 0; i < TC; ++i) {
+      e = fma((double)ab[i], e, (double)vb[i]);
+      P *= (double)ab[i];
     }
   }
-  const int64_t t0 = c * T_c;
-  const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
-  const int64_t off = (m * L + t0) * N + n;
-  double G = R;
-  for (int64_t i = len - 1; i >= 0; --i) {
-    const int64_t t = t0 + i;
-    const double an = (t + 1 < L) ? (double)a[off + (i + 1) * N] : 1.0;
-    G = fma(an, G, (double)g[off + i * N]);
-    gv[off + i * N] = (float)G;
-    const double xprev = (t > 0) ? (double)out[off + (i - 1) * N] : (x0 ? (double)x0[lane] : 0.0);
-    glam[off + i * N] = (float)(G * xprev);
+  s_e[k][lid] = make_double2(P, e);
+  __syncthreads();
+  if (k == 0 && live) {
+    double2 s = s_e[0][lid];
+    for (int j = 1; j < K; ++j) s = compose(s, s_e[j][lid]);
+    E[sc * lanes + lane] = s;
   }
-  if (c == 0 && gx0) gx0[lane] = (float)((double)a[off] * G);
 }
 
-// Chunk length: enough (lane, chunk) threads to cover the device several times over, but
-// chunks long enough that the carry fold (O(nchunk) per thread) stays negligible.
-int64_t pick_chunk(int64_t lanes, int64_t L) {
-  if (L < 1) return 1;
-  const int64_t target_threads = 256 * 1024 * 2;  // ~8 waves of 64 per SIMD on 256 CUs
-  int64_t T_c = L;
-  while (T_c > 64 && lanes * ((L + T_c - 1) / T_c) < target_threads) T_c = (T_c + 1) / 2;
-  if (T_c < 1) T_c = 1;
-  return T_c;
+// In-place inclusive scan of n affine maps per lane: state_r = P_r state_{r-1} + e_r from
+// init (NULL: zero); the state replaces e_r. Map r of a lane sits at S[(first + dir*r) * lanes
+// + lane]. One workgroup per 64-lane group; wave k composes the k-th of 16 contiguous segments.
+__global__ void __launch_bounds__(1024) sel_carry(const float* __restrict__ init, double2* __restrict__ S,
+                                                  int64_t lanes, int64_t n, int64_t first, int64_t dir) {
+  __shared__ double2 s_p[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t lane = blockIdx.x * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t seg = (n + kMaxWaves - 1) / kMaxWaves;
+  const int64_t r0 = k * seg, r1 = (r0 + seg < n) ? r0 + seg : n;
+  double2 p = make_double2(1.0, 0.0);
+  if (live) {
+#pragma unroll 8
+    for (int64_t r = r0; r < r1; ++r) p = compose(p, S[(first + dir * r) * lanes + lane]);
+  }
+  s_p[k][lid] = p;
+  __syncthreads();
+  if (live && r0 < r1) {
+    double s = init ? (double)init[lane] : 0.0;
+    for (int j = 0; j < k; ++j) s = fma(s_p[j][lid].x, s, s_p[j][lid].y);
+#pragma unroll 8
+    for (int64_t r = r0; r < r1; ++r) {
+      double2* q = S + (first + dir * r) * lanes + lane;
+      const double2 m = *q;
+      s = fma(m.x, s, m.y);
+      q->y = s;
+    }
+  }
+}
+
+template <int TC>
+__global__ void __launch_bounds__(1024) sel_fwd_apply(const float* __restrict__ a, const float* __restrict__ v,
+                                                      const float* __restrict__ x0, const double2* __restrict__ E,
+                                                      float* __restrict__ out, int64_t lanes, int64_t L, int64_t N,
+                                                      int64_t groups, int K, int starts_ready) {
+  __shared__ double2 s_e[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t g = blockIdx.x % groups, sc = blockIdx.x / groups;
+  const int64_t lane = g * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t t0 = sc * K * TC + (int64_t)k * TC;
+  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+  double P = 1.0, e = 0.0;
+  float ab[TC], vb[TC];
+  int64_t base = 0;
+  if (live) {
+    const int64_t m = lane / N, n = lane - m * N;
+    base = (m * L + t0) * N + n;
+    if (len == TC) {  // full chunk: every load issued before the arithmetic, no per-step guard
+#pragma unroll
+      for (int i = 0; i < TC; ++i) {
+        ab[i] = a[base + i * N];
+        vb[i] = v[base + i * N];
+      }
+#pragma unroll
+      for (int i = 0; i < TC; ++i) {
+        e = fma((double)ab[i], e, (double)vb[i]);
+        P *= (double)ab[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TC; ++i) {
+        ab[i] = i < len ? a[base + i * N] : 1.0f;
+        vb[i] = i < len ? v[base + i * N] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < TC; ++i)
+        if (i < len) {
+          e = fma((double)ab[i], e, (double)vb[i]);
+          P *= (double)ab[i];
+        }
+    }
+  }
+  s_e[k][lid] = make_double2(P, e);
+  __syncthreads();
+  if (!live || len == 0) return;  // no barrier follows
+  double s = x0 ? (double)x0[lane] : 0.0;
+  if (sc > 0) {
+    if (starts_ready) {
+      s = E[(sc - 1) * lanes + lane].y;
+    } else {
+#pragma unroll 8
+      for (int64_t j = 0; j < sc; ++j) {
+        const double2 mp = E[j * lanes + lane];
+        s = fma(mp.x, s, mp.y);
+      }
+    }
+  }
+  for (int j = 0; j < k; ++j) s = fma(s_e[j][lid].x, s, s_e[j][lid].y);
+  if (len == TC) {
+#pragma unroll
+    for (int i = 0; i < TC; ++i) {
+      s = fma((double)ab[i], s, (double)vb[i]);
+      out[base + i * N] = (float)s;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TC; ++i)
+      if (i < len) {
+        s = fma((double)ab[i], s, (double)vb[i]);
+        out[base + i * N] = (float)s;
+      }
+  }
+}
+
+// Reverse summary of super-chunk sc >= 1: the map G_enter -> G at its first step,
+// G_t = g_t + a_{t+1} G_{t+1}, as (multiplier, value) with the multiplier the product of
+// a_{t0+1} .. a_{t1} (a_{t1} is the next super-chunk's first coefficient). F [nsuper, lanes].
+template <int TC>
+__global__ void __launch_bounds__(1024) sel_bwd_summary(const float* __restrict__ a, const float* __restrict__ g,
+                                                        double2* __restrict__ F, int64_t lanes, int64_t L, int64_t N,
+                                                        int64_t groups, int K) {
+  __shared__ double2 s_f[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t gr = blockIdx.x % groups, sc = blockIdx.x / groups + 1;  // super-chunks 1 .. nsuper-1
+  const int64_t lane = gr * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t t0 = sc * K * TC + (int64_t)k * TC;
+  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+  double M = 1.0, f = 0.0;
+  if (live && len > 0) {
+    const int64_t m = lane / N, n = lane - m * N;
+    const int64_t base = (m * L + t0) * N + n;
+    float gb[TC], an[TC];  // g_t and a_{t+1} of the chunk's steps (a_L taken as 0: nothing enters)
+    if (len == TC && t0 + TC < L) {  // full chunk with a following step: no per-step guard
+#pragma unroll
+      for (int i = 0; i < TC; ++i) {
+        gb[i] = g[base + i * N];
+        an[i] = a[base + (i + 1) * N];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TC; ++i) {
+        gb[i] = i < len ? g[base + i * N] : 0.0f;
+        an[i] = (i < len && t0 + i + 1 < L) ? a[base + (i + 1) * N] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = TC - 1; i >= 0; --i)
+      if (i < len) {
+        f = fma((double)an[i], f, (double)gb[i]);
+        M *= (double)an[i];
+      }
+  }
+  s_f[k][lid] = make_double2(M, f);
+  __syncthreads();
+  if (k == 0 && live) {
+    double2 s = s_f[K - 1][lid];
+    for (int j = K - 2; j >= 0; --j) s = compose(s, s_f[j][lid]);
+    F[sc * lanes + lane] = s;
+  }
+}
+
+template <int TC>
+__global__ void __launch_bounds__(1024) sel_bwd_apply(const float* __restrict__ a, const float* __restrict__ g,
+                                                      const float* __restrict__ out, const float* __restrict__ x0,
+                                                      const double2* __restrict__ F, float* __restrict__ glam,
+                                                      float* __restrict__ gv, float* __restrict__ gx0, int64_t lanes,
+                                                      int64_t L, int64_t N, int64_t groups, int K, int64_t nsuper,
+                                                      int starts_ready) {
+  __shared__ double2 s_f[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t gr = blockIdx.x % groups, sc = blockIdx.x / groups;
+  const int64_t lane = gr * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t t0 = sc * K * TC + (int64_t)k * TC;
+  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+  double M = 1.0, f = 0.0;
+  float gb[TC], an[TC], xb[TC];  // g_t, a_{t+1}, x_{t-1}
+  int64_t base = 0;
+  if (live && len > 0) {
+    const int64_t m = lane / N, n = lane - m * N;
+    base = (m * L + t0) * N + n;
+    const float xinit = x0 ? x0[lane] : 0.0f;  // x_{-1}
+    if (len == TC && t0 > 0 && t0 + TC < L) {  // interior full chunk: no per-step guard
+#pragma unroll
+      for (int i = 0; i < TC; ++i) {
+        gb[i] = g[base + i * N];
+        an[i] = a[base + (i + 1) * N];
+        xb[i] = out[base + (i - 1) * N];
+      }
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i) {
+        f = fma((double)an[i], f, (double)gb[i]);
+        M *= (double)an[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TC; ++i) {
+        gb[i] = i < len ? g[base + i * N] : 0.0f;
+        an[i] = (i < len && t0 + i + 1 < L) ? a[base + (i + 1) * N] : 0.0f;
+        xb[i] = i >= len ? 0.0f : (t0 + i > 0) ? out[base + (i - 1) * N] : xinit;
+      }
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i)
+        if (i < len) {
+          f = fma((double)an[i], f, (double)gb[i]);
+          M *= (double)an[i];
+        }
+    }
+  }
+  s_f[k][lid] = make_double2(M, f);
+  __syncthreads();
+  if (!live || len == 0) return;  // no barrier follows
+  // G entering the super-chunk from the right: G at the first step of super-chunk sc + 1
+  double R = 0.0;
+  if (sc + 1 < nsuper) {
+    if (starts_ready) {
+      R = F[(sc + 1) * lanes + lane].y;
+    } else {
+      R = F[(nsuper - 1) * lanes + lane].y;
+#pragma unroll 8
+      for (int64_t j = nsuper - 2; j > sc; --j) {
+        const double2 mp = F[j * lanes + lane];
+        R = fma(mp.x, R, mp.y);
+      }
+    }
+  }
+  for (int j = K - 1; j > k; --j) R = fma(s_f[j][lid].x, R, s_f[j][lid].y);
+  double G = R;
+  if (len == TC) {
+#pragma unroll
+    for (int i = TC - 1; i >= 0; --i) {
+      G = fma((double)an[i], G, (double)gb[i]);
+      gv[base + i * N] = (float)G;
+      glam[base + i * N] = (float)(G * (double)xb[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = TC - 1; i >= 0; --i)
+      if (i < len) {
+        G = fma((double)an[i], G, (double)gb[i]);
+        gv[base + i * N] = (float)G;
+        glam[base + i * N] = (float)(G * (double)xb[i]);
+      }
+  }
+  if (t0 == 0 && gx0) gx0[lane] = (float)((double)a[base] * G);
 }
 
 inline dim3 grid_for(int64_t threads) { return dim3((unsigned)((threads + 255) / 256)); }
@@ -509,13 +670,13 @@ struct DiagTile {
   bool carry_kernel = false;
 };
 
-DiagTile diag_tile(int64_t lanes, int64_t L, bool cplx) {
+DiagTile diag_tile(int64_t lanes, int64_t L, bool cplx, int kmax = kMaxWaves) {
   DiagTile t;
   t.lanes = lanes;
   if (lanes < 1 || L < 1) return t;
   t.groups = (lanes + 63) / 64;
   t.TC = (cplx || t.groups * ((L + 31) / 32) < kDiagWaveTarget) ? 16 : 32;
-  t.K = kMaxWaves;
+  t.K = kmax;
   auto wgs = [&](int K) { return t.groups * ((L + (int64_t)t.TC * K - 1) / ((int64_t)t.TC * K)); };
   while (t.K > 4 && wgs(t.K) < kDiagWgTarget) t.K /= 2;
   const int64_t chunks = (L + t.TC - 1) / t.TC;
@@ -560,6 +721,39 @@ void diag_bwd_launch(const DiagTile& t, const T* g, const T* lam, const T* out, 
   if (t.nsuper > 1)
     hipLaunchKernelGGL(diag_sum_parts<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s,
                        (const typename Wide<T>::type*)part, glam, t.lanes, t.nsuper);
+}
+
+// The time-varying kernels use the same tiles; the backward keeps three TC-step arrays per
+// thread (g_t, a_{t+1}, x_{t-1}), so it always runs TC = 16.
+DiagTile sel_tile(int64_t lanes, int64_t L, bool bwd) { return diag_tile(lanes, L, bwd); }
+
+template <int TC>
+void sel_fwd_launch(const DiagTile& t, const float* a, const float* v, const float* x0, float* out, double2* E,
+                    int64_t L, int64_t N, hipStream_t s) {
+  const dim3 blk(64 * t.K);
+  if (t.nsuper > 1) {
+    hipLaunchKernelGGL((sel_fwd_summary<TC>), dim3((unsigned)(t.groups * (t.nsuper - 1))), blk, 0, s, a, v, E,
+                       t.lanes, L, N, t.groups, t.K);
+    if (t.carry_kernel)
+      hipLaunchKernelGGL(sel_carry, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, x0, E, t.lanes,
+                         t.nsuper - 1, (int64_t)0, (int64_t)1);
+  }
+  hipLaunchKernelGGL((sel_fwd_apply<TC>), dim3((unsigned)(t.groups * t.nsuper)), blk, 0, s, a, v, x0,
+                     (const double2*)E, out, t.lanes, L, N, t.groups, t.K, (int)t.carry_kernel);
+}
+
+void sel_bwd_launch(const DiagTile& t, const float* g, const float* a, const float* out, const float* x0, float* glam,
+                    float* gv, float* gx0, double2* F, int64_t L, int64_t N, hipStream_t s) {
+  const dim3 blk(64 * t.K);
+  if (t.nsuper > 1) {
+    hipLaunchKernelGGL((sel_bwd_summary<16>), dim3((unsigned)(t.groups * (t.nsuper - 1))), blk, 0, s, a, g, F,
+                       t.lanes, L, N, t.groups, t.K);
+    if (t.carry_kernel)
+      hipLaunchKernelGGL(sel_carry, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, (const float*)nullptr, F,
+                         t.lanes, t.nsuper - 1, t.nsuper - 1, (int64_t)-1);
+  }
+  hipLaunchKernelGGL((sel_bwd_apply<16>), dim3((unsigned)(t.groups * t.nsuper)), blk, 0, s, a, g, out, x0,
+                     (const double2*)F, glam, gv, gx0, t.lanes, L, N, t.groups, t.K, t.nsuper, (int)t.carry_kernel);
 }
 
 }  // namespace
@@ -630,10 +824,9 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
 }
 
 int64_t tsfast_hip_sel_workspace_bytes(int64_t M, int64_t L, int64_t N) {
-  const int64_t lanes = M * N;
-  const int64_t T_c = pick_chunk(lanes, L);
-  const int64_t nchunk = (L + T_c - 1) / T_c;
-  return nchunk * lanes * 16;  // fp64 (product, state) pairs
+  // fp64 (product, state) maps [nsuper, lanes] for the larger of the forward / backward tilings
+  const DiagTile f = sel_tile(M * N, L, false), b = sel_tile(M * N, L, true);
+  return (f.nsuper > b.nsuper ? f.nsuper : b.nsuper) * M * N * 16;
 }
 
 int tsfast_hip_sel_fwd(int64_t M, int64_t L, int64_t N, const float* a, const float* v, const float* x0, float* out,
@@ -642,15 +835,14 @@ int tsfast_hip_sel_fwd(int64_t M, int64_t L, int64_t N, const float* a, const fl
   if (M == 0 || L == 0 || N == 0) return TSF_OK;
   if (!a || !v || !out) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_sel_workspace_bytes(M, L, N) || !workspace) return TSF_ERR_WORKSPACE;
+  const DiagTile t = sel_tile(M * N, L, false);
+  if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t lanes = M * N;
-  const int64_t T_c = pick_chunk(lanes, L);
-  const int64_t nchunk = (L + T_c - 1) / T_c;
-  auto* c = static_cast<double2*>(workspace);
-  if (nchunk > 1)
-    hipLaunchKernelGGL(sel_fwd_chunk_end, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s, a, v, c, M, L, N, T_c,
-                       nchunk);
-  hipLaunchKernelGGL(sel_fwd_apply, grid_for(lanes * nchunk), dim3(256), 0, s, a, v, x0, c, out, M, L, N, T_c, nchunk);
+  auto* E = static_cast<double2*>(workspace);
+  if (t.TC == 32)
+    sel_fwd_launch<32>(t, a, v, x0, out, E, L, N, s);
+  else
+    sel_fwd_launch<16>(t, a, v, x0, out, E, L, N, s);
   return tsf_launch_status();
 }
 
@@ -668,14 +860,9 @@ int tsfast_hip_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const fl
   }
   if (!g || !a || !out || !gv || !glam) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_sel_workspace_bytes(M, L, N) || !workspace) return TSF_ERR_WORKSPACE;
-  const int64_t T_c = pick_chunk(lanes, L);
-  const int64_t nchunk = (L + T_c - 1) / T_c;
-  auto* c = static_cast<double2*>(workspace);
-  if (nchunk > 1)
-    hipLaunchKernelGGL(sel_bwd_chunk_start, grid_for(lanes * (nchunk - 1)), dim3(256), 0, s, a, g, c, M, L, N, T_c,
-                       nchunk);
-  hipLaunchKernelGGL(sel_bwd_apply, grid_for(lanes * nchunk), dim3(256), 0, s, a, g, out, x0, c, glam, gv, gx0, M, L,
-                     N, T_c, nchunk);
+  const DiagTile t = sel_tile(lanes, L, true);
+  if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
+  sel_bwd_launch(t, g, a, out, x0, glam, gv, gx0, static_cast<double2*>(workspace), L, N, s);
   return tsf_launch_status();
 }
 
