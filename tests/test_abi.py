@@ -43,7 +43,10 @@ def test_status_strings(lib):
 
 def test_size_queries(lib):
     assert lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 0) > 0
-    assert lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 1) == 2 * lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 0)
+    # a 256-byte tile counter, then 4 words per lane and super-chunk (complex: 16-byte words)
+    real, cplx = (lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, c) for c in (0, 1))
+    assert (real - 256) % (32 * 64 * 4 * 8) == 0 and (cplx - 256) % (32 * 64 * 4 * 16) == 0
+    assert (lib.tsfast_hip_sel_workspace_bytes(4, 300, 40) - 256) % (4 * 40 * 24) == 0
     assert lib.tsfast_hip_mamba_chk_interval(16) >= 1
     k = lib.tsfast_hip_mamba_chk_interval(16)
     # per batch row: fp32 checkpoints [ceil(L/k), N, D], then y [L, D] in the I/O type

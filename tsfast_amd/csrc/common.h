@@ -203,6 +203,19 @@ TSF_DEV void wave_reduce_scatter(float* v, int lane) {
   }
 }
 
+// Compute units of the current device (queried once per device).
+inline unsigned device_cus() {
+  static unsigned cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = (unsigned)n;
+  }
+  return cache[dev];
+}
+
 }  // namespace tsf
 
 // Host side: status of the launches just enqueued (records the HIP error for the status string).

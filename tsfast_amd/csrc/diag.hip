@@ -6,13 +6,15 @@
 // Reference semantics: tsfast/models/_core/scan.py:100-215 (ops), :52-80 (doubling scans),
 // scan_backends/diagonal_triton.py:82-228 and selective_triton.py:48-109 (kernels).
 //
-// Both are chunked two-pass scans with no inter-workgroup waiting: chunk summaries from a zero
-// state first, then a re-scan of every chunk from its true start state, the carries composed in
-// fp64 (complex128). Consecutive threads own consecutive lanes, so every per-step load/store is a
-// coalesced row segment along N; the re-read of the input in pass 2 is the price of needing no
-// global barrier. Both keep a chunk in registers and combine chunk summaries inside a workgroup
-// through LDS (tiling described at the constant-coefficient kernels); the time-varying kernels
-// carry (product of coefficients, state) affine maps where the constant ones carry states.
+// Both are single-pass scans with decoupled look-back: every input element is read once and every
+// output element written once. A tile (one workgroup of K waves) covers 64 consecutive lanes by
+// one super-chunk of K * TC consecutive steps; consecutive threads own consecutive lanes, so
+// every per-step load/store of a wave is one coalesced row segment along N, and each wave keeps
+// its TC-step chunk in registers. A tile summarises its chunks from a zero state, composes the
+// summaries in LDS into its super-chunk's affine map, publishes that map, obtains the state
+// entering the super-chunk from the tiles before it (look-back), publishes the state leaving
+// it, and re-runs its chunks from registers. Carries are fp64 (complex128). Workgroups are
+// persistent and take tiles in scan order from a counter.
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -21,306 +23,431 @@ using namespace tsf;
 namespace {
 
 // All kernels load fp32 (or complex64) and carry the recurrence in fp64 (complex128): W below.
-
-// ---------------------------------------------------------------- constant coefficient
-// Tiling. A workgroup of K waves (K <= 16) owns 64 consecutive lanes (thread lid of every wave
-// owns lane group * 64 + lid) and one super-chunk of K * TC consecutive steps; wave k owns the
-// k-th chunk of TC steps. A thread keeps its chunk's TC inputs in registers, scans them from a
-// zero state, the K chunk summaries meet in LDS, and the thread re-runs its chunk from its true
-// start state. Super-chunk summaries (one per lane and super-chunk) go through HBM:
-//   summary  end state of every super-chunk but the last from a zero start, E [nsuper, lanes]
-//   carry    (long sequences only) in-place scan of E into true super-chunk start states
-//   apply    fold of E before the super-chunk (or the carried start), then the chunk scan.
-// The backward mirrors this from the right end with conj(lam), and reduces the glam partials of
-// the K chunks in LDS and of the super-chunks in a fixed-order sum (deterministic).
 constexpr int kMaxWaves = 16;
 
+// ---------------------------------------------------------------- affine maps and look-back
+template <typename W>
+struct Map {  // x -> P x + e
+  W P, e;
+};
+template <typename W>
+TSF_DEV Map<W> then(Map<W> first, Map<W> second) {  // apply `first`, then `second`
+  return {Num<W>::mul(second.P, first.P), Num<W>::fma(second.P, first.e, second.e)};
+}
+template <typename W>
+TSF_DEV W apply(Map<W> m, W x) {
+  return Num<W>::fma(m.P, x, m.e);
+}
+
+// Published words start as kUnset, a signalling NaN: arithmetic results and float -> double
+// conversions are never signalling NaNs, so a word that differs from kUnset has been written.
+// Each 8-byte word is stored and polled with agent-scope atomics (coherent across the L2s of
+// the XCDs) and validated on its own, so no fence has to order data against a flag.
+constexpr uint64_t kUnset = 0x7FF00000DEADBEEFull;
+// Polls without progress before a look-back gives up and yields NaN (about a second): every
+// wait ends even if an invariant below were broken, and the NaN shows in the outputs.
+constexpr uint32_t kSpinMax = 1u << 20;
+constexpr int kWindow = kMaxWaves;  // look-back slots examined per round
+
+TSF_DEV void put_word(double* p, double x) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), static_cast<uint64_t>(__double_as_longlong(x)), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+TSF_DEV bool get_word(const double* p, double& x) {
+  const uint64_t b = __hip_atomic_load(const_cast<uint64_t*>(reinterpret_cast<const uint64_t*>(p)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  x = __longlong_as_double(static_cast<long long>(b));
+  return b != kUnset;
+}
+TSF_DEV void put(double* p, double x) { put_word(p, x); }
+TSF_DEV void put(double2* p, double2 x) {
+  put_word(&p->x, x.x);
+  put_word(&p->y, x.y);
+}
+TSF_DEV bool get(const double* p, double& x) { return get_word(p, x); }
+TSF_DEV bool get(const double2* p, double2& x) {
+  const bool a = get_word(&p->x, x.x);
+  const bool b = get_word(&p->y, x.y);
+  return a && b;
+}
+template <typename W>
+TSF_DEV void put(Map<W>* p, Map<W> m) {
+  put(&p->P, m.P);
+  put(&p->e, m.e);
+}
+template <typename W>
+TSF_DEV bool get(const Map<W>* p, Map<W>& m) {
+  const bool a = get(&p->P, m.P);
+  const bool b = get(&p->e, m.e);
+  return a && b;
+}
+
+template <typename W>
+TSF_DEV W quiet_nan();
+template <>
+TSF_DEV double quiet_nan<double>() {
+  return __longlong_as_double(0x7FF8000000000000ll);
+}
+template <>
+TSF_DEV double2 quiet_nan<double2>() {
+  return make_double2(quiet_nan<double>(), quiet_nan<double>());
+}
+
+// State entering a tile, found by looking back over the tiles before it in scan order. Called
+// by every thread of the workgroup (it holds barriers) with a workgroup-uniform decision to call
+// it; `need` marks the lanes (of wave 0) that look back, starting at super-chunk `pos0` and
+// stepping by dj; slot r of a lane is at r * lanes + lane. Wave 0 first probes slot pos0 alone.
+// Lanes that are still pending then go through rounds: the K waves read the kWindow slots pos,
+// pos + dj, ... of every pending lane (inc and agg words together; slot w by wave w mod K) into
+// LDS, and wave 0 walks the window in order. A published inc (state leaving that tile) ends the
+// lane's walk, a published agg (that tile's map from a zero start) is composed and the walk
+// moves on, an unpublished slot ends the round (the next round starts there). The walk always
+// ends: the first tile in scan order publishes its inc without looking back, and every tile
+// waited on was taken from the counter earlier by a workgroup that is running; a lane that
+// makes no progress for kSpinMax rounds gives up with NaN. Returns the entering state in wave
+// 0's lanes. LDS: win/flag [kWindow][64], pos [64] and one flag word, owned by the caller.
+template <typename W>
+TSF_DEV W look_back(const Map<W>* __restrict__ agg, const W* __restrict__ inc, bool need, int64_t pos0, int64_t dj,
+                    int64_t nsuper, int64_t lanes, int64_t lane, int K, int k, int lid, Map<W> (*win)[64],
+                    int (*flag)[64], int64_t* pos_s, int* any_s) {
+  Map<W> acc = {Num<W>::one(), Num<W>::zero()};  // composition of the aggregates walked over
+  W result = Num<W>::zero();
+  uint32_t spins = 0;
+  if (k == 0) {
+    // direct probe of the nearest tile by wave 0: in the steady state of a long scan its inc is
+    // already published, and the window rounds below are skipped
+    int64_t p = -1;
+    if (need) {
+      W x;
+      Map<W> m;
+      const bool have_inc = get(inc + pos0 * lanes + lane, x);
+      const bool have_agg = get(agg + pos0 * lanes + lane, m);
+      if (have_inc) {
+        result = x;
+      } else if (have_agg) {  // never the first tile in scan order, which publishes no agg
+        acc = m;
+        p = pos0 + dj;
+      } else {
+        p = pos0;
+      }
+    }
+    pos_s[lid] = p;
+    const bool any = __any(p >= 0);
+    if (lid == 0) *any_s = any ? 1 : 0;
+  }
+  __syncthreads();
+  while (*any_s) {
+    const int64_t pos = pos_s[lid];
+    if (pos >= 0) {
+      for (int w = k; w < kWindow; w += K) {
+        const int64_t r = pos + dj * w;
+        int f = 0;
+        Map<W> m = {Num<W>::zero(), Num<W>::zero()};
+        if (r >= 0 && r < nsuper) {
+          W x;
+          const bool have_inc = get(inc + r * lanes + lane, x);
+          const bool have_agg = get(agg + r * lanes + lane, m);
+          if (have_inc) {
+            f = 2;
+            m.e = x;
+          } else if (have_agg) {
+            f = 1;
+          }
+        }
+        flag[w][lid] = f;
+        win[w][lid] = m;
+      }
+    }
+    __syncthreads();
+    if (k == 0) {
+      bool pending = false;
+      if (pos >= 0) {
+        int64_t p = pos;
+        int w = 0;
+        for (; w < kWindow; ++w) {
+          const int f = flag[w][lid];
+          if (f == 2) {
+            result = apply(acc, win[w][lid].e);
+            p = -1;
+            break;
+          }
+          if (f != 1) break;
+          acc = then(win[w][lid], acc);
+          p += dj;
+        }
+        if (p >= 0 && w == 0 && ++spins > kSpinMax) {
+          result = quiet_nan<W>();
+          p = -1;
+        }
+        pending = p >= 0;
+        pos_s[lid] = p;
+      }
+      const bool any = __any(pending);
+      if (lid == 0) *any_s = any ? 1 : 0;
+    }
+    __syncthreads();
+  }
+  return result;
+}
+
+TSF_DEV unsigned take_tile(unsigned* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Resets the look-back words to kUnset and the tile counter to zero before every scan (a
+// kernel rather than a memset node, so that a captured graph replays it reliably).
+__global__ void __launch_bounds__(256) lookback_reset(uint64_t* __restrict__ words, int64_t n,
+                                                      unsigned* __restrict__ counter) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) words[i] = kUnset;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *counter = 0u;
+}
+
+// ---------------------------------------------------------------- constant coefficient
+// One tile = 64 lanes x one super-chunk of K * TC steps (K waves of TC-step chunks). Tile index
+// `tile` is super-chunk tile / groups (forward from the left, backward from the right) of lane
+// group tile % groups. Per tile: every wave loads its chunk (all loads issued at once) and
+// summarises it from a zero state; wave 0 composes the K summaries into the super-chunk's map,
+// publishes it, looks back for the state entering the super-chunk, publishes the state leaving
+// it and writes the state entering each chunk to LDS; every wave then re-runs its chunk from
+// registers. Each wave reads only its own slot of s_start after the second barrier, so the next
+// tile's first writes (before its first barrier) cannot race with a slower wave's reads.
 template <typename T, int TC>
-__global__ void __launch_bounds__(1024) diag_fwd_summary(const T* __restrict__ lam, const T* __restrict__ v,
-                                                         typename Wide<T>::type* __restrict__ E, int64_t lanes,
-                                                         int64_t L, int64_t N, int64_t groups, int K) {
+__global__ void __launch_bounds__(1024) diag_fwd(const T* __restrict__ lam, const T* __restrict__ v,
+                                                 const T* __restrict__ x0, T* __restrict__ out,
+                                                 Map<typename Wide<T>::type>* __restrict__ agg,
+                                                 typename Wide<T>::type* __restrict__ inc, unsigned* __restrict__ counter,
+                                                 int64_t lanes, int64_t L, int64_t N, int64_t groups, int K,
+                                                 int64_t nsuper) {
   using W = typename Wide<T>::type;
   __shared__ W s_e[kMaxWaves][64];
+  // the look-back window, then (once the look-back is done) the state entering each chunk
+  __shared__ Map<W> s_win[kMaxWaves][64];
+  __shared__ int s_flag[kMaxWaves][64];
+  __shared__ int64_t s_pos[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  W(*s_start)[64] = reinterpret_cast<W(*)[64]>(&s_win[0][0]);
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t g = blockIdx.x % groups, sc = blockIdx.x / groups;  // super-chunks 0 .. nsuper-2
-  const int64_t lane = g * 64 + lid;
-  const bool live = lane < lanes;
-  W a = Num<W>::zero(), e = Num<W>::zero();
-  if (live) {
-    a = Wide<T>::up(lam[lane]);
-    const int64_t m = lane / N, n = lane - m * N;
-    // every chunk of a super-chunk before the last is full
-    const T* vp = v + (m * L + sc * K * TC + (int64_t)k * TC) * N + n;
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * TC;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
+  __syncthreads();
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t sc = tile / groups, lane = (tile - sc * groups) * 64 + lid;
+    const bool live = lane < lanes;
+    const int64_t t0 = sc * SL + (int64_t)k * TC;
+    const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+    W a = Num<W>::zero(), e = Num<W>::zero();
     T vb[TC];
+    int64_t base = 0;
+    if (live) {
+      a = Wide<T>::up(lam[lane]);
+      const int64_t m = lane / N, n = lane - m * N;
+      base = (m * L + t0) * N + n;
+      const T* vp = v + base;
+      if (len == TC) {
 #pragma unroll
-    for (int i = 0; i < TC; ++i) vb[i] = vp[i * N];
+        for (int i = 0; i < TC; ++i) vb[i] = vp[i * N];
 #pragma unroll
-    for (int i = 0; i < TC; ++i) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
-  }
-  s_e[k][lid] = e;
-  __syncthreads();
-  if (k == 0 && live) {
-    const W P = ipow(a, TC);
-    W s = s_e[0][lid];
-    for (int j = 1; j < K; ++j) s = Num<W>::fma(P, s, s_e[j][lid]);
-    E[sc * lanes + lane] = s;
-  }
-}
-
-// In-place inclusive scan s_r = c * s_{r-1} + S[r] over n summaries per lane, with s_{-1} = init
-// (NULL: zero). Summary r of lane `lane` sits at S[(first + dir * r) * lanes + lane]; c is the
-// per-super-chunk multiplier lam^SL (conj(lam)^SL when `conjugate`). One workgroup per 64-lane
-// group; wave k scans the k-th of 16 contiguous segments, and the segment results meet in LDS.
-template <typename T>
-__global__ void __launch_bounds__(1024) diag_carry(const T* __restrict__ lam, const T* __restrict__ init,
-                                                   typename Wide<T>::type* __restrict__ S, int64_t lanes, int64_t n,
-                                                   int64_t first, int64_t dir, int64_t SL, int conjugate) {
-  using W = typename Wide<T>::type;
-  __shared__ W s_p[kMaxWaves][64];
-  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t lane = blockIdx.x * 64 + lid;
-  const bool live = lane < lanes;
-  const int64_t seg = (n + kMaxWaves - 1) / kMaxWaves;
-  const int64_t r0 = k * seg, r1 = (r0 + seg < n) ? r0 + seg : n;
-  W c = Num<W>::zero(), p = Num<W>::zero();
-  if (live) {
-    W a = Wide<T>::up(lam[lane]);
-    if (conjugate) a = Num<W>::conj(a);
-    c = ipow(a, SL);
-#pragma unroll 8
-    for (int64_t r = r0; r < r1; ++r) p = Num<W>::fma(c, p, S[(first + dir * r) * lanes + lane]);
-  }
-  s_p[k][lid] = p;
-  __syncthreads();
-  if (live && r0 < r1) {
-    W s = init ? Wide<T>::up(init[lane]) : Num<W>::zero();
-    const W cs = ipow(c, seg);  // every segment before a non-empty one is full
-    for (int j = 0; j < k; ++j) s = Num<W>::fma(cs, s, s_p[j][lid]);
-#pragma unroll 8
-    for (int64_t r = r0; r < r1; ++r) {
-      W* q = S + (first + dir * r) * lanes + lane;
-      s = Num<W>::fma(c, s, *q);
-      *q = s;
-    }
-  }
-}
-
-template <typename T, int TC>
-__global__ void __launch_bounds__(1024) diag_fwd_apply(const T* __restrict__ lam, const T* __restrict__ v,
-                                                       const T* __restrict__ x0,
-                                                       const typename Wide<T>::type* __restrict__ E,
-                                                       T* __restrict__ out, int64_t lanes, int64_t L, int64_t N,
-                                                       int64_t groups, int K, int starts_ready) {
-  using W = typename Wide<T>::type;
-  __shared__ W s_e[kMaxWaves][64];
-  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t g = blockIdx.x % groups, sc = blockIdx.x / groups;
-  const int64_t lane = g * 64 + lid;
-  const bool live = lane < lanes;
-  const int64_t SL = (int64_t)K * TC;
-  const int64_t t0 = sc * SL + (int64_t)k * TC;
-  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
-  W a = Num<W>::zero(), e = Num<W>::zero();
-  T vb[TC];
-  int64_t base = 0;
-  if (live) {
-    a = Wide<T>::up(lam[lane]);
-    const int64_t m = lane / N, n = lane - m * N;
-    base = (m * L + t0) * N + n;
-    const T* vp = v + base;
-    if (len == TC) {
+        for (int i = 0; i < TC; ++i) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
+      } else {
 #pragma unroll
-      for (int i = 0; i < TC; ++i) vb[i] = vp[i * N];
+        for (int i = 0; i < TC; ++i)
+          if (i < len) vb[i] = vp[i * N];
 #pragma unroll
-      for (int i = 0; i < TC; ++i) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
-    } else {
-#pragma unroll
-      for (int i = 0; i < TC; ++i)
-        if (i < len) vb[i] = vp[i * N];
-#pragma unroll
-      for (int i = 0; i < TC; ++i)
-        if (i < len) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
-    }
-  }
-  s_e[k][lid] = e;
-  __syncthreads();
-  if (!live || len == 0) return;  // no barrier follows
-  // state entering the super-chunk
-  W s = x0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
-  if (sc > 0) {
-    if (starts_ready) {
-      s = E[(sc - 1) * lanes + lane];
-    } else {
-      const W Q = ipow(a, SL);
-#pragma unroll 8
-      for (int64_t j = 0; j < sc; ++j) s = Num<W>::fma(Q, s, E[j * lanes + lane]);
-    }
-  }
-  // state entering chunk k
-  if (k > 0) {
-    const W P = ipow(a, TC);
-    for (int j = 0; j < k; ++j) s = Num<W>::fma(P, s, s_e[j][lid]);
-  }
-  T* op = out + base;
-  if (len == TC) {
-#pragma unroll
-    for (int i = 0; i < TC; ++i) {
-      s = Num<W>::fma(a, s, Wide<T>::up(vb[i]));
-      op[i * N] = Wide<T>::down(s);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < TC; ++i)
-      if (i < len) {
-        s = Num<W>::fma(a, s, Wide<T>::up(vb[i]));
-        op[i * N] = Wide<T>::down(s);
+        for (int i = 0; i < TC; ++i)
+          if (i < len) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
       }
+    }
+    s_e[k][lid] = e;
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    // chunks before a non-empty one are full, so lam^TC is every fold's multiplier; the
+    // super-chunk map is published only for full super-chunks (all but the last)
+    const W Pc = ipow(a, TC);
+    Map<W> sup = {ipow(Pc, K), Num<W>::zero()};
+    if (k == 0 && live) {
+      sup.e = s_e[0][lid];
+      for (int j = 1; j < K; ++j) sup.e = Num<W>::fma(Pc, sup.e, s_e[j][lid]);
+      if (sc > 0 && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
+    }
+    W s = x0 && live && k == 0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
+    if (sc > 0)  // uniform over the workgroup
+      s = look_back(agg, inc, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
+                    s_pos, &s_any);
+    if (k == 0 && live) {
+      if (sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
+      for (int j = 0; j < K; ++j) {
+        s_start[j][lid] = s;
+        s = Num<W>::fma(Pc, s, s_e[j][lid]);
+      }
+    }
+    __syncthreads();
+    if (live && len > 0) {
+      W s = s_start[k][lid];
+      T* op = out + base;
+      if (len == TC) {
+#pragma unroll
+        for (int i = 0; i < TC; ++i) {
+          s = Num<W>::fma(a, s, Wide<T>::up(vb[i]));
+          op[i * N] = Wide<T>::down(s);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < TC; ++i)
+          if (i < len) {
+            s = Num<W>::fma(a, s, Wide<T>::up(vb[i]));
+            op[i * N] = Wide<T>::down(s);
+          }
+      }
+    }
   }
 }
 
-// Reverse summary of super-chunk sc >= 1: G at its first step with no gradient entering from the
-// right, F [nsuper, lanes] (slot 0 unused). Chunks past the end of the sequence are empty and
-// contribute zero, so the full-chunk multiplier conj(lam)^TC is right for every fold.
+// Backward: G_t = g_t + conj(lam) G_{t+1} from the right end; gv = G, gx0 = conj(lam) G_0, and
+// glam = sum_t G_t conj(x_{t-1}) reduced over the K chunks in LDS and over super-chunks by
+// diag_sum_parts (fixed order, deterministic). Chunks past the end of the sequence are empty and
+// contribute zero, so conj(lam)^TC is the right multiplier for every fold.
 template <typename T, int TC>
-__global__ void __launch_bounds__(1024) diag_bwd_summary(const T* __restrict__ lam, const T* __restrict__ g,
-                                                         typename Wide<T>::type* __restrict__ F, int64_t lanes,
-                                                         int64_t L, int64_t N, int64_t groups, int K) {
+__global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, const T* __restrict__ g,
+                                                 const T* __restrict__ out, const T* __restrict__ x0,
+                                                 Map<typename Wide<T>::type>* __restrict__ agg,
+                                                 typename Wide<T>::type* __restrict__ inc, unsigned* __restrict__ counter,
+                                                 T* __restrict__ gv, typename Wide<T>::type* __restrict__ part,
+                                                 T* __restrict__ glam, T* __restrict__ gx0, int64_t lanes, int64_t L,
+                                                 int64_t N, int64_t groups, int K, int64_t nsuper) {
   using W = typename Wide<T>::type;
   __shared__ W s_f[kMaxWaves][64];
+  // the look-back window, then G entering each chunk from the right (s_start) and the glam
+  // partials of the chunks (s_acc)
+  __shared__ Map<W> s_win[kMaxWaves][64];
+  __shared__ int s_flag[kMaxWaves][64];
+  __shared__ int64_t s_pos[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  W(*s_start)[64] = reinterpret_cast<W(*)[64]>(&s_win[0][0]);
+  W(*s_acc)[64] = s_start + kMaxWaves;
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t gr = blockIdx.x % groups, sc = blockIdx.x / groups + 1;  // super-chunks 1 .. nsuper-1
-  const int64_t lane = gr * 64 + lid;
-  const bool live = lane < lanes;
-  const int64_t t0 = sc * K * TC + (int64_t)k * TC;
-  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
-  W ac = Num<W>::zero(), f = Num<W>::zero();
-  if (live) {
-    ac = Num<W>::conj(Wide<T>::up(lam[lane]));
-    const int64_t m = lane / N, n = lane - m * N;
-    const T* gp = g + (m * L + t0) * N + n;
-    T gb[TC];
-    if (len == TC) {
-#pragma unroll
-      for (int i = 0; i < TC; ++i) gb[i] = gp[i * N];
-#pragma unroll
-      for (int i = TC - 1; i >= 0; --i) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
-    } else {
-#pragma unroll
-      for (int i = 0; i < TC; ++i)
-        if (i < len) gb[i] = gp[i * N];
-#pragma unroll
-      for (int i = TC - 1; i >= 0; --i)
-        if (i < len) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
-    }
-  }
-  s_f[k][lid] = f;
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * TC;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
   __syncthreads();
-  if (k == 0 && live) {
-    const W P = ipow(ac, TC);
-    W s = s_f[K - 1][lid];
-    for (int j = K - 2; j >= 0; --j) s = Num<W>::fma(P, s, s_f[j][lid]);
-    F[sc * lanes + lane] = s;
-  }
-}
-
-template <typename T, int TC>
-__global__ void __launch_bounds__(1024) diag_bwd_apply(const T* __restrict__ lam, const T* __restrict__ g,
-                                                       const T* __restrict__ out, const T* __restrict__ x0,
-                                                       const typename Wide<T>::type* __restrict__ F,
-                                                       T* __restrict__ gv, typename Wide<T>::type* __restrict__ part,
-                                                       T* __restrict__ glam, T* __restrict__ gx0, int64_t lanes,
-                                                       int64_t L, int64_t N, int64_t groups, int K, int64_t nsuper,
-                                                       int starts_ready) {
-  using W = typename Wide<T>::type;
-  __shared__ W s_f[kMaxWaves][64];
-  __shared__ W s_acc[kMaxWaves][64];
-  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t gr = blockIdx.x % groups, sc = blockIdx.x / groups;
-  const int64_t lane = gr * 64 + lid;
-  const bool live = lane < lanes;
-  const int64_t SL = (int64_t)K * TC;
-  const int64_t t0 = sc * SL + (int64_t)k * TC;
-  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
-  W ac = Num<W>::zero(), f = Num<W>::zero();
-  T gb[TC], xb[TC];  // g_t and x_{t-1} of the chunk's steps
-  int64_t base = 0;
-  if (live) {
-    ac = Num<W>::conj(Wide<T>::up(lam[lane]));
-    const int64_t m = lane / N, n = lane - m * N;
-    base = (m * L + t0) * N + n;
-    const T* gp = g + base;
-    const T* xp = out + base;
-    if (len == TC && t0 > 0) {
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t r = tile / groups, sc = nsuper - 1 - r, lane = (tile - r * groups) * 64 + lid;
+    const bool live = lane < lanes;
+    const int64_t t0 = sc * SL + (int64_t)k * TC;
+    const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+    // With R the G entering the chunk from the right, G_t = G0_t + c^(t_end - t) R (c = conj(lam),
+    // G0 the chunk's scan from zero), so the chunk's glam partial is A + R B with
+    // A = sum_t G0_t conj(x_{t-1}) = sum_s g_s H_s, H_s = c H_{s-1} + conj(x_{s-1}) (H before the
+    // chunk = 0), and B = sum_t c^(t_end - t) conj(x_{t-1}) = c H_last. Everything runs forward
+    // through the chunk, and x_{t-1} is not kept in registers across the look-back.
+    W ac = Num<W>::zero(), f = Num<W>::zero(), A = Num<W>::zero(), B = Num<W>::zero();
+    T gb[TC];  // g_t of the chunk's steps
+    int64_t base = 0;
+    if (live) {
+      ac = Num<W>::conj(Wide<T>::up(lam[lane]));
+      const int64_t m = lane / N, n = lane - m * N;
+      base = (m * L + t0) * N + n;
+      const T* gp = g + base;
+      const T* xp = out + base;
+      T xb[TC];  // x_{t-1}
+      W H = Num<W>::zero(), pw = Num<W>::one();
+      if (len == TC && t0 > 0) {
 #pragma unroll
-      for (int i = 0; i < TC; ++i) {
-        gb[i] = gp[i * N];
-        xb[i] = xp[(i - 1) * N];
-      }
-#pragma unroll
-      for (int i = TC - 1; i >= 0; --i) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
-    } else if (len > 0) {
-      const T xinit = x0 ? x0[lane] : T{};  // x_{-1}: the initial state (zero without x0)
-#pragma unroll
-      for (int i = 0; i < TC; ++i)
-        if (i < len) {
+        for (int i = 0; i < TC; ++i) {
           gb[i] = gp[i * N];
-          xb[i] = (t0 + i > 0) ? xp[(i - 1) * N] : xinit;
+          xb[i] = xp[(i - 1) * N];
         }
 #pragma unroll
-      for (int i = TC - 1; i >= 0; --i)
-        if (i < len) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
+        for (int i = 0; i < TC; ++i) {
+          const W gi = Wide<T>::up(gb[i]);
+          H = Num<W>::fma(ac, H, Num<W>::conj(Wide<T>::up(xb[i])));
+          A = Num<W>::fma(gi, H, A);
+          f = Num<W>::fma(pw, gi, f);
+          pw = Num<W>::mul(pw, ac);
+        }
+      } else if (len > 0) {
+        // partial or first chunk: loads clamped into the chunk (branch-free), steps guarded
+#pragma unroll
+        for (int i = 0; i < TC; ++i) {
+          const int ii = i < len ? i : len - 1;
+          gb[i] = gp[ii * N];
+          xb[i] = xp[(t0 + ii > 0 ? ii - 1 : 0) * N];
+        }
+        if (t0 == 0) xb[0] = x0 ? x0[lane] : T{};  // x_{-1}: the initial state (zero without x0)
+#pragma unroll
+        for (int i = 0; i < TC; ++i)
+          if (i < len) {
+            const W gi = Wide<T>::up(gb[i]);
+            H = Num<W>::fma(ac, H, Num<W>::conj(Wide<T>::up(xb[i])));
+            A = Num<W>::fma(gi, H, A);
+            f = Num<W>::fma(pw, gi, f);
+            pw = Num<W>::mul(pw, ac);
+          }
+      }
+      B = Num<W>::mul(ac, H);
     }
-  }
-  s_f[k][lid] = f;
-  __syncthreads();
-  W acc = Num<W>::zero();
-  if (live && len > 0) {
-    // G entering the super-chunk from the right: G at the first step of super-chunk sc + 1
-    W R = Num<W>::zero();
-    if (sc + 1 < nsuper) {
-      if (starts_ready) {
-        R = F[(sc + 1) * lanes + lane];
-      } else {
-        const W Q = ipow(ac, SL);
-        R = F[(nsuper - 1) * lanes + lane];
-#pragma unroll 8
-        for (int64_t j = nsuper - 2; j > sc; --j) R = Num<W>::fma(Q, R, F[j * lanes + lane]);
+    s_f[k][lid] = f;
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    const W Pc = ipow(ac, TC);
+    Map<W> sup = {ipow(Pc, K), Num<W>::zero()};
+    if (k == 0 && live) {
+      sup.e = s_f[K - 1][lid];
+      for (int j = K - 2; j >= 0; --j) sup.e = Num<W>::fma(Pc, sup.e, s_f[j][lid]);
+      if (sc > 0 && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
+    }
+    W R = Num<W>::zero();  // G entering the super-chunk from the right
+    if (sc + 1 < nsuper)   // uniform over the workgroup
+      R = look_back(agg, inc, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid, s_win, s_flag, s_pos,
+                    &s_any);
+    if (k == 0 && live) {
+      if (sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
+      for (int j = K - 1; j >= 0; --j) {
+        s_start[j][lid] = R;
+        R = Num<W>::fma(Pc, R, s_f[j][lid]);
       }
     }
-    // G entering chunk k from the right
-    if (k + 1 < K) {
-      const W P = ipow(ac, TC);
-      for (int j = K - 1; j > k; --j) R = Num<W>::fma(P, R, s_f[j][lid]);
-    }
-    W G = R;
-    T* gvp = gv + base;
-    if (len == TC) {
+    __syncthreads();
+    W acc = Num<W>::zero();
+    if (live && len > 0) {
+      W G = s_start[k][lid];
+      acc = Num<W>::fma(G, B, A);
+      T* gvp = gv + base;
+      if (len == TC) {
 #pragma unroll
-      for (int i = TC - 1; i >= 0; --i) {
-        G = Num<W>::fma(ac, G, Wide<T>::up(gb[i]));
-        gvp[i * N] = Wide<T>::down(G);
-        acc = Num<W>::add(acc, Num<W>::mul_conj(G, Wide<T>::up(xb[i])));
-      }
-    } else {
-#pragma unroll
-      for (int i = TC - 1; i >= 0; --i)
-        if (i < len) {
+        for (int i = TC - 1; i >= 0; --i) {
           G = Num<W>::fma(ac, G, Wide<T>::up(gb[i]));
           gvp[i * N] = Wide<T>::down(G);
-          acc = Num<W>::add(acc, Num<W>::mul_conj(G, Wide<T>::up(xb[i])));
         }
+      } else {
+#pragma unroll
+        for (int i = TC - 1; i >= 0; --i)
+          if (i < len) {
+            G = Num<W>::fma(ac, G, Wide<T>::up(gb[i]));
+            gvp[i * N] = Wide<T>::down(G);
+          }
+      }
+      if (t0 == 0 && gx0) gx0[lane] = Wide<T>::down(Num<W>::mul(ac, G));
     }
-    if (t0 == 0 && gx0) gx0[lane] = Wide<T>::down(Num<W>::mul(ac, G));
-  }
-  s_acc[k][lid] = acc;
-  __syncthreads();
-  if (k == 0 && live) {
-    W s = s_acc[0][lid];
-    for (int j = 1; j < K; ++j) s = Num<W>::add(s, s_acc[j][lid]);
-    if (nsuper == 1)
-      glam[lane] = Wide<T>::down(s);
-    else
-      part[sc * lanes + lane] = s;
+    s_acc[k][lid] = acc;
+    __syncthreads();
+    if (k == 0 && live) {
+      W s = s_acc[0][lid];
+      for (int j = 1; j < K; ++j) s = Num<W>::add(s, s_acc[j][lid]);
+      if (nsuper == 1)
+        glam[lane] = Wide<T>::down(s);
+      else
+        part[sc * lanes + lane] = s;
+    }
   }
 }
 
@@ -357,403 +484,350 @@ __global__ void __launch_bounds__(256) zero_fill(float* __restrict__ p, int64_t 
   if (i < n) p[i] = 0.0f;
 }
 
-
 // ---------------------------------------------------------------- time-varying coefficient (real)
-// Same tiling as the constant-coefficient kernels; a chunk's summary is the affine map
-// s -> P s + e with P the product of its coefficients, stored as double2 (P, e), composed in
-// LDS across the K chunks of a super-chunk and through HBM across super-chunks.
-TSF_DEV double2 compose(double2 first, double2 then) {  // apply `first`, then `then`
-  return make_double2(then.x * first.x, fma(then.x, first.y, then.y));
-}
-
+// Same tiles and look-back; a chunk's summary is the affine map x -> P x + e with P the product
+// of its coefficients, and the chunk maps (P, e) meet in LDS.
 template <int TC>
-__global__ void __launch_bounds__(1024) sel_fwd_summary(const float* __restrict__ a, const float* __restrict__ v,
-                                                        double2* __restrict__ E, int64_t lanes, int64_t L, int64_t N,
-                                                        int64_t groups, int K) {
-  __shared__ double2 s_e[kMaxWaves][64];
+__global__ void __launch_bounds__(1024) sel_fwd(const float* __restrict__ a, const float* __restrict__ v,
+                                                const float* __restrict__ x0, float* __restrict__ out,
+                                                Map<double>* __restrict__ agg, double* __restrict__ inc,
+                                                unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t N,
+                                                int64_t groups, int K, int64_t nsuper) {
+  __shared__ double2 s_m[kMaxWaves][64];  // chunk maps (P, e)
+  // the look-back window, then the state entering each chunk
+  __shared__ Map<double> s_win[kMaxWaves][64];
+  __shared__ int s_flag[kMaxWaves][64];
+  __shared__ int64_t s_pos[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  double(*s_start)[64] = reinterpret_cast<double(*)[64]>(&s_win[0][0]);
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t g = blockIdx.x % groups, sc = blockIdx.x / groups;  // super-chunks 0 .. nsuper-2
-  const int64_t lane = g * 64 + lid;
-  const bool live = lane < lanes;
-  double P = 1.0, e = 0.0;
-  if (live) {
-    const int64_t m = lane / N, n = lane - m * N;
-    const int64_t base = (m * L + sc * K * TC + (int64_t)k * TC) * N + n;  // full chunks only
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * TC;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
+  __syncthreads();
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t sc = tile / groups, lane = (tile - sc * groups) * 64 + lid;
+    const bool live = lane < lanes;
+    const int64_t t0 = sc * SL + (int64_t)k * TC;
+    const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+    double P = 1.0, e = 0.0;
     float ab[TC], vb[TC];
+    int64_t base = 0;
+    if (live) {
+      const int64_t m = lane / N, n = lane - m * N;
+      base = (m * L + t0) * N + n;
+      if (len == TC) {  // full chunk: every load issued before the arithmetic, no per-step guard
 #pragma unroll
-    for (int i = 0; i < TC; ++i) {
-      ab[i] = a[base + i * N];
-      vb[i] = v[base + i * N];
-    }
+        for (int i = 0; i < TC; ++i) {
+          ab[i] = a[base + i * N];
+          vb[i] = v[base + i * N];
+        }
 #pragma unroll
-    for (int i = 0; i < TC; ++i) {
-      e = fma((double)ab[i], e, (double)vb[i]);
-      P *= (double)ab[i];
-    }
-  }
-  s_e[k][lid] = make_double2(P, e);
-  __syncthreads();
-  if (k == 0 && live) {
-    double2 s = s_e[0][lid];
-    for (int j = 1; j < K; ++j) s = compose(s, s_e[j][lid]);
-    E[sc * lanes + lane] = s;
-  }
-}
-
-// In-place inclusive scan of n affine maps per lane: state_r = P_r state_{r-1} + e_r from
-// init (NULL: zero); the state replaces e_r. Map r of a lane sits at S[(first + dir*r) * lanes
-// + lane]. One workgroup per 64-lane group; wave k composes the k-th of 16 contiguous segments.
-__global__ void __launch_bounds__(1024) sel_carry(const float* __restrict__ init, double2* __restrict__ S,
-                                                  int64_t lanes, int64_t n, int64_t first, int64_t dir) {
-  __shared__ double2 s_p[kMaxWaves][64];
-  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t lane = blockIdx.x * 64 + lid;
-  const bool live = lane < lanes;
-  const int64_t seg = (n + kMaxWaves - 1) / kMaxWaves;
-  const int64_t r0 = k * seg, r1 = (r0 + seg < n) ? r0 + seg : n;
-  double2 p = make_double2(1.0, 0.0);
-  if (live) {
-#pragma unroll 8
-    for (int64_t r = r0; r < r1; ++r) p = compose(p, S[(first + dir * r) * lanes + lane]);
-  }
-  s_p[k][lid] = p;
-  __syncthreads();
-  if (live && r0 < r1) {
-    double s = init ? (double)init[lane] : 0.0;
-    for (int j = 0; j < k; ++j) s = fma(s_p[j][lid].x, s, s_p[j][lid].y);
-#pragma unroll 8
-    for (int64_t r = r0; r < r1; ++r) {
-      double2* q = S + (first + dir * r) * lanes + lane;
-      const double2 m = *q;
-      s = fma(m.x, s, m.y);
-      q->y = s;
-    }
-  }
-}
-
-template <int TC>
-__global__ void __launch_bounds__(1024) sel_fwd_apply(const float* __restrict__ a, const float* __restrict__ v,
-                                                      const float* __restrict__ x0, const double2* __restrict__ E,
-                                                      float* __restrict__ out, int64_t lanes, int64_t L, int64_t N,
-                                                      int64_t groups, int K, int starts_ready) {
-  __shared__ double2 s_e[kMaxWaves][64];
-  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t g = blockIdx.x % groups, sc = blockIdx.x / groups;
-  const int64_t lane = g * 64 + lid;
-  const bool live = lane < lanes;
-  const int64_t t0 = sc * K * TC + (int64_t)k * TC;
-  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
-  double P = 1.0, e = 0.0;
-  float ab[TC], vb[TC];
-  int64_t base = 0;
-  if (live) {
-    const int64_t m = lane / N, n = lane - m * N;
-    base = (m * L + t0) * N + n;
-    if (len == TC) {  // full chunk: every load issued before the arithmetic, no per-step guard
-#pragma unroll
-      for (int i = 0; i < TC; ++i) {
-        ab[i] = a[base + i * N];
-        vb[i] = v[base + i * N];
-      }
-#pragma unroll
-      for (int i = 0; i < TC; ++i) {
-        e = fma((double)ab[i], e, (double)vb[i]);
-        P *= (double)ab[i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < TC; ++i) {
-        ab[i] = i < len ? a[base + i * N] : 1.0f;
-        vb[i] = i < len ? v[base + i * N] : 0.0f;
-      }
-#pragma unroll
-      for (int i = 0; i < TC; ++i)
-        if (i < len) {
+        for (int i = 0; i < TC; ++i) {
           e = fma((double)ab[i], e, (double)vb[i]);
           P *= (double)ab[i];
         }
-    }
-  }
-  s_e[k][lid] = make_double2(P, e);
-  __syncthreads();
-  if (!live || len == 0) return;  // no barrier follows
-  double s = x0 ? (double)x0[lane] : 0.0;
-  if (sc > 0) {
-    if (starts_ready) {
-      s = E[(sc - 1) * lanes + lane].y;
-    } else {
-#pragma unroll 8
-      for (int64_t j = 0; j < sc; ++j) {
-        const double2 mp = E[j * lanes + lane];
-        s = fma(mp.x, s, mp.y);
+      } else {
+#pragma unroll
+        for (int i = 0; i < TC; ++i) {
+          ab[i] = i < len ? a[base + i * N] : 1.0f;
+          vb[i] = i < len ? v[base + i * N] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < TC; ++i)
+          if (i < len) {
+            e = fma((double)ab[i], e, (double)vb[i]);
+            P *= (double)ab[i];
+          }
       }
     }
-  }
-  for (int j = 0; j < k; ++j) s = fma(s_e[j][lid].x, s, s_e[j][lid].y);
-  if (len == TC) {
-#pragma unroll
-    for (int i = 0; i < TC; ++i) {
-      s = fma((double)ab[i], s, (double)vb[i]);
-      out[base + i * N] = (float)s;
+    s_m[k][lid] = make_double2(P, e);
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    Map<double> sup = {1.0, 0.0};
+    if (k == 0 && live) {
+      for (int j = 0; j < K; ++j) sup = then(sup, Map<double>{s_m[j][lid].x, s_m[j][lid].y});
+      if (sc > 0 && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
     }
-  } else {
-#pragma unroll
-    for (int i = 0; i < TC; ++i)
-      if (i < len) {
-        s = fma((double)ab[i], s, (double)vb[i]);
-        out[base + i * N] = (float)s;
+    double s = x0 && live && k == 0 ? (double)x0[lane] : 0.0;
+    if (sc > 0)  // uniform over the workgroup
+      s = look_back(agg, inc, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
+                    s_pos, &s_any);
+    if (k == 0 && live) {
+      if (sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
+      for (int j = 0; j < K; ++j) {
+        s_start[j][lid] = s;
+        s = fma(s_m[j][lid].x, s, s_m[j][lid].y);
       }
+    }
+    __syncthreads();
+    if (live && len > 0) {
+      double s = s_start[k][lid];
+      if (len == TC) {
+#pragma unroll
+        for (int i = 0; i < TC; ++i) {
+          s = fma((double)ab[i], s, (double)vb[i]);
+          out[base + i * N] = (float)s;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < TC; ++i)
+          if (i < len) {
+            s = fma((double)ab[i], s, (double)vb[i]);
+            out[base + i * N] = (float)s;
+          }
+      }
+    }
   }
 }
 
-// Reverse summary of super-chunk sc >= 1: the map G_enter -> G at its first step,
-// G_t = g_t + a_{t+1} G_{t+1}, as (multiplier, value) with the multiplier the product of
-// a_{t0+1} .. a_{t1} (a_{t1} is the next super-chunk's first coefficient). F [nsuper, lanes].
+// Backward: G_t = g_t + a_{t+1} G_{t+1} from the right end (a_L taken as 0: nothing enters),
+// gv = G, glam_t = G_t x_{t-1} (x_{-1} the initial state), gx0 = a_0 G_0. A chunk's map takes
+// G at the first step after it to G at its first step: (product of its a_{t+1}, value from zero).
 template <int TC>
-__global__ void __launch_bounds__(1024) sel_bwd_summary(const float* __restrict__ a, const float* __restrict__ g,
-                                                        double2* __restrict__ F, int64_t lanes, int64_t L, int64_t N,
-                                                        int64_t groups, int K) {
-  __shared__ double2 s_f[kMaxWaves][64];
+__global__ void __launch_bounds__(1024) sel_bwd(const float* __restrict__ a, const float* __restrict__ g,
+                                                const float* __restrict__ out, const float* __restrict__ x0,
+                                                Map<double>* __restrict__ agg, double* __restrict__ inc,
+                                                unsigned* __restrict__ counter, float* __restrict__ glam,
+                                                float* __restrict__ gv, float* __restrict__ gx0, int64_t lanes,
+                                                int64_t L, int64_t N, int64_t groups, int K, int64_t nsuper) {
+  __shared__ double2 s_m[kMaxWaves][64];
+  // the look-back window, then G entering each chunk from the right
+  __shared__ Map<double> s_win[kMaxWaves][64];
+  __shared__ int s_flag[kMaxWaves][64];
+  __shared__ int64_t s_pos[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  double(*s_start)[64] = reinterpret_cast<double(*)[64]>(&s_win[0][0]);
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t gr = blockIdx.x % groups, sc = blockIdx.x / groups + 1;  // super-chunks 1 .. nsuper-1
-  const int64_t lane = gr * 64 + lid;
-  const bool live = lane < lanes;
-  const int64_t t0 = sc * K * TC + (int64_t)k * TC;
-  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
-  double M = 1.0, f = 0.0;
-  if (live && len > 0) {
-    const int64_t m = lane / N, n = lane - m * N;
-    const int64_t base = (m * L + t0) * N + n;
-    float gb[TC], an[TC];  // g_t and a_{t+1} of the chunk's steps (a_L taken as 0: nothing enters)
-    if (len == TC && t0 + TC < L) {  // full chunk with a following step: no per-step guard
-#pragma unroll
-      for (int i = 0; i < TC; ++i) {
-        gb[i] = g[base + i * N];
-        an[i] = a[base + (i + 1) * N];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < TC; ++i) {
-        gb[i] = i < len ? g[base + i * N] : 0.0f;
-        an[i] = (i < len && t0 + i + 1 < L) ? a[base + (i + 1) * N] : 0.0f;
-      }
-    }
-#pragma unroll
-    for (int i = TC - 1; i >= 0; --i)
-      if (i < len) {
-        f = fma((double)an[i], f, (double)gb[i]);
-        M *= (double)an[i];
-      }
-  }
-  s_f[k][lid] = make_double2(M, f);
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * TC;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
   __syncthreads();
-  if (k == 0 && live) {
-    double2 s = s_f[K - 1][lid];
-    for (int j = K - 2; j >= 0; --j) s = compose(s, s_f[j][lid]);
-    F[sc * lanes + lane] = s;
-  }
-}
-
-template <int TC>
-__global__ void __launch_bounds__(1024) sel_bwd_apply(const float* __restrict__ a, const float* __restrict__ g,
-                                                      const float* __restrict__ out, const float* __restrict__ x0,
-                                                      const double2* __restrict__ F, float* __restrict__ glam,
-                                                      float* __restrict__ gv, float* __restrict__ gx0, int64_t lanes,
-                                                      int64_t L, int64_t N, int64_t groups, int K, int64_t nsuper,
-                                                      int starts_ready) {
-  __shared__ double2 s_f[kMaxWaves][64];
-  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t gr = blockIdx.x % groups, sc = blockIdx.x / groups;
-  const int64_t lane = gr * 64 + lid;
-  const bool live = lane < lanes;
-  const int64_t t0 = sc * K * TC + (int64_t)k * TC;
-  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
-  double M = 1.0, f = 0.0;
-  float gb[TC], an[TC], xb[TC];  // g_t, a_{t+1}, x_{t-1}
-  int64_t base = 0;
-  if (live && len > 0) {
-    const int64_t m = lane / N, n = lane - m * N;
-    base = (m * L + t0) * N + n;
-    const float xinit = x0 ? x0[lane] : 0.0f;  // x_{-1}
-    if (len == TC && t0 > 0 && t0 + TC < L) {  // interior full chunk: no per-step guard
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t r = tile / groups, sc = nsuper - 1 - r, lane = (tile - r * groups) * 64 + lid;
+    const bool live = lane < lanes;
+    const int64_t t0 = sc * SL + (int64_t)k * TC;
+    const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+    double M = 1.0, f = 0.0;
+    float gb[TC], an[TC], xb[TC];  // g_t, a_{t+1}, x_{t-1}
+    int64_t base = 0;
+    if (live && len > 0) {
+      const int64_t m = lane / N, n = lane - m * N;
+      base = (m * L + t0) * N + n;
+      if (len == TC && t0 > 0 && t0 + TC < L) {  // interior full chunk: no per-step guard
 #pragma unroll
-      for (int i = 0; i < TC; ++i) {
-        gb[i] = g[base + i * N];
-        an[i] = a[base + (i + 1) * N];
-        xb[i] = out[base + (i - 1) * N];
-      }
+        for (int i = 0; i < TC; ++i) {
+          gb[i] = g[base + i * N];
+          an[i] = a[base + (i + 1) * N];
+          xb[i] = out[base + (i - 1) * N];
+        }
 #pragma unroll
-      for (int i = TC - 1; i >= 0; --i) {
-        f = fma((double)an[i], f, (double)gb[i]);
-        M *= (double)an[i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < TC; ++i) {
-        gb[i] = i < len ? g[base + i * N] : 0.0f;
-        an[i] = (i < len && t0 + i + 1 < L) ? a[base + (i + 1) * N] : 0.0f;
-        xb[i] = i >= len ? 0.0f : (t0 + i > 0) ? out[base + (i - 1) * N] : xinit;
-      }
-#pragma unroll
-      for (int i = TC - 1; i >= 0; --i)
-        if (i < len) {
+        for (int i = TC - 1; i >= 0; --i) {
           f = fma((double)an[i], f, (double)gb[i]);
           M *= (double)an[i];
         }
-    }
-  }
-  s_f[k][lid] = make_double2(M, f);
-  __syncthreads();
-  if (!live || len == 0) return;  // no barrier follows
-  // G entering the super-chunk from the right: G at the first step of super-chunk sc + 1
-  double R = 0.0;
-  if (sc + 1 < nsuper) {
-    if (starts_ready) {
-      R = F[(sc + 1) * lanes + lane].y;
-    } else {
-      R = F[(nsuper - 1) * lanes + lane].y;
-#pragma unroll 8
-      for (int64_t j = nsuper - 2; j > sc; --j) {
-        const double2 mp = F[j * lanes + lane];
-        R = fma(mp.x, R, mp.y);
+      } else {
+        const float xinit = x0 ? x0[lane] : 0.0f;  // x_{-1}
+#pragma unroll
+        for (int i = 0; i < TC; ++i) {
+          gb[i] = i < len ? g[base + i * N] : 0.0f;
+          an[i] = (i < len && t0 + i + 1 < L) ? a[base + (i + 1) * N] : 0.0f;
+          xb[i] = i >= len ? 0.0f : (t0 + i > 0) ? out[base + (i - 1) * N] : xinit;
+        }
+#pragma unroll
+        for (int i = TC - 1; i >= 0; --i)
+          if (i < len) {
+            f = fma((double)an[i], f, (double)gb[i]);
+            M *= (double)an[i];
+          }
       }
     }
-  }
-  for (int j = K - 1; j > k; --j) R = fma(s_f[j][lid].x, R, s_f[j][lid].y);
-  double G = R;
-  if (len == TC) {
-#pragma unroll
-    for (int i = TC - 1; i >= 0; --i) {
-      G = fma((double)an[i], G, (double)gb[i]);
-      gv[base + i * N] = (float)G;
-      glam[base + i * N] = (float)(G * (double)xb[i]);
+    s_m[k][lid] = make_double2(M, f);
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    Map<double> sup = {1.0, 0.0};
+    if (k == 0 && live) {
+      sup = Map<double>{s_m[K - 1][lid].x, s_m[K - 1][lid].y};
+      for (int j = K - 2; j >= 0; --j) sup = then(sup, Map<double>{s_m[j][lid].x, s_m[j][lid].y});
+      if (sc > 0 && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
     }
-  } else {
-#pragma unroll
-    for (int i = TC - 1; i >= 0; --i)
-      if (i < len) {
-        G = fma((double)an[i], G, (double)gb[i]);
-        gv[base + i * N] = (float)G;
-        glam[base + i * N] = (float)(G * (double)xb[i]);
+    double R = 0.0;
+    if (sc + 1 < nsuper)  // uniform over the workgroup
+      R = look_back(agg, inc, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
+                    s_pos, &s_any);
+    if (k == 0 && live) {
+      if (sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
+      for (int j = K - 1; j >= 0; --j) {
+        s_start[j][lid] = R;
+        R = fma(s_m[j][lid].x, R, s_m[j][lid].y);
       }
+    }
+    __syncthreads();
+    if (live && len > 0) {
+      double G = s_start[k][lid];
+      if (len == TC) {
+#pragma unroll
+        for (int i = TC - 1; i >= 0; --i) {
+          G = fma((double)an[i], G, (double)gb[i]);
+          gv[base + i * N] = (float)G;
+          glam[base + i * N] = (float)(G * (double)xb[i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = TC - 1; i >= 0; --i)
+          if (i < len) {
+            G = fma((double)an[i], G, (double)gb[i]);
+            gv[base + i * N] = (float)G;
+            glam[base + i * N] = (float)(G * (double)xb[i]);
+          }
+      }
+      if (t0 == 0 && gx0) gx0[lane] = (float)((double)a[base] * G);
+    }
   }
-  if (t0 == 0 && gx0) gx0[lane] = (float)((double)a[base] * G);
 }
 
 inline dim3 grid_for(int64_t threads) { return dim3((unsigned)((threads + 255) / 256)); }
 
-// Tile shape of the constant-coefficient kernels for one call. TC (steps per chunk) is a
-// template parameter: 16 or 32 for real lanes, 16 for complex ones (their backward keeps 2 x TC
-// complex values per thread in registers, within the 128 VGPRs a 1024-thread workgroup allows).
-// Every thread issues all TC loads of its chunk at once, so the bytes in flight do not depend on
-// TC; the wave count (lanes / 64 x L / TC) does, and real lanes drop to TC = 16 when 32 would
-// leave fewer than kDiagWaveTarget waves. K (chunks per workgroup) starts at 16, which keeps
-// the super-chunk count and the summary folds small, and halves down to 4 only while the grid
-// holds fewer than kDiagWgTarget workgroups. The carry kernel replaces the per-thread fold of
-// super-chunk summaries once there are more than kDiagFoldMax of them.
-#ifndef TSF_DIAG_WG_TARGET
-#define TSF_DIAG_WG_TARGET 256
+// Tile shape for one call. TC (steps per chunk) is a template parameter, at most tc_max: 32 for
+// real lanes, 16 for complex ones and for the time-varying backward (a thread keeps its chunk's
+// inputs in registers across the look-back: TC complex values, or three TC-step arrays, within
+// the 128 VGPRs a 1024-thread workgroup allows). Every
+// thread issues all TC loads of its chunk at once, so the bytes in flight do not depend on TC;
+// the wave count (lanes / 64 x L / TC) does, and TC drops to 16 when 32 would leave fewer than
+// kDiagWaveTarget waves. K (chunks per tile) starts at TSF_DIAG_KMAX and halves down to 4 while
+// there are fewer than kDiagTileTarget tiles.
+#ifndef TSF_DIAG_TILE_TARGET
+#define TSF_DIAG_TILE_TARGET 256
 #endif
 #ifndef TSF_DIAG_WAVE_TARGET
 #define TSF_DIAG_WAVE_TARGET 4096
 #endif
-#ifndef TSF_DIAG_FOLD_MAX
-#define TSF_DIAG_FOLD_MAX 16
+#ifndef TSF_DIAG_KMAX
+#define TSF_DIAG_KMAX 16
 #endif
-constexpr int64_t kDiagWgTarget = TSF_DIAG_WG_TARGET;
+constexpr int64_t kDiagTileTarget = TSF_DIAG_TILE_TARGET;
 constexpr int64_t kDiagWaveTarget = TSF_DIAG_WAVE_TARGET;
-constexpr int64_t kDiagFoldMax = TSF_DIAG_FOLD_MAX;
+static_assert(TSF_DIAG_KMAX >= 4 && TSF_DIAG_KMAX <= kMaxWaves, "K range");
 
 struct DiagTile {
   int64_t lanes = 0, groups = 0, nsuper = 0, SL = 0;
   int TC = 0, K = 0;
-  bool carry_kernel = false;
 };
 
-DiagTile diag_tile(int64_t lanes, int64_t L, bool cplx, int kmax = kMaxWaves) {
+DiagTile diag_tile(int64_t lanes, int64_t L, int tc_max) {
   DiagTile t;
   t.lanes = lanes;
   if (lanes < 1 || L < 1) return t;
   t.groups = (lanes + 63) / 64;
-  t.TC = (cplx || t.groups * ((L + 31) / 32) < kDiagWaveTarget) ? 16 : 32;
-  t.K = kmax;
-  auto wgs = [&](int K) { return t.groups * ((L + (int64_t)t.TC * K - 1) / ((int64_t)t.TC * K)); };
-  while (t.K > 4 && wgs(t.K) < kDiagWgTarget) t.K /= 2;
+  t.TC = (t.groups * ((L + 31) / 32) < kDiagWaveTarget) ? 16 : 32;
+  if (t.TC > tc_max) t.TC = tc_max;
+  t.K = TSF_DIAG_KMAX;
+  auto tiles = [&](int K) { return t.groups * ((L + (int64_t)t.TC * K - 1) / ((int64_t)t.TC * K)); };
+  while (t.K > 4 && tiles(t.K) < kDiagTileTarget) t.K /= 2;
   const int64_t chunks = (L + t.TC - 1) / t.TC;
   if (t.K > chunks) t.K = (int)chunks;  // no waves past the end of a short sequence
   t.SL = (int64_t)t.TC * t.K;
   t.nsuper = (L + t.SL - 1) / t.SL;
-  t.carry_kernel = t.nsuper - 1 > kDiagFoldMax;
   return t;
 }
 
+DiagTile const_tile(int64_t lanes, int64_t L, bool cplx, bool bwd) {
+  (void)bwd;
+  return diag_tile(lanes, L, cplx ? 16 : 32);
+}
+DiagTile sel_tile(int64_t lanes, int64_t L, bool bwd) { return diag_tile(lanes, L, bwd ? 16 : 32); }
+
 inline bool grid_fits(const DiagTile& t) { return t.groups * t.nsuper <= INT32_MAX; }
 
-template <typename T, int TC>
-void diag_fwd_launch(const DiagTile& t, const T* lam, const T* v, const T* x0, T* out, typename Wide<T>::type* E,
-                     int64_t L, int64_t N, hipStream_t s) {
-  const dim3 blk(64 * t.K);
-  if (t.nsuper > 1) {
-    hipLaunchKernelGGL((diag_fwd_summary<T, TC>), dim3((unsigned)(t.groups * (t.nsuper - 1))), blk, 0, s, lam, v, E,
-                       t.lanes, L, N, t.groups, t.K);
-    if (t.carry_kernel)
-      hipLaunchKernelGGL(diag_carry<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, lam, x0, E, t.lanes,
-                         t.nsuper - 1, (int64_t)0, (int64_t)1, t.SL, 0);
+// Workspace of one scan: the tile counter (first 256 bytes), then agg [nsuper, lanes] maps and
+// inc [nsuper, lanes] states of the look-back, then (constant-coefficient backward) the glam
+// partials [nsuper, lanes].
+constexpr int64_t kCounterBytes = 256;
+inline int64_t lookback_bytes(const DiagTile& t, int64_t wbytes) { return t.nsuper * t.lanes * 3 * wbytes; }
+
+// Workgroups that stay resident at once (persistent grid size), per kernel and block size.
+template <typename F>
+int64_t resident_wgs(F kern, int threads, int* cache) {
+  int& c = cache[threads / 64];
+  if (c == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, 0) != hipSuccess || n < 1) n = 1;
+    c = n;
   }
-  hipLaunchKernelGGL((diag_fwd_apply<T, TC>), dim3((unsigned)(t.groups * t.nsuper)), blk, 0, s, lam, v, x0,
-                     (const typename Wide<T>::type*)E, out, t.lanes, L, N, t.groups, t.K, (int)t.carry_kernel);
+  return (int64_t)c * device_cus();
+}
+
+template <typename F>
+unsigned persistent_grid(const DiagTile& t, F kern, int* cache) {
+  const int64_t tiles = t.groups * t.nsuper, cap = resident_wgs(kern, 64 * t.K, cache);
+  return (unsigned)(tiles < cap ? tiles : cap);
+}
+
+void lookback_reset_launch(char* ws, int64_t words, hipStream_t s) {
+  int64_t blocks = (words + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 2048) blocks = 2048;
+  hipLaunchKernelGGL(lookback_reset, dim3((unsigned)blocks), dim3(256), 0, s,
+                     reinterpret_cast<uint64_t*>(ws + kCounterBytes), words, reinterpret_cast<unsigned*>(ws));
+}
+
+template <typename T, int TC>
+void diag_fwd_launch(const DiagTile& t, const T* lam, const T* v, const T* x0, T* out, char* ws, int64_t L, int64_t N,
+                     hipStream_t s) {
+  using W = typename Wide<T>::type;
+  static int occ[kMaxWaves + 1];
+  auto* agg = reinterpret_cast<Map<W>*>(ws + kCounterBytes);
+  auto* inc = reinterpret_cast<W*>(agg + t.nsuper * t.lanes);
+  lookback_reset_launch(ws, lookback_bytes(t, sizeof(W)) / 8, s);
+  hipLaunchKernelGGL((diag_fwd<T, TC>), dim3(persistent_grid(t, diag_fwd<T, TC>, occ)), dim3(64 * t.K), 0, s, lam, v,
+                     x0, out, agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper);
 }
 
 template <typename T, int TC>
 void diag_bwd_launch(const DiagTile& t, const T* g, const T* lam, const T* out, const T* x0, T* gv, T* glam, T* gx0,
-                     typename Wide<T>::type* F, typename Wide<T>::type* part, int64_t L, int64_t N, hipStream_t s) {
-  const dim3 blk(64 * t.K);
-  if (t.nsuper > 1) {
-    hipLaunchKernelGGL((diag_bwd_summary<T, TC>), dim3((unsigned)(t.groups * (t.nsuper - 1))), blk, 0, s, lam, g, F,
-                       t.lanes, L, N, t.groups, t.K);
-    if (t.carry_kernel)
-      hipLaunchKernelGGL(diag_carry<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, lam, (const T*)nullptr,
-                         F, t.lanes, t.nsuper - 1, t.nsuper - 1, (int64_t)-1, t.SL, 1);
-  }
-  hipLaunchKernelGGL((diag_bwd_apply<T, TC>), dim3((unsigned)(t.groups * t.nsuper)), blk, 0, s, lam, g, out, x0,
-                     (const typename Wide<T>::type*)F, gv, part, glam, gx0, t.lanes, L, N, t.groups, t.K, t.nsuper,
-                     (int)t.carry_kernel);
+                     char* ws, int64_t L, int64_t N, hipStream_t s) {
+  using W = typename Wide<T>::type;
+  static int occ[kMaxWaves + 1];
+  auto* agg = reinterpret_cast<Map<W>*>(ws + kCounterBytes);
+  auto* inc = reinterpret_cast<W*>(agg + t.nsuper * t.lanes);
+  W* part = inc + t.nsuper * t.lanes;
+  lookback_reset_launch(ws, lookback_bytes(t, sizeof(W)) / 8, s);
+  hipLaunchKernelGGL((diag_bwd<T, TC>), dim3(persistent_grid(t, diag_bwd<T, TC>, occ)), dim3(64 * t.K), 0, s, lam, g,
+                     out, x0, agg, inc, reinterpret_cast<unsigned*>(ws), gv, part, glam, gx0, t.lanes, L, N, t.groups,
+                     t.K, t.nsuper);
   if (t.nsuper > 1)
-    hipLaunchKernelGGL(diag_sum_parts<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s,
-                       (const typename Wide<T>::type*)part, glam, t.lanes, t.nsuper);
+    hipLaunchKernelGGL(diag_sum_parts<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, (const W*)part, glam,
+                       t.lanes, t.nsuper);
 }
 
-// The time-varying kernels use the same tiles; the backward keeps three TC-step arrays per
-// thread (g_t, a_{t+1}, x_{t-1}), so it always runs TC = 16.
-DiagTile sel_tile(int64_t lanes, int64_t L, bool bwd) { return diag_tile(lanes, L, bwd); }
-
 template <int TC>
-void sel_fwd_launch(const DiagTile& t, const float* a, const float* v, const float* x0, float* out, double2* E,
+void sel_fwd_launch(const DiagTile& t, const float* a, const float* v, const float* x0, float* out, char* ws,
                     int64_t L, int64_t N, hipStream_t s) {
-  const dim3 blk(64 * t.K);
-  if (t.nsuper > 1) {
-    hipLaunchKernelGGL((sel_fwd_summary<TC>), dim3((unsigned)(t.groups * (t.nsuper - 1))), blk, 0, s, a, v, E,
-                       t.lanes, L, N, t.groups, t.K);
-    if (t.carry_kernel)
-      hipLaunchKernelGGL(sel_carry, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, x0, E, t.lanes,
-                         t.nsuper - 1, (int64_t)0, (int64_t)1);
-  }
-  hipLaunchKernelGGL((sel_fwd_apply<TC>), dim3((unsigned)(t.groups * t.nsuper)), blk, 0, s, a, v, x0,
-                     (const double2*)E, out, t.lanes, L, N, t.groups, t.K, (int)t.carry_kernel);
+  static int occ[kMaxWaves + 1];
+  auto* agg = reinterpret_cast<Map<double>*>(ws + kCounterBytes);
+  auto* inc = reinterpret_cast<double*>(agg + t.nsuper * t.lanes);
+  lookback_reset_launch(ws, lookback_bytes(t, 8) / 8, s);
+  hipLaunchKernelGGL((sel_fwd<TC>), dim3(persistent_grid(t, sel_fwd<TC>, occ)), dim3(64 * t.K), 0, s, a, v, x0, out,
+                     agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper);
 }
 
 void sel_bwd_launch(const DiagTile& t, const float* g, const float* a, const float* out, const float* x0, float* glam,
-                    float* gv, float* gx0, double2* F, int64_t L, int64_t N, hipStream_t s) {
-  const dim3 blk(64 * t.K);
-  if (t.nsuper > 1) {
-    hipLaunchKernelGGL((sel_bwd_summary<16>), dim3((unsigned)(t.groups * (t.nsuper - 1))), blk, 0, s, a, g, F,
-                       t.lanes, L, N, t.groups, t.K);
-    if (t.carry_kernel)
-      hipLaunchKernelGGL(sel_carry, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, (const float*)nullptr, F,
-                         t.lanes, t.nsuper - 1, t.nsuper - 1, (int64_t)-1);
-  }
-  hipLaunchKernelGGL((sel_bwd_apply<16>), dim3((unsigned)(t.groups * t.nsuper)), blk, 0, s, a, g, out, x0,
-                     (const double2*)F, glam, gv, gx0, t.lanes, L, N, t.groups, t.K, t.nsuper, (int)t.carry_kernel);
+                    float* gv, float* gx0, char* ws, int64_t L, int64_t N, hipStream_t s) {
+  static int occ[kMaxWaves + 1];
+  auto* agg = reinterpret_cast<Map<double>*>(ws + kCounterBytes);
+  auto* inc = reinterpret_cast<double*>(agg + t.nsuper * t.lanes);
+  lookback_reset_launch(ws, lookback_bytes(t, 8) / 8, s);
+  hipLaunchKernelGGL((sel_bwd<16>), dim3(persistent_grid(t, sel_bwd<16>, occ)), dim3(64 * t.K), 0, s, a, g, out, x0,
+                     agg, inc, reinterpret_cast<unsigned*>(ws), glam, gv, gx0, t.lanes, L, N, t.groups, t.K,
+                     t.nsuper);
 }
 
 }  // namespace
@@ -761,10 +835,10 @@ void sel_bwd_launch(const DiagTile& t, const float* g, const float* a, const flo
 extern "C" {
 
 int64_t tsfast_hip_diag_workspace_bytes(int64_t M, int64_t L, int64_t N, int is_complex) {
-  const DiagTile t = diag_tile(M * N, L, is_complex != 0);
-  // fp64 super-chunk summaries [nsuper, lanes] plus fp64 glam partials [nsuper, lanes]
-  // (complex128 when complex)
-  return 2 * t.nsuper * t.lanes * (is_complex ? 16 : 8);
+  const DiagTile f = const_tile(M * N, L, is_complex != 0, false), b = const_tile(M * N, L, is_complex != 0, true);
+  // counter, then fp64 look-back maps and states and glam partials, 4 words per lane and
+  // super-chunk (complex128 when complex), for the larger of the forward / backward tilings
+  return kCounterBytes + 4 * (f.nsuper > b.nsuper ? f.nsuper : b.nsuper) * M * N * (is_complex ? 16 : 8);
 }
 
 int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const void* lam, const void* v,
@@ -773,18 +847,16 @@ int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   if (M == 0 || L == 0 || N == 0) return TSF_OK;
   if (!lam || !v || !out) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
-  const DiagTile t = diag_tile(M * N, L, is_complex != 0);
+  const DiagTile t = const_tile(M * N, L, is_complex != 0, false);
   if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
   if (is_complex)
-    diag_fwd_launch<float2, 16>(t, (const float2*)lam, (const float2*)v, (const float2*)x0, (float2*)out,
-                                static_cast<double2*>(workspace), L, N, s);
+    diag_fwd_launch<float2, 16>(t, (const float2*)lam, (const float2*)v, (const float2*)x0, (float2*)out, ws, L, N, s);
   else if (t.TC == 32)
-    diag_fwd_launch<float, 32>(t, (const float*)lam, (const float*)v, (const float*)x0, (float*)out,
-                               static_cast<double*>(workspace), L, N, s);
+    diag_fwd_launch<float, 32>(t, (const float*)lam, (const float*)v, (const float*)x0, (float*)out, ws, L, N, s);
   else
-    diag_fwd_launch<float, 16>(t, (const float*)lam, (const float*)v, (const float*)x0, (float*)out,
-                               static_cast<double*>(workspace), L, N, s);
+    diag_fwd_launch<float, 16>(t, (const float*)lam, (const float*)v, (const float*)x0, (float*)out, ws, L, N, s);
   return tsf_launch_status();
 }
 
@@ -805,28 +877,26 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   }
   if (!g || !out || !gv) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
-  const DiagTile t = diag_tile(lanes, L, is_complex != 0);
+  const DiagTile t = const_tile(lanes, L, is_complex != 0, true);
   if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
-  if (is_complex) {
-    auto* F = static_cast<double2*>(workspace);
+  char* ws = static_cast<char*>(workspace);
+  if (is_complex)
     diag_bwd_launch<float2, 16>(t, (const float2*)g, (const float2*)lam, (const float2*)out, (const float2*)x0,
-                                (float2*)gv, (float2*)glam, (float2*)gx0, F, F + t.nsuper * lanes, L, N, s);
-  } else {
-    auto* F = static_cast<double*>(workspace);
-    if (t.TC == 32)
-      diag_bwd_launch<float, 32>(t, (const float*)g, (const float*)lam, (const float*)out, (const float*)x0,
-                                 (float*)gv, (float*)glam, (float*)gx0, F, F + t.nsuper * lanes, L, N, s);
-    else
-      diag_bwd_launch<float, 16>(t, (const float*)g, (const float*)lam, (const float*)out, (const float*)x0,
-                                 (float*)gv, (float*)glam, (float*)gx0, F, F + t.nsuper * lanes, L, N, s);
-  }
+                                (float2*)gv, (float2*)glam, (float2*)gx0, ws, L, N, s);
+  else if (t.TC == 32)
+    diag_bwd_launch<float, 32>(t, (const float*)g, (const float*)lam, (const float*)out, (const float*)x0, (float*)gv,
+                               (float*)glam, (float*)gx0, ws, L, N, s);
+  else
+    diag_bwd_launch<float, 16>(t, (const float*)g, (const float*)lam, (const float*)out, (const float*)x0, (float*)gv,
+                               (float*)glam, (float*)gx0, ws, L, N, s);
   return tsf_launch_status();
 }
 
 int64_t tsfast_hip_sel_workspace_bytes(int64_t M, int64_t L, int64_t N) {
-  // fp64 (product, state) maps [nsuper, lanes] for the larger of the forward / backward tilings
+  // counter, then fp64 look-back maps (P, e) and states, 3 words per lane and super-chunk, for
+  // the larger of the forward / backward tilings
   const DiagTile f = sel_tile(M * N, L, false), b = sel_tile(M * N, L, true);
-  return (f.nsuper > b.nsuper ? f.nsuper : b.nsuper) * M * N * 16;
+  return kCounterBytes + (f.nsuper > b.nsuper ? f.nsuper : b.nsuper) * M * N * 24;
 }
 
 int tsfast_hip_sel_fwd(int64_t M, int64_t L, int64_t N, const float* a, const float* v, const float* x0, float* out,
@@ -838,11 +908,11 @@ int tsfast_hip_sel_fwd(int64_t M, int64_t L, int64_t N, const float* a, const fl
   const DiagTile t = sel_tile(M * N, L, false);
   if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  auto* E = static_cast<double2*>(workspace);
+  char* ws = static_cast<char*>(workspace);
   if (t.TC == 32)
-    sel_fwd_launch<32>(t, a, v, x0, out, E, L, N, s);
+    sel_fwd_launch<32>(t, a, v, x0, out, ws, L, N, s);
   else
-    sel_fwd_launch<16>(t, a, v, x0, out, E, L, N, s);
+    sel_fwd_launch<16>(t, a, v, x0, out, ws, L, N, s);
   return tsf_launch_status();
 }
 
@@ -862,7 +932,7 @@ int tsfast_hip_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const fl
   if (workspace_bytes < tsfast_hip_sel_workspace_bytes(M, L, N) || !workspace) return TSF_ERR_WORKSPACE;
   const DiagTile t = sel_tile(lanes, L, true);
   if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
-  sel_bwd_launch(t, g, a, out, x0, glam, gv, gx0, static_cast<double2*>(workspace), L, N, s);
+  sel_bwd_launch(t, g, a, out, x0, glam, gv, gx0, static_cast<char*>(workspace), L, N, s);
   return tsf_launch_status();
 }
 

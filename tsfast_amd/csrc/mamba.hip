@@ -97,18 +97,6 @@ TSF_DEV void set_wave_priority(unsigned p) {
   }
 }
 
-// Compute units of the current device (queried once per device).
-unsigned device_cus() {
-  static unsigned cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = (unsigned)n;
-  }
-  return cache[dev];
-}
 
 // Streaming store for the training forward's saved state, which is read back only by the
 // backward (non-temporal: it is not kept in the caches on the way out).
