@@ -45,13 +45,21 @@ CFG3 = dict(B=16, L=4096, D=1536, N=16)
 
 # HBM bytes per call measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on the default bench
 # workload, each scaled by the same counter on a 512 MiB elementwise copy (FETCH x 2.0, WRITE
-# x 1.0): (config, I/O dtype) -> {phase: (bytes, source)}. Counters cannot be read from inside
+# x 1.0): (config number or "selective", I/O dtype) -> {phase: (bytes, source)}. Counters cannot be read from inside
 # this process, so the figures come from the committed summary and must be re-measured when the
 # kernels change.
 MEASURED_TRAFFIC = {
     (3, "bf16"): {
         "fwd": (2_083_282_000, "profiles/mamba_scan_config3_traffic.md"),
         "bwd": (3_736_450_000, "profiles/mamba_scan_config3_traffic.md"),
+    },
+    (2, "f32"): {
+        "fwd": (1_139_400_000, "profiles/diag_scan_config2_traffic.md"),
+        "bwd": (1_686_700_000, "profiles/diag_scan_config2_traffic.md"),
+    },
+    ("selective", "f32"): {
+        "fwd": (1_631_000_000, "profiles/selective_scan_traffic.md"),
+        "bwd": (2_727_900_000, "profiles/selective_scan_traffic.md"),
     },
 }
 
@@ -289,8 +297,8 @@ def run_diag(args, line):
     line.update(config={"workload": workload, "M": M, "L": L, "N": N, "io_dtype": "complex64" if cplx else "f32"},
                 fwd_ms=round(fwd_ms, 4), bwd_ms=round(bwd_ms, 4))
     line["dtype"] = "c128" if cplx else "f64"  # fp32/complex64 I/O, fp64 state inside
-    kernels = {"fwd": ("diag fwd (chunk summaries + re-scan)", fwd_ms, fwd_b),
-               "bwd": ("diag bwd (chunk summaries + re-scan + lane sums)", bwd_ms, bwd_b)}
+    kernels = {"fwd": ("diag_fwd look-back scan + workspace reset", fwd_ms, fwd_b),
+               "bwd": ("diag_bwd look-back scan + reset + glam lane sums", bwd_ms, bwd_b)}
     cpu = None
     if not args.no_cpu:
         def cpu_leg():
@@ -413,8 +421,8 @@ def run_selective(args, line):
     )
     line["metric"] = "fwd+bwd ms + achieved HBM GB/s, selective scan [16, 4096, 2048] fp32"
     line["dtype"] = "f64"  # fp32 I/O, fp64 state inside
-    kernels = {"fwd": ("sel fwd (chunk maps + re-scan)", fwd_ms, fwd_b),
-               "bwd": ("sel bwd (chunk maps + re-scan)", bwd_ms, bwd_b)}
+    kernels = {"fwd": ("sel_fwd look-back scan + workspace reset", fwd_ms, fwd_b),
+               "bwd": ("sel_bwd look-back scan + workspace reset", bwd_ms, bwd_b)}
     cpu = None
     if not args.no_cpu:
         def cpu_leg():
@@ -555,7 +563,8 @@ def main():
     phase = max(kernels, key=lambda k: kernels[k][1])
     name, dom_ms, dom_b = kernels[phase]
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
-    measured = None if (args.conv or args.selective) else MEASURED_TRAFFIC.get((args.config, args.io if args.config == 3 else "f32"), {}).get(phase)
+    key = ("selective", "f32") if args.selective else (args.config, args.io if args.config == 3 else "f32")
+    measured = None if args.conv else MEASURED_TRAFFIC.get(key, {}).get(phase)
     line["roofline"] = {
         "bound": "hbm",
         "kernel": name,

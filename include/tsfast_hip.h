@@ -44,6 +44,9 @@ int tsfast_hip_version(void);
  * (forward(lam, v, x0) / backward(g, lam, out, x0)), reached from the tsfast::scan_diagonal ops
  * (tsfast/models/_core/scan.py:100-154).
  * Layout: lam [M, N], v/out/g/gv [M, L, N], x0/gx0/glam [M, N]; float32 or complex64.
+ * Single-pass kernels with an inter-workgroup look-back: the workspace holds the tile counter and
+ * the published super-chunk states; each call re-initialises it on its stream (no caller set-up),
+ * so two calls in flight at once must not share one workspace.
  */
 int64_t tsfast_hip_diag_workspace_bytes(int64_t M, int64_t L, int64_t N, int is_complex);
 int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const void* lam, const void* v,
@@ -57,7 +60,7 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
  * Time-varying (selective) diagonal scan  x_t = a_t * x_{t-1} + v_t  and its adjoint, float32.
  * Replaces tsfast/models/_core/scan_backends/selective_triton.py:112-160 (forward / backward),
  * reached from the tsfast::scan_selective ops (tsfast/models/_core/scan.py:157-215).
- * Layout: a/v/out/g/gv/glam [M, L, N], x0/gx0 [M, N].
+ * Layout: a/v/out/g/gv/glam [M, L, N], x0/gx0 [M, N]. Workspace as for the diagonal scan.
  */
 int64_t tsfast_hip_sel_workspace_bytes(int64_t M, int64_t L, int64_t N);
 int tsfast_hip_sel_fwd(int64_t M, int64_t L, int64_t N, const float* a, const float* v, const float* x0, float* out,

@@ -2,8 +2,9 @@
 
 Drop-in for the ``diagonal`` family of ``tsfast/models/_core/scan.py:32-42`` (the role of
 ``scan_backends/diagonal_triton.py:236-305``). Lane layout: lam ``[M, N]``, v ``[M, L, N]``,
-x0 ``[M, N]``, contiguous, on the GPU. The kernels (``csrc/diag.hip``) run a chunked two-pass
-scan: chunk-end summaries, then a re-scan of every chunk from its composed start state.
+x0 ``[M, N]``, contiguous, on the GPU. The kernels (``csrc/diag.hip``) are single-pass scans with
+a decoupled look-back between workgroups: each tile of lanes x steps publishes its summary, takes
+its start state from the tiles before it and re-scans its chunk from registers.
 """
 
 from __future__ import annotations

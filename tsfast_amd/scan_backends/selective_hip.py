@@ -2,7 +2,8 @@
 
 Drop-in for the ``selective`` family of ``tsfast/models/_core/scan.py:32-42`` (the role of
 ``scan_backends/selective_triton.py:112-160``). Lane layout: lam and v ``[M, L, N]``, x0
-``[M, N]``. Kernels in ``csrc/diag.hip`` (chunk summaries carry the coefficient product).
+``[M, N]``. Kernels in ``csrc/diag.hip``: single-pass look-back scans whose chunk summaries are
+(coefficient product, state) affine maps.
 """
 
 from __future__ import annotations
