@@ -463,8 +463,8 @@ def run_allpole(args, line):
     line.update(config={"workload": "dynoNet all-pole IIR scan fwd+bwd, na=3, BASELINE config 4",
                         "lanes": lanes, "L": L, "na": 3}, fwd_ms=round(fwd_ms, 4), bwd_ms=round(bwd_ms, 4))
     line["dtype"] = "f64"  # fp32 I/O, fp64 recurrence inside
-    kernels = {"fwd": ("allpole fwd (transfer + chunk ends + carries + apply)", fwd_ms, fwd_b),
-               "bwd": ("allpole bwd", bwd_ms, bwd_b)}
+    kernels = {"fwd": ("allpole_fwd_lb look-back scan + transfer + reset", fwd_ms, fwd_b),
+               "bwd": ("allpole_bwd_lb look-back scan + transfer + reset + finish", bwd_ms, bwd_b)}
     cpu = None
     if not args.no_cpu:
         def cpu_leg():

@@ -112,7 +112,8 @@ int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
  * Replaces the generated kernels of tsfast/models/architectures/dynonet/allpole_triton.py:59-233
  * (tsfast::dynonet_allpole / dynonet_allpole_bwd, including the host-side y0 head taps at :202-213).
  * Layout: a [lanes, na], w/y/g/gw [lanes, L] (time contiguous), y0/gy0 [lanes, na] newest first
- * (y0[j] = y_{-1-j}).
+ * (y0[j] = y_{-1-j}). For na <= 4 the workspace also carries the look-back state of a single-pass
+ * scan, re-initialised by each call on its stream: two calls in flight must not share one.
  */
 int64_t tsfast_hip_allpole_workspace_bytes(int64_t lanes, int64_t L, int64_t na);
 int tsfast_hip_allpole_fwd(int64_t lanes, int64_t L, int64_t na, const float* a, const float* w, const float* y0,

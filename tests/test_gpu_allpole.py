@@ -27,6 +27,13 @@ _SHAPES = [
     (1, 1, 513, 1),
     (2, 3, 300, 16),
     (8, 64, 16384, 3),  # config 4 with the batch reduced from 64 to 8
+    # single-pass look-back path (na <= 4): many super-chunks, lanes off multiples of 64,
+    # sequence lengths off multiples of the 32-step chunk
+    (3, 50, 5000, 3),
+    (2, 100, 3333, 4),
+    (1, 70, 20000, 1),
+    (5, 13, 4100, 2),
+    (4, 20, 2000, 6),  # two-pass path (na > 4) with several chunks
 ]
 
 

@@ -12,17 +12,18 @@
 // accumulators). High-order direct-form filters amplify fp32 rounding badly (order 16 with
 // poles near 0.98 loses ~3 digits), and the scan is HBM-bound, so the wider state is free.
 //
-// Parallel structure: time is cut into chunks of T_c steps and every (lane, chunk) pair is a
-// thread. The state entering a chunk is the last NA outputs before it. A chunk maps its
-// entering state s to  M s + e,  with M = C^{T_c} the companion matrix raised to the chunk
-// length and e the chunk's zero-state end, so:
-//   1. transfer   per lane: M by binary powering of C (NA x NA), stored in the workspace;
+// Parallel structure. A chunk of steps maps its entering state s (the last NA outputs before it)
+// to M s + e, with M a power of the companion matrix C and e the chunk's zero-state end. Orders
+// NA <= 4 run single-pass kernels with a decoupled look-back between workgroups (every input
+// element read once; described at allpole_fwd_lb). Higher orders, whose NA x NA matrices do not
+// fit in registers, run a two-pass scan with chunks of T_c steps, one thread per (lane, chunk):
+//   1. transfer   per lane: M = C^{T_c} by binary powering, stored in the workspace;
 //   2. chunk_end  per (lane, chunk): e_c from a zero entering state;
 //   3. carry      per lane: entering states S_c = M S_{c-1} + e_{c-1}, sequential over chunks;
 //   4. apply      per (lane, chunk): run the chunk from S_c and write y.
 // The adjoint G_t = g_t - sum_i a_i G_{t+i} is the same filter run backwards, so the backward
-// reuses M with the chunk order reversed, accumulates grad_a partials per chunk, and a final
-// per-lane kernel adds the y0 head taps and grad_y0.
+// reuses the matrices with the chunk order reversed and accumulates grad_a partials per chunk;
+// a final cooperative kernel sums them in a fixed order and adds the y0 head taps and grad_y0.
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -31,6 +32,8 @@ using namespace tsf;
 namespace {
 
 constexpr int kMaxNA = 16;
+
+#include "lookback.h"
 
 inline dim3 grid_for(int64_t threads) { return dim3((unsigned)((threads + 255) / 256)); }
 
@@ -60,23 +63,24 @@ constexpr int kTileT = 32;  // time steps per tile (tile columns)
 struct TileRegs {
   float v[kTile / 2];
 };
+// `lid` is the thread's lane within its wave (the tile belongs to one wave).
 TSF_DEV void tile_fetch(TileRegs& rg, const float* __restrict__ src, int64_t lanes, int64_t L, int64_t l0, int64_t c0,
-                        int ncol) {
-  const int col = threadIdx.x & (kTileT - 1), half = threadIdx.x >> 5;
+                        int ncol, int lid) {
+  const int col = lid & (kTileT - 1), half = lid >> 5;
 #pragma unroll
   for (int r2 = 0; r2 < kTile / 2; ++r2) {
     const int64_t lane = l0 + 2 * r2 + half;
     rg.v[r2] = (lane < lanes && col < ncol) ? src[lane * L + c0 + col] : 0.0f;
   }
 }
-TSF_DEV void tile_put(const TileRegs& rg, float (*tile)[kTileT + 1]) {
-  const int col = threadIdx.x & (kTileT - 1), half = threadIdx.x >> 5;
+TSF_DEV void tile_put(const TileRegs& rg, float (*tile)[kTileT + 1], int lid) {
+  const int col = lid & (kTileT - 1), half = lid >> 5;
 #pragma unroll
   for (int r2 = 0; r2 < kTile / 2; ++r2) tile[2 * r2 + half][col] = rg.v[r2];
 }
 TSF_DEV void tile_store(float (*tile)[kTileT + 1], float* __restrict__ dst, int64_t lanes, int64_t L, int64_t l0,
-                        int64_t c0, int ncol) {
-  const int col = threadIdx.x & (kTileT - 1), half = threadIdx.x >> 5;
+                        int64_t c0, int ncol, int lid) {
+  const int col = lid & (kTileT - 1), half = lid >> 5;
 #pragma unroll 8
   for (int r2 = 0; r2 < kTile / 2; ++r2) {
     const int r = 2 * r2 + half;
@@ -173,13 +177,13 @@ __global__ void __launch_bounds__(kTile) allpole_fwd_chunk_end(const float* __re
   }
   const int64_t t0 = c * T_c;
   TileRegs rg;
-  tile_fetch(rg, w, lanes, L, l0, t0, (int)(T_c < kTileT ? T_c : kTileT));
+  tile_fetch(rg, w, lanes, L, l0, t0, (int)(T_c < kTileT ? T_c : kTileT), tid);
   for (int64_t tt = 0; tt < T_c; tt += kTileT) {
     const int n = (int)((T_c - tt) < kTileT ? (T_c - tt) : kTileT);
-    tile_put(rg, tile);
+    tile_put(rg, tile, tid);
     __syncthreads();
     if (tt + kTileT < T_c)
-      tile_fetch(rg, w, lanes, L, l0, t0 + tt + kTileT, (int)((T_c - tt - kTileT) < kTileT ? (T_c - tt - kTileT) : kTileT));
+      tile_fetch(rg, w, lanes, L, l0, t0 + tt + kTileT, (int)((T_c - tt - kTileT) < kTileT ? (T_c - tt - kTileT) : kTileT), tid);
     if (n == kTileT) {
 #pragma unroll
       for (int k = 0; k < kTileT; ++k) step<NA>(av, s, (double)tile[tid][k]);
@@ -244,13 +248,13 @@ __global__ void __launch_bounds__(kTile) allpole_fwd_apply(const float* __restri
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   TileRegs rg;
-  tile_fetch(rg, w, lanes, L, l0, t0, (int)(len < kTileT ? len : kTileT));
+  tile_fetch(rg, w, lanes, L, l0, t0, (int)(len < kTileT ? len : kTileT), tid);
   for (int64_t tt = 0; tt < len; tt += kTileT) {
     const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
-    tile_put(rg, tile);
+    tile_put(rg, tile, tid);
     __syncthreads();
     if (tt + kTileT < len)
-      tile_fetch(rg, w, lanes, L, l0, t0 + tt + kTileT, (int)((len - tt - kTileT) < kTileT ? (len - tt - kTileT) : kTileT));
+      tile_fetch(rg, w, lanes, L, l0, t0 + tt + kTileT, (int)((len - tt - kTileT) < kTileT ? (len - tt - kTileT) : kTileT), tid);
     if (n == kTileT) {
 #pragma unroll
       for (int k = 0; k < kTileT; ++k) tile[tid][k] = (float)step<NA>(av, s, (double)tile[tid][k]);
@@ -258,7 +262,7 @@ __global__ void __launch_bounds__(kTile) allpole_fwd_apply(const float* __restri
       for (int k = 0; k < n; ++k) tile[tid][k] = (float)step<NA>(av, s, (double)tile[tid][k]);
     }
     __syncthreads();
-    tile_store(tile, y, lanes, L, l0, t0 + tt, n);
+    tile_store(tile, y, lanes, L, l0, t0 + tt, n, tid);
     __syncthreads();
   }
 }
@@ -284,12 +288,12 @@ __global__ void __launch_bounds__(kTile) allpole_bwd_chunk_start(const float* __
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const int64_t last = ((len - 1) / kTileT) * kTileT;
   TileRegs rg;
-  tile_fetch(rg, g, lanes, L, l0, t0 + last, (int)((len - last) < kTileT ? (len - last) : kTileT));
+  tile_fetch(rg, g, lanes, L, l0, t0 + last, (int)((len - last) < kTileT ? (len - last) : kTileT), tid);
   for (int64_t tt = last; tt >= 0; tt -= kTileT) {
     const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
-    tile_put(rg, tile);
+    tile_put(rg, tile, tid);
     __syncthreads();
-    if (tt > 0) tile_fetch(rg, g, lanes, L, l0, t0 + tt - kTileT, kTileT);
+    if (tt > 0) tile_fetch(rg, g, lanes, L, l0, t0 + tt - kTileT, kTileT, tid);
     if (n == kTileT) {
 #pragma unroll
       for (int k = kTileT - 1; k >= 0; --k) step<NA>(av, s, (double)tile[tid][k]);
@@ -364,17 +368,17 @@ __global__ void __launch_bounds__(kTile) allpole_bwd_apply(const float* __restri
   TileRegs rgg, rgy;
   {
     const int n0 = (int)((len - last) < kTileT ? (len - last) : kTileT);
-    tile_fetch(rgg, g, lanes, L, l0, t0 + last, n0);
-    tile_fetch(rgy, y, lanes, L, l0, t0 + last, n0);
+    tile_fetch(rgg, g, lanes, L, l0, t0 + last, n0, tid);
+    tile_fetch(rgy, y, lanes, L, l0, t0 + last, n0, tid);
   }
   for (int64_t tt = last; tt >= 0; tt -= kTileT) {
     const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
-    tile_put(rgg, tg);
-    tile_put(rgy, ty);
+    tile_put(rgg, tg, tid);
+    tile_put(rgy, ty, tid);
     __syncthreads();
     if (tt > 0) {
-      tile_fetch(rgg, g, lanes, L, l0, t0 + tt - kTileT, kTileT);
-      tile_fetch(rgy, y, lanes, L, l0, t0 + tt - kTileT, kTileT);
+      tile_fetch(rgg, g, lanes, L, l0, t0 + tt - kTileT, kTileT, tid);
+      tile_fetch(rgy, y, lanes, L, l0, t0 + tt - kTileT, kTileT, tid);
     }
     auto bstep = [&](int k) __attribute__((always_inline)) {
       const double yu = ty[tid][k];
@@ -389,7 +393,7 @@ __global__ void __launch_bounds__(kTile) allpole_bwd_apply(const float* __restri
       for (int k = n - 1; k >= 0; --k) bstep(k);
     }
     __syncthreads();
-    tile_store(tg, gw, lanes, L, l0, t0 + tt, n);
+    tile_store(tg, gw, lanes, L, l0, t0 + tt, n, tid);
     __syncthreads();
   }
   if (act) {
@@ -398,36 +402,509 @@ __global__ void __launch_bounds__(kTile) allpole_bwd_apply(const float* __restri
   }
 }
 
-// Backward 5. per lane: grad_a = -(sum of chunk partials + y0 head taps), grad_y0.
+// ---------------------------------------------------------------- single-pass path, NA <= kLbNA
+// For low orders the forward and backward are single-pass kernels with a decoupled look-back
+// between workgroups (the protocol of lookback.h), so every input element is read once from HBM.
+// A tile is 64 lanes x one super-chunk of K x 32 steps; wave k of the workgroup owns the k-th
+// 32-step chunk: it moves the chunk through its own [64 x 33] LDS tile into registers (each
+// thread then holds 32 values of its lane's row), summarises it from a zero state, and re-runs
+// it from its true entering state once that is known. A chunk maps its entering state s to
+// Mc s + e (Mc = C^32), a super-chunk to Ms s + e (Ms = C^(32 K)); both matrices come from
+// allpole_transfer2. Only the e vectors are published: agg = a super-chunk's e from a zero
+// state, inc = the state leaving it. Between the tile's barriers a wave's LDS tile is reused as
+// two fp64 areas: vec [64][NA] (chunk summary -> entering state -> grad_a partial) and
+// slot [64][NA] (its look-back window entry).
+constexpr int kLbNA = 4;     // highest order on the single-pass path (matrices stay in registers)
+#ifndef TSF_AP_KMAX
+#define TSF_AP_KMAX 8
+#endif
+constexpr int kLbWaves = TSF_AP_KMAX;  // chunks per tile at most (sizes the LDS of a workgroup)
+
+using LdsTile = float[kTile][kTileT + 1];
+
 template <int NA>
-__global__ void __launch_bounds__(256) allpole_bwd_finish(const float* __restrict__ a, const float* __restrict__ gw,
-                                                          const float* __restrict__ y0,
-                                                          const double* __restrict__ ga_part, float* __restrict__ ga,
-                                                          float* __restrict__ gy0, int64_t lanes, int64_t L,
-                                                          int64_t nchunk) {
+TSF_DEV double* vec_area(LdsTile* lds, int wv) {
+  return reinterpret_cast<double*>(&lds[wv][0][0]);
+}
+template <int NA>
+TSF_DEV double* slot_area(LdsTile* lds, int wv) {
+  return reinterpret_cast<double*>(&lds[wv][0][0]) + 64 * kLbNA;
+}
+
+template <int NA>
+TSF_DEV void load_mat(double (&m)[NA][NA], const double* __restrict__ src) {
+#pragma unroll
+  for (int r = 0; r < NA; ++r)
+#pragma unroll
+    for (int c = 0; c < NA; ++c) m[r][c] = src[r * NA + c];
+}
+template <int NA>
+TSF_DEV void matvec_add(double (&out)[NA], const double (&m)[NA][NA], const double (&x)[NA], const double (&b)[NA]) {
+  double t[NA];
+#pragma unroll
+  for (int r = 0; r < NA; ++r) {
+    double acc = b[r];
+#pragma unroll
+    for (int c = 0; c < NA; ++c) acc = fma(m[r][c], x[c], acc);
+    t[r] = acc;
+  }
+#pragma unroll
+  for (int r = 0; r < NA; ++r) out[r] = t[r];
+}
+
+// Both transfer matrices per lane: Mc = C^32 and Ms = Mc^K (row-major, [lanes][NA][NA] each).
+template <int NA>
+__global__ void __launch_bounds__(256) allpole_transfer2(const float* __restrict__ a, double* __restrict__ Mc,
+                                                         double* __restrict__ Ms, int64_t lanes, int K) {
   const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (lane >= lanes) return;
+  double P[NA][NA], R[NA][NA], T[NA][NA];
+  auto mul = [&](double (&dst)[NA][NA], const double (&x)[NA][NA], const double (&y)[NA][NA]) {
+#pragma unroll
+    for (int r = 0; r < NA; ++r)
+#pragma unroll
+      for (int c = 0; c < NA; ++c) {
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < NA; ++j) s = fma(x[r][j], y[j][c], s);
+        T[r][c] = s;
+      }
+#pragma unroll
+    for (int r = 0; r < NA; ++r)
+#pragma unroll
+      for (int c = 0; c < NA; ++c) dst[r][c] = T[r][c];
+  };
+#pragma unroll
+  for (int r = 0; r < NA; ++r)
+#pragma unroll
+    for (int c = 0; c < NA; ++c) P[r][c] = (r == 0) ? -(double)a[lane * NA + c] : (c == r - 1 ? 1.0 : 0.0);
+  for (int i = 0; i < 5; ++i) mul(P, P, P);  // C^32
+#pragma unroll
+  for (int r = 0; r < NA; ++r)
+#pragma unroll
+    for (int c = 0; c < NA; ++c) {
+      Mc[(lane * NA + r) * NA + c] = P[r][c];
+      R[r][c] = (r == c) ? 1.0 : 0.0;
+    }
+  for (int k = K; k > 0; k >>= 1) {
+    if (k & 1) mul(R, R, P);
+    if (k > 1) mul(P, P, P);
+  }
+#pragma unroll
+  for (int r = 0; r < NA; ++r)
+#pragma unroll
+    for (int c = 0; c < NA; ++c) Ms[(lane * NA + r) * NA + c] = R[r][c];
+}
+
+template <int NA>
+TSF_DEV bool get_vec(const double* __restrict__ p, double (&x)[NA]) {
+  bool ok = true;
+#pragma unroll
+  for (int q = 0; q < NA; ++q) ok = get_word(p + q, x[q]) && ok;
+  return ok;
+}
+template <int NA>
+TSF_DEV void put_vec(double* p, const double (&x)[NA]) {
+#pragma unroll
+  for (int q = 0; q < NA; ++q) put_word(p + q, x[q]);
+}
+
+// State entering a super-chunk (result in wave 0's lanes), by looking back over the super-chunks
+// before it in scan order: pos0 is the nearest, dj the step away from it; the words of slot r of
+// a lane are at (r * lanes + lane) * NA. Called by every thread of the workgroup (it holds
+// barriers). Wave 0 first probes the nearest inc. Pending lanes then go through rounds in which
+// wave w reads slot pos0 + w dj (its inc, else its agg) into its slot area, and wave 0 looks for
+// an inc at some slot w* with published aggs at every slot before it: the entering state is then
+// Horner's rule back from that inc (s <- Ms s + agg). Otherwise the round is repeated. Every
+// wait ends: the nearest super-chunk publishes its inc once its own look-back ends, and the first
+// one in scan order publishes its inc without looking back (the window never has to move); a
+// lane without progress for kSpinMax rounds gives up with NaN.
+template <int NA>
+TSF_DEV void ap_look_back(double (&S)[NA], const double* __restrict__ agg, const double* __restrict__ inc,
+                          const double* __restrict__ MsLane, bool need, int64_t pos0, int64_t dj, int64_t nsuper,
+                          int64_t lanes, int64_t lane, int K, int k, int lid, LdsTile* lds, int (*flag)[64],
+                          int* pend_s, int* any_s) {
+  uint32_t spins = 0;
+  if (k == 0) {
+    int p = 0;
+    if (need) {
+      double x[NA];
+      if (get_vec<NA>(inc + (pos0 * lanes + lane) * NA, x)) {
+#pragma unroll
+        for (int q = 0; q < NA; ++q) S[q] = x[q];
+      } else {
+        p = 1;
+      }
+    }
+    pend_s[lid] = p;
+    const bool any = __any(p != 0);
+    if (lid == 0) *any_s = any ? 1 : 0;
+  }
+  __syncthreads();
+  while (*any_s) {
+    if (pend_s[lid]) {
+      const int64_t r = pos0 + dj * k;
+      int f = 0;
+      double* sl = slot_area<NA>(lds, k) + lid * NA;
+      if (r >= 0 && r < nsuper) {
+        double xi[NA], xa[NA];
+        const bool hi = get_vec<NA>(inc + (r * lanes + lane) * NA, xi);
+        const bool ha = get_vec<NA>(agg + (r * lanes + lane) * NA, xa);
+        if (hi || ha) {
+          f = hi ? 2 : 1;
+#pragma unroll
+          for (int q = 0; q < NA; ++q) sl[q] = hi ? xi[q] : xa[q];
+        }
+      }
+      flag[k][lid] = f;
+    }
+    __syncthreads();
+    if (k == 0) {
+      bool pending = false;
+      if (pend_s[lid]) {
+        int w = 0;
+        for (; w < K; ++w)
+          if (flag[w][lid] != 1) break;
+        if (w < K && flag[w][lid] == 2) {
+          double ms[NA][NA];
+          load_mat<NA>(ms, MsLane);
+          const double* sw = slot_area<NA>(lds, w) + lid * NA;
+#pragma unroll
+          for (int q = 0; q < NA; ++q) S[q] = sw[q];
+          for (int v = w - 1; v >= 0; --v) {
+            double ag[NA];
+            const double* sv = slot_area<NA>(lds, v) + lid * NA;
+#pragma unroll
+            for (int q = 0; q < NA; ++q) ag[q] = sv[q];
+            matvec_add<NA>(S, ms, S, ag);
+          }
+        } else if (++spins > kSpinMax) {
+#pragma unroll
+          for (int q = 0; q < NA; ++q) S[q] = quiet_nan<double>();
+        } else {
+          pending = true;
+        }
+        pend_s[lid] = pending ? 1 : 0;
+      }
+      const bool any = __any(pending);
+      if (lid == 0) *any_s = any ? 1 : 0;
+    }
+    __syncthreads();
+  }
+}
+
+// Loads the chunk [t0, t0 + n) of the wave's 64 rows through its LDS tile into xb (this
+// thread's row). Cooperative over the wave.
+TSF_DEV void chunk_to_regs(float (&xb)[kTileT], const float* __restrict__ src, int64_t lanes, int64_t L, int64_t l0,
+                           int64_t t0, int n, float (*tile)[kTileT + 1], int lid) {
+  TileRegs rg;
+  tile_fetch(rg, src, lanes, L, l0, t0, n, lid);
+  tile_put(rg, tile, lid);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < kTileT; ++i) xb[i] = tile[lid][i];
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Stores xb (this thread's row) as the chunk [t0, t0 + n) of the wave's 64 rows, through its LDS
+// tile. Cooperative over the wave.
+TSF_DEV void regs_to_chunk(const float (&xb)[kTileT], float* __restrict__ dst, int64_t lanes, int64_t L, int64_t l0,
+                           int64_t t0, int n, float (*tile)[kTileT + 1], int lid) {
+#pragma unroll
+  for (int i = 0; i < kTileT; ++i) tile[lid][i] = xb[i];
+  __builtin_amdgcn_wave_barrier();
+  tile_store(tile, dst, lanes, L, l0, t0, n, lid);
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int NA>
+__global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
+    const float* __restrict__ a, const float* __restrict__ w, const float* __restrict__ y0, float* __restrict__ y,
+    const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
+    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper) {
+  __shared__ LdsTile s_lds[kLbWaves];
+  __shared__ int s_flag[kLbWaves][64];
+  __shared__ int s_pend[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
+  __syncthreads();
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t sc = tile / groups, l0 = (tile - sc * groups) * kTile, lane = l0 + lid;
+    const bool live = lane < lanes;
+    const int64_t t0 = sc * SL + (int64_t)k * kTileT;
+    const int n = (L - t0) >= kTileT ? kTileT : (L - t0) > 0 ? (int)(L - t0) : 0;
+    double av[NA], s[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      av[q] = live ? (double)a[lane * NA + q] : 0.0;
+      s[q] = 0.0;
+    }
+    float xb[kTileT];
+    if (n > 0) chunk_to_regs(xb, w, lanes, L, l0, t0, n, s_lds[k], lid);
+    if (n == kTileT) {
+#pragma unroll
+      for (int i = 0; i < kTileT; ++i) step<NA>(av, s, (double)xb[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kTileT; ++i)
+        if (i < n) step<NA>(av, s, (double)xb[i]);
+    }
+    double* vk = vec_area<NA>(s_lds, k) + lid * NA;
+#pragma unroll
+    for (int q = 0; q < NA; ++q) vk[q] = s[q];
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    // wave 0: the super-chunk's zero-state end (chunks before a non-empty one are full, so Mc is
+    // every fold's matrix; the map is published only for full super-chunks)
+    double sup[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) sup[q] = 0.0;
+    if (k == 0 && live) {
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int j = 0; j < K; ++j) {
+        double ej[NA];
+        const double* vj = vec_area<NA>(s_lds, j) + lid * NA;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) ej[q] = vj[q];
+        matvec_add<NA>(sup, mc, sup, ej);
+      }
+      if (sc > 0 && sc + 1 < nsuper) put_vec<NA>(agg + (sc * lanes + lane) * NA, sup);
+    }
+    double S[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && y0 && live && k == 0) ? (double)y0[lane * NA + q] : 0.0;
+    if (sc > 0)  // uniform over the workgroup
+      ap_look_back<NA>(S, agg, inc, Ms + lane * NA * NA, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
+                       k, lid, s_lds, s_flag, s_pend, &s_any);
+    if (k == 0 && live) {
+      if (sc + 1 < nsuper) {
+        double ms[NA][NA], o[NA];
+        load_mat<NA>(ms, Ms + lane * NA * NA);
+        matvec_add<NA>(o, ms, S, sup);
+        put_vec<NA>(inc + (sc * lanes + lane) * NA, o);
+      }
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int j = 0; j < K; ++j) {  // entering state of every chunk, in place of its summary
+        double ej[NA];
+        double* vj = vec_area<NA>(s_lds, j) + lid * NA;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) {
+          ej[q] = vj[q];
+          vj[q] = S[q];
+        }
+        matvec_add<NA>(S, mc, S, ej);
+      }
+    }
+    __syncthreads();
+    if (n > 0) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q) s[q] = vk[q];
+      if (n == kTileT) {
+#pragma unroll
+        for (int i = 0; i < kTileT; ++i) xb[i] = (float)step<NA>(av, s, (double)xb[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kTileT; ++i)
+          if (i < n) xb[i] = (float)step<NA>(av, s, (double)xb[i]);
+      }
+      __builtin_amdgcn_wave_barrier();
+      regs_to_chunk(xb, y, lanes, L, l0, t0, n, s_lds[k], lid);
+    }
+  }
+}
+
+// Backward: the adjoint G_t = g_t - sum_i a_i G_{t+i} is the same filter run from the right
+// end, so the chunk and super-chunk maps are the same matrices with the scan order reversed.
+// y enters only the grad_a sums, so it is loaded after the look-back (it does not stay in
+// registers across it). grad_a partials (sum_u G_{u+1+q} y_u) are summed over the K chunks in
+// LDS and written per super-chunk; allpole_finish adds them up in a fixed order.
+template <int NA>
+__global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per_eu(4))) allpole_bwd_lb(
+    const float* __restrict__ a, const float* __restrict__ g, const float* __restrict__ y,
+    const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
+    unsigned* __restrict__ counter, float* __restrict__ gw, double* __restrict__ part, int64_t lanes, int64_t L,
+    int64_t groups, int K, int64_t nsuper) {
+  __shared__ LdsTile s_lds[kLbWaves];
+  __shared__ int s_flag[kLbWaves][64];
+  __shared__ int s_pend[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
+  __syncthreads();
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t r = tile / groups, sc = nsuper - 1 - r, l0 = (tile - r * groups) * kTile, lane = l0 + lid;
+    const bool live = lane < lanes;
+    const int64_t t0 = sc * SL + (int64_t)k * kTileT;
+    const int n = (L - t0) >= kTileT ? kTileT : (L - t0) > 0 ? (int)(L - t0) : 0;
+    double av[NA], s[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      av[q] = live ? (double)a[lane * NA + q] : 0.0;
+      s[q] = 0.0;
+    }
+    float gb[kTileT];
+    if (n > 0) chunk_to_regs(gb, g, lanes, L, l0, t0, n, s_lds[k], lid);
+    if (n == kTileT) {
+#pragma unroll
+      for (int i = kTileT - 1; i >= 0; --i) step<NA>(av, s, (double)gb[i]);
+    } else {
+#pragma unroll
+      for (int i = kTileT - 1; i >= 0; --i)
+        if (i < n) step<NA>(av, s, (double)gb[i]);
+    }
+    double* vk = vec_area<NA>(s_lds, k) + lid * NA;
+#pragma unroll
+    for (int q = 0; q < NA; ++q) vk[q] = s[q];
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    // wave 0: the super-chunk's exit to the left from a zero entering state, folded from its
+    // rightmost chunk (chunks past the end of the sequence are empty and contribute zero)
+    double sup[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) sup[q] = 0.0;
+    if (k == 0 && live) {
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int j = K - 1; j >= 0; --j) {
+        double fj[NA];
+        const double* vj = vec_area<NA>(s_lds, j) + lid * NA;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) fj[q] = vj[q];
+        matvec_add<NA>(sup, mc, sup, fj);
+      }
+      if (sc > 0 && sc + 1 < nsuper) put_vec<NA>(agg + (sc * lanes + lane) * NA, sup);
+    }
+    double R[NA];  // state entering the super-chunk from the right
+#pragma unroll
+    for (int q = 0; q < NA; ++q) R[q] = 0.0;
+    if (sc + 1 < nsuper)  // uniform over the workgroup
+      ap_look_back<NA>(R, agg, inc, Ms + lane * NA * NA, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K,
+                       k, lid, s_lds, s_flag, s_pend, &s_any);
+    if (k == 0 && live) {
+      if (sc > 0) {
+        double ms[NA][NA], o[NA];
+        load_mat<NA>(ms, Ms + lane * NA * NA);
+        matvec_add<NA>(o, ms, R, sup);
+        put_vec<NA>(inc + (sc * lanes + lane) * NA, o);
+      }
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int j = K - 1; j >= 0; --j) {  // state entering every chunk from the right
+        double fj[NA];
+        double* vj = vec_area<NA>(s_lds, j) + lid * NA;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) {
+          fj[q] = vj[q];
+          vj[q] = R[q];
+        }
+        matvec_add<NA>(R, mc, R, fj);
+      }
+    }
+    __syncthreads();
+    double ga[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) ga[q] = 0.0;
+    if (n > 0) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q) s[q] = vk[q];
+      __builtin_amdgcn_wave_barrier();
+      float yb[kTileT];
+      chunk_to_regs(yb, y, lanes, L, l0, t0, n, s_lds[k], lid);
+      auto bstep = [&](int i) __attribute__((always_inline)) {
+        const double yu = yb[i];
+#pragma unroll
+        for (int q = 0; q < NA; ++q) ga[q] = fma(s[q], yu, ga[q]);  // s_q = G_{u+1+q} before the step
+        gb[i] = (float)step<NA>(av, s, (double)gb[i]);
+      };
+      if (n == kTileT) {
+#pragma unroll
+        for (int i = kTileT - 1; i >= 0; --i) bstep(i);
+      } else {
+#pragma unroll
+        for (int i = kTileT - 1; i >= 0; --i)
+          if (i < n) bstep(i);
+      }
+      regs_to_chunk(gb, gw, lanes, L, l0, t0, n, s_lds[k], lid);
+    }
+#pragma unroll
+    for (int q = 0; q < NA; ++q) vk[q] = ga[q];
+    __syncthreads();
+    if (k == 0 && live) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q) {
+        double t = 0.0;
+        for (int j = 0; j < K; ++j) t += (vec_area<NA>(s_lds, j) + lid * NA)[q];
+        part[(sc * lanes + lane) * NA + q] = t;
+      }
+    }
+    __syncthreads();  // wave 0's reads of every vec area precede the next tile's loads into them
+  }
+}
+
+// grad_a = -(sum over the n partials [n][lanes][NA] + y0 head taps) and grad_y0, per lane. One
+// workgroup of 16 waves per 64 lanes: wave k sums the k-th of 16 contiguous segments of the
+// partials, and wave 0 adds the 16 segment sums in order (fixed order, deterministic).
+template <int NA>
+__global__ void __launch_bounds__(1024) allpole_finish(const float* __restrict__ a, const float* __restrict__ gw,
+                                                       const float* __restrict__ y0, const double* __restrict__ part,
+                                                       float* __restrict__ ga, float* __restrict__ gy0, int64_t lanes,
+                                                       int64_t L, int64_t n) {
+  __shared__ double s_p[16][64];
+  __shared__ double s_tot[NA][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t lane = blockIdx.x * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t seg = (n + 15) / 16;
+  const int64_t r0 = k * seg, r1 = (r0 + seg < n) ? r0 + seg : n;
+  for (int q = 0; q < NA; ++q) {
+    double acc = 0.0;
+    if (live)
+      for (int64_t r = r0; r < r1; ++r) acc += part[(r * lanes + lane) * NA + q];
+    s_p[k][lid] = acc;
+    __syncthreads();
+    if (k == 0) {
+      double t = s_p[0][lid];
+      for (int j = 1; j < 16; ++j) t += s_p[j][lid];
+      s_tot[q][lid] = t;
+    }
+    __syncthreads();
+  }
+  if (k != 0 || !live) return;  // no barrier follows
   double Gh[NA];  // G_0 .. G_{NA-1}, zero past the end of the sequence
 #pragma unroll
-  for (int k = 0; k < NA; ++k) Gh[k] = (k < L) ? (double)gw[lane * L + k] : 0.0;
+  for (int q = 0; q < NA; ++q) Gh[q] = (q < L) ? (double)gw[lane * L + q] : 0.0;
 #pragma unroll
-  for (int k = 0; k < NA; ++k) {
-    double acc = 0.0;
-    for (int64_t c = 0; c < nchunk; ++c) acc += ga_part[(c * lanes + lane) * NA + k];
+  for (int q = 0; q < NA; ++q) {
+    double t = s_tot[q][lid];
     if (y0) {
-      // a_i (i = k + 1) also multiplied y_{t-i} = y0[i-t-1] for t < i
+      // a_i (i = q + 1) also multiplied y_{t-i} = y0[i-t-1] for t < i
 #pragma unroll
-      for (int j = 1; j <= k + 1; ++j) acc = fma(Gh[k + 1 - j], (double)y0[lane * NA + j - 1], acc);
+      for (int j = 1; j <= q + 1; ++j) t = fma(Gh[q + 1 - j], (double)y0[lane * NA + j - 1], t);
     }
-    ga[lane * NA + k] = (float)(-acc);
+    ga[lane * NA + q] = (float)(-t);
   }
   if (y0 && gy0) {
 #pragma unroll
     for (int j = 0; j < NA; ++j) {
-      double acc = 0.0;
+      double t = 0.0;
 #pragma unroll
-      for (int i = j + 1; i <= NA; ++i) acc = fma((double)a[lane * NA + i - 1], Gh[i - 1 - j], acc);
-      gy0[lane * NA + j] = (float)(-acc);
+      for (int i = j + 1; i <= NA; ++i) t = fma((double)a[lane * NA + i - 1], Gh[i - 1 - j], t);
+      gy0[lane * NA + j] = (float)(-t);
     }
   }
 }
@@ -450,9 +927,90 @@ Plan plan(int64_t lanes, int64_t L, int64_t na) {
   return p;
 }
 
+// Tile plan of the single-pass path: K (chunks per tile) starts at kLbWaves and halves down to 2
+// while there are fewer than kApTileTarget tiles. Workspace: the tile counter, agg and inc
+// [nsuper][lanes][NA] (reset before each scan), the grad_a partials [nsuper][lanes][NA], and
+// the transfer matrices Mc, Ms [lanes][NA][NA].
+#ifndef TSF_AP_TILE_TARGET
+#define TSF_AP_TILE_TARGET 256
+#endif
+constexpr int64_t kApTileTarget = TSF_AP_TILE_TARGET;
+
+struct LbPlan {
+  int64_t groups = 0, nsuper = 0;
+  int K = 1;
+  size_t off_agg = 0, off_inc = 0, off_part = 0, off_Mc = 0, off_Ms = 0, bytes = 0;
+};
+
+LbPlan lb_plan(int64_t lanes, int64_t L, int64_t na) {
+  LbPlan p;
+  p.groups = (lanes + kTile - 1) / kTile;
+  if (L > 0) {
+    p.K = kLbWaves;
+    auto tiles = [&](int K) { return p.groups * ((L + (int64_t)kTileT * K - 1) / ((int64_t)kTileT * K)); };
+    while (p.K > 2 && tiles(p.K) < kApTileTarget) p.K /= 2;
+    const int64_t chunks = (L + kTileT - 1) / kTileT;
+    if (p.K > chunks) p.K = (int)chunks;
+    p.nsuper = (L + (int64_t)kTileT * p.K - 1) / ((int64_t)kTileT * p.K);
+  }
+  const size_t f = 8, vecs = f * p.nsuper * lanes * na;
+  p.off_agg = kCounterBytes;
+  p.off_inc = p.off_agg + vecs;
+  p.off_part = p.off_inc + vecs;
+  p.off_Mc = p.off_part + vecs;
+  p.off_Ms = p.off_Mc + f * lanes * na * na;
+  p.bytes = p.off_Ms + f * lanes * na * na;
+  return p;
+}
+
+template <int NA>
+void fwd_lb(int64_t lanes, int64_t L, const float* a, const float* w, const float* y0, float* y, char* ws,
+            hipStream_t s) {
+  static int occ[kMaxNA + 1];
+  const LbPlan p = lb_plan(lanes, L, NA);
+  double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
+  double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
+  hipLaunchKernelGGL((allpole_transfer2<NA>), grid_for(lanes), dim3(256), 0, s, a, Mc, Ms, lanes, p.K);
+  lookback_reset_launch(ws, 2 * p.nsuper * lanes * NA, s);
+  const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(allpole_fwd_lb<NA>, 64 * p.K, occ);
+  hipLaunchKernelGGL((allpole_fwd_lb<NA>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, a, w,
+                     y0, y, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
+                     reinterpret_cast<double*>(ws + p.off_inc), reinterpret_cast<unsigned*>(ws), lanes, L, p.groups,
+                     p.K, p.nsuper);
+}
+
+template <int NA>
+void bwd_lb(int64_t lanes, int64_t L, const float* g, const float* a, const float* y, const float* y0, float* gw,
+            float* ga, float* gy0, char* ws, hipStream_t s) {
+  static int occ[kMaxNA + 1];
+  const LbPlan p = lb_plan(lanes, L, NA);
+  double* part = reinterpret_cast<double*>(ws + p.off_part);
+  if (L > 0) {
+    double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
+    double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
+    hipLaunchKernelGGL((allpole_transfer2<NA>), grid_for(lanes), dim3(256), 0, s, a, Mc, Ms, lanes, p.K);
+    lookback_reset_launch(ws, 2 * p.nsuper * lanes * NA, s);
+    const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(allpole_bwd_lb<NA>, 64 * p.K, occ);
+    hipLaunchKernelGGL((allpole_bwd_lb<NA>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, a, g,
+                       y, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
+                       reinterpret_cast<double*>(ws + p.off_inc), reinterpret_cast<unsigned*>(ws), gw, part, lanes, L,
+                       p.groups, p.K, p.nsuper);
+  }
+  hipLaunchKernelGGL((allpole_finish<NA>), dim3((unsigned)p.groups), dim3(1024), 0, s, a, gw, y0, (const double*)part,
+                     ga, gy0, lanes, L, p.nsuper);
+}
+
+size_t workspace_bytes_for(int64_t lanes, int64_t L, int64_t na) {
+  return na <= kLbNA ? lb_plan(lanes, L, na).bytes : plan(lanes, L, na).bytes;
+}
+
 template <int NA>
 int fwd_impl(int64_t lanes, int64_t L, const float* a, const float* w, const float* y0, float* y, char* ws,
              hipStream_t s) {
+  if constexpr (NA <= kLbNA) {
+    fwd_lb<NA>(lanes, L, a, w, y0, y, ws, s);
+    return tsf_launch_status();
+  }
   const Plan p = plan(lanes, L, NA);
   double* M = reinterpret_cast<double*>(ws + p.off_M);
   double* e = reinterpret_cast<double*>(ws + p.off_e);
@@ -471,6 +1029,10 @@ int fwd_impl(int64_t lanes, int64_t L, const float* a, const float* w, const flo
 template <int NA>
 int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* a, const float* y, const float* y0, float* gw,
              float* ga, float* gy0, char* ws, hipStream_t s) {
+  if constexpr (NA <= kLbNA) {
+    bwd_lb<NA>(lanes, L, g, a, y, y0, gw, ga, gy0, ws, s);
+    return tsf_launch_status();
+  }
   const Plan p = plan(lanes, L, NA);
   double* M = reinterpret_cast<double*>(ws + p.off_M);
   double* f = reinterpret_cast<double*>(ws + p.off_e);
@@ -486,8 +1048,8 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* a, const flo
     hipLaunchKernelGGL((allpole_bwd_apply<NA>), dim3(groups, (unsigned)p.nchunk), dim3(kTile), 0, s, a, g, y, R, gw,
                        part, lanes, L, p.T_c, p.nchunk);
   }
-  hipLaunchKernelGGL((allpole_bwd_finish<NA>), grid_for(lanes), dim3(256), 0, s, a, gw, y0, part, ga, gy0, lanes, L,
-                     p.nchunk);
+  hipLaunchKernelGGL((allpole_finish<NA>), dim3((unsigned)((lanes + kTile - 1) / kTile)), dim3(1024), 0, s, a, gw, y0,
+                     (const double*)part, ga, gy0, lanes, L, L > 0 ? p.nchunk : (int64_t)0);
   return tsf_launch_status();
 }
 
@@ -499,7 +1061,7 @@ extern "C" {
 
 int64_t tsfast_hip_allpole_workspace_bytes(int64_t lanes, int64_t L, int64_t na) {
   if (lanes < 0 || L < 0 || na < 1 || na > kMaxNA) return -1;
-  return (int64_t)plan(lanes, L, na).bytes;
+  return (int64_t)workspace_bytes_for(lanes, L, na);
 }
 
 int tsfast_hip_allpole_fwd(int64_t lanes, int64_t L, int64_t na, const float* a, const float* w, const float* y0,

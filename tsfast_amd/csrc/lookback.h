@@ -1,0 +1,83 @@
+// Shared protocol of the single-pass look-back scans (diag.hip, allpole.hip): published 8-byte
+// words with a per-word ready marker, the in-order tile counter and the per-call reset kernel.
+// Included inside each file's anonymous namespace (after common.h and `using namespace tsf`).
+#pragma once
+
+// Published words start as kUnset, a signalling NaN: arithmetic results and float -> double
+// conversions are never signalling NaNs, so a word that differs from kUnset has been written.
+// Each 8-byte word is stored and polled with agent-scope atomics (coherent across the L2s of
+// the XCDs) and validated on its own, so no fence has to order data against a flag.
+constexpr uint64_t kUnset = 0x7FF00000DEADBEEFull;
+// Polls without progress before a look-back gives up and yields NaN (about a second): every
+// wait ends even if an invariant below were broken, and the NaN shows in the outputs.
+constexpr uint32_t kSpinMax = 1u << 20;
+
+TSF_DEV void put_word(double* p, double x) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), static_cast<uint64_t>(__double_as_longlong(x)), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+TSF_DEV bool get_word(const double* p, double& x) {
+  const uint64_t b = __hip_atomic_load(const_cast<uint64_t*>(reinterpret_cast<const uint64_t*>(p)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  x = __longlong_as_double(static_cast<long long>(b));
+  return b != kUnset;
+}
+TSF_DEV void put(double* p, double x) { put_word(p, x); }
+TSF_DEV void put(double2* p, double2 x) {
+  put_word(&p->x, x.x);
+  put_word(&p->y, x.y);
+}
+TSF_DEV bool get(const double* p, double& x) { return get_word(p, x); }
+TSF_DEV bool get(const double2* p, double2& x) {
+  const bool a = get_word(&p->x, x.x);
+  const bool b = get_word(&p->y, x.y);
+  return a && b;
+}
+template <typename W>
+TSF_DEV W quiet_nan();
+template <>
+TSF_DEV double quiet_nan<double>() {
+  return __longlong_as_double(0x7FF8000000000000ll);
+}
+template <>
+TSF_DEV double2 quiet_nan<double2>() {
+  return make_double2(quiet_nan<double>(), quiet_nan<double>());
+}
+
+TSF_DEV unsigned take_tile(unsigned* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Resets the look-back words to kUnset and the tile counter to zero before every scan (a
+// kernel rather than a memset node, so that a captured graph replays it reliably).
+__global__ void __launch_bounds__(256) lookback_reset(uint64_t* __restrict__ words, int64_t n,
+                                                      unsigned* __restrict__ counter) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) words[i] = kUnset;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *counter = 0u;
+}
+
+
+// Host side. A workspace starts with the tile counter (kCounterBytes), followed by the published
+// words that lookback_reset_launch marks unset.
+constexpr int64_t kCounterBytes = 256;
+
+// Workgroups that stay resident at once (persistent grid size), per kernel and block size.
+template <typename F>
+int64_t resident_wgs(F kern, int threads, int* cache) {
+  int& c = cache[threads / 64];
+  if (c == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, 0) != hipSuccess || n < 1) n = 1;
+    c = n;
+  }
+  return (int64_t)c * device_cus();
+}
+
+void lookback_reset_launch(char* ws, int64_t words, hipStream_t s) {
+  int64_t blocks = (words + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 2048) blocks = 2048;
+  hipLaunchKernelGGL(lookback_reset, dim3((unsigned)blocks), dim3(256), 0, s,
+                     reinterpret_cast<uint64_t*>(ws + kCounterBytes), words, reinterpret_cast<unsigned*>(ws));
+}
