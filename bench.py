@@ -63,6 +63,18 @@ MEASURED_TRAFFIC = {
     },
 }
 
+# VALU issue per call, for the VALU-bound fused Mamba scan: rocprofv3 SQ_ACTIVE_INST_VALU (quad-cycles
+# a SIMD spends issuing vector instructions, transcendentals counting two) summed over the
+# kernels of one ABI call; same provenance rules as MEASURED_TRAFFIC.
+MEASURED_VALU = {
+    (3, "bf16"): {
+        "fwd": (274_501_632, "profiles/mamba_scan_config3_valu.md"),
+        "bwd": (576_915_392, "profiles/mamba_scan_config3_valu.md"),
+    },
+}
+VALU_PEAK_CLOCK_HZ = 2.4e9  # MI355X peak engine clock
+SIMDS_PER_CU = 4
+
 
 # --------------------------------------------------------------------------- algorithmic bytes
 def mamba_bytes(B, L, D, N, io_bytes):
@@ -578,6 +590,23 @@ def main():
         line["roofline"]["traffic_unit"] = "bytes per call"
         line["roofline"]["traffic_source"] = measured[1]
         line["roofline"]["algorithmic_bytes"] = dom_b
+    valu = None if (args.conv or args.selective) else MEASURED_VALU.get(key, {}).get(phase)
+    if valu:
+        # VALU issue capacity: every SIMD issues one wave64 instruction per quad-cycle
+        import torch
+
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        peak = cus * SIMDS_PER_CU * VALU_PEAK_CLOCK_HZ / 4
+        got = valu[0] / (dom_ms * 1e-3)
+        line["valu"] = {
+            "kernel": name,
+            "achieved": round(got / 1e9, 2),
+            "peak": round(peak / 1e9, 2),
+            "unit": "G VALU issue quad-cycles/s",
+            "frac": round(got / peak, 4),
+            "issue_per_call": valu[0],
+            "source": valu[1],
+        }
     if cpu is not None:
         try:
             line["cpu_baseline"] = cpu()
