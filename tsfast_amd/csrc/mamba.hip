@@ -19,8 +19,8 @@
 //  * Time advances in chunks. Per-(t, d) scalar work (softplus, sigmoid, gates, the D skip) is
 //    done once per (t, d) by an "owner" thread and staged through LDS, with coalesced 32-channel
 //    row loads/stores; each lane then runs only the per-state recurrence.
-//  * Forward: sums over states (y = h.C) are pre-reduced between the two adjacent lanes of a
-//    state pair with one DPP swap and finished by the owner thread from LDS.
+//  * Forward: every lane stores its partial sum over its states (y = h.C) to LDS and the owner
+//    thread adds the NG partials of its (t, d).
 //  * Backward: each 16-lane DPP row holds one state group; the chunk's B_t/C_t values live in
 //    VGPRs spread over the row and reach the lanes through DPP row broadcasts. It recomputes
 //    each chunk's states from the forward's fp32 checkpoint into registers (lam_t, lam_t h_{t-1}
@@ -56,7 +56,6 @@ struct MCfg {
   static constexpr int NPT = NS / NG;          // states per lane
   static constexpr int DT = 32;                // channels per workgroup
   static constexpr int TH = DT * NG;           // threads per workgroup
-  static constexpr int NPAIR = NG / 2;         // state-pair partial slots per channel
   // checkpoint interval = backward recompute chunk (lam_t and h_t of a chunk live in VGPRs)
   static constexpr int CHK = NPT <= 2 ? 8 : (NPT == 4 ? 8 : 4);
   static constexpr int TF = NPT <= 2 ? 32 : 2 * CHK;  // forward steps per LDS round
@@ -65,11 +64,6 @@ struct MCfg {
   static constexpr int IT_B = (CHK * DT + TH - 1) / TH;  // owned (t, d) items per thread, backward
   static constexpr int BC_F = (TF * NS + TH - 1) / TH;   // B/C tile elements per thread, forward
 };
-
-// Swap with the neighbouring lane (lane ^ 1) through DPP: one VALU op, no LDS round trip.
-TSF_DEV float swap_lane1(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1 /* quad_perm [1,0,3,2] */, 0xF, 0xF, false));
-}
 
 template <typename TIO>
 TSF_DEV TIO io_zero();
@@ -132,10 +126,10 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     int64_t L, int64_t D, int N, int64_t NC, unsigned cus) {
   using C = MCfg<NS>;
   constexpr int NPT = C::NPT, NG = C::NG, DT = C::DT, TH = C::TH, CHK = C::CHK, TF = C::TF;
-  constexpr int IT = C::IT_F, BCI = C::BC_F, NPAIR = C::NPAIR;
+  constexpr int IT = C::IT_F, BCI = C::BC_F;
   __shared__ float2 s_sc[TF][DT];       // (delta, delta * u)
   __shared__ float2 s_bc[TF][NS];       // (B, C)
-  __shared__ float s_y[TF][NPAIR][DT];  // y partial per state pair
+  __shared__ float s_y[TF][NG][DT];     // y partial per lane (state group)
 
   const int tid = threadIdx.x;
   int64_t tile, b;
@@ -183,8 +177,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
       const uint32_t t = (uint32_t)(idx / DT);
-      bool v = idx < TF * DT && oact;
-      if (!FULL) v = v && (int64_t)(t0 + t) < L;
+      bool v = idx < TF * DT;
+      if (!FULL) v = v && oact && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Du + (uint32_t)od;
       r_dr[k] = v ? ld32(drw, o) : io_zero<TIO>();
       r_u[k] = v ? ld32(urw, o) : io_zero<TIO>();
@@ -194,15 +188,18 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     for (int k = 0; k < BCI; ++k) {
       const int idx = tid + k * TH;
       const uint32_t t = (uint32_t)(idx / NS), n = (uint32_t)(idx % NS);
-      bool v = idx < TF * NS && (int)n < N;
-      if (!FULL) v = v && (int64_t)(t0 + t) < L;
+      bool v = idx < TF * NS;
+      if (!FULL) v = v && (int)n < N && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Nu + n;
       r_b[k] = v ? ld32(brw, o) : io_zero<TIO>();
       r_c[k] = v ? ld32(crw, o) : io_zero<TIO>();
     }
   };
+  // FULL loads (no per-element guard): all TF steps in the sequence, all DT channels in range
+  // and N == NS; workgroup-uniform
+  const bool wg_full = d0 + DT <= D && N == NS;
   if (L > 0) {
-    if (TF <= L)
+    if (TF <= L && wg_full)
       load_chunk(0u, Bool<true>());
     else
       load_chunk(0u, Bool<false>());
@@ -232,15 +229,15 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     // prefetch the next round while this one computes
     const uint32_t t1 = t0 + TF;
     if ((int64_t)t1 < L) {
-      if ((int64_t)t1 + TF <= L)
+      if ((int64_t)t1 + TF <= L && wg_full)
         load_chunk(t1, Bool<true>());
       else
         load_chunk(t1, Bool<false>());
     }
     __syncthreads();
     // phase 2: the recurrence, NPT states per lane. LDS operands are read kRd steps ahead of
-    // their use, and the step body has no branch (both lanes of a pair store the same pair sum
-    // to the same slot), so the reads of later steps overlap the arithmetic of earlier ones.
+    // their use, and the step body has no branch (every lane stores its own y partial), so the
+    // reads of later steps overlap the arithmetic of earlier ones.
     constexpr int kRd = NPT <= 2 ? 4 : 2;
     static_assert(TF % kRd == 0 && CHK % kRd == 0, "read batches must not straddle checkpoints");
 #pragma unroll
@@ -262,8 +259,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
           h[j] = fmaf(lam, h[j], sv[r].y * bcv[r][j].x);
           y = fmaf(h[j], bcv[r][j].y, y);
         }
-        y += swap_lane1(y);
-        s_y[i][ng >> 1][dl] = y;
+        s_y[i][ng][dl] = y;
       }
       // checkpoint slot k holds the state after step (k + 1) * CHK - 1 (layout [B, NC, N, D])
       const int ie = i0 + kRd - 1;
@@ -283,7 +279,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       if (idx < TF * DT && t < len && oact) {
         float y = 0.0f;
 #pragma unroll
-        for (int p = 0; p < NPAIR; ++p) y += s_y[t][p][od];
+        for (int g = 0; g < NG; ++g) y += s_y[t][g][od];
         const float zz = o_z[k];
         const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
         const float yv = fmaf(dp_o, o_u[k], y);
