@@ -509,6 +509,113 @@ def run_allpole(args, line):
     return ms, fwd_b + bwd_b, kernels, cpu
 
 
+def gblock_inputs(dev, B=64, L=16384, I=8, O=8, nb=8, na=3):
+    """Config 4's channel structure (batch 64, 8 in x 8 out, L 16384, na 3) through a whole G-block
+    with nb = 8 FIR taps (the reference's default, dynonet/core.py:172), stable poles."""
+    import numpy as np
+    import torch
+
+    g = torch.Generator().manual_seed(4)
+    u = torch.randn(B, L, I, generator=g)
+    b = torch.randn(O, I, nb, generator=g) * 0.05
+    a = torch.empty(O, I, na)
+    for o in range(O):
+        for j in range(I):
+            r = (torch.rand(na, generator=g) * 0.48 + 0.5).numpy()
+            a[o, j] = torch.tensor(np.poly(r)[1:], dtype=torch.float32)
+    gy = torch.randn(B, L, O, generator=g)
+    return u.to(dev), b.to(dev), a.to(dev), gy.to(dev)
+
+
+def run_gblock(args, line):
+    """The fused dynoNet G-block (FIR + all-pole + input sum) at config 4's channel structure, with
+    the reference's unfused three-stage path (conv1d, all-pole op, sum) timed in the same run."""
+    import torch
+
+    from tsfast_amd.dynonet import core as dcore
+    from tsfast_amd.dynonet import gblock_hip
+
+    u, b, a, gy = gblock_inputs("cuda")
+    B, L, I = u.shape
+    O, _, nb = b.shape
+    na = a.shape[-1]
+    P = I * O
+    tail = u.new_zeros(B, nb - 1, I)
+    x0 = u.new_zeros(B, P, na)
+
+    def step(ev):
+        mark(ev)
+        y, x_last, saved = gblock_hip._gblock_op(u, b, a, tail, x0)
+        mark(ev)
+        gblock_hip._gblock_bwd_op(gy, None, u, b, a, tail, x0, saved)
+        mark(ev)
+
+    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
+
+    def unfused(ev):
+        uu = u.detach().requires_grad_()
+        bb = b.detach().requires_grad_()
+        aa = a.detach().requires_grad_()
+        mark(ev)
+        u_buf = torch.cat((tail, uu), dim=1)
+        w = torch.nn.functional.conv1d(u_buf.transpose(1, 2), bb.permute(1, 0, 2).reshape(P, 1, nb).flip(-1), groups=I)
+        y_pairs = dcore.allpole(aa.permute(1, 0, 2).reshape(P, na).expand(B, P, na), w, x0)
+        y = y_pairs.view(B, I, O, L).sum(1).transpose(1, 2)
+        mark(ev)
+        torch.autograd.backward(y, gy)
+        mark(ev)
+
+    ums, (ufwd, ubwd) = time_steps(unfused, max(args.steps // 2, 2), 2)
+    f4 = 4
+    fwd_b = B * L * I * f4 + B * L * O * f4  # read u, write y
+    bwd_b = B * L * O * f4 + B * L * I * f4 + B * L * I * f4  # read gy and u, write gu
+    line.update(
+        metric="fwd+bwd ms + achieved HBM GB/s, fused dynoNet G-block (FIR + all-pole + input sum)",
+        config={"workload": f"fused dynoNet G-block fwd+bwd: batch {B}, {I} in x {O} out, L {L}, nb {nb}, na {na} "
+                            "(BASELINE config 4 channel structure)", "B": B, "L": L, "I": I, "O": O, "nb": nb,
+                "na": na},
+        fwd_ms=round(fwd_ms, 4),
+        bwd_ms=round(bwd_ms, 4),
+        unfused_ms={"fwd": round(ufwd, 4), "bwd": round(ubwd, 4), "total": round(ums, 4),
+                    "path": "F.conv1d + tsfast_hip::dynonet_allpole + sum over inputs (the reference's stages)"},
+    )
+    line["dtype"] = "f64"  # fp32 I/O, fp64 recurrence inside
+    kernels = {"fwd": ("gblock_fwd_lb look-back scan + transfer + reset", fwd_ms, fwd_b),
+               "bwd": ("gblock_bwd_lb look-back scan + transfer + reset + finish", bwd_ms, bwd_b)}
+    cpu = None
+    if not args.no_cpu:
+        def cpu_leg():
+            import torch.nn.functional as F
+
+            from tsfast_amd.dynonet.core import companion, linear_recurrence
+
+            threads = os.cpu_count() or 1
+            torch.set_num_threads(threads)
+            rows = 2
+            u_c = u[:rows].cpu().requires_grad_()
+            b_c, a_c, gy_c = b.cpu(), a.cpu(), gy[:rows].cpu()
+            Cm = companion(a_c.permute(1, 0, 2).reshape(P, na))
+
+            def fb():
+                u_buf = torch.cat((u_c.new_zeros(rows, nb - 1, I), u_c), dim=1)
+                w = F.conv1d(u_buf.transpose(1, 2), b_c.permute(1, 0, 2).reshape(P, 1, nb).flip(-1), groups=I)
+                x = linear_recurrence(Cm, F.pad(w.unsqueeze(-1), (0, na - 1)), None)
+                y = x[..., 0].view(rows, I, O, L).sum(1).transpose(1, 2)
+                y.backward(gy_c)
+
+            med, n = cpu_time(fb)
+            sf = rows * L * (I + O) * 4
+            sb = rows * L * (O + 2 * I) * 4
+            return {
+                "value": round((sf + sb) / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": (f"{rows} of {B} batch rows, L={L}: conv1d + companion-matrix doubling scan + sum on CPU "
+                           f"(the reference CPU path, dynonet/core.py:23-88, 212-250), fwd+bwd median of {n} runs "
+                           f"= {med * 1e3:.1f} ms"),
+            }
+        cpu = cpu_leg
+    return ms, fwd_b + bwd_b, kernels, cpu
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -520,6 +627,8 @@ def main():
                     help="measure the selective (time-varying) diagonal scan instead of a BASELINE config")
     ap.add_argument("--conv", action="store_true",
                     help="measure the fused Mamba conv+SiLU at config 3's shape instead of a BASELINE config")
+    ap.add_argument("--gblock", action="store_true",
+                    help="measure the fused dynoNet G-block (FIR + all-pole + input sum) at config 4's channels")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument(
         "--copy-calibration",
@@ -565,7 +674,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
     }
-    runner = run_conv if args.conv else run_selective if args.selective else {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config]
+    runner = (run_conv if args.conv else run_selective if args.selective else run_gblock if args.gblock
+              else {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config])
     ms, total_bytes, kernels, cpu = runner(args, line)
     gbs = total_bytes / (ms * 1e-3) / 1e9
     line["value"] = round(gbs, 2)
@@ -576,7 +686,7 @@ def main():
     name, dom_ms, dom_b = kernels[phase]
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
     key = ("selective", "f32") if args.selective else (args.config, args.io if args.config == 3 else "f32")
-    measured = None if args.conv else MEASURED_TRAFFIC.get(key, {}).get(phase)
+    measured = None if (args.conv or args.gblock) else MEASURED_TRAFFIC.get(key, {}).get(phase)
     line["roofline"] = {
         "bound": "hbm",
         "kernel": name,
@@ -590,7 +700,7 @@ def main():
         line["roofline"]["traffic_unit"] = "bytes per call"
         line["roofline"]["traffic_source"] = measured[1]
         line["roofline"]["algorithmic_bytes"] = dom_b
-    valu = None if (args.conv or args.selective) else MEASURED_VALU.get(key, {}).get(phase)
+    valu = None if (args.conv or args.selective or args.gblock) else MEASURED_VALU.get(key, {}).get(phase)
     if valu:
         # VALU issue capacity: every SIMD issues one wave64 instruction per quad-cycle
         import torch

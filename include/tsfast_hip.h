@@ -145,6 +145,31 @@ int tsfast_hip_conv_silu_bwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_
                              const void* gy, void* gx, void* gtail, float* gw, float* gb, void* workspace,
                              int64_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Fused dynoNet G-block: the FIR + all-pole + input-sum body of LinearDynamicalOperator.forward
+ * (tsfast/models/architectures/dynonet/core.py:196-258; the reference runs it as F.conv1d at
+ * :219-222, the tsfast::dynonet_allpole op at :225-235 and a sum at :250), per pair p = j*O + o:
+ *   w_p[t] = sum_k b[o,j,k] u[t-k, j],  y_p[t] = w_p[t] - sum_i a[o,j,i] y_p[t-i],
+ *   y[t, o] = sum_j y_p[t],  x_last[p, q] = y_p[L-1-q] (x0 beyond the start).
+ * float32 in and out, fp64 state; 1 <= na <= 4, 1 <= nb <= 16, I*O dividing 64, else
+ * TSF_ERR_UNSUPPORTED. Layout: u/gu [B, L, I], y/gy [B, L, O] (channel-last, contiguous),
+ * b/gb [O, I, nb], a/ga [O, I, na], u_tail/gu_tail [B, nb-1, I] (the carried FIR input; NULL =
+ * zeros), x0/gx0/x_last/g_xlast [B, I*O, na] newest first (NULL x0 = zeros; x_last, g_xlast may
+ * be NULL). `saved` [saved_doubles] (fp64) receives the per-super-chunk entering states for the
+ * backward (may be NULL for inference). The workspace holds the look-back state of a single-pass
+ * scan, re-initialised by each call on its stream: two calls in flight must not share one.
+ */
+int64_t tsfast_hip_gblock_workspace_bytes(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na);
+int64_t tsfast_hip_gblock_saved_doubles(int64_t B, int64_t L, int64_t I, int64_t O, int64_t na);
+int tsfast_hip_gblock_fwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na, const float* u,
+                          const float* b, const float* a, const float* u_tail, const float* x0, float* y,
+                          float* x_last, double* saved, void* workspace, int64_t workspace_bytes, void* stream);
+/* gb, ga: full parameter gradients (summed over batch and time); gu_tail and gx0 may be NULL. */
+int tsfast_hip_gblock_bwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na, const float* gy,
+                          const float* g_xlast, const float* u, const float* b, const float* a, const float* u_tail,
+                          const float* x0, const double* saved, float* gu, float* gu_tail, float* gb, float* ga,
+                          float* gx0, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

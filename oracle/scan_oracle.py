@@ -35,6 +35,8 @@ __all__ = [
     "allpole_backward",
     "conv_silu_forward",
     "conv_silu_backward",
+    "gblock_forward",
+    "gblock_backward",
 ]
 
 
@@ -291,3 +293,75 @@ def conv_silu_backward(gy, x, tail, w, bias=None):
     gw = np.stack([np.sum(gpre * buf[:, k : k + L], axis=(0, 1)) for k in range(K)], axis=1)
     gb = None if bias is None else np.sum(gpre, axis=(0, 1))
     return gx, gtail, gw, gb
+
+
+# --------------------------------------------------------------------------- dynoNet G-block
+def _gblock_fir(u, b, u_tail):
+    """FIR stage of LinearDynamicalOperator.forward (dynonet/core.py:219-222): ``ubuf =
+    cat(u_tail, u)`` along time and, per pair p = j * O + o (input-major, :158-159),
+    ``w[b, p, t] = sum_k bcoef[o, j, k] ubuf[b, t + nb - 1 - k, j]``. u [B, L, I], bcoef
+    [O, I, nb], u_tail [B, nb-1, I]. Returns (w [B, P, L], ubuf [B, nb-1+L, I])."""
+    u, b, u_tail = _hi(u), _hi(b), _hi(u_tail)
+    Bsz, L, I = u.shape
+    O, _, nb = b.shape
+    ubuf = np.concatenate([u_tail, u], axis=1)
+    w = np.zeros((Bsz, I, O, L))
+    for k in range(nb):
+        # [B, I, 1, L] * [1, I, O, 1]
+        w += ubuf[:, nb - 1 - k : nb - 1 - k + L, :].transpose(0, 2, 1)[:, :, None, :] * b[:, :, k].T[None, :, :, None]
+    return w.reshape(Bsz, I * O, L), ubuf
+
+
+def gblock_forward(u, b, a, u_tail, x0):
+    """LinearDynamicalOperator.forward (dynonet/core.py:196-258) with the all-pole stage:
+    FIR per pair, ``y_pairs = allpole(a, w, x0)`` per pair (:228-235), then the sum over inputs
+    ``y[b, t, o] = sum_j y_pairs[b, j * O + o, t]`` (:250). a [O, I, na] (pair coefficients
+    a.permute(1, 0, 2), :229), x0 [B, P, na] newest first. Returns (y [B, L, O], x_last
+    [B, P, na], y_pairs [B, P, L]); x_last[j] = y_{L-1-j}, from x0 when L < na (:239-244)."""
+    Bsz, L, I = np.shape(u)
+    O, _, na = np.shape(a)
+    P = I * O
+    w, _ = _gblock_fir(u, b, u_tail)
+    ap = np.broadcast_to(_hi(a).transpose(1, 0, 2).reshape(1, P, na), (Bsz, P, na)).reshape(-1, na)
+    yp = allpole_forward(ap, w.reshape(-1, L), _hi(x0).reshape(-1, na)).reshape(Bsz, P, L)
+    y = yp.reshape(Bsz, I, O, L).sum(1).transpose(0, 2, 1)
+    ext = np.concatenate([_hi(x0)[:, :, ::-1], yp], axis=2)  # oldest .. newest
+    x_last = ext[:, :, ::-1][:, :, :na]
+    return y, x_last, yp
+
+
+def gblock_backward(gy, g_xlast, u, b, a, u_tail, x0):
+    """Adjoint of gblock_forward: the upstream gradient of every pair's output is gy of its
+    output channel, plus g_xlast on the last na outputs (or on x0 when the sequence is shorter);
+    the all-pole adjoint gives (ga, gw, gx0) per pair; the FIR adjoint gives
+    ``gb[o, j, k] = sum_{b,t} gw[b, p, t] ubuf[b, t + nb - 1 - k, j]`` and the input gradient
+    ``gubuf[b, s, j] = sum_o sum_k bcoef[o, j, k] gw[b, p, s - (nb - 1) + k]``.
+    Returns (gu [B, L, I], gu_tail [B, nb-1, I], gb [O, I, nb], ga [O, I, na], gx0 [B, P, na])."""
+    gy, b = _hi(gy), _hi(b)
+    Bsz, L, O = gy.shape
+    _, I, nb = b.shape
+    na = np.shape(a)[2]
+    P = I * O
+    _, _, yp = gblock_forward(u, b, a, u_tail, x0)
+    w, ubuf = _gblock_fir(u, b, u_tail)
+    gpair = np.broadcast_to(gy.transpose(0, 2, 1)[:, None, :, :], (Bsz, I, O, L)).reshape(Bsz, P, L).copy()
+    gx0_direct = np.zeros((Bsz, P, na))
+    if g_xlast is not None:
+        gxl = _hi(g_xlast)
+        for j in range(na):  # x_last[j] = y_{L-1-j}, or x0[j - L] for j >= L
+            if L - 1 - j >= 0:
+                gpair[:, :, L - 1 - j] += gxl[:, :, j]
+            else:
+                gx0_direct[:, :, j - L] += gxl[:, :, j]
+    ap = np.broadcast_to(_hi(a).transpose(1, 0, 2).reshape(1, P, na), (Bsz, P, na)).reshape(-1, na)
+    ga_l, gw, gx0_l = allpole_backward(gpair.reshape(-1, L), ap, yp.reshape(-1, L), _hi(x0).reshape(-1, na))
+    gw = gw.reshape(Bsz, I, O, L)
+    ga = ga_l.reshape(Bsz, I, O, na).sum(0).transpose(1, 0, 2)
+    gx0 = gx0_l.reshape(Bsz, P, na) + gx0_direct
+    gb = np.zeros((O, I, nb))
+    gubuf = np.zeros((Bsz, nb - 1 + L, I))
+    for k in range(nb):
+        seg = ubuf[:, nb - 1 - k : nb - 1 - k + L, :].transpose(0, 2, 1)  # [B, I, L]
+        gb[:, :, k] = np.einsum("bjol,bjl->oj", gw, seg)
+        gubuf[:, nb - 1 - k : nb - 1 - k + L, :] += np.einsum("bjol,oj->blj", gw, b[:, :, k])
+    return gubuf[:, nb - 1 :], gubuf[:, : nb - 1], gb, ga, gx0

@@ -1,0 +1,127 @@
+"""GPU parity: the fused dynoNet G-block (FIR + all-pole + input sum) vs the fp64 oracle.
+
+The oracle (oracle/scan_oracle.py::gblock_forward/backward) is pinned against float64 autograd
+through the reference's own formulation (grouped conv1d, a sequential all-pole loop, the sum
+over inputs; tests/test_oracle.py). Shapes cover every tap padding (nb 1..16 -> 2, 4, 8, 16),
+every order na 1..4, pair counts 1..64 (64 / (I*O) batch rows per tile), sequences shorter
+than na and than one chunk, many super-chunks, and absent initial state. Bar: max relative
+error <= 1e-5 for outputs, the returned state and every gradient (fp32 I/O, fp64 state).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import scan_oracle as O
+from tsfast_amd import dispatch
+from tsfast_amd.dynonet import core as dcore
+from tsfast_amd.dynonet import gblock_hip
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _np(t):
+    return None if t is None else t.detach().cpu().numpy().astype(np.float64)
+
+
+def _make(B, L, I, O_, nb, na, seed, with_state=True):
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(B, L, I, generator=g)
+    b = torch.randn(O_, I, nb, generator=g) * (0.5 / nb)
+    # stable denominators: poles inside 0.9 of the unit circle, scaled per pair
+    a = torch.empty(O_, I, na)
+    for o in range(O_):
+        for j in range(I):
+            r = torch.rand(na, generator=g) * 0.9
+            poly = np.poly(r.numpy() * np.sign(torch.rand(na, generator=g).numpy() - 0.5))
+            a[o, j] = torch.tensor(poly[1:], dtype=torch.float32)
+    ut = torch.randn(B, nb - 1, I, generator=g) if with_state else None
+    x0 = torch.randn(B, I * O_, na, generator=g) if with_state else None
+    gy = torch.randn(B, L, O_, generator=g)
+    gxl = torch.randn(B, I * O_, na, generator=g)
+    return u, b, a, ut, x0, gy, gxl
+
+
+# (B, L, I, O, nb, na)
+_SHAPES = [
+    (2, 100, 8, 8, 8, 3),  # 64 pairs: one batch row per tile
+    (4, 300, 2, 4, 4, 2),
+    (3, 77, 1, 1, 1, 1),  # 1 pair: 64 batch rows per tile, mostly idle lanes
+    (2, 5000, 4, 4, 16, 4),  # 16 taps, many super-chunks
+    (1, 2, 2, 2, 3, 4),  # L < na
+    (2, 1, 8, 8, 8, 2),  # L = 1
+    (5, 1000, 2, 2, 5, 1),
+    (6, 2049, 1, 8, 2, 3),
+    (4, 4096, 8, 8, 8, 3),  # config-4 channel structure, reduced batch and length
+]
+
+
+@pytest.mark.parametrize("with_state", [True, False])
+@pytest.mark.parametrize("shape", _SHAPES)
+def test_gblock_matches_oracle(gpu, shape, with_state):
+    B, L, I, O_, nb, na = shape
+    u, b, a, ut, x0, gy, gxl = _make(*shape, seed=sum(shape), with_state=with_state)
+    ts = [t.to(gpu).requires_grad_() if t is not None else None for t in (u, b, a, ut, x0)]
+    assert gblock_hip.supports(*ts) is None
+    y, x_last = gblock_hip.run(*ts)
+    torch.autograd.backward([y, x_last], [gy.to(gpu), gxl.to(gpu)])
+    z = lambda t, shp: np.zeros(shp) if t is None else _np(t)  # noqa: E731
+    args = (_np(u), _np(b), _np(a), z(ut, (B, nb - 1, I)), z(x0, (B, I * O_, na)))
+    want_y, want_xl, _ = O.gblock_forward(*args)
+    assert O.rel_err(_np(y), want_y) < TOL, "y"
+    assert O.rel_err(_np(x_last), want_xl) < TOL, "x_last"
+    gu, gut, gb, ga, gx0 = O.gblock_backward(_np(gy), _np(gxl), *args)
+    assert O.rel_err(_np(ts[0].grad), gu) < TOL, "gu"
+    assert O.rel_err(_np(ts[1].grad), gb) < TOL, "gb"
+    assert O.rel_err(_np(ts[2].grad), ga) < TOL, "ga"
+    if with_state:
+        if nb > 1:
+            assert O.rel_err(_np(ts[3].grad), gut) < TOL, "gu_tail"
+        assert O.rel_err(_np(ts[4].grad), gx0) < TOL, "gx0"
+
+
+def test_gblock_operator_dispatch_and_chunked_state(gpu):
+    """linear_dynamical_operator picks the fused kernel, and two chunks with the carried state
+    ({"u": FIR tail, "x": IIR state}) equal one pass over the whole sequence."""
+    B, L, I, O_, nb, na = 3, 700, 4, 2, 6, 2
+    u, b, a, _, _, _, _ = _make(B, L, I, O_, nb, na, seed=9)
+    u, b, a = u.to(gpu), b.to(gpu), a.to(gpu)
+    with dispatch.use_backend("hip"):
+        zeros = (u.new_zeros(B, nb - 1, I), u.new_zeros(B, I * O_, na))
+        assert dispatch.resolve("dynonet.gblock", dcore._GBLOCK_BACKENDS, ("hip",), (u, b, a, *zeros)) is gblock_hip
+        full, st_full = dcore.linear_dynamical_operator(u, b, a, return_state=True)
+        y1, st = dcore.linear_dynamical_operator(u[:, :333], b, a, return_state=True)
+        y2, st2 = dcore.linear_dynamical_operator(u[:, 333:], b, a, state=st, return_state=True)
+    chunked = torch.cat((y1, y2), 1)
+    want, want_xl, _ = O.gblock_forward(_np(u), _np(b), _np(a), np.zeros((B, nb - 1, I)), np.zeros((B, I * O_, na)))
+    assert O.rel_err(_np(full), want) < TOL
+    assert O.rel_err(_np(chunked), want) < TOL
+    assert O.rel_err(_np(st2["x"]), want_xl) < TOL
+    assert torch.equal(st2["u"], st_full["u"])
+
+
+def test_gblock_matches_unfused_path(gpu):
+    """The fused kernel and the reference's three-stage path (conv1d, all-pole op, sum) agree."""
+    B, L, I, O_, nb, na = 4, 1500, 8, 8, 8, 3
+    u, b, a, ut, x0, gy, _ = _make(B, L, I, O_, nb, na, seed=21)
+    state = {"u": ut.to(gpu), "x": x0.to(gpu)}
+    u, b, a = u.to(gpu), b.to(gpu), a.to(gpu)
+    fused = dcore.linear_dynamical_operator(u, b, a, state=state)
+    P = I * O_
+    u_buf = torch.cat((state["u"], u), dim=1)
+    w = torch.nn.functional.conv1d(u_buf.transpose(1, 2), b.permute(1, 0, 2).reshape(P, 1, nb).flip(-1), groups=I)
+    y_pairs = dcore.allpole(a.permute(1, 0, 2).reshape(P, na).expand(B, P, na), w, state["x"])
+    unfused = y_pairs.view(B, I, O_, L).sum(1).transpose(1, 2)
+    assert O.rel_err(_np(fused), _np(unfused)) < TOL
+
+
+def test_gblock_supports_reasons(gpu):
+    u = torch.randn(2, 10, 3, device=gpu)
+    b = torch.randn(5, 3, 4, device=gpu)
+    a = torch.randn(5, 3, 2, device=gpu)
+    assert "divide 64" in gblock_hip.supports(u, b, a, None, None)
+    b2, a2 = torch.randn(2, 3, 4, device=gpu), torch.randn(2, 3, 5, device=gpu)
+    assert "order" in gblock_hip.supports(u[..., :2], b2[:, :2], a2[:, :2], None, None)
+    assert "GPU-only" in gblock_hip.supports(u.cpu(), b.cpu(), a.cpu(), None, None)

@@ -462,3 +462,92 @@ def test_conv_check_rejects_forward(mutant):
 @pytest.mark.parametrize("mutant", [_conv_no_silu_prime, _conv_tail_grad_zero])
 def test_conv_check_rejects_backward(mutant):
     assert not check_conv(O.conv_silu_forward, mutant)
+
+
+# ------------------------------------------------------------------------ dynoNet G-block (FIR + all-pole + input sum)
+def _torch_gblock(u, b, a, u_tail, x0):
+    """LinearDynamicalOperator.forward written as the reference does it (dynonet/core.py:212-258):
+    grouped conv1d with flipped taps over cat(u_tail, u), the all-pole recurrence as a plain
+    sequential loop per pair (input-major pairs), then the sum over inputs; returns (y, x_last)."""
+    Bsz, L, I = u.shape
+    O_, _, nb = b.shape
+    na = a.shape[-1]
+    P = I * O_
+    ubuf = torch.cat((u_tail, u), dim=1)
+    weight = b.permute(1, 0, 2).reshape(P, 1, nb).flip(-1)
+    w = torch.nn.functional.conv1d(ubuf.transpose(1, 2), weight, groups=I)
+    ap = a.permute(1, 0, 2).reshape(P, na)
+    s = [x0[:, :, k] for k in range(na)]
+    ys = []
+    for t in range(L):
+        yt = w[:, :, t] - sum(ap[:, i] * s[i] for i in range(na))
+        ys.append(yt)
+        s = [yt] + s[:-1]
+    yp = torch.stack(ys, -1) if L > 0 else w
+    y = yp.view(Bsz, I, O_, L).sum(1).transpose(1, 2)
+    return y, torch.stack(s, -1)
+
+
+def check_gblock(fwd, bwd):
+    rng = _rng(11)
+    for Bsz, L, I, O_, nb, na in ((2, 23, 3, 2, 4, 2), (1, 9, 2, 4, 8, 3), (3, 2, 2, 2, 3, 4), (2, 30, 1, 1, 1, 1),
+                                  (1, 17, 4, 2, 6, 2)):
+        P = I * O_
+        u = rng.standard_normal((Bsz, L, I))
+        b = rng.standard_normal((O_, I, nb)) * 0.5
+        a = rng.uniform(-0.3, 0.3, (O_, I, na))
+        ut = rng.standard_normal((Bsz, nb - 1, I))
+        x0 = rng.standard_normal((Bsz, P, na))
+        args = (u, b, a, ut, x0)
+        want_y, want_xl = (t.numpy() for t in _torch_gblock(*[torch.tensor(x) for x in args]))
+        y, xl, _ = fwd(*args)
+        if O.rel_err(y, want_y) > TOL or O.rel_err(xl, want_xl) > TOL:
+            return False
+        gy = rng.standard_normal((Bsz, L, O_))
+        gxl = rng.standard_normal((Bsz, P, na))
+        want = _vjp(_torch_gblock, list(args), (gy, gxl))
+        gu, gut, gb, ga, gx0 = bwd(gy, gxl, *args)
+        for g_got, g_want in zip((gu, gb, ga, gut, gx0), want):  # the order of args
+            if O.rel_err(g_got, g_want) > TOL:
+                return False
+    return True
+
+
+def test_gblock_conv1d_loop_and_autograd():
+    assert check_gblock(O.gblock_forward, O.gblock_backward)
+
+
+def _gblock_output_major(u, b, a, u_tail, x0):
+    # pairs flattened output-major (o * I + j) instead of input-major
+    Bsz, L, I = np.shape(u)
+    O_ = np.shape(b)[0]
+    y, xl, yp = O.gblock_forward(u, b, a, u_tail, x0)
+    yp2 = yp.reshape(Bsz, O_, I, L)
+    return yp2.sum(2).transpose(0, 2, 1), xl, yp
+
+
+def _gblock_no_tail(u, b, a, u_tail, x0):
+    return O.gblock_forward(u, b, a, np.zeros_like(u_tail), x0)
+
+
+def _gblock_taps_unflipped(u, b, a, u_tail, x0):
+    return O.gblock_forward(u, np.asarray(b)[:, :, ::-1], a, u_tail, x0)
+
+
+def _gblock_drop_gxlast(gy, g_xlast, *args):
+    return O.gblock_backward(gy, None, *args)
+
+
+def _gblock_gb_unsummed_batch(gy, g_xlast, u, b, a, u_tail, x0):
+    gu, gut, gb, ga, gx0 = O.gblock_backward(gy, g_xlast, u, b, a, u_tail, x0)
+    return gu, gut, gb / np.shape(u)[0], ga, gx0
+
+
+@pytest.mark.parametrize("mutant", [_gblock_output_major, _gblock_no_tail, _gblock_taps_unflipped])
+def test_gblock_check_rejects_forward(mutant):
+    assert not check_gblock(mutant, O.gblock_backward)
+
+
+@pytest.mark.parametrize("mutant", [_gblock_drop_gxlast, _gblock_gb_unsummed_batch])
+def test_gblock_check_rejects_backward(mutant):
+    assert not check_gblock(O.gblock_forward, mutant)

@@ -48,6 +48,10 @@ _SIGNATURES: dict[str, tuple[list, object]] = {
         [_i64, _i64, _i64, _i64, _int, _ptr, _i64, _i64, _i64] + [_ptr] * 9 + [_i64, _ptr],
         _int,
     ),
+    "tsfast_hip_gblock_workspace_bytes": ([_i64] * 6, _i64),
+    "tsfast_hip_gblock_saved_doubles": ([_i64] * 5, _i64),
+    "tsfast_hip_gblock_fwd": ([_i64] * 6 + [_ptr] * 9 + [_i64, _ptr], _int),
+    "tsfast_hip_gblock_bwd": ([_i64] * 6 + [_ptr] * 14 + [_i64, _ptr], _int),
 }
 
 TSF_DTYPE_F32 = 0

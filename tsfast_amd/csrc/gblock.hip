@@ -1,0 +1,767 @@
+// Fused dynoNet G-block: LinearDynamicalOperator.forward with an all-pole denominator,
+//
+//   w_p[t] = sum_k b[o, j, k] u[t - k, j]                      (FIR per pair, u_{-m} from u_tail)
+//   y_p[t] = w_p[t] - sum_{i=1..na} a[o, j, i] y_p[t - i]       (all-pole per pair, y_{-m} from x0)
+//   y[t, o] = sum_j y_p[t]                                      (sum over inputs)
+//
+// for pairs p = j * O + o (the reference's input-major order), u [B, L, I] and y [B, L, O]
+// channel-last, fp32 in and out, fp64 recurrence state. Reference semantics:
+// tsfast/models/architectures/dynonet/core.py:196-258 (FIR conv1d :219-222, all-pole :225-235,
+// input sum :250, returned state :239-245, 254-257).
+//
+// Neither the FIR output w nor the per-pair outputs y_p (each [B, P, L], P times the size of u)
+// ever reach HBM: the forward reads u and writes y; the backward reads u and gy and writes gu.
+// Both run the single-pass look-back scheme of the all-pole kernels (allpole_core.h) over lanes
+// lane = b * P + p, 64 lanes (64 / P whole batch rows) to a tile:
+//   forward   each wave loads its lanes' u window (its 32-step chunk plus the nb - 1 step FIR
+//             halo, straight from u: the lanes of one batch row read a few contiguous bytes per
+//             step), forms w, runs the all-pole scan with look-back, saves each super-chunk's
+//             entering state for the backward (nsuper x lanes x na doubles), and sums the pairs
+//             of each output channel through its LDS tile.
+//   backward  recomputes y_p per chunk from the saved entering state, then runs two adjoint
+//             recurrences of the same dynamics with one look-back: G (the all-pole adjoint of the
+//             pair's upstream gradient g = gy[., o] + the x_last gradient) and c = A^-T (B^T g).
+//             FIR and all-pole commute, so c is the FIR adjoint of G, i.e. the pair's input
+//             gradient; forming it from B^T g needs only the gy halo to the right, not another
+//             tile's G. grad a = -sum G_t y_{t-i} and grad b = sum G_t u_{t-k} are reduced per
+//             tile; gu (sum of c over o) and the tail gradient go through LDS.
+// Orders na <= 4, nb <= 16 (taps padded to NBT in {2, 4, 8, 16} with zeros), I * O dividing 64.
+#include "common.h"
+#include "tsfast_hip.h"
+
+using namespace tsf;
+
+namespace {
+
+#include "allpole_core.h"
+
+constexpr int kGbMaxNB = 16;
+
+struct GbLane {
+  int64_t b;
+  int p, j, o;
+  bool live;
+};
+TSF_DEV GbLane gb_lane(int64_t lane, int64_t lanes, int P, int O) {
+  GbLane g;
+  g.live = lane < lanes;
+  const int64_t l = g.live ? lane : 0;
+  g.b = l / P;
+  g.p = (int)(l - g.b * P);
+  g.j = g.p / O;
+  g.o = g.p - g.j * O;
+  return g;
+}
+
+// The lane's FIR input u_s for s in [t0 - (NBT - 1), t0 + kTileT): u [B, L, I] for s in [0, L),
+// u_tail [B, nb - 1, I] for s in [-(nb - 1), 0) (zero when u_tail is NULL), zero elsewhere.
+template <int NBT>
+TSF_DEV void load_u_window(float (&uw)[kTileT + NBT - 1], const float* __restrict__ u,
+                           const float* __restrict__ u_tail, const GbLane& g, int64_t t0, int64_t L, int I, int nb) {
+  const float* __restrict__ urow = u + g.b * L * I + g.j;
+  if (t0 - (NBT - 1) >= 0 && t0 + kTileT <= L) {  // the whole window inside the sequence
+#pragma unroll
+    for (int i = 0; i < kTileT + NBT - 1; ++i) uw[i] = g.live ? urow[(t0 - (NBT - 1) + i) * I] : 0.0f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < kTileT + NBT - 1; ++i) {
+      const int64_t s = t0 - (NBT - 1) + i;
+      float v = 0.0f;
+      if (g.live) {
+        if (s >= 0 && s < L)
+          v = urow[s * I];
+        else if (s < 0 && s >= -(nb - 1) && u_tail)
+          v = u_tail[(g.b * (nb - 1) + (s + nb - 1)) * I + g.j];
+      }
+      uw[i] = v;
+    }
+  }
+}
+
+// w_{t0+i} = sum_k b_k u_{t0+i-k} for the chunk's 32 steps.
+template <int NBT>
+TSF_DEV void fir(float (&w)[kTileT], const float (&uw)[kTileT + NBT - 1], const float (&bk)[NBT]) {
+#pragma unroll
+  for (int i = 0; i < kTileT; ++i) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NBT; ++k) s = fmaf(bk[k], uw[i + NBT - 1 - k], s);
+    w[i] = s;
+  }
+}
+
+template <int NA, int NBT>
+TSF_DEV void load_coeffs(double (&av)[NA], float (&bk)[NBT], const float* __restrict__ bcoef,
+                         const float* __restrict__ acoef, const GbLane& g, int I, int nb) {
+  const int pair = g.o * I + g.j;  // [O, I, .] parameter layout
+#pragma unroll
+  for (int q = 0; q < NA; ++q) av[q] = g.live ? (double)acoef[pair * NA + q] : 0.0;
+#pragma unroll
+  for (int k = 0; k < NBT; ++k) bk[k] = (g.live && k < nb) ? bcoef[pair * nb + k] : 0.0f;
+}
+
+// Transfer matrices per lane from its pair's coefficients a [O, I, NA] (lane = b * P + j * O + o).
+template <int NA>
+__global__ void __launch_bounds__(256) gblock_transfer(const float* __restrict__ acoef, double* __restrict__ Mc,
+                                                       double* __restrict__ Ms, int64_t lanes, int I, int O, int K) {
+  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (lane >= lanes) return;
+  const int P = I * O, p = (int)(lane % P), j = p / O, o = p % O;
+  companion_powers<NA>(acoef + (o * I + j) * NA, Mc + lane * NA * NA, Ms + lane * NA * NA, K);
+}
+
+// ---------------------------------------------------------------------------------- forward
+template <int NA, int NBT>
+__global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
+    const float* __restrict__ u, const float* __restrict__ bcoef, const float* __restrict__ acoef,
+    const float* __restrict__ u_tail, const float* __restrict__ x0, float* __restrict__ y, float* __restrict__ x_last,
+    double* __restrict__ saved, const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg,
+    double* __restrict__ inc, unsigned* __restrict__ counter, int64_t B, int64_t L, int I, int O, int nb,
+    int64_t groups, int K, int64_t nsuper) {
+  __shared__ LdsTile s_lds[kLbWaves];
+  __shared__ int s_flag[kLbWaves][64];
+  __shared__ int s_pend[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int P = I * O, R = kTile / P;
+  const int64_t lanes = B * P;
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
+  __syncthreads();
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t sc = tile / groups, l0 = (tile - sc * groups) * kTile, lane = l0 + lid;
+    const GbLane g = gb_lane(lane, lanes, P, O);
+    const bool live = g.live;
+    const int64_t t0 = sc * SL + (int64_t)k * kTileT;
+    const int n = (L - t0) >= kTileT ? kTileT : (L - t0) > 0 ? (int)(L - t0) : 0;
+    double av[NA], s[NA];
+    float bk[NBT];
+    load_coeffs<NA, NBT>(av, bk, bcoef, acoef, g, I, nb);
+#pragma unroll
+    for (int q = 0; q < NA; ++q) s[q] = 0.0;
+    float xb[kTileT];
+    if (n > 0) {
+      float uw[kTileT + NBT - 1];
+      load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
+      fir<NBT>(xb, uw, bk);
+      if (n == kTileT) {
+#pragma unroll
+        for (int i = 0; i < kTileT; ++i) step<NA>(av, s, (double)xb[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kTileT; ++i)
+          if (i < n) step<NA>(av, s, (double)xb[i]);
+      }
+    }
+    double* vk = vec_area<NA>(s_lds, k) + lid * NA;
+#pragma unroll
+    for (int q = 0; q < NA; ++q) vk[q] = s[q];
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    double sup[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) sup[q] = 0.0;
+    if (k == 0 && live) {
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int jj = 0; jj < K; ++jj) {
+        double ej[NA];
+        const double* vj = vec_area<NA>(s_lds, jj) + lid * NA;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) ej[q] = vj[q];
+        matvec_add<NA>(sup, mc, sup, ej);
+      }
+      if (sc > 0 && sc + 1 < nsuper) put_vec<NA>(agg + (sc * lanes + lane) * NA, sup);
+    }
+    double S[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[lane * NA + q] : 0.0;
+    if (sc > 0)  // uniform over the workgroup
+      ap_look_back<NA>(S, agg, inc, Ms + lane * NA * NA, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
+                       k, lid, s_lds, s_flag, s_pend, &s_any);
+    if (k == 0 && live) {
+      if (saved) {
+#pragma unroll
+        for (int q = 0; q < NA; ++q) saved[(sc * lanes + lane) * NA + q] = S[q];
+      }
+      if (sc + 1 < nsuper) {
+        double ms[NA][NA], o[NA];
+        load_mat<NA>(ms, Ms + lane * NA * NA);
+        matvec_add<NA>(o, ms, S, sup);
+        put_vec<NA>(inc + (sc * lanes + lane) * NA, o);
+      }
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int jj = 0; jj < K; ++jj) {
+        double ej[NA];
+        double* vj = vec_area<NA>(s_lds, jj) + lid * NA;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) {
+          ej[q] = vj[q];
+          vj[q] = S[q];
+        }
+        matvec_add<NA>(S, mc, S, ej);
+      }
+    }
+    __syncthreads();
+    if (n > 0) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q) s[q] = vk[q];
+      if (n == kTileT) {
+#pragma unroll
+        for (int i = 0; i < kTileT; ++i) xb[i] = (float)step<NA>(av, s, (double)xb[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kTileT; ++i)
+          if (i < n) xb[i] = (float)step<NA>(av, s, (double)xb[i]);
+      }
+      // the delay line after the sequence's last step is the returned state (newest first)
+      if (x_last && live && t0 + n == L) {
+#pragma unroll
+        for (int q = 0; q < NA; ++q) x_last[lane * NA + q] = (float)s[q];
+      }
+      // y[b, t, o] = sum_j y_{j*O+o}[t]: the pairs' rows meet in the wave's LDS tile
+      float(*tl)[kTileT + 1] = s_lds[k];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i = 0; i < kTileT; ++i) tl[lid][i] = xb[i];
+      __builtin_amdgcn_wave_barrier();
+      const int64_t b0 = l0 / P;
+      for (int qi = lid; qi < R * kTileT * O; qi += kTile) {
+        const int o = qi % O, i = (qi / O) % kTileT, rb = qi / (O * kTileT);
+        const int64_t bb = b0 + rb;
+        if (i < n && bb < B) {
+          float acc = 0.0f;
+          for (int jj = 0; jj < I; ++jj) acc += tl[rb * P + jj * O + o][i];
+          y[(bb * L + t0 + i) * O + o] = acc;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+}
+
+// --------------------------------------------------------------------------------- backward
+// Per-lane partials of one tile: grad a (NA doubles) then grad b (NBT floats) in a wave's LDS tile.
+template <int NA, int NBT>
+TSF_DEV double* part_a_area(LdsTile* lds, int wv) {
+  return reinterpret_cast<double*>(&lds[wv][0][0]);
+}
+template <int NA, int NBT>
+TSF_DEV float* part_b_area(LdsTile* lds, int wv) {
+  return reinterpret_cast<float*>(reinterpret_cast<double*>(&lds[wv][0][0]) + 64 * NA);
+}
+
+template <int NA, int NBT>
+__global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
+    const float* __restrict__ gy, const float* __restrict__ g_xlast, const float* __restrict__ u,
+    const float* __restrict__ bcoef, const float* __restrict__ acoef, const float* __restrict__ u_tail,
+    const float* __restrict__ x0, const double* __restrict__ saved, const double* __restrict__ Mc,
+    const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc, unsigned* __restrict__ counter,
+    float* __restrict__ gu, float* __restrict__ gu_tail, double* __restrict__ part_ga, double* __restrict__ part_gb,
+    double* __restrict__ gh, int64_t B, int64_t L, int I, int O, int nb, int64_t groups, int K, int64_t nsuper) {
+  static_assert(64 * (NA * sizeof(double) + NBT * sizeof(float)) <= sizeof(LdsTile), "partials fit in a tile");
+  constexpr int V = 2 * NA;  // adjoint state: G then c
+  __shared__ LdsTile s_lds[kLbWaves];
+  __shared__ int s_flag[kLbWaves][64];
+  __shared__ int s_pend[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int P = I * O, R = kTile / P;
+  const int64_t lanes = B * P;
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
+  __syncthreads();
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t r = tile / groups, sc = nsuper - 1 - r, l0 = (tile - r * groups) * kTile, lane = l0 + lid;
+    const GbLane g = gb_lane(lane, lanes, P, O);
+    const bool live = g.live;
+    const int64_t t0 = sc * SL + (int64_t)k * kTileT;
+    const int n = (L - t0) >= kTileT ? kTileT : (L - t0) > 0 ? (int)(L - t0) : 0;
+    double av[NA], s[NA];
+    float bk[NBT];
+    load_coeffs<NA, NBT>(av, bk, bcoef, acoef, g, I, nb);
+    // --- forward recompute of the chunk's pair outputs y_p (into xb) from the saved state
+    float xb[kTileT];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) s[q] = 0.0;
+    if (n > 0) {
+      float uw[kTileT + NBT - 1];
+      load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
+      fir<NBT>(xb, uw, bk);
+#pragma unroll
+      for (int i = 0; i < kTileT; ++i)
+        if (i < n) step<NA>(av, s, (double)xb[i]);
+    }
+    double* vk = vec_area<NA>(s_lds, k) + lid * V;
+#pragma unroll
+    for (int q = 0; q < NA; ++q) vk[q] = s[q];
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    if (k == 0 && live) {
+      double st[NA];
+#pragma unroll
+      for (int q = 0; q < NA; ++q) st[q] = sc == 0 ? (x0 ? (double)x0[lane * NA + q] : 0.0) : saved[(sc * lanes + lane) * NA + q];
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int jj = 0; jj < K; ++jj) {
+        double ej[NA];
+        double* vj = vec_area<NA>(s_lds, jj) + lid * V;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) {
+          ej[q] = vj[q];
+          vj[q] = st[q];
+        }
+        matvec_add<NA>(st, mc, st, ej);
+      }
+    }
+    __syncthreads();
+    if (n > 0) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q) s[q] = vk[q];
+#pragma unroll
+      for (int i = 0; i < kTileT; ++i)
+        if (i < n) xb[i] = (float)step<NA>(av, s, (double)xb[i]);
+    }
+    // --- adjoint: upstream gradient window g_s for s in [t0, t0 + 32 + NBT - 1)
+    float gw[kTileT + NBT - 1];
+    {
+      const float* __restrict__ grow = gy + g.b * L * O + g.o;
+#pragma unroll
+      for (int i = 0; i < kTileT + NBT - 1; ++i) {
+        const int64_t s2 = t0 + i;
+        float v = (live && s2 < L) ? grow[s2 * O] : 0.0f;
+        if (g_xlast && live && s2 < L && s2 >= L - NA) v += g_xlast[lane * NA + (L - 1 - s2)];
+        gw[i] = v;
+      }
+    }
+    // zero-state summaries of both adjoint recurrences over the chunk, right to left
+    double sG[NA], sC[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) sG[q] = sC[q] = 0.0;
+#pragma unroll
+    for (int i = kTileT - 1; i >= 0; --i)
+      if (i < n) {
+        float h = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < NBT; ++kk) h = fmaf(bk[kk], gw[i + kk], h);
+        step<NA>(av, sG, (double)gw[i]);
+        step<NA>(av, sC, (double)h);
+      }
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      vk[q] = sG[q];
+      vk[NA + q] = sC[q];
+    }
+    __syncthreads();
+    double sup[V];
+#pragma unroll
+    for (int q = 0; q < V; ++q) sup[q] = 0.0;
+    if (k == 0 && live) {
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int jj = K - 1; jj >= 0; --jj) {
+        double fj[V];
+        const double* vj = vec_area<NA>(s_lds, jj) + lid * V;
+#pragma unroll
+        for (int q = 0; q < V; ++q) fj[q] = vj[q];
+        block_matvec_add<NA, 2>(sup, mc, sup, fj);
+      }
+      if (sc > 0 && sc + 1 < nsuper) put_vec<V>(agg + (sc * lanes + lane) * V, sup);
+    }
+    double Rv[V];  // adjoint state entering the super-chunk from the right
+#pragma unroll
+    for (int q = 0; q < V; ++q) Rv[q] = 0.0;
+    if (sc + 1 < nsuper)  // uniform over the workgroup
+      ap_look_back<NA, 2>(Rv, agg, inc, Ms + lane * NA * NA, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane,
+                          K, k, lid, s_lds, s_flag, s_pend, &s_any);
+    if (k == 0 && live) {
+      if (sc > 0) {
+        double ms[NA][NA], o[V];
+        load_mat<NA>(ms, Ms + lane * NA * NA);
+        block_matvec_add<NA, 2>(o, ms, Rv, sup);
+        put_vec<V>(inc + (sc * lanes + lane) * V, o);
+      }
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int jj = K - 1; jj >= 0; --jj) {
+        double fj[V];
+        double* vj = vec_area<NA>(s_lds, jj) + lid * V;
+#pragma unroll
+        for (int q = 0; q < V; ++q) {
+          fj[q] = vj[q];
+          vj[q] = Rv[q];
+        }
+        block_matvec_add<NA, 2>(Rv, mc, Rv, fj);
+      }
+    }
+    __syncthreads();
+    // --- adjoint sweep: G, c, grad a, grad b, head taps and the tail gradient
+    double ga[NA];
+    float gbk[NBT];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) ga[q] = 0.0;
+#pragma unroll
+    for (int kk = 0; kk < NBT; ++kk) gbk[kk] = 0.0f;
+    float(*tl)[kTileT + 1] = s_lds[k];
+    if (n > 0) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q) {
+        sG[q] = vk[q];
+        sC[q] = vk[NA + q];
+      }
+      float gt[NBT > 1 ? NBT - 1 : 1];  // tail gradient of this lane, t0 == 0 only
+#pragma unroll
+      for (int m = 0; m < (NBT > 1 ? NBT - 1 : 1); ++m) gt[m] = 0.0f;
+      float uw[kTileT + NBT - 1];
+      load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
+#pragma unroll
+      for (int i = kTileT - 1; i >= 0; --i)
+        if (i < n) {
+          const double yu = xb[i];
+#pragma unroll
+          for (int q = 0; q < NA; ++q) ga[q] = fma(sG[q], yu, ga[q]);  // sG_q = G_{t+1+q} before the step
+          float h = 0.0f;
+#pragma unroll
+          for (int kk = 0; kk < NBT; ++kk) h = fmaf(bk[kk], gw[i + kk], h);
+          const float G = (float)step<NA>(av, sG, (double)gw[i]);
+          xb[i] = (float)step<NA>(av, sC, (double)h);  // c_t, the pair's input gradient at t
+#pragma unroll
+          for (int kk = 0; kk < NBT; ++kk) gbk[kk] = fmaf(G, uw[i + NBT - 1 - kk], gbk[kk]);
+          if (t0 == 0) {
+            // u_tail[m] (time m - (nb - 1)) met b_kk at steps i = m - (nb - 1) + kk >= 0
+#pragma unroll
+            for (int kk = 1; kk < NBT; ++kk)
+              if (i < kk && i - kk + NBT - 1 >= 0) gt[i - kk + NBT - 1] = fmaf(bk[kk], G, gt[i - kk + NBT - 1]);
+            if (i < NA && live) gh[lane * NA + i] = G;  // G_0 .. G_{NA-1} for the x0 head taps
+          }
+        }
+      // gu[b, t, j] = sum_o c_{j*O+o}[t] through the wave's LDS tile
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i = 0; i < kTileT; ++i) tl[lid][i] = xb[i];
+      __builtin_amdgcn_wave_barrier();
+      const int64_t b0 = l0 / P;
+      for (int qi = lid; qi < R * kTileT * I; qi += kTile) {
+        const int jj = qi % I, i = (qi / I) % kTileT, rb = qi / (I * kTileT);
+        const int64_t bb = b0 + rb;
+        if (i < n && bb < B) {
+          float acc = 0.0f;
+          for (int o = 0; o < O; ++o) acc += tl[rb * P + jj * O + o][i];
+          gu[(bb * L + t0 + i) * I + jj] = acc;
+        }
+      }
+      if (t0 == 0 && gu_tail && nb > 1) {
+        // gt[m'] holds tail position m' - (NBT - 1) + (nb - 1) = m; only m' >= NBT - nb are real
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int m = 0; m < (NBT > 1 ? NBT - 1 : 1); ++m) tl[lid][m] = gt[m];
+        __builtin_amdgcn_wave_barrier();
+        for (int qi = lid; qi < R * (nb - 1) * I; qi += kTile) {
+          const int jj = qi % I, m = (qi / I) % (nb - 1), rb = qi / (I * (nb - 1));
+          const int64_t bb = b0 + rb;
+          if (bb < B) {
+            float acc = 0.0f;
+            for (int o = 0; o < O; ++o) acc += tl[rb * P + jj * O + o][m + NBT - nb];
+            gu_tail[(bb * (nb - 1) + m) * I + jj] = acc;
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    // grad a / grad b partials: summed over the K chunks in LDS, one row per (super-chunk, lane)
+    {
+      double* pa = part_a_area<NA, NBT>(s_lds, k) + lid * NA;
+      float* pb = part_b_area<NA, NBT>(s_lds, k) + lid * NBT;
+#pragma unroll
+      for (int q = 0; q < NA; ++q) pa[q] = ga[q];
+#pragma unroll
+      for (int kk = 0; kk < NBT; ++kk) pb[kk] = gbk[kk];
+    }
+    __syncthreads();
+    if (k == 0 && live) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q) {
+        double t = 0.0;
+        for (int jj = 0; jj < K; ++jj) t += (part_a_area<NA, NBT>(s_lds, jj) + lid * NA)[q];
+        part_ga[(sc * lanes + lane) * NA + q] = t;
+      }
+#pragma unroll
+      for (int kk = 0; kk < NBT; ++kk) {
+        double t = 0.0;
+        for (int jj = 0; jj < K; ++jj) t += (double)(part_b_area<NA, NBT>(s_lds, jj) + lid * NBT)[kk];
+        part_gb[(sc * lanes + lane) * NBT + kk] = t;
+      }
+    }
+    __syncthreads();  // wave 0's reads of every tile precede the next tile's writes into them
+  }
+}
+
+// Per lane: grad a = -(sum over super-chunks + x0 head taps), grad x0 (head taps plus the x_last
+// gradient that lands on x0 when L < na), grad b = sum over super-chunks; the super-chunk sums
+// run in a fixed order (16 waves per 64 lanes, contiguous segments, then in order).
+template <int NA, int NBT>
+__global__ void __launch_bounds__(1024) gblock_finish_lane(
+    const float* __restrict__ acoef, const float* __restrict__ x0, const float* __restrict__ g_xlast,
+    const double* __restrict__ gh, const double* __restrict__ part_ga, const double* __restrict__ part_gb,
+    double* __restrict__ ga_lane, double* __restrict__ gb_lane, float* __restrict__ gx0, int64_t lanes, int I, int O,
+    int64_t L, int64_t n) {
+  __shared__ double s_p[16][64];
+  __shared__ double s_tot[NA + NBT][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t lane = blockIdx.x * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t seg = (n + 15) / 16;
+  const int64_t r0 = k * seg, r1 = (r0 + seg < n) ? r0 + seg : n;
+  for (int q = 0; q < NA + NBT; ++q) {
+    double acc = 0.0;
+    if (live)
+      for (int64_t r = r0; r < r1; ++r)
+        acc += q < NA ? part_ga[(r * lanes + lane) * NA + q] : part_gb[(r * lanes + lane) * NBT + (q - NA)];
+    s_p[k][lid] = acc;
+    __syncthreads();
+    if (k == 0) {
+      double t = s_p[0][lid];
+      for (int j = 1; j < 16; ++j) t += s_p[j][lid];
+      s_tot[q][lid] = t;
+    }
+    __syncthreads();
+  }
+  if (k != 0 || !live) return;  // no barrier follows
+  const int P = I * O;
+  const int p = (int)(lane % P), j = p / O, o = p % O;
+  const int pair = o * I + j;
+  double Gh[NA];  // G_0 .. G_{NA-1}, zero past the end of the sequence
+#pragma unroll
+  for (int q = 0; q < NA; ++q) Gh[q] = (q < L) ? gh[lane * NA + q] : 0.0;
+#pragma unroll
+  for (int q = 0; q < NA; ++q) {
+    double t = s_tot[q][lid];
+    if (x0) {
+#pragma unroll
+      for (int jj = 1; jj <= q + 1; ++jj) t = fma(Gh[q + 1 - jj], (double)x0[lane * NA + jj - 1], t);
+    }
+    ga_lane[lane * NA + q] = -t;
+  }
+#pragma unroll
+  for (int kk = 0; kk < NBT; ++kk) gb_lane[lane * NBT + kk] = s_tot[NA + kk][lid];
+  if (gx0) {
+#pragma unroll
+    for (int jj = 0; jj < NA; ++jj) {
+      double t = 0.0;
+#pragma unroll
+      for (int i = jj + 1; i <= NA; ++i) t = fma((double)acoef[pair * NA + i - 1], Gh[i - 1 - jj], t);
+      t = -t;
+      // x_last[q] = x0[q - L] for q >= L: that part of the x_last gradient reaches x0 directly
+      if (g_xlast && jj + L < NA) t += (double)g_xlast[lane * NA + jj + L];
+      gx0[lane * NA + jj] = (float)t;
+    }
+  }
+}
+
+// grad a [O, I, NA] and grad b [O, I, nb]: per pair, the sum over batch rows in order.
+template <int NA, int NBT>
+__global__ void __launch_bounds__(256) gblock_finish_pairs(const double* __restrict__ ga_lane,
+                                                            const double* __restrict__ gb_lane, float* __restrict__ ga,
+                                                            float* __restrict__ gb, int64_t B, int I, int O, int nb) {
+  const int P = I * O;
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)P * (NA + nb)) return;
+  const int p = (int)(idx / (NA + nb)), q = (int)(idx % (NA + nb));
+  const int j = p / O, o = p % O, pair = o * I + j;
+  double t = 0.0;
+  for (int64_t b = 0; b < B; ++b)
+    t += q < NA ? ga_lane[(b * P + p) * NA + q] : gb_lane[(b * P + p) * NBT + (q - NA)];
+  if (q < NA)
+    ga[pair * NA + q] = (float)t;
+  else
+    gb[pair * nb + (q - NA)] = (float)t;
+}
+
+// L == 0: the returned state is x0 (zero without it).
+__global__ void __launch_bounds__(256) gblock_copy_state(const float* __restrict__ x0, float* __restrict__ x_last,
+                                                          int64_t n) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) x_last[i] = x0 ? x0[i] : 0.0f;
+}
+
+__global__ void __launch_bounds__(256) gblock_zero(float* __restrict__ p, int64_t n) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+// ------------------------------------------------------------------------------------- host
+int nbt_for(int64_t nb) { return nb <= 2 ? 2 : nb <= 4 ? 4 : nb <= 8 ? 8 : 16; }
+
+// Workspace (both directions): the tile counter, agg and inc [nsuper][lanes][2 na] (reset before
+// each scan), grad-a and grad-b partials [nsuper][lanes][na | NBT], the head taps G_0.. [lanes][na],
+// per-lane grad a / grad b [lanes][na | NBT], and the transfer matrices Mc, Ms [lanes][na][na].
+struct GbPlan {
+  LbPlan lb;
+  int64_t lanes = 0;
+  int nbt = 2;
+  size_t off_agg = 0, off_inc = 0, off_pa = 0, off_pb = 0, off_gh = 0, off_gal = 0, off_gbl = 0, off_Mc = 0,
+         off_Ms = 0, bytes = 0;
+};
+
+GbPlan gb_plan(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na) {
+  GbPlan p;
+  p.lanes = B * I * O;
+  p.nbt = nbt_for(nb);
+  p.lb = lb_plan(p.lanes, L, na);
+  const size_t f = 8, rows = (size_t)p.lb.nsuper * p.lanes;
+  p.off_agg = kCounterBytes;
+  p.off_inc = p.off_agg + f * rows * 2 * na;
+  p.off_pa = p.off_inc + f * rows * 2 * na;
+  p.off_pb = p.off_pa + f * rows * na;
+  p.off_gh = p.off_pb + f * rows * p.nbt;
+  p.off_gal = p.off_gh + f * p.lanes * na;
+  p.off_gbl = p.off_gal + f * p.lanes * na;
+  p.off_Mc = p.off_gbl + f * p.lanes * p.nbt;
+  p.off_Ms = p.off_Mc + f * p.lanes * na * na;
+  p.bytes = p.off_Ms + f * p.lanes * na * na;
+  return p;
+}
+
+int gb_args_status(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na) {
+  if (B < 0 || L < 0 || I < 1 || O < 1 || nb < 1 || na < 1) return TSF_ERR_ARG;
+  if (na > kLbNA || nb > kGbMaxNB || kTile % (I * O) != 0) return TSF_ERR_UNSUPPORTED;
+  if (B * I * O * (L > 0 ? L : 1) >= ((int64_t)1 << 40)) return TSF_ERR_UNSUPPORTED;
+  return TSF_OK;
+}
+
+template <int NA, int NBT>
+void fwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const float* u, const float* bcoef,
+              const float* acoef, const float* u_tail, const float* x0, float* y, float* x_last, double* saved,
+              char* ws, hipStream_t s) {
+  static int occ[kMaxNA + 1];
+  double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
+  double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
+  hipLaunchKernelGGL((gblock_transfer<NA>), grid_for(p.lanes), dim3(256), 0, s, acoef, Mc, Ms, p.lanes, I, O, p.lb.K);
+  lookback_reset_launch(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, s);
+  const int64_t tiles = p.lb.groups * p.lb.nsuper, cap = resident_wgs(gblock_fwd_lb<NA, NBT>, 64 * p.lb.K, occ);
+  hipLaunchKernelGGL((gblock_fwd_lb<NA, NBT>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.lb.K), 0, s, u,
+                     bcoef, acoef, u_tail, x0, y, x_last, saved, (const double*)Mc, (const double*)Ms,
+                     reinterpret_cast<double*>(ws + p.off_agg), reinterpret_cast<double*>(ws + p.off_inc),
+                     reinterpret_cast<unsigned*>(ws), B, L, I, O, nb, p.lb.groups, p.lb.K, p.lb.nsuper);
+}
+
+template <int NA, int NBT>
+void bwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const float* gy, const float* g_xlast,
+              const float* u, const float* bcoef, const float* acoef, const float* u_tail, const float* x0,
+              const double* saved, float* gu, float* gu_tail, float* gb, float* ga, float* gx0, char* ws,
+              hipStream_t s) {
+  static int occ[kMaxNA + 1];
+  double* gh = reinterpret_cast<double*>(ws + p.off_gh);
+  double* pa = reinterpret_cast<double*>(ws + p.off_pa);
+  double* pb = reinterpret_cast<double*>(ws + p.off_pb);
+  if (L > 0) {
+    double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
+    double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
+    hipLaunchKernelGGL((gblock_transfer<NA>), grid_for(p.lanes), dim3(256), 0, s, acoef, Mc, Ms, p.lanes, I, O,
+                       p.lb.K);
+    lookback_reset_launch(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, s);
+    const int64_t tiles = p.lb.groups * p.lb.nsuper, cap = resident_wgs(gblock_bwd_lb<NA, NBT>, 64 * p.lb.K, occ);
+    hipLaunchKernelGGL((gblock_bwd_lb<NA, NBT>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.lb.K), 0, s,
+                       gy, g_xlast, u, bcoef, acoef, u_tail, x0, saved, (const double*)Mc, (const double*)Ms,
+                       reinterpret_cast<double*>(ws + p.off_agg), reinterpret_cast<double*>(ws + p.off_inc),
+                       reinterpret_cast<unsigned*>(ws), gu, gu_tail, pa, pb, gh, B, L, I, O, nb, p.lb.groups, p.lb.K,
+                       p.lb.nsuper);
+  } else if (gu_tail && nb > 1) {
+    const int64_t nt = B * (nb - 1) * I;
+    hipLaunchKernelGGL(gblock_zero, grid_for(nt), dim3(256), 0, s, gu_tail, nt);
+  }
+  double* gal = reinterpret_cast<double*>(ws + p.off_gal);
+  double* gbl = reinterpret_cast<double*>(ws + p.off_gbl);
+  hipLaunchKernelGGL((gblock_finish_lane<NA, NBT>), dim3((unsigned)p.lb.groups > 0 ? (unsigned)p.lb.groups : 1u),
+                     dim3(1024), 0, s, acoef, x0, g_xlast, (const double*)gh, (const double*)pa, (const double*)pb, gal,
+                     gbl, gx0, p.lanes, I, O, L, L > 0 ? p.lb.nsuper : (int64_t)0);
+  const int64_t np = (int64_t)I * O * (NA + nb);
+  hipLaunchKernelGGL((gblock_finish_pairs<NA, NBT>), grid_for(np), dim3(256), 0, s, (const double*)gal,
+                     (const double*)gbl, ga, gb, B, I, O, nb);
+}
+
+#define TSF_GB_CASES(X) \
+  X(1, 2) X(1, 4) X(1, 8) X(1, 16) X(2, 2) X(2, 4) X(2, 8) X(2, 16) X(3, 2) X(3, 4) X(3, 8) X(3, 16) X(4, 2) X(4, 4) X(4, 8) X(4, 16)
+
+}  // namespace
+
+extern "C" {
+
+int64_t tsfast_hip_gblock_workspace_bytes(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na) {
+  if (gb_args_status(B, L, I, O, nb, na) != TSF_OK) return -1;
+  return (int64_t)gb_plan(B, L, I, O, nb, na).bytes;
+}
+
+int64_t tsfast_hip_gblock_saved_doubles(int64_t B, int64_t L, int64_t I, int64_t O, int64_t na) {
+  if (gb_args_status(B, L, I, O, 1, na) != TSF_OK) return -1;
+  const GbPlan p = gb_plan(B, L, I, O, 1, na);
+  return p.lb.nsuper * p.lanes * na;
+}
+
+int tsfast_hip_gblock_fwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na, const float* u,
+                          const float* b, const float* a, const float* u_tail, const float* x0, float* y,
+                          float* x_last, double* saved, void* workspace, int64_t workspace_bytes, void* stream) {
+  const int st = gb_args_status(B, L, I, O, nb, na);
+  if (st != TSF_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (B == 0) return TSF_OK;
+  if (L == 0) {
+    if (x_last) hipLaunchKernelGGL(gblock_copy_state, grid_for(B * I * O * na), dim3(256), 0, s, x0, x_last, B * I * O * na);
+    return tsf_launch_status();
+  }
+  if (!u || !b || !a || !y) return TSF_ERR_ARG;
+  if (!workspace || workspace_bytes < tsfast_hip_gblock_workspace_bytes(B, L, I, O, nb, na)) return TSF_ERR_WORKSPACE;
+  const GbPlan p = gb_plan(B, L, I, O, nb, na);
+  char* ws = static_cast<char*>(workspace);
+  switch (na * 100 + p.nbt) {
+#define X(NA_, NB_)                                                                                                  \
+  case NA_ * 100 + NB_:                                                                                              \
+    fwd_impl<NA_, NB_>(p, B, L, (int)I, (int)O, (int)nb, u, b, a, u_tail, x0, y, x_last, saved, ws, s); \
+    break;
+    TSF_GB_CASES(X)
+#undef X
+    default:
+      return TSF_ERR_UNSUPPORTED;
+  }
+  return tsf_launch_status();
+}
+
+int tsfast_hip_gblock_bwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na, const float* gy,
+                          const float* g_xlast, const float* u, const float* b, const float* a, const float* u_tail,
+                          const float* x0, const double* saved, float* gu, float* gu_tail, float* gb, float* ga,
+                          float* gx0, void* workspace, int64_t workspace_bytes, void* stream) {
+  const int st = gb_args_status(B, L, I, O, nb, na);
+  if (st != TSF_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!b || !a || !gb || !ga) return TSF_ERR_ARG;
+  if (L > 0 && (!gy || !u || !gu)) return TSF_ERR_ARG;
+  if (L > 0 && !saved && gb_plan(B, L, I, O, nb, na).lb.nsuper > 1) return TSF_ERR_ARG;
+  if (!workspace || workspace_bytes < tsfast_hip_gblock_workspace_bytes(B, L, I, O, nb, na)) return TSF_ERR_WORKSPACE;
+  const GbPlan p = gb_plan(B, L, I, O, nb, na);
+  char* ws = static_cast<char*>(workspace);
+  switch (na * 100 + p.nbt) {
+#define X(NA_, NB_)                                                                                                  \
+  case NA_ * 100 + NB_:                                                                                              \
+    bwd_impl<NA_, NB_>(p, B, L, (int)I, (int)O, (int)nb, gy, g_xlast, u, b, a, u_tail, x0, saved, gu, gu_tail, gb, ga, \
+                       gx0, ws, s);                                                                                  \
+    break;
+    TSF_GB_CASES(X)
+#undef X
+    default:
+      return TSF_ERR_UNSUPPORTED;
+  }
+  return tsf_launch_status();
+}
+
+}  // extern "C"

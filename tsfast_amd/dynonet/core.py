@@ -9,15 +9,16 @@ else ``linear_recurrence`` over the companion matrices.
 
 from __future__ import annotations
 
-__all__ = ["linear_recurrence", "allpole", "companion"]
+__all__ = ["linear_recurrence", "allpole", "companion", "linear_dynamical_operator"]
 
 import torch
 import torch.nn.functional as F
 
 from ..dispatch import resolve
-from . import allpole_hip
+from . import allpole_hip, gblock_hip
 
 _ALLPOLE_BACKENDS = {"hip": allpole_hip}
+_GBLOCK_BACKENDS = {"hip": gblock_hip}
 
 
 def _doubling_matrix_scan(A: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
@@ -118,3 +119,51 @@ def allpole(a: torch.Tensor, w: torch.Tensor, y0: torch.Tensor | None = None) ->
     na = a.shape[-1]
     x = linear_recurrence(companion(a), F.pad(w.unsqueeze(-1), (0, na - 1)), y0)
     return x[..., 0]
+
+
+def linear_dynamical_operator(
+    u: torch.Tensor,
+    b_coeff: torch.Tensor,
+    a_coeff: torch.Tensor,
+    state: dict | None = None,
+    return_state: bool = False,
+) -> torch.Tensor | tuple[torch.Tensor, dict]:
+    """The body of ``LinearDynamicalOperator.forward`` (dynonet/core.py:196-258) for ``na >= 1``.
+
+    ``u [B, L, I]``, ``b_coeff [O, I, nb]``, ``a_coeff [O, I, na]``; ``state`` is the reference's
+    ``{"u": FIR tail [B, nb-1, I], "x": IIR states [B, I*O, na]}`` (zeros if None). The fused
+    G-block kernel runs FIR, all-pole and the sum over inputs in one pass when it serves the
+    inputs; otherwise the reference's three stages run (grouped ``conv1d`` with flipped taps,
+    the all-pole op per pair, the sum over inputs). Returns ``y [B, L, O]`` and, with
+    ``return_state``, the new state.
+    """
+    B, L, I = u.shape
+    O, _, nb = b_coeff.shape
+    na = a_coeff.shape[-1]
+    P = I * O
+    match state:
+        case {"u": u_tail, "x": x0}:
+            pass
+        case None:
+            u_tail = u.new_zeros(B, nb - 1, I)
+            x0 = u.new_zeros(B, P, na)
+        case _:
+            raise TypeError(f"expected state dict {{'u': tensor, 'x': tensor}}, got {type(state)}")
+    order = ("hip",) if u.device.type == "cuda" else ()
+    mod = resolve("dynonet.gblock", _GBLOCK_BACKENDS, order, (u, b_coeff, a_coeff, u_tail, x0))
+    if mod is not None:
+        y, x_last = mod.run(u, b_coeff, a_coeff, u_tail, x0)
+    else:
+        u_buf = torch.cat((u_tail, u), dim=1)
+        weight = b_coeff.permute(1, 0, 2).reshape(P, 1, nb).flip(-1)
+        w = F.conv1d(u_buf.transpose(1, 2), weight, groups=I)
+        a_pairs = a_coeff.permute(1, 0, 2).reshape(P, na).expand(B, P, na)
+        y_pairs = allpole(a_pairs, w, x0)
+        x_last = (
+            y_pairs[..., L - na :].flip(-1) if L >= na else torch.cat((y_pairs.flip(-1), x0[..., : na - L]), dim=-1)
+        )
+        y = y_pairs.view(B, I, O, L).sum(1).transpose(1, 2)
+    if not return_state:
+        return y
+    u_buf = torch.cat((u_tail, u), dim=1)
+    return y, {"u": u_buf[:, u_buf.shape[1] - (nb - 1) :], "x": x_last}

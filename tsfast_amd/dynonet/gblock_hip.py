@@ -1,0 +1,178 @@
+"""Fused dynoNet G-block, HIP backend: FIR + all-pole + sum over inputs in one pass.
+
+The body of ``LinearDynamicalOperator.forward`` (``tsfast/models/architectures/dynonet/core.py:196-258``)
+for a non-zero denominator: the reference forms ``w = F.conv1d(cat(u_tail, u), flipped taps,
+groups=I)`` (``:219-222``), runs the all-pole op per pair (``:225-235``, ``_fused_allpole``) and sums
+the pairs over inputs (``:250``). Here one kernel per direction does all three, so neither ``w``
+nor the per-pair outputs (each ``[B, I*O, L]``) reach HBM; the backward recomputes the pair
+outputs from per-super-chunk states the forward saves (a few MB).
+
+``supports(u, b_coeff, a_coeff, u_tail, x0)`` and ``run(u, b_coeff, a_coeff, u_tail, x0) ->
+(y, x_last)``, differentiable in all inputs through the ``tsfast_hip::dynonet_gblock`` /
+``dynonet_gblock_bwd`` custom ops. Shapes follow the reference: ``u [B, L, I]``, ``b_coeff
+[O, I, nb]``, ``a_coeff [O, I, na]``, ``u_tail [B, nb-1, I]``, ``x0 [B, I*O, na]`` (pairs input-major,
+newest first); ``y [B, L, O]``, ``x_last [B, I*O, na]``. float32; ``1 <= na <= 4``, ``nb <= 16``,
+``I*O`` dividing 64.
+"""
+
+from __future__ import annotations
+
+__all__ = ["supports", "run"]
+
+import torch
+
+from .. import _lib
+
+_MAX_NA = 4
+_MAX_NB = 16
+
+
+def supports(u, b_coeff, a_coeff, u_tail, x0) -> str | None:
+    """Reason the fused G-block kernel cannot handle these tensors, or None if it can."""
+    if u.device.type != "cuda":
+        return f"u on {u.device.type}, hip backend is GPU-only"
+    tensors = {"u": u, "b_coeff": b_coeff, "a_coeff": a_coeff, "u_tail": u_tail, "x0": x0}
+    for name, t in tensors.items():
+        if t is None:
+            continue
+        if t.dtype != torch.float32:
+            return f"{name} dtype {t.dtype} not float32"
+        if t.device != u.device:
+            return f"{name} on {t.device}, u on {u.device}"
+    if u.dim() != 3 or b_coeff.dim() != 3 or a_coeff.dim() != 3:
+        return "expected u [B, L, I], b_coeff [O, I, nb], a_coeff [O, I, na]"
+    B, L, I = u.shape
+    O, I_b, nb = b_coeff.shape
+    na = a_coeff.shape[-1]
+    if I_b != I or tuple(a_coeff.shape[:2]) != (O, I):
+        return f"coefficient shapes {tuple(b_coeff.shape)}, {tuple(a_coeff.shape)} do not match {I} inputs"
+    if not 1 <= na <= _MAX_NA:
+        return f"denominator order {na} outside [1, {_MAX_NA}]"
+    if not 1 <= nb <= _MAX_NB:
+        return f"numerator taps {nb} outside [1, {_MAX_NB}]"
+    if 64 % (I * O) != 0:
+        return f"{I} x {O} channel pairs do not divide 64"
+    if u_tail is not None and tuple(u_tail.shape) != (B, nb - 1, I):
+        return f"u_tail.shape {tuple(u_tail.shape)} != {(B, nb - 1, I)}"
+    if x0 is not None and tuple(x0.shape) != (B, I * O, na):
+        return f"x0.shape {tuple(x0.shape)} != {(B, I * O, na)}"
+    return None
+
+
+def _dims(u, b, a):
+    B, L, I = u.shape
+    O, _, nb = b.shape
+    return B, L, I, O, nb, a.shape[-1]
+
+
+def _workspace(lib, u, b, a):
+    n = lib.tsfast_hip_gblock_workspace_bytes(*_dims(u, b, a))
+    if n < 0:
+        raise RuntimeError("tsfast_hip_gblock_workspace_bytes: unsupported shape")
+    return _lib.workspace(n, u.device), n
+
+
+def _screen(u, b, a, u_tail, x0):
+    dev = u.device
+    for name, t in (("u", u), ("b_coeff", b), ("a_coeff", a), ("u_tail", u_tail), ("x0", x0)):
+        _lib.require(t, name, (torch.float32,), dev)
+
+
+@torch.library.custom_op("tsfast_hip::dynonet_gblock", mutates_args=())
+def _gblock_op(
+    u: torch.Tensor, b: torch.Tensor, a: torch.Tensor, u_tail: torch.Tensor | None, x0: torch.Tensor | None
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    u, b, a = u.contiguous(), b.contiguous(), a.contiguous()
+    u_tail = u_tail.contiguous() if u_tail is not None else None
+    x0 = x0.contiguous() if x0 is not None else None
+    _screen(u, b, a, u_tail, x0)
+    B, L, I, O, nb, na = _dims(u, b, a)
+    y = torch.empty(B, L, O, device=u.device, dtype=torch.float32)
+    x_last = torch.empty(B, I * O, na, device=u.device, dtype=torch.float32)
+    saved = torch.empty(max(lib.tsfast_hip_gblock_saved_doubles(B, L, I, O, na), 1), device=u.device,
+                        dtype=torch.float64)
+    ws, nbytes = _workspace(lib, u, b, a)
+    _lib.check(
+        lib.tsfast_hip_gblock_fwd(
+            B, L, I, O, nb, na, _lib.ptr(u), _lib.ptr(b), _lib.ptr(a), _lib.ptr(u_tail), _lib.ptr(x0), _lib.ptr(y),
+            _lib.ptr(x_last), _lib.ptr(saved), _lib.ptr(ws), nbytes, _lib.stream_of(u),
+        ),
+        "tsfast_hip_gblock_fwd",
+    )
+    return y, x_last, saved
+
+
+@_gblock_op.register_fake
+def _(u, b, a, u_tail, x0):
+    B, L, _ = u.shape
+    O = b.shape[0]
+    P, na = u.shape[-1] * O, a.shape[-1]
+    return u.new_empty(B, L, O), u.new_empty(B, P, na), u.new_empty(1, dtype=torch.float64)
+
+
+@torch.library.custom_op("tsfast_hip::dynonet_gblock_bwd", mutates_args=())
+def _gblock_bwd_op(
+    gy: torch.Tensor, g_xlast: torch.Tensor | None, u: torch.Tensor, b: torch.Tensor, a: torch.Tensor,
+    u_tail: torch.Tensor | None, x0: torch.Tensor | None, saved: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    gy = gy.contiguous()
+    g_xlast = g_xlast.contiguous() if g_xlast is not None else None
+    _lib.require(gy, "gy", (torch.float32,), u.device)
+    _lib.require(g_xlast, "g_xlast", (torch.float32,), u.device)
+    B, L, I, O, nb, na = _dims(u, b, a)
+    gu = torch.empty_like(u)
+    gu_tail = torch.zeros(B, nb - 1, I, device=u.device, dtype=torch.float32)
+    gb = torch.empty_like(b)
+    ga = torch.empty_like(a)
+    gx0 = torch.empty(B, I * O, na, device=u.device, dtype=torch.float32)
+    ws, nbytes = _workspace(lib, u, b, a)
+    _lib.check(
+        lib.tsfast_hip_gblock_bwd(
+            B, L, I, O, nb, na, _lib.ptr(gy), _lib.ptr(g_xlast), _lib.ptr(u), _lib.ptr(b), _lib.ptr(a),
+            _lib.ptr(u_tail), _lib.ptr(x0), _lib.ptr(saved), _lib.ptr(gu), _lib.ptr(gu_tail), _lib.ptr(gb),
+            _lib.ptr(ga), _lib.ptr(gx0), _lib.ptr(ws), nbytes, _lib.stream_of(u),
+        ),
+        "tsfast_hip_gblock_bwd",
+    )
+    return gu, gu_tail, gb, ga, gx0
+
+
+@_gblock_bwd_op.register_fake
+def _(gy, g_xlast, u, b, a, u_tail, x0, saved):
+    B, _, I = u.shape
+    O, _, nb = b.shape
+    na = a.shape[-1]
+    return (torch.empty_like(u), u.new_empty(B, nb - 1, I), torch.empty_like(b), torch.empty_like(a),
+            u.new_empty(B, I * O, na))
+
+
+def _gblock_setup(ctx, inputs, output):
+    u, b, a, u_tail, x0 = inputs
+    _, _, saved = output
+    ctx.has_tail, ctx.has_x0 = u_tail is not None, x0 is not None
+    ctx.save_for_backward(u, b, a, u_tail, x0, saved)
+
+
+def _gblock_backward(ctx, gy, g_xlast, g_saved):
+    u, b, a, u_tail, x0, saved = ctx.saved_tensors
+    if gy is None:
+        gy = torch.zeros(u.shape[0], u.shape[1], b.shape[0], device=u.device, dtype=torch.float32)
+    gu, gu_tail, gb, ga, gx0 = _gblock_bwd_op(gy, g_xlast, u.contiguous(), b.contiguous(), a.contiguous(),
+                                              u_tail.contiguous() if u_tail is not None else None,
+                                              x0.contiguous() if x0 is not None else None, saved)
+    return gu, gb, ga, (gu_tail if ctx.has_tail else None), (gx0 if ctx.has_x0 else None)
+
+
+_gblock_op.register_autograd(_gblock_backward, setup_context=_gblock_setup)
+
+
+def run(u, b_coeff, a_coeff, u_tail, x0):
+    """Fused G-block: ``y [B, L, O]`` and the all-pole state ``x_last [B, I*O, na]`` (newest first).
+
+    ``u_tail`` (the last ``nb - 1`` inputs before ``u``) and ``x0`` may be None (zero initial
+    conditions). Differentiable in all inputs (``tsfast_hip::dynonet_gblock``).
+    """
+    y, x_last, _ = _gblock_op(u, b_coeff, a_coeff, u_tail, x0)
+    return y, x_last
