@@ -15,7 +15,8 @@ route — brute-force closed-form sums, ``scipy.signal.lfilter``, a textbook sel
 written as einsums, the companion-matrix doubling scan, and torch float64 autograd through
 sequential loops — plus special cases (constant coefficients reduce the selective scan to the
 diagonal one, delta -> 0 makes Mamba the identity map on the state, N = 1 reduces it to a
-scalar recurrence).
+scalar recurrence); the G-block functions compose the FIR and all-pole restatements and are
+checked against autograd through the reference's grouped-conv1d formulation.
 """
 
 from __future__ import annotations
