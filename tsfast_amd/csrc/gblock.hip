@@ -291,78 +291,43 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     double av[NA], s[NA];
     float bk[NBT];
     load_coeffs<NA, NBT>(av, bk, bcoef, acoef, g, I, nb);
-    // --- forward recompute of the chunk's pair outputs y_p (into xb) from the saved state
-    float xb[kTileT];
-#pragma unroll
-    for (int q = 0; q < NA; ++q) s[q] = 0.0;
-    if (n > 0) {
-      float uw[kTileT + NBT - 1];
-      load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
-      fir<NBT>(xb, uw, bk);
-#pragma unroll
-      for (int i = 0; i < kTileT; ++i)
-        if (i < n) step<NA>(av, s, (double)xb[i]);
-    }
-    double* vk = vec_area<NA>(s_lds, k) + lid * V;
-#pragma unroll
-    for (int q = 0; q < NA; ++q) vk[q] = s[q];
-    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
-    __syncthreads();
-    if (k == 0 && live) {
-      double st[NA];
-#pragma unroll
-      for (int q = 0; q < NA; ++q) st[q] = sc == 0 ? (x0 ? (double)x0[lane * NA + q] : 0.0) : saved[(sc * lanes + lane) * NA + q];
-      double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
-      for (int jj = 0; jj < K; ++jj) {
-        double ej[NA];
-        double* vj = vec_area<NA>(s_lds, jj) + lid * V;
-#pragma unroll
-        for (int q = 0; q < NA; ++q) {
-          ej[q] = vj[q];
-          vj[q] = st[q];
-        }
-        matvec_add<NA>(st, mc, st, ej);
-      }
-    }
-    __syncthreads();
-    if (n > 0) {
-#pragma unroll
-      for (int q = 0; q < NA; ++q) s[q] = vk[q];
-#pragma unroll
-      for (int i = 0; i < kTileT; ++i)
-        if (i < n) xb[i] = (float)step<NA>(av, s, (double)xb[i]);
-    }
-    // --- adjoint: upstream gradient window g_s for s in [t0, t0 + 32 + NBT - 1)
-    float gw[kTileT + NBT - 1];
-    {
+    // The phases are ordered so that no 32-step window is live across the look-back: the adjoint
+    // summaries and look-back first (g window dropped after the summaries), then the forward
+    // recompute of y_p, then the sweep over a reloaded g window.
+    auto load_g_window = [&](float (&gw_)[kTileT + NBT - 1]) __attribute__((always_inline)) {
       const float* __restrict__ grow = gy + g.b * L * O + g.o;
 #pragma unroll
       for (int i = 0; i < kTileT + NBT - 1; ++i) {
         const int64_t s2 = t0 + i;
         float v = (live && s2 < L) ? grow[s2 * O] : 0.0f;
         if (g_xlast && live && s2 < L && s2 >= L - NA) v += g_xlast[lane * NA + (L - 1 - s2)];
-        gw[i] = v;
+        gw_[i] = v;
       }
-    }
-    // zero-state summaries of both adjoint recurrences over the chunk, right to left
+    };
+    double* vk = vec_area<NA>(s_lds, k) + lid * V;
     double sG[NA], sC[NA];
+    {
+      // --- zero-state summaries of both adjoint recurrences over the chunk, right to left
+      float gw[kTileT + NBT - 1];
+      load_g_window(gw);
 #pragma unroll
-    for (int q = 0; q < NA; ++q) sG[q] = sC[q] = 0.0;
+      for (int q = 0; q < NA; ++q) sG[q] = sC[q] = 0.0;
 #pragma unroll
-    for (int i = kTileT - 1; i >= 0; --i)
-      if (i < n) {
-        float h = 0.0f;
+      for (int i = kTileT - 1; i >= 0; --i)
+        if (i < n) {
+          float h = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < NBT; ++kk) h = fmaf(bk[kk], gw[i + kk], h);
-        step<NA>(av, sG, (double)gw[i]);
-        step<NA>(av, sC, (double)h);
-      }
+          for (int kk = 0; kk < NBT; ++kk) h = fmaf(bk[kk], gw[i + kk], h);
+          step<NA>(av, sG, (double)gw[i]);
+          step<NA>(av, sC, (double)h);
+        }
+    }
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
       vk[q] = sG[q];
       vk[NA + q] = sC[q];
     }
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
     __syncthreads();
     double sup[V];
 #pragma unroll
@@ -406,6 +371,52 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
       }
     }
     __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {  // this chunk's adjoint entering state, kept for the sweep
+      sG[q] = vk[q];
+      sC[q] = vk[NA + q];
+    }
+    // --- forward recompute of the chunk's pair outputs y_p (into xb) from the saved state
+    float xb[kTileT];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) s[q] = 0.0;
+    if (n > 0) {
+      float uw[kTileT + NBT - 1];
+      load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
+      fir<NBT>(xb, uw, bk);
+#pragma unroll
+      for (int i = 0; i < kTileT; ++i)
+        if (i < n) step<NA>(av, s, (double)xb[i]);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int q = 0; q < NA; ++q) vk[q] = s[q];
+    __syncthreads();
+    if (k == 0 && live) {
+      double st[NA];
+#pragma unroll
+      for (int q = 0; q < NA; ++q) st[q] = sc == 0 ? (x0 ? (double)x0[lane * NA + q] : 0.0) : saved[(sc * lanes + lane) * NA + q];
+      double mc[NA][NA];
+      load_mat<NA>(mc, Mc + lane * NA * NA);
+      for (int jj = 0; jj < K; ++jj) {
+        double ej[NA];
+        double* vj = vec_area<NA>(s_lds, jj) + lid * V;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) {
+          ej[q] = vj[q];
+          vj[q] = st[q];
+        }
+        matvec_add<NA>(st, mc, st, ej);
+      }
+    }
+    __syncthreads();
+    if (n > 0) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q) s[q] = vk[q];
+#pragma unroll
+      for (int i = 0; i < kTileT; ++i)
+        if (i < n) xb[i] = (float)step<NA>(av, s, (double)xb[i]);
+    }
     // --- adjoint sweep: G, c, grad a, grad b, head taps and the tail gradient
     double ga[NA];
     float gbk[NBT];
@@ -415,16 +426,10 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     for (int kk = 0; kk < NBT; ++kk) gbk[kk] = 0.0f;
     float(*tl)[kTileT + 1] = s_lds[k];
     if (n > 0) {
-#pragma unroll
-      for (int q = 0; q < NA; ++q) {
-        sG[q] = vk[q];
-        sC[q] = vk[NA + q];
-      }
-      float gt[NBT > 1 ? NBT - 1 : 1];  // tail gradient of this lane, t0 == 0 only
-#pragma unroll
-      for (int m = 0; m < (NBT > 1 ? NBT - 1 : 1); ++m) gt[m] = 0.0f;
-      float uw[kTileT + NBT - 1];
-      load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
+      float gw[kTileT + NBT - 1];
+      load_g_window(gw);
+      // pass 1, right to left: G, c (into xb) and grad a; G_t then goes into gw[i + NBT - 1],
+      // the window slot no later step reads (step i' < i reads gw[i' .. i' + NBT - 1])
 #pragma unroll
       for (int i = kTileT - 1; i >= 0; --i)
         if (i < n) {
@@ -436,15 +441,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
           for (int kk = 0; kk < NBT; ++kk) h = fmaf(bk[kk], gw[i + kk], h);
           const float G = (float)step<NA>(av, sG, (double)gw[i]);
           xb[i] = (float)step<NA>(av, sC, (double)h);  // c_t, the pair's input gradient at t
-#pragma unroll
-          for (int kk = 0; kk < NBT; ++kk) gbk[kk] = fmaf(G, uw[i + NBT - 1 - kk], gbk[kk]);
-          if (t0 == 0) {
-            // u_tail[m] (time m - (nb - 1)) met b_kk at steps i = m - (nb - 1) + kk >= 0
-#pragma unroll
-            for (int kk = 1; kk < NBT; ++kk)
-              if (i < kk && i - kk + NBT - 1 >= 0) gt[i - kk + NBT - 1] = fmaf(bk[kk], G, gt[i - kk + NBT - 1]);
-            if (i < NA && live) gh[lane * NA + i] = G;  // G_0 .. G_{NA-1} for the x0 head taps
-          }
+          gw[i + NBT - 1] = G;
         }
       // gu[b, t, j] = sum_o c_{j*O+o}[t] through the wave's LDS tile
       __builtin_amdgcn_wave_barrier();
@@ -460,6 +457,28 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
           for (int o = 0; o < O; ++o) acc += tl[rb * P + jj * O + o][i];
           gu[(bb * L + t0 + i) * I + jj] = acc;
         }
+      }
+      // pass 2: grad b = sum_t G_t u_{t-k} (u window reloaded), head taps, tail gradient
+      float gt[NBT > 1 ? NBT - 1 : 1];  // tail gradient of this lane, t0 == 0 only
+#pragma unroll
+      for (int m = 0; m < (NBT > 1 ? NBT - 1 : 1); ++m) gt[m] = 0.0f;
+      {
+        float uw[kTileT + NBT - 1];
+        load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
+#pragma unroll
+        for (int i = 0; i < kTileT; ++i)
+          if (i < n) {
+            const float G = gw[i + NBT - 1];
+#pragma unroll
+            for (int kk = 0; kk < NBT; ++kk) gbk[kk] = fmaf(G, uw[i + NBT - 1 - kk], gbk[kk]);
+            if (t0 == 0) {
+              // u_tail[m] (time m - (nb - 1)) met b_kk at steps i = m - (nb - 1) + kk >= 0
+#pragma unroll
+              for (int kk = 1; kk < NBT; ++kk)
+                if (i < kk && i - kk + NBT - 1 >= 0) gt[i - kk + NBT - 1] = fmaf(bk[kk], G, gt[i - kk + NBT - 1]);
+              if (i < NA && live) gh[lane * NA + i] = G;  // G_0 .. G_{NA-1} for the x0 head taps
+            }
+          }
       }
       if (t0 == 0 && gu_tail && nb > 1) {
         // gt[m'] holds tail position m' - (NBT - 1) + (nb - 1) = m; only m' >= NBT - nb are real
@@ -580,6 +599,7 @@ __global__ void __launch_bounds__(256) gblock_finish_pairs(const double* __restr
   const int p = (int)(idx / (NA + nb)), q = (int)(idx % (NA + nb));
   const int j = p / O, o = p % O, pair = o * I + j;
   double t = 0.0;
+#pragma unroll 8
   for (int64_t b = 0; b < B; ++b)
     t += q < NA ? ga_lane[(b * P + p) * NA + q] : gb_lane[(b * P + p) * NBT + (q - NA)];
   if (q < NA)
