@@ -129,7 +129,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   constexpr int IT = C::IT_F, BCI = C::BC_F;
   __shared__ float2 s_sc[TF][DT];       // (delta, delta * u)
   __shared__ float2 s_bc[TF][NS];       // (B, C)
-  __shared__ float s_y[TF][NG][DT];     // y partial per lane (state group)
+  // y partial per lane (state group); odd groups store channel dl at column dl ^ 16, so the two
+  // lanes of a state pair (same channel, rows 32 floats apart) write to different banks
+  __shared__ float s_y[TF][NG][DT];
 
   const int tid = threadIdx.x;
   int64_t tile, b;
@@ -259,7 +261,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
           h[j] = fmaf(lam, h[j], sv[r].y * bcv[r][j].x);
           y = fmaf(h[j], bcv[r][j].y, y);
         }
-        s_y[i][ng][dl] = y;
+        s_y[i][ng][dl ^ ((ng & 1) << 4)] = y;
       }
       // checkpoint slot k holds the state after step (k + 1) * CHK - 1 (layout [B, NC, N, D])
       const int ie = i0 + kRd - 1;
@@ -279,7 +281,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       if (idx < TF * DT && t < len && oact) {
         float y = 0.0f;
 #pragma unroll
-        for (int g = 0; g < NG; ++g) y += s_y[t][g][od];
+        for (int g = 0; g < NG; ++g) y += s_y[t][g][od ^ ((g & 1) << 4)];
         const float zz = o_z[k];
         const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
         const float yv = fmaf(dp_o, o_u[k], y);
