@@ -170,6 +170,25 @@ int tsfast_hip_gblock_bwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb
                           const float* x0, const double* saved, float* gu, float* gu_tail, float* gb, float* ga,
                           float* gx0, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Constant-matrix linear recurrence  x_t = A x_{t-1} + v_t  (x_0 = x0, zero when NULL), the
+ * tsfast::linear_recurrence op and its adjoint tsfast::linear_recurrence_bwd
+ * (tsfast/models/architectures/dynonet/core.py:45-52 forward, :60-73 adjoint
+ * G_t = A^T G_{t+1} + g_t, grad_A = sum_t G_t x_{t-1}^T, grad_x0 = A^T G_1; the reference runs
+ * both as log-doubling scans, :23-37). Lanes are the flattened leading dims:
+ * A/gA [lanes, n, n] row-major, v/x/g/gv [lanes, L, n] contiguous, x0/gx0 [lanes, n].
+ * float32 in and out, fp64 state; 1 <= n <= 4, else TSF_ERR_UNSUPPORTED. The workspace holds
+ * the look-back state of a single-pass scan, re-initialised by each call on its stream: two
+ * calls in flight must not share one.
+ */
+int64_t tsfast_hip_linrec_workspace_bytes(int64_t lanes, int64_t L, int64_t n);
+int tsfast_hip_linrec_fwd(int64_t lanes, int64_t L, int64_t n, const float* A, const float* v, const float* x0,
+                          float* x, void* workspace, int64_t workspace_bytes, void* stream);
+/* out = the forward's x; gA is the full per-lane gradient; gx0 written iff x0 given. */
+int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, const float* A, const float* out,
+                          const float* x0, float* gA, float* gv, float* gx0, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,7 +16,9 @@ written as einsums, the companion-matrix doubling scan, and torch float64 autogr
 sequential loops — plus special cases (constant coefficients reduce the selective scan to the
 diagonal one, delta -> 0 makes Mamba the identity map on the state, N = 1 reduces it to a
 scalar recurrence); the G-block functions compose the FIR and all-pole restatements and are
-checked against autograd through the reference's grouped-conv1d formulation.
+checked against autograd through the reference's grouped-conv1d formulation; the constant-matrix
+recurrence is checked against matrix-power closed forms, torch float64 autograd through a loop,
+and its diagonal and companion special cases (the diagonal scan and the all-pole filter).
 """
 
 from __future__ import annotations
@@ -38,6 +40,8 @@ __all__ = [
     "conv_silu_backward",
     "gblock_forward",
     "gblock_backward",
+    "linrec_forward",
+    "linrec_backward",
 ]
 
 
@@ -366,3 +370,37 @@ def gblock_backward(gy, g_xlast, u, b, a, u_tail, x0):
         gb[:, :, k] = np.einsum("bjol,bjl->oj", gw, seg)
         gubuf[:, nb - 1 - k : nb - 1 - k + L, :] += np.einsum("bjol,oj->blj", gw, b[:, :, k])
     return gubuf[:, nb - 1 :], gubuf[:, : nb - 1], gb, ga, gx0
+
+
+# --------------------------------------------------------------------------- constant-matrix recurrence
+def linrec_forward(A, v, x0=None):
+    """``x_t = A x_{t-1} + v_t`` per lane with a constant matrix (dynonet/core.py:23-52, 103-127):
+    A [M, n, n], v [M, L, n], x0 [M, n] or None (zero start). Returns x_1 .. x_L as [M, L, n]."""
+    A, v = _hi(A), _hi(v)
+    M, L, n = v.shape
+    x = np.zeros((M, n)) if x0 is None else _hi(x0).copy()
+    out = np.empty((M, L, n))
+    for t in range(L):
+        x = np.einsum("mij,mj->mi", A, x) + v[:, t]
+        out[:, t] = x
+    return out
+
+
+def linrec_backward(g, A, out, x0=None):
+    """Adjoint (dynonet/core.py:60-73): ``G_t = A^T G_{t+1} + g_t`` from the right end,
+    ``gv = G``, ``gA = sum_t G_t x_{t-1}^T`` with ``x_0 = x0`` (zero if None), ``gx0 = A^T G_1``
+    (None without x0; zero for an empty sequence). Returns ``(gA, gv, gx0)``."""
+    g, A, out = _hi(g), _hi(A), _hi(out)
+    M, L, n = g.shape
+    G = np.zeros((M, L, n))
+    acc = np.zeros((M, n))
+    for t in range(L - 1, -1, -1):
+        acc = np.einsum("mji,mj->mi", A, acc) + g[:, t]
+        G[:, t] = acc
+    head = np.zeros((M, 1, n)) if x0 is None else _hi(x0)[:, None, :]
+    prev = np.concatenate([head, out[:, :-1]], axis=1)[:, :L]
+    gA = np.einsum("mti,mtj->mij", G, prev)
+    gx0 = None
+    if x0 is not None:
+        gx0 = np.einsum("mji,mj->mi", A, G[:, 0]) if L > 0 else np.zeros((M, n))
+    return gA, G, gx0

@@ -551,3 +551,101 @@ def test_gblock_check_rejects_forward(mutant):
 @pytest.mark.parametrize("mutant", [_gblock_drop_gxlast, _gblock_gb_unsummed_batch])
 def test_gblock_check_rejects_backward(mutant):
     assert not check_gblock(O.gblock_forward, mutant)
+
+
+# ------------------------------------------------------------------------ constant-matrix recurrence
+def _torch_linrec_loop(A, v, x0):
+    x = torch.zeros_like(v[:, 0]) if x0 is None else x0
+    outs = []
+    for t in range(v.shape[1]):
+        x = torch.einsum("mij,mj->mi", A, x) + v[:, t]
+        outs.append(x)
+    return torch.stack(outs, 1)
+
+
+def check_linrec(fwd, bwd):
+    """Forward: the matrix-power closed form ``x_t = A^(t+1) x0 + sum_{s<=t} A^(t-s) v_s``.
+    Backward: torch float64 autograd through a sequential loop (all of gA, gv, gx0)."""
+    rng = _rng(11)
+    for M, L, n, with_x0 in ((3, 9, 3, True), (2, 1, 2, True), (2, 6, 4, False), (4, 7, 1, True), (2, 5, 5, True)):
+        A = rng.standard_normal((M, n, n)) * (0.8 / np.sqrt(n))
+        v = rng.standard_normal((M, L, n))
+        x0 = rng.standard_normal((M, n)) if with_x0 else None
+        P = [np.stack([np.linalg.matrix_power(A[m], p) for m in range(M)]) for p in range(L + 1)]
+        want = np.stack(
+            [
+                sum(np.einsum("mij,mj->mi", P[t - s], v[:, s]) for s in range(t + 1))
+                + (np.einsum("mij,mj->mi", P[t + 1], x0) if with_x0 else 0.0)
+                for t in range(L)
+            ],
+            1,
+        )
+        out = fwd(A, v, x0)
+        if O.rel_err(out, want) > TOL:
+            return False
+        g = rng.standard_normal((M, L, n))
+        want_A, want_v, want_x0 = _vjp(_torch_linrec_loop, [A, v, x0], g)
+        gA, gv, gx0 = bwd(g, A, out, x0)
+        if O.rel_err(gA, want_A) > TOL or O.rel_err(gv, want_v) > TOL:
+            return False
+        if with_x0 and O.rel_err(gx0, want_x0) > TOL:
+            return False
+    return True
+
+
+def test_linrec_closed_form_and_autograd():
+    assert check_linrec(O.linrec_forward, O.linrec_backward)
+
+
+def test_linrec_special_cases():
+    """A diagonal matrix is n independent diagonal scans; a companion matrix with input
+    (w_t, 0, ..., 0) is the all-pole filter, its first state component the output."""
+    rng = _rng(12)
+    M, L, n = 3, 17, 3
+    lam = rng.uniform(-0.9, 0.9, (M, n))
+    v, x0, g = rng.standard_normal((M, L, n)), rng.standard_normal((M, n)), rng.standard_normal((M, L, n))
+    A = np.stack([np.diag(lam[m]) for m in range(M)])
+    out = O.linrec_forward(A, v, x0)
+    assert O.rel_err(out, O.diag_forward(lam, v, x0)) < TOL
+    gA, gv, gx0 = O.linrec_backward(g, A, out, x0)
+    glam, gvd, gx0d = O.diag_backward(g, lam, out, x0)
+    assert O.rel_err(np.diagonal(gA, axis1=1, axis2=2), glam) < TOL
+    assert O.rel_err(gv, gvd) < TOL and O.rel_err(gx0, gx0d) < TOL
+    a = rng.standard_normal((M, n)) * 0.3
+    w = rng.standard_normal((M, L))
+    y0 = rng.standard_normal((M, n))
+    C = np.zeros((M, n, n))
+    C[:, 0, :] = -a
+    C[:, 1:, :-1] = np.eye(n - 1)
+    vc = np.zeros((M, L, n))
+    vc[:, :, 0] = w
+    assert O.rel_err(O.linrec_forward(C, vc, y0)[:, :, 0], O.allpole_forward(a, w, y0)) < TOL
+
+
+def _linrec_transposed(A, v, x0=None):
+    return O.linrec_forward(np.swapaxes(np.asarray(A), 1, 2), v, x0)
+
+
+def _linrec_bwd_adjoint_untransposed(g, A, out, x0=None):
+    return O.linrec_backward(g, np.swapaxes(np.asarray(A), 1, 2), out, x0)
+
+
+def _linrec_bwd_gA_transposed(g, A, out, x0=None):
+    gA, gv, gx0 = O.linrec_backward(g, A, out, x0)
+    return np.swapaxes(gA, 1, 2), gv, gx0
+
+
+def _linrec_bwd_prev_off_by_one(g, A, out, x0=None):
+    gA, gv, gx0 = O.linrec_backward(g, A, out, x0)
+    return np.einsum("mti,mtj->mij", gv, np.asarray(out, dtype=np.float64)), gv, gx0
+
+
+def test_linrec_check_rejects_forward():
+    assert not check_linrec(_linrec_transposed, O.linrec_backward)
+
+
+@pytest.mark.parametrize(
+    "mutant", [_linrec_bwd_adjoint_untransposed, _linrec_bwd_gA_transposed, _linrec_bwd_prev_off_by_one]
+)
+def test_linrec_check_rejects_backward(mutant):
+    assert not check_linrec(O.linrec_forward, mutant)

@@ -1,0 +1,536 @@
+// Constant-matrix linear recurrence  x_t = A x_{t-1} + v_t  and its adjoint, float32 I/O.
+//
+// Reference semantics: tsfast/models/architectures/dynonet/core.py:23-52 (the log-doubling scan
+// and the tsfast::linear_recurrence op, x0 folded into the first step), :60-73 (the analytic
+// adjoint: G_t = A^T G_{t+1} + g_t, grad_v = G, grad_A = sum_t G_t x_{t-1}^T, grad_x0 = A^T G_1)
+// and :103-127 (linear_recurrence, which broadcasts A, v and x0 to common leading dims).
+//
+// Layout: lanes are the flattened leading dims. A [lanes, n, n] row-major, v, x and g
+// [lanes, L, n] (per lane the n state components of a step are contiguous, steps follow each
+// other), x0 [lanes, n]. The state size n (1..4) is a template parameter, so a step is n x n
+// fp64 FMAs on registers.
+//
+// A lane's sequence is one row of L * n floats, so a chunk of S = floor(32 / n) steps is a row
+// segment of S * n <= 32 floats, and the [64 x 33] LDS tiles of the all-pole scan move the
+// segments of 64 lanes with coalesced 128-byte row accesses. The parallel structure is the
+// single-pass look-back scan of allpole_core.h with a dense step: a chunk maps its entering state
+// s to Mc s + e (Mc = A^S), a super-chunk of K chunks to Ms s + e (Ms = A^(S K)), and only the
+// e vectors are published between workgroups. The adjoint runs the same machinery from the right
+// end with A^T; its grad_A partials are summed over the K chunks of a tile in LDS, written per
+// super-chunk, and added up in a fixed order by linrec_finish (deterministic run to run).
+//
+// Arithmetic: fp32 in and out, fp64 state, transfer matrices, published words and grad_A sums.
+
+#include "common.h"
+#include "tsfast_hip.h"
+
+using namespace tsf;
+
+namespace {
+
+#include "allpole_core.h"
+
+constexpr int kMaxNS = 4;  // state sizes on the single-pass path (an n x n fp64 matrix per thread)
+static_assert(kMaxNS <= kLbNA, "the look-back areas hold kLbNA doubles per lane");
+
+template <int NS>
+constexpr int steps_per_chunk() {
+  return kTileT / NS;
+}
+
+// Transfer matrices per lane: Mc = P^S and Ms = Mc^K with P = A (forward) or A^T (adjoint).
+template <int NS>
+__global__ void __launch_bounds__(256) linrec_transfer(const float* __restrict__ A, double* __restrict__ Mc,
+                                                       double* __restrict__ Ms, int64_t lanes, int K, int transpose) {
+  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (lane >= lanes) return;
+  constexpr int S = steps_per_chunk<NS>();
+  double P[NS][NS], R[NS][NS], T[NS][NS];
+  auto mul = [&](double (&dst)[NS][NS], const double (&x)[NS][NS], const double (&y)[NS][NS]) {
+#pragma unroll
+    for (int r = 0; r < NS; ++r)
+#pragma unroll
+      for (int c = 0; c < NS; ++c) {
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < NS; ++j) s = fma(x[r][j], y[j][c], s);
+        T[r][c] = s;
+      }
+#pragma unroll
+    for (int r = 0; r < NS; ++r)
+#pragma unroll
+      for (int c = 0; c < NS; ++c) dst[r][c] = T[r][c];
+  };
+  auto power = [&](double (&base)[NS][NS], int e) {  // R = base^e (base is consumed)
+#pragma unroll
+    for (int r = 0; r < NS; ++r)
+#pragma unroll
+      for (int c = 0; c < NS; ++c) R[r][c] = (r == c) ? 1.0 : 0.0;
+    for (; e > 0; e >>= 1) {
+      if (e & 1) mul(R, R, base);
+      if (e > 1) mul(base, base, base);
+    }
+  };
+  const float* a = A + lane * NS * NS;
+#pragma unroll
+  for (int r = 0; r < NS; ++r)
+#pragma unroll
+    for (int c = 0; c < NS; ++c) P[r][c] = (double)(transpose ? a[c * NS + r] : a[r * NS + c]);
+  power(P, S);
+#pragma unroll
+  for (int r = 0; r < NS; ++r)
+#pragma unroll
+    for (int c = 0; c < NS; ++c) {
+      Mc[lane * NS * NS + r * NS + c] = R[r][c];
+      P[r][c] = R[r][c];
+    }
+  power(P, K);
+#pragma unroll
+  for (int r = 0; r < NS; ++r)
+#pragma unroll
+    for (int c = 0; c < NS; ++c) Ms[lane * NS * NS + r * NS + c] = R[r][c];
+}
+
+// One step s <- m s + x (x the NS floats of the step).
+template <int NS>
+TSF_DEV void dense_step(const double (&m)[NS][NS], double (&s)[NS], const float* x) {
+  double t[NS];
+#pragma unroll
+  for (int r = 0; r < NS; ++r) {
+    double acc = (double)x[r];
+#pragma unroll
+    for (int c = 0; c < NS; ++c) acc = fma(m[r][c], s[c], acc);
+    t[r] = acc;
+  }
+#pragma unroll
+  for (int r = 0; r < NS; ++r) s[r] = t[r];
+}
+
+// Forward. A tile is 64 lanes x one super-chunk of K chunks; wave k owns chunk k. The wave moves
+// its chunk's row segments through its LDS tile into registers, summarises the chunk from a zero
+// state, and after the look-back re-runs it from its entering state, writing x in place of v.
+template <int NS>
+__global__ void __launch_bounds__(64 * kLbWaves) linrec_fwd_lb(
+    const float* __restrict__ A, const float* __restrict__ v, const float* __restrict__ x0, float* __restrict__ x,
+    const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
+    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper) {
+  constexpr int S = steps_per_chunk<NS>();
+  __shared__ LdsTile s_lds[kLbWaves];
+  __shared__ int s_flag[kLbWaves][64];
+  __shared__ int s_pend[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * S, row = L * NS;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
+  __syncthreads();
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t sc = tile / groups, l0 = (tile - sc * groups) * kTile, lane = l0 + lid;
+    const bool live = lane < lanes;
+    const int64_t t0 = sc * SL + (int64_t)k * S;
+    const int n = (L - t0) >= S ? S : (L - t0) > 0 ? (int)(L - t0) : 0;
+    double am[NS][NS], s[NS];
+#pragma unroll
+    for (int r = 0; r < NS; ++r) {
+#pragma unroll
+      for (int c = 0; c < NS; ++c) am[r][c] = live ? (double)A[lane * NS * NS + r * NS + c] : 0.0;
+      s[r] = 0.0;
+    }
+    float xb[kTileT];
+    if (n > 0) chunk_to_regs(xb, v, lanes, row, l0, t0 * NS, n * NS, s_lds[k], lid);
+    if (n == S) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) dense_step<NS>(am, s, &xb[i * NS]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < S; ++i)
+        if (i < n) dense_step<NS>(am, s, &xb[i * NS]);
+    }
+    double* vk = vec_area<NS>(s_lds, k) + lid * NS;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) vk[q] = s[q];
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    // wave 0: the super-chunk's zero-state end (chunks before a non-empty one are full, so Mc is
+    // every fold's matrix; the map is published only for full super-chunks)
+    double sup[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) sup[q] = 0.0;
+    if (k == 0 && live) {
+      double mc[NS][NS];
+      load_mat<NS>(mc, Mc + lane * NS * NS);
+      for (int j = 0; j < K; ++j) {
+        double ej[NS];
+        const double* vj = vec_area<NS>(s_lds, j) + lid * NS;
+#pragma unroll
+        for (int q = 0; q < NS; ++q) ej[q] = vj[q];
+        matvec_add<NS>(sup, mc, sup, ej);
+      }
+      if (sc > 0 && sc + 1 < nsuper) put_vec<NS>(agg + (sc * lanes + lane) * NS, sup);
+    }
+    double St[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) St[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[lane * NS + q] : 0.0;
+    if (sc > 0)  // uniform over the workgroup
+      ap_look_back<NS>(St, agg, inc, Ms + lane * NS * NS, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
+                       k, lid, s_lds, s_flag, s_pend, &s_any);
+    if (k == 0 && live) {
+      if (sc + 1 < nsuper) {
+        double ms[NS][NS], o[NS];
+        load_mat<NS>(ms, Ms + lane * NS * NS);
+        matvec_add<NS>(o, ms, St, sup);
+        put_vec<NS>(inc + (sc * lanes + lane) * NS, o);
+      }
+      double mc[NS][NS];
+      load_mat<NS>(mc, Mc + lane * NS * NS);
+      for (int j = 0; j < K; ++j) {  // entering state of every chunk, in place of its summary
+        double ej[NS];
+        double* vj = vec_area<NS>(s_lds, j) + lid * NS;
+#pragma unroll
+        for (int q = 0; q < NS; ++q) {
+          ej[q] = vj[q];
+          vj[q] = St[q];
+        }
+        matvec_add<NS>(St, mc, St, ej);
+      }
+    }
+    __syncthreads();
+    if (n > 0) {
+#pragma unroll
+      for (int q = 0; q < NS; ++q) s[q] = vk[q];
+      auto fstep = [&](int i) __attribute__((always_inline)) {
+        dense_step<NS>(am, s, &xb[i * NS]);
+#pragma unroll
+        for (int r = 0; r < NS; ++r) xb[i * NS + r] = (float)s[r];
+      };
+      if (n == S) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) fstep(i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < S; ++i)
+          if (i < n) fstep(i);
+      }
+      __builtin_amdgcn_wave_barrier();
+      regs_to_chunk(xb, x, lanes, row, l0, t0 * NS, n * NS, s_lds[k], lid);
+    }
+  }
+}
+
+// Backward: G_t = A^T G_{t+1} + g_t is the same scan from the right end with A^T (Mc and Ms are
+// the powers of A^T here). After the look-back each wave re-runs its chunk from the right, writes
+// grad_v = G, and accumulates grad_A += G_t x_{t-1}^T in fp64, with x_{t-1} from the forward
+// output (loaded after the look-back, so it does not stay in registers across it) or x0. The
+// tile's K per-chunk sums are added in LDS and written per super-chunk.
+template <int NS>
+__global__ void __launch_bounds__(64 * kLbWaves) linrec_bwd_lb(
+    const float* __restrict__ A, const float* __restrict__ g, const float* __restrict__ out,
+    const float* __restrict__ x0, float* __restrict__ gv, float* __restrict__ gx0, const double* __restrict__ Mc,
+    const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc, double* __restrict__ part,
+    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper) {
+  constexpr int S = steps_per_chunk<NS>(), NN = NS * NS;
+  static_assert(64 * NN * sizeof(double) <= sizeof(LdsTile), "a wave's grad_A sums fit in its tile");
+  __shared__ LdsTile s_lds[kLbWaves];
+  __shared__ int s_flag[kLbWaves][64];
+  __shared__ int s_pend[64];
+  __shared__ int s_any;
+  __shared__ unsigned s_tile[2];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t tiles = groups * nsuper, SL = (int64_t)K * S, row = L * NS;
+  if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
+  __syncthreads();
+  for (int buf = 0;; buf ^= 1) {
+    const int64_t tile = s_tile[buf];
+    if (tile >= tiles) break;
+    unsigned next = 0;
+    if (threadIdx.x == 0) next = take_tile(counter);
+    const int64_t r = tile / groups, sc = nsuper - 1 - r, l0 = (tile - r * groups) * kTile, lane = l0 + lid;
+    const bool live = lane < lanes;
+    const int64_t t0 = sc * SL + (int64_t)k * S;
+    const int n = (L - t0) >= S ? S : (L - t0) > 0 ? (int)(L - t0) : 0;
+    double at[NS][NS], s[NS];  // at = A^T
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+#pragma unroll
+      for (int c = 0; c < NS; ++c) at[i][c] = live ? (double)A[lane * NN + c * NS + i] : 0.0;
+      s[i] = 0.0;
+    }
+    float gb[kTileT];
+    if (n > 0) chunk_to_regs(gb, g, lanes, row, l0, t0 * NS, n * NS, s_lds[k], lid);
+    if (n == S) {
+#pragma unroll
+      for (int i = S - 1; i >= 0; --i) dense_step<NS>(at, s, &gb[i * NS]);
+    } else {
+#pragma unroll
+      for (int i = S - 1; i >= 0; --i)
+        if (i < n) dense_step<NS>(at, s, &gb[i * NS]);
+    }
+    double* vk = vec_area<NS>(s_lds, k) + lid * NS;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) vk[q] = s[q];
+    if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
+    __syncthreads();
+    // wave 0: the super-chunk's exit to the left from a zero entering state, folded from its
+    // rightmost chunk (chunks past the end of the sequence are empty and contribute zero)
+    double sup[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) sup[q] = 0.0;
+    if (k == 0 && live) {
+      double mc[NS][NS];
+      load_mat<NS>(mc, Mc + lane * NN);
+      for (int j = K - 1; j >= 0; --j) {
+        double fj[NS];
+        const double* vj = vec_area<NS>(s_lds, j) + lid * NS;
+#pragma unroll
+        for (int q = 0; q < NS; ++q) fj[q] = vj[q];
+        matvec_add<NS>(sup, mc, sup, fj);
+      }
+      if (sc > 0 && sc + 1 < nsuper) put_vec<NS>(agg + (sc * lanes + lane) * NS, sup);
+    }
+    double R[NS];  // adjoint state entering the super-chunk from the right
+#pragma unroll
+    for (int q = 0; q < NS; ++q) R[q] = 0.0;
+    if (sc + 1 < nsuper)  // uniform over the workgroup
+      ap_look_back<NS>(R, agg, inc, Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid,
+                       s_lds, s_flag, s_pend, &s_any);
+    if (k == 0 && live) {
+      if (sc > 0) {
+        double ms[NS][NS], o[NS];
+        load_mat<NS>(ms, Ms + lane * NN);
+        matvec_add<NS>(o, ms, R, sup);
+        put_vec<NS>(inc + (sc * lanes + lane) * NS, o);
+      }
+      double mc[NS][NS];
+      load_mat<NS>(mc, Mc + lane * NN);
+      for (int j = K - 1; j >= 0; --j) {  // state entering every chunk from the right
+        double fj[NS];
+        double* vj = vec_area<NS>(s_lds, j) + lid * NS;
+#pragma unroll
+        for (int q = 0; q < NS; ++q) {
+          fj[q] = vj[q];
+          vj[q] = R[q];
+        }
+        matvec_add<NS>(R, mc, R, fj);
+      }
+    }
+    __syncthreads();
+    double acc[NN];
+#pragma unroll
+    for (int q = 0; q < NN; ++q) acc[q] = 0.0;
+    if (n > 0) {
+#pragma unroll
+      for (int q = 0; q < NS; ++q) s[q] = vk[q];
+      auto bstep = [&](int i) __attribute__((always_inline)) {
+        dense_step<NS>(at, s, &gb[i * NS]);
+#pragma unroll
+        for (int q = 0; q < NS; ++q) gb[i * NS + q] = (float)s[q];
+      };
+      if (n == S) {
+#pragma unroll
+        for (int i = S - 1; i >= 0; --i) bstep(i);
+      } else {
+#pragma unroll
+        for (int i = S - 1; i >= 0; --i)
+          if (i < n) bstep(i);
+      }
+      // grad_x0 = A^T G at the first step, from the chunk that holds it
+      if (t0 == 0 && gx0 && live) {
+#pragma unroll
+        for (int q = 0; q < NS; ++q) {
+          double t = 0.0;
+#pragma unroll
+          for (int c = 0; c < NS; ++c) t = fma(at[q][c], s[c], t);
+          gx0[lane * NS + q] = (float)t;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      regs_to_chunk(gb, gv, lanes, row, l0, t0 * NS, n * NS, s_lds[k], lid);
+      // x_{t-1} for the chunk's steps: x at t0 - 1 (or x0), then the chunk's own outputs but the last
+      float pv[NS];
+#pragma unroll
+      for (int q = 0; q < NS; ++q)
+        pv[q] = !live ? 0.0f : t0 > 0 ? out[lane * row + (t0 - 1) * NS + q] : (x0 ? x0[lane * NS + q] : 0.0f);
+      float xc[kTileT];
+      chunk_to_regs(xc, out, lanes, row, l0, t0 * NS, n * NS, s_lds[k], lid);
+      auto gstep = [&](int i) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < NS; ++p)
+#pragma unroll
+          for (int c = 0; c < NS; ++c)
+            acc[p * NS + c] = fma((double)gb[i * NS + p], (double)(i == 0 ? pv[c] : xc[(i - 1) * NS + c]),
+                                  acc[p * NS + c]);
+      };
+      if (n == S) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) gstep(i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < S; ++i)
+          if (i < n) gstep(i);
+      }
+    }
+    // the K chunks' grad_A sums, added in LDS in chunk order, one partial per super-chunk
+    double* ak = reinterpret_cast<double*>(&s_lds[k][0][0]) + lid * NN;
+#pragma unroll
+    for (int q = 0; q < NN; ++q) ak[q] = acc[q];
+    __syncthreads();
+    for (int e = threadIdx.x; e < 64 * NN; e += blockDim.x) {
+      const int el = e / NN, q = e - el * NN;
+      if (l0 + el < lanes) {
+        double t = 0.0;
+        for (int j = 0; j < K; ++j) t += reinterpret_cast<const double*>(&s_lds[j][0][0])[el * NN + q];
+        part[(sc * lanes + l0 + el) * NN + q] = t;
+      }
+    }
+    __syncthreads();  // every read of the tiles precedes the next tile's loads into them
+  }
+}
+
+// grad_A[lane] = sum over the super-chunks' partials, in super-chunk order (deterministic).
+template <int NS>
+__global__ void __launch_bounds__(256) linrec_finish(const double* __restrict__ part, float* __restrict__ gA,
+                                                     int64_t lanes, int64_t nsuper) {
+  constexpr int NN = NS * NS;
+  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // (lane, entry)
+  if (e >= lanes * NN) return;
+  double t = 0.0;
+  for (int64_t r = 0; r < nsuper; ++r) t += part[r * lanes * NN + e];
+  gA[e] = (float)t;
+}
+
+__global__ void __launch_bounds__(256) linrec_zero(float* __restrict__ p, int64_t n) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+// Plan: K (chunks per tile) starts at kLbWaves and halves down to 2 while there are fewer than
+// kApTileTarget tiles. Workspace: the tile counter, agg and inc [nsuper][lanes][n] (reset
+// before each scan), the grad_A partials [nsuper][lanes][n][n], and Mc, Ms [lanes][n][n].
+struct LrPlan {
+  int64_t groups = 0, nsuper = 0;
+  int K = 1;
+  size_t off_agg = 0, off_inc = 0, off_part = 0, off_Mc = 0, off_Ms = 0, bytes = 0;
+};
+
+LrPlan lr_plan(int64_t lanes, int64_t L, int64_t ns) {
+  LrPlan p;
+  const int64_t S = kTileT / ns;
+  p.groups = (lanes + kTile - 1) / kTile;
+  if (L > 0) {
+    p.K = kLbWaves;
+    auto tiles = [&](int K) { return p.groups * ((L + S * K - 1) / (S * K)); };
+    while (p.K > 2 && tiles(p.K) < kApTileTarget) p.K /= 2;
+    const int64_t chunks = (L + S - 1) / S;
+    if (p.K > chunks) p.K = (int)chunks;
+    p.nsuper = (L + S * p.K - 1) / (S * p.K);
+  }
+  const size_t f = 8, vecs = f * p.nsuper * lanes * ns;
+  p.off_agg = kCounterBytes;
+  p.off_inc = p.off_agg + vecs;
+  p.off_part = p.off_inc + vecs;
+  p.off_Mc = p.off_part + vecs * ns;
+  p.off_Ms = p.off_Mc + f * lanes * ns * ns;
+  p.bytes = p.off_Ms + f * lanes * ns * ns;
+  return p;
+}
+
+inline unsigned blocks_for(int64_t threads) { return (unsigned)((threads + 255) / 256); }
+
+template <int NS>
+int fwd_impl(int64_t lanes, int64_t L, const float* A, const float* v, const float* x0, float* x, char* ws,
+             hipStream_t s) {
+  static int occ[kLbWaves + 1];
+  const LrPlan p = lr_plan(lanes, L, NS);
+  double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
+  double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
+  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes)), dim3(256), 0, s, A, Mc, Ms, lanes, p.K, 0);
+  lookback_reset_launch(ws, 2 * p.nsuper * lanes * NS, s);
+  const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(linrec_fwd_lb<NS>, 64 * p.K, occ);
+  hipLaunchKernelGGL((linrec_fwd_lb<NS>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, A, v, x0,
+                     x, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
+                     reinterpret_cast<double*>(ws + p.off_inc), reinterpret_cast<unsigned*>(ws), lanes, L, p.groups,
+                     p.K, p.nsuper);
+  return tsf_launch_status();
+}
+
+template <int NS>
+int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const float* out, const float* x0, float* gA,
+             float* gv, float* gx0, char* ws, hipStream_t s) {
+  static int occ[kLbWaves + 1];
+  if (L == 0) {  // no steps: grad_A = 0, grad_x0 = A^T G_1 with G empty = 0
+    hipLaunchKernelGGL(linrec_zero, dim3(blocks_for(lanes * NS * NS)), dim3(256), 0, s, gA, lanes * NS * NS);
+    if (gx0) hipLaunchKernelGGL(linrec_zero, dim3(blocks_for(lanes * NS)), dim3(256), 0, s, gx0, lanes * NS);
+    return tsf_launch_status();
+  }
+  const LrPlan p = lr_plan(lanes, L, NS);
+  double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
+  double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
+  double* part = reinterpret_cast<double*>(ws + p.off_part);
+  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes)), dim3(256), 0, s, A, Mc, Ms, lanes, p.K, 1);
+  lookback_reset_launch(ws, 2 * p.nsuper * lanes * NS, s);
+  const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(linrec_bwd_lb<NS>, 64 * p.K, occ);
+  hipLaunchKernelGGL((linrec_bwd_lb<NS>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, A, g, out,
+                     x0, gv, gx0, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
+                     reinterpret_cast<double*>(ws + p.off_inc), part, reinterpret_cast<unsigned*>(ws), lanes, L,
+                     p.groups, p.K, p.nsuper);
+  hipLaunchKernelGGL((linrec_finish<NS>), dim3(blocks_for(lanes * NS * NS)), dim3(256), 0, s, (const double*)part, gA,
+                     lanes, p.nsuper);
+  return tsf_launch_status();
+}
+
+#define TSF_NS_CASES(X) X(1) X(2) X(3) X(4)
+
+}  // namespace
+
+extern "C" {
+
+int64_t tsfast_hip_linrec_workspace_bytes(int64_t lanes, int64_t L, int64_t n) {
+  if (lanes < 0 || L < 0 || n < 1 || n > kMaxNS) return -1;
+  return (int64_t)lr_plan(lanes, L, n).bytes;
+}
+
+int tsfast_hip_linrec_fwd(int64_t lanes, int64_t L, int64_t n, const float* A, const float* v, const float* x0,
+                          float* x, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (lanes < 0 || L < 0) return TSF_ERR_ARG;
+  if (n < 1 || n > kMaxNS) return TSF_ERR_UNSUPPORTED;
+  if (lanes == 0 || L == 0) return TSF_OK;
+  if (!A || !v || !x) return TSF_ERR_ARG;
+  if (!workspace || workspace_bytes < tsfast_hip_linrec_workspace_bytes(lanes, L, n)) return TSF_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  switch (n) {
+#define X(K) \
+  case K:    \
+    return fwd_impl<K>(lanes, L, A, v, x0, x, ws, s);
+    TSF_NS_CASES(X)
+#undef X
+  }
+  return TSF_ERR_UNSUPPORTED;
+}
+
+int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, const float* A, const float* out,
+                          const float* x0, float* gA, float* gv, float* gx0, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
+  if (lanes < 0 || L < 0) return TSF_ERR_ARG;
+  if (n < 1 || n > kMaxNS) return TSF_ERR_UNSUPPORTED;
+  if (lanes == 0) return TSF_OK;
+  if (!A || !gA || (L > 0 && (!g || !out || !gv))) return TSF_ERR_ARG;
+  if (x0 && !gx0) return TSF_ERR_ARG;
+  if (!workspace || workspace_bytes < tsfast_hip_linrec_workspace_bytes(lanes, L, n)) return TSF_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  switch (n) {
+#define X(K) \
+  case K:    \
+    return bwd_impl<K>(lanes, L, g, A, out, x0, gA, gv, gx0, ws, s);
+    TSF_NS_CASES(X)
+#undef X
+  }
+  return TSF_ERR_UNSUPPORTED;
+}
+
+}  // extern "C"

@@ -1,7 +1,8 @@
-"""dynoNet all-pole section with its fused-kernel dispatch, and the companion-matrix scan.
+"""dynoNet all-pole section with its fused-kernel dispatch, and the constant-matrix scan.
 
 Mirrors ``tsfast/models/architectures/dynonet/core.py``: ``linear_recurrence`` (the log-doubling
-scan ``x_t = A x_{t-1} + v_t`` with its analytic matrix adjoint, ``:23-127``) and the all-pole
+scan ``x_t = A x_{t-1} + v_t`` with its analytic matrix adjoint, ``:23-127``; on GPU the
+``"hip"`` family's single-pass scan serves it for state sizes n <= 4) and the all-pole
 branch of ``LinearDynamicalOperator.forward`` (``:221-248``): the fused backend when one serves
 the inputs (``_fused_allpole``, ``:91-100``; here the ``"hip"`` family for ``"cuda"`` tensors),
 else ``linear_recurrence`` over the companion matrices.
@@ -15,10 +16,11 @@ import torch
 import torch.nn.functional as F
 
 from ..dispatch import resolve
-from . import allpole_hip, gblock_hip
+from . import allpole_hip, gblock_hip, linrec_hip
 
 _ALLPOLE_BACKENDS = {"hip": allpole_hip}
 _GBLOCK_BACKENDS = {"hip": gblock_hip}
+_LINREC_BACKENDS = {"hip": linrec_hip}
 
 
 def _doubling_matrix_scan(A: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
@@ -83,11 +85,19 @@ _linear_recurrence_op.register_autograd(_linrec_backward, setup_context=_linrec_
 
 
 def linear_recurrence(A: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None = None) -> torch.Tensor:
-    """``x_t = A x_{t-1} + v_t`` with constant ``A [..., n, n]`` by log-doubling (``core.py:103-127``)."""
+    """``x_t = A x_{t-1} + v_t`` with constant ``A [..., n, n]`` (``core.py:103-127``).
+
+    A, v and x0 are broadcast to common leading dims; a backend that serves the inputs (the
+    ``"hip"`` family for ``"cuda"`` tensors) runs them, else the log-doubling scan op.
+    """
     bshape = torch.broadcast_shapes(A.shape[:-2], v.shape[:-2], () if x0 is None else x0.shape[:-1])
     A_b = A.broadcast_to(bshape + A.shape[-2:])
     v_b = v.broadcast_to(bshape + v.shape[-2:])
     x0_b = None if x0 is None else x0.broadcast_to(bshape + x0.shape[-1:])
+    order = ("hip",) if v_b.device.type == "cuda" else ()
+    mod = resolve("dynonet.linear_recurrence", _LINREC_BACKENDS, order, (A_b, v_b, x0_b))
+    if mod is not None:
+        return mod.run(A_b, v_b, x0_b)
     return _linear_recurrence_op(A_b, v_b, x0_b)
 
 
