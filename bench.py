@@ -23,6 +23,7 @@ companion-matrix doubling scan (tsfast_amd.dynonet.linear_recurrence on CPU, the
 path of dynonet/core.py:23-88) for config 4.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 3] [--io bf16|fp32] [--no-cpu]
+       (or one of --selective, --conv, --gblock, --linrec for the other rows' workloads)
 """
 
 from __future__ import annotations
@@ -616,6 +617,82 @@ def run_gblock(args, line):
     return ms, fwd_b + bwd_b, kernels, cpu
 
 
+def run_linrec(args, line):
+    """The constant-matrix linear_recurrence (dynonet/core.py:103-127) on config 4's route: the
+    companion matrices of the config-4 denominators (n = 3) driven by (w_t, 0, 0), the way the
+    reference runs dynoNet's all-pole section without a fused kernel. The reference's own
+    algorithm on the same GPU (the log-doubling scan op and its adjoint) is timed in the same run."""
+    import torch
+    import torch.nn.functional as F
+
+    from tsfast_amd.dynonet import core as dcore
+    from tsfast_amd.dynonet import linrec_hip
+
+    a, w, gout = allpole_inputs("cuda")
+    lanes, L = w.shape
+    n = a.shape[-1]
+    A = dcore.companion(a).contiguous()
+    v = F.pad(w.unsqueeze(-1), (0, n - 1)).contiguous()
+    g = F.pad(gout.unsqueeze(-1), (0, n - 1)).contiguous()
+    del w, gout
+
+    def step(ev):
+        mark(ev)
+        x = linrec_hip._linrec_op(A, v, None)
+        mark(ev)
+        linrec_hip._linrec_bwd_op(g, A, x, None)
+        mark(ev)
+
+    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
+
+    def doubling(ev):
+        mark(ev)
+        x = dcore._linear_recurrence_op(A, v, None)
+        mark(ev)
+        dcore._linear_recurrence_bwd_op(g, A, x, None)
+        mark(ev)
+
+    dms, (dfwd, dbwd) = time_steps(doubling, 3, 1)
+    nbytes = v.numel() * 4
+    fwd_b, bwd_b = 2 * nbytes, 3 * nbytes  # read v, write x | read g and x, write grad_v
+    line.update(
+        metric="fwd+bwd ms + achieved HBM GB/s, constant-matrix linear_recurrence (BASELINE config 4 route)",
+        config={"workload": f"linear_recurrence fwd+bwd: {lanes} lanes x L {L}, n {n} companion matrices of the "
+                            "config-4 denominators, input (w_t, 0, 0) (BASELINE config 4 via the reference's "
+                            "companion-matrix route)", "lanes": lanes, "L": L, "n": n},
+        fwd_ms=round(fwd_ms, 4),
+        bwd_ms=round(bwd_ms, 4),
+        doubling_scan_ms={"fwd": round(dfwd, 4), "bwd": round(dbwd, 4), "total": round(dms, 4),
+                          "path": "tsfast_hip::linear_recurrence (the reference's log-doubling scan op) on this GPU"},
+    )
+    line["dtype"] = "f64"  # fp32 I/O, fp64 recurrence inside
+    kernels = {"fwd": ("linrec_fwd_lb look-back scan + transfer + reset", fwd_ms, fwd_b),
+               "bwd": ("linrec_bwd_lb look-back scan + transfer + reset + finish", bwd_ms, bwd_b)}
+    cpu = None
+    if not args.no_cpu:
+        def cpu_leg():
+            threads = os.cpu_count() or 1
+            torch.set_num_threads(threads)
+            rows = 64
+            A_c, v_c, g_c = A[:rows].cpu(), v[:rows].cpu(), g[:rows].cpu()
+
+            def fb():
+                vv = v_c.clone().requires_grad_()
+                x = dcore._linear_recurrence_op(A_c, vv, None)
+                x.backward(g_c)
+
+            med, nrun = cpu_time(fb)
+            sb = rows * L * n * 4 * 5
+            return {
+                "value": round(sb / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": (f"{rows} of {lanes} lanes, L={L}, n={n}: the log-doubling scan and its adjoint on CPU "
+                           f"(the reference CPU path, dynonet/core.py:23-73), fwd+bwd median of {nrun} runs "
+                           f"= {med * 1e3:.1f} ms"),
+            }
+        cpu = cpu_leg
+    return ms, fwd_b + bwd_b, kernels, cpu
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -629,6 +706,8 @@ def main():
                     help="measure the fused Mamba conv+SiLU at config 3's shape instead of a BASELINE config")
     ap.add_argument("--gblock", action="store_true",
                     help="measure the fused dynoNet G-block (FIR + all-pole + input sum) at config 4's channels")
+    ap.add_argument("--linrec", action="store_true",
+                    help="measure the constant-matrix linear_recurrence on config 4's companion-matrix route")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument(
         "--copy-calibration",
@@ -675,6 +754,7 @@ def main():
         "data": "synthetic",
     }
     runner = (run_conv if args.conv else run_selective if args.selective else run_gblock if args.gblock
+              else run_linrec if args.linrec
               else {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config])
     ms, total_bytes, kernels, cpu = runner(args, line)
     gbs = total_bytes / (ms * 1e-3) / 1e9
@@ -686,7 +766,7 @@ def main():
     name, dom_ms, dom_b = kernels[phase]
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
     key = ("selective", "f32") if args.selective else (args.config, args.io if args.config == 3 else "f32")
-    measured = None if (args.conv or args.gblock) else MEASURED_TRAFFIC.get(key, {}).get(phase)
+    measured = None if (args.conv or args.gblock or args.linrec) else MEASURED_TRAFFIC.get(key, {}).get(phase)
     line["roofline"] = {
         "bound": "hbm",
         "kernel": name,
@@ -700,7 +780,7 @@ def main():
         line["roofline"]["traffic_unit"] = "bytes per call"
         line["roofline"]["traffic_source"] = measured[1]
         line["roofline"]["algorithmic_bytes"] = dom_b
-    valu = None if (args.conv or args.selective or args.gblock) else MEASURED_VALU.get(key, {}).get(phase)
+    valu = None if (args.conv or args.selective or args.gblock or args.linrec) else MEASURED_VALU.get(key, {}).get(phase)
     if valu:
         # VALU issue capacity: every SIMD issues one wave64 instruction per quad-cycle
         import torch

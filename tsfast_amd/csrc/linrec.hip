@@ -91,6 +91,40 @@ __global__ void __launch_bounds__(256) linrec_transfer(const float* __restrict__
     for (int c = 0; c < NS; ++c) Ms[lane * NS * NS + r * NS + c] = R[r][c];
 }
 
+// The lane's matrix (or its transpose) in fp64. The kernels load it once before the look-back
+// and again after it, through a pointer the compiler cannot see through, so that the n x n
+// doubles are not held in registers across the look-back (an L2 hit instead of a spill).
+template <int NS>
+TSF_DEV void load_lane_matrix(double (&m)[NS][NS], const float* A, int64_t lane, bool live, bool transpose) {
+  asm volatile("" : "+v"(A));
+  const float* a = A + lane * NS * NS;
+#pragma unroll
+  for (int r = 0; r < NS; ++r)
+#pragma unroll
+    for (int c = 0; c < NS; ++c) m[r][c] = live ? (double)a[transpose ? c * NS + r : r * NS + c] : 0.0;
+}
+
+// Transfer matrices of a tile's 64 lanes, staged in LDS by the whole workgroup when the tile
+// starts (the loads overlap the chunk loads): wave 0's folds, its look-back and the inclusive
+// map then read them from LDS instead of waiting on global memory three times in a row. Mc and
+// Ms of 64 consecutive lanes are contiguous blocks of [lanes][n][n]. States up to 3 fit next to
+// the tiles with two workgroups per CU; n = 4 reads them from global memory.
+template <int NS>
+struct MatStage {
+  static constexpr bool kLds = NS <= 3;
+  static constexpr int kDoubles = kLds ? 2 * 64 * NS * NS : 1;
+};
+template <int NS>
+TSF_DEV void stage_mats(double* s_mat, const double* __restrict__ Mc, const double* __restrict__ Ms, int64_t l0,
+                        int64_t lanes) {
+  constexpr int NN = NS * NS;
+  const int64_t valid = ((lanes - l0) < 64 ? (lanes - l0) : 64) * NN;
+  for (int e = threadIdx.x; e < 2 * 64 * NN; e += blockDim.x) {
+    const int h = e >= 64 * NN, q = e - h * 64 * NN;
+    s_mat[e] = q < valid ? (h ? Ms : Mc)[l0 * NN + q] : 0.0;
+  }
+}
+
 // One step s <- m s + x (x the NS floats of the step).
 template <int NS>
 TSF_DEV void dense_step(const double (&m)[NS][NS], double (&s)[NS], const float* x) {
@@ -110,45 +144,71 @@ TSF_DEV void dense_step(const double (&m)[NS][NS], double (&s)[NS], const float*
 // its chunk's row segments through its LDS tile into registers, summarises the chunk from a zero
 // state, and after the look-back re-runs it from its entering state, writing x in place of v.
 template <int NS>
-__global__ void __launch_bounds__(64 * kLbWaves) linrec_fwd_lb(
+__global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per_eu(4))) linrec_fwd_lb(
     const float* __restrict__ A, const float* __restrict__ v, const float* __restrict__ x0, float* __restrict__ x,
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
     unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper) {
-  constexpr int S = steps_per_chunk<NS>();
+  constexpr int S = steps_per_chunk<NS>(), NN = NS * NS;
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
   __shared__ int s_pend[64];
   __shared__ int s_any;
   __shared__ unsigned s_tile[2];
+  __shared__ double s_mat[MatStage<NS>::kDoubles];
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int64_t tiles = groups * nsuper, SL = (int64_t)K * S, row = L * NS;
+  // This wave's chunk of a tile: first lane, first step and length.
+  auto chunk_of = [&](int64_t tile, int64_t& sc, int64_t& l0, int64_t& t0) __attribute__((always_inline)) {
+    sc = tile / groups;
+    l0 = (tile - sc * groups) * kTile;
+    t0 = sc * SL + (int64_t)k * S;
+    return (L - t0) >= S ? S : (L - t0) > 0 ? (int)(L - t0) : 0;
+  };
+  // For small states the next tile's chunk is fetched into rg while the current tile finishes
+  // (after its look-back), so its load latency overlaps the re-run and the stores; larger states
+  // have no registers to spare and load each chunk when its tile starts.
+  constexpr bool kPrefetch = NS <= 2;
+  TileRegs rg;
   if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
   __syncthreads();
+  if (kPrefetch && (int64_t)s_tile[0] < tiles) {
+    int64_t sc0, l00, t00;
+    const int n0 = chunk_of(s_tile[0], sc0, l00, t00);
+    if (n0 > 0) tile_fetch(rg, v, lanes, row, l00, t00 * NS, n0 * NS, lid);
+  }
   for (int buf = 0;; buf ^= 1) {
     const int64_t tile = s_tile[buf];
     if (tile >= tiles) break;
     unsigned next = 0;
     if (threadIdx.x == 0) next = take_tile(counter);
-    const int64_t sc = tile / groups, l0 = (tile - sc * groups) * kTile, lane = l0 + lid;
+    int64_t sc, l0, t0;
+    const int n = chunk_of(tile, sc, l0, t0);
+    const int64_t lane = l0 + lid;
     const bool live = lane < lanes;
-    const int64_t t0 = sc * SL + (int64_t)k * S;
-    const int n = (L - t0) >= S ? S : (L - t0) > 0 ? (int)(L - t0) : 0;
-    double am[NS][NS], s[NS];
+    double s[NS];
 #pragma unroll
-    for (int r = 0; r < NS; ++r) {
-#pragma unroll
-      for (int c = 0; c < NS; ++c) am[r][c] = live ? (double)A[lane * NS * NS + r * NS + c] : 0.0;
-      s[r] = 0.0;
-    }
+    for (int r = 0; r < NS; ++r) s[r] = 0.0;
     float xb[kTileT];
-    if (n > 0) chunk_to_regs(xb, v, lanes, row, l0, t0 * NS, n * NS, s_lds[k], lid);
-    if (n == S) {
+    if (n > 0 && !kPrefetch) tile_fetch(rg, v, lanes, row, l0, t0 * NS, n * NS, lid);
+    if (n > 0) {
+      tile_put(rg, s_lds[k], lid);
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int i = 0; i < S; ++i) dense_step<NS>(am, s, &xb[i * NS]);
-    } else {
+      for (int i = 0; i < kTileT; ++i) xb[i] = s_lds[k][lid][i];
+      __builtin_amdgcn_wave_barrier();
+    }
+    if constexpr (MatStage<NS>::kLds) stage_mats<NS>(s_mat, Mc, Ms, l0, lanes);
+    {
+      double am[NS][NS];
+      load_lane_matrix<NS>(am, A, lane, live, false);
+      if (n == S) {
 #pragma unroll
-      for (int i = 0; i < S; ++i)
-        if (i < n) dense_step<NS>(am, s, &xb[i * NS]);
+        for (int i = 0; i < S; ++i) dense_step<NS>(am, s, &xb[i * NS]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < S; ++i)
+          if (i < n) dense_step<NS>(am, s, &xb[i * NS]);
+      }
     }
     double* vk = vec_area<NS>(s_lds, k) + lid * NS;
 #pragma unroll
@@ -162,7 +222,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_fwd_lb(
     for (int q = 0; q < NS; ++q) sup[q] = 0.0;
     if (k == 0 && live) {
       double mc[NS][NS];
-      load_mat<NS>(mc, Mc + lane * NS * NS);
+      load_mat<NS>(mc, MatStage<NS>::kLds ? &s_mat[lid * NN] : Mc + lane * NN);
       for (int j = 0; j < K; ++j) {
         double ej[NS];
         const double* vj = vec_area<NS>(s_lds, j) + lid * NS;
@@ -176,17 +236,17 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_fwd_lb(
 #pragma unroll
     for (int q = 0; q < NS; ++q) St[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[lane * NS + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
-      ap_look_back<NS>(St, agg, inc, Ms + lane * NS * NS, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
+      ap_look_back<NS>(St, agg, inc, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
                        k, lid, s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
       if (sc + 1 < nsuper) {
         double ms[NS][NS], o[NS];
-        load_mat<NS>(ms, Ms + lane * NS * NS);
+        load_mat<NS>(ms, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN);
         matvec_add<NS>(o, ms, St, sup);
         put_vec<NS>(inc + (sc * lanes + lane) * NS, o);
       }
       double mc[NS][NS];
-      load_mat<NS>(mc, Mc + lane * NS * NS);
+      load_mat<NS>(mc, MatStage<NS>::kLds ? &s_mat[lid * NN] : Mc + lane * NN);
       for (int j = 0; j < K; ++j) {  // entering state of every chunk, in place of its summary
         double ej[NS];
         double* vj = vec_area<NS>(s_lds, j) + lid * NS;
@@ -198,10 +258,17 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_fwd_lb(
         matvec_add<NS>(St, mc, St, ej);
       }
     }
+    if (kPrefetch && (int64_t)s_tile[buf ^ 1] < tiles) {  // prefetch the next tile's chunk
+      int64_t sc1, l01, t01;
+      const int n1 = chunk_of(s_tile[buf ^ 1], sc1, l01, t01);
+      if (n1 > 0) tile_fetch(rg, v, lanes, row, l01, t01 * NS, n1 * NS, lid);
+    }
     __syncthreads();
     if (n > 0) {
 #pragma unroll
       for (int q = 0; q < NS; ++q) s[q] = vk[q];
+      double am[NS][NS];
+      load_lane_matrix<NS>(am, A, lane, live, false);
       auto fstep = [&](int i) __attribute__((always_inline)) {
         dense_step<NS>(am, s, &xb[i * NS]);
 #pragma unroll
@@ -227,7 +294,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_fwd_lb(
 // output (loaded after the look-back, so it does not stay in registers across it) or x0. The
 // tile's K per-chunk sums are added in LDS and written per super-chunk.
 template <int NS>
-__global__ void __launch_bounds__(64 * kLbWaves) linrec_bwd_lb(
+__global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per_eu(4))) linrec_bwd_lb(
     const float* __restrict__ A, const float* __restrict__ g, const float* __restrict__ out,
     const float* __restrict__ x0, float* __restrict__ gv, float* __restrict__ gx0, const double* __restrict__ Mc,
     const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc, double* __restrict__ part,
@@ -239,6 +306,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_bwd_lb(
   __shared__ int s_pend[64];
   __shared__ int s_any;
   __shared__ unsigned s_tile[2];
+  __shared__ double s_mat[MatStage<NS>::kDoubles];
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int64_t tiles = groups * nsuper, SL = (int64_t)K * S, row = L * NS;
   if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
@@ -252,22 +320,23 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_bwd_lb(
     const bool live = lane < lanes;
     const int64_t t0 = sc * SL + (int64_t)k * S;
     const int n = (L - t0) >= S ? S : (L - t0) > 0 ? (int)(L - t0) : 0;
-    double at[NS][NS], s[NS];  // at = A^T
+    double s[NS];
 #pragma unroll
-    for (int i = 0; i < NS; ++i) {
-#pragma unroll
-      for (int c = 0; c < NS; ++c) at[i][c] = live ? (double)A[lane * NN + c * NS + i] : 0.0;
-      s[i] = 0.0;
-    }
+    for (int i = 0; i < NS; ++i) s[i] = 0.0;
     float gb[kTileT];
+    if constexpr (MatStage<NS>::kLds) stage_mats<NS>(s_mat, Mc, Ms, l0, lanes);
     if (n > 0) chunk_to_regs(gb, g, lanes, row, l0, t0 * NS, n * NS, s_lds[k], lid);
-    if (n == S) {
+    {
+      double at[NS][NS];  // A^T
+      load_lane_matrix<NS>(at, A, lane, live, true);
+      if (n == S) {
 #pragma unroll
-      for (int i = S - 1; i >= 0; --i) dense_step<NS>(at, s, &gb[i * NS]);
-    } else {
+        for (int i = S - 1; i >= 0; --i) dense_step<NS>(at, s, &gb[i * NS]);
+      } else {
 #pragma unroll
-      for (int i = S - 1; i >= 0; --i)
-        if (i < n) dense_step<NS>(at, s, &gb[i * NS]);
+        for (int i = S - 1; i >= 0; --i)
+          if (i < n) dense_step<NS>(at, s, &gb[i * NS]);
+      }
     }
     double* vk = vec_area<NS>(s_lds, k) + lid * NS;
 #pragma unroll
@@ -281,7 +350,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_bwd_lb(
     for (int q = 0; q < NS; ++q) sup[q] = 0.0;
     if (k == 0 && live) {
       double mc[NS][NS];
-      load_mat<NS>(mc, Mc + lane * NN);
+      load_mat<NS>(mc, MatStage<NS>::kLds ? &s_mat[lid * NN] : Mc + lane * NN);
       for (int j = K - 1; j >= 0; --j) {
         double fj[NS];
         const double* vj = vec_area<NS>(s_lds, j) + lid * NS;
@@ -295,17 +364,17 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_bwd_lb(
 #pragma unroll
     for (int q = 0; q < NS; ++q) R[q] = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
-      ap_look_back<NS>(R, agg, inc, Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid,
+      ap_look_back<NS>(R, agg, inc, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid,
                        s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
       if (sc > 0) {
         double ms[NS][NS], o[NS];
-        load_mat<NS>(ms, Ms + lane * NN);
+        load_mat<NS>(ms, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN);
         matvec_add<NS>(o, ms, R, sup);
         put_vec<NS>(inc + (sc * lanes + lane) * NS, o);
       }
       double mc[NS][NS];
-      load_mat<NS>(mc, Mc + lane * NN);
+      load_mat<NS>(mc, MatStage<NS>::kLds ? &s_mat[lid * NN] : Mc + lane * NN);
       for (int j = K - 1; j >= 0; --j) {  // state entering every chunk from the right
         double fj[NS];
         double* vj = vec_area<NS>(s_lds, j) + lid * NS;
@@ -324,6 +393,8 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_bwd_lb(
     if (n > 0) {
 #pragma unroll
       for (int q = 0; q < NS; ++q) s[q] = vk[q];
+      double at[NS][NS];
+      load_lane_matrix<NS>(at, A, lane, live, true);
       auto bstep = [&](int i) __attribute__((always_inline)) {
         dense_step<NS>(at, s, &gb[i * NS]);
 #pragma unroll
@@ -390,16 +461,26 @@ __global__ void __launch_bounds__(64 * kLbWaves) linrec_bwd_lb(
   }
 }
 
-// grad_A[lane] = sum over the super-chunks' partials, in super-chunk order (deterministic).
-template <int NS>
-__global__ void __launch_bounds__(256) linrec_finish(const double* __restrict__ part, float* __restrict__ gA,
-                                                     int64_t lanes, int64_t nsuper) {
-  constexpr int NN = NS * NS;
-  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // (lane, entry)
-  if (e >= lanes * NN) return;
-  double t = 0.0;
-  for (int64_t r = 0; r < nsuper; ++r) t += part[r * lanes * NN + e];
-  gA[e] = (float)t;
+// grad_A = the sum of the super-chunks' partials [nsuper][lanes * n * n]. A workgroup of 16 waves
+// owns 64 consecutive entries: wave k sums the k-th of 16 contiguous runs of super-chunks (64
+// consecutive doubles per read), and the 16 run sums are added in order (deterministic).
+__global__ void __launch_bounds__(1024) linrec_finish(const double* __restrict__ part, float* __restrict__ gA,
+                                                      int64_t entries, int64_t nsuper) {
+  __shared__ double s_p[16][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t e = blockIdx.x * 64 + lid;
+  const int64_t seg = (nsuper + 15) / 16;
+  const int64_t r0 = k * seg, r1 = (r0 + seg < nsuper) ? r0 + seg : nsuper;
+  double acc = 0.0;
+  if (e < entries)
+    for (int64_t r = r0; r < r1; ++r) acc += part[r * entries + e];
+  s_p[k][lid] = acc;
+  __syncthreads();
+  if (k == 0 && e < entries) {
+    double t = s_p[0][lid];
+    for (int j = 1; j < 16; ++j) t += s_p[j][lid];
+    gA[e] = (float)t;
+  }
 }
 
 __global__ void __launch_bounds__(256) linrec_zero(float* __restrict__ p, int64_t n) {
@@ -477,8 +558,8 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const flo
                      x0, gv, gx0, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
                      reinterpret_cast<double*>(ws + p.off_inc), part, reinterpret_cast<unsigned*>(ws), lanes, L,
                      p.groups, p.K, p.nsuper);
-  hipLaunchKernelGGL((linrec_finish<NS>), dim3(blocks_for(lanes * NS * NS)), dim3(256), 0, s, (const double*)part, gA,
-                     lanes, p.nsuper);
+  hipLaunchKernelGGL(linrec_finish, dim3((unsigned)((lanes * NS * NS + 63) / 64)), dim3(1024), 0, s,
+                     (const double*)part, gA, lanes * NS * NS, p.nsuper);
   return tsf_launch_status();
 }
 
