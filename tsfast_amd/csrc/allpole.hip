@@ -336,11 +336,13 @@ __global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
     const float* __restrict__ a, const float* __restrict__ w, const float* __restrict__ y0, float* __restrict__ y,
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
     unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper) {
+  constexpr int NN = NA * NA;
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
   __shared__ int s_pend[64];
   __shared__ int s_any;
   __shared__ unsigned s_tile[2];
+  __shared__ double s_mat[MatStage<NA>::kDoubles];
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
   if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
@@ -362,6 +364,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
     }
     float xb[kTileT];
     if (n > 0) chunk_to_regs(xb, w, lanes, L, l0, t0, n, s_lds[k], lid);
+    if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, l0, lanes);
     if (n == kTileT) {
 #pragma unroll
       for (int i = 0; i < kTileT; ++i) step<NA>(av, s, (double)xb[i]);
@@ -382,7 +385,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
     for (int q = 0; q < NA; ++q) sup[q] = 0.0;
     if (k == 0 && live) {
       double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
+      load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NN] : Mc + lane * NN);
       for (int j = 0; j < K; ++j) {
         double ej[NA];
         const double* vj = vec_area<NA>(s_lds, j) + lid * NA;
@@ -396,17 +399,17 @@ __global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
 #pragma unroll
     for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && y0 && live && k == 0) ? (double)y0[lane * NA + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
-      ap_look_back<NA>(S, agg, inc, Ms + lane * NA * NA, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
+      ap_look_back<NA>(S, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
                        k, lid, s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
       if (sc + 1 < nsuper) {
         double ms[NA][NA], o[NA];
-        load_mat<NA>(ms, Ms + lane * NA * NA);
+        load_mat<NA>(ms, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN);
         matvec_add<NA>(o, ms, S, sup);
         put_vec<NA>(inc + (sc * lanes + lane) * NA, o);
       }
       double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
+      load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NN] : Mc + lane * NN);
       for (int j = 0; j < K; ++j) {  // entering state of every chunk, in place of its summary
         double ej[NA];
         double* vj = vec_area<NA>(s_lds, j) + lid * NA;
@@ -447,11 +450,13 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
     unsigned* __restrict__ counter, float* __restrict__ gw, double* __restrict__ part, int64_t lanes, int64_t L,
     int64_t groups, int K, int64_t nsuper) {
+  constexpr int NN = NA * NA;
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
   __shared__ int s_pend[64];
   __shared__ int s_any;
   __shared__ unsigned s_tile[2];
+  __shared__ double s_mat[MatStage<NA>::kDoubles];
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
   if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
@@ -473,6 +478,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     }
     float gb[kTileT];
     if (n > 0) chunk_to_regs(gb, g, lanes, L, l0, t0, n, s_lds[k], lid);
+    if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, l0, lanes);
     if (n == kTileT) {
 #pragma unroll
       for (int i = kTileT - 1; i >= 0; --i) step<NA>(av, s, (double)gb[i]);
@@ -493,7 +499,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     for (int q = 0; q < NA; ++q) sup[q] = 0.0;
     if (k == 0 && live) {
       double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
+      load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NN] : Mc + lane * NN);
       for (int j = K - 1; j >= 0; --j) {
         double fj[NA];
         const double* vj = vec_area<NA>(s_lds, j) + lid * NA;
@@ -507,17 +513,17 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
 #pragma unroll
     for (int q = 0; q < NA; ++q) R[q] = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
-      ap_look_back<NA>(R, agg, inc, Ms + lane * NA * NA, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K,
+      ap_look_back<NA>(R, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K,
                        k, lid, s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
       if (sc > 0) {
         double ms[NA][NA], o[NA];
-        load_mat<NA>(ms, Ms + lane * NA * NA);
+        load_mat<NA>(ms, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN);
         matvec_add<NA>(o, ms, R, sup);
         put_vec<NA>(inc + (sc * lanes + lane) * NA, o);
       }
       double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
+      load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NN] : Mc + lane * NN);
       for (int j = K - 1; j >= 0; --j) {  // state entering every chunk from the right
         double fj[NA];
         double* vj = vec_area<NA>(s_lds, j) + lid * NA;

@@ -104,27 +104,6 @@ TSF_DEV void load_lane_matrix(double (&m)[NS][NS], const float* A, int64_t lane,
     for (int c = 0; c < NS; ++c) m[r][c] = live ? (double)a[transpose ? c * NS + r : r * NS + c] : 0.0;
 }
 
-// Transfer matrices of a tile's 64 lanes, staged in LDS by the whole workgroup when the tile
-// starts (the loads overlap the chunk loads): wave 0's folds, its look-back and the inclusive
-// map then read them from LDS instead of waiting on global memory three times in a row. Mc and
-// Ms of 64 consecutive lanes are contiguous blocks of [lanes][n][n]. States up to 3 fit next to
-// the tiles with two workgroups per CU; n = 4 reads them from global memory.
-template <int NS>
-struct MatStage {
-  static constexpr bool kLds = NS <= 3;
-  static constexpr int kDoubles = kLds ? 2 * 64 * NS * NS : 1;
-};
-template <int NS>
-TSF_DEV void stage_mats(double* s_mat, const double* __restrict__ Mc, const double* __restrict__ Ms, int64_t l0,
-                        int64_t lanes) {
-  constexpr int NN = NS * NS;
-  const int64_t valid = ((lanes - l0) < 64 ? (lanes - l0) : 64) * NN;
-  for (int e = threadIdx.x; e < 2 * 64 * NN; e += blockDim.x) {
-    const int h = e >= 64 * NN, q = e - h * 64 * NN;
-    s_mat[e] = q < valid ? (h ? Ms : Mc)[l0 * NN + q] : 0.0;
-  }
-}
-
 // One step s <- m s + x (x the NS floats of the step).
 template <int NS>
 TSF_DEV void dense_step(const double (&m)[NS][NS], double (&s)[NS], const float* x) {
