@@ -62,6 +62,14 @@ MEASURED_TRAFFIC = {
         "fwd": (1_631_000_000, "profiles/selective_scan_traffic.md"),
         "bwd": (2_727_900_000, "profiles/selective_scan_traffic.md"),
     },
+    (4, "f32"): {
+        "fwd": (672_000_000, "profiles/allpole_scan_config4_traffic.md"),
+        "bwd": (961_100_000, "profiles/allpole_scan_config4_traffic.md"),
+    },
+    ("linrec", "f32"): {
+        "fwd": (2_122_100_000, "profiles/linrec_config4route_traffic.md"),
+        "bwd": (3_258_500_000, "profiles/linrec_config4route_traffic.md"),
+    },
 }
 
 # VALU issue per call, for the VALU-bound fused Mamba scan: rocprofv3 SQ_ACTIVE_INST_VALU (quad-cycles
@@ -765,8 +773,9 @@ def main():
     phase = max(kernels, key=lambda k: kernels[k][1])
     name, dom_ms, dom_b = kernels[phase]
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
-    key = ("selective", "f32") if args.selective else (args.config, args.io if args.config == 3 else "f32")
-    measured = None if (args.conv or args.gblock or args.linrec) else MEASURED_TRAFFIC.get(key, {}).get(phase)
+    key = (("selective", "f32") if args.selective else ("linrec", "f32") if args.linrec
+           else (args.config, args.io if args.config == 3 else "f32"))
+    measured = None if (args.conv or args.gblock) else MEASURED_TRAFFIC.get(key, {}).get(phase)
     line["roofline"] = {
         "bound": "hbm",
         "kernel": name,
