@@ -8,14 +8,20 @@
 // Reference semantics: tsfast/models/architectures/mamba/conv_triton.py:59-263 (kernels and
 // ops, tail gradient at :241-250) and the eager path mamba/core.py:38-58.
 //
-// No recurrence: each thread owns VEC consecutive channels and a run of kRun consecutive steps,
-// keeps the K-1 step causal window in registers, and streams x once (plus a K-1 step halo per
-// run); consecutive threads own consecutive channel groups, so every per-step access of a wave
-// is one coalesced row segment. Memory-bound: fwd reads x and writes out, bwd reads x and gy and
-// writes gx. The backward recomputes p (cheaper than storing it), forms gx from the K shifted
-// pre-activation gradients, and reduces grad-w / grad-bias in registers over a thread's runs,
-// in LDS over a workgroup, and over (batch, run block) in a second kernel, in a fixed order
-// (deterministic).
+// No recurrence, so the layout is chosen for memory-level parallelism, per I/O type:
+//  * fp32: a thread owns 4 channels (one 16-byte vector per row) and a run of steps, and keeps
+//    the whole run plus its K-1 step halo in registers, loaded before the arithmetic.
+//  * bf16: a 16-byte vector holds 8 channels, too many for register tiles, so a workgroup owns
+//    256 consecutive channels (one per thread) of one batch row over a segment of kSeg steps.
+//    Row tiles are moved into LDS with 16-byte vector loads (element loads for layouts without
+//    aligned rows), and the next tile's loads are in flight while the current tile is computed.
+//    Each thread walks its channel's column with K-step rolling windows in registers (tile rows
+//    are a multiple of K, so ring slots are compile-time), so its registers hold only the windows,
+//    taps and partial sums and many waves stay resident.
+// fwd reads x and writes out; bwd reads x and gy and writes gx, recomputing p (cheaper than
+// storing it), forming gx from the K-step window of pre-activation gradients, and accumulating
+// grad-w / grad-bias per 128 steps, summed over (batch, segment) by a second kernel in a fixed
+// order (deterministic).
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -23,9 +29,17 @@ using namespace tsf;
 
 namespace {
 
-constexpr int kRun = 16;   // forward steps per thread
-constexpr int kCgWg = 64;  // channel groups per workgroup (one wave wide)
-constexpr int kRunsWg = 4; // runs per workgroup (one per wave)
+#ifndef TSF_CONV_SEG
+#define TSF_CONV_SEG 128
+#endif
+#ifndef TSF_CONV_FWD_TM
+#define TSF_CONV_FWD_TM 2
+#endif
+#ifndef TSF_CONV_BWD_TM
+#define TSF_CONV_BWD_TM 1
+#endif
+constexpr int kCh = 256;           // channels per workgroup, one per thread
+constexpr int kSeg = TSF_CONV_SEG;  // steps per workgroup segment (one grad-w / grad-bias partial each)
 
 template <typename TIO>
 TSF_DEV TIO zero_io();
@@ -39,6 +53,256 @@ TSF_DEV bf16 zero_io<bf16>() {
   r.bits = 0;
   return r;
 }
+
+// Rows per LDS tile: a multiple of K near 16, so that a step's ring slot (stream row mod K) is
+// the same compile-time value in every tile.
+template <int K>
+struct Tile {
+  static constexpr int TR = K * ((16 + K - 1) / K);
+};
+
+// One 16-byte piece of a tile row (VE elements).
+template <typename TIO>
+struct alignas(16) Piece {
+  static constexpr int VE = 16 / sizeof(TIO);
+  TIO v[VE];
+};
+
+// A tile of TR rows x kCh channels of one tensor, staged through registers: thread t handles
+// pieces e = t + q * kCh (row e / PPR, piece e % PPR). Rows outside [0, L) and channels past D
+// read as zero. VECL: rows are 16-byte aligned runs (channel stride 1, D a multiple of VE), so a
+// piece is one vector load; otherwise its elements are loaded one by one.
+template <typename TIO, int TR>
+struct TileRegs2 {
+  static constexpr int VE = Piece<TIO>::VE;
+  static constexpr int PPR = kCh / VE;  // pieces per row
+  static constexpr int NQ = (TR * PPR + kCh - 1) / kCh;
+  Piece<TIO> r[NQ];
+};
+
+// Issue the loads of stream rows [s0, s0 + TR) (sequence rows; row s at base + s * sl + c * sc for
+// channel c) into the staging registers.
+template <typename TIO, int TR, bool VECL>
+TSF_DEV void tile_issue(TileRegs2<TIO, TR>& rg, const TIO* __restrict__ base, int64_t s0, int64_t L, int64_t c0,
+                        int64_t D, int64_t sl, int64_t sc) {
+  using R = TileRegs2<TIO, TR>;
+#pragma unroll
+  for (int q = 0; q < R::NQ; ++q) {
+    const int e = threadIdx.x + q * kCh;
+    const int row = e / R::PPR, pc = e % R::PPR;
+    const int64_t srow = s0 + row, c = c0 + (int64_t)pc * R::VE;
+    const bool rok = e < TR * R::PPR && srow >= 0 && srow < L;
+    if (VECL) {
+      if (rok && c < D) {
+        rg.r[q] = ld32(reinterpret_cast<const Piece<TIO>*>(base), (uint32_t)((srow * sl + c) / R::VE));
+      } else {
+#pragma unroll
+        for (int v = 0; v < R::VE; ++v) rg.r[q].v[v] = zero_io<TIO>();
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < R::VE; ++v)
+        rg.r[q].v[v] = (rok && c + v < D) ? ld32(base, (uint32_t)(srow * sl + (c + v) * sc)) : zero_io<TIO>();
+    }
+  }
+}
+
+template <typename TIO, int TR>
+TSF_DEV void tile_commit(const TileRegs2<TIO, TR>& rg, TIO (*tile)[kCh]) {
+  using R = TileRegs2<TIO, TR>;
+#pragma unroll
+  for (int q = 0; q < R::NQ; ++q) {
+    const int e = threadIdx.x + q * kCh;
+    if (e < TR * R::PPR) *reinterpret_cast<Piece<TIO>*>(&tile[e / R::PPR][(e % R::PPR) * R::VE]) = rg.r[q];
+  }
+}
+
+// Store tile rows r (r0 <= r < r1) as sequence rows s0 + r of a contiguous [*, L, D] row source
+// (dst = its batch row), channels past D skipped; the same piece mapping as tile_issue.
+template <typename TIO, int TR, bool VECL>
+TSF_DEV void tile_store(TIO (*tile)[kCh], TIO* __restrict__ dst, int64_t s0, int r0, int r1, int64_t c0, int64_t D) {
+  using R = TileRegs2<TIO, TR>;
+#pragma unroll
+  for (int q = 0; q < R::NQ; ++q) {
+    const int e = threadIdx.x + q * kCh;
+    const int row = e / R::PPR, pc = e % R::PPR;
+    const int64_t c = c0 + (int64_t)pc * R::VE;
+    if (e < TR * R::PPR && row >= r0 && row < r1) {
+      const Piece<TIO> v = *reinterpret_cast<const Piece<TIO>*>(&tile[row][pc * R::VE]);
+      const int64_t o = (s0 + row) * D + c;
+      if (VECL) {
+        if (c < D) st32(reinterpret_cast<Piece<TIO>*>(dst), (uint32_t)(o / R::VE), v);
+      } else {
+#pragma unroll
+        for (int u = 0; u < R::VE; ++u)
+          if (c + u < D) st32(dst, (uint32_t)(o + u), v.v[u]);
+      }
+    }
+  }
+}
+
+TSF_DEV float silu_f(float p) { return p * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-p * kLog2e)); }
+
+// xbuf_s of channel d for s < 0 (the carried tail, zero without one) or s >= 0 (x).
+template <typename TIO, int K>
+TSF_DEV float xbuf_at(const TIO* __restrict__ xrow, const TIO* __restrict__ tail, int64_t b, int64_t s, int64_t d,
+                      int64_t L, int64_t D, int64_t sxl, int64_t sxd) {
+  if (s >= 0) return s < L ? to_f32(ld32(xrow, (uint32_t)(s * sxl + d * sxd))) : 0.0f;
+  return tail ? to_f32(tail[(b * D + d) * (K - 1) + (K - 1 + s)]) : 0.0f;
+}
+
+// ------------------------------------------------------------------------------------ forward
+template <typename TIO, int K, bool VECL>
+__global__ void __launch_bounds__(kCh) conv_silu_fwd_kernel(const TIO* __restrict__ x, const TIO* __restrict__ tail,
+                                                            const float* __restrict__ w,
+                                                            const float* __restrict__ bias, TIO* __restrict__ out,
+                                                            int64_t L, int64_t D, int64_t sxb, int64_t sxl,
+                                                            int64_t sxd) {
+  constexpr int TR = TSF_CONV_FWD_TM * Tile<K>::TR;  // one input tile only: more rows between barriers
+  __shared__ __align__(16) TIO s_x[TR][kCh];
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.x * kCh, d = c0 + tid, b = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.y * kSeg;
+  const bool live = d < D;
+  const int64_t nrow = (L - t0) < kSeg ? (L - t0) : kSeg;  // stream rows: the segment's steps
+  const TIO* xrow = x + b * sxb;
+  float wk[K], xr[K], bv = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    wk[k] = live ? w[d * K + k] : 0.0f;
+    xr[k] = 0.0f;
+  }
+  if (live && bias) bv = bias[d];
+  // ring slot of stream row j is j mod K; rows -(K-1) .. -1 take slots 1 .. K-1
+#pragma unroll
+  for (int k = 1; k < K; ++k)
+    if (live) xr[k] = xbuf_at<TIO, K>(xrow, tail, b, t0 - K + k, d, L, D, sxl, sxd);
+  TIO* orow = out + b * L * D;
+  TileRegs2<TIO, TR> rg;
+  tile_issue<TIO, TR, VECL>(rg, xrow, t0, L, c0, D, sxl, sxd);
+  for (int64_t jb = 0; jb < nrow; jb += TR) {
+    __syncthreads();
+    tile_commit<TIO, TR>(rg, s_x);
+    __syncthreads();
+    if (jb + TR < nrow) tile_issue<TIO, TR, VECL>(rg, xrow, t0 + jb + TR, L, c0, D, sxl, sxd);
+#pragma unroll
+    for (int i = 0; i < TR; ++i) {
+      if (jb + i >= nrow) break;  // uniform over the workgroup
+      xr[i % K] = to_f32(s_x[i][tid]);
+      float p = bv;
+#pragma unroll
+      for (int k = 0; k < K; ++k) p = fmaf(wk[k], xr[(i + 1 + k) % K], p);
+      if (live) st32(orow, (uint32_t)((t0 + jb + i) * D + d), from_f32<TIO>(silu_f(p)));
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------- backward
+// gpre_t = gy_t silu'(p_t); gx_t = sum_k w_k gpre_{t+K-1-k}; grad w_k = sum_t gpre_t
+// xbuf_{t-(K-1)+k}; grad bias = sum_t gpre_t; grad tail_j = sum_{t<=j} gpre_t w_{j-t}.
+// A segment streams rows t0 .. t0+kSeg+K-2 (the last K-1 give the gpre that its own last gx
+// rows need); gx of row j - (K-1) is formed once gpre_j is known. One partial row per (batch,
+// segment): part [B, nseg, D, K+1] (K taps, then the bias term).
+template <typename TIO, int K, bool VECL>
+__global__ void __launch_bounds__(kCh) conv_silu_bwd_kernel(
+    const TIO* __restrict__ x, const TIO* __restrict__ tail, const float* __restrict__ w,
+    const float* __restrict__ bias, const TIO* __restrict__ gy, TIO* __restrict__ gx, TIO* __restrict__ gtail,
+    float* __restrict__ part, int64_t L, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd) {
+  constexpr int TR = TSF_CONV_BWD_TM * Tile<K>::TR;
+  constexpr int KP = K + 1;
+  __shared__ __align__(16) TIO s_x[TR][kCh];
+  __shared__ __align__(16) TIO s_g[TR][kCh];
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.x * kCh, d = c0 + tid, b = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.y * kSeg;
+  const bool live = d < D;
+  const int64_t own = (L - t0) < kSeg ? (L - t0) : kSeg;  // the segment's own steps
+  const int64_t nrow = own + K - 1;                        // stream rows, with the right halo
+  const TIO* xrow = x + b * sxb;
+  const TIO* gyrow = gy + b * L * D;
+  TIO* gxrow = gx + b * L * D;
+  float wk[K], xr[K], gr[K], acc[KP], bv = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    wk[k] = live ? w[d * K + k] : 0.0f;
+    xr[k] = 0.0f;
+    gr[k] = 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < KP; ++k) acc[k] = 0.0f;
+  if (live && bias) bv = bias[d];
+#pragma unroll
+  for (int k = 1; k < K; ++k)
+    if (live) xr[k] = xbuf_at<TIO, K>(xrow, tail, b, t0 - K + k, d, L, D, sxl, sxd);
+  TileRegs2<TIO, TR> rx, rgy;
+  tile_issue<TIO, TR, VECL>(rx, xrow, t0, L, c0, D, sxl, sxd);
+  tile_issue<TIO, TR, VECL>(rgy, gyrow, t0, L, c0, D, D, 1);
+  for (int64_t jb = 0; jb < nrow; jb += TR) {
+    __syncthreads();
+    tile_commit<TIO, TR>(rx, s_x);
+    tile_commit<TIO, TR>(rgy, s_g);
+    __syncthreads();
+    if (jb + TR < nrow) {
+      tile_issue<TIO, TR, VECL>(rx, xrow, t0 + jb + TR, L, c0, D, sxl, sxd);
+      tile_issue<TIO, TR, VECL>(rgy, gyrow, t0 + jb + TR, L, c0, D, D, 1);
+    }
+#pragma unroll
+    for (int i = 0; i < TR; ++i) {
+      const int64_t j = jb + i;  // stream row; sequence row t0 + j
+      if (j >= nrow) break;      // uniform over the workgroup
+      xr[i % K] = to_f32(s_x[i][tid]);
+      float p = bv;
+#pragma unroll
+      for (int k = 0; k < K; ++k) p = fmaf(wk[k], xr[(i + 1 + k) % K], p);
+      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-p * kLog2e));
+      const float gp = to_f32(s_g[i][tid]) * (sg * fmaf(p, 1.0f - sg, 1.0f));  // zero past L (gy = 0)
+      gr[i % K] = gp;
+      if (j < own) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc[k] = fmaf(gp, xr[(i + 1 + k) % K], acc[k]);
+        acc[K] += gp;
+      }
+      {
+        // gx of sequence row t0 + j - (K-1) replaces gy in tile row i (stored below)
+        float g = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) g = fmaf(wk[k], gr[(i - k + K) % K], g);
+        s_g[i][tid] = from_f32<TIO>(g);
+      }
+      // the carried tail feeds the first K-1 outputs: once gpre_0 .. gpre_{K-2} are known
+      if (t0 == 0 && j == K - 2 && gtail && live) {
+#pragma unroll
+        for (int jj = 0; jj < K - 1; ++jj) {
+          float g = 0.0f;
+#pragma unroll
+          for (int t = 0; t <= jj; ++t) g = fmaf(gr[t], wk[jj - t], g);  // gpre_t in slot t (t < K)
+          gtail[(b * D + d) * (K - 1) + jj] = from_f32<TIO>(g);
+        }
+      }
+    }
+    // tile row i holds gx of sequence row t0 + jb + i - (K-1): store those in [t0, t0 + own)
+    __syncthreads();
+    {
+      const int64_t lo = (K - 1) - jb, hi = own + (K - 1) - jb;
+      const int r0 = lo > 0 ? (int)lo : 0, r1 = hi < TR ? (int)(hi > 0 ? hi : 0) : TR;
+      tile_store<TIO, TR, VECL>(s_g, gxrow, t0 + jb - (K - 1), r0, r1, c0, D);
+    }
+  }
+  if (live) {
+    float* pr = part + (((int64_t)b * gridDim.y + blockIdx.y) * D + d) * KP;
+#pragma unroll
+    for (int k = 0; k < KP; ++k) pr[k] = acc[k];
+  }
+}
+
+// ------------------------------------------------------------------ float I/O: register tiles
+// With fp32 rows a 16-byte vector holds 4 channels, so a thread owns 4 channels and a run of
+// steps and keeps the whole run (plus the K-1 step halo) in registers, loaded with one vector per
+// row before the arithmetic; consecutive threads own consecutive channel groups. This measures
+// faster for fp32 than staging through LDS; bf16 (8 channels per vector) uses the LDS tiles below.
+constexpr int kRun = 16;   // forward steps per thread
+constexpr int kCgWg = 64;  // channel groups per workgroup (one wave wide)
+constexpr int kRunsWg = 4; // runs per workgroup (one per wave)
 
 // VEC consecutive channels of one row: one vector access when the row is contiguous.
 template <typename TIO, int VEC>
@@ -71,7 +335,6 @@ TSF_DEV void store_vec(TIO* base, uint32_t o, const float (&src)[VEC]) {
   }
 }
 
-TSF_DEV float silu_f(float p) { return p * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-p * kLog2e)); }
 
 // Thread coordinates: channel group cg (VEC channels from d0 = cg * VEC), run r, batch row b.
 struct Coord {
@@ -107,9 +370,9 @@ TSF_DEV void load_xbuf(float (&dst)[VEC], const TIO* __restrict__ xrow, const TI
   }
 }
 
-// ------------------------------------------------------------------------------------ forward
+// ------------------------------------------------------------------ register-tiled forward (fp32)
 template <typename TIO, int K, int VEC>
-__global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_fwd_kernel(
+__global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_fwd_reg(
     const TIO* __restrict__ x, const TIO* __restrict__ tail, const float* __restrict__ w,
     const float* __restrict__ bias, TIO* __restrict__ out, int64_t L, int64_t D, int64_t sxb, int64_t sxl,
     int64_t sxd, int64_t runs) {
@@ -145,7 +408,7 @@ __global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_fwd_kernel(
   }
 }
 
-// ----------------------------------------------------------------------------------- backward
+// ----------------------------------------------------------------- register-tiled backward (fp32)
 // gpre_t = gy_t silu'(p_t); gx_t = sum_k w_k gpre_{t+K-1-k}; grad w_k = sum_t gpre_t
 // xbuf_{t-(K-1)+k}; grad bias = sum_t gpre_t; grad tail_j = sum_{t<=j} gpre_t w_{j-t}.
 // A backward thread walks kRpt consecutive runs, accumulating its parameter partials in
@@ -153,9 +416,10 @@ __global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_fwd_kernel(
 // one partial row per (batch, run block): part [B, G, D, K+1] (K taps, then the bias term).
 constexpr int kRpt = 4;
 constexpr int kRunB = 8;  // backward steps per run: its register tiles hold x and gy with halos
+static_assert(kRunsWg * kRpt * kRunB == kSeg, "both backward paths write one partial per kSeg steps");
 
 template <typename TIO, int K, int VEC>
-__global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_bwd_kernel(
+__global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_bwd_reg(
     const TIO* __restrict__ x, const TIO* __restrict__ tail, const float* __restrict__ w,
     const float* __restrict__ bias, const TIO* __restrict__ gy, TIO* __restrict__ gx, TIO* __restrict__ gtail,
     float* __restrict__ part, int64_t L, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd, int64_t runs) {
@@ -300,13 +564,64 @@ __global__ void __launch_bounds__(256) conv_zero_f32(float* __restrict__ p, int6
   if (i < n) p[i] = 0.0f;
 }
 
+// Grid: (channel blocks of kCh, segments of kSeg steps, batch rows).
 struct ConvPlan {
+  int64_t cblocks, nseg;
+};
+ConvPlan conv_plan(int64_t L, int64_t D) {
+  ConvPlan p;
+  p.cblocks = (D + kCh - 1) / kCh;
+  p.nseg = (L + kSeg - 1) / kSeg;
+  return p;
+}
+
+// Whole 16-byte pieces per tile row: channel stride 1, D and the row strides multiples of the
+// piece, 16-byte aligned bases (y, z: the contiguous [B, L, D] tensors read or written the same
+// way, or NULL).
+template <typename TIO>
+bool vec_rows(const void* x, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd, const void* y, const void* z) {
+  constexpr int64_t VE = 16 / sizeof(TIO);
+  const uintptr_t a = (uintptr_t)x | (uintptr_t)y | (uintptr_t)z;
+  return sxd == 1 && D % VE == 0 && sxl % VE == 0 && sxb % VE == 0 && a % 16 == 0;
+}
+
+template <typename TIO, int K>
+void fwd_k(bool vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
+           const void* tail, const float* w, const float* bias, void* out, hipStream_t s) {
+  const ConvPlan p = conv_plan(L, D);
+  const dim3 grid((unsigned)p.cblocks, (unsigned)p.nseg, (unsigned)B);
+  if (vec)
+    hipLaunchKernelGGL((conv_silu_fwd_kernel<TIO, K, true>), grid, dim3(kCh), 0, s, (const TIO*)x, (const TIO*)tail, w,
+                       bias, (TIO*)out, L, D, sxb, sxl, sxd);
+  else
+    hipLaunchKernelGGL((conv_silu_fwd_kernel<TIO, K, false>), grid, dim3(kCh), 0, s, (const TIO*)x, (const TIO*)tail,
+                       w, bias, (TIO*)out, L, D, sxb, sxl, sxd);
+}
+
+template <typename TIO, int K>
+void bwd_k(bool vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
+           const void* tail, const float* w, const float* bias, const void* gy, void* gx, void* gtail, float* gw,
+           float* gb, float* part, hipStream_t s) {
+  const ConvPlan p = conv_plan(L, D);
+  const dim3 grid((unsigned)p.cblocks, (unsigned)p.nseg, (unsigned)B);
+  if (vec)
+    hipLaunchKernelGGL((conv_silu_bwd_kernel<TIO, K, true>), grid, dim3(kCh), 0, s, (const TIO*)x, (const TIO*)tail, w,
+                       bias, (const TIO*)gy, (TIO*)gx, (TIO*)gtail, part, L, D, sxb, sxl, sxd);
+  else
+    hipLaunchKernelGGL((conv_silu_bwd_kernel<TIO, K, false>), grid, dim3(kCh), 0, s, (const TIO*)x, (const TIO*)tail,
+                       w, bias, (const TIO*)gy, (TIO*)gx, (TIO*)gtail, part, L, D, sxb, sxl, sxd);
+  const int64_t n = D * (K + 1);
+  hipLaunchKernelGGL(conv_reduce_params, dim3((unsigned)((n + 63) / 64)), dim3(64 * kRedWaves), 0, s,
+                     (const float*)part, gw, gb, B * p.nseg, D, K);
+}
+
+struct RegPlan {
   int64_t runs, cg_blocks, run_groups;
 };
 // run_groups: runs per workgroup row of the grid (kRunsWg for the forward, kRunsWg * kRpt for
 // the backward, whose threads walk kRpt runs each)
-ConvPlan conv_plan(int64_t L, int64_t D, int vec, int run_len, int runs_per_group) {
-  ConvPlan p;
+RegPlan reg_plan(int64_t L, int64_t D, int vec, int run_len, int runs_per_group) {
+  RegPlan p;
   p.runs = (L + run_len - 1) / run_len;
   p.cg_blocks = ((D + vec - 1) / vec + kCgWg - 1) / kCgWg;
   p.run_groups = (p.runs + runs_per_group - 1) / runs_per_group;
@@ -325,9 +640,9 @@ int vec_for(const void* x, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd, con
 template <typename TIO, int K, int VEC>
 void launch_fwd(int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
                 const void* tail, const float* w, const float* bias, void* out, hipStream_t s) {
-  const ConvPlan p = conv_plan(L, D, VEC, kRun, kRunsWg);
+  const RegPlan p = reg_plan(L, D, VEC, kRun, kRunsWg);
   dim3 grid((unsigned)p.cg_blocks, (unsigned)p.run_groups, (unsigned)B);
-  hipLaunchKernelGGL((conv_silu_fwd_kernel<TIO, K, VEC>), grid, dim3(kCgWg * kRunsWg), 0, s, (const TIO*)x,
+  hipLaunchKernelGGL((conv_silu_fwd_reg<TIO, K, VEC>), grid, dim3(kCgWg * kRunsWg), 0, s, (const TIO*)x,
                      (const TIO*)tail, w, bias, (TIO*)out, L, D, sxb, sxl, sxd, p.runs);
 }
 
@@ -335,9 +650,9 @@ template <typename TIO, int K, int VEC>
 void launch_bwd(int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
                 const void* tail, const float* w, const float* bias, const void* gy, void* gx, void* gtail,
                 float* gw, float* gb, float* part, hipStream_t s) {
-  const ConvPlan p = conv_plan(L, D, VEC, kRunB, kRunsWg * kRpt);
+  const RegPlan p = reg_plan(L, D, VEC, kRunB, kRunsWg * kRpt);
   dim3 grid((unsigned)p.cg_blocks, (unsigned)p.run_groups, (unsigned)B);
-  hipLaunchKernelGGL((conv_silu_bwd_kernel<TIO, K, VEC>), grid, dim3(kCgWg * kRunsWg), 0, s, (const TIO*)x,
+  hipLaunchKernelGGL((conv_silu_bwd_reg<TIO, K, VEC>), grid, dim3(kCgWg * kRunsWg), 0, s, (const TIO*)x,
                      (const TIO*)tail, w, bias, (const TIO*)gy, (TIO*)gx, (TIO*)gtail, part, L, D, sxb, sxl, sxd,
                      p.runs);
   const int64_t n = D * (K + 1);
@@ -346,7 +661,7 @@ void launch_bwd(int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int
 }
 
 template <typename TIO, int K>
-void fwd_k(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
+void fwd_reg(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
            const void* tail, const float* w, const float* bias, void* out, hipStream_t s) {
   if (vec == 4)
     launch_fwd<TIO, K, 4>(B, L, D, x, sxb, sxl, sxd, tail, w, bias, out, s);
@@ -355,7 +670,7 @@ void fwd_k(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb,
 }
 
 template <typename TIO, int K>
-void bwd_k(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
+void bwd_reg(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
            const void* tail, const float* w, const float* bias, const void* gy, void* gx, void* gtail, float* gw,
            float* gb, float* part, hipStream_t s) {
   if (vec == 4)
@@ -379,7 +694,7 @@ void bwd_k(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb,
 // TSF_OK when the sizes are valid and supported, else the status to return
 int conv_args_status(int64_t B, int64_t L, int64_t D, int64_t K) {
   if (B < 0 || L < 0 || D < 0 || K < 2) return TSF_ERR_ARG;
-  if (K > 8 || B > 65535) return TSF_ERR_UNSUPPORTED;
+  if (K > 8 || B > 65535 || (L + kSeg - 1) / kSeg > 65535) return TSF_ERR_UNSUPPORTED;
   return TSF_OK;
 }
 
@@ -397,8 +712,7 @@ extern "C" {
 
 int64_t tsfast_hip_conv_silu_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t K) {
   if (conv_args_status(B, L, D, K) != TSF_OK) return -1;
-  const ConvPlan p = conv_plan(L, D, 1, kRunB, kRunsWg * kRpt);
-  return B * p.run_groups * D * (K + 1) * 4;
+  return B * conv_plan(L, D).nseg * D * (K + 1) * 4;
 }
 
 int tsfast_hip_conv_silu_fwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_dtype, const void* x, int64_t sxb,
@@ -411,11 +725,11 @@ int tsfast_hip_conv_silu_fwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (io_dtype == TSF_DTYPE_F32) {
     const int vec = vec_for<float>(x, D, sxb, sxl, sxd, out);
-#define CALL(KK) fwd_k<float, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, out, s)
+#define CALL(KK) fwd_reg<float, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, out, s)
     TSF_CONV_K_SWITCH(K, CALL)
 #undef CALL
   } else if (io_dtype == TSF_DTYPE_BF16) {
-    const int vec = vec_for<bf16>(x, D, sxb, sxl, sxd, out);
+    const bool vec = vec_rows<bf16>(x, D, sxb, sxl, sxd, out, nullptr);
 #define CALL(KK) fwd_k<bf16, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, out, s)
     TSF_CONV_K_SWITCH(K, CALL)
 #undef CALL
@@ -447,11 +761,11 @@ int tsfast_hip_conv_silu_bwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_
   float* part = static_cast<float*>(workspace);
   if (io_dtype == TSF_DTYPE_F32) {
     const int vec = vec_for<float>(x, D, sxb, sxl, sxd, gy) == 4 && ((uintptr_t)gx % 16 == 0) ? 4 : 1;
-#define CALL(KK) bwd_k<float, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, gy, gx, gtail, gw, gb, part, s)
+#define CALL(KK) bwd_reg<float, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, gy, gx, gtail, gw, gb, part, s)
     TSF_CONV_K_SWITCH(K, CALL)
 #undef CALL
   } else if (io_dtype == TSF_DTYPE_BF16) {
-    const int vec = vec_for<bf16>(x, D, sxb, sxl, sxd, gy) == 4 && ((uintptr_t)gx % 8 == 0) ? 4 : 1;
+    const bool vec = vec_rows<bf16>(x, D, sxb, sxl, sxd, gy, gx);
 #define CALL(KK) bwd_k<bf16, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, gy, gx, gtail, gw, gb, part, s)
     TSF_CONV_K_SWITCH(K, CALL)
 #undef CALL
