@@ -1,4 +1,5 @@
-"""The single-pass look-back scans under HIP graph capture and on concurrent streams.
+"""The single-pass look-back scans (diagonal, selective, all-pole, constant-matrix) under HIP
+graph capture and on concurrent streams.
 
 Each call resets its workspace (tile counter and published look-back words) with a kernel, not a
 memset node, so a captured forward + backward must match eager results on every replay, with
@@ -7,9 +8,11 @@ its own workspace) must not interfere. A look-back may compose the same maps in 
 from run to run, so results agree to fp64 rounding (compared at 1e-6 relative), not bit for bit.
 """
 
+import numpy as np
 import pytest
 import torch
 
+from tsfast_amd.dynonet import allpole_hip, linrec_hip
 from tsfast_amd.scan_backends import diagonal_hip, selective_hip
 
 pytestmark = pytest.mark.gpu
@@ -97,3 +100,55 @@ def test_two_streams_in_flight(gpu, kind):
     for got, want in ((got_a, want_a), (got_b, want_b)):
         for c, e in zip(got, want):
             assert _close(c, e)
+
+
+def _linrec_inputs(seed, dev, M=96, L=5000, n=3):
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(M, n, n, generator=g, dtype=torch.float64)
+    rho = torch.linalg.eigvals(A).abs().amax(-1).clamp_min(1e-6)
+    A = (A * (0.95 / rho)[:, None, None]).float()
+    return [t.to(dev) for t in (A, torch.randn(M, L, n, generator=g), torch.randn(M, n, generator=g),
+                                torch.randn(M, L, n, generator=g))]
+
+
+def _allpole_inputs(seed, dev, lanes=200, L=9000, na=3):
+    g = torch.Generator().manual_seed(seed)
+    r = torch.rand(lanes, na, generator=g, dtype=torch.float64) * 0.9
+    a = torch.stack([torch.tensor(np.poly(ri.numpy())[1:]) for ri in r]).float()
+    return [t.to(dev) for t in (a, torch.randn(lanes, L, generator=g), torch.randn(lanes, na, generator=g),
+                                torch.randn(lanes, L, generator=g))]
+
+
+def _run_linrec(A, v, x0, gout):
+    x = linrec_hip._linrec_op(A, v, x0)
+    return (x, *linrec_hip._linrec_bwd_op(gout, A, x, x0))
+
+
+def _run_allpole(a, w, y0, gout):
+    y = allpole_hip._allpole_op(a, w, y0)
+    return (y, *allpole_hip._allpole_bwd_op(gout, a, y, y0))
+
+
+@pytest.mark.parametrize("kind", ["linrec", "allpole"])
+def test_graph_replay_dynonet_scans(gpu, kind):
+    """The constant-matrix recurrence and the all-pole scan (look-back words reset by a kernel)
+    replay correctly from a captured graph, with new inputs and eager work between replays."""
+    make, run = (_linrec_inputs, _run_linrec) if kind == "linrec" else (_allpole_inputs, _run_allpole)
+    ins = make(0, gpu)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run(*ins)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = run(*ins)
+    for rep in range(1, 4):
+        for dst, src in zip(ins, make(rep, gpu)):
+            dst.copy_(src)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = run(*ins)
+        torch.cuda.synchronize()
+        for i, (c, e) in enumerate(zip(captured, eager)):
+            assert _close(c, e), f"replay {rep}: output {i}"
