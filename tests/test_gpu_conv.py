@@ -46,6 +46,9 @@ _SHAPES = [
     (2, 64, 64, 8, True, False),
     (3, 17, 12, 3, False, False),
     (2, 100, 24, 5, True, True),
+    (2, 150, 40, 6, True, True),  # K = 6: 18-row tiles
+    (1, 300, 16, 7, False, True),  # K = 7: 21-row tiles, several segments
+    (3, 700, 264, 4, True, True),  # two channel blocks, the second nearly empty
     (2, 1024, 1536, 4, True, True),  # config-3 channel count, reduced batch and length
 ]
 
