@@ -123,6 +123,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
   __shared__ int s_pend[64];
   __shared__ int s_any;
   __shared__ unsigned s_tile[2];
+  __shared__ double s_mat[MatStage<NA>::kDoubles];
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int P = I * O, R = kTile / P;
   const int64_t lanes = B * P;
@@ -158,6 +159,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
           if (i < n) step<NA>(av, s, (double)xb[i]);
       }
     }
+    if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, l0, lanes);
     double* vk = vec_area<NA>(s_lds, k) + lid * NA;
 #pragma unroll
     for (int q = 0; q < NA; ++q) vk[q] = s[q];
@@ -168,7 +170,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
     for (int q = 0; q < NA; ++q) sup[q] = 0.0;
     if (k == 0 && live) {
       double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
+      load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NA * NA] : Mc + lane * NA * NA);
       for (int jj = 0; jj < K; ++jj) {
         double ej[NA];
         const double* vj = vec_area<NA>(s_lds, jj) + lid * NA;
@@ -182,7 +184,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
 #pragma unroll
     for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[lane * NA + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
-      ap_look_back<NA>(S, agg, inc, Ms + lane * NA * NA, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
+      ap_look_back<NA>(S, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
                        k, lid, s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
       if (saved) {
@@ -191,12 +193,12 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
       }
       if (sc + 1 < nsuper) {
         double ms[NA][NA], o[NA];
-        load_mat<NA>(ms, Ms + lane * NA * NA);
+        load_mat<NA>(ms, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA);
         matvec_add<NA>(o, ms, S, sup);
         put_vec<NA>(inc + (sc * lanes + lane) * NA, o);
       }
       double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
+      load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NA * NA] : Mc + lane * NA * NA);
       for (int jj = 0; jj < K; ++jj) {
         double ej[NA];
         double* vj = vec_area<NA>(s_lds, jj) + lid * NA;
@@ -272,6 +274,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
   __shared__ int s_pend[64];
   __shared__ int s_any;
   __shared__ unsigned s_tile[2];
+  __shared__ double s_mat[MatStage<NA>::kDoubles];
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int P = I * O, R = kTile / P;
   const int64_t lanes = B * P;
@@ -322,6 +325,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
           step<NA>(av, sC, (double)h);
         }
     }
+    if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, l0, lanes);
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
       vk[q] = sG[q];
@@ -334,7 +338,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     for (int q = 0; q < V; ++q) sup[q] = 0.0;
     if (k == 0 && live) {
       double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
+      load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NA * NA] : Mc + lane * NA * NA);
       for (int jj = K - 1; jj >= 0; --jj) {
         double fj[V];
         const double* vj = vec_area<NA>(s_lds, jj) + lid * V;
@@ -348,17 +352,17 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
 #pragma unroll
     for (int q = 0; q < V; ++q) Rv[q] = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
-      ap_look_back<NA, 2>(Rv, agg, inc, Ms + lane * NA * NA, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane,
+      ap_look_back<NA, 2>(Rv, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane,
                           K, k, lid, s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
       if (sc > 0) {
         double ms[NA][NA], o[V];
-        load_mat<NA>(ms, Ms + lane * NA * NA);
+        load_mat<NA>(ms, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA);
         block_matvec_add<NA, 2>(o, ms, Rv, sup);
         put_vec<V>(inc + (sc * lanes + lane) * V, o);
       }
       double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
+      load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NA * NA] : Mc + lane * NA * NA);
       for (int jj = K - 1; jj >= 0; --jj) {
         double fj[V];
         double* vj = vec_area<NA>(s_lds, jj) + lid * V;
@@ -397,7 +401,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
 #pragma unroll
       for (int q = 0; q < NA; ++q) st[q] = sc == 0 ? (x0 ? (double)x0[lane * NA + q] : 0.0) : saved[(sc * lanes + lane) * NA + q];
       double mc[NA][NA];
-      load_mat<NA>(mc, Mc + lane * NA * NA);
+      load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NA * NA] : Mc + lane * NA * NA);
       for (int jj = 0; jj < K; ++jj) {
         double ej[NA];
         double* vj = vec_area<NA>(s_lds, jj) + lid * V;
