@@ -649,3 +649,27 @@ def test_linrec_check_rejects_forward():
 )
 def test_linrec_check_rejects_backward(mutant):
     assert not check_linrec(O.linrec_forward, mutant)
+
+
+def test_linrec_doubling_scan_matches_oracle():
+    """The CPU route of linear_recurrence (the reference's log-doubling op and its adjoint, which
+    every non-GPU call and every unsupported shape takes) against the oracle, with A broadcast
+    over a batch dim so the adjoint's grad_A is summed back."""
+    from tsfast_amd.dynonet.core import linear_recurrence
+
+    rng = _rng(13)
+    Bb, P, L, n = 2, 3, 37, 5  # n = 5: beyond the GPU kernel's range
+    A = rng.standard_normal((P, n, n)) * (0.8 / np.sqrt(n))
+    v = rng.standard_normal((Bb, P, L, n))
+    x0 = rng.standard_normal((Bb, P, n))
+    g = rng.standard_normal((Bb, P, L, n))
+    At, vt, x0t = (torch.tensor(t, requires_grad=True) for t in (A, v, x0))
+    x = linear_recurrence(At, vt, x0t)
+    x.backward(torch.tensor(g))
+    Ab = np.broadcast_to(A, (Bb, P, n, n)).reshape(Bb * P, n, n)
+    want = O.linrec_forward(Ab, v.reshape(Bb * P, L, n), x0.reshape(Bb * P, n))
+    assert O.rel_err(x.detach().numpy().reshape(Bb * P, L, n), want) < TOL
+    gA, gv, gx0 = O.linrec_backward(g.reshape(Bb * P, L, n), Ab, want, x0.reshape(Bb * P, n))
+    assert O.rel_err(At.grad.numpy(), gA.reshape(Bb, P, n, n).sum(0)) < TOL
+    assert O.rel_err(vt.grad.numpy().reshape(Bb * P, L, n), gv) < TOL
+    assert O.rel_err(x0t.grad.numpy().reshape(Bb * P, n), gx0) < TOL
