@@ -404,6 +404,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
 
   TIO r_dr[IT], r_u[IT], r_z[IT], r_go[IT], r_y[IT], r_bv[NBV], r_cv[NBV];
   float r_hs[NPT];
+  // FULL loads (no per-element guard): all CHK steps in the sequence, all DT channels in range
+  // and N == NS; workgroup-uniform
+  const bool wg_full = d0 + DT <= D && N == NS;
   auto load_chunk = [&](int64_t c, auto full) __attribute__((always_inline)) {
     constexpr bool FULL = decltype(full)::value;
     const uint32_t t0 = (uint32_t)(c * CHK);
@@ -411,8 +414,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
       const uint32_t t = (uint32_t)(idx / DT);
-      bool v = idx < CHK * DT && oact;
-      if (!FULL) v = v && (int64_t)(t0 + t) < L;
+      bool v = (CHK * DT) % TH == 0 || idx < CHK * DT;
+      if (!FULL) v = v && oact && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Du + (uint32_t)od;
       r_dr[k] = v ? ld32(drw, o) : io_zero<TIO>();
       r_u[k] = v ? ld32(urw, o) : io_zero<TIO>();
@@ -426,8 +429,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       const int s = v * 16 + lk;
       const uint32_t t = (uint32_t)(s / NPT);
       const int n = (s % NPT) * NG + ng;
-      bool ok = s < NSL && n < N;
-      if (!FULL) ok = ok && (int64_t)(t0 + t) < L;
+      bool ok = NSL % 16 == 0 || s < NSL;
+      if (!FULL) ok = ok && n < N && (int64_t)(t0 + t) < L;
       const uint32_t o = (t0 + t) * Nu + (uint32_t)n;
       r_bv[v] = ok ? ld32(brw, o) : io_zero<TIO>();
       r_cv[v] = ok ? ld32(crw, o) : io_zero<TIO>();
@@ -437,17 +440,16 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     for (int j = 0; j < NPT; ++j) {
       const int n = j * NG + ng;
       float v0 = 0.0f;
-      if (act && n < N) {
-        if (c > 0)
-          v0 = ld32(chkb, ((uint32_t)(c - 1) * Nu + (uint32_t)n) * Du + (uint32_t)dl);
-        else if (h0)
-          v0 = h0[(b * D + d) * N + n];
+      if (c > 0) {
+        if (FULL || (act && n < N)) v0 = ld32(chkb, ((uint32_t)(c - 1) * Nu + (uint32_t)n) * Du + (uint32_t)dl);
+      } else if (h0 && act && n < N) {
+        v0 = h0[(b * D + d) * N + n];
       }
       r_hs[j] = v0;
     }
   };
   auto load_any = [&](int64_t c) __attribute__((always_inline)) {
-    if ((c + 1) * CHK <= L)
+    if ((c + 1) * CHK <= L && wg_full)
       load_chunk(c, Bool<true>());
     else
       load_chunk(c, Bool<false>());
@@ -486,7 +488,13 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     }
 #pragma unroll
     for (int j = 0; j < NPT; ++j) hst[j] = r_hs[j];
-    if (c > 0) load_chunk(c - 1, Bool<true>());  // every chunk before the last is full
+    // every chunk before the last is full in time
+    if (c > 0) {
+      if (wg_full)
+        load_chunk(c - 1, Bool<true>());
+      else
+        load_chunk(c - 1, Bool<false>());
+    }
     __syncthreads();
 
     // recompute this chunk's states into registers: lam_t, lam_t h_{t-1} and h_t
