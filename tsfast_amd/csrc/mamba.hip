@@ -96,6 +96,11 @@ TSF_DEV void set_wave_priority(unsigned p) {
 // backward (non-temporal: it is not kept in the caches on the way out).
 TSF_DEV void nt_store(float* p, float v) { __builtin_nontemporal_store(v, p); }
 TSF_DEV void nt_store(bf16* p, bf16 v) { __builtin_nontemporal_store(v.bits, &p->bits); }
+// The same at a 32-bit element index from a workgroup-uniform base (SGPR base + VGPR offset).
+template <typename T>
+TSF_DEV void nt_st32(T* __restrict__ base, uint32_t idx, T v) {
+  nt_store(reinterpret_cast<T*>(reinterpret_cast<char*>(base) + idx * (uint32_t)sizeof(T)), v);
+}
 
 // Floats of training-forward saved state per batch row: fp32 checkpoints [NC, N, D], then the
 // pre-gate output y [L, D] in the I/O type (padded to whole floats).
@@ -215,7 +220,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
 #pragma unroll
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
-      if (idx < TF * DT) {
+      if ((TF * DT) % TH == 0 || idx < TF * DT) {
         o_u[k] = to_f32(r_u[k]);
         o_z[k] = to_f32(r_z[k]);
         const bool live = oact && idx / DT < len;
@@ -269,7 +274,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         const uint32_t slot = (t0 + (uint32_t)ie) / CHK;
 #pragma unroll
         for (int j = 0; j < NPT; ++j)
-          if (n0 + j < N) nt_store(chkb + ((slot * Nu + (uint32_t)(n0 + j)) * Du + (uint32_t)dl), h[j]);
+          if (n0 + j < N) nt_st32(chkb, (slot * Nu + (uint32_t)(n0 + j)) * Du + (uint32_t)dl, h[j]);
       }
     }
     __syncthreads();
@@ -278,7 +283,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
       const int t = idx / DT;
-      if (idx < TF * DT && t < len && oact) {
+      if (((TF * DT) % TH == 0 || idx < TF * DT) && t < len && oact) {
         float y = 0.0f;
 #pragma unroll
         for (int g = 0; g < NG; ++g) y += s_y[t][g][od ^ ((g & 1) << 4)];
@@ -286,7 +291,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
         const float yv = fmaf(dp_o, o_u[k], y);
         st32(orw, o, from_f32<TIO>(yv * zz * sigmoid_fast(zz)));
-        if (yrw) nt_store(yrw + o, from_f32<TIO>(yv));  // the backward's gate gradient needs y before the gate
+        if (yrw) nt_st32(yrw, o, from_f32<TIO>(yv));  // the backward's gate gradient needs y before the gate
       }
     }
   };
