@@ -102,6 +102,16 @@ TSF_DEV void nt_st32(T* __restrict__ base, uint32_t idx, T v) {
   nt_store(reinterpret_cast<T*>(reinterpret_cast<char*>(base) + idx * (uint32_t)sizeof(T)), v);
 }
 
+// Pairwise sum of K values (K a power of two), in a fixed order.
+template <int K>
+TSF_DEV float tree_sum(const float* v) {
+  if constexpr (K == 1) {
+    return v[0];
+  } else {
+    return tree_sum<K / 2>(v) + tree_sum<K / 2>(v + K / 2);
+  }
+}
+
 // Floats of training-forward saved state per batch row: fp32 checkpoints [NC, N, D], then the
 // pre-gate output y [L, D] in the I/O type (padded to whole floats).
 template <typename TIO>
@@ -123,7 +133,8 @@ TSF_DEV void xcd_remap(int64_t& tile, int64_t& row) {
 }
 
 // ------------------------------------------------------------------------------------ forward
-template <typename TIO, int NS>
+// SAVE: training forward (writes the checkpoints and y to chk); chk is unused otherwise.
+template <typename TIO, int NS, bool SAVE>
 __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     const TIO* __restrict__ draw, const float* __restrict__ A, const TIO* __restrict__ Bt,
     const TIO* __restrict__ Ct, const TIO* __restrict__ u, const TIO* __restrict__ z, const float* __restrict__ Dp,
@@ -173,9 +184,9 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   const TIO* __restrict__ brw = Bt + rowN;
   const TIO* __restrict__ crw = Ct + rowN;
   // saved state of this batch row (training only): checkpoints [NC, N, D], then y [L, D]
-  float* __restrict__ svb = chk ? chk + b * saved_row_floats<TIO>(L, D, N, NC) : nullptr;
-  float* __restrict__ chkb = chk ? svb + d0 : nullptr;
-  TIO* __restrict__ yrw = chk ? reinterpret_cast<TIO*>(svb + NC * N * D) + d0 : nullptr;
+  float* __restrict__ svb = SAVE ? chk + b * saved_row_floats<TIO>(L, D, N, NC) : nullptr;
+  float* __restrict__ chkb = SAVE ? svb + d0 : nullptr;
+  TIO* __restrict__ yrw = SAVE ? reinterpret_cast<TIO*>(svb + NC * N * D) + d0 : nullptr;
 
   TIO r_dr[IT], r_u[IT], r_z[IT], r_b[BCI], r_c[BCI];
   auto load_chunk = [&](uint32_t t0, auto full) __attribute__((always_inline)) {
@@ -270,7 +281,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       }
       // checkpoint slot k holds the state after step (k + 1) * CHK - 1 (layout [B, NC, N, D])
       const int ie = i0 + kRd - 1;
-      if ((ie % CHK) == CHK - 1 && chk && act && ie < len) {
+      if (SAVE && (ie % CHK) == CHK - 1 && act && ie < len) {
         const uint32_t slot = (t0 + (uint32_t)ie) / CHK;
 #pragma unroll
         for (int j = 0; j < NPT; ++j)
@@ -284,14 +295,15 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       const int idx = tid + k * TH;
       const int t = idx / DT;
       if (((TF * DT) % TH == 0 || idx < TF * DT) && t < len && oact) {
-        float y = 0.0f;
+        float yp[NG];
 #pragma unroll
-        for (int g = 0; g < NG; ++g) y += s_y[t][g][od ^ ((g & 1) << 4)];
+        for (int g = 0; g < NG; ++g) yp[g] = s_y[t][g][od ^ ((g & 1) << 4)];
+        const float y = tree_sum<NG>(yp);
         const float zz = o_z[k];
         const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
         const float yv = fmaf(dp_o, o_u[k], y);
         st32(orw, o, from_f32<TIO>(yv * zz * sigmoid_fast(zz)));
-        if (yrw) nt_st32(yrw, o, from_f32<TIO>(yv));  // the backward's gate gradient needs y before the gate
+        if (SAVE) nt_st32(yrw, o, from_f32<TIO>(yv));  // the backward's gate gradient needs y before the gate
       }
     }
   };
@@ -553,12 +565,13 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
         const int t = idx / DT;
         if (idx < CHK * DT && t >= sb * TB && t < sb * TB + TB && t < len && oact) {
           const int ii = t - sb * TB;
-          float aq = 0.0f, gb = 0.0f;
+          float aqp[NG], gbp[NG];
 #pragma unroll
           for (int g = 0; g < NG; ++g) {
-            aq += s_np[ii][0][g][od];
-            gb += s_np[ii][1][g][od];
+            aqp[g] = s_np[ii][0][g][od];
+            gbp[g] = s_np[ii][1][g][od];
           }
+          const float aq = tree_sum<NG>(aqp), gb = tree_sum<NG>(gbp);
           const float4 sc = s_sc[t][od];
           const float uu = o_u[k], zz = o_z[k], sg = o_sg[k];
           const float gzv = o_go[k] * o_y[k] * sg * (1.0f + zz * (1.0f - sg));
@@ -582,7 +595,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
             const float4 v = row[(q + (col >> 1)) & 7];
-            s += (v.x + v.y) + (v.z + v.w);
+            const float part = (v.x + v.y) + (v.z + v.w);
+            s = q == 0 ? part : s + part;
           }
           st32(gbcb, (t0 + (uint32_t)t) * (uint32_t)W2 + (uint32_t)col, s);
         }
@@ -657,9 +671,14 @@ int launch_fwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
   using C = MCfg<NS>;
   const int64_t NC = (L + C::CHK - 1) / C::CHK;
   dim3 grid((unsigned)((D + C::DT - 1) / C::DT), (unsigned)B);
-  hipLaunchKernelGGL((mamba_fwd_kernel<TIO, NS>), grid, dim3(C::TH), 0, s, (const TIO*)draw, A, (const TIO*)Bt,
-                     (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, (TIO*)out, h_last, chk, L, D, (int)N, NC,
-                     device_cus());
+  if (chk)
+    hipLaunchKernelGGL((mamba_fwd_kernel<TIO, NS, true>), grid, dim3(C::TH), 0, s, (const TIO*)draw, A,
+                       (const TIO*)Bt, (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, (TIO*)out, h_last, chk, L,
+                       D, (int)N, NC, device_cus());
+  else
+    hipLaunchKernelGGL((mamba_fwd_kernel<TIO, NS, false>), grid, dim3(C::TH), 0, s, (const TIO*)draw, A,
+                       (const TIO*)Bt, (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, (TIO*)out, h_last, chk, L,
+                       D, (int)N, NC, device_cus());
   return tsf_launch_status();
 }
 
