@@ -168,12 +168,15 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   const uint32_t Du = (uint32_t)D, Nu = (uint32_t)N;
 
   float A2[NPT], h[NPT];
+  uint32_t co[NPT];  // offset of state n0 + j of this channel within one checkpoint slot [N, D]
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
     const int n = n0 + j;
     A2[j] = (act && n < N) ? A[d * N + n] * kLog2e : 0.0f;
     h[j] = (act && h0 && n < N) ? h0[(b * D + d) * N + n] : 0.0f;
+    co[j] = (uint32_t)n * Du + (uint32_t)dl;
   }
+  const uint32_t slot_floats = Nu * Du;
   const float dp_o = oact ? Dp[d0 + od] : 0.0f;
 
   // workgroup-uniform row bases: loads use SGPR base + 32-bit VGPR offset addressing
@@ -285,7 +288,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         const uint32_t slot = (t0 + (uint32_t)ie) / CHK;
 #pragma unroll
         for (int j = 0; j < NPT; ++j)
-          if (n0 + j < N) nt_st32(chkb, (slot * Nu + (uint32_t)(n0 + j)) * Du + (uint32_t)dl, h[j]);
+          if (n0 + j < N) nt_st32(chkb, slot * slot_floats + co[j], h[j]);
       }
     }
     __syncthreads();
@@ -391,10 +394,12 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
   const uint32_t Du = (uint32_t)D, Nu = (uint32_t)N;
 
   float A2[NPT], Av[NPT], G[NPT], gA[NPT], lam_next[NPT];
+  uint32_t co[NPT];  // offset of state j * NG + ng of this channel within one checkpoint slot [N, D]
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
     const int n = j * NG + ng;
     const bool v = act && n < N;
+    co[j] = (uint32_t)n * Du + (uint32_t)dl;
     Av[j] = v ? A[d * N + n] : 0.0f;
     A2[j] = Av[j] * kLog2e;
     G[j] = (v && ghlast) ? ghlast[(b * D + d) * N + n] : 0.0f;
@@ -458,7 +463,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
       const int n = j * NG + ng;
       float v0 = 0.0f;
       if (c > 0) {
-        if (FULL || (act && n < N)) v0 = ld32(chkb, ((uint32_t)(c - 1) * Nu + (uint32_t)n) * Du + (uint32_t)dl);
+        if (FULL || (act && n < N)) v0 = ld32(chkb, (uint32_t)(c - 1) * (Nu * Du) + co[j]);
       } else if (h0 && act && n < N) {
         v0 = h0[(b * D + d) * N + n];
       }
