@@ -50,6 +50,11 @@ int ns_for(int64_t N) {
   return 0;
 }
 
+// Forward steps whose LDS operands are read in one batch, ahead of their use (NPT <= 2).
+#ifndef TSF_MAMBA_FWD_RD
+#define TSF_MAMBA_FWD_RD 4
+#endif
+
 template <int NS>
 struct MCfg {
   static constexpr int NG = NS >= 8 ? 8 : NS;  // lanes per channel
@@ -259,7 +264,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
     // phase 2: the recurrence, NPT states per lane. LDS operands are read kRd steps ahead of
     // their use, and the step body has no branch (every lane stores its own y partial), so the
     // reads of later steps overlap the arithmetic of earlier ones.
-    constexpr int kRd = NPT <= 2 ? 4 : 2;
+    constexpr int kRd = NPT <= 2 ? TSF_MAMBA_FWD_RD : 2;
     static_assert(TF % kRd == 0 && CHK % kRd == 0, "read batches must not straddle checkpoints");
 #pragma unroll
     for (int i0 = 0; i0 < TF; i0 += kRd) {
