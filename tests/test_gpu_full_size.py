@@ -1,0 +1,171 @@
+"""GPU parity at BASELINE.json's full sizes (configs 2-5), through properties that do not need the
+oracle to run the whole workload.
+
+* Independence: lanes (and, for Mamba, batch rows and channels) do not interact, so a slice of
+  the full-size result must equal the fp64 oracle run on that slice alone at the full sequence
+  length. Config 3 also checks every batch row of the full call bit for bit against a call on
+  that row alone, and its batch-summed gradients (grad A, grad D) against the ordered sum of the
+  per-row calls, bit for bit (the same fp32 additions in the same order).
+* Config 4 runs the oracle on all 4096 lanes (it is a vectorised loop over 16384 steps).
+* Config 5: 64 TBPTT chunks of 4096 steps with the last state carried equal one unchunked call
+  (forward), chunk slicing is exact, and the truncated per-chunk backward matches the oracle.
+
+Bars: 1e-5 max relative error for fp32 / complex64 I/O, 2e-2 for bf16 I/O with fp32 state.
+Inputs follow the configs' distributions with fixed seeds.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import scan_oracle as O
+from tsfast_amd.dynonet import allpole_hip
+from tsfast_amd.mamba import mamba_hip
+from tsfast_amd.scan_backends import diagonal_hip
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _rel_gpu(a, b):
+    """max |a - b| / max |b| on the device (no host copy of full-size tensors)."""
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+
+
+def test_config2_full_size(gpu):
+    """Complex diagonal scan, B64 L4096 N256 (complex64): rows 0, 37 and 63 against the oracle."""
+    g = torch.Generator().manual_seed(1)
+    B, L, N = 64, 4096, 256
+    r = torch.rand(N, generator=g) * 0.099 + 0.9
+    th = torch.rand(N, generator=g) * (np.pi / 10)
+    lam = torch.polar(r, th).expand(B, N).contiguous().to(gpu)
+    v = torch.randn(B, L, N, dtype=torch.complex64, generator=g).to(gpu)
+    gout = torch.randn(B, L, N, dtype=torch.complex64, generator=g).to(gpu)
+    out = diagonal_hip.forward(lam, v, None)
+    glam, gv, _ = diagonal_hip.backward(gout, lam, out, None)
+    for b in (0, 37, 63):
+        want = O.diag_forward(_np(lam[b : b + 1]), _np(v[b : b + 1]))
+        wglam, wgv, _ = O.diag_backward(_np(gout[b : b + 1]), _np(lam[b : b + 1]), want)
+        assert O.rel_err(_np(out[b : b + 1]), want) < 1e-5, f"x row {b}"
+        assert O.rel_err(_np(gv[b : b + 1]), wgv) < 1e-5, f"gv row {b}"
+        assert O.rel_err(_np(glam[b : b + 1]), wglam) < 1e-5, f"glam row {b}"
+
+
+def _mamba_call(args, gout):
+    leaves = [a.detach().clone().requires_grad_() if a is not None else None for a in args]
+    out, h_last = mamba_hip.run(*leaves)
+    torch.autograd.backward([out], [gout])
+    grads = [x.grad if x is not None else None for x in leaves]
+    return out.detach(), h_last.detach(), grads
+
+
+def test_config3_full_size(gpu):
+    """Fused Mamba scan at B16 L4096 D1536 N16, bf16 I/O, config 3's distributions."""
+    g = torch.Generator().manual_seed(2)
+    B, L, D, N = 16, 4096, 1536, 16
+    bf = torch.bfloat16
+    A = -torch.exp(torch.log(torch.arange(1, N + 1, dtype=torch.float32))).expand(D, N).contiguous()
+    draw = (torch.randn(B, L, D, generator=g) - 4.0).to(bf)
+    Bt = torch.randn(B, L, N, generator=g).to(bf)
+    Ct = torch.randn(B, L, N, generator=g).to(bf)
+    u = torch.randn(B, L, D, generator=g).to(bf)
+    z = torch.randn(B, L, D, generator=g).to(bf)
+    Dp = torch.randn(D, generator=g)
+    gout = torch.randn(B, L, D, generator=g).to(bf)
+    args = [t.to(gpu) for t in (draw, A, Bt, Ct, u, z, Dp)] + [None]
+    gout = gout.to(gpu)
+    out, h_last, grads = _mamba_call(args, gout)
+    gdraw, gA, gBt, gCt, gu, gz, gDp, _ = grads
+
+    # every batch row alone gives the same bits; the batch-summed grads are the ordered row sums
+    gA_sum = torch.zeros_like(gA)
+    gDp_sum = torch.zeros_like(gDp)
+    for b in range(B):
+        row = [a[b : b + 1] if a is not None and a.dim() == 3 else a for a in args]
+        o1, h1, g1 = _mamba_call(row, gout[b : b + 1])
+        assert torch.equal(o1, out[b : b + 1]) and torch.equal(h1, h_last[b : b + 1]), f"row {b} forward"
+        for k, full in ((0, gdraw), (2, gBt), (3, gCt), (4, gu), (5, gz)):
+            assert torch.equal(g1[k], full[b : b + 1]), f"row {b} grad {k}"
+        gA_sum = gA_sum + g1[1]
+        gDp_sum = gDp_sum + g1[6]
+    assert torch.equal(gA_sum, gA) and torch.equal(gDp_sum, gDp)
+
+    # a full-length slice (row 7, channels 256..383) against the fp64 oracle: the per-channel
+    # outputs and gradients depend on that slice alone
+    b, ds = 7, slice(256, 384)
+    sl = [
+        _np64(draw[b : b + 1, :, ds]), _np64(A[ds]), _np64(Bt[b : b + 1]), _np64(Ct[b : b + 1]),
+        _np64(u[b : b + 1, :, ds]), _np64(z[b : b + 1, :, ds]), _np64(Dp[ds]),
+    ]
+    want_out, want_h = O.mamba_forward(*sl)
+    wgdraw, _, _, _, wgu, wgz, _, _ = O.mamba_backward(_np64(gout[b : b + 1, :, ds]), None, *sl)
+    tol = 2e-2
+    assert O.rel_err(_np64(out[b : b + 1, :, ds]), want_out) < tol
+    assert O.rel_err(_np64(h_last.view(B, D, N)[b : b + 1, ds]), want_h) < tol
+    assert O.rel_err(_np64(gdraw[b : b + 1, :, ds]), wgdraw) < tol
+    assert O.rel_err(_np64(gu[b : b + 1, :, ds]), wgu) < tol
+    assert O.rel_err(_np64(gz[b : b + 1, :, ds]), wgz) < tol
+
+
+def test_config4_full_size(gpu):
+    """All-pole order 3, 64 pairs x 64 batch, L16384; the oracle runs on all 4096 lanes."""
+    g = torch.Generator().manual_seed(3)
+    Bb, P, L, na = 64, 64, 16384, 3
+    rows = []
+    for _ in range(P):
+        rp = 0.5 + 0.48 * torch.rand(1, generator=g).item()
+        th = np.pi * torch.rand(1, generator=g).item()
+        rr = (0.5 + 0.48 * torch.rand(1, generator=g).item()) * (1 if torch.rand(1, generator=g).item() < 0.5 else -1)
+        rows.append(np.real(np.poly([rp * np.exp(1j * th), rp * np.exp(-1j * th), rr]))[1:])
+    a = torch.tensor(np.array(rows), dtype=torch.float32)
+    w = torch.randn(Bb, P, L, generator=g)
+    gout = torch.randn(Bb, P, L, generator=g)
+    a_d, w_d = a.to(gpu).requires_grad_(), w.to(gpu).requires_grad_()
+    y = allpole_hip.run(a_d, w_d, None)
+    y.backward(gout.to(gpu))
+    lanes = Bb * P
+    a_l = a.expand(Bb, P, na).reshape(lanes, na).double().numpy()
+    want = O.allpole_forward(a_l, w.reshape(lanes, L).double().numpy())
+    ga, gw, _ = O.allpole_backward(gout.reshape(lanes, L).double().numpy(), a_l, want)
+    assert O.rel_err(_np(y).reshape(lanes, L), want) < 1e-5
+    assert O.rel_err(_np(w_d.grad).reshape(lanes, L), gw) < 1e-5
+    assert O.rel_err(_np(a_d.grad), ga.reshape(Bb, P, na).sum(0)) < 1e-5
+
+
+def test_config5_full_size(gpu):
+    """TBPTT: B8 L262144 N128 as 64 chunks of 4096 with the last state carried, vs one call."""
+    g = torch.Generator().manual_seed(4)
+    B, N, C, T = 8, 128, 64, 4096
+    lam = (torch.rand(B, N, generator=g) * 0.0099 + 0.99).to(gpu)
+    v = torch.randn(B, C * T, N, generator=g).to(gpu)
+    with torch.no_grad():
+        full = diagonal_hip.forward(lam, v, None)
+        x0, parts, x0s = None, [], []
+        for k in range(C):
+            x0s.append(x0)
+            o = diagonal_hip.forward(lam, v[:, k * T : (k + 1) * T].contiguous(), x0)
+            parts.append(o)
+            x0 = o[:, -1].contiguous()
+        chunked = torch.cat(parts, 1)
+    assert chunked.shape == full.shape == v.shape
+    assert _rel_gpu(chunked, full) < 1e-5
+    for b in (0, 7):
+        want = O.diag_forward(_np(lam[b : b + 1]), _np(v[b : b + 1]))
+        assert O.rel_err(_np(full[b : b + 1]), want) < 1e-5, f"unchunked row {b}"
+        assert O.rel_err(_np(chunked[b : b + 1]), want) < 1e-5, f"chunked row {b}"
+    # truncated backward of the first and the last chunk (the state entering a chunk is detached)
+    for k in (0, C - 1):
+        gk = torch.randn(B, T, N, generator=g).to(gpu)
+        glam, gv, gx0 = diagonal_hip.backward(gk, lam, parts[k], x0s[k])
+        x0n = None if x0s[k] is None else _np(x0s[k])
+        wglam, wgv, wgx0 = O.diag_backward(_np(gk), _np(lam), _np(parts[k]), x0n)
+        assert O.rel_err(_np(gv), wgv) < 1e-5 and O.rel_err(_np(glam), wglam) < 1e-5, f"chunk {k}"
+        if x0s[k] is not None:
+            assert O.rel_err(_np(gx0), wgx0) < 1e-5
