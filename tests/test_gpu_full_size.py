@@ -1,4 +1,4 @@
-"""GPU parity at BASELINE.json's full sizes (configs 2-5), through properties that do not need the
+"""GPU parity at BASELINE.json's full sizes (configs 2-5, and the next rows' bench shapes), through properties that do not need the
 oracle to run the whole workload.
 
 * Independence: lanes (and, for Mamba, batch rows and channels) do not interact, so a slice of
@@ -9,6 +9,8 @@ oracle to run the whole workload.
 * Config 4 runs the oracle on all 4096 lanes (it is a vectorised loop over 16384 steps).
 * Config 5: 64 TBPTT chunks of 4096 steps with the last state carried equal one unchunked call
   (forward), chunk slicing is exact, and the truncated per-chunk backward matches the oracle.
+* The next rows at their bench shapes (conv + SiLU at config 3's, the G-block at config 4's
+  channels, the constant-matrix recurrence on config 4's route): the oracle on all of it.
 
 Bars: 1e-5 max relative error for fp32 / complex64 I/O, 2e-2 for bf16 I/O with fp32 state.
 Inputs follow the configs' distributions with fixed seeds.
@@ -169,3 +171,78 @@ def test_config5_full_size(gpu):
         assert O.rel_err(_np(gv), wgv) < 1e-5 and O.rel_err(_np(glam), wglam) < 1e-5, f"chunk {k}"
         if x0s[k] is not None:
             assert O.rel_err(_np(gx0), wgx0) < 1e-5
+
+
+def test_conv_config3_shape_full_size(gpu):
+    """Fused conv + SiLU at the bench shape (config 3: B16 L4096 D1536, K 4, bf16 I/O, x the
+    strided in_proj chunk view), every output and gradient against the oracle on all of it."""
+    from tsfast_amd.mamba import conv_hip
+
+    g = torch.Generator().manual_seed(5)
+    B, L, D, K = 16, 4096, 1536, 4
+    bf = torch.bfloat16
+    xz = torch.randn(B, L, 2 * D, generator=g).to(gpu, bf).requires_grad_()
+    x = xz[..., :D]
+    tail = torch.zeros(B, D, K - 1, device=gpu, dtype=bf, requires_grad=True)
+    w = (torch.randn(D, 1, K, generator=g) * 0.5).to(gpu).requires_grad_()
+    bias = torch.randn(D, generator=g).to(gpu).requires_grad_()
+    gy = torch.randn(B, L, D, generator=g).to(gpu, bf)
+    out = conv_hip.run(x, tail, w, bias)
+    out.backward(gy)
+    xs, ts, ws, bs = _np64(x), _np64(tail), _np64(w[:, 0]), _np64(bias)
+    assert O.rel_err(_np64(out), O.conv_silu_forward(xs, ts, ws, bs)) < 2e-2
+    w_gx, w_gt, w_gw, w_gb = O.conv_silu_backward(_np64(gy), xs, ts, ws, bs)
+    assert O.rel_err(_np64(xz.grad[..., :D]), w_gx) < 2e-2
+    assert O.rel_err(_np64(tail.grad), w_gt) < 2e-2
+    assert O.rel_err(_np64(w.grad[:, 0]), w_gw) < 2e-2
+    assert O.rel_err(_np64(bias.grad), w_gb) < 2e-2
+
+
+def test_gblock_config4_shape_full_size(gpu):
+    """Fused G-block at the bench shape (config 4's channels: B64 L16384, 8 in x 8 out, nb 8,
+    na 3, zero initial state), fp32, against the oracle on all of it."""
+    from tsfast_amd.dynonet import gblock_hip
+
+    g = torch.Generator().manual_seed(6)
+    B, L, I, O_, nb, na = 64, 16384, 8, 8, 8, 3
+    u = torch.randn(B, L, I, generator=g)
+    b = torch.randn(O_, I, nb, generator=g) * 0.05
+    a = torch.empty(O_, I, na)
+    for o in range(O_):
+        for j in range(I):
+            r = (torch.rand(na, generator=g) * 0.48 + 0.5).numpy()
+            a[o, j] = torch.tensor(np.poly(r)[1:], dtype=torch.float32)
+    gy = torch.randn(B, L, O_, generator=g)
+    ts = [t.to(gpu).requires_grad_() for t in (u, b, a)]
+    y, x_last = gblock_hip.run(*ts, None, None)
+    y.backward(gy.to(gpu))
+    args = (u.double().numpy(), b.double().numpy(), a.double().numpy(), np.zeros((B, nb - 1, I)),
+            np.zeros((B, I * O_, na)))
+    want_y, want_xl, _ = O.gblock_forward(*args)
+    assert O.rel_err(_np64(y), want_y) < 1e-5 and O.rel_err(_np64(x_last), want_xl) < 1e-5
+    gu, _, gb, ga, _ = O.gblock_backward(gy.double().numpy(), None, *args)
+    assert O.rel_err(_np64(ts[0].grad), gu) < 1e-5
+    assert O.rel_err(_np64(ts[1].grad), gb) < 1e-5
+    assert O.rel_err(_np64(ts[2].grad), ga) < 1e-5
+
+
+def test_linrec_config4_route_full_size(gpu):
+    """Constant-matrix recurrence on config 4's route (4096 lanes x L16384, companion matrices of
+    order-3 denominators driven by (w_t, 0, 0)), fp32, against the oracle on all of it."""
+    from tsfast_amd.dynonet import core as dcore
+    from tsfast_amd.dynonet import linrec_hip
+
+    g = torch.Generator().manual_seed(7)
+    lanes, L, n = 4096, 16384, 3
+    r = (torch.rand(lanes, n, generator=g) * 0.48 + 0.5).numpy()
+    a = torch.tensor(np.array([np.poly(ri)[1:] for ri in r]), dtype=torch.float32)
+    A = dcore.companion(a).contiguous()
+    v = torch.nn.functional.pad(torch.randn(lanes, L, 1, generator=g), (0, n - 1))
+    gx = torch.randn(lanes, L, n, generator=g)
+    A_d, v_d = A.to(gpu).requires_grad_(), v.to(gpu).requires_grad_()
+    x = linrec_hip.run(A_d, v_d, None)
+    x.backward(gx.to(gpu))
+    want = O.linrec_forward(A.double().numpy(), v.double().numpy())
+    assert O.rel_err(_np64(x), want) < 1e-5
+    gA, gv, _ = O.linrec_backward(gx.double().numpy(), A.double().numpy(), want)
+    assert O.rel_err(_np64(A_d.grad), gA) < 1e-5 and O.rel_err(_np64(v_d.grad), gv) < 1e-5
