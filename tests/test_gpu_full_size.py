@@ -1,5 +1,5 @@
-"""GPU parity at BASELINE.json's full sizes (configs 2-5, and the next rows' bench shapes), through properties that do not need the
-oracle to run the whole workload.
+"""GPU parity at BASELINE.json's full sizes (configs 2-5) and at the next rows' bench shapes,
+through properties that do not need the oracle to run the whole workload where it would be slow.
 
 * Independence: lanes (and, for Mamba, batch rows and channels) do not interact, so a slice of
   the full-size result must equal the fp64 oracle run on that slice alone at the full sequence
