@@ -372,7 +372,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     const float* __restrict__ h0, const float* __restrict__ saved, const TIO* __restrict__ gout,
     const float* __restrict__ ghlast, TIO* __restrict__ gdraw, TIO* __restrict__ gu, TIO* __restrict__ gz,
     float* __restrict__ gA_part, float* __restrict__ gDp_part, float* __restrict__ gBC_part, float* __restrict__ gh0,
-    int64_t B, int64_t L, int64_t D, int N, int64_t NC) {
+    int64_t B, int64_t L, int64_t D, int N, int64_t NC, unsigned cus) {
   using C = MCfg<NS>;
   constexpr int NPT = C::NPT, NG = C::NG, DT = C::DT, TH = C::TH, CHK = C::CHK, TB = C::TB, IT = C::IT_B;
   constexpr int NSB = CHK / TB;
@@ -616,7 +616,12 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
 #pragma unroll
     for (int j = 0; j < NPT; ++j) lam_next[j] = lamb[0][j];
   };
+  // The forward's issue-priority rotation among the workgroups sharing a CU (every 16 chunks =
+  // 128 steps): without it the oldest workgroup races ahead and the last one finishes alone.
+  const unsigned slot = (blockIdx.x + blockIdx.y * gridDim.x) / cus;
   for (int64_t c = NC - 1; c >= 0; --c) {
+    const int64_t r = NC - 1 - c;
+    if ((r & 15) == 0) set_wave_priority((slot + (unsigned)(r / 16)) % 3);
     const int64_t t0 = c * CHK;
     chunk(c, (int)((L - t0) < CHK ? (L - t0) : CHK));
   }
@@ -714,7 +719,8 @@ int launch_bwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
   if (B > 0 && D > 0)
     hipLaunchKernelGGL((mamba_bwd_kernel<TIO, NS>), grid, dim3(C::TH), 0, s, (const TIO*)draw, A, (const TIO*)Bt,
                        (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, chk, (const TIO*)gout, ghlast,
-                       (TIO*)gdraw, (TIO*)gu, (TIO*)gz, gA_part, gDp_part, gBC_part, gh0, B, L, D, (int)N, NC);
+                       (TIO*)gdraw, (TIO*)gu, (TIO*)gz, gA_part, gDp_part, gBC_part, gh0, B, L, D, (int)N, NC,
+                       device_cus());
   const int64_t BLN = B * L * N;
   if (BLN > 0)
     hipLaunchKernelGGL((mamba_reduce_bc<TIO>), dim3((unsigned)((BLN + 255) / 256)), dim3(256), 0, s, gBC_part,
