@@ -725,8 +725,9 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(
-            "bench.py measures one GPU only: this build has no multi-GPU path (every config shards "
-            "over lanes with no communication; see DESIGN.md). Run with --gpus 1.",
+            "bench.py measures one GPU only: this build has no multi-GPU path (every config would "
+            "shard over independent lanes: batch rows, channels or filter pairs, with no "
+            "communication in the scan). Run with --gpus 1.",
             file=sys.stderr,
         )
         sys.exit(2)
