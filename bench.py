@@ -155,17 +155,24 @@ def diag_inputs(cfg, device):
 
 
 def allpole_inputs(device, P=64, B=64, L=16384, na=3):
-    """Config 4: per pair, poles p, conj(p), r with |p|, |r| ~ U(0.5, 0.98); a = poly(poles)[1:]."""
+    """Config 4: per pair, poles p, conj(p), r with |p|, |r| ~ U(0.5, 0.98); a = poly(poles)[1:].
+    Other orders (the --linrec --order option) draw na // 2 conjugate pairs, plus a real pole
+    when na is odd, from the same distributions (na = 3 gives config 4's draws)."""
     import numpy as np
     import torch
 
     rng = np.random.default_rng(3)
     rows = []
     for _ in range(P):
-        rp = rng.uniform(0.5, 0.98)
-        th = rng.uniform(0, math.pi)
-        rr = rng.uniform(0.5, 0.98) * (1 if rng.random() < 0.5 else -1)
-        rows.append(np.real(np.poly([rp * np.exp(1j * th), rp * np.exp(-1j * th), rr]))[1:])
+        poles = []
+        while len(poles) < na:
+            if na - len(poles) >= 2:
+                rp = rng.uniform(0.5, 0.98)
+                th = rng.uniform(0, math.pi)
+                poles += [rp * np.exp(1j * th), rp * np.exp(-1j * th)]
+            else:
+                poles.append(rng.uniform(0.5, 0.98) * (1 if rng.random() < 0.5 else -1))
+        rows.append(np.real(np.poly(poles))[1:])
     a = torch.tensor(np.array(rows), dtype=torch.float32)
     g = torch.Generator().manual_seed(3)
     w = torch.randn(B, P, L, generator=g)
@@ -636,7 +643,7 @@ def run_linrec(args, line):
     from tsfast_amd.dynonet import core as dcore
     from tsfast_amd.dynonet import linrec_hip
 
-    a, w, gout = allpole_inputs("cuda")
+    a, w, gout = allpole_inputs("cuda", na=args.order)
     lanes, L = w.shape
     n = a.shape[-1]
     A = dcore.companion(a).contiguous()
@@ -665,17 +672,23 @@ def run_linrec(args, line):
     fwd_b, bwd_b = 2 * nbytes, 3 * nbytes  # read v, write x | read g and x, write grad_v
     line.update(
         metric="fwd+bwd ms + achieved HBM GB/s, constant-matrix linear_recurrence (BASELINE config 4 route)",
-        config={"workload": f"linear_recurrence fwd+bwd: {lanes} lanes x L {L}, n {n} companion matrices of the "
-                            "config-4 denominators, input (w_t, 0, 0) (BASELINE config 4 via the reference's "
-                            "companion-matrix route)", "lanes": lanes, "L": L, "n": n},
+        config={"workload": f"linear_recurrence fwd+bwd: {lanes} lanes x L {L}, n {n} companion matrices of "
+                            + ("the config-4 denominators" if n == 3 else f"order-{n} denominators drawn like config 4's")
+                            + ", input (w_t, 0, ..) (BASELINE config 4 via the reference's companion-matrix route)",
+                "lanes": lanes, "L": L, "n": n},
         fwd_ms=round(fwd_ms, 4),
         bwd_ms=round(bwd_ms, 4),
         doubling_scan_ms={"fwd": round(dfwd, 4), "bwd": round(dbwd, 4), "total": round(dms, 4),
                           "path": "tsfast_hip::linear_recurrence (the reference's log-doubling scan op) on this GPU"},
     )
     line["dtype"] = "f64"  # fp32 I/O, fp64 recurrence inside
-    kernels = {"fwd": ("linrec_fwd_lb look-back scan + transfer + reset", fwd_ms, fwd_b),
-               "bwd": ("linrec_bwd_lb look-back scan + transfer + reset + finish", bwd_ms, bwd_b)}
+    if n <= 4:
+        kernels = {"fwd": ("linrec_fwd_lb look-back scan + transfer + reset", fwd_ms, fwd_b),
+                   "bwd": ("linrec_bwd_lb look-back scan + transfer + reset + finish", bwd_ms, bwd_b)}
+    else:
+        kernels = {"fwd": ("lw_sum_fwd + lw_carry_fwd + lw_apply_fwd two-pass scan + lw_power", fwd_ms, fwd_b),
+                   "bwd": ("lw_sum_bwd + lw_carry_bwd + lw_apply_bwd two-pass scan + lw_power + finish", bwd_ms,
+                           bwd_b)}
     cpu = None
     if not args.no_cpu:
         def cpu_leg():
@@ -716,6 +729,8 @@ def main():
                     help="measure the fused dynoNet G-block (FIR + all-pole + input sum) at config 4's channels")
     ap.add_argument("--linrec", action="store_true",
                     help="measure the constant-matrix linear_recurrence on config 4's companion-matrix route")
+    ap.add_argument("--order", type=int, default=3,
+                    help="with --linrec: the denominator order n (state size 1..8; config 4 is 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument(
         "--copy-calibration",
@@ -774,8 +789,8 @@ def main():
     phase = max(kernels, key=lambda k: kernels[k][1])
     name, dom_ms, dom_b = kernels[phase]
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
-    key = (("selective", "f32") if args.selective else ("linrec", "f32") if args.linrec
-           else (args.config, args.io if args.config == 3 else "f32"))
+    key = (("selective", "f32") if args.selective else ("linrec", "f32") if args.linrec and args.order == 3
+           else None if args.linrec else (args.config, args.io if args.config == 3 else "f32"))
     measured = None if (args.conv or args.gblock) else MEASURED_TRAFFIC.get(key, {}).get(phase)
     line["roofline"] = {
         "bound": "hbm",

@@ -5,7 +5,8 @@ closed forms, torch float64 autograd through a sequential loop, and the diagonal
 all-pole special cases (tests/test_oracle.py). Shapes cover every state size n = 1..4 (chunks of
 32, 16, 10 and 8 steps), lane counts below, at and above one 64-lane tile row, sequences shorter
 than one chunk and than one super-chunk, ragged tails, many super-chunks (the look-back), and
-absent initial state. Bar: max relative error <= 1e-5 for x and every gradient (fp32 I/O, fp64
+absent initial state; n = 5..8 (the two-pass path) with one and many 256-step chunks, ragged
+last chunks and several lane blocks. Bar: max relative error <= 1e-5 for x and every gradient (fp32 I/O, fp64
 state). Matrices are scaled to spectral radius 0.97 so the states neither vanish nor blow up.
 """
 
@@ -49,6 +50,14 @@ _SHAPES = [
     (1, 20000, 1),  # one lane, a long look-back chain
     (33, 1, 2),  # L = 1
     (96, 5000, 2),
+    # n = 5..8: the two-pass path (chunks of 256 steps)
+    (5, 40, 5),
+    (70, 1000, 6),  # ragged last chunk, two lane blocks
+    (130, 777, 7),
+    (64, 600, 8),
+    (3, 1, 8),
+    (1, 5000, 5),  # one lane, 20 chunks of carry
+    (300, 256, 6),  # exactly one chunk
 ]
 
 
@@ -70,12 +79,13 @@ def test_linrec_matches_oracle(gpu, shape, with_x0):
         assert O.rel_err(_np(ts[2].grad), gx0) < TOL, "gx0"
 
 
-def test_linrec_empty_sequence(gpu):
-    A, _, x0, _ = _make(4, 1, 3, seed=3)
+@pytest.mark.parametrize("n", [3, 6])
+def test_linrec_empty_sequence(gpu, n):
+    A, _, x0, _ = _make(4, 1, n, seed=3)
     A, x0 = A.to(gpu).requires_grad_(), x0.to(gpu).requires_grad_()
-    v = torch.zeros(4, 0, 3, device=gpu, requires_grad=True)
+    v = torch.zeros(4, 0, n, device=gpu, requires_grad=True)
     x = linrec_hip.run(A, v, x0)
-    assert x.shape == (4, 0, 3)
+    assert x.shape == (4, 0, n)
     x.sum().backward()
     assert torch.count_nonzero(A.grad) == 0 and torch.count_nonzero(x0.grad) == 0
 
@@ -103,10 +113,11 @@ def test_linrec_dispatch_broadcast_and_doubling_scan(gpu):
     assert O.rel_err(_np(gA_hip), _np(gA_ref)) < TOL
 
 
-def test_linrec_companion_is_allpole(gpu):
+@pytest.mark.parametrize("na", [3, 6])
+def test_linrec_companion_is_allpole(gpu, na):
     """Companion matrices with input (w_t, 0, ..) give the all-pole filter (the reference's CPU
     route for dynoNet, allpole via linear_recurrence), matching the fused all-pole kernel."""
-    lanes, L, na = 100, 3000, 3
+    lanes, L = 100, 3000
     g = torch.Generator().manual_seed(8)
     r = torch.rand(lanes, na, generator=g) * 0.9
     a = torch.stack([torch.tensor(np.poly(ri.numpy())[1:], dtype=torch.float32) for ri in r]).to(gpu)
@@ -119,8 +130,8 @@ def test_linrec_companion_is_allpole(gpu):
 
 
 def test_linrec_supports_reasons(gpu):
-    A = torch.randn(2, 5, 5, device=gpu)
-    v = torch.randn(2, 10, 5, device=gpu)
+    A = torch.randn(2, 9, 9, device=gpu)
+    v = torch.randn(2, 10, 9, device=gpu)
     assert "state size" in linrec_hip.supports(A, v, None)
     assert "GPU-only" in linrec_hip.supports(A[:, :2, :2].cpu(), v[..., :2].cpu(), None)
     assert "float32" in linrec_hip.supports(A[:, :2, :2].double(), v[..., :2].double(), None)

@@ -7,8 +7,10 @@
 //
 // Layout: lanes are the flattened leading dims. A [lanes, n, n] row-major, v, x and g
 // [lanes, L, n] (per lane the n state components of a step are contiguous, steps follow each
-// other), x0 [lanes, n]. The state size n (1..4) is a template parameter, so a step is n x n
-// fp64 FMAs on registers.
+// other), x0 [lanes, n]. The state size n (1..8) is a template parameter, so a step is n x n
+// fp64 FMAs on registers. n = 1..4 take the single-pass look-back scan described next; n = 5..8,
+// whose n x n matrices and n-vectors do not fit that scan's registers and look-back areas, take
+// the two-pass path at the end of the file.
 //
 // A lane's sequence is one row of L * n floats, so a chunk of S = floor(32 / n) steps is a row
 // segment of S * n <= 32 floats, and the [64 x 33] LDS tiles of the all-pole scan move the
@@ -32,6 +34,7 @@ namespace {
 
 constexpr int kMaxNS = 4;  // state sizes on the single-pass path (an n x n fp64 matrix per thread)
 static_assert(kMaxNS <= kLbNA, "the look-back areas hold kLbNA doubles per lane");
+constexpr int kMaxWideNS = 8;  // state sizes 5..8 take the two-pass path below
 
 template <int NS>
 constexpr int steps_per_chunk() {
@@ -544,20 +547,315 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const flo
 
 #define TSF_NS_CASES(X) X(1) X(2) X(3) X(4)
 
+// ------------------------------------------------------------------------------ n = 5..8
+// Two-pass path for state sizes above the single-pass kernels' look-back areas. One thread per
+// lane and chunk of kWideT steps, no waiting between workgroups:
+//   forward:  chunk ends from a zero state (e) -> per lane, the entering state of every chunk by a
+//             sequential carry over the chunks with M = A^kWideT -> every chunk re-run from its
+//             entering state, writing x;
+//   backward: chunk starts of the adjoint from a zero right-end state (f) -> per lane, the adjoint
+//             entering every chunk from the right with M = (A^T)^kWideT, and grad_x0 -> every
+//             chunk re-run backwards, writing grad_v and its grad_A partial; linrec_finish adds the
+//             partials up in chunk order.
+// A stays fp32 in registers (exact in fp64 on use); state, carries and partials are fp64.
+constexpr int kWideT = 256;
+constexpr int kWideThreads = 256;
+
+template <int NS>
+TSF_DEV void load_matrix_f32(float (&m)[NS][NS], const float* __restrict__ A, int64_t lane) {
+  const float* a = A + lane * NS * NS;
+#pragma unroll
+  for (int r = 0; r < NS; ++r)
+#pragma unroll
+    for (int c = 0; c < NS; ++c) m[r][c] = a[r * NS + c];
+}
+
+// s <- m s + x (TR: m^T s + x), m fp32, s fp64
+template <int NS, bool TR>
+TSF_DEV void wide_step(const float (&m)[NS][NS], double (&s)[NS], const float* __restrict__ x) {
+  double t[NS];
+#pragma unroll
+  for (int r = 0; r < NS; ++r) {
+    double acc = (double)x[r];
+#pragma unroll
+    for (int c = 0; c < NS; ++c) acc = fma((double)(TR ? m[c][r] : m[r][c]), s[c], acc);
+    t[r] = acc;
+  }
+#pragma unroll
+  for (int r = 0; r < NS; ++r) s[r] = t[r];
+}
+
+// M = P^e per lane, P = A or A^T (binary powering in fp64)
+template <int NS>
+__global__ void __launch_bounds__(64) lw_power(const float* __restrict__ A, double* __restrict__ M, int64_t lanes,
+                                                int e, int transpose) {
+  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (lane >= lanes) return;
+  double B[NS][NS], R[NS][NS], T[NS][NS];
+  const float* a = A + lane * NS * NS;
+  for (int r = 0; r < NS; ++r)
+    for (int c = 0; c < NS; ++c) {
+      B[r][c] = (double)(transpose ? a[c * NS + r] : a[r * NS + c]);
+      R[r][c] = r == c ? 1.0 : 0.0;
+    }
+  auto mul = [&](double (&dst)[NS][NS], const double (&x)[NS][NS], const double (&y)[NS][NS]) {
+    for (int r = 0; r < NS; ++r)
+      for (int c = 0; c < NS; ++c) {
+        double acc = 0.0;
+        for (int j = 0; j < NS; ++j) acc = fma(x[r][j], y[j][c], acc);
+        T[r][c] = acc;
+      }
+    for (int r = 0; r < NS; ++r)
+      for (int c = 0; c < NS; ++c) dst[r][c] = T[r][c];
+  };
+  for (; e > 0; e >>= 1) {
+    if (e & 1) mul(R, R, B);
+    if (e > 1) mul(B, B, B);
+  }
+  for (int r = 0; r < NS; ++r)
+    for (int c = 0; c < NS; ++c) M[lane * NS * NS + r * NS + c] = R[r][c];
+}
+
+// Forward chunk ends from a zero state: e [nchunks][lanes][NS]
+template <int NS>
+__global__ void __launch_bounds__(kWideThreads) lw_sum_fwd(const float* __restrict__ A, const float* __restrict__ v,
+                                                           double* __restrict__ e, int64_t lanes, int64_t L) {
+  const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
+  if (lane >= lanes) return;
+  const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
+  float m[NS][NS];
+  load_matrix_f32<NS>(m, A, lane);
+  double s[NS];
+#pragma unroll
+  for (int r = 0; r < NS; ++r) s[r] = 0.0;
+  const float* row = v + lane * L * NS;
+  for (int64_t t = t0; t < t1; ++t) wide_step<NS, false>(m, s, row + t * NS);
+#pragma unroll
+  for (int r = 0; r < NS; ++r) e[(c * lanes + lane) * NS + r] = s[r];
+}
+
+// Entering state of every chunk: carry[c] = M carry[c-1] + e[c-1], carry[0] = x0 (or 0)
+template <int NS>
+__global__ void __launch_bounds__(64) lw_carry_fwd(const double* __restrict__ M, const float* __restrict__ x0,
+                                                    const double* __restrict__ e, double* __restrict__ carry,
+                                                    int64_t lanes, int64_t nchunks) {
+  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (lane >= lanes) return;
+  double m[NS][NS], s[NS];
+  for (int r = 0; r < NS; ++r) {
+    for (int c = 0; c < NS; ++c) m[r][c] = M[lane * NS * NS + r * NS + c];
+    s[r] = x0 ? (double)x0[lane * NS + r] : 0.0;
+  }
+  for (int64_t c = 0; c < nchunks; ++c) {
+    double t[NS];
+    for (int r = 0; r < NS; ++r) {
+      carry[(c * lanes + lane) * NS + r] = s[r];
+      double acc = e[(c * lanes + lane) * NS + r];
+      for (int j = 0; j < NS; ++j) acc = fma(m[r][j], s[j], acc);
+      t[r] = acc;
+    }
+    for (int r = 0; r < NS; ++r) s[r] = t[r];
+  }
+}
+
+// Every chunk re-run from its entering state, writing x
+template <int NS>
+__global__ void __launch_bounds__(kWideThreads) lw_apply_fwd(const float* __restrict__ A, const float* __restrict__ v,
+                                                             const double* __restrict__ carry, float* __restrict__ x,
+                                                             int64_t lanes, int64_t L) {
+  const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
+  if (lane >= lanes) return;
+  const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
+  float m[NS][NS];
+  load_matrix_f32<NS>(m, A, lane);
+  double s[NS];
+#pragma unroll
+  for (int r = 0; r < NS; ++r) s[r] = carry[(c * lanes + lane) * NS + r];
+  const float* row = v + lane * L * NS;
+  float* xrow = x + lane * L * NS;
+  for (int64_t t = t0; t < t1; ++t) {
+    wide_step<NS, false>(m, s, row + t * NS);
+#pragma unroll
+    for (int r = 0; r < NS; ++r) xrow[t * NS + r] = (float)s[r];
+  }
+}
+
+// Adjoint chunk starts from a zero right-end state: f [nchunks][lanes][NS]
+template <int NS>
+__global__ void __launch_bounds__(kWideThreads) lw_sum_bwd(const float* __restrict__ A, const float* __restrict__ g,
+                                                           double* __restrict__ f, int64_t lanes, int64_t L) {
+  const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
+  if (lane >= lanes) return;
+  const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
+  float m[NS][NS];
+  load_matrix_f32<NS>(m, A, lane);
+  double G[NS];
+#pragma unroll
+  for (int r = 0; r < NS; ++r) G[r] = 0.0;
+  const float* row = g + lane * L * NS;
+  for (int64_t t = t1 - 1; t >= t0; --t) wide_step<NS, true>(m, G, row + t * NS);
+#pragma unroll
+  for (int r = 0; r < NS; ++r) f[(c * lanes + lane) * NS + r] = G[r];
+}
+
+// Adjoint entering every chunk from the right: rc[c] = G at the first step of chunk c + 1 (zero
+// for the last chunk), rc[c-1] = f[c] + M rc[c]; then grad_x0 = A^T G_0 with G_0 = f[0] + M rc[0].
+template <int NS>
+__global__ void __launch_bounds__(64) lw_carry_bwd(const float* __restrict__ A, const double* __restrict__ M,
+                                                    const double* __restrict__ f, double* __restrict__ rc,
+                                                    float* __restrict__ gx0, int64_t lanes, int64_t nchunks) {
+  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (lane >= lanes) return;
+  double m[NS][NS], R[NS];
+  for (int r = 0; r < NS; ++r) {
+    for (int c = 0; c < NS; ++c) m[r][c] = M[lane * NS * NS + r * NS + c];
+    R[r] = 0.0;
+  }
+  for (int64_t c = nchunks - 1; c >= 0; --c) {
+    double t[NS];
+    for (int r = 0; r < NS; ++r) {
+      rc[(c * lanes + lane) * NS + r] = R[r];
+      double acc = f[(c * lanes + lane) * NS + r];
+      for (int j = 0; j < NS; ++j) acc = fma(m[r][j], R[j], acc);
+      t[r] = acc;
+    }
+    for (int r = 0; r < NS; ++r) R[r] = t[r];
+  }
+  if (gx0) {  // R now holds G_0; grad_x0 = A^T G_0
+    const float* a = A + lane * NS * NS;
+    for (int r = 0; r < NS; ++r) {
+      double acc = 0.0;
+      for (int j = 0; j < NS; ++j) acc = fma((double)a[j * NS + r], R[j], acc);
+      gx0[lane * NS + r] = (float)acc;
+    }
+  }
+}
+
+// Every chunk re-run backwards from its right-end adjoint, writing grad_v and the chunk's grad_A
+// partial sum_t G_t x_{t-1}^T (x_{-1} = x0 or 0) into part [nchunks][lanes][NS * NS]
+template <int NS>
+__global__ void __launch_bounds__(kWideThreads) lw_apply_bwd(const float* __restrict__ A, const float* __restrict__ g,
+                                                             const float* __restrict__ out, const float* __restrict__ x0,
+                                                             const double* __restrict__ rc, float* __restrict__ gv,
+                                                             double* __restrict__ part, int64_t lanes, int64_t L) {
+  const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
+  if (lane >= lanes) return;
+  const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
+  float m[NS][NS];
+  load_matrix_f32<NS>(m, A, lane);
+  double G[NS], acc[NS][NS];
+#pragma unroll
+  for (int r = 0; r < NS; ++r) {
+    G[r] = rc[(c * lanes + lane) * NS + r];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) acc[r][q] = 0.0;
+  }
+  const float* grow = g + lane * L * NS;
+  const float* xrow = out + lane * L * NS;
+  float* gvrow = gv + lane * L * NS;
+  for (int64_t t = t1 - 1; t >= t0; --t) {
+    wide_step<NS, true>(m, G, grow + t * NS);
+    float xp[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      xp[q] = t > 0 ? xrow[(t - 1) * NS + q] : (x0 ? x0[lane * NS + q] : 0.0f);
+      gvrow[t * NS + q] = (float)G[q];
+    }
+#pragma unroll
+    for (int r = 0; r < NS; ++r)
+#pragma unroll
+      for (int q = 0; q < NS; ++q) acc[r][q] = fma(G[r], (double)xp[q], acc[r][q]);
+  }
+#pragma unroll
+  for (int r = 0; r < NS; ++r)
+#pragma unroll
+    for (int q = 0; q < NS; ++q) part[(c * lanes + lane) * NS * NS + r * NS + q] = acc[r][q];
+}
+
+// Workspace of the two-pass path: e/f and the carries [nchunks][lanes][n], M [lanes][n][n], and
+// the grad_A partials [nchunks][lanes][n][n] (fp64).
+struct LwPlan {
+  int64_t nchunks = 0;
+  size_t off_e = 0, off_carry = 0, off_M = 0, off_part = 0, bytes = 0;
+};
+
+LwPlan lw_plan(int64_t lanes, int64_t L, int64_t ns) {
+  LwPlan p;
+  p.nchunks = (L + kWideT - 1) / kWideT;
+  const size_t f = 8, vecs = f * p.nchunks * lanes * ns;
+  p.off_e = 0;
+  p.off_carry = vecs;
+  p.off_M = 2 * vecs;
+  p.off_part = p.off_M + f * lanes * ns * ns;
+  p.bytes = p.off_part + vecs * ns;
+  return p;
+}
+
+inline bool lw_grid_fits(int64_t lanes, int64_t L) {
+  return (L + kWideT - 1) / kWideT <= 65535 && (lanes + kWideThreads - 1) / kWideThreads <= INT32_MAX;
+}
+
+template <int NS>
+int wide_fwd_impl(int64_t lanes, int64_t L, const float* A, const float* v, const float* x0, float* x, char* ws,
+                  hipStream_t s) {
+  const LwPlan p = lw_plan(lanes, L, NS);
+  double* e = reinterpret_cast<double*>(ws + p.off_e);
+  double* carry = reinterpret_cast<double*>(ws + p.off_carry);
+  double* M = reinterpret_cast<double*>(ws + p.off_M);
+  const dim3 grid((unsigned)((lanes + kWideThreads - 1) / kWideThreads), (unsigned)p.nchunks);
+  const unsigned lb = (unsigned)((lanes + 63) / 64);
+  hipLaunchKernelGGL((lw_power<NS>), dim3(lb), dim3(64), 0, s, A, M, lanes, kWideT, 0);
+  hipLaunchKernelGGL((lw_sum_fwd<NS>), grid, dim3(kWideThreads), 0, s, A, v, e, lanes, L);
+  hipLaunchKernelGGL((lw_carry_fwd<NS>), dim3(lb), dim3(64), 0, s, (const double*)M, x0, (const double*)e, carry,
+                     lanes, p.nchunks);
+  hipLaunchKernelGGL((lw_apply_fwd<NS>), grid, dim3(kWideThreads), 0, s, A, v, (const double*)carry, x, lanes, L);
+  return tsf_launch_status();
+}
+
+template <int NS>
+int wide_bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const float* out, const float* x0,
+                  float* gA, float* gv, float* gx0, char* ws, hipStream_t s) {
+  if (L == 0) {
+    hipLaunchKernelGGL(linrec_zero, dim3(blocks_for(lanes * NS * NS)), dim3(256), 0, s, gA, lanes * NS * NS);
+    if (gx0) hipLaunchKernelGGL(linrec_zero, dim3(blocks_for(lanes * NS)), dim3(256), 0, s, gx0, lanes * NS);
+    return tsf_launch_status();
+  }
+  const LwPlan p = lw_plan(lanes, L, NS);
+  double* f = reinterpret_cast<double*>(ws + p.off_e);
+  double* rc = reinterpret_cast<double*>(ws + p.off_carry);
+  double* M = reinterpret_cast<double*>(ws + p.off_M);
+  double* part = reinterpret_cast<double*>(ws + p.off_part);
+  const dim3 grid((unsigned)((lanes + kWideThreads - 1) / kWideThreads), (unsigned)p.nchunks);
+  const unsigned lb = (unsigned)((lanes + 63) / 64);
+  hipLaunchKernelGGL((lw_power<NS>), dim3(lb), dim3(64), 0, s, A, M, lanes, kWideT, 1);
+  hipLaunchKernelGGL((lw_sum_bwd<NS>), grid, dim3(kWideThreads), 0, s, A, g, f, lanes, L);
+  hipLaunchKernelGGL((lw_carry_bwd<NS>), dim3(lb), dim3(64), 0, s, A, (const double*)M, (const double*)f, rc, gx0,
+                     lanes, p.nchunks);
+  hipLaunchKernelGGL((lw_apply_bwd<NS>), grid, dim3(kWideThreads), 0, s, A, g, out, x0, (const double*)rc, gv, part,
+                     lanes, L);
+  hipLaunchKernelGGL(linrec_finish, dim3((unsigned)((lanes * NS * NS + 63) / 64)), dim3(1024), 0, s,
+                     (const double*)part, gA, lanes * NS * NS, p.nchunks);
+  return tsf_launch_status();
+}
+
+#define TSF_WIDE_CASES(X) X(5) X(6) X(7) X(8)
+
 }  // namespace
 
 extern "C" {
 
 int64_t tsfast_hip_linrec_workspace_bytes(int64_t lanes, int64_t L, int64_t n) {
-  if (lanes < 0 || L < 0 || n < 1 || n > kMaxNS) return -1;
+  if (lanes < 0 || L < 0 || n < 1 || n > kMaxWideNS) return -1;
+  if (n > kMaxNS) return (int64_t)lw_plan(lanes, L, n).bytes;
   return (int64_t)lr_plan(lanes, L, n).bytes;
 }
 
 int tsfast_hip_linrec_fwd(int64_t lanes, int64_t L, int64_t n, const float* A, const float* v, const float* x0,
                           float* x, void* workspace, int64_t workspace_bytes, void* stream) {
   if (lanes < 0 || L < 0) return TSF_ERR_ARG;
-  if (n < 1 || n > kMaxNS) return TSF_ERR_UNSUPPORTED;
+  if (n < 1 || n > kMaxWideNS) return TSF_ERR_UNSUPPORTED;
   if (lanes == 0 || L == 0) return TSF_OK;
+  if (n > kMaxNS && !lw_grid_fits(lanes, L)) return TSF_ERR_UNSUPPORTED;
   if (!A || !v || !x) return TSF_ERR_ARG;
   if (!workspace || workspace_bytes < tsfast_hip_linrec_workspace_bytes(lanes, L, n)) return TSF_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -568,6 +866,11 @@ int tsfast_hip_linrec_fwd(int64_t lanes, int64_t L, int64_t n, const float* A, c
     return fwd_impl<K>(lanes, L, A, v, x0, x, ws, s);
     TSF_NS_CASES(X)
 #undef X
+#define X(K) \
+  case K:    \
+    return wide_fwd_impl<K>(lanes, L, A, v, x0, x, ws, s);
+    TSF_WIDE_CASES(X)
+#undef X
   }
   return TSF_ERR_UNSUPPORTED;
 }
@@ -576,8 +879,9 @@ int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, c
                           const float* x0, float* gA, float* gv, float* gx0, void* workspace, int64_t workspace_bytes,
                           void* stream) {
   if (lanes < 0 || L < 0) return TSF_ERR_ARG;
-  if (n < 1 || n > kMaxNS) return TSF_ERR_UNSUPPORTED;
+  if (n < 1 || n > kMaxWideNS) return TSF_ERR_UNSUPPORTED;
   if (lanes == 0) return TSF_OK;
+  if (n > kMaxNS && !lw_grid_fits(lanes, L)) return TSF_ERR_UNSUPPORTED;
   if (!A || !gA || (L > 0 && (!g || !out || !gv))) return TSF_ERR_ARG;
   if (x0 && !gx0) return TSF_ERR_ARG;
   if (!workspace || workspace_bytes < tsfast_hip_linrec_workspace_bytes(lanes, L, n)) return TSF_ERR_WORKSPACE;
@@ -588,6 +892,11 @@ int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, c
   case K:    \
     return bwd_impl<K>(lanes, L, g, A, out, x0, gA, gv, gx0, ws, s);
     TSF_NS_CASES(X)
+#undef X
+#define X(K) \
+  case K:    \
+    return wide_bwd_impl<K>(lanes, L, g, A, out, x0, gA, gv, gx0, ws, s);
+    TSF_WIDE_CASES(X)
 #undef X
   }
   return TSF_ERR_UNSUPPORTED;

@@ -10,7 +10,7 @@ and writes the states once. ``supports(A, v, x0)`` and ``run(A, v, x0) -> x``, d
 
 Shapes follow the reference: ``A [..., n, n]``, ``v [..., L, n]``, ``x0 [..., n]`` with common
 leading dims (``linear_recurrence`` broadcasts them first); states ``x_1 .. x_L`` as ``[..., L, n]``.
-float32, ``1 <= n <= 4``.
+float32, ``1 <= n <= 8`` (``n <= 4`` a single-pass look-back scan, ``5..8`` a two-pass scan).
 """
 
 from __future__ import annotations
@@ -23,7 +23,8 @@ import torch
 
 from .. import _lib
 
-_MAX_N = 4
+_MAX_N = 8
+_MAX_WIDE_L = 65535 * 256  # two-pass path (n > 4): chunks of 256 steps, one grid row each
 
 
 def supports(A: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> str | None:
@@ -39,6 +40,8 @@ def supports(A: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> str |
     n = v.shape[-1]
     if not 1 <= n <= _MAX_N:
         return f"state size n={n} outside the supported range [1, {_MAX_N}]"
+    if n > 4 and v.shape[-2] > _MAX_WIDE_L:
+        return f"sequence length {v.shape[-2]} above {_MAX_WIDE_L} for n > 4"
     lead = v.shape[:-2]
     if tuple(A.shape) != tuple(lead) + (n, n):
         return f"A.shape {tuple(A.shape)} != {tuple(lead) + (n, n)}"
