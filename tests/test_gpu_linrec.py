@@ -135,3 +135,26 @@ def test_linrec_supports_reasons(gpu):
     assert "state size" in linrec_hip.supports(A, v, None)
     assert "GPU-only" in linrec_hip.supports(A[:, :2, :2].cpu(), v[..., :2].cpu(), None)
     assert "float32" in linrec_hip.supports(A[:, :2, :2].double(), v[..., :2].double(), None)
+
+
+@pytest.mark.parametrize("n", [6, 8])
+def test_linrec_wide_misaligned_rows(gpu, n):
+    """n = 5..8 read and write whole steps as float4 / float2 when every row pointer allows it;
+    inputs that start 4 bytes into a buffer take the per-float path and give the same result."""
+    M, L = 40, 700
+    A, v, x0, gx = _make(M, L, n, seed=11 + n)
+    buf = torch.empty(1 + M * L * n, device=gpu)
+    v_mis = buf[1:].view(M, L, n)
+    v_mis.copy_(v.to(gpu))
+    assert v_mis.data_ptr() % 8 != 0
+    ts = [A.to(gpu).requires_grad_(), v_mis.requires_grad_(), x0.to(gpu).requires_grad_()]
+    x = linrec_hip.run(*ts)
+    want = O.linrec_forward(_np(A), _np(v), _np(x0))
+    assert O.rel_err(_np(x), want) < TOL
+    gbuf = torch.empty(1 + M * L * n, device=gpu)
+    g_mis = gbuf[1:].view(M, L, n)
+    g_mis.copy_(gx.to(gpu))
+    x.backward(g_mis)
+    gA, gv, gx0 = O.linrec_backward(_np(gx), _np(A), want, _np(x0))
+    assert O.rel_err(_np(ts[0].grad), gA) < TOL and O.rel_err(_np(ts[1].grad), gv) < TOL
+    assert O.rel_err(_np(ts[2].grad), gx0) < TOL

@@ -23,6 +23,8 @@
 //
 // Arithmetic: fp32 in and out, fp64 state, transfer matrices, published words and grad_A sums.
 
+#include <initializer_list>
+
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -585,6 +587,42 @@ TSF_DEV void wide_step(const float (&m)[NS][NS], double (&s)[NS], const float* _
   for (int r = 0; r < NS; ++r) s[r] = t[r];
 }
 
+// One step's NS floats of a lane's row, VEC floats per access (VEC divides NS; the host picks
+// VEC = 4 or 2 only when every row pointer is aligned to it).
+template <int NS, int VEC>
+TSF_DEV void ld_step(float (&d)[NS], const float* __restrict__ p) {
+  if constexpr (VEC == 4) {
+#pragma unroll
+    for (int i = 0; i < NS; i += 4) {
+      const float4 q = *reinterpret_cast<const float4*>(p + i);
+      d[i] = q.x; d[i + 1] = q.y; d[i + 2] = q.z; d[i + 3] = q.w;
+    }
+  } else if constexpr (VEC == 2) {
+#pragma unroll
+    for (int i = 0; i < NS; i += 2) {
+      const float2 q = *reinterpret_cast<const float2*>(p + i);
+      d[i] = q.x; d[i + 1] = q.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) d[i] = p[i];
+  }
+}
+template <int NS, int VEC>
+TSF_DEV void st_step(float* __restrict__ p, const double (&s)[NS]) {
+  if constexpr (VEC == 4) {
+#pragma unroll
+    for (int i = 0; i < NS; i += 4)
+      *reinterpret_cast<float4*>(p + i) = make_float4((float)s[i], (float)s[i + 1], (float)s[i + 2], (float)s[i + 3]);
+  } else if constexpr (VEC == 2) {
+#pragma unroll
+    for (int i = 0; i < NS; i += 2) *reinterpret_cast<float2*>(p + i) = make_float2((float)s[i], (float)s[i + 1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) p[i] = (float)s[i];
+  }
+}
+
 // M = P^e per lane, P = A or A^T (binary powering in fp64)
 template <int NS>
 __global__ void __launch_bounds__(64) lw_power(const float* __restrict__ A, double* __restrict__ M, int64_t lanes,
@@ -617,7 +655,7 @@ __global__ void __launch_bounds__(64) lw_power(const float* __restrict__ A, doub
 }
 
 // Forward chunk ends from a zero state: e [nchunks][lanes][NS]
-template <int NS>
+template <int NS, int VEC>
 __global__ void __launch_bounds__(kWideThreads) lw_sum_fwd(const float* __restrict__ A, const float* __restrict__ v,
                                                            double* __restrict__ e, int64_t lanes, int64_t L) {
   const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
@@ -629,7 +667,11 @@ __global__ void __launch_bounds__(kWideThreads) lw_sum_fwd(const float* __restri
 #pragma unroll
   for (int r = 0; r < NS; ++r) s[r] = 0.0;
   const float* row = v + lane * L * NS;
-  for (int64_t t = t0; t < t1; ++t) wide_step<NS, false>(m, s, row + t * NS);
+  for (int64_t t = t0; t < t1; ++t) {
+    float d[NS];
+    ld_step<NS, VEC>(d, row + t * NS);
+    wide_step<NS, false>(m, s, d);
+  }
 #pragma unroll
   for (int r = 0; r < NS; ++r) e[(c * lanes + lane) * NS + r] = s[r];
 }
@@ -659,7 +701,7 @@ __global__ void __launch_bounds__(64) lw_carry_fwd(const double* __restrict__ M,
 }
 
 // Every chunk re-run from its entering state, writing x
-template <int NS>
+template <int NS, int VEC>
 __global__ void __launch_bounds__(kWideThreads) lw_apply_fwd(const float* __restrict__ A, const float* __restrict__ v,
                                                              const double* __restrict__ carry, float* __restrict__ x,
                                                              int64_t lanes, int64_t L) {
@@ -674,14 +716,15 @@ __global__ void __launch_bounds__(kWideThreads) lw_apply_fwd(const float* __rest
   const float* row = v + lane * L * NS;
   float* xrow = x + lane * L * NS;
   for (int64_t t = t0; t < t1; ++t) {
-    wide_step<NS, false>(m, s, row + t * NS);
-#pragma unroll
-    for (int r = 0; r < NS; ++r) xrow[t * NS + r] = (float)s[r];
+    float d[NS];
+    ld_step<NS, VEC>(d, row + t * NS);
+    wide_step<NS, false>(m, s, d);
+    st_step<NS, VEC>(xrow + t * NS, s);
   }
 }
 
 // Adjoint chunk starts from a zero right-end state: f [nchunks][lanes][NS]
-template <int NS>
+template <int NS, int VEC>
 __global__ void __launch_bounds__(kWideThreads) lw_sum_bwd(const float* __restrict__ A, const float* __restrict__ g,
                                                            double* __restrict__ f, int64_t lanes, int64_t L) {
   const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
@@ -693,7 +736,11 @@ __global__ void __launch_bounds__(kWideThreads) lw_sum_bwd(const float* __restri
 #pragma unroll
   for (int r = 0; r < NS; ++r) G[r] = 0.0;
   const float* row = g + lane * L * NS;
-  for (int64_t t = t1 - 1; t >= t0; --t) wide_step<NS, true>(m, G, row + t * NS);
+  for (int64_t t = t1 - 1; t >= t0; --t) {
+    float d[NS];
+    ld_step<NS, VEC>(d, row + t * NS);
+    wide_step<NS, true>(m, G, d);
+  }
 #pragma unroll
   for (int r = 0; r < NS; ++r) f[(c * lanes + lane) * NS + r] = G[r];
 }
@@ -733,7 +780,7 @@ __global__ void __launch_bounds__(64) lw_carry_bwd(const float* __restrict__ A, 
 
 // Every chunk re-run backwards from its right-end adjoint, writing grad_v and the chunk's grad_A
 // partial sum_t G_t x_{t-1}^T (x_{-1} = x0 or 0) into part [nchunks][lanes][NS * NS]
-template <int NS>
+template <int NS, int VEC>
 __global__ void __launch_bounds__(kWideThreads) lw_apply_bwd(const float* __restrict__ A, const float* __restrict__ g,
                                                              const float* __restrict__ out, const float* __restrict__ x0,
                                                              const double* __restrict__ rc, float* __restrict__ gv,
@@ -754,12 +801,15 @@ __global__ void __launch_bounds__(kWideThreads) lw_apply_bwd(const float* __rest
   const float* xrow = out + lane * L * NS;
   float* gvrow = gv + lane * L * NS;
   for (int64_t t = t1 - 1; t >= t0; --t) {
-    wide_step<NS, true>(m, G, grow + t * NS);
-    float xp[NS];
+    float d[NS], xp[NS];
+    ld_step<NS, VEC>(d, grow + t * NS);
+    wide_step<NS, true>(m, G, d);
+    st_step<NS, VEC>(gvrow + t * NS, G);
+    if (t > 0) {
+      ld_step<NS, VEC>(xp, xrow + (t - 1) * NS);
+    } else {
 #pragma unroll
-    for (int q = 0; q < NS; ++q) {
-      xp[q] = t > 0 ? xrow[(t - 1) * NS + q] : (x0 ? x0[lane * NS + q] : 0.0f);
-      gvrow[t * NS + q] = (float)G[q];
+      for (int q = 0; q < NS; ++q) xp[q] = x0 ? x0[lane * NS + q] : 0.0f;
     }
 #pragma unroll
     for (int r = 0; r < NS; ++r)
@@ -795,7 +845,7 @@ inline bool lw_grid_fits(int64_t lanes, int64_t L) {
   return (L + kWideT - 1) / kWideT <= 65535 && (lanes + kWideThreads - 1) / kWideThreads <= INT32_MAX;
 }
 
-template <int NS>
+template <int NS, int VEC>
 int wide_fwd_impl(int64_t lanes, int64_t L, const float* A, const float* v, const float* x0, float* x, char* ws,
                   hipStream_t s) {
   const LwPlan p = lw_plan(lanes, L, NS);
@@ -805,14 +855,14 @@ int wide_fwd_impl(int64_t lanes, int64_t L, const float* A, const float* v, cons
   const dim3 grid((unsigned)((lanes + kWideThreads - 1) / kWideThreads), (unsigned)p.nchunks);
   const unsigned lb = (unsigned)((lanes + 63) / 64);
   hipLaunchKernelGGL((lw_power<NS>), dim3(lb), dim3(64), 0, s, A, M, lanes, kWideT, 0);
-  hipLaunchKernelGGL((lw_sum_fwd<NS>), grid, dim3(kWideThreads), 0, s, A, v, e, lanes, L);
+  hipLaunchKernelGGL((lw_sum_fwd<NS, VEC>), grid, dim3(kWideThreads), 0, s, A, v, e, lanes, L);
   hipLaunchKernelGGL((lw_carry_fwd<NS>), dim3(lb), dim3(64), 0, s, (const double*)M, x0, (const double*)e, carry,
                      lanes, p.nchunks);
-  hipLaunchKernelGGL((lw_apply_fwd<NS>), grid, dim3(kWideThreads), 0, s, A, v, (const double*)carry, x, lanes, L);
+  hipLaunchKernelGGL((lw_apply_fwd<NS, VEC>), grid, dim3(kWideThreads), 0, s, A, v, (const double*)carry, x, lanes, L);
   return tsf_launch_status();
 }
 
-template <int NS>
+template <int NS, int VEC>
 int wide_bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const float* out, const float* x0,
                   float* gA, float* gv, float* gx0, char* ws, hipStream_t s) {
   if (L == 0) {
@@ -828,14 +878,45 @@ int wide_bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, cons
   const dim3 grid((unsigned)((lanes + kWideThreads - 1) / kWideThreads), (unsigned)p.nchunks);
   const unsigned lb = (unsigned)((lanes + 63) / 64);
   hipLaunchKernelGGL((lw_power<NS>), dim3(lb), dim3(64), 0, s, A, M, lanes, kWideT, 1);
-  hipLaunchKernelGGL((lw_sum_bwd<NS>), grid, dim3(kWideThreads), 0, s, A, g, f, lanes, L);
+  hipLaunchKernelGGL((lw_sum_bwd<NS, VEC>), grid, dim3(kWideThreads), 0, s, A, g, f, lanes, L);
   hipLaunchKernelGGL((lw_carry_bwd<NS>), dim3(lb), dim3(64), 0, s, A, (const double*)M, (const double*)f, rc, gx0,
                      lanes, p.nchunks);
-  hipLaunchKernelGGL((lw_apply_bwd<NS>), grid, dim3(kWideThreads), 0, s, A, g, out, x0, (const double*)rc, gv, part,
+  hipLaunchKernelGGL((lw_apply_bwd<NS, VEC>), grid, dim3(kWideThreads), 0, s, A, g, out, x0, (const double*)rc, gv, part,
                      lanes, L);
   hipLaunchKernelGGL(linrec_finish, dim3((unsigned)((lanes * NS * NS + 63) / 64)), dim3(1024), 0, s,
                      (const double*)part, gA, lanes * NS * NS, p.nchunks);
   return tsf_launch_status();
+}
+
+// Widest access every row pointer allows: rows start at multiples of NS floats.
+template <int NS>
+int wide_vec(std::initializer_list<const void*> ptrs) {
+  auto aligned = [&](uintptr_t a) {
+    for (const void* p : ptrs)
+      if (p && (reinterpret_cast<uintptr_t>(p) % a) != 0) return false;
+    return true;
+  };
+  if (NS % 4 == 0 && aligned(16)) return 4;
+  if (NS % 2 == 0 && aligned(8)) return 2;
+  return 1;
+}
+template <int NS>
+int wide_fwd(int64_t lanes, int64_t L, const float* A, const float* v, const float* x0, float* x, char* ws,
+             hipStream_t s) {
+  switch (wide_vec<NS>({v, x})) {
+    case 4: return wide_fwd_impl<NS, (NS % 4 == 0 ? 4 : 1)>(lanes, L, A, v, x0, x, ws, s);
+    case 2: return wide_fwd_impl<NS, (NS % 2 == 0 ? 2 : 1)>(lanes, L, A, v, x0, x, ws, s);
+    default: return wide_fwd_impl<NS, 1>(lanes, L, A, v, x0, x, ws, s);
+  }
+}
+template <int NS>
+int wide_bwd(int64_t lanes, int64_t L, const float* g, const float* A, const float* out, const float* x0, float* gA,
+             float* gv, float* gx0, char* ws, hipStream_t s) {
+  switch (wide_vec<NS>({g, out, gv})) {
+    case 4: return wide_bwd_impl<NS, (NS % 4 == 0 ? 4 : 1)>(lanes, L, g, A, out, x0, gA, gv, gx0, ws, s);
+    case 2: return wide_bwd_impl<NS, (NS % 2 == 0 ? 2 : 1)>(lanes, L, g, A, out, x0, gA, gv, gx0, ws, s);
+    default: return wide_bwd_impl<NS, 1>(lanes, L, g, A, out, x0, gA, gv, gx0, ws, s);
+  }
 }
 
 #define TSF_WIDE_CASES(X) X(5) X(6) X(7) X(8)
@@ -868,7 +949,7 @@ int tsfast_hip_linrec_fwd(int64_t lanes, int64_t L, int64_t n, const float* A, c
 #undef X
 #define X(K) \
   case K:    \
-    return wide_fwd_impl<K>(lanes, L, A, v, x0, x, ws, s);
+    return wide_fwd<K>(lanes, L, A, v, x0, x, ws, s);
     TSF_WIDE_CASES(X)
 #undef X
   }
@@ -895,7 +976,7 @@ int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, c
 #undef X
 #define X(K) \
   case K:    \
-    return wide_bwd_impl<K>(lanes, L, g, A, out, x0, gA, gv, gx0, ws, s);
+    return wide_bwd<K>(lanes, L, g, A, out, x0, gA, gv, gx0, ws, s);
     TSF_WIDE_CASES(X)
 #undef X
   }
