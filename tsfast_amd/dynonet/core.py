@@ -2,7 +2,8 @@
 
 Mirrors ``tsfast/models/architectures/dynonet/core.py``: ``linear_recurrence`` (the log-doubling
 scan ``x_t = A x_{t-1} + v_t`` with its analytic matrix adjoint, ``:23-127``; on GPU the
-``"hip"`` family's single-pass scan serves it for state sizes n <= 4) and the all-pole
+``"hip"`` family serves it for state sizes n <= 8: a single-pass scan for n <= 4, a two-pass
+scan above) and the all-pole
 branch of ``LinearDynamicalOperator.forward`` (``:221-248``): the fused backend when one serves
 the inputs (``_fused_allpole``, ``:91-100``; here the ``"hip"`` family for ``"cuda"`` tensors),
 else ``linear_recurrence`` over the companion matrices.
