@@ -561,6 +561,7 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const flo
 //             partials up in chunk order.
 // A stays fp32 in registers (exact in fp64 on use); state, carries and partials are fp64.
 constexpr int kWideT = 256;
+constexpr int kWidePf = 4;  // steps fetched ahead by the chunk kernels
 constexpr int kWideThreads = 256;
 
 template <int NS>
@@ -667,10 +668,20 @@ __global__ void __launch_bounds__(kWideThreads) lw_sum_fwd(const float* __restri
 #pragma unroll
   for (int r = 0; r < NS; ++r) s[r] = 0.0;
   const float* row = v + lane * L * NS;
-  for (int64_t t = t0; t < t1; ++t) {
-    float d[NS];
-    ld_step<NS, VEC>(d, row + t * NS);
-    wide_step<NS, false>(m, s, d);
+  // kWidePf steps' loads in flight: step t + kWidePf is fetched while step t computes
+  float d[kWidePf][NS];
+#pragma unroll
+  for (int k = 0; k < kWidePf; ++k)
+    if (t0 + k < t1) ld_step<NS, VEC>(d[k], row + (t0 + k) * NS);
+  for (int64_t tb = t0; tb < t1; tb += kWidePf) {
+#pragma unroll
+    for (int k = 0; k < kWidePf; ++k) {
+      const int64_t t = tb + k;
+      if (t < t1) {
+        wide_step<NS, false>(m, s, d[k]);
+        if (t + kWidePf < t1) ld_step<NS, VEC>(d[k], row + (t + kWidePf) * NS);
+      }
+    }
   }
 #pragma unroll
   for (int r = 0; r < NS; ++r) e[(c * lanes + lane) * NS + r] = s[r];
@@ -715,11 +726,20 @@ __global__ void __launch_bounds__(kWideThreads) lw_apply_fwd(const float* __rest
   for (int r = 0; r < NS; ++r) s[r] = carry[(c * lanes + lane) * NS + r];
   const float* row = v + lane * L * NS;
   float* xrow = x + lane * L * NS;
-  for (int64_t t = t0; t < t1; ++t) {
-    float d[NS];
-    ld_step<NS, VEC>(d, row + t * NS);
-    wide_step<NS, false>(m, s, d);
-    st_step<NS, VEC>(xrow + t * NS, s);
+  float d[kWidePf][NS];
+#pragma unroll
+  for (int k = 0; k < kWidePf; ++k)
+    if (t0 + k < t1) ld_step<NS, VEC>(d[k], row + (t0 + k) * NS);
+  for (int64_t tb = t0; tb < t1; tb += kWidePf) {
+#pragma unroll
+    for (int k = 0; k < kWidePf; ++k) {
+      const int64_t t = tb + k;
+      if (t < t1) {
+        wide_step<NS, false>(m, s, d[k]);
+        st_step<NS, VEC>(xrow + t * NS, s);
+        if (t + kWidePf < t1) ld_step<NS, VEC>(d[k], row + (t + kWidePf) * NS);
+      }
+    }
   }
 }
 
@@ -736,10 +756,19 @@ __global__ void __launch_bounds__(kWideThreads) lw_sum_bwd(const float* __restri
 #pragma unroll
   for (int r = 0; r < NS; ++r) G[r] = 0.0;
   const float* row = g + lane * L * NS;
-  for (int64_t t = t1 - 1; t >= t0; --t) {
-    float d[NS];
-    ld_step<NS, VEC>(d, row + t * NS);
-    wide_step<NS, true>(m, G, d);
+  float d[kWidePf][NS];
+#pragma unroll
+  for (int k = 0; k < kWidePf; ++k)
+    if (t1 - 1 - k >= t0) ld_step<NS, VEC>(d[k], row + (t1 - 1 - k) * NS);
+  for (int64_t tb = t1 - 1; tb >= t0; tb -= kWidePf) {
+#pragma unroll
+    for (int k = 0; k < kWidePf; ++k) {
+      const int64_t t = tb - k;
+      if (t >= t0) {
+        wide_step<NS, true>(m, G, d[k]);
+        if (t - kWidePf >= t0) ld_step<NS, VEC>(d[k], row + (t - kWidePf) * NS);
+      }
+    }
   }
 #pragma unroll
   for (int r = 0; r < NS; ++r) f[(c * lanes + lane) * NS + r] = G[r];
