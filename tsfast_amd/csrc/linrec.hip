@@ -829,17 +829,32 @@ __global__ void __launch_bounds__(kWideThreads) lw_apply_bwd(const float* __rest
   const float* grow = g + lane * L * NS;
   const float* xrow = out + lane * L * NS;
   float* gvrow = gv + lane * L * NS;
-  for (int64_t t = t1 - 1; t >= t0; --t) {
-    float d[NS], xp[NS];
-    ld_step<NS, VEC>(d, grow + t * NS);
-    wide_step<NS, true>(m, G, d);
-    st_step<NS, VEC>(gvrow + t * NS, G);
+  // g_t and x_{t-1} of the next kPfB steps are fetched while step t computes
+  constexpr int kPfB = 2;
+  float dg[kPfB][NS], dx[kPfB][NS];
+  auto fetch = [&](int k, int64_t t) __attribute__((always_inline)) {
+    ld_step<NS, VEC>(dg[k], grow + t * NS);
     if (t > 0) {
-      ld_step<NS, VEC>(xp, xrow + (t - 1) * NS);
+      ld_step<NS, VEC>(dx[k], xrow + (t - 1) * NS);
     } else {
 #pragma unroll
-      for (int q = 0; q < NS; ++q) xp[q] = x0 ? x0[lane * NS + q] : 0.0f;
+      for (int q = 0; q < NS; ++q) dx[k][q] = x0 ? x0[lane * NS + q] : 0.0f;
     }
+  };
+#pragma unroll
+  for (int k = 0; k < kPfB; ++k)
+    if (t1 - 1 - k >= t0) fetch(k, t1 - 1 - k);
+  for (int64_t tb = t1 - 1; tb >= t0; tb -= kPfB)
+#pragma unroll
+  for (int k = 0; k < kPfB; ++k) {
+    const int64_t t = tb - k;
+    if (t < t0) break;
+    float xp[NS];
+    wide_step<NS, true>(m, G, dg[k]);
+    st_step<NS, VEC>(gvrow + t * NS, G);
+#pragma unroll
+    for (int q = 0; q < NS; ++q) xp[q] = dx[k][q];
+    if (t - kPfB >= t0) fetch(k, t - kPfB);
 #pragma unroll
     for (int r = 0; r < NS; ++r)
 #pragma unroll
