@@ -711,35 +711,62 @@ __global__ void __launch_bounds__(64) lw_carry_fwd(const double* __restrict__ M,
   }
 }
 
-// Every chunk re-run from its entering state, writing x
+// Steps per output sub-block of the re-run kernels: a multiple of kWidePf whose NS-float steps fill
+// at most 64 floats, so one lane's sub-block is one contiguous row segment of <= 256 bytes.
+template <int NS>
+constexpr int wide_out_sb() {
+  return kWidePf * (64 / (kWidePf * NS));
+}
+
+// Every chunk re-run from its entering state, writing x. Each thread leaves its outputs in its
+// LDS row; every wave then writes its 64 lanes' row segments with whole-segment (coalesced)
+// stores, one lane at a time, so HBM sees full lines instead of one step per lane per store.
 template <int NS, int VEC>
 __global__ void __launch_bounds__(kWideThreads) lw_apply_fwd(const float* __restrict__ A, const float* __restrict__ v,
                                                              const double* __restrict__ carry, float* __restrict__ x,
                                                              int64_t lanes, int64_t L) {
-  const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
-  if (lane >= lanes) return;
+  constexpr int SB = wide_out_sb<NS>();
+  __shared__ float s_o[kWideThreads][SB * NS + 1];
+  const int tid = threadIdx.x, wl = tid & 63, w0 = tid & ~63;
+  const int64_t l0 = blockIdx.x * (int64_t)kWideThreads, lane = l0 + tid;
+  const bool live = lane < lanes;
   const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
   float m[NS][NS];
-  load_matrix_f32<NS>(m, A, lane);
   double s[NS];
-#pragma unroll
-  for (int r = 0; r < NS; ++r) s[r] = carry[(c * lanes + lane) * NS + r];
-  const float* row = v + lane * L * NS;
-  float* xrow = x + lane * L * NS;
   float d[kWidePf][NS];
+  const float* row = v + (live ? lane : 0) * L * NS;
+  if (live) {
+    load_matrix_f32<NS>(m, A, lane);
 #pragma unroll
-  for (int k = 0; k < kWidePf; ++k)
-    if (t0 + k < t1) ld_step<NS, VEC>(d[k], row + (t0 + k) * NS);
-  for (int64_t tb = t0; tb < t1; tb += kWidePf) {
+    for (int r = 0; r < NS; ++r) s[r] = carry[(c * lanes + lane) * NS + r];
 #pragma unroll
-    for (int k = 0; k < kWidePf; ++k) {
-      const int64_t t = tb + k;
-      if (t < t1) {
-        wide_step<NS, false>(m, s, d[k]);
-        st_step<NS, VEC>(xrow + t * NS, s);
-        if (t + kWidePf < t1) ld_step<NS, VEC>(d[k], row + (t + kWidePf) * NS);
+    for (int k = 0; k < kWidePf; ++k)
+      if (t0 + k < t1) ld_step<NS, VEC>(d[k], row + (t0 + k) * NS);
+  }
+  for (int64_t tb = t0; tb < t1; tb += SB) {
+    const int cnt = (int)((t1 - tb) < SB ? (t1 - tb) : SB);
+    if (live) {
+      for (int kk = 0; kk < SB; kk += kWidePf) {
+#pragma unroll
+        for (int k = 0; k < kWidePf; ++k) {
+          const int64_t t = tb + kk + k;
+          if (t < t1) {
+            wide_step<NS, false>(m, s, d[k]);
+#pragma unroll
+            for (int r = 0; r < NS; ++r) s_o[tid][(kk + k) * NS + r] = (float)s[r];
+            if (t + kWidePf < t1) ld_step<NS, VEC>(d[k], row + (t + kWidePf) * NS);
+          }
+        }
       }
     }
+    __syncthreads();
+    const int wseg = cnt * NS;
+#pragma unroll 8
+    for (int l = 0; l < 64; ++l) {
+      const int64_t ln = l0 + w0 + l;
+      if (ln < lanes && wl < wseg) x[(ln * L + tb) * NS + wl] = s_o[w0 + l][wl];
+    }
+    __syncthreads();
   }
 }
 
