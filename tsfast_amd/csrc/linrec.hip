@@ -835,29 +835,33 @@ __global__ void __launch_bounds__(64) lw_carry_bwd(const float* __restrict__ A, 
 }
 
 // Every chunk re-run backwards from its right-end adjoint, writing grad_v and the chunk's grad_A
-// partial sum_t G_t x_{t-1}^T (x_{-1} = x0 or 0) into part [nchunks][lanes][NS * NS]
+// partial sum_t G_t x_{t-1}^T (x_{-1} = x0 or 0) into part [nchunks][lanes][NS * NS]. grad_v goes
+// out through LDS as whole row segments, like x in the forward re-run.
 template <int NS, int VEC>
 __global__ void __launch_bounds__(kWideThreads) lw_apply_bwd(const float* __restrict__ A, const float* __restrict__ g,
                                                              const float* __restrict__ out, const float* __restrict__ x0,
                                                              const double* __restrict__ rc, float* __restrict__ gv,
                                                              double* __restrict__ part, int64_t lanes, int64_t L) {
-  const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
-  if (lane >= lanes) return;
+  constexpr int SB = wide_out_sb<NS>();
+  constexpr int kPfB = 2;  // steps fetched ahead; SB is a multiple of it
+  static_assert(SB % kPfB == 0, "sub-blocks hold whole prefetch pairs");
+  __shared__ float s_o[kWideThreads][SB * NS + 1];
+  const int tid = threadIdx.x, wl = tid & 63, w0 = tid & ~63;
+  const int64_t l0 = blockIdx.x * (int64_t)kWideThreads, lane = l0 + tid;
+  const bool live = lane < lanes;
   const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
   float m[NS][NS];
-  load_matrix_f32<NS>(m, A, lane);
   double G[NS], acc[NS][NS];
 #pragma unroll
   for (int r = 0; r < NS; ++r) {
-    G[r] = rc[(c * lanes + lane) * NS + r];
+    G[r] = live ? rc[(c * lanes + lane) * NS + r] : 0.0;
 #pragma unroll
     for (int q = 0; q < NS; ++q) acc[r][q] = 0.0;
   }
-  const float* grow = g + lane * L * NS;
-  const float* xrow = out + lane * L * NS;
-  float* gvrow = gv + lane * L * NS;
-  // g_t and x_{t-1} of the next kPfB steps are fetched while step t computes
-  constexpr int kPfB = 2;
+  const int64_t lrow = (live ? lane : 0) * L * NS;
+  const float* grow = g + lrow;
+  const float* xrow = out + lrow;
+  // slot k of the ring holds g_t and x_{t-1} of a step t with (t - t0) % kPfB == k
   float dg[kPfB][NS], dx[kPfB][NS];
   auto fetch = [&](int k, int64_t t) __attribute__((always_inline)) {
     ld_step<NS, VEC>(dg[k], grow + t * NS);
@@ -868,29 +872,57 @@ __global__ void __launch_bounds__(kWideThreads) lw_apply_bwd(const float* __rest
       for (int q = 0; q < NS; ++q) dx[k][q] = x0 ? x0[lane * NS + q] : 0.0f;
     }
   };
+  if (live) {
+    load_matrix_f32<NS>(m, A, lane);
+    if (((t1 - 1 - t0) & 1) == 0) {
+      fetch(0, t1 - 1);
+      if (t1 - 2 >= t0) fetch(1, t1 - 2);
+    } else {
+      fetch(1, t1 - 1);
+      if (t1 - 2 >= t0) fetch(0, t1 - 2);
+    }
+  }
+  const int64_t nsb = (t1 - t0 + SB - 1) / SB;
+  for (int64_t j = nsb - 1; j >= 0; --j) {
+    const int64_t tb = t0 + j * SB;
+    const int cnt = (int)((t1 - tb) < SB ? (t1 - tb) : SB);
+    if (live) {
+      for (int kk = SB - kPfB; kk >= 0; kk -= kPfB) {
 #pragma unroll
-  for (int k = 0; k < kPfB; ++k)
-    if (t1 - 1 - k >= t0) fetch(k, t1 - 1 - k);
-  for (int64_t tb = t1 - 1; tb >= t0; tb -= kPfB)
+        for (int k = kPfB - 1; k >= 0; --k) {
+          const int64_t t = tb + kk + k;
+          if (t < t1) {
+            wide_step<NS, true>(m, G, dg[k]);
+            float xp[NS];
 #pragma unroll
-  for (int k = 0; k < kPfB; ++k) {
-    const int64_t t = tb - k;
-    if (t < t0) break;
-    float xp[NS];
-    wide_step<NS, true>(m, G, dg[k]);
-    st_step<NS, VEC>(gvrow + t * NS, G);
+            for (int r = 0; r < NS; ++r) {
+              s_o[tid][(kk + k) * NS + r] = (float)G[r];
+              xp[r] = dx[k][r];
+            }
+            if (t - kPfB >= t0) fetch(k, t - kPfB);
 #pragma unroll
-    for (int q = 0; q < NS; ++q) xp[q] = dx[k][q];
-    if (t - kPfB >= t0) fetch(k, t - kPfB);
+            for (int r = 0; r < NS; ++r)
+#pragma unroll
+              for (int q = 0; q < NS; ++q) acc[r][q] = fma(G[r], (double)xp[q], acc[r][q]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int wseg = cnt * NS;
+#pragma unroll 8
+    for (int l = 0; l < 64; ++l) {
+      const int64_t ln = l0 + w0 + l;
+      if (ln < lanes && wl < wseg) gv[(ln * L + tb) * NS + wl] = s_o[w0 + l][wl];
+    }
+    __syncthreads();
+  }
+  if (live) {
 #pragma unroll
     for (int r = 0; r < NS; ++r)
 #pragma unroll
-      for (int q = 0; q < NS; ++q) acc[r][q] = fma(G[r], (double)xp[q], acc[r][q]);
+      for (int q = 0; q < NS; ++q) part[(c * lanes + lane) * NS * NS + r * NS + q] = acc[r][q];
   }
-#pragma unroll
-  for (int r = 0; r < NS; ++r)
-#pragma unroll
-    for (int q = 0; q < NS; ++q) part[(c * lanes + lane) * NS * NS + r * NS + q] = acc[r][q];
 }
 
 // Workspace of the two-pass path: e/f and the carries [nchunks][lanes][n], M [lanes][n][n], and
