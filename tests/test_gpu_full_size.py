@@ -5,7 +5,9 @@ through properties that do not need the oracle to run the whole workload where i
   the full-size result must equal the fp64 oracle run on that slice alone at the full sequence
   length. Config 3 also checks every batch row of the full call bit for bit against a call on
   that row alone, and its batch-summed gradients (grad A, grad D) against the ordered sum of the
-  per-row calls, bit for bit (the same fp32 additions in the same order).
+  per-row calls, bit for bit (the same fp32 additions in the same order). One batch row at the
+  full length and width runs through the oracle with every gradient, the channel- and
+  time-summed ones (grad B_t, grad C_t, grad A, grad D) included.
 * Config 4 runs the oracle on all 4096 lanes (it is a vectorised loop over 16384 steps).
 * Config 5: 64 TBPTT chunks of 4096 steps with the last state carried equal one unchunked call
   (forward), chunk slicing is exact, and the truncated per-chunk backward matches the oracle.
@@ -114,6 +116,35 @@ def test_config3_full_size(gpu):
     assert O.rel_err(_np64(gdraw[b : b + 1, :, ds]), wgdraw) < tol
     assert O.rel_err(_np64(gu[b : b + 1, :, ds]), wgu) < tol
     assert O.rel_err(_np64(gz[b : b + 1, :, ds]), wgz) < tol
+
+
+def test_config3_full_width_row_all_grads(gpu):
+    """One batch row of config 3 at its full length and width (L4096, D1536, N16, bf16 I/O)
+    against the fp64 oracle, every output and gradient included: gBt / gCt sum over all 48
+    32-channel tiles of the backward's partial buffer and gA / gDp over the whole sequence, so
+    the cross-tile reduction is checked at the headline width, not only at D = 256."""
+    g = torch.Generator().manual_seed(5)
+    L, D, N = 4096, 1536, 16
+    bf = torch.bfloat16
+    A = -torch.exp(torch.log(torch.arange(1, N + 1, dtype=torch.float32))).expand(D, N).contiguous()
+    draw = (torch.randn(1, L, D, generator=g) - 4.0).to(bf)
+    Bt = torch.randn(1, L, N, generator=g).to(bf)
+    Ct = torch.randn(1, L, N, generator=g).to(bf)
+    u = torch.randn(1, L, D, generator=g).to(bf)
+    z = torch.randn(1, L, D, generator=g).to(bf)
+    Dp = torch.randn(D, generator=g)
+    gout = torch.randn(1, L, D, generator=g).to(bf)
+    args = [t.to(gpu) for t in (draw, A, Bt, Ct, u, z, Dp)] + [None]
+    out, h_last, grads = _mamba_call(args, gout.to(gpu))
+    np_args = [_np64(t) for t in (draw, A, Bt, Ct, u, z, Dp)]
+    want_out, want_h = O.mamba_forward(*np_args)
+    want = O.mamba_backward(_np64(gout), None, *np_args)
+    tol = 2e-2
+    assert O.rel_err(_np64(out), want_out) < tol
+    assert O.rel_err(_np64(h_last.view(1, D, N)), want_h) < tol
+    for name, got, w in zip(("draw", "A", "Bt", "Ct", "u", "z", "Dp"), grads[:7], want[:7]):
+        err = O.rel_err(_np64(got), w)
+        assert err < tol, f"grad {name}: {err:.2e}"
 
 
 def test_config4_full_size(gpu):
