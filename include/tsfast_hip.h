@@ -30,6 +30,7 @@ extern "C" {
 #define TSF_ERR_WORKSPACE (-2)   /* workspace missing or smaller than the *_workspace_bytes query */
 #define TSF_ERR_UNSUPPORTED (-3) /* shape outside what the kernels are built for (e.g. N > 64) */
 #define TSF_ERR_HIP (-4)         /* a HIP runtime call or kernel launch failed */
+#define TSF_ERR_SCRATCH (-5)     /* more scratch than a no-allocation entry point holds */
 
 #define TSF_DTYPE_F32 0
 #define TSF_DTYPE_BF16 1
@@ -55,6 +56,18 @@ int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
 int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const void* g, const void* lam,
                         const void* out, const void* x0, void* gv, void* glam, void* gx0, void* workspace,
                         int64_t workspace_bytes, void* stream);
+
+/* No-allocation variant of tsfast_hip_diag_fwd. It has no counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The look-back workspace is a fixed per-GPU device array of
+ * tsfast_hip_diag_noalloc_max_bytes() bytes (32 MiB), held until the process ends; a shape whose
+ * tsfast_hip_diag_workspace_bytes exceeds it returns TSF_ERR_SCRATCH before any launch. Each call
+ * re-initialises the array on its stream before the scan, but calls that overlap on one GPU (two
+ * streams or two host threads) share the array and race: serialise them. The stream must belong
+ * to the current device. Same results as tsfast_hip_diag_fwd; allocates nothing. */
+int64_t tsfast_hip_diag_noalloc_max_bytes(void);
+int tsfast_hip_diag_fwd_noalloc(int64_t M, int64_t L, int64_t N, int is_complex, const void* lam, const void* v,
+                                const void* x0, void* out, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * Time-varying (selective) diagonal scan  x_t = a_t * x_{t-1} + v_t  and its adjoint, float32.

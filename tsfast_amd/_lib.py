@@ -31,6 +31,8 @@ _SIGNATURES: dict[str, tuple[list, object]] = {
     "tsfast_hip_diag_workspace_bytes": ([_i64, _i64, _i64, _int], _i64),
     "tsfast_hip_diag_fwd": ([_i64, _i64, _i64, _int] + [_ptr] * 5 + [_i64, _ptr], _int),
     "tsfast_hip_diag_bwd": ([_i64, _i64, _i64, _int] + [_ptr] * 8 + [_i64, _ptr], _int),
+    "tsfast_hip_diag_noalloc_max_bytes": ([], _i64),
+    "tsfast_hip_diag_fwd_noalloc": ([_i64, _i64, _i64, _int] + [_ptr] * 5, _int),
     "tsfast_hip_sel_workspace_bytes": ([_i64, _i64, _i64], _i64),
     "tsfast_hip_sel_fwd": ([_i64, _i64, _i64] + [_ptr] * 5 + [_i64, _ptr], _int),
     "tsfast_hip_sel_bwd": ([_i64, _i64, _i64] + [_ptr] * 8 + [_i64, _ptr], _int),

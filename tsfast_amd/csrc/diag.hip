@@ -15,6 +15,9 @@
 // entering the super-chunk from the tiles before it (look-back), publishes the state leaving
 // it, and re-runs its chunks from registers. Carries are fp64 (complex128). Workgroups are
 // persistent and take tiles in scan order from a counter.
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -763,6 +766,50 @@ void sel_bwd_launch(const DiagTile& t, const float* g, const float* a, const flo
 
 }  // namespace
 
+// ---------------------------------------------------------------- no-allocation entry point
+// The look-back workspace of tsfast_hip_diag_fwd_noalloc: a fixed array in device memory, one
+// copy per GPU, held until the process ends. Host code never uses this name as an address: the
+// device address of each GPU's copy comes from hipGetSymbolAddress (below).
+constexpr int64_t kNoAllocScratchBytes = (int64_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<char*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of this GPU's `scratch`, looked up once per device with that device current;
+// the call's stream must belong to the current device.
+int noalloc_scratch(hipStream_t s, char** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return tsf_record_hip_error(e);
+  if (s != nullptr) {
+    hipDevice_t sdev = cur;
+    e = hipStreamGetDevice(s, &sdev);
+    if (e != hipSuccess) return tsf_record_hip_error(e);
+    if (sdev != cur) return TSF_ERR_ARG;
+  }
+  if (cur < 0 || cur >= kMaxDevices) return TSF_ERR_UNSUPPORTED;
+  char* p = g_scratch_addr[cur].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[cur].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return tsf_record_hip_error(e);
+      p = static_cast<char*>(addr);
+      g_scratch_addr[cur].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return TSF_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int64_t tsfast_hip_diag_workspace_bytes(int64_t M, int64_t L, int64_t N, int is_complex) {
@@ -821,6 +868,23 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
     diag_bwd_launch<float, 16>(t, (const float*)g, (const float*)lam, (const float*)out, (const float*)x0, (float*)gv,
                                (float*)glam, (float*)gx0, ws, L, N, s);
   return tsf_launch_status();
+}
+
+int64_t tsfast_hip_diag_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+int tsfast_hip_diag_fwd_noalloc(int64_t M, int64_t L, int64_t N, int is_complex, const void* lam, const void* v,
+                                const void* x0, void* out, void* stream) {
+  if (M < 0 || L < 0 || N < 0) return TSF_ERR_ARG;
+  if (M == 0 || L == 0 || N == 0) return TSF_OK;
+  if (!lam || !v || !out) return TSF_ERR_ARG;
+  const int64_t need = tsfast_hip_diag_workspace_bytes(M, L, N, is_complex);
+  if (need > kNoAllocScratchBytes) return TSF_ERR_SCRATCH;
+  char* ws = nullptr;
+  const int st = noalloc_scratch(static_cast<hipStream_t>(stream), &ws);
+  if (st != TSF_OK) return st;
+  // the kernels of tsfast_hip_diag_fwd; its reset kernel marks the look-back words in `scratch`
+  // unset and zeroes the tile counter on the stream before the scan runs
+  return tsfast_hip_diag_fwd(M, L, N, is_complex, lam, v, x0, out, ws, need, stream);
 }
 
 int64_t tsfast_hip_sel_workspace_bytes(int64_t M, int64_t L, int64_t N) {

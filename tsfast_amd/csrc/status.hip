@@ -28,6 +28,8 @@ const char* tsfast_hip_status_string(int status) {
       return "workspace missing or too small";
     case TSF_ERR_UNSUPPORTED:
       return "shape not supported by the kernels";
+    case TSF_ERR_SCRATCH:
+      return "shape needs more scratch than the no-allocation entry point's fixed device array holds";
     case TSF_ERR_HIP:
       return g_msg[0] ? g_msg : "HIP error";
     default:
