@@ -19,8 +19,8 @@ design notes, the driver's line is config 3.
 The CPU column times the reference CPU path on a bounded sample of the same workload, on the
 host's cores: the C++/OpenMP port of the reference CPU kernels (oracle/cpu_baseline.cpp, after
 mamba/backend_c.py and scan_backends/diagonal_c.py) for configs 1, 2, 3, 5, and the
-companion-matrix doubling scan (tsfast_amd.dynonet.linear_recurrence on CPU, the reference CPU
-path of dynonet/core.py:23-88) for config 4.
+companion-matrix doubling scan and its adjoint (oracle/torch_reference.py, a restatement of the
+reference CPU path of dynonet/core.py:23-88) for config 4.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 3] [--io bf16|fp32] [--no-cpu]
        (or one of --selective, --conv, --gblock, --linrec for the other rows' workloads)
@@ -392,7 +392,7 @@ def run_conv(args, line):
     cpu = None
     if not args.no_cpu:
         def cpu_leg():
-            from tsfast_amd.mamba.core import _causal_depthwise_silu
+            from oracle import torch_reference as TR
 
             threads = os.cpu_count() or 1
             torch.set_num_threads(threads)
@@ -404,7 +404,7 @@ def run_conv(args, line):
             gc = gy[:rows].float().cpu()
 
             def fb():
-                _causal_depthwise_silu(xc, tc, wc, bc).backward(gc)
+                TR.causal_depthwise_silu(xc, tc, wc, bc).backward(gc)
 
             med, n = cpu_time(fb)
             sf = 2 * rows * L * D * 4 + 3 * rows * L * D * 4
@@ -499,20 +499,20 @@ def run_allpole(args, line):
             import torch
             import torch.nn.functional as F
 
-            from tsfast_amd.dynonet.core import companion, linear_recurrence
+            from oracle import torch_reference as TR
+            from tsfast_amd.dynonet.core import companion
 
             threads = os.cpu_count() or 1
             torch.set_num_threads(threads)
             rows = 64
             a_c = a[:rows].cpu()
             w_c = w[:rows].cpu()
-            g_c = gout[:rows].cpu()
+            g_c = F.pad(gout[:rows].cpu().unsqueeze(-1), (0, 2))
             Cm = companion(a_c)
 
             def fb():
-                v = F.pad(w_c.unsqueeze(-1), (0, 2)).requires_grad_()
-                x = linear_recurrence(Cm, v, None)
-                x[..., 0].backward(g_c)
+                x = TR.linrec_forward(Cm, F.pad(w_c.unsqueeze(-1), (0, 2)))
+                TR.linrec_backward(g_c, Cm, x)
 
             med, n = cpu_time(fb)
             sf, sb = scan_bytes(rows * L, 4, rows, 12)
@@ -603,7 +603,8 @@ def run_gblock(args, line):
         def cpu_leg():
             import torch.nn.functional as F
 
-            from tsfast_amd.dynonet.core import companion, linear_recurrence
+            from oracle import torch_reference as TR
+            from tsfast_amd.dynonet.core import companion
 
             threads = os.cpu_count() or 1
             torch.set_num_threads(threads)
@@ -615,7 +616,7 @@ def run_gblock(args, line):
             def fb():
                 u_buf = torch.cat((u_c.new_zeros(rows, nb - 1, I), u_c), dim=1)
                 w = F.conv1d(u_buf.transpose(1, 2), b_c.permute(1, 0, 2).reshape(P, 1, nb).flip(-1), groups=I)
-                x = linear_recurrence(Cm, F.pad(w.unsqueeze(-1), (0, na - 1)), None)
+                x = TR.LinRec.apply(Cm.expand(rows, P, na, na), F.pad(w.unsqueeze(-1), (0, na - 1)))
                 y = x[..., 0].view(rows, I, O, L).sum(1).transpose(1, 2)
                 y.backward(gy_c)
 
@@ -635,8 +636,7 @@ def run_gblock(args, line):
 def run_linrec(args, line):
     """The constant-matrix linear_recurrence (dynonet/core.py:103-127) on config 4's route: the
     companion matrices of the config-4 denominators (n = 3) driven by (w_t, 0, 0), the way the
-    reference runs dynoNet's all-pole section without a fused kernel. The reference's own
-    algorithm on the same GPU (the log-doubling scan op and its adjoint) is timed in the same run."""
+    reference runs dynoNet's all-pole section without a fused kernel."""
     import torch
     import torch.nn.functional as F
 
@@ -660,14 +660,6 @@ def run_linrec(args, line):
 
     ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
 
-    def doubling(ev):
-        mark(ev)
-        x = dcore._linear_recurrence_op(A, v, None)
-        mark(ev)
-        dcore._linear_recurrence_bwd_op(g, A, x, None)
-        mark(ev)
-
-    dms, (dfwd, dbwd) = time_steps(doubling, 3, 1)
     nbytes = v.numel() * 4
     fwd_b, bwd_b = 2 * nbytes, 3 * nbytes  # read v, write x | read g and x, write grad_v
     line.update(
@@ -678,8 +670,6 @@ def run_linrec(args, line):
                 "lanes": lanes, "L": L, "n": n},
         fwd_ms=round(fwd_ms, 4),
         bwd_ms=round(bwd_ms, 4),
-        doubling_scan_ms={"fwd": round(dfwd, 4), "bwd": round(dbwd, 4), "total": round(dms, 4),
-                          "path": "tsfast_hip::linear_recurrence (the reference's log-doubling scan op) on this GPU"},
     )
     line["dtype"] = "f64"  # fp32 I/O, fp64 recurrence inside
     if n <= 4:
@@ -697,10 +687,11 @@ def run_linrec(args, line):
             rows = 64
             A_c, v_c, g_c = A[:rows].cpu(), v[:rows].cpu(), g[:rows].cpu()
 
+            from oracle import torch_reference as TR
+
             def fb():
-                vv = v_c.clone().requires_grad_()
-                x = dcore._linear_recurrence_op(A_c, vv, None)
-                x.backward(g_c)
+                x = TR.linrec_forward(A_c, v_c)
+                TR.linrec_backward(g_c, A_c, x)
 
             med, nrun = cpu_time(fb)
             sb = rows * L * n * 4 * 5

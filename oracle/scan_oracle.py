@@ -261,7 +261,7 @@ def allpole_backward(g, a, y, y0=None):
 # --------------------------------------------------------------------------- causal depthwise conv + SiLU
 def _conv_pre(x, tail, w, bias):
     """Pre-activation ``p_t = bias + sum_k w_k xbuf_{t-(K-1)+k}`` with ``xbuf = cat(tail, x)``
-    along time, as the shifted multiply-adds of mamba/core.py:38-58 (``_causal_depthwise_silu``).
+    along time, as the shifted multiply-adds of mamba/core.py:38-58 (the reference's ``_causal_depthwise_silu``).
     x [B, L, D], tail [B, D, K-1], w [D, K], bias [D] or None. Returns (p [B, L, D], xbuf)."""
     x, tail, w = _hi(x), _hi(tail), _hi(w)
     Bsz, L, D = x.shape

@@ -67,3 +67,33 @@ def test_selective_port_matches_oracle(lib):
     wl, wv, wx = O.selective_backward(g, a, want, x0)
     assert O.rel_err(out, want) < 1e-5
     assert O.rel_err(glam, wl) < 1e-5 and O.rel_err(gv, wv) < 1e-5 and O.rel_err(gx0, wx) < 1e-5
+
+
+def test_torch_reference_doubling_scan_matches_oracle():
+    """Config 4's CPU column (oracle/torch_reference.py, the reference's doubling scan and its
+    adjoint restated) against the fp64 oracle, x0 included."""
+    import torch
+
+    from oracle import torch_reference as TR
+
+    rng = np.random.default_rng(21)
+    A = rng.standard_normal((3, 4, 4)) * 0.3
+    v, g, x0 = rng.standard_normal((3, 50, 4)), rng.standard_normal((3, 50, 4)), rng.standard_normal((3, 4))
+    x = TR.linrec_forward(torch.tensor(A), torch.tensor(v), torch.tensor(x0))
+    want = O.linrec_forward(A, v, x0)
+    assert O.rel_err(x.numpy(), want) < 1e-12
+    got = TR.linrec_backward(torch.tensor(g), torch.tensor(A), x, torch.tensor(x0))
+    for a, b in zip(got, O.linrec_backward(g, A, want, x0)):
+        assert O.rel_err(a.numpy(), b) < 1e-12
+
+
+def test_torch_reference_conv_matches_oracle():
+    import torch
+
+    from oracle import torch_reference as TR
+
+    rng = np.random.default_rng(22)
+    B, L, D, K = 2, 13, 5, 4
+    x, tail, w, b = (rng.standard_normal(s) for s in ((B, L, D), (B, D, K - 1), (D, 1, K), (D,)))
+    y = TR.causal_depthwise_silu(*(torch.tensor(t) for t in (x, tail, w, b)))
+    assert O.rel_err(y.numpy(), O.conv_silu_forward(x, tail, w[:, 0], b)) < 1e-12

@@ -3,7 +3,7 @@
 Every oracle function is checked against something that does not share its arithmetic:
 brute-force closed-form sums, scipy.signal.lfilter, a textbook selective scan written as
 einsums (the state-spaces/mamba ``selective_scan_ref`` form the reference transcribes in
-tests/test_mamba.py:26-50), the companion-matrix doubling scan, and torch float64 autograd
+tests/test_mamba.py:26-50), the companion-matrix blocked scan, and torch float64 autograd
 through plain sequential loops. Each check is also run against deliberately broken variants
 of the oracle (a dropped conjugate, a sign flip, a missing factor, an off-by-one in time) and
 must reject every one of them, so the checks have the power to catch those mistakes.
@@ -651,8 +651,8 @@ def test_linrec_check_rejects_backward(mutant):
     assert not check_linrec(O.linrec_forward, mutant)
 
 
-def test_linrec_doubling_scan_matches_oracle():
-    """The CPU route of linear_recurrence (the reference's log-doubling op and its adjoint, which
+def test_linrec_blocked_scan_matches_oracle():
+    """The CPU route of linear_recurrence (the blocked two-level matrix scan and its adjoint, which
     every non-GPU call and every unsupported shape takes) against the oracle, with A broadcast
     over a batch dim so the adjoint's grad_A is summed back."""
     from tsfast_amd.dynonet.core import linear_recurrence

@@ -1,12 +1,20 @@
-"""dynoNet all-pole section with its fused-kernel dispatch, and the constant-matrix scan.
+"""dynoNet sections with fused-kernel dispatch, and the constant-matrix recurrence.
 
-Mirrors ``tsfast/models/architectures/dynonet/core.py``: ``linear_recurrence`` (the log-doubling
-scan ``x_t = A x_{t-1} + v_t`` with its analytic matrix adjoint, ``:23-127``; on GPU the
-``"hip"`` family serves it for state sizes n <= 8: a single-pass scan for n <= 4, a two-pass
-scan above) and the all-pole
-branch of ``LinearDynamicalOperator.forward`` (``:221-248``): the fused backend when one serves
-the inputs (``_fused_allpole``, ``:91-100``; here the ``"hip"`` family for ``"cuda"`` tensors),
-else ``linear_recurrence`` over the companion matrices.
+Counterparts of ``tsfast/models/architectures/dynonet/core.py``:
+
+* ``linear_recurrence`` (``:103-127``): ``x_t = A x_{t-1} + v_t`` with constant ``A [..., n, n]``
+  and its matrix adjoint. On GPU the ``"hip"`` family serves state sizes n <= 8 (a single-pass
+  scan for n <= 4, a two-pass scan above); otherwise the ``tsfast_hip::linear_recurrence`` op
+  runs the blocked torch scan of :mod:`tsfast_amd.blocked_scan` (the reference runs a
+  log-doubling scan, ``:23-37``).
+* ``allpole``: the all-pole branch of ``LinearDynamicalOperator.forward`` (``:221-248``), the
+  fused backend when one serves the inputs (``_fused_allpole``, ``:91-100``), else
+  ``linear_recurrence`` over the companion matrices.
+* ``linear_dynamical_operator``: the whole G-block (FIR, all-pole, sum over inputs), fused
+  when a backend serves it.
+
+Adjoint of the matrix recurrence: ``G_t = A^T G_{t+1} + g_t``, ``dL/dv = G``,
+``dL/dA = sum_t G_t x_{t-1}^T``, ``dL/dx_0 = A^T G_1``.
 """
 
 from __future__ import annotations
@@ -16,6 +24,7 @@ __all__ = ["linear_recurrence", "allpole", "companion", "linear_dynamical_operat
 import torch
 import torch.nn.functional as F
 
+from .. import blocked_scan
 from ..dispatch import resolve
 from . import allpole_hip, gblock_hip, linrec_hip
 
@@ -24,29 +33,9 @@ _GBLOCK_BACKENDS = {"hip": gblock_hip}
 _LINREC_BACKENDS = {"hip": linrec_hip}
 
 
-def _doubling_matrix_scan(A: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-    """``x_t = A x_{t-1} + v_t`` from a zero state: doubling span, one batched matmul per level."""
-    L = v.shape[-2]
-    x = v.clone() if L <= 1 else v
-    span, P = 1, A
-    while span < L:
-        shifted = F.pad(x[..., :-span, :], (0, 0, span, 0))
-        x = x + shifted @ P.transpose(-1, -2)
-        P = P @ P
-        span <<= 1
-    return x
-
-
-def _prev(x: torch.Tensor, x0: torch.Tensor | None) -> torch.Tensor:
-    head = torch.zeros_like(x[..., :1, :]) if x0 is None else x0.unsqueeze(-2).expand_as(x[..., :1, :])
-    return torch.cat((head, x[..., :-1, :]), dim=-2)
-
-
 @torch.library.custom_op("tsfast_hip::linear_recurrence", mutates_args=())
 def _linear_recurrence_op(A: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> torch.Tensor:
-    if x0 is not None:
-        v = torch.cat((v[..., :1, :] + x0.unsqueeze(-2) @ A.transpose(-1, -2), v[..., 1:, :]), dim=-2)
-    return _doubling_matrix_scan(A, v)
+    return blocked_scan.scan_matrix(A, v, x0)
 
 
 @_linear_recurrence_op.register_fake
@@ -58,48 +47,56 @@ def _(A, v, x0):
 def _linear_recurrence_bwd_op(
     g: torch.Tensor, A: torch.Tensor, out: torch.Tensor, x0: torch.Tensor | None
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    # adjoint G_t = A^T G_{t+1} + g_t: the same scan with A transposed, run time-reversed
-    G = _doubling_matrix_scan(A.transpose(-1, -2), g.flip(-2)).flip(-2)
-    grad_A = G.transpose(-1, -2) @ _prev(out, x0)
-    grad_x0 = (G[..., :1, :] @ A).squeeze(-2) if x0 is not None else A.new_empty(0)
+    At = A.transpose(-1, -2)
+    G = blocked_scan.scan_matrix(At, g.flip(-2)).flip(-2)  # reverse-time scan with A^T
+    prev = out.roll(1, dims=-2)  # x_{t-1} for every step t
+    if prev.shape[-2] > 0:
+        prev[..., 0, :] = 0 if x0 is None else x0
+    grad_A = torch.einsum("...ti,...tj->...ij", G, prev)
+    if x0 is None:
+        grad_x0 = A.new_empty(0)
+    elif G.shape[-2] > 0:
+        grad_x0 = (At @ G[..., 0, :].unsqueeze(-1)).squeeze(-1)
+    else:
+        grad_x0 = torch.zeros_like(x0)
     return grad_A, G, grad_x0
 
 
 @_linear_recurrence_bwd_op.register_fake
 def _(g, A, out, x0):
-    gx0 = torch.empty_like(x0) if x0 is not None else A.new_empty(0)
-    return torch.empty_like(A), torch.empty_like(g), gx0
+    return torch.empty_like(A), torch.empty_like(g), (A.new_empty(0) if x0 is None else torch.empty_like(x0))
 
 
-def _linrec_setup(ctx, inputs, output):
-    A, v, x0 = inputs
+def _linrec_save(ctx, inputs, output):
+    A, _, x0 = inputs
     ctx.save_for_backward(A, output, x0)
 
 
-def _linrec_backward(ctx, g):
+def _linrec_grads(ctx, g):
     A, out, x0 = ctx.saved_tensors
-    grad_A, grad_v, grad_x0 = _linear_recurrence_bwd_op(g, A, out, x0)
-    return grad_A, grad_v, (grad_x0 if x0 is not None else None)
+    gA, gv, gx0 = _linear_recurrence_bwd_op(g, A, out, x0)
+    return gA, gv, None if x0 is None else gx0
 
 
-_linear_recurrence_op.register_autograd(_linrec_backward, setup_context=_linrec_setup)
+_linear_recurrence_op.register_autograd(_linrec_grads, setup_context=_linrec_save)
 
 
 def linear_recurrence(A: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None = None) -> torch.Tensor:
-    """``x_t = A x_{t-1} + v_t`` with constant ``A [..., n, n]`` (``core.py:103-127``).
+    """``x_t = A x_{t-1} + v_t`` with constant ``A [..., n, n]`` (``dynonet/core.py:103-127``).
 
-    A, v and x0 are broadcast to common leading dims; a backend that serves the inputs (the
-    ``"hip"`` family for ``"cuda"`` tensors) runs them, else the log-doubling scan op.
+    ``A``, ``v [..., L, n]`` and ``x0 [..., n]`` (zero if None) are broadcast to common leading
+    dims; a backend that serves them (the ``"hip"`` family for ``"cuda"`` tensors) runs the
+    scan, else the ``tsfast_hip::linear_recurrence`` op. Returns ``x_1 .. x_L``, ``[..., L, n]``.
     """
-    bshape = torch.broadcast_shapes(A.shape[:-2], v.shape[:-2], () if x0 is None else x0.shape[:-1])
-    A_b = A.broadcast_to(bshape + A.shape[-2:])
-    v_b = v.broadcast_to(bshape + v.shape[-2:])
-    x0_b = None if x0 is None else x0.broadcast_to(bshape + x0.shape[-1:])
-    order = ("hip",) if v_b.device.type == "cuda" else ()
-    mod = resolve("dynonet.linear_recurrence", _LINREC_BACKENDS, order, (A_b, v_b, x0_b))
-    if mod is not None:
-        return mod.run(A_b, v_b, x0_b)
-    return _linear_recurrence_op(A_b, v_b, x0_b)
+    lead = torch.broadcast_shapes(A.shape[:-2], v.shape[:-2], () if x0 is None else x0.shape[:-1])
+    args = (
+        A.expand(*lead, *A.shape[-2:]),
+        v.expand(*lead, *v.shape[-2:]),
+        None if x0 is None else x0.expand(*lead, x0.shape[-1]),
+    )
+    order = ("hip",) if v.device.type == "cuda" else ()
+    mod = resolve("dynonet.linear_recurrence", _LINREC_BACKENDS, order, args)
+    return mod.run(*args) if mod is not None else _linear_recurrence_op(*args)
 
 
 def companion(a: torch.Tensor) -> torch.Tensor:
@@ -111,7 +108,7 @@ def companion(a: torch.Tensor) -> torch.Tensor:
 
 
 def _fused_allpole(a, w, y0):
-    """Dispatch the fused all-pole kernel; None means run the matrix doubling scan."""
+    """The fused all-pole backend's output, or None when none serves the inputs."""
     order = ("hip",) if w.device.type == "cuda" else ()
     mod = resolve("dynonet.allpole", _ALLPOLE_BACKENDS, order, (a, w, y0))
     return None if mod is None else mod.run(a, w, y0)
@@ -120,9 +117,9 @@ def _fused_allpole(a, w, y0):
 def allpole(a: torch.Tensor, w: torch.Tensor, y0: torch.Tensor | None = None) -> torch.Tensor:
     """``y_t = w_t - sum_i a_i y_{t-i}`` over lanes ``w [..., L]`` with ``a [..., na]``, ``y0 [..., na]``.
 
-    The fused kernel when one serves the inputs, else the companion-matrix doubling scan
-    (the reference CPU path): the companion state is a shift register of past outputs, so
-    ``y`` is its first component.
+    The fused kernel when one serves the inputs, else ``linear_recurrence`` over the companion
+    matrices: the companion state is a shift register of past outputs, so ``y`` is its first
+    component.
     """
     y = _fused_allpole(a, w, y0)
     if y is not None:
