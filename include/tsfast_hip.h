@@ -102,8 +102,9 @@ int tsfast_hip_sel_bwd(int64_t M, int64_t L, int64_t N, const float* g, const fl
  * gradient reads it instead of recomputing sum_n h_t C_t). chk == NULL selects the inference
  * kernel, which saves nothing.
  * The kernels address one batch row with 32-bit byte offsets: (L + 64) * D, (L + 64) * 2 * N'
- * (N' = N rounded up to 4, 8, 16, 32 or 64) and NC * N * D + L * D must stay below 2^30, else
- * TSF_ERR_UNSUPPORTED.
+ * (N' = N rounded up to 4, 8, 16, 32 or 64) and NC * N * D + L * D must stay below 2^29, else
+ * TSF_ERR_UNSUPPORTED (tsfast_hip_mamba_saved_floats then returns -1, so it doubles as the size
+ * check).
  */
 int64_t tsfast_hip_mamba_chk_interval(int64_t N);
 int64_t tsfast_hip_mamba_saved_floats(int64_t L, int64_t D, int64_t N, int io_dtype);

@@ -97,3 +97,18 @@ def test_loader_arity_matches_header():
     assert sorted(arity) == _declared()
     for name, (argtypes, _) in _lib._SIGNATURES.items():
         assert len(argtypes) == arity[name], name
+
+
+def test_mamba_supports_mirrors_the_kernel_size_limits(lib):
+    """mamba_hip keeps the checkpoint interval and the per-row addressing limit in Python (so
+    supports() makes no library call inside a compiled graph); both must agree with the C side,
+    so a shape the kernels would reject falls back through dispatch instead of raising."""
+    from tsfast_amd.mamba import mamba_hip
+
+    for N in range(1, 65):
+        assert mamba_hip._chk_steps(N) == lib.tsfast_hip_mamba_chk_interval(N), N
+    # around the 2 GiB row boundary at D = 1536 (L near 2^29 / 1536 = 349525 minus padding)
+    for N in (1, 16, 64):
+        for L in (1, 4096, 349_000, 349_400, 349_460, 349_500, 349_600, 400_000):
+            c_ok = lib.tsfast_hip_mamba_saved_floats(L, 1536, N, 0) >= 0
+            assert mamba_hip._rows_fit(L, 1536, N) == c_ok, (L, N)

@@ -49,6 +49,36 @@ TSF_DEV void st32(T* __restrict__ base, uint32_t idx, T v) {
   *reinterpret_cast<T*>(reinterpret_cast<char*>(base) + idx * (uint32_t)sizeof(T)) = v;
 }
 
+// ------------------------------------------------------------------ buffer accesses
+// A raw buffer resource over [base, base + bytes): the hardware checks every access against
+// `bytes`, so a load at or beyond it returns 0 and such a store is dropped. Offsets are a per-lane
+// VGPR byte offset plus a wave-uniform SGPR byte offset (stepped by scalar adds), so streaming
+// through a row costs no vector address arithmetic. The kernels keep voff + soff below 2^32.
+using Rsrc = __amdgpu_buffer_rsrc_t;
+// gfx9 raw-buffer descriptor word 3 (32-bit data format, no swizzle)
+constexpr int kBufWord3 = 0x00020000;
+TSF_DEV Rsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufWord3);
+}
+TSF_DEV float buf_ld(Rsrc r, uint32_t voff, uint32_t soff, float*) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+TSF_DEV bf16 buf_ld(Rsrc r, uint32_t voff, uint32_t soff, bf16*) {
+  bf16 v;
+  v.bits = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+  return v;
+}
+template <typename T>
+TSF_DEV T buf_load(Rsrc r, uint32_t voff, uint32_t soff) {
+  return buf_ld(r, voff, soff, static_cast<T*>(nullptr));
+}
+TSF_DEV void buf_store(float v, Rsrc r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, voff, soff, 0);
+}
+TSF_DEV void buf_store(bf16 v, Rsrc r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b16(v.bits, r, voff, soff, 0);
+}
+
 // ------------------------------------------------------------------ complex (interleaved re/im)
 TSF_DEV float2 cmul(float2 a, float2 b) { return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x); }
 // a * conj(b)
@@ -172,6 +202,12 @@ TSF_DEV SoftplusParts softplus_parts(float x) {
   return r;
 }
 TSF_DEV float softplus_fast(float x) { return softplus_parts(x).value; }
+// softplus as the reference's kernels write it (mamba_triton.py:75-78): log(1 + e^x) with x
+// above 20 passed through, on the transcendental unit (v_exp, v_log)
+TSF_DEV float softplus_ref(float x) {
+  const float e = __builtin_amdgcn_exp2f(fminf(x, 20.0f) * kLog2e);
+  return x > 20.0f ? x : __builtin_amdgcn_logf(1.0f + e) * kLn2;
+}
 TSF_DEV float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e)); }
 
 // ------------------------------------------------------------------ wave reductions

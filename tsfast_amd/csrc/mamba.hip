@@ -137,6 +137,41 @@ TSF_DEV void xcd_remap(int64_t& tile, int64_t& row) {
   row = lin / gx;
 }
 
+// ------------------------------------------------------------------------------------ DPP rows
+// Lane layout shared by both directions: the workgroup's TH = DT * NG threads form rows of 16
+// lanes (a DPP row); row r holds state group ng = r / (DT / 16) for channels
+// dl = 16 * (r % (DT / 16)) + (lane in row), and a lane's NPT states are n = j * NG + ng. B_t and
+// C_t of a row's states are the same for its 16 lanes, so a tile of B/C values sits in VGPRs
+// spread over the row (slot s = i * NPT + j in lane s % 16 of register s / 16) and reaches every
+// lane through a DPP row broadcast (row_newbcast) folded into the consuming multiply; no LDS
+// round trip. Consecutive state groups sit in adjacent rows of the per-state-group scratch, so
+// every per-step LDS store of a wave is 64 consecutive floats.
+template <int K>
+TSF_DEV float row_bcast_k(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + K, 0xF, 0xF, true));
+}
+// lane k (0..15) of this lane's DPP row; k must fold to a constant at compile time
+TSF_DEV float row_bcast(float x, int k) {
+  switch (k) {
+    case 0: return row_bcast_k<0>(x);
+    case 1: return row_bcast_k<1>(x);
+    case 2: return row_bcast_k<2>(x);
+    case 3: return row_bcast_k<3>(x);
+    case 4: return row_bcast_k<4>(x);
+    case 5: return row_bcast_k<5>(x);
+    case 6: return row_bcast_k<6>(x);
+    case 7: return row_bcast_k<7>(x);
+    case 8: return row_bcast_k<8>(x);
+    case 9: return row_bcast_k<9>(x);
+    case 10: return row_bcast_k<10>(x);
+    case 11: return row_bcast_k<11>(x);
+    case 12: return row_bcast_k<12>(x);
+    case 13: return row_bcast_k<13>(x);
+    case 14: return row_bcast_k<14>(x);
+    default: return row_bcast_k<15>(x);
+  }
+}
+
 // ------------------------------------------------------------------------------------ forward
 // SAVE: training forward (writes the checkpoints and y to chk); chk is unused otherwise.
 template <typename TIO, int NS, bool SAVE>
@@ -243,7 +278,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         o_u[k] = to_f32(r_u[k]);
         o_z[k] = to_f32(r_z[k]);
         const bool live = oact && idx / DT < len;
-        const float delta = live ? softplus_fast(to_f32(r_dr[k])) : 0.0f;
+        const float delta = live ? softplus_ref(to_f32(r_dr[k])) : 0.0f;
         s_sc[idx / DT][idx % DT] = make_float2(delta, delta * o_u[k]);
       }
     }
@@ -332,69 +367,64 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
 }
 
 // ------------------------------------------------------------------------------------ backward
-// Lane layout: the workgroup's TH threads form 2*NG rows of 16 lanes (a DPP row). Row r holds
-// state group ng = r / 2 for channels dl = 16 * (r % 2) + (lane in row), and a lane's NPT states
-// are n = j * NG + ng. B_t and C_t of a row's states are the same for its 16 lanes, so each
-// chunk's B/C tile sits in VGPRs spread over the row (slot s = i * NPT + j in lane s % 16 of
-// register s / 16) and reaches every lane through a DPP row broadcast (row_newbcast) folded into
-// the consuming multiply; no LDS round trip. Consecutive state groups sit in adjacent rows of the
-// channel-sum scratch, so every per-step LDS store of a wave is 64 consecutive floats.
-template <int K>
-TSF_DEV float row_bcast_k(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + K, 0xF, 0xF, true));
-}
-// lane k (0..15) of this lane's DPP row; k must fold to a constant at compile time
-TSF_DEV float row_bcast(float x, int k) {
-  switch (k) {
-    case 0: return row_bcast_k<0>(x);
-    case 1: return row_bcast_k<1>(x);
-    case 2: return row_bcast_k<2>(x);
-    case 3: return row_bcast_k<3>(x);
-    case 4: return row_bcast_k<4>(x);
-    case 5: return row_bcast_k<5>(x);
-    case 6: return row_bcast_k<6>(x);
-    case 7: return row_bcast_k<7>(x);
-    case 8: return row_bcast_k<8>(x);
-    case 9: return row_bcast_k<9>(x);
-    case 10: return row_bcast_k<10>(x);
-    case 11: return row_bcast_k<11>(x);
-    case 12: return row_bcast_k<12>(x);
-    case 13: return row_bcast_k<13>(x);
-    case 14: return row_bcast_k<14>(x);
-    default: return row_bcast_k<15>(x);
-  }
-}
+// Tiling: a workgroup covers one batch row x DT = 32 channels (config 3: 768 workgroups of 4
+// waves, three per CU, so a workgroup waiting at a barrier leaves the CU to the other two), in
+// the DPP-row lane layout above; each chunk's B/C tile is broadcast from registers.
+template <int NS, int DT_>
+struct BCfg {
+  static constexpr int NG = MCfg<NS>::NG, NPT = MCfg<NS>::NPT;
+  static constexpr int DT = DT_;
+  static constexpr int TH = DT * NG;
+  static constexpr int RPG = DT / 16;                    // DPP rows per state group
+  static constexpr int CHK = MCfg<NS>::CHK;              // the forward's checkpoint interval
+  static constexpr int IT = (CHK * DT + TH - 1) / TH;    // owned (t, d) items per thread
+  static constexpr int W2 = 2 * NS;                      // grad B / grad C columns
+  static constexpr int NSL = CHK * NPT;                  // B/C broadcast slots per chunk and row
+  static constexpr int NBV = (NSL + 15) / 16;            // VGPRs per B (and per C) tile
+  static constexpr int WAVES = TH / 64;
+  static constexpr int OCC = (12 / WAVES) > 1 ? (12 / WAVES) : 1;  // workgroups per CU aimed at
+  static_assert(DT % 16 == 0, "channel tile must be whole DPP rows");
+};
 
-template <typename TIO, int NS>
-__global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
+// Per chunk of CHK steps (walking from the end of the sequence), between two barriers:
+//   A  recompute the chunk's states from its checkpoint into registers (lam_t, lam_t h_{t-1}, h_t)
+//   B  adjoint G_t = gy_t C_t + lam_{t+1} G_{t+1} backwards through the chunk; per-lane partial
+//      sums over states (sum_n A Q, sum_n G B) and the channel terms of grad B / grad C to LDS
+//   -- barrier --
+//   C  owners finish the chunk's per-(t, d) gradients; the channel sums of grad B / grad C
+//      are written as this tile's partials
+//   D  owners prepare the previous chunk's per-(t, d) scalars in LDS (its inputs were loaded
+//      at the top of this iteration) and store grad z, which needs no recurrence
+//   -- barrier --
+template <typename TIO, int NS, int DT_>
+__global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mamba_bwd_kernel(
     const TIO* __restrict__ draw, const float* __restrict__ A, const TIO* __restrict__ Bt,
     const TIO* __restrict__ Ct, const TIO* __restrict__ u, const TIO* __restrict__ z, const float* __restrict__ Dp,
     const float* __restrict__ h0, const float* __restrict__ saved, const TIO* __restrict__ gout,
     const float* __restrict__ ghlast, TIO* __restrict__ gdraw, TIO* __restrict__ gu, TIO* __restrict__ gz,
     float* __restrict__ gA_part, float* __restrict__ gDp_part, float* __restrict__ gBC_part, float* __restrict__ gh0,
     int64_t B, int64_t L, int64_t D, int N, int64_t NC, unsigned cus) {
-  using C = MCfg<NS>;
-  constexpr int NPT = C::NPT, NG = C::NG, DT = C::DT, TH = C::TH, CHK = C::CHK, TB = C::TB, IT = C::IT_B;
-  constexpr int NSB = CHK / TB;
-  constexpr int W2 = 2 * NS;                   // grad B / grad C columns
-  constexpr int NSL = CHK * NPT;               // B/C broadcast slots per chunk and row
-  constexpr int NBV = (NSL + 15) / 16;         // VGPRs per B (and per C) tile
-  static_assert(DT == 32 && TH == 32 * NG, "two 16-lane rows per state group cover the 32 channels");
-  __shared__ float4 s_sc[CHK][DT];                  // (delta, delta * u, gy, -) per (t, d)
-  __shared__ float s_np[TB][2][NG][DT];             // (sum_n A Q, sum_n G B) per state group
-  __shared__ __align__(16) float s_dp[TB][W2][DT];  // per (step, column): the 32 channels' (G du | gy h)
+  using C = BCfg<NS, DT_>;
+  constexpr int NPT = C::NPT, NG = C::NG, DT = C::DT, TH = C::TH, CHK = C::CHK, IT = C::IT;
+  constexpr int W2 = C::W2, NBV = C::NBV, NSL = C::NSL, RPG = C::RPG;
+  // per (t, d): (delta, delta u) as an aligned pair, and gy in its own array. gy also weights
+  // the channel sums of grad C, which read it after the chunk's adjoint while the next chunk's
+  // values are being written: two copies by chunk parity. 52 KB in all at DT = 32, so that three
+  // workgroups share a CU.
+  __shared__ float2 s_dx[CHK][DT];
+  __shared__ __align__(16) float s_gw[2][CHK][DT];
+  __shared__ float s_np[CHK][2][NG][DT];             // (sum_n A Q, sum_n G B) per state group
+  __shared__ __align__(16) float s_dp[CHK][W2][DT];  // per (step, column): the channels' (G du | h)
 
   const int tid = threadIdx.x;
   int64_t tile, b;
   xcd_remap(tile, b);
   const int64_t d0 = tile * DT;
   const int rw = tid >> 4, lk = tid & 15;
-  const int ng = rw >> 1;
-  const int dl = lk | ((rw & 1) << 4);
+  const int ng = rw / RPG;
+  const int dl = lk + 16 * (rw % RPG);
   const int64_t d = d0 + dl;
   const bool act = d < D;
-  const int od = tid % DT;
-  const bool oact = d0 + od < D;
   const int64_t rowD = b * L * D + d0, rowN = b * L * N;
   const uint32_t Du = (uint32_t)D, Nu = (uint32_t)N;
 
@@ -411,219 +441,241 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     gA[j] = 0.0f;
     lam_next[j] = 1.0f;  // no step after the last one
   }
-  const float dp_o = oact ? Dp[d0 + od] : 0.0f;
   float gdp = 0.0f;
 
-  const TIO* __restrict__ drw = draw + rowD;
-  const TIO* __restrict__ urw = u + rowD;
-  const TIO* __restrict__ zrw = z + rowD;
-  const TIO* __restrict__ grw = gout + rowD;
-  TIO* __restrict__ gdrw = gdraw + rowD;
-  TIO* __restrict__ gurw = gu + rowD;
-  TIO* __restrict__ gzrw = gz + rowD;
-  const TIO* __restrict__ brw = Bt + rowN;
-  const TIO* __restrict__ crw = Ct + rowN;
+  // Row streams through buffer resources (see make_rsrc): a per-lane byte offset fixed for the
+  // whole walk plus a per-chunk SGPR offset. An inactive lane (channel or state beyond the tensor,
+  // a padding slot) gets the resource's size as its offset, and steps past the end of the sequence
+  // fall beyond it too, so their loads read 0 and their stores are dropped: no guarded copy of the
+  // load code for partial tiles or the last chunk.
+  constexpr uint32_t esz = sizeof(TIO);
+  const uint32_t rowD_bytes = (uint32_t)((L * D - d0) * esz);  // [L, D] rows seen from channel d0
+  const uint32_t rowN_bytes = (uint32_t)(L * N * esz);
   // saved state of this batch row: checkpoints [NC, N, D] then pre-gate outputs y [L, D]
   const float* __restrict__ svb = saved + b * saved_row_floats<TIO>(L, D, N, NC);
-  const float* __restrict__ chkb = svb + d0;
-  const TIO* __restrict__ yrw = reinterpret_cast<const TIO*>(svb + NC * N * D) + d0;
-  float* __restrict__ gbcb = gBC_part + (tile * B + b) * L * (2 * NS);  // [L, 2*NS] partials
+  const uint32_t chk_bytes = (uint32_t)((NC * N * D - d0) * 4);
+  const Rsrc rs_dr = make_rsrc(draw + rowD, rowD_bytes), rs_u = make_rsrc(u + rowD, rowD_bytes);
+  const Rsrc rs_z = make_rsrc(z + rowD, rowD_bytes), rs_go = make_rsrc(gout + rowD, rowD_bytes);
+  const Rsrc rs_y = make_rsrc(reinterpret_cast<const TIO*>(svb + NC * N * D) + d0, rowD_bytes);
+  const Rsrc rs_gd = make_rsrc(gdraw + rowD, rowD_bytes), rs_gu = make_rsrc(gu + rowD, rowD_bytes);
+  const Rsrc rs_gz = make_rsrc(gz + rowD, rowD_bytes);
+  const Rsrc rs_b = make_rsrc(Bt + rowN, rowN_bytes), rs_c = make_rsrc(Ct + rowN, rowN_bytes);
+  const Rsrc rs_ck = make_rsrc(svb + d0, chk_bytes);
+  const Rsrc rs_pt = make_rsrc(gBC_part + (tile * B + b) * L * W2, (uint32_t)(L * W2 * 4));  // [L, 2*NS] partials
 
+  // owner items: item k of this thread is (t = idx / DT, channel d0 + idx % DT), idx = tid + k * TH
+  float dp_o[IT];
+  uint32_t ov[IT];  // byte offset of the item within a chunk of a [L, D] row
+#pragma unroll
+  for (int k = 0; k < IT; ++k) {
+    const int idx = tid + k * TH;
+    const int od = idx % DT, t = idx / DT;
+    const bool ok = d0 + od < D && ((CHK * DT) % TH == 0 || idx < CHK * DT);
+    dp_o[k] = d0 + od < D ? Dp[d0 + od] : 0.0f;
+    ov[k] = ok ? ((uint32_t)t * Du + (uint32_t)od) * esz : rowD_bytes;
+  }
+  // B/C broadcast slots of this lane: slot s = i * NPT + j -> (step i of the chunk, state j * NG + ng)
+  uint32_t bco[NBV];
+#pragma unroll
+  for (int q = 0; q < NBV; ++q) {
+    const int s = q * 16 + lk;
+    const int n = (s % NPT) * NG + ng;
+    const bool ok = n < N && (NSL % 16 == 0 || s < NSL);
+    bco[q] = ok ? ((uint32_t)(s / NPT) * Nu + (uint32_t)n) * esz : rowN_bytes;
+  }
+  uint32_t cko[NPT];  // byte offset of this lane's states within a checkpoint slot
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) cko[j] = (act && j * NG + ng < N) ? co[j] * 4u : chk_bytes;
+
+  // inputs of one chunk, loaded at the top of the iteration that consumes them
   TIO r_dr[IT], r_u[IT], r_z[IT], r_go[IT], r_y[IT], r_bv[NBV], r_cv[NBV];
   float r_hs[NPT];
-  // FULL loads (no per-element guard): all CHK steps in the sequence, all DT channels in range
-  // and N == NS; workgroup-uniform
-  const bool wg_full = d0 + DT <= D && N == NS;
-  auto load_chunk = [&](int64_t c, auto full) __attribute__((always_inline)) {
-    constexpr bool FULL = decltype(full)::value;
+  auto load_chunk = [&](int64_t c) __attribute__((always_inline)) {
     const uint32_t t0 = (uint32_t)(c * CHK);
+    const uint32_t sD = t0 * Du * esz, sN = t0 * Nu * esz;
 #pragma unroll
     for (int k = 0; k < IT; ++k) {
-      const int idx = tid + k * TH;
-      const uint32_t t = (uint32_t)(idx / DT);
-      bool v = (CHK * DT) % TH == 0 || idx < CHK * DT;
-      if (!FULL) v = v && oact && (int64_t)(t0 + t) < L;
-      const uint32_t o = (t0 + t) * Du + (uint32_t)od;
-      r_dr[k] = v ? ld32(drw, o) : io_zero<TIO>();
-      r_u[k] = v ? ld32(urw, o) : io_zero<TIO>();
-      r_z[k] = v ? ld32(zrw, o) : io_zero<TIO>();
-      r_go[k] = v ? ld32(grw, o) : io_zero<TIO>();
-      r_y[k] = v ? ld32(yrw, o) : io_zero<TIO>();
+      r_dr[k] = buf_load<TIO>(rs_dr, ov[k], sD);
+      r_u[k] = buf_load<TIO>(rs_u, ov[k], sD);
+      r_z[k] = buf_load<TIO>(rs_z, ov[k], sD);
+      r_go[k] = buf_load<TIO>(rs_go, ov[k], sD);
+      r_y[k] = buf_load<TIO>(rs_y, ov[k], sD);
     }
-    // B/C broadcast slots of this lane: slot s = i * NPT + j -> (step t0 + i, state j * NG + ng)
 #pragma unroll
-    for (int v = 0; v < NBV; ++v) {
-      const int s = v * 16 + lk;
-      const uint32_t t = (uint32_t)(s / NPT);
-      const int n = (s % NPT) * NG + ng;
-      bool ok = NSL % 16 == 0 || s < NSL;
-      if (!FULL) ok = ok && n < N && (int64_t)(t0 + t) < L;
-      const uint32_t o = (t0 + t) * Nu + (uint32_t)n;
-      r_bv[v] = ok ? ld32(brw, o) : io_zero<TIO>();
-      r_cv[v] = ok ? ld32(crw, o) : io_zero<TIO>();
+    for (int q = 0; q < NBV; ++q) {
+      r_bv[q] = buf_load<TIO>(rs_b, bco[q], sN);
+      r_cv[q] = buf_load<TIO>(rs_c, bco[q], sN);
     }
     // state entering the chunk: checkpoint slot c-1, or h0 for the first chunk
+    if (c > 0) {
+      const uint32_t sC = (uint32_t)(c - 1) * (Nu * Du) * 4u;
 #pragma unroll
-    for (int j = 0; j < NPT; ++j) {
-      const int n = j * NG + ng;
-      float v0 = 0.0f;
-      if (c > 0) {
-        if (FULL || (act && n < N)) v0 = ld32(chkb, (uint32_t)(c - 1) * (Nu * Du) + co[j]);
-      } else if (h0 && act && n < N) {
-        v0 = h0[(b * D + d) * N + n];
+      for (int j = 0; j < NPT; ++j) r_hs[j] = buf_load<float>(rs_ck, cko[j], sC);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NPT; ++j) {
+        const int n = j * NG + ng;
+        r_hs[j] = (h0 && act && n < N) ? h0[(b * D + d) * N + n] : 0.0f;
       }
-      r_hs[j] = v0;
     }
   };
-  auto load_any = [&](int64_t c) __attribute__((always_inline)) {
-    if ((c + 1) * CHK <= L && wg_full)
-      load_chunk(c, Bool<true>());
-    else
-      load_chunk(c, Bool<false>());
-  };
-  if (NC > 0) load_any(NC - 1);
 
-  float lamb[CHK][NPT], lhb[CHK][NPT], hb[CHK][NPT];
-  float o_u[IT], o_z[IT], o_sg[IT], o_go[IT], o_sd[IT], o_y[IT];
-  // Steps past the end of the sequence run as identity steps (delta = 0, gy = 0: lam = 1, no
-  // input, no injected gradient), so the sweeps need no per-step guard; only stores check len.
-  auto chunk = [&](int64_t c, int len) __attribute__((always_inline)) {
+  // per-(t, d) values the owner keeps from D to C: u, sigmoid(draw), delta, gy
+  float o_u[IT], o_sd[IT], o_dl[IT], o_gy[IT];
+  float bv[NBV], cv[NBV], hst[NPT];
+  // D: the loaded chunk c's per-(t, d) scalars into LDS, grad z out, B/C and entering state into
+  // their registers. Steps past the end of the sequence get delta = 0 and gy = 0 (identity steps
+  // with no injected gradient), so the sweeps need no per-step guard; only stores check the length.
+  auto prepare = [&](int64_t c) __attribute__((always_inline)) {
     const uint32_t t0 = (uint32_t)(c * CHK);
-    // phase 1: owner scalars into LDS
+    const int wb = (int)(c & 1);
+    const int64_t len = (L - (int64_t)t0) < CHK ? (L - (int64_t)t0) : CHK;
 #pragma unroll
     for (int k = 0; k < IT; ++k) {
       const int idx = tid + k * TH;
-      if (idx < CHK * DT) {
-        const float uu = to_f32(r_u[k]), zz = to_f32(r_z[k]), go = to_f32(r_go[k]);
-        const SoftplusParts sp = softplus_parts(to_f32(r_dr[k]));
-        const float delta = (oact && idx / DT < len) ? sp.value : 0.0f;
+      if ((CHK * DT) % TH == 0 || idx < CHK * DT) {
+        const int t = idx / DT, od = idx % DT;
+        const bool live = d0 + od < D && t < len;
+        const float xd = to_f32(r_dr[k]), uu = to_f32(r_u[k]), zz = to_f32(r_z[k]), go = to_f32(r_go[k]);
+        // softplus as the reference writes it (mamba_triton.py:75-78): log(1 + e^x), x above 20
+        // passed through; d softplus / d draw = e^x / (1 + e^x)
+        const float e = fast_exp2(fminf(xd, 20.0f) * kLog2e);
+        const float up = 1.0f + e;
+        const float delta = live ? (xd > 20.0f ? xd : __builtin_amdgcn_logf(up) * kLn2) : 0.0f;
         const float sg = sigmoid_fast(zz);
+        const float gyv = live ? go * zz * sg : 0.0f;
         o_u[k] = uu;
-        o_z[k] = zz;
-        o_sg[k] = sg;
-        o_go[k] = go;
-        o_y[k] = to_f32(r_y[k]);
-        o_sd[k] = sp.e * __builtin_amdgcn_rcpf(sp.u);  // d softplus / d draw = sigmoid(draw)
-        s_sc[idx / DT][idx % DT] = make_float4(delta, delta * uu, go * zz * sg, 0.0f);
+        o_sd[k] = e * __builtin_amdgcn_rcpf(up);
+        o_dl[k] = delta;
+        o_gy[k] = gyv;
+        gdp = fmaf(gyv, uu, gdp);
+        s_dx[t][od] = make_float2(delta, delta * uu);
+        s_gw[wb][t][od] = gyv;
+        buf_store(from_f32<TIO>(go * to_f32(r_y[k]) * sg * fmaf(zz, 1.0f - sg, 1.0f)), rs_gz, ov[k], t0 * Du * esz);
       }
     }
-    float bv[NBV], cv[NBV], hst[NPT];
 #pragma unroll
-    for (int v = 0; v < NBV; ++v) {
-      bv[v] = to_f32(r_bv[v]);
-      cv[v] = to_f32(r_cv[v]);
+    for (int q = 0; q < NBV; ++q) {
+      bv[q] = to_f32(r_bv[q]);
+      cv[q] = to_f32(r_cv[q]);
     }
 #pragma unroll
     for (int j = 0; j < NPT; ++j) hst[j] = r_hs[j];
-    // every chunk before the last is full in time
-    if (c > 0) {
-      if (wg_full)
-        load_chunk(c - 1, Bool<true>());
-      else
-        load_chunk(c - 1, Bool<false>());
-    }
-    __syncthreads();
+  };
 
-    // recompute this chunk's states into registers: lam_t, lam_t h_{t-1} and h_t
+  if (NC > 0) {
+    load_chunk(NC - 1);
+    prepare(NC - 1);
+  }
+  __syncthreads();
+
+  float lamb[CHK][NPT], lhb[CHK][NPT], hb[CHK][NPT];
+  // The forward's issue-priority rotation among the workgroups sharing a CU (every 16 chunks =
+  // 128 steps): without it the oldest workgroup races ahead and the last one finishes alone.
+  const unsigned slot = (blockIdx.x + blockIdx.y * gridDim.x) / cus;
+  for (int64_t c = NC - 1; c >= 0; --c) {
+    const int64_t r = NC - 1 - c;
+    if (C::OCC > 1 && (r & 15) == 0) set_wave_priority((slot + (unsigned)(r / 16)) % C::OCC);
+    const uint32_t t0 = (uint32_t)(c * CHK);
+    const int wb = (int)(c & 1);
+    // the previous chunk's inputs, consumed at the end of this iteration (D): loads issued and
+    // used within one iteration, so no pending load is carried around the loop
+    if (c > 0) load_chunk(c - 1);
+
+    // A: recompute this chunk's states into registers: lam_t, lam_t h_{t-1} and h_t
     {
       float hs[NPT];
 #pragma unroll
       for (int j = 0; j < NPT; ++j) hs[j] = hst[j];
 #pragma unroll
       for (int i = 0; i < CHK; ++i) {
-        const float4 sc = s_sc[i][dl];
+        const float2 sc = s_dx[i][dl];
 #pragma unroll
         for (int j = 0; j < NPT; ++j) {
           const int s = i * NPT + j;
           const float lam = fast_exp2(sc.x * A2[j]);
           lamb[i][j] = lam;
           lhb[i][j] = lam * hs[j];
-          hs[j] = lhb[i][j] + row_bcast(bv[s / 16], s % 16) * sc.y;
+          hs[j] = fmaf(row_bcast(bv[s / 16], s % 16), sc.y, lhb[i][j]);
           hb[i][j] = hs[j];
         }
       }
     }
-
-    // adjoint sweep, backwards through the chunk in sub-blocks of TB steps
+    // B: adjoint sweep backwards through the chunk
 #pragma unroll
-    for (int sb = NSB - 1; sb >= 0; --sb) {
+    for (int i = CHK - 1; i >= 0; --i) {
+      const float2 sc = s_dx[i][dl];  // (delta, delta * u)
+      const float gyv = s_gw[wb][i][dl];
+      float aq = 0.0f, gb = 0.0f;
 #pragma unroll
-      for (int ii = TB - 1; ii >= 0; --ii) {
-        const int i = sb * TB + ii;
-        const float4 sc = s_sc[i][dl];  // (delta, delta * u, gy)
-        float aq = 0.0f, gb = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NPT; ++j) {
-          const int s = i * NPT + j;
-          const float an = (i + 1 < CHK) ? lamb[(i + 1) % CHK][j] : lam_next[j];
-          G[j] = fmaf(an, G[j], row_bcast(cv[s / 16], s % 16) * sc.z);
-          const float Q = G[j] * lhb[i][j];  // G_t * lam_t h_{t-1}
-          gA[j] = fmaf(sc.x, Q, gA[j]);
-          aq = fmaf(Av[j], Q, aq);
-          gb = fmaf(row_bcast(bv[s / 16], s % 16), G[j], gb);
-          s_dp[ii][j * NG + ng][dl] = G[j] * sc.y;
-          s_dp[ii][NS + j * NG + ng][dl] = sc.z * hb[i][j];
-        }
-        s_np[ii][0][ng][dl] = aq;
-        s_np[ii][1][ng][dl] = gb;
+      for (int j = 0; j < NPT; ++j) {
+        const int s = i * NPT + j;
+        const float an = (i + 1 < CHK) ? lamb[(i + 1) % CHK][j] : lam_next[j];
+        G[j] = fmaf(an, G[j], row_bcast(cv[s / 16], s % 16) * gyv);
+        const float Q = G[j] * lhb[i][j];  // G_t * lam_t h_{t-1}
+        gA[j] = fmaf(sc.x, Q, gA[j]);
+        aq = fmaf(Av[j], Q, aq);
+        gb = fmaf(row_bcast(bv[s / 16], s % 16), G[j], gb);
+        s_dp[i][j * NG + ng][dl] = G[j] * sc.y;
+        s_dp[i][NS + j * NG + ng][dl] = hb[i][j];
       }
-      __syncthreads();
-      // owners: finish the per-(t, d) gradients of this sub-block
-#pragma unroll
-      for (int k = 0; k < IT; ++k) {
-        const int idx = tid + k * TH;
-        const int t = idx / DT;
-        if (idx < CHK * DT && t >= sb * TB && t < sb * TB + TB && t < len && oact) {
-          const int ii = t - sb * TB;
-          float aqp[NG], gbp[NG];
-#pragma unroll
-          for (int g = 0; g < NG; ++g) {
-            aqp[g] = s_np[ii][0][g][od];
-            gbp[g] = s_np[ii][1][g][od];
-          }
-          const float aq = tree_sum<NG>(aqp), gb = tree_sum<NG>(gbp);
-          const float4 sc = s_sc[t][od];
-          const float uu = o_u[k], zz = o_z[k], sg = o_sg[k];
-          const float gzv = o_go[k] * o_y[k] * sg * (1.0f + zz * (1.0f - sg));
-          const float gdelta = fmaf(uu, gb, aq);
-          const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
-          st32(gdrw, o, from_f32<TIO>(gdelta * o_sd[k]));
-          st32(gurw, o, from_f32<TIO>(fmaf(sc.x, gb, sc.z * dp_o)));
-          st32(gzrw, o, from_f32<TIO>(gzv));
-          gdp = fmaf(sc.z, uu, gdp);
-        }
-      }
-      // grad B_t / grad C_t: sum the tile's 32 channels for each (t, column); each thread
-      // reads its row as eight float4s, starting at a column-dependent eighth so that the 16
-      // lanes of one b128 pass (16 consecutive columns, rows 128 B apart) hit distinct banks
-      for (int idx = tid; idx < TB * W2; idx += TH) {
-        const int ii = idx / W2, col = idx % W2;
-        const int t = sb * TB + ii;
-        if (t < len) {
-          const float4* row = reinterpret_cast<const float4*>(&s_dp[ii][col][0]);
-          float s = 0.0f;
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const float4 v = row[(q + (col >> 1)) & 7];
-            const float part = (v.x + v.y) + (v.z + v.w);
-            s = q == 0 ? part : s + part;
-          }
-          st32(gbcb, (t0 + (uint32_t)t) * (uint32_t)W2 + (uint32_t)col, s);
-        }
-      }
-      __syncthreads();
+      s_np[i][0][ng][dl] = aq;
+      s_np[i][1][ng][dl] = gb;
     }
 #pragma unroll
     for (int j = 0; j < NPT; ++j) lam_next[j] = lamb[0][j];
-  };
-  // The forward's issue-priority rotation among the workgroups sharing a CU (every 16 chunks =
-  // 128 steps): without it the oldest workgroup races ahead and the last one finishes alone.
-  const unsigned slot = (blockIdx.x + blockIdx.y * gridDim.x) / cus;
-  for (int64_t c = NC - 1; c >= 0; --c) {
-    const int64_t r = NC - 1 - c;
-    if ((r & 15) == 0) set_wave_priority((slot + (unsigned)(r / 16)) % 3);
-    const int64_t t0 = c * CHK;
-    chunk(c, (int)((L - t0) < CHK ? (L - t0) : CHK));
+    __syncthreads();
+
+    // C: owners finish this chunk's per-(t, d) gradients
+#pragma unroll
+    for (int k = 0; k < IT; ++k) {
+      const int idx = tid + k * TH;
+      const int t = idx / DT, od = idx % DT;
+      if ((CHK * DT) % TH == 0 || idx < CHK * DT) {  // stores of steps past L or inactive channels drop
+        float aqp[NG], gbp[NG];
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          aqp[g] = s_np[t][0][g][od];
+          gbp[g] = s_np[t][1][g][od];
+        }
+        const float aq = tree_sum<NG>(aqp), gb = tree_sum<NG>(gbp);
+        buf_store(from_f32<TIO>(fmaf(o_u[k], gb, aq) * o_sd[k]), rs_gd, ov[k], t0 * Du * esz);
+        buf_store(from_f32<TIO>(fmaf(o_dl[k], gb, o_gy[k] * dp_o[k])), rs_gu, ov[k], t0 * Du * esz);
+      }
+    }
+    // grad B_t / grad C_t: the tile's DT channels of each (t, column) summed, grad C's weighted
+    // by the channel's gy (grad B's terms carry delta u already). Items are ordered grad B first,
+    // so for NS >= 8 every wave takes one kind (no divergence). Each thread reads its row as DT/4
+    // float4s starting at a column-dependent offset, so that the lanes of one b128 pass
+    // (consecutive columns, rows a multiple of 128 B apart) hit distinct banks.
+    for (int idx = tid; idx < CHK * W2; idx += TH) {
+      const int half = idx / (CHK * NS), r = idx % (CHK * NS);
+      const int ii = r / NS, c = r % NS, col = half * NS + c;
+      const float4* row = reinterpret_cast<const float4*>(&s_dp[ii][col][0]);
+      constexpr int NQ = DT / 4;
+      float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (half == 0) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const float4 v = row[(q + (c >> 1)) % NQ];
+          part[q & 3] += (v.x + v.y) + (v.z + v.w);
+        }
+      } else {
+        const float4* wrow = reinterpret_cast<const float4*>(&s_gw[wb][ii][0]);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const int f = (q + (c >> 1)) % NQ;
+          const float4 v = row[f], w = wrow[f];
+          part[q & 3] = fmaf(v.x, w.x, fmaf(v.y, w.y, fmaf(v.z, w.z, fmaf(v.w, w.w, part[q & 3]))));
+        }
+      }
+      // rows past the end of the sequence fall beyond the partials' resource
+      buf_store((part[0] + part[1]) + (part[2] + part[3]), rs_pt, ((uint32_t)ii * W2 + (uint32_t)col) * 4u,
+                t0 * (uint32_t)W2 * 4u);
+    }
+    // D: the previous chunk's inputs (loaded during this one) into place
+    if (c > 0) prepare(c - 1);
+    __syncthreads();
   }
 
   if (act) {
@@ -637,13 +689,12 @@ __global__ void __launch_bounds__(MCfg<NS>::TH, 3) mamba_bwd_kernel(
     for (int j = 0; j < NPT; ++j)
       if (j * NG + ng < N) gh0[(b * D + d) * N + j * NG + ng] = lam_next[j] * G[j];
   }
-  // gDp: every owner thread of channel od holds a partial; sum them through LDS
-  __syncthreads();
+  // gDp: every owner thread of channel od holds a partial; sum them through LDS (in a fixed order)
   float* red = &s_dp[0][0][0];
-  static_assert(TB * W2 * DT >= TH, "reduction scratch too small");
+  static_assert(CHK * W2 * DT >= TH, "reduction scratch too small");
   red[tid] = gdp;
   __syncthreads();
-  if (tid < DT && oact) {
+  if (tid < DT && d0 + tid < D) {
     float s = 0.0f;
     for (int k = tid; k < TH; k += DT) s += red[k];
     gDp_part[b * D + d0 + tid] = s;
@@ -697,11 +748,28 @@ int launch_fwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
   return tsf_launch_status();
 }
 
+// Channel tile of the backward. (A 96-channel tile, one 12-wave workgroup per CU with a third of
+// the grad-B/C partials, measured 16% slower at config 3: with one workgroup per CU nothing runs
+// while its waves wait at the chunk barriers.)
+constexpr int kBwdDT = 32;
+
 template <int NS>
 int64_t bwd_workspace_floats(int64_t B, int64_t L, int64_t D, int64_t N) {
-  using C = MCfg<NS>;
-  const int64_t nT = (D + C::DT - 1) / C::DT;
+  const int64_t nT = (D + kBwdDT - 1) / kBwdDT;
   return nT * B * L * 2 * NS + B * D * N + B * D;
+}
+
+template <typename TIO, int NS, int DT>
+void launch_bwd_tile(int64_t B, int64_t L, int64_t D, int64_t N, int64_t NC, const void* draw, const float* A,
+                     const void* Bt, const void* Ct, const void* u, const void* z, const float* Dp, const float* h0,
+                     const float* chk, const void* gout, const float* ghlast, void* gdraw, void* gu, void* gz,
+                     float* gA_part, float* gDp_part, float* gBC_part, float* gh0, hipStream_t s) {
+  using C = BCfg<NS, DT>;
+  const int64_t nT = (D + DT - 1) / DT;
+  hipLaunchKernelGGL((mamba_bwd_kernel<TIO, NS, DT>), dim3((unsigned)nT, (unsigned)B), dim3(C::TH), 0, s,
+                     (const TIO*)draw, A, (const TIO*)Bt, (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, chk,
+                     (const TIO*)gout, ghlast, (TIO*)gdraw, (TIO*)gu, (TIO*)gz, gA_part, gDp_part, gBC_part, gh0, B,
+                     L, D, (int)N, NC, device_cus());
 }
 
 template <typename TIO, int NS>
@@ -711,16 +779,13 @@ int launch_bwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
                float* gDp, float* gh0, void* workspace, hipStream_t s) {
   using C = MCfg<NS>;
   const int64_t NC = (L + C::CHK - 1) / C::CHK;
-  const int64_t nT = (D + C::DT - 1) / C::DT;
+  const int64_t nT = (D + kBwdDT - 1) / kBwdDT;
   float* gBC_part = static_cast<float*>(workspace);
   float* gA_part = gBC_part + nT * B * L * 2 * NS;
   float* gDp_part = gA_part + B * D * N;
-  dim3 grid((unsigned)nT, (unsigned)B);
   if (B > 0 && D > 0)
-    hipLaunchKernelGGL((mamba_bwd_kernel<TIO, NS>), grid, dim3(C::TH), 0, s, (const TIO*)draw, A, (const TIO*)Bt,
-                       (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, chk, (const TIO*)gout, ghlast,
-                       (TIO*)gdraw, (TIO*)gu, (TIO*)gz, gA_part, gDp_part, gBC_part, gh0, B, L, D, (int)N, NC,
-                       device_cus());
+    launch_bwd_tile<TIO, NS, kBwdDT>(B, L, D, N, NC, draw, A, Bt, Ct, u, z, Dp, h0, chk, gout, ghlast, gdraw, gu, gz,
+                                     gA_part, gDp_part, gBC_part, gh0, s);
   const int64_t BLN = B * L * N;
   if (BLN > 0)
     hipLaunchKernelGGL((mamba_reduce_bc<TIO>), dim3((unsigned)((BLN + 255) / 256)), dim3(256), 0, s, gBC_part,
@@ -778,13 +843,13 @@ int bwd_bf16(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, const
                               gz, gDp, gh0, ws, s);
 }
 
-// The kernels index one batch row with 32-bit element offsets (t * D + d, t * N + n).
-// Per-row accesses use 32-bit byte offsets from a per-workgroup base: one batch row of every
-// [B, L, *] tensor (fp32 at most, the last chunk's identity steps included), one batch row of
-// the saved state (checkpoints [NC, N, D] and y [L, D]) and of the grad-B/C partials [L, 2*NS]
-// must stay below 4 GiB.
+// The kernels index one batch row with 32-bit byte offsets from a per-workgroup base, and the
+// backward streams rows through buffer resources whose size is a signed 32-bit byte count: one
+// batch row of every [B, L, *] tensor (fp32 at most, the last chunk's identity steps included),
+// one batch row of the saved state (checkpoints [NC, N, D] and y [L, D]) and of the grad-B/C
+// partials [L, 2*NS] must stay below 2 GiB. (mamba_hip.supports repeats this test.)
 bool offsets_fit(int64_t L, int64_t D, int64_t N, int64_t chk_interval) {
-  const int64_t lim = ((int64_t)1 << 32) / 4;  // fp32 elements
+  const int64_t lim = ((int64_t)1 << 31) / 4;  // fp32 elements
   const int64_t nc = (L + chk_interval - 1) / chk_interval;
   return (L + 64) * D < lim && (L + 64) * 2 * ns_for(N) < lim && nc * N * D + L * D < lim;
 }
@@ -832,6 +897,7 @@ int64_t tsfast_hip_mamba_chk_interval(int64_t N) { return chk_interval_for(ns_fo
 int64_t tsfast_hip_mamba_saved_floats(int64_t L, int64_t D, int64_t N, int io_dtype) {
   const int ns = ns_for(N);
   if (ns == 0 || N < 1 || L < 0 || D < 0) return -1;
+  if (!offsets_fit(L, D, N, chk_interval_for(ns))) return -1;
   const int64_t nc = (L + chk_interval_for(ns) - 1) / chk_interval_for(ns);
   if (io_dtype == TSF_DTYPE_F32) return saved_row_floats<float>(L, D, N, nc);
   if (io_dtype == TSF_DTYPE_BF16) return saved_row_floats<bf16>(L, D, N, nc);

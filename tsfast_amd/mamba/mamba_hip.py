@@ -28,6 +28,25 @@ _IO_DTYPES = {torch.float32: _lib.TSF_DTYPE_F32, torch.bfloat16: _lib.TSF_DTYPE_
 _MAX_N = 64
 
 
+def _state_tile(N: int) -> int:
+    """N rounded up to the kernels' state tile (4, 8, 16, 32 or 64)."""
+    return next(k for k in (4, 8, 16, 32, 64) if N <= k)
+
+
+def _chk_steps(N: int) -> int:
+    """Checkpoint interval for state size N (the kernels' MCfg<NS>::CHK; tests pin it against
+    tsfast_hip_mamba_chk_interval). Kept in Python so that supports() makes no library call."""
+    return 4 if _state_tile(N) == 64 else 8
+
+
+def _rows_fit(L: int, D: int, N: int) -> bool:
+    """The kernels' per-batch-row addressing limit (mamba.hip offsets_fit): one row of every
+    [B, L, *] tensor, of the saved state and of the grad-B/C partials below 2 GiB of fp32."""
+    lim = (1 << 31) // 4
+    nc = -(-L // _chk_steps(N))
+    return (L + 64) * D < lim and (L + 64) * 2 * _state_tile(N) < lim and nc * N * D + L * D < lim
+
+
 def chk_interval(N: int) -> int:
     """Checkpoint interval (steps) the kernels use for state size N."""
     return int(_lib.load().tsfast_hip_mamba_chk_interval(N))
@@ -70,6 +89,8 @@ def supports(draw, A, Bt, Ct, u, z, Dp, h0) -> str | None:
         return f"state size N={N} outside [1, {_MAX_N}]"
     if B > 65535:
         return f"batch {B} above the 65535 grid limit"
+    if not _rows_fit(L, D, N):
+        return f"one batch row (L={L}, D={D}, N={N}) exceeds the kernels' 2 GiB per-row addressing"
     if tuple(u.shape) != (B, L, D) or tuple(z.shape) != (B, L, D):
         return f"u/z shapes {tuple(u.shape)}/{tuple(z.shape)} != {(B, L, D)}"
     if tuple(Bt.shape) != (B, L, N) or tuple(Ct.shape) != (B, L, N):
