@@ -112,3 +112,13 @@ def test_mamba_supports_mirrors_the_kernel_size_limits(lib):
         for L in (1, 4096, 349_000, 349_400, 349_460, 349_500, 349_600, 400_000):
             c_ok = lib.tsfast_hip_mamba_saved_floats(L, 1536, N, 0) >= 0
             assert mamba_hip._rows_fit(L, 1536, N) == c_ok, (L, N)
+
+
+def test_mamba_saved_floats_formula_matches_the_library(lib):
+    import torch
+
+    from tsfast_amd.mamba import mamba_hip
+
+    for L, D, N in ((1, 1, 1), (45, 40, 16), (4096, 1536, 16), (33, 16, 8), (1000, 70, 64), (7, 8, 33)):
+        for dt, code in ((torch.float32, 0), (torch.bfloat16, 1)):
+            assert mamba_hip.saved_floats(L, D, N, dt) == lib.tsfast_hip_mamba_saved_floats(L, D, N, code)

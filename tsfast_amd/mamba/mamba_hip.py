@@ -54,8 +54,13 @@ def chk_interval(N: int) -> int:
 
 def saved_floats(L: int, D: int, N: int, dtype: torch.dtype = torch.float32) -> int:
     """float32 words of training-forward saved state per batch row for I/O dtype ``dtype``:
-    fp32 checkpoints [NC, N, D], then the pre-gate output y [L, D] in ``dtype``."""
-    return int(_lib.load().tsfast_hip_mamba_saved_floats(L, D, N, _IO_DTYPES[dtype]))
+    fp32 checkpoints [NC, N, D], then the pre-gate output y [L, D] in ``dtype`` (padded to whole
+    words). Computed here rather than through the library, so that the training op's fake
+    implementation makes no library call while torch.compile traces it (tests pin this formula
+    against tsfast_hip_mamba_saved_floats)."""
+    nc = -(-L // _chk_steps(N))
+    esz = 2 if dtype == torch.bfloat16 else 4
+    return nc * N * D + (L * D * esz + 3) // 4
 
 
 def supports(draw, A, Bt, Ct, u, z, Dp, h0) -> str | None:
