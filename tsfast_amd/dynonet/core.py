@@ -149,14 +149,14 @@ def linear_dynamical_operator(
     O, _, nb = b_coeff.shape
     na = a_coeff.shape[-1]
     P = I * O
-    match state:
-        case {"u": u_tail, "x": x0}:
-            pass
-        case None:
-            u_tail = u.new_zeros(B, nb - 1, I)
-            x0 = u.new_zeros(B, P, na)
-        case _:
-            raise TypeError(f"expected state dict {{'u': tensor, 'x': tensor}}, got {type(state)}")
+    # plain branches, not a mapping `match`: Dynamo cannot trace mapping patterns
+    if state is None:
+        u_tail = u.new_zeros(B, nb - 1, I)
+        x0 = u.new_zeros(B, P, na)
+    elif isinstance(state, dict) and "u" in state and "x" in state:
+        u_tail, x0 = state["u"], state["x"]
+    else:
+        raise TypeError(f"expected state dict {{'u': tensor, 'x': tensor}}, got {type(state)}")
     order = ("hip",) if u.device.type == "cuda" else ()
     mod = resolve("dynonet.gblock", _GBLOCK_BACKENDS, order, (u, b_coeff, a_coeff, u_tail, x0))
     if mod is not None:

@@ -105,10 +105,13 @@ def _gblock_op(
 
 @_gblock_op.register_fake
 def _(u, b, a, u_tail, x0):
-    B, L, _ = u.shape
+    B, L, I = u.shape
     O = b.shape[0]
-    P, na = u.shape[-1] * O, a.shape[-1]
-    return u.new_empty(B, L, O), u.new_empty(B, P, na), u.new_empty(1, dtype=torch.float64)
+    na = a.shape[-1]
+    # the saved boundary states must have the size the real op allocates, or a compiled graph's
+    # metadata disagrees with what the kernel writes
+    n_saved = _lib.load().tsfast_hip_gblock_saved_doubles(int(B), int(L), int(I), int(O), int(na))
+    return u.new_empty(B, L, O), u.new_empty(B, I * O, na), u.new_empty(max(n_saved, 1), dtype=torch.float64)
 
 
 @torch.library.custom_op("tsfast_hip::dynonet_gblock_bwd", mutates_args=())
