@@ -204,6 +204,27 @@ int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, c
                           const float* x0, float* gA, float* gv, float* gx0, void* workspace, int64_t workspace_bytes,
                           void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Projected complex diagonal scan, the LRU / S5 layer core in one pass:
+ *   v_t = W u_t,  x_t = lam * x_{t-1} + v_t (x_{-1} = x0, zero when NULL),  y_t = Re(C x_t).
+ * Replaces the composition complex_in_proj -> diagonal_recurrence -> real_out_proj
+ * (tsfast/models/_core/scan.py:221-243, 272-313) as LRU.forward (architectures/lru.py:100-110)
+ * and S5.forward (architectures/s5.py:180-198) call it, plus the returned state x[..., -1, :].
+ * Layout: u [B, L, H] float32; w_re/w_im [N, H]; lam [N] complex64 (interleaved re, im);
+ * c_re/c_im [O, N]; x0 and x_last [B, N] complex64; y [B, L, O] float32; all contiguous.
+ * Limits: H <= 32, N <= 256, O <= 32 and B * L * H * 4 < 2^31, else TSF_ERR_UNSUPPORTED.
+ * saved (may be NULL) receives the state entering each 64-step chunk, [B, ceil(L/64), N]
+ * complex64 (tsfast_hip_projscan_saved_floats floats), for the backward pass. The workspace holds
+ * the look-back words, re-initialised by each call on its stream: two calls in flight must not
+ * share one.
+ */
+int64_t tsfast_hip_projscan_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t N, int64_t O);
+int64_t tsfast_hip_projscan_saved_floats(int64_t B, int64_t L, int64_t N);
+int tsfast_hip_projscan_fwd(int64_t B, int64_t L, int64_t H, int64_t N, int64_t O, const float* u, const float* w_re,
+                            const float* w_im, const void* lam, const float* c_re, const float* c_im, const void* x0,
+                            float* y, void* x_last, float* saved, void* workspace, int64_t workspace_bytes,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

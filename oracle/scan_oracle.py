@@ -42,6 +42,10 @@ __all__ = [
     "gblock_backward",
     "linrec_forward",
     "linrec_backward",
+    "complex_in_proj",
+    "real_out_proj",
+    "projscan_forward",
+    "projscan_backward",
 ]
 
 
@@ -404,3 +408,53 @@ def linrec_backward(g, A, out, x0=None):
     if x0 is not None:
         gx0 = np.einsum("mji,mj->mi", A, G[:, 0]) if L > 0 else np.zeros((M, n))
     return gA, G, gx0
+
+
+# --------------------------------------------------------------------------- projected diagonal scan (LRU / S5 core)
+def complex_in_proj(u, W_re, W_im):
+    """``u @ (W_re + i W_im)^T``: real ``u [..., d]``, weights ``[n, d]`` -> complex ``[..., n]``
+    (tsfast/models/_core/scan.py:272-291)."""
+    return _hi(u) @ (_hi(W_re) + 1j * _hi(W_im)).T
+
+
+def real_out_proj(x, W_re, W_im):
+    """``Re(x @ (W_re + i W_im)^T)``: complex ``x [..., n]``, weights ``[o, n]`` -> real ``[..., o]``
+    (tsfast/models/_core/scan.py:294-313)."""
+    return (_hi(x) @ (_hi(W_re) + 1j * _hi(W_im)).T).real
+
+
+def projscan_forward(u, W_re, W_im, lam, C_re, C_im, x0=None):
+    """The LRU / S5 layer core as the reference composes it (lru.py:100-110, s5.py:180-198):
+    ``v = complex_in_proj(u, W)``, ``x = diagonal_recurrence(lam, v, x0)`` with ``lam [n]`` shared
+    by every row, ``y = real_out_proj(x, C)``. u [B, L, d]; returns ``(y [B, L, o], x [B, L, n])``
+    (the states, whose last step is the layer's returned state)."""
+    v = complex_in_proj(u, W_re, W_im)
+    Bsz, L, n = v.shape
+    lanes = np.broadcast_to(_hi(lam), (Bsz, n))
+    x = diag_forward(lanes, v, x0)
+    return real_out_proj(x, C_re, C_im), x
+
+
+def projscan_backward(gy, g_xlast, u, W_re, W_im, lam, C_re, C_im, x, x0=None):
+    """Adjoint of :func:`projscan_forward` given the upstream ``gy [B, L, o]`` and the gradient
+    ``g_xlast [B, n]`` of the returned last state (None for zero), in torch's convention.
+
+    ``g_x = gy @ conj(C)`` (+ ``g_xlast`` at the last step); ``G`` = the diagonal adjoint scan of
+    ``g_x``; ``g_u = Re(G @ conj(W))``; ``g_W_re = sum G_re u^T``, ``g_W_im = sum G_im u^T``;
+    ``g_C_re = sum gy Re(x)^T``, ``g_C_im = -sum gy Im(x)^T``; ``g_lam = sum_{b,t} G_t conj(x_{t-1})``;
+    ``g_x0 = conj(lam) G_0``. Returns ``(g_u, g_W_re, g_W_im, g_lam, g_C_re, g_C_im, g_x0)``."""
+    gy, u, x = _hi(gy), _hi(u), _hi(x)
+    W = _hi(W_re) + 1j * _hi(W_im)
+    C = _hi(C_re) + 1j * _hi(C_im)
+    gx = gy @ np.conj(C)
+    if g_xlast is not None and gx.shape[1] > 0:
+        gx[:, -1] += _hi(g_xlast)
+    Bsz, L, n = x.shape
+    lanes = np.broadcast_to(_hi(lam), (Bsz, n))
+    glam_rows, G, gx0 = diag_backward(gx, lanes, x, x0)
+    g_u = (G @ np.conj(W)).real
+    g_W_re = np.einsum("bln,bld->nd", G.real, u)
+    g_W_im = np.einsum("bln,bld->nd", G.imag, u)
+    g_C_re = np.einsum("blo,bln->on", gy, x.real)
+    g_C_im = -np.einsum("blo,bln->on", gy, x.imag)
+    return g_u, g_W_re, g_W_im, glam_rows.sum(0), g_C_re, g_C_im, gx0

@@ -673,3 +673,107 @@ def test_linrec_blocked_scan_matches_oracle():
     assert O.rel_err(At.grad.numpy(), gA.reshape(Bb, P, n, n).sum(0)) < TOL
     assert O.rel_err(vt.grad.numpy().reshape(Bb * P, L, n), gv) < TOL
     assert O.rel_err(x0t.grad.numpy().reshape(Bb * P, n), gx0) < TOL
+
+
+# ------------------------------------------------------------------------ projected diagonal scan
+def _torch_projscan_loop(u, W_re, W_im, lam, C_re, C_im, x0):
+    W = torch.complex(W_re, W_im)
+    C = torch.complex(C_re, C_im)
+    x = torch.zeros(u.shape[0], W.shape[0], dtype=torch.complex128) if x0 is None else x0
+    ys = []
+    for t in range(u.shape[1]):
+        x = lam * x + u[:, t].to(torch.complex128) @ W.T
+        ys.append((x @ C.T).real)
+    return torch.stack(ys, 1), x
+
+
+def check_projscan(fwd, bwd):
+    """Forward: the closed form ``y_t = Re C (lam^(t+1) x0 + sum_{s<=t} lam^(t-s) W u_s)`` with
+    explicit powers. Backward: torch float64/complex128 autograd through a per-step loop, for
+    the upstream gradient of y and of the returned last state (all seven gradients)."""
+    rng = _rng(14)
+    for Bsz, L, d, n, o, with_x0 in ((2, 7, 3, 4, 2, True), (1, 1, 2, 3, 3, True), (3, 5, 4, 2, 5, False)):
+        u = rng.standard_normal((Bsz, L, d))
+        W_re, W_im = rng.standard_normal((n, d)), rng.standard_normal((n, d))
+        lam = rng.uniform(0.5, 0.95, n) * np.exp(1j * rng.uniform(0, np.pi, n))
+        C_re, C_im = rng.standard_normal((o, n)), rng.standard_normal((o, n))
+        x0 = _cplx(rng, Bsz, n) if with_x0 else None
+        W, C = W_re + 1j * W_im, C_re + 1j * C_im
+        want = np.zeros((Bsz, L, o))
+        for b in range(Bsz):
+            for t in range(L):
+                state = sum(lam ** (t - s) * (W @ u[b, s]) for s in range(t + 1))
+                if with_x0:
+                    state = state + lam ** (t + 1) * x0[b]
+                want[b, t] = (C @ state).real
+        y, x = fwd(u, W_re, W_im, lam, C_re, C_im, x0)
+        if O.rel_err(y, want) > TOL:
+            return False
+        gy, g_xl = rng.standard_normal((Bsz, L, o)), _cplx(rng, Bsz, n)
+        want_g = _vjp(_torch_projscan_loop, [u, W_re, W_im, lam, C_re, C_im, x0], (gy, g_xl))
+        got = bwd(gy, g_xl, u, W_re, W_im, lam, C_re, C_im, x, x0)
+        for gw, gg in zip(want_g, got):
+            if gw is not None and O.rel_err(gg, gw) > TOL:
+                return False
+    return True
+
+
+def test_projscan_closed_form_and_autograd():
+    assert check_projscan(O.projscan_forward, O.projscan_backward)
+
+
+def test_projections_match_interleaved_real_gemm():
+    """complex_in_proj / real_out_proj as the reference computes them: one real GEMM against
+    the interleaved weight ``[d, 2n]`` (re, im per state) read as complex pairs, and one real
+    GEMM of the interleaved state against ``[o, 2n]`` with ``-W_im`` in the odd columns."""
+    rng = _rng(15)
+    u = rng.standard_normal((2, 5, 3))
+    W_re, W_im = rng.standard_normal((4, 3)), rng.standard_normal((4, 3))
+    inter = np.stack((W_re, W_im), -1).transpose(1, 0, 2).reshape(3, 8)
+    v = (u @ inter).reshape(2, 5, 4, 2)
+    assert O.rel_err(O.complex_in_proj(u, W_re, W_im), v[..., 0] + 1j * v[..., 1]) < TOL
+    x = _cplx(rng, 2, 5, 4)
+    C_re, C_im = rng.standard_normal((6, 4)), rng.standard_normal((6, 4))
+    Wo = np.stack((C_re, -C_im), -1).reshape(6, 8)
+    xr = np.stack((x.real, x.imag), -1).reshape(2, 5, 8)
+    assert O.rel_err(O.real_out_proj(x, C_re, C_im), xr @ Wo.T) < TOL
+
+
+def _projscan_fwd_readout_conj(u, W_re, W_im, lam, C_re, C_im, x0=None):
+    y, x = O.projscan_forward(u, W_re, W_im, lam, C_re, C_im, x0)
+    return O.real_out_proj(x, C_re, -np.asarray(C_im)), x
+
+
+def _projscan_bwd_gu_no_conj(gy, g_xl, u, W_re, W_im, lam, C_re, C_im, x, x0=None):
+    r = list(O.projscan_backward(gy, g_xl, u, W_re, W_im, lam, C_re, C_im, x, x0))
+    r[0] = O.projscan_backward(gy, g_xl, u, W_re, -np.asarray(W_im), lam, C_re, C_im, x, x0)[0]
+    return tuple(r)
+
+
+def _projscan_bwd_gc_im_sign(gy, g_xl, u, W_re, W_im, lam, C_re, C_im, x, x0=None):
+    r = list(O.projscan_backward(gy, g_xl, u, W_re, W_im, lam, C_re, C_im, x, x0))
+    r[5] = -r[5]
+    return tuple(r)
+
+
+def _projscan_bwd_glam_current_state(gy, g_xl, u, W_re, W_im, lam, C_re, C_im, x, x0=None):
+    r = list(O.projscan_backward(gy, g_xl, u, W_re, W_im, lam, C_re, C_im, x, x0))
+    G = O.diag_backward(np.asarray(gy) @ np.conj(np.asarray(C_re) + 1j * np.asarray(C_im)), np.broadcast_to(lam, x.shape[::2]), x, x0)[1]
+    r[3] = (G * np.conj(x)).sum((0, 1))
+    return tuple(r)
+
+
+def _projscan_bwd_no_state_grad(gy, g_xl, u, W_re, W_im, lam, C_re, C_im, x, x0=None):
+    return O.projscan_backward(gy, None, u, W_re, W_im, lam, C_re, C_im, x, x0)
+
+
+def test_projscan_check_rejects_forward():
+    assert not check_projscan(_projscan_fwd_readout_conj, O.projscan_backward)
+
+
+@pytest.mark.parametrize(
+    "mutant",
+    [_projscan_bwd_gu_no_conj, _projscan_bwd_gc_im_sign, _projscan_bwd_glam_current_state, _projscan_bwd_no_state_grad],
+)
+def test_projscan_check_rejects_backward(mutant):
+    assert not check_projscan(O.projscan_forward, mutant)

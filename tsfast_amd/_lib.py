@@ -57,6 +57,11 @@ _SIGNATURES: dict[str, tuple[list, object]] = {
     "tsfast_hip_linrec_workspace_bytes": ([_i64] * 3, _i64),
     "tsfast_hip_linrec_fwd": ([_i64] * 3 + [_ptr] * 5 + [_i64, _ptr], _int),
     "tsfast_hip_linrec_bwd": ([_i64] * 3 + [_ptr] * 8 + [_i64, _ptr], _int),
+    "tsfast_hip_projscan_workspace_bytes": ([_i64] * 5, _i64),
+    "tsfast_hip_projscan_saved_floats": ([_i64] * 3, _i64),
+    "tsfast_hip_projscan_fwd": ([_i64] * 5 + [_ptr] * 11 + [_i64, _ptr], _int),
+    "tsfast_hip_projscan_bwd_workspace_bytes": ([_i64] * 5, _i64),
+    "tsfast_hip_projscan_bwd": ([_i64] * 5 + [_ptr] * 17 + [_i64, _ptr], _int),
 }
 
 TSF_DTYPE_F32 = 0
