@@ -213,7 +213,7 @@ int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, c
  * Layout: u [B, L, H] float32; w_re/w_im [N, H]; lam [N] complex64 (interleaved re, im);
  * c_re/c_im [O, N]; x0 and x_last [B, N] complex64; y [B, L, O] float32; all contiguous.
  * Limits: H <= 32, N <= 256, O <= 32 and B * L * H * 4 < 2^31, else TSF_ERR_UNSUPPORTED.
- * saved (may be NULL) receives the state entering each 64-step chunk, [B, ceil(L/64), N]
+ * saved (may be NULL) receives the state entering each 32-step sub-chunk, [B, ceil(L/32), N]
  * complex64 (tsfast_hip_projscan_saved_floats floats), for the backward pass. The workspace holds
  * the look-back words, re-initialised by each call on its stream: two calls in flight must not
  * share one.
@@ -224,6 +224,17 @@ int tsfast_hip_projscan_fwd(int64_t B, int64_t L, int64_t H, int64_t N, int64_t 
                             const float* w_im, const void* lam, const float* c_re, const float* c_im, const void* x0,
                             float* y, void* x_last, float* saved, void* workspace, int64_t workspace_bytes,
                             void* stream);
+/* Adjoint of tsfast_hip_projscan_fwd (the autograd of the same reference composition):
+ * gy [B, L, O] float32, g_xlast [B, N] complex64 (gradient of the returned state; NULL = zero),
+ * saved = the forward's saved states. Writes g_u [B, L, H], g_w_re/g_w_im [N, H], g_lam [N]
+ * complex64 (summed over rows), g_c_re/g_c_im [O, N], and g_x0 [B, N] complex64 when non-NULL.
+ * Parameter gradients are per-workgroup partial sums added in a fixed workgroup order. */
+int64_t tsfast_hip_projscan_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t N, int64_t O);
+int tsfast_hip_projscan_bwd(int64_t B, int64_t L, int64_t H, int64_t N, int64_t O, const float* gy,
+                            const void* g_xlast, const float* saved, const float* u, const float* w_re,
+                            const float* w_im, const void* lam, const float* c_re, const float* c_im, float* g_u,
+                            float* g_w_re, float* g_w_im, void* g_lam, float* g_c_re, float* g_c_im, void* g_x0,
+                            void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }
