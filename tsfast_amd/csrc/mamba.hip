@@ -29,7 +29,8 @@
 //    backwards through the chunk, so exp is evaluated once per element per pass; the gate
 //    gradient reads the forward's saved pre-gate output y instead of recomputing sum_n h C.
 //  * grad B_t / grad C_t (sums over channels) are reduced over the 32 channels of the tile in
-//    LDS and written as fp32 partials [D/32, B, L, 2*NS]; a second kernel sums the partials in a
+//    LDS and written as partials [D/32, B, L, 2*NS] in the I/O type (the reference keeps its
+//    per-block partials in the I/O dtype too); a second kernel sums the partials in fp32 in a
 //    fixed order (no atomics: deterministic run to run).
 // The next chunk's inputs are loaded into registers while the current chunk computes.
 #include <type_traits>
@@ -296,29 +297,34 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
         load_chunk(t1, Bool<false>());
     }
     __syncthreads();
-    // phase 2: the recurrence, NPT states per lane. LDS operands are read kRd steps ahead of
-    // their use, and the step body has no branch (every lane stores its own y partial), so the
-    // reads of later steps overlap the arithmetic of earlier ones.
+    // phase 2: the recurrence, NPT states per lane, in batches of kRd steps. The LDS operands
+    // of the next batch are read while the current batch computes (two register buffers), and
+    // the step body has no branch (every lane stores its own y partial).
     constexpr int kRd = NPT <= 2 ? TSF_MAMBA_FWD_RD : 2;
     static_assert(TF % kRd == 0 && CHK % kRd == 0, "read batches must not straddle checkpoints");
-#pragma unroll
-    for (int i0 = 0; i0 < TF; i0 += kRd) {
-      float2 sv[kRd], bcv[kRd][NPT];
+    float2 sv[2][kRd], bcv[2][kRd][NPT];
+    auto read_batch = [&](int buf, int i0) __attribute__((always_inline)) {
 #pragma unroll
       for (int r = 0; r < kRd; ++r) {
-        sv[r] = s_sc[i0 + r][dl];
+        sv[buf][r] = s_sc[i0 + r][dl];
 #pragma unroll
-        for (int j = 0; j < NPT; ++j) bcv[r][j] = s_bc[i0 + r][n0 + j];
+        for (int j = 0; j < NPT; ++j) bcv[buf][r][j] = s_bc[i0 + r][n0 + j];
       }
+    };
+    read_batch(0, 0);
+#pragma unroll
+    for (int i0 = 0; i0 < TF; i0 += kRd) {
+      const int cur = (i0 / kRd) & 1;
+      if (i0 + kRd < TF) read_batch(cur ^ 1, i0 + kRd);
 #pragma unroll
       for (int r = 0; r < kRd; ++r) {
         const int i = i0 + r;
         float y = 0.0f;
 #pragma unroll
         for (int j = 0; j < NPT; ++j) {
-          const float lam = fast_exp2(sv[r].x * A2[j]);
-          h[j] = fmaf(lam, h[j], sv[r].y * bcv[r][j].x);
-          y = fmaf(h[j], bcv[r][j].y, y);
+          const float lam = fast_exp2(sv[cur][r].x * A2[j]);
+          h[j] = fmaf(lam, h[j], sv[cur][r].y * bcv[cur][r][j].x);
+          y = fmaf(h[j], bcv[cur][r][j].y, y);
         }
         s_y[i][ng][dl ^ ((ng & 1) << 4)] = y;
       }
@@ -402,7 +408,7 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
     const TIO* __restrict__ Ct, const TIO* __restrict__ u, const TIO* __restrict__ z, const float* __restrict__ Dp,
     const float* __restrict__ h0, const float* __restrict__ saved, const TIO* __restrict__ gout,
     const float* __restrict__ ghlast, TIO* __restrict__ gdraw, TIO* __restrict__ gu, TIO* __restrict__ gz,
-    float* __restrict__ gA_part, float* __restrict__ gDp_part, float* __restrict__ gBC_part, float* __restrict__ gh0,
+    float* __restrict__ gA_part, float* __restrict__ gDp_part, TIO* __restrict__ gBC_part, float* __restrict__ gh0,
     int64_t B, int64_t L, int64_t D, int N, int64_t NC, unsigned cus) {
   using C = BCfg<NS, DT_>;
   constexpr int NPT = C::NPT, NG = C::NG, DT = C::DT, TH = C::TH, CHK = C::CHK, IT = C::IT;
@@ -461,7 +467,7 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
   const Rsrc rs_gz = make_rsrc(gz + rowD, rowD_bytes);
   const Rsrc rs_b = make_rsrc(Bt + rowN, rowN_bytes), rs_c = make_rsrc(Ct + rowN, rowN_bytes);
   const Rsrc rs_ck = make_rsrc(svb + d0, chk_bytes);
-  const Rsrc rs_pt = make_rsrc(gBC_part + (tile * B + b) * L * W2, (uint32_t)(L * W2 * 4));  // [L, 2*NS] partials
+  const Rsrc rs_pt = make_rsrc(gBC_part + (tile * B + b) * L * W2, (uint32_t)(L * W2 * esz));  // [L, 2*NS] partials
 
   // owner items: item k of this thread is (t = idx / DT, channel d0 + idx % DT), idx = tid + k * TH
   float dp_o[IT];
@@ -670,8 +676,8 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
         }
       }
       // rows past the end of the sequence fall beyond the partials' resource
-      buf_store((part[0] + part[1]) + (part[2] + part[3]), rs_pt, ((uint32_t)ii * W2 + (uint32_t)col) * 4u,
-                t0 * (uint32_t)W2 * 4u);
+      buf_store(from_f32<TIO>((part[0] + part[1]) + (part[2] + part[3])), rs_pt,
+                ((uint32_t)ii * W2 + (uint32_t)col) * esz, t0 * (uint32_t)W2 * esz);
     }
     // D: the previous chunk's inputs (loaded during this one) into place
     if (c > 0) prepare(c - 1);
@@ -701,9 +707,9 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
   }
 }
 
-// gBt/gCt: sum the per-tile partials [nT, B, L, 2*NS] over the channel tiles, in order.
+// gBt/gCt: sum the per-tile partials [nT, B, L, 2*NS] over the channel tiles, in order, in fp32.
 template <typename TIO>
-__global__ void __launch_bounds__(256) mamba_reduce_bc(const float* __restrict__ part, TIO* __restrict__ gBt,
+__global__ void __launch_bounds__(256) mamba_reduce_bc(const TIO* __restrict__ part, TIO* __restrict__ gBt,
                                                        TIO* __restrict__ gCt, int64_t nT, int64_t BL, int N,
                                                        int NS) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // over BL * N
@@ -712,9 +718,9 @@ __global__ void __launch_bounds__(256) mamba_reduce_bc(const float* __restrict__
   const int n = (int)(i % N);
   float sb = 0.0f, sc = 0.0f;
   for (int64_t k = 0; k < nT; ++k) {
-    const float* p = part + (k * BL + row) * (2 * NS);
-    sb += p[n];
-    sc += p[NS + n];
+    const TIO* p = part + (k * BL + row) * (2 * NS);
+    sb += to_f32(p[n]);
+    sc += to_f32(p[NS + n]);
   }
   gBt[i] = from_f32<TIO>(sb);
   gCt[i] = from_f32<TIO>(sc);
@@ -753,17 +759,23 @@ int launch_fwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
 // while its waves wait at the chunk barriers.)
 constexpr int kBwdDT = 32;
 
+// Backward workspace: grad-B/C partials [nT, B, L, 2*NS] in the I/O type (padded to 256 bytes),
+// then the fp32 per-row partials of gA [B, D, N] and gDp [B, D].
 template <int NS>
-int64_t bwd_workspace_floats(int64_t B, int64_t L, int64_t D, int64_t N) {
+int64_t bwd_partial_bytes(int64_t B, int64_t L, int64_t D, int64_t esz) {
   const int64_t nT = (D + kBwdDT - 1) / kBwdDT;
-  return nT * B * L * 2 * NS + B * D * N + B * D;
+  return (nT * B * L * 2 * NS * esz + 255) / 256 * 256;
+}
+template <int NS>
+int64_t bwd_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t N, int64_t esz) {
+  return bwd_partial_bytes<NS>(B, L, D, esz) + 4 * (B * D * N + B * D);
 }
 
 template <typename TIO, int NS, int DT>
 void launch_bwd_tile(int64_t B, int64_t L, int64_t D, int64_t N, int64_t NC, const void* draw, const float* A,
                      const void* Bt, const void* Ct, const void* u, const void* z, const float* Dp, const float* h0,
                      const float* chk, const void* gout, const float* ghlast, void* gdraw, void* gu, void* gz,
-                     float* gA_part, float* gDp_part, float* gBC_part, float* gh0, hipStream_t s) {
+                     float* gA_part, float* gDp_part, TIO* gBC_part, float* gh0, hipStream_t s) {
   using C = BCfg<NS, DT>;
   const int64_t nT = (D + DT - 1) / DT;
   hipLaunchKernelGGL((mamba_bwd_kernel<TIO, NS, DT>), dim3((unsigned)nT, (unsigned)B), dim3(C::TH), 0, s,
@@ -780,8 +792,8 @@ int launch_bwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
   using C = MCfg<NS>;
   const int64_t NC = (L + C::CHK - 1) / C::CHK;
   const int64_t nT = (D + kBwdDT - 1) / kBwdDT;
-  float* gBC_part = static_cast<float*>(workspace);
-  float* gA_part = gBC_part + nT * B * L * 2 * NS;
+  TIO* gBC_part = static_cast<TIO*>(workspace);
+  float* gA_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + bwd_partial_bytes<NS>(B, L, D, sizeof(TIO)));
   float* gDp_part = gA_part + B * D * N;
   if (B > 0 && D > 0)
     launch_bwd_tile<TIO, NS, kBwdDT>(B, L, D, N, NC, draw, A, Bt, Ct, u, z, Dp, h0, chk, gout, ghlast, gdraw, gu, gz,
@@ -871,18 +883,19 @@ int chk_interval_for(int ns) {
   }
 }
 
-int64_t workspace_floats(int ns, int64_t B, int64_t L, int64_t D, int64_t N) {
+// The workspace for fp32 I/O, which also covers bf16 I/O (half-size partials).
+int64_t workspace_bytes(int ns, int64_t B, int64_t L, int64_t D, int64_t N) {
   switch (ns) {
     case 4:
-      return bwd_workspace_floats<4>(B, L, D, N);
+      return bwd_workspace_bytes<4>(B, L, D, N, 4);
     case 8:
-      return bwd_workspace_floats<8>(B, L, D, N);
+      return bwd_workspace_bytes<8>(B, L, D, N, 4);
     case 16:
-      return bwd_workspace_floats<16>(B, L, D, N);
+      return bwd_workspace_bytes<16>(B, L, D, N, 4);
     case 32:
-      return bwd_workspace_floats<32>(B, L, D, N);
+      return bwd_workspace_bytes<32>(B, L, D, N, 4);
     case 64:
-      return bwd_workspace_floats<64>(B, L, D, N);
+      return bwd_workspace_bytes<64>(B, L, D, N, 4);
     default:
       return -1;
   }
@@ -907,7 +920,7 @@ int64_t tsfast_hip_mamba_saved_floats(int64_t L, int64_t D, int64_t N, int io_dt
 int64_t tsfast_hip_mamba_workspace_bytes(int64_t B, int64_t L, int64_t D, int64_t N) {
   const int ns = ns_for(N);
   if (ns == 0 || N < 1) return -1;
-  return 4 * workspace_floats(ns, B, L, D, N);
+  return workspace_bytes(ns, B, L, D, N);
 }
 
 int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtype, const void* draw, const float* A,
