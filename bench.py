@@ -51,8 +51,8 @@ CFG3 = dict(B=16, L=4096, D=1536, N=16)
 # kernels change.
 MEASURED_TRAFFIC = {
     (3, "bf16"): {
-        "fwd": (2_083_282_000, "profiles/mamba_scan_config3_traffic.md"),
-        "bwd": (3_736_450_000, "profiles/mamba_scan_config3_traffic.md"),
+        "fwd": (2_085_800_000, "profiles/mamba_scan_config3_traffic.md"),
+        "bwd": (3_015_800_000, "profiles/mamba_scan_config3_traffic.md"),
     },
     (2, "f32"): {
         "fwd": (1_139_400_000, "profiles/diag_scan_config2_traffic.md"),
@@ -77,8 +77,8 @@ MEASURED_TRAFFIC = {
 # kernels of one ABI call; same provenance rules as MEASURED_TRAFFIC.
 MEASURED_VALU = {
     (3, "bf16"): {
-        "fwd": (241_102_848, "profiles/mamba_scan_config3_valu.md"),
-        "bwd": (559_632_320, "profiles/mamba_scan_config3_valu.md"),
+        "fwd": (230_092_800, "profiles/mamba_scan_config3_valu.md"),
+        "bwd": (501_887_680, "profiles/mamba_scan_config3_valu.md"),
     },
 }
 VALU_PEAK_CLOCK_HZ = 2.4e9  # MI355X peak engine clock

@@ -726,6 +726,38 @@ __global__ void __launch_bounds__(256) mamba_reduce_bc(const TIO* __restrict__ p
   gCt[i] = from_f32<TIO>(sc);
 }
 
+// The same sum with 16-byte accesses when N == NS and a 16-byte vector holds whole columns of
+// one kind (NS a multiple of V = 16 / sizeof(TIO)): thread (row, q) adds columns V q .. V q + V - 1
+// of every tile's [2*NS] row, in tile order, and writes them to gBt (V q < NS) or gCt.
+template <typename TIO>
+__global__ void __launch_bounds__(256) mamba_reduce_bc_vec(const TIO* __restrict__ part, TIO* __restrict__ gBt,
+                                                           TIO* __restrict__ gCt, int64_t nT, int64_t BL, int NS) {
+  constexpr int V = 16 / sizeof(TIO);
+  const int QR = 2 * NS / V;  // vectors per row
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // over BL * QR
+  if (i >= BL * QR) return;
+  const int64_t row = i / QR;
+  const int q = (int)(i % QR);
+  float acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = 0.0f;
+  const uint4* src = reinterpret_cast<const uint4*>(part + row * 2 * NS) + q;
+  const int64_t tstride = BL * 2 * NS / V;  // uint4 per tile
+  for (int64_t k = 0; k < nT; ++k) {
+    const uint4 w = src[k * tstride];
+    const TIO* e = reinterpret_cast<const TIO*>(&w);
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] += to_f32(e[v]);
+  }
+  uint4 o;
+  TIO* oe = reinterpret_cast<TIO*>(&o);
+#pragma unroll
+  for (int v = 0; v < V; ++v) oe[v] = from_f32<TIO>(acc[v]);
+  const int c0 = q * V;
+  TIO* dst = c0 < NS ? gBt + row * NS + c0 : gCt + row * NS + (c0 - NS);
+  *reinterpret_cast<uint4*>(dst) = o;
+}
+
 // Sum [B, X] partials over the batch into [X] (gA with X = D*N, gDp with X = D).
 __global__ void __launch_bounds__(256) mamba_reduce_batch(const float* __restrict__ part, float* __restrict__ dst,
                                                           int64_t B, int64_t X) {
@@ -799,9 +831,15 @@ int launch_bwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
     launch_bwd_tile<TIO, NS, kBwdDT>(B, L, D, N, NC, draw, A, Bt, Ct, u, z, Dp, h0, chk, gout, ghlast, gdraw, gu, gz,
                                      gA_part, gDp_part, gBC_part, gh0, s);
   const int64_t BLN = B * L * N;
-  if (BLN > 0)
+  constexpr int V = 16 / sizeof(TIO);
+  if (BLN > 0 && N == NS && NS % V == 0) {
+    const int64_t items = B * L * (2 * NS / V);
+    hipLaunchKernelGGL((mamba_reduce_bc_vec<TIO>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, gBC_part,
+                       (TIO*)gBt, (TIO*)gCt, nT, B * L, NS);
+  } else if (BLN > 0) {
     hipLaunchKernelGGL((mamba_reduce_bc<TIO>), dim3((unsigned)((BLN + 255) / 256)), dim3(256), 0, s, gBC_part,
                        (TIO*)gBt, (TIO*)gCt, nT, B * L, (int)N, NS);
+  }
   if (D > 0) {
     hipLaunchKernelGGL(mamba_reduce_batch, dim3((unsigned)((D * N + 255) / 256)), dim3(256), 0, s, gA_part, gA, B,
                        D * N);
