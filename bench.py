@@ -633,6 +633,74 @@ def run_gblock(args, line):
     return ms, fwd_b + bwd_b, kernels, cpu
 
 
+def projected_inputs(device, B=64, L=4096, H=32, N=256, O=32, seed=4):
+    """BASELINE config 2's layer: u ~ N(0,1) [B, L, H], lam = r e^(i theta) with r ~ U(0.9, 0.999)
+    and theta ~ U(0, pi/10), C ~ N(0, 1/N) (the readout of config 2), W ~ N(0, 1/H)."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(B, L, H, generator=g)
+    W_re, W_im = torch.randn(N, H, generator=g) / math.sqrt(H), torch.randn(N, H, generator=g) / math.sqrt(H)
+    lam = torch.polar(torch.rand(N, generator=g) * 0.099 + 0.9, torch.rand(N, generator=g) * (math.pi / 10))
+    C_re, C_im = torch.randn(O, N, generator=g) / math.sqrt(N), torch.randn(O, N, generator=g) / math.sqrt(N)
+    gy = torch.randn(B, L, O, generator=g)
+    return [t.to(device) for t in (u, W_re, W_im, lam, C_re, C_im, gy)]
+
+
+def run_projected(args, line):
+    """The fused projected complex diagonal scan (LRU / S5 layer core) at config 2's shape, with the
+    reference's unfused stack (complex_in_proj -> diagonal_recurrence -> real_out_proj, HIP scan
+    backend, autograd) timed in the same run. Both projections run on the fp32 matrix cores, so
+    the roofline is fp32 MFMA."""
+    import torch
+
+    from tsfast_amd import scan
+    from tsfast_amd.scan_backends import projected_hip
+
+    u, W_re, W_im, lam, C_re, C_im, gy = projected_inputs("cuda")
+    B, L, H = u.shape
+    N, O = lam.shape[0], C_re.shape[0]
+
+    def step(ev):
+        mark(ev)
+        y, x_last, saved = projected_hip._scan_train_op(u, W_re, W_im, lam, C_re, C_im, None)
+        mark(ev)
+        projected_hip._scan_bwd_op(gy, None, saved, u, W_re, W_im, lam, C_re, C_im, None)
+        mark(ev)
+
+    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
+
+    def unfused(ev):
+        ins = [t.detach().requires_grad_() for t in (u, W_re, W_im, lam, C_re, C_im)]
+        mark(ev)
+        x = scan.diagonal_recurrence(ins[3], scan.complex_in_proj(ins[0], ins[1], ins[2]))
+        y = scan.real_out_proj(x, ins[4], ins[5])
+        mark(ev)
+        torch.autograd.backward(y, gy)
+        mark(ev)
+
+    ums, (ufwd, ubwd) = time_steps(unfused, max(args.steps // 2, 2), 2)
+    bl = B * L
+    fwd_f = 2 * bl * 2 * N * (H + O)  # in-projection and read-out
+    bwd_f = 2 * bl * 2 * N * (2 * O + 3 * H)  # g_x, v recompute, grad C, grad W, g_u
+    line.update(
+        metric="fwd+bwd ms + achieved fp32 TFLOP/s, fused projected complex diagonal scan (LRU/S5 layer core)",
+        unit="TFLOP/s",
+        config={"workload": f"fused complex_in_proj -> diagonal_recurrence -> real_out_proj fwd+bwd: batch {B}, "
+                            f"L {L}, N {N} complex states, H {H} inputs, O {O} outputs (BASELINE config 2 scan)",
+                "B": B, "L": L, "N": N, "H": H, "O": O},
+        fwd_ms=round(fwd_ms, 4),
+        bwd_ms=round(bwd_ms, 4),
+        unfused_ms={"fwd": round(ufwd, 4), "bwd": round(ubwd, 4), "total": round(ums, 4),
+                    "path": "complex_in_proj (GEMM) + tsfast_hip::scan_diagonal + real_out_proj (GEMM), autograd"},
+        algorithmic_flops={"fwd": fwd_f, "bwd": bwd_f},
+        _mfma_peak_tflops=157.3,
+    )
+    kernels = {"fwd": ("projscan_fwd (in-projection, scan, read-out on fp32 MFMA)", fwd_ms, fwd_f),
+               "bwd": ("projscan_bwd + projscan_bwd_reduce", bwd_ms, bwd_f)}
+    return ms, fwd_f + bwd_f, kernels, None
+
+
 def run_linrec(args, line):
     """The constant-matrix linear_recurrence (dynonet/core.py:103-127) on config 4's route: the
     companion matrices of the config-4 denominators (n = 3) driven by (w_t, 0, 0), the way the
@@ -720,6 +788,8 @@ def main():
                     help="measure the fused dynoNet G-block (FIR + all-pole + input sum) at config 4's channels")
     ap.add_argument("--linrec", action="store_true",
                     help="measure the constant-matrix linear_recurrence on config 4's companion-matrix route")
+    ap.add_argument("--projected", action="store_true",
+                    help="measure the fused projected complex diagonal scan (LRU/S5 core) at config 2's shape")
     ap.add_argument("--order", type=int, default=3,
                     help="with --linrec: the denominator order n (state size 1..8; config 4 is 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
@@ -769,9 +839,21 @@ def main():
         "data": "synthetic",
     }
     runner = (run_conv if args.conv else run_selective if args.selective else run_gblock if args.gblock
-              else run_linrec if args.linrec
+              else run_linrec if args.linrec else run_projected if args.projected
               else {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config])
     ms, total_bytes, kernels, cpu = runner(args, line)
+    mfma_peak = line.pop("_mfma_peak_tflops", None)
+    if mfma_peak is not None:
+        # a matrix-core workload: throughput in algorithmic TFLOP/s against the dense fp32 MFMA peak
+        line["value"] = round(total_bytes / (ms * 1e-3) / 1e12, 3)
+        line["ms_per_step"] = round(ms, 4)
+        phase = max(kernels, key=lambda k: kernels[k][1])
+        name, dom_ms, dom_f = kernels[phase]
+        got = dom_f / (dom_ms * 1e-3) / 1e12
+        line["roofline"] = {"bound": "mfma", "kernel": name, "achieved": round(got, 3), "peak": mfma_peak,
+                            "unit": "TFLOP/s", "frac": round(got / mfma_peak, 4), "traffic": None}
+        print(json.dumps(line), flush=True)
+        return
     gbs = total_bytes / (ms * 1e-3) / 1e9
     line["value"] = round(gbs, 2)
     line["ms_per_step"] = round(ms, 4)

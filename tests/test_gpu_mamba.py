@@ -148,3 +148,39 @@ def test_mamba_chunked_state_equivalence(gpu):
             o, h = mamba_hip.run(*[sl[k] for k in _NAMES])
             outs.append(o)
     assert O.rel_err(_np64(torch.cat(outs, 1)), _np64(full)) < 1e-5
+
+
+@pytest.mark.parametrize("N", [96, 130])
+@pytest.mark.parametrize("io", ["fp32", "bf16"])
+def test_mamba_state_groups_above_64(gpu, N, io):
+    """N above the 64 states of one launch runs in state groups of up to 64 (96 = 64 + 32,
+    130 = 64 + 64 + 2), every output and gradient against the oracle (the reference's fused
+    backend has no state cap, mamba_triton.py:490-520)."""
+    io_dtype = torch.float32 if io == "fp32" else torch.bfloat16
+    tol = 1e-5 if io == "fp32" else 2e-2
+    t, gout, ghlast = _make(2, 45, 40, N, seed=N, io_dtype=io_dtype, with_h0=True)
+    out, h_last, grads = _run_hip(t, gout, ghlast, gpu, use_ghlast=True)
+    assert out.dtype == io_dtype and h_last.shape == (2, 40, N)
+    args = [_np64(t[k]) for k in _NAMES]
+    want_out, want_h = O.mamba_forward(*args)
+    got = O.mamba_backward(_np64(gout), _np64(ghlast), *args)
+    assert O.rel_err(_np64(out), want_out) < tol, "out"
+    assert O.rel_err(_np64(h_last), want_h) < tol, "h_last"
+    for name, want in zip(_NAMES, got):
+        if want is not None:
+            assert grads[name].dtype == t[name].dtype
+            assert O.rel_err(_np64(grads[name]), want) < tol, name
+
+
+def test_mamba_batch_above_65535(gpu):
+    """More batch rows than a grid's y dimension holds: the grid is one-dimensional."""
+    t, gout, ghlast = _make(70_000, 3, 32, 4, seed=21, io_dtype=torch.float32, with_h0=True)
+    out, h_last, grads = _run_hip(t, gout, ghlast, gpu, use_ghlast=True)
+    args = [_np64(t[k]) for k in _NAMES]
+    want_out, want_h = O.mamba_forward(*args)
+    got = O.mamba_backward(_np64(gout), _np64(ghlast), *args)
+    assert O.rel_err(_np64(out), want_out) < 1e-5
+    assert O.rel_err(_np64(h_last), want_h) < 1e-5
+    for name, want in zip(_NAMES, got):
+        if want is not None:
+            assert O.rel_err(_np64(grads[name]), want) < 1e-5, name

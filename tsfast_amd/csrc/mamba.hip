@@ -129,13 +129,15 @@ TSF_HOST_DEV int64_t saved_row_floats(int64_t L, int64_t D, int64_t N, int64_t N
 // that every XCD receives a contiguous range of (channel tile, batch row) pairs: neighbouring
 // channel tiles share the 128-byte lines of each bf16 [B, L, D] row (one tile's row segment is
 // 64 bytes), and on one XCD the second read of a line hits that XCD's L2 instead of HBM.
+// The grid is one-dimensional (nT channel tiles x B batch rows, tile-major), so the batch size
+// is not bounded by the 65535 limit of a grid's y dimension.
 constexpr unsigned kXcds = 8;
-TSF_DEV void xcd_remap(int64_t& tile, int64_t& row) {
-  const unsigned gx = gridDim.x, total = gridDim.x * gridDim.y;
-  unsigned lin = blockIdx.x + blockIdx.y * gx;
+TSF_DEV void xcd_remap(int64_t nT, int64_t& tile, int64_t& row) {
+  const unsigned total = gridDim.x;
+  unsigned lin = blockIdx.x;
   if (total % kXcds == 0) lin = (lin % kXcds) * (total / kXcds) + lin / kXcds;
-  tile = lin % gx;
-  row = lin / gx;
+  tile = lin % nT;
+  row = lin / nT;
 }
 
 // ------------------------------------------------------------------------------------ DPP rows
@@ -192,7 +194,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
 
   const int tid = threadIdx.x;
   int64_t tile, b;
-  xcd_remap(tile, b);
+  xcd_remap((D + DT - 1) / DT, tile, b);
   const int64_t d0 = tile * DT;
   // recurrence mapping: adjacent lanes hold the two halves of a state pair
   const int pr = tid & 1;
@@ -359,7 +361,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   // Workgroups sharing a CU (slot = dispatch round) are issued oldest-first, so the first one
   // races ahead and the last ones finish alone; rotating the issue priority among the slots
   // every four rounds evens their progress and shortens the tail.
-  const unsigned slot = (blockIdx.x + blockIdx.y * gridDim.x) / cus;
+  const unsigned slot = blockIdx.x / cus;
   for (int64_t t0 = 0; t0 < L; t0 += TF) {
     if (((t0 / TF) & 3) == 0) set_wave_priority((slot + (unsigned)(t0 / TF / 4)) % 3);
     chunk((uint32_t)t0, (int)((L - t0) < TF ? (L - t0) : TF));
@@ -424,7 +426,7 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
 
   const int tid = threadIdx.x;
   int64_t tile, b;
-  xcd_remap(tile, b);
+  xcd_remap((D + DT - 1) / DT, tile, b);
   const int64_t d0 = tile * DT;
   const int rw = tid >> 4, lk = tid & 15;
   const int ng = rw / RPG;
@@ -578,7 +580,7 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
   float lamb[CHK][NPT], lhb[CHK][NPT], hb[CHK][NPT];
   // The forward's issue-priority rotation among the workgroups sharing a CU (every 16 chunks =
   // 128 steps): without it the oldest workgroup races ahead and the last one finishes alone.
-  const unsigned slot = (blockIdx.x + blockIdx.y * gridDim.x) / cus;
+  const unsigned slot = blockIdx.x / cus;
   for (int64_t c = NC - 1; c >= 0; --c) {
     const int64_t r = NC - 1 - c;
     if (C::OCC > 1 && (r & 15) == 0) set_wave_priority((slot + (unsigned)(r / 16)) % C::OCC);
@@ -774,7 +776,7 @@ int launch_fwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
                float* h_last, float* chk, hipStream_t s) {
   using C = MCfg<NS>;
   const int64_t NC = (L + C::CHK - 1) / C::CHK;
-  dim3 grid((unsigned)((D + C::DT - 1) / C::DT), (unsigned)B);
+  dim3 grid((unsigned)((D + C::DT - 1) / C::DT * B));
   if (chk)
     hipLaunchKernelGGL((mamba_fwd_kernel<TIO, NS, true>), grid, dim3(C::TH), 0, s, (const TIO*)draw, A,
                        (const TIO*)Bt, (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, (TIO*)out, h_last, chk, L,
@@ -810,7 +812,7 @@ void launch_bwd_tile(int64_t B, int64_t L, int64_t D, int64_t N, int64_t NC, con
                      float* gA_part, float* gDp_part, TIO* gBC_part, float* gh0, hipStream_t s) {
   using C = BCfg<NS, DT>;
   const int64_t nT = (D + DT - 1) / DT;
-  hipLaunchKernelGGL((mamba_bwd_kernel<TIO, NS, DT>), dim3((unsigned)nT, (unsigned)B), dim3(C::TH), 0, s,
+  hipLaunchKernelGGL((mamba_bwd_kernel<TIO, NS, DT>), dim3((unsigned)(nT * B)), dim3(C::TH), 0, s,
                      (const TIO*)draw, A, (const TIO*)Bt, (const TIO*)Ct, (const TIO*)u, (const TIO*)z, Dp, h0, chk,
                      (const TIO*)gout, ghlast, (TIO*)gdraw, (TIO*)gu, (TIO*)gz, gA_part, gDp_part, gBC_part, gh0, B,
                      L, D, (int)N, NC, device_cus());
@@ -965,7 +967,7 @@ int tsfast_hip_mamba_fwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
                          const void* Bt, const void* Ct, const void* u, const void* z, const float* Dp,
                          const float* h0, void* out, float* h_last, float* chk, void* stream) {
   if (B < 0 || L < 0 || D < 0 || N < 1) return TSF_ERR_ARG;
-  if (B > 65535) return TSF_ERR_UNSUPPORTED;
+  if ((D + 31) / 32 * B > INT32_MAX) return TSF_ERR_UNSUPPORTED;  // one-dimensional grid
   const int ns = ns_for(N);
   if (ns == 0) return TSF_ERR_UNSUPPORTED;
   if (B == 0 || D == 0) return TSF_OK;
@@ -987,7 +989,7 @@ int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
                          float* gA, void* gBt, void* gCt, void* gu, void* gz, float* gDp, float* gh0, void* workspace,
                          int64_t workspace_bytes, void* stream) {
   if (B < 0 || L < 0 || D < 0 || N < 1) return TSF_ERR_ARG;
-  if (B > 65535) return TSF_ERR_UNSUPPORTED;
+  if ((D + 31) / 32 * B > INT32_MAX) return TSF_ERR_UNSUPPORTED;  // one-dimensional grid
   const int ns = ns_for(N);
   if (ns == 0) return TSF_ERR_UNSUPPORTED;
   if (!A || !Dp || !gA || !gDp) return TSF_ERR_ARG;

@@ -90,11 +90,11 @@ def supports(draw, A, Bt, Ct, u, z, Dp, h0) -> str | None:
     N = A.shape[-1]
     if tuple(A.shape) != (D, N):
         return f"A.shape {tuple(A.shape)} incompatible with draw {tuple(draw.shape)}"
-    if not 1 <= N <= _MAX_N:
-        return f"state size N={N} outside [1, {_MAX_N}]"
-    if B > 65535:
-        return f"batch {B} above the 65535 grid limit"
-    if not _rows_fit(L, D, N):
+    if N < 1:
+        return f"state size N={N} below 1"
+    if -(-D // 32) * B > 2**31 - 1:
+        return f"{B} batch rows x {-(-D // 32)} channel tiles exceed the kernels' one-dimensional grid"
+    if not _rows_fit(L, D, min(N, _MAX_N)):
         return f"one batch row (L={L}, D={D}, N={N}) exceeds the kernels' 2 GiB per-row addressing"
     if tuple(u.shape) != (B, L, D) or tuple(z.shape) != (B, L, D):
         return f"u/z shapes {tuple(u.shape)}/{tuple(z.shape)} != {(B, L, D)}"
@@ -270,15 +270,39 @@ def _scan_backward(ctx, gout, ghlast, gchk):
 _scan_train_op.register_autograd(_scan_backward, setup_context=_scan_setup)
 
 
+def _run_group(draw, A, Bt, Ct, u, z, Dp, h0):
+    inputs = (draw, A, Bt, Ct, u, z, Dp) + ((h0,) if h0 is not None else ())
+    if not torch.is_grad_enabled() or not any(t.requires_grad for t in inputs):
+        return _scan_op(draw, A, Bt, Ct, u, z, Dp, h0)
+    out, h_last, _chk = _scan_train_op(draw, A, Bt, Ct, u, z, Dp, h0)
+    return out, h_last
+
+
 def run(draw, A, Bt, Ct, u, z, Dp, h0):
     """Fused Mamba SSM: ``h_t = exp(softplus(draw_t) A) h_{t-1} + softplus(draw_t) u_t B_t``,
     ``out_t = (h_t . C_t + Dp u_t) * silu(z_t)``.
 
     Returns ``(out [B, L, D], h_last [B, D, N] float32)``; differentiable in all inputs. Without
     grad the inference op (no checkpoints) runs. (Contract of ``mamba_triton.py:523-534``.)
+
+    A launch serves at most 64 states. Larger N runs the states in groups of up to 64: the states
+    evolve independently, and the output is linear in the per-state sum ``h . C`` for fixed
+    draw, u, z (``out = (sum over groups of h_g . C_g + Dp u) * silu(z)``), so the groups' outputs
+    add up to the output (the D skip goes with the first group only), and their gradients add up
+    the same way through autograd. Group outputs are summed in float32 and rounded once.
     """
-    inputs = (draw, A, Bt, Ct, u, z, Dp) + ((h0,) if h0 is not None else ())
-    if not torch.is_grad_enabled() or not any(t.requires_grad for t in inputs):
-        return _scan_op(draw, A, Bt, Ct, u, z, Dp, h0)
-    out, h_last, _chk = _scan_train_op(draw, A, Bt, Ct, u, z, Dp, h0)
-    return out, h_last
+    N = A.shape[-1]
+    if N <= _MAX_N:
+        return _run_group(draw, A, Bt, Ct, u, z, Dp, h0)
+    outs, lasts = [], []
+    for n0 in range(0, N, _MAX_N):
+        n1 = min(n0 + _MAX_N, N)
+        dp = Dp if n0 == 0 else torch.zeros_like(Dp)
+        hg = h0[..., n0:n1] if h0 is not None else None
+        o, hl = _run_group(draw, A[:, n0:n1], Bt[..., n0:n1], Ct[..., n0:n1], u, z, dp, hg)
+        outs.append(o.float())
+        lasts.append(hl)
+    out = outs[0]
+    for o in outs[1:]:
+        out = out + o
+    return out.to(draw.dtype), torch.cat(lasts, dim=-1)
