@@ -36,6 +36,19 @@ extern "C" {
 #define TSF_DTYPE_BF16 1
 
 const char* tsfast_hip_status_string(int status);
+
+/* Deterministic mode of the single-pass look-back scans (diag, selective, all-pole, linear
+ * recurrence, G-block, projected), process-wide, read when a scan is launched. Off (0, the default):
+ * a tile composes the published maps back to the nearest tile that has published its leaving
+ * state, so which maps are composed depends on timing and results agree run to run to fp64
+ * rounding. On: only every s-th tile in scan order publishes its leaving state and the others their
+ * aggregates, so every launch composes the same maps in the same order and the outputs are bitwise
+ * reproducible (the parameter-gradient sums of the projected scan excepted); a few to 20% slower.
+ * No counterpart in the reference, whose kernels are deterministic by construction
+ * (tsfast/models/architectures/mamba/mamba_triton.py:19-22); the Python backends set it from
+ * torch.are_deterministic_algorithms_enabled(). */
+void tsfast_hip_set_deterministic(int on);
+int tsfast_hip_get_deterministic(void);
 /* Library version, for the Python loader's sanity check. */
 int tsfast_hip_version(void);
 

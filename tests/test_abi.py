@@ -122,3 +122,17 @@ def test_mamba_saved_floats_formula_matches_the_library(lib):
     for L, D, N in ((1, 1, 1), (45, 40, 16), (4096, 1536, 16), (33, 16, 8), (1000, 70, 64), (7, 8, 33)):
         for dt, code in ((torch.float32, 0), (torch.bfloat16, 1)):
             assert mamba_hip.saved_floats(L, D, N, dt) == lib.tsfast_hip_mamba_saved_floats(L, D, N, code)
+
+
+def test_conv_supports_mirrors_the_kernel_grid_limit(lib):
+    """conv_hip's size screen repeats the kernels' limits (B and the number of 128-step segments
+    each at most 65535), so a shape the library rejects falls back through dispatch instead of
+    raising in the op."""
+    from tsfast_amd.mamba import conv_hip
+
+    D, K = 64, 4
+    for B, L in ((1, 1), (1, 128), (1, 65535 * 128 - 1), (1, 65535 * 128), (1, 65535 * 128 + 1), (1, 65536 * 128),
+                 (65535, 8), (65536, 8)):
+        c_ok = lib.tsfast_hip_conv_silu_workspace_bytes(B, L, D, K) >= 0
+        py_ok = conv_hip._size_reason(B, L, D, D, 1, 2) is None
+        assert py_ok == c_ok, (B, L)

@@ -277,3 +277,44 @@ def test_linrec_config4_route_full_size(gpu):
     assert O.rel_err(_np64(x), want) < 1e-5
     gA, gv, _ = O.linrec_backward(gx.double().numpy(), A.double().numpy(), want)
     assert O.rel_err(_np64(A_d.grad), gA) < 1e-5 and O.rel_err(_np64(v_d.grad), gv) < 1e-5
+
+
+def test_linrec_order8_config4_route_full_size(gpu):
+    """The two-pass n = 8 path on config 4's route at full size (4096 lanes x L16384, companion
+    matrices of order-8 denominators driven by (w_t, 0, ...), 16 lane blocks x 64 chunks, the
+    whole-step float4 row accesses): lanes are independent, so 48 lanes spread over every lane
+    block (each block's first, middle and last lane) are checked against the oracle over the full
+    length, x and every gradient."""
+    from tsfast_amd.dynonet import core as dcore
+    from tsfast_amd.dynonet import linrec_hip
+
+    g = torch.Generator().manual_seed(8)
+    lanes, L, n = 4096, 16384, 8
+    # four conjugate pole pairs per lane, |p| ~ U(0.5, 0.98), angles ~ U(0, pi) (bench.py's
+    # draws for --linrec --order 8). Order-8 roots near the unit circle are sensitive to the
+    # fp32 rounding of the coefficients: lanes whose rounded filter is not stable (spectral
+    # radius >= 0.99, whose exact output leaves fp32's range) get their poles pulled inwards.
+    rho = (torch.rand(lanes, n // 2, generator=g, dtype=torch.float64) * 0.48 + 0.5).numpy()
+    th = (torch.rand(lanes, n // 2, generator=g, dtype=torch.float64) * np.pi).numpy()
+    for _ in range(20):
+        poles = np.concatenate([rho * np.exp(1j * th), rho * np.exp(-1j * th)], axis=1)
+        a = torch.tensor(np.array([np.real(np.poly(p))[1:] for p in poles]), dtype=torch.float32)
+        radius = np.abs(np.linalg.eigvals(dcore.companion(a).double().numpy())).max(-1)
+        if (radius < 0.99).all():
+            break
+        rho = np.where((radius >= 0.99)[:, None], rho * 0.97, rho)
+    assert (radius < 0.99).all()
+    A = dcore.companion(a).contiguous()
+    v = torch.nn.functional.pad(torch.randn(lanes, L, 1, generator=g), (0, n - 1))
+    gx = torch.randn(lanes, L, n, generator=g)
+    A_d, v_d = A.to(gpu).requires_grad_(), v.to(gpu).requires_grad_()
+    assert linrec_hip.supports(A_d, v_d, None) is None
+    x = linrec_hip.run(A_d, v_d, None)
+    x.backward(gx.to(gpu))
+    pick = torch.tensor(sorted({b * 256 + o for b in range(16) for o in (0, 128, 255)}))
+    A_s, v_s, g_s = (t[pick].double().numpy() for t in (A, v, gx))
+    want = O.linrec_forward(A_s, v_s)
+    assert O.rel_err(_np64(x[pick.to(gpu)]), want) < 1e-5
+    gA, gv, _ = O.linrec_backward(g_s, A_s, want)
+    assert O.rel_err(_np64(A_d.grad[pick.to(gpu)]), gA) < 1e-5
+    assert O.rel_err(_np64(v_d.grad[pick.to(gpu)]), gv) < 1e-5

@@ -5,8 +5,8 @@ closed forms, torch float64 autograd through a sequential loop, and the diagonal
 all-pole special cases (tests/test_oracle.py). Shapes cover every state size n = 1..4 (chunks of
 32, 16, 10 and 8 steps), lane counts below, at and above one 64-lane tile row, sequences shorter
 than one chunk and than one super-chunk, ragged tails, many super-chunks (the look-back), and
-absent initial state; n = 5..8 (the two-pass path) with one and many 256-step chunks, ragged
-last chunks and several lane blocks. Bar: max relative error <= 1e-5 for x and every gradient (fp32 I/O, fp64
+absent initial state; n = 5..8 (the two-pass path, blocks of 256 lanes) with one and many
+256-step chunks, ragged last chunks, and several lane blocks combined with several chunks. Bar: max relative error <= 1e-5 for x and every gradient (fp32 I/O, fp64
 state). Matrices are scaled to spectral radius 0.97 so the states neither vanish nor blow up.
 """
 
@@ -52,12 +52,14 @@ _SHAPES = [
     (96, 5000, 2),
     # n = 5..8: the two-pass path (chunks of 256 steps)
     (5, 40, 5),
-    (70, 1000, 6),  # ragged last chunk, two lane blocks
+    (70, 1000, 6),  # ragged last chunk, one lane block (256 lanes per block)
     (130, 777, 7),
     (64, 600, 8),
     (3, 1, 8),
     (1, 5000, 5),  # one lane, 20 chunks of carry
-    (300, 256, 6),  # exactly one chunk
+    (300, 256, 6),  # exactly one chunk, two lane blocks
+    (600, 3000, 8),  # three lane blocks (the last partial) x twelve chunks (the last ragged)
+    (520, 1500, 5),  # three lane blocks x six chunks
 ]
 
 

@@ -129,11 +129,18 @@ def _run_allpole(a, w, y0, gout):
     return (y, *allpole_hip._allpole_bwd_op(gout, a, y, y0))
 
 
-@pytest.mark.parametrize("kind", ["linrec", "allpole"])
+@pytest.mark.parametrize("kind", ["linrec", "linrec6", "linrec8", "allpole"])
 def test_graph_replay_dynonet_scans(gpu, kind):
-    """The constant-matrix recurrence and the all-pole scan (look-back words reset by a kernel)
-    replay correctly from a captured graph, with new inputs and eager work between replays."""
-    make, run = (_linrec_inputs, _run_linrec) if kind == "linrec" else (_allpole_inputs, _run_allpole)
+    """The constant-matrix recurrence (n = 3 single-pass look-back; n = 6 and 8 two-pass chunk
+    kernels, 600 lanes x 3000 steps: three 256-lane blocks and twelve 256-step chunks) and the
+    all-pole scan replay correctly from a captured graph, with new inputs and eager work between
+    replays."""
+    if kind.startswith("linrec"):
+        n = int(kind[6:] or 3)
+        shape = dict(n=n) if n == 3 else dict(M=600, L=3000, n=n)
+        make, run = (lambda seed, dev: _linrec_inputs(seed, dev, **shape)), _run_linrec
+    else:
+        make, run = _allpole_inputs, _run_allpole
     ins = make(0, gpu)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())

@@ -28,6 +28,8 @@ _ptr = ctypes.c_void_p
 _SIGNATURES: dict[str, tuple[list, object]] = {
     "tsfast_hip_version": ([], _int),
     "tsfast_hip_status_string": ([_int], ctypes.c_char_p),
+    "tsfast_hip_set_deterministic": ([_int], None),
+    "tsfast_hip_get_deterministic": ([], _int),
     "tsfast_hip_diag_workspace_bytes": ([_i64, _i64, _i64, _int], _i64),
     "tsfast_hip_diag_fwd": ([_i64, _i64, _i64, _int] + [_ptr] * 5 + [_i64, _ptr], _int),
     "tsfast_hip_diag_bwd": ([_i64, _i64, _i64, _int] + [_ptr] * 8 + [_i64, _ptr], _int),
@@ -89,6 +91,20 @@ def load() -> ctypes.CDLL:
                 fn.restype = restype
             _lib = lib
     return _lib
+
+
+_det_mode: int | None = None
+
+
+def sync_deterministic() -> None:
+    """Put the library's look-back scans in deterministic mode exactly when
+    ``torch.are_deterministic_algorithms_enabled()`` (bitwise reproducible outputs at some cost
+    in speed); called before every look-back scan is launched."""
+    global _det_mode
+    want = 1 if torch.are_deterministic_algorithms_enabled() else 0
+    if want != _det_mode:
+        load().tsfast_hip_set_deterministic(want)
+        _det_mode = want
 
 
 def available() -> bool:

@@ -17,7 +17,7 @@
 // NA <= 4 run single-pass kernels with a decoupled look-back between workgroups (every input
 // element read once; described at allpole_fwd_lb). Higher orders, whose NA x NA matrices do not
 // fit in registers, run a two-pass scan with chunks of T_c steps, one thread per (lane, chunk):
-//   1. transfer   per lane: M = C^{T_c} by binary powering, stored in the workspace;
+//   1. transfer   per lane: M = C^{T_c} (built step by step up to C^256), stored in the workspace;
 //   2. chunk_end  per (lane, chunk): e_c from a zero entering state;
 //   3. carry      per lane: entering states S_c = M S_{c-1} + e_{c-1}, sequential over chunks;
 //   4. apply      per (lane, chunk): run the chunk from S_c and write y.
@@ -34,57 +34,53 @@ namespace {
 #include "allpole_core.h"
 
 
+// M = C^{T_c} per lane. Powers up to C^256 are built step by step from the unit vectors (fp64;
+// see companion_powers for why not by squaring); a longer chunk takes (C^256)^q C^r, squaring only
+// C^256, whose transient growth has decayed for the stable filters this scan serves.
 template <int NA>
 __global__ void __launch_bounds__(256) allpole_transfer(const float* __restrict__ a, double* __restrict__ Mout,
                                                         int64_t lanes, int64_t T_c) {
   const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (lane >= lanes) return;
-  double P[NA][NA], R[NA][NA], T[NA][NA];
+  constexpr int64_t kStep = 256;
+  double ac[NA];
 #pragma unroll
-  for (int r = 0; r < NA; ++r)
+  for (int c = 0; c < NA; ++c) ac[c] = (double)a[lane * NA + c];
+  const int64_t base = T_c < kStep ? T_c : kStep;
+  const int64_t q = T_c / base, rem = T_c - q * base;
+  double Q[NA][NA], R[NA][NA], T[NA][NA];  // Q = C^base, R = C^rem
+  for (int col = 0; col < NA; ++col) {
+    double x[NA];
 #pragma unroll
-    for (int c = 0; c < NA; ++c) {
-      P[r][c] = (r == 0) ? -(double)a[lane * NA + c] : (c == r - 1 ? 1.0 : 0.0);
-      R[r][c] = (r == c) ? 1.0 : 0.0;
+    for (int r = 0; r < NA; ++r) x[r] = r == col ? 1.0 : 0.0;
+    for (int64_t step = 1; step <= base; ++step) {
+      companion_apply<NA>(x, ac);
+      if (step == rem)
+#pragma unroll
+        for (int r = 0; r < NA; ++r) R[r][col] = x[r];
     }
-  int64_t k = T_c;
-  while (k > 0) {
-    if (k & 1) {
 #pragma unroll
-      for (int r = 0; r < NA; ++r)
+    for (int r = 0; r < NA; ++r) Q[r][col] = x[r];
+    if (rem == 0)
 #pragma unroll
-        for (int c = 0; c < NA; ++c) {
-          double s = 0.0;
-#pragma unroll
-          for (int j = 0; j < NA; ++j) s = fma(R[r][j], P[j][c], s);
-          T[r][c] = s;
-        }
-#pragma unroll
-      for (int r = 0; r < NA; ++r)
-#pragma unroll
-        for (int c = 0; c < NA; ++c) R[r][c] = T[r][c];
-    }
-    k >>= 1;
-    if (k > 0) {
-#pragma unroll
-      for (int r = 0; r < NA; ++r)
-#pragma unroll
-        for (int c = 0; c < NA; ++c) {
-          double s = 0.0;
-#pragma unroll
-          for (int j = 0; j < NA; ++j) s = fma(P[r][j], P[j][c], s);
-          T[r][c] = s;
-        }
-#pragma unroll
-      for (int r = 0; r < NA; ++r)
-#pragma unroll
-        for (int c = 0; c < NA; ++c) P[r][c] = T[r][c];
-    }
+      for (int r = 0; r < NA; ++r) R[r][col] = r == col ? 1.0 : 0.0;
   }
-#pragma unroll
+  auto mul = [&](double (&dst)[NA][NA], const double (&x)[NA][NA], const double (&y)[NA][NA]) {
+    for (int r = 0; r < NA; ++r)
+      for (int c = 0; c < NA; ++c) {
+        double s = 0.0;
+        for (int j = 0; j < NA; ++j) s = fma(x[r][j], y[j][c], s);
+        T[r][c] = s;
+      }
+    for (int r = 0; r < NA; ++r)
+      for (int c = 0; c < NA; ++c) dst[r][c] = T[r][c];
+  };
+  for (int64_t k = q; k > 0; k >>= 1) {  // R <- R Q^q
+    if (k & 1) mul(R, R, Q);
+    if (k > 1) mul(Q, Q, Q);
+  }
   for (int r = 0; r < NA; ++r)
-#pragma unroll
-    for (int c = 0; c < NA; ++c) Mout[(lane * NA + r) * NA + c] = R[r][c];
+    for (int c = 0; c < NA; ++c) Mout[lane * NA * NA + r * NA + c] = R[r][c];
 }
 
 // 2. forward chunk ends from a zero entering state, chunks 0 .. nchunk-2.
@@ -335,7 +331,7 @@ template <int NA>
 __global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
     const float* __restrict__ a, const float* __restrict__ w, const float* __restrict__ y0, float* __restrict__ y,
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
-    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper) {
+    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   constexpr int NN = NA * NA;
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
@@ -393,7 +389,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
         for (int q = 0; q < NA; ++q) ej[q] = vj[q];
         matvec_add<NA>(sup, mc, sup, ej);
       }
-      if (sc > 0 && sc + 1 < nsuper) put_vec<NA>(agg + (sc * lanes + lane) * NA, sup);
+      if (lb_pub_agg(sc, lb_spacing) && sc + 1 < nsuper) put_vec<NA>(agg + (sc * lanes + lane) * NA, sup);
     }
     double S[NA];
 #pragma unroll
@@ -402,7 +398,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
       ap_look_back<NA>(S, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
                        k, lid, s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
-      if (sc + 1 < nsuper) {
+      if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) {
         double ms[NA][NA], o[NA];
         load_mat<NA>(ms, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN);
         matvec_add<NA>(o, ms, S, sup);
@@ -449,7 +445,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     const float* __restrict__ a, const float* __restrict__ g, const float* __restrict__ y,
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
     unsigned* __restrict__ counter, float* __restrict__ gw, double* __restrict__ part, int64_t lanes, int64_t L,
-    int64_t groups, int K, int64_t nsuper) {
+    int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   constexpr int NN = NA * NA;
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
@@ -507,7 +503,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
         for (int q = 0; q < NA; ++q) fj[q] = vj[q];
         matvec_add<NA>(sup, mc, sup, fj);
       }
-      if (sc > 0 && sc + 1 < nsuper) put_vec<NA>(agg + (sc * lanes + lane) * NA, sup);
+      if (lb_pub_agg(nsuper - 1 - sc, lb_spacing) && sc > 0) put_vec<NA>(agg + (sc * lanes + lane) * NA, sup);
     }
     double R[NA];  // state entering the super-chunk from the right
 #pragma unroll
@@ -516,7 +512,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
       ap_look_back<NA>(R, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K,
                        k, lid, s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
-      if (sc > 0) {
+      if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) {
         double ms[NA][NA], o[NA];
         load_mat<NA>(ms, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN);
         matvec_add<NA>(o, ms, R, sup);
@@ -654,13 +650,13 @@ void fwd_lb(int64_t lanes, int64_t L, const float* a, const float* w, const floa
   const LbPlan p = lb_plan(lanes, L, NA);
   double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
   double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-  hipLaunchKernelGGL((allpole_transfer2<NA>), grid_for(lanes), dim3(256), 0, s, a, Mc, Ms, lanes, p.K);
+  hipLaunchKernelGGL((allpole_transfer2<NA>), transfer_grid(lanes, NA), dim3(64), 0, s, a, Mc, Ms, lanes, p.K);
   lookback_reset_launch(ws, 2 * p.nsuper * lanes * NA, s);
   const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(allpole_fwd_lb<NA>, 64 * p.K, occ);
   hipLaunchKernelGGL((allpole_fwd_lb<NA>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, a, w,
                      y0, y, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
                      reinterpret_cast<double*>(ws + p.off_inc), reinterpret_cast<unsigned*>(ws), lanes, L, p.groups,
-                     p.K, p.nsuper);
+                     p.K, p.nsuper, lb_spacing_for(p.K));
 }
 
 template <int NA>
@@ -672,13 +668,13 @@ void bwd_lb(int64_t lanes, int64_t L, const float* g, const float* a, const floa
   if (L > 0) {
     double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
     double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-    hipLaunchKernelGGL((allpole_transfer2<NA>), grid_for(lanes), dim3(256), 0, s, a, Mc, Ms, lanes, p.K);
+    hipLaunchKernelGGL((allpole_transfer2<NA>), transfer_grid(lanes, NA), dim3(64), 0, s, a, Mc, Ms, lanes, p.K);
     lookback_reset_launch(ws, 2 * p.nsuper * lanes * NA, s);
     const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(allpole_bwd_lb<NA>, 64 * p.K, occ);
     hipLaunchKernelGGL((allpole_bwd_lb<NA>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, a, g,
                        y, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
                        reinterpret_cast<double*>(ws + p.off_inc), reinterpret_cast<unsigned*>(ws), gw, part, lanes, L,
-                       p.groups, p.K, p.nsuper);
+                       p.groups, p.K, p.nsuper, lb_spacing_for(p.K));
   }
   hipLaunchKernelGGL((allpole_finish<NA>), dim3((unsigned)p.groups), dim3(1024), 0, s, a, gw, y0, (const double*)part,
                      ga, gy0, lanes, L, p.nsuper);

@@ -131,57 +131,52 @@ TSF_DEV void matvec_add(double (&out)[NA], const double (&m)[NA][NA], const doub
   for (int r = 0; r < NA; ++r) out[r] = t[r];
 }
 
-// Both transfer matrices of one companion matrix (row 0 = -arow): Mc = C^32 and Ms = Mc^K,
-// row-major NA x NA each.
+// y = C x for the companion matrix C of a (row 0 = -a, ones on the subdiagonal), in fp64.
 template <int NA>
-TSF_DEV void companion_powers(const float* __restrict__ arow, double* __restrict__ Mc_out, double* __restrict__ Ms_out,
-                              int K) {
-  double P[NA][NA], R[NA][NA], T[NA][NA];
-  auto mul = [&](double (&dst)[NA][NA], const double (&x)[NA][NA], const double (&y)[NA][NA]) {
+TSF_DEV void companion_apply(double (&x)[NA], const double (&a)[NA]) {
+  double y0 = 0.0;
 #pragma unroll
-    for (int r = 0; r < NA; ++r)
+  for (int c = 0; c < NA; ++c) y0 = fma(-a[c], x[c], y0);
 #pragma unroll
-      for (int c = 0; c < NA; ++c) {
-        double s = 0.0;
+  for (int r = NA - 1; r > 0; --r) x[r] = x[r - 1];
+  x[0] = y0;
+}
+
+// Column `col` of both transfer matrices of one companion matrix (row 0 = -arow): Mc = C^32 and
+// Ms = C^(32 K), row-major NA x NA each. The column is C applied step by step to the unit vector
+// e_col in fp64: repeated squaring would compound rounding errors through the transient growth of
+// the powers of a non-normal C (poles near the unit circle), step-by-step application keeps them
+// at the level of the recurrence itself. One thread per column keeps the dependent chain short.
+template <int NA>
+TSF_DEV void companion_powers_col(const float* __restrict__ arow, double* __restrict__ Mc_out,
+                                  double* __restrict__ Ms_out, int K, int col) {
+  double a[NA], x[NA];
 #pragma unroll
-        for (int j = 0; j < NA; ++j) s = fma(x[r][j], y[j][c], s);
-        T[r][c] = s;
-      }
+  for (int c = 0; c < NA; ++c) {
+    a[c] = (double)arow[c];
+    x[c] = c == col ? 1.0 : 0.0;
+  }
+  for (int step = 1; step <= 32 * K; ++step) {
+    companion_apply<NA>(x, a);
+    if (step == 32)
 #pragma unroll
-    for (int r = 0; r < NA; ++r)
-#pragma unroll
-      for (int c = 0; c < NA; ++c) dst[r][c] = T[r][c];
-  };
-#pragma unroll
-  for (int r = 0; r < NA; ++r)
-#pragma unroll
-    for (int c = 0; c < NA; ++c) P[r][c] = (r == 0) ? -(double)arow[c] : (c == r - 1 ? 1.0 : 0.0);
-  for (int i = 0; i < 5; ++i) mul(P, P, P);  // C^32
-#pragma unroll
-  for (int r = 0; r < NA; ++r)
-#pragma unroll
-    for (int c = 0; c < NA; ++c) {
-      Mc_out[r * NA + c] = P[r][c];
-      R[r][c] = (r == c) ? 1.0 : 0.0;
-    }
-  for (int k = K; k > 0; k >>= 1) {
-    if (k & 1) mul(R, R, P);
-    if (k > 1) mul(P, P, P);
+      for (int r = 0; r < NA; ++r) Mc_out[r * NA + col] = x[r];
   }
 #pragma unroll
-  for (int r = 0; r < NA; ++r)
-#pragma unroll
-    for (int c = 0; c < NA; ++c) Ms_out[r * NA + c] = R[r][c];
+  for (int r = 0; r < NA; ++r) Ms_out[r * NA + col] = x[r];
 }
 
 // Both transfer matrices per lane ([lanes][NA][NA] each), a [lanes, NA].
+// One thread per (lane, column).
 template <int NA>
-__global__ void __launch_bounds__(256) allpole_transfer2(const float* __restrict__ a, double* __restrict__ Mc,
-                                                         double* __restrict__ Ms, int64_t lanes, int K) {
-  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (lane >= lanes) return;
-  companion_powers<NA>(a + lane * NA, Mc + lane * NA * NA, Ms + lane * NA * NA, K);
+__global__ void __launch_bounds__(64) allpole_transfer2(const float* __restrict__ a, double* __restrict__ Mc,
+                                                        double* __restrict__ Ms, int64_t lanes, int K) {
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= lanes * NA) return;
+  const int64_t lane = idx / NA;
+  companion_powers_col<NA>(a + lane * NA, Mc + lane * NA * NA, Ms + lane * NA * NA, K, (int)(idx - lane * NA));
 }
+inline dim3 transfer_grid(int64_t lanes, int na) { return dim3((unsigned)((lanes * na + 63) / 64)); }
 
 template <int NA>
 TSF_DEV bool get_vec(const double* __restrict__ p, double (&x)[NA]) {

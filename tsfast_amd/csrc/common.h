@@ -257,3 +257,5 @@ inline unsigned device_cus() {
 // Host side: status of the launches just enqueued (records the HIP error for the status string).
 int tsf_record_hip_error(hipError_t e);
 inline int tsf_launch_status() { return tsf_record_hip_error(hipGetLastError()); }
+// Process-wide deterministic mode of the look-back scans (tsfast_hip_set_deterministic).
+int tsf_deterministic();

@@ -172,7 +172,7 @@ __global__ void __launch_bounds__(1024) diag_fwd(const T* __restrict__ lam, cons
                                                  Map<typename Wide<T>::type>* __restrict__ agg,
                                                  typename Wide<T>::type* __restrict__ inc, unsigned* __restrict__ counter,
                                                  int64_t lanes, int64_t L, int64_t N, int64_t groups, int K,
-                                                 int64_t nsuper) {
+                                                 int64_t nsuper, int lb_spacing) {
   using W = typename Wide<T>::type;
   __shared__ W s_e[kMaxWaves][64];
   // the look-back window, then (once the look-back is done) the state entering each chunk
@@ -227,14 +227,14 @@ __global__ void __launch_bounds__(1024) diag_fwd(const T* __restrict__ lam, cons
     if (k == 0 && live) {
       sup.e = s_e[0][lid];
       for (int j = 1; j < K; ++j) sup.e = Num<W>::fma(Pc, sup.e, s_e[j][lid]);
-      if (sc > 0 && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
+      if (lb_pub_agg(sc, lb_spacing) && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
     }
     W s = x0 && live && k == 0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
     if (sc > 0)  // uniform over the workgroup
       s = look_back(agg, inc, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
                     s_pos, &s_any);
     if (k == 0 && live) {
-      if (sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
+      if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
       for (int j = 0; j < K; ++j) {
         s_start[j][lid] = s;
         s = Num<W>::fma(Pc, s, s_e[j][lid]);
@@ -273,7 +273,7 @@ __global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, cons
                                                  typename Wide<T>::type* __restrict__ inc, unsigned* __restrict__ counter,
                                                  T* __restrict__ gv, typename Wide<T>::type* __restrict__ part,
                                                  T* __restrict__ glam, T* __restrict__ gx0, int64_t lanes, int64_t L,
-                                                 int64_t N, int64_t groups, int K, int64_t nsuper) {
+                                                 int64_t N, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   using W = typename Wide<T>::type;
   __shared__ W s_f[kMaxWaves][64];
   // the look-back window, then G entering each chunk from the right (s_start) and the glam
@@ -357,14 +357,14 @@ __global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, cons
     if (k == 0 && live) {
       sup.e = s_f[K - 1][lid];
       for (int j = K - 2; j >= 0; --j) sup.e = Num<W>::fma(Pc, sup.e, s_f[j][lid]);
-      if (sc > 0 && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
+      if (lb_pub_agg(nsuper - 1 - sc, lb_spacing) && sc > 0) put(agg + sc * lanes + lane, sup);
     }
     W R = Num<W>::zero();  // G entering the super-chunk from the right
     if (sc + 1 < nsuper)   // uniform over the workgroup
       R = look_back(agg, inc, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid, s_win, s_flag, s_pos,
                     &s_any);
     if (k == 0 && live) {
-      if (sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
+      if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
       for (int j = K - 1; j >= 0; --j) {
         s_start[j][lid] = R;
         R = Num<W>::fma(Pc, R, s_f[j][lid]);
@@ -446,7 +446,7 @@ __global__ void __launch_bounds__(1024) sel_fwd(const float* __restrict__ a, con
                                                 const float* __restrict__ x0, float* __restrict__ out,
                                                 Map<double>* __restrict__ agg, double* __restrict__ inc,
                                                 unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t N,
-                                                int64_t groups, int K, int64_t nsuper) {
+                                                int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   __shared__ double2 s_m[kMaxWaves][64];  // chunk maps (P, e)
   // the look-back window, then the state entering each chunk
   __shared__ Map<double> s_win[kMaxWaves][64];
@@ -505,14 +505,14 @@ __global__ void __launch_bounds__(1024) sel_fwd(const float* __restrict__ a, con
     Map<double> sup = {1.0, 0.0};
     if (k == 0 && live) {
       for (int j = 0; j < K; ++j) sup = then(sup, Map<double>{s_m[j][lid].x, s_m[j][lid].y});
-      if (sc > 0 && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
+      if (lb_pub_agg(sc, lb_spacing) && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
     }
     double s = x0 && live && k == 0 ? (double)x0[lane] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       s = look_back(agg, inc, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
                     s_pos, &s_any);
     if (k == 0 && live) {
-      if (sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
+      if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
       for (int j = 0; j < K; ++j) {
         s_start[j][lid] = s;
         s = fma(s_m[j][lid].x, s, s_m[j][lid].y);
@@ -548,7 +548,7 @@ __global__ void __launch_bounds__(1024) sel_bwd(const float* __restrict__ a, con
                                                 Map<double>* __restrict__ agg, double* __restrict__ inc,
                                                 unsigned* __restrict__ counter, float* __restrict__ glam,
                                                 float* __restrict__ gv, float* __restrict__ gx0, int64_t lanes,
-                                                int64_t L, int64_t N, int64_t groups, int K, int64_t nsuper) {
+                                                int64_t L, int64_t N, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   __shared__ double2 s_m[kMaxWaves][64];
   // the look-back window, then G entering each chunk from the right
   __shared__ Map<double> s_win[kMaxWaves][64];
@@ -611,14 +611,14 @@ __global__ void __launch_bounds__(1024) sel_bwd(const float* __restrict__ a, con
     if (k == 0 && live) {
       sup = Map<double>{s_m[K - 1][lid].x, s_m[K - 1][lid].y};
       for (int j = K - 2; j >= 0; --j) sup = then(sup, Map<double>{s_m[j][lid].x, s_m[j][lid].y});
-      if (sc > 0 && sc + 1 < nsuper) put(agg + sc * lanes + lane, sup);
+      if (lb_pub_agg(nsuper - 1 - sc, lb_spacing) && sc > 0) put(agg + sc * lanes + lane, sup);
     }
     double R = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
       R = look_back(agg, inc, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
                     s_pos, &s_any);
     if (k == 0 && live) {
-      if (sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
+      if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
       for (int j = K - 1; j >= 0; --j) {
         s_start[j][lid] = R;
         R = fma(s_m[j][lid].x, R, s_m[j][lid].y);
@@ -722,7 +722,7 @@ void diag_fwd_launch(const DiagTile& t, const T* lam, const T* v, const T* x0, T
   auto* inc = reinterpret_cast<W*>(agg + t.nsuper * t.lanes);
   lookback_reset_launch(ws, lookback_bytes(t, sizeof(W)) / 8, s);
   hipLaunchKernelGGL((diag_fwd<T, TC>), dim3(persistent_grid(t, diag_fwd<T, TC>, occ)), dim3(64 * t.K), 0, s, lam, v,
-                     x0, out, agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper);
+                     x0, out, agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper, lb_spacing_for(kAnchorSpacing));
 }
 
 template <typename T, int TC>
@@ -736,7 +736,7 @@ void diag_bwd_launch(const DiagTile& t, const T* g, const T* lam, const T* out, 
   lookback_reset_launch(ws, lookback_bytes(t, sizeof(W)) / 8, s);
   hipLaunchKernelGGL((diag_bwd<T, TC>), dim3(persistent_grid(t, diag_bwd<T, TC>, occ)), dim3(64 * t.K), 0, s, lam, g,
                      out, x0, agg, inc, reinterpret_cast<unsigned*>(ws), gv, part, glam, gx0, t.lanes, L, N, t.groups,
-                     t.K, t.nsuper);
+                     t.K, t.nsuper, lb_spacing_for(kAnchorSpacing));
   if (t.nsuper > 1)
     hipLaunchKernelGGL(diag_sum_parts<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, (const W*)part, glam,
                        t.lanes, t.nsuper);
@@ -750,7 +750,7 @@ void sel_fwd_launch(const DiagTile& t, const float* a, const float* v, const flo
   auto* inc = reinterpret_cast<double*>(agg + t.nsuper * t.lanes);
   lookback_reset_launch(ws, lookback_bytes(t, 8) / 8, s);
   hipLaunchKernelGGL((sel_fwd<TC>), dim3(persistent_grid(t, sel_fwd<TC>, occ)), dim3(64 * t.K), 0, s, a, v, x0, out,
-                     agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper);
+                     agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper, lb_spacing_for(kAnchorSpacing));
 }
 
 void sel_bwd_launch(const DiagTile& t, const float* g, const float* a, const float* out, const float* x0, float* glam,
@@ -761,7 +761,7 @@ void sel_bwd_launch(const DiagTile& t, const float* g, const float* a, const flo
   lookback_reset_launch(ws, lookback_bytes(t, 8) / 8, s);
   hipLaunchKernelGGL((sel_bwd<16>), dim3(persistent_grid(t, sel_bwd<16>, occ)), dim3(64 * t.K), 0, s, a, g, out, x0,
                      agg, inc, reinterpret_cast<unsigned*>(ws), glam, gv, gx0, t.lanes, L, N, t.groups, t.K,
-                     t.nsuper);
+                     t.nsuper, lb_spacing_for(kAnchorSpacing));
 }
 
 }  // namespace

@@ -101,13 +101,16 @@ TSF_DEV void load_coeffs(double (&av)[NA], float (&bk)[NBT], const float* __rest
 }
 
 // Transfer matrices per lane from its pair's coefficients a [O, I, NA] (lane = b * P + j * O + o).
+// One thread per (lane, column).
 template <int NA>
-__global__ void __launch_bounds__(256) gblock_transfer(const float* __restrict__ acoef, double* __restrict__ Mc,
-                                                       double* __restrict__ Ms, int64_t lanes, int I, int O, int K) {
-  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (lane >= lanes) return;
+__global__ void __launch_bounds__(64) gblock_transfer(const float* __restrict__ acoef, double* __restrict__ Mc,
+                                                      double* __restrict__ Ms, int64_t lanes, int I, int O, int K) {
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= lanes * NA) return;
+  const int64_t lane = idx / NA;
   const int P = I * O, p = (int)(lane % P), j = p / O, o = p % O;
-  companion_powers<NA>(acoef + (o * I + j) * NA, Mc + lane * NA * NA, Ms + lane * NA * NA, K);
+  companion_powers_col<NA>(acoef + (o * I + j) * NA, Mc + lane * NA * NA, Ms + lane * NA * NA, K,
+                           (int)(idx - lane * NA));
 }
 
 // ---------------------------------------------------------------------------------- forward
@@ -117,7 +120,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
     const float* __restrict__ u_tail, const float* __restrict__ x0, float* __restrict__ y, float* __restrict__ x_last,
     double* __restrict__ saved, const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg,
     double* __restrict__ inc, unsigned* __restrict__ counter, int64_t B, int64_t L, int I, int O, int nb,
-    int64_t groups, int K, int64_t nsuper) {
+    int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
   __shared__ int s_pend[64];
@@ -178,7 +181,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
         for (int q = 0; q < NA; ++q) ej[q] = vj[q];
         matvec_add<NA>(sup, mc, sup, ej);
       }
-      if (sc > 0 && sc + 1 < nsuper) put_vec<NA>(agg + (sc * lanes + lane) * NA, sup);
+      if (lb_pub_agg(sc, lb_spacing) && sc + 1 < nsuper) put_vec<NA>(agg + (sc * lanes + lane) * NA, sup);
     }
     double S[NA];
 #pragma unroll
@@ -191,7 +194,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
 #pragma unroll
         for (int q = 0; q < NA; ++q) saved[(sc * lanes + lane) * NA + q] = S[q];
       }
-      if (sc + 1 < nsuper) {
+      if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) {
         double ms[NA][NA], o[NA];
         load_mat<NA>(ms, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA);
         matvec_add<NA>(o, ms, S, sup);
@@ -266,7 +269,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     const float* __restrict__ x0, const double* __restrict__ saved, const double* __restrict__ Mc,
     const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc, unsigned* __restrict__ counter,
     float* __restrict__ gu, float* __restrict__ gu_tail, double* __restrict__ part_ga, double* __restrict__ part_gb,
-    double* __restrict__ gh, int64_t B, int64_t L, int I, int O, int nb, int64_t groups, int K, int64_t nsuper) {
+    double* __restrict__ gh, int64_t B, int64_t L, int I, int O, int nb, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   static_assert(64 * (NA * sizeof(double) + NBT * sizeof(float)) <= sizeof(LdsTile), "partials fit in a tile");
   constexpr int V = 2 * NA;  // adjoint state: G then c
   __shared__ LdsTile s_lds[kLbWaves];
@@ -346,7 +349,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
         for (int q = 0; q < V; ++q) fj[q] = vj[q];
         block_matvec_add<NA, 2>(sup, mc, sup, fj);
       }
-      if (sc > 0 && sc + 1 < nsuper) put_vec<V>(agg + (sc * lanes + lane) * V, sup);
+      if (lb_pub_agg(nsuper - 1 - sc, lb_spacing) && sc > 0) put_vec<V>(agg + (sc * lanes + lane) * V, sup);
     }
     double Rv[V];  // adjoint state entering the super-chunk from the right
 #pragma unroll
@@ -355,7 +358,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
       ap_look_back<NA, 2>(Rv, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane,
                           K, k, lid, s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
-      if (sc > 0) {
+      if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) {
         double ms[NA][NA], o[V];
         load_mat<NA>(ms, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA);
         block_matvec_add<NA, 2>(o, ms, Rv, sup);
@@ -671,13 +674,13 @@ void fwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
   static int occ[kMaxNA + 1];
   double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
   double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-  hipLaunchKernelGGL((gblock_transfer<NA>), grid_for(p.lanes), dim3(256), 0, s, acoef, Mc, Ms, p.lanes, I, O, p.lb.K);
+  hipLaunchKernelGGL((gblock_transfer<NA>), transfer_grid(p.lanes, NA), dim3(64), 0, s, acoef, Mc, Ms, p.lanes, I, O, p.lb.K);
   lookback_reset_launch(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, s);
   const int64_t tiles = p.lb.groups * p.lb.nsuper, cap = resident_wgs(gblock_fwd_lb<NA, NBT>, 64 * p.lb.K, occ);
   hipLaunchKernelGGL((gblock_fwd_lb<NA, NBT>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.lb.K), 0, s, u,
                      bcoef, acoef, u_tail, x0, y, x_last, saved, (const double*)Mc, (const double*)Ms,
                      reinterpret_cast<double*>(ws + p.off_agg), reinterpret_cast<double*>(ws + p.off_inc),
-                     reinterpret_cast<unsigned*>(ws), B, L, I, O, nb, p.lb.groups, p.lb.K, p.lb.nsuper);
+                     reinterpret_cast<unsigned*>(ws), B, L, I, O, nb, p.lb.groups, p.lb.K, p.lb.nsuper, lb_spacing_for(p.lb.K));
 }
 
 template <int NA, int NBT>
@@ -692,7 +695,7 @@ void bwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
   if (L > 0) {
     double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
     double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-    hipLaunchKernelGGL((gblock_transfer<NA>), grid_for(p.lanes), dim3(256), 0, s, acoef, Mc, Ms, p.lanes, I, O,
+    hipLaunchKernelGGL((gblock_transfer<NA>), transfer_grid(p.lanes, NA), dim3(64), 0, s, acoef, Mc, Ms, p.lanes, I, O,
                        p.lb.K);
     lookback_reset_launch(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, s);
     const int64_t tiles = p.lb.groups * p.lb.nsuper, cap = resident_wgs(gblock_bwd_lb<NA, NBT>, 64 * p.lb.K, occ);
@@ -700,7 +703,7 @@ void bwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
                        gy, g_xlast, u, bcoef, acoef, u_tail, x0, saved, (const double*)Mc, (const double*)Ms,
                        reinterpret_cast<double*>(ws + p.off_agg), reinterpret_cast<double*>(ws + p.off_inc),
                        reinterpret_cast<unsigned*>(ws), gu, gu_tail, pa, pb, gh, B, L, I, O, nb, p.lb.groups, p.lb.K,
-                       p.lb.nsuper);
+                       p.lb.nsuper, lb_spacing_for(p.lb.K));
   } else if (gu_tail && nb > 1) {
     const int64_t nt = B * (nb - 1) * I;
     hipLaunchKernelGGL(gblock_zero, grid_for(nt), dim3(256), 0, s, gu_tail, nt);

@@ -19,7 +19,8 @@
 // s to Mc s + e (Mc = A^S), a super-chunk of K chunks to Ms s + e (Ms = A^(S K)), and only the
 // e vectors are published between workgroups. The adjoint runs the same machinery from the right
 // end with A^T; its grad_A partials are summed over the K chunks of a tile in LDS, written per
-// super-chunk, and added up in a fixed order by linrec_finish (deterministic run to run).
+// super-chunk, and added up in a fixed order by linrec_finish. (With the look-back in its
+// deterministic mode, lookback.h, every output is then bitwise reproducible run to run.)
 //
 // Arithmetic: fp32 in and out, fp64 state, transfer matrices, published words and grad_A sums.
 
@@ -43,57 +44,46 @@ constexpr int steps_per_chunk() {
   return kTileT / NS;
 }
 
-// Transfer matrices per lane: Mc = P^S and Ms = Mc^K with P = A (forward) or A^T (adjoint).
+// Transfer matrices per lane: Mc = P^S and Ms = P^(S K) with P = A (forward) or A^T (adjoint),
+// one thread per (lane, column c): column c is P applied S K times to the unit vector e_c, in
+// fp64. (Repeated squaring would compound rounding errors through the transient growth of
+// non-normal powers, which for companion matrices with poles near the unit circle reach 1e5
+// before they decay; step-by-step application keeps them at the level of the recurrence itself.)
 template <int NS>
 __global__ void __launch_bounds__(256) linrec_transfer(const float* __restrict__ A, double* __restrict__ Mc,
                                                        double* __restrict__ Ms, int64_t lanes, int K, int transpose) {
-  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (lane >= lanes) return;
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= lanes * NS) return;
+  const int64_t lane = idx / NS;
+  const int col = (int)(idx - lane * NS);
   constexpr int S = steps_per_chunk<NS>();
-  double P[NS][NS], R[NS][NS], T[NS][NS];
-  auto mul = [&](double (&dst)[NS][NS], const double (&x)[NS][NS], const double (&y)[NS][NS]) {
-#pragma unroll
-    for (int r = 0; r < NS; ++r)
-#pragma unroll
-      for (int c = 0; c < NS; ++c) {
-        double s = 0.0;
-#pragma unroll
-        for (int j = 0; j < NS; ++j) s = fma(x[r][j], y[j][c], s);
-        T[r][c] = s;
-      }
-#pragma unroll
-    for (int r = 0; r < NS; ++r)
-#pragma unroll
-      for (int c = 0; c < NS; ++c) dst[r][c] = T[r][c];
-  };
-  auto power = [&](double (&base)[NS][NS], int e) {  // R = base^e (base is consumed)
-#pragma unroll
-    for (int r = 0; r < NS; ++r)
-#pragma unroll
-      for (int c = 0; c < NS; ++c) R[r][c] = (r == c) ? 1.0 : 0.0;
-    for (; e > 0; e >>= 1) {
-      if (e & 1) mul(R, R, base);
-      if (e > 1) mul(base, base, base);
-    }
-  };
+  double P[NS][NS], x[NS];
   const float* a = A + lane * NS * NS;
 #pragma unroll
-  for (int r = 0; r < NS; ++r)
+  for (int r = 0; r < NS; ++r) {
+    x[r] = r == col ? 1.0 : 0.0;
 #pragma unroll
     for (int c = 0; c < NS; ++c) P[r][c] = (double)(transpose ? a[c * NS + r] : a[r * NS + c]);
-  power(P, S);
+  }
+  double* mc = Mc + lane * NS * NS + col;
+  double* ms = Ms + lane * NS * NS + col;
+  for (int step = 1; step <= S * K; ++step) {
+    double y[NS];
 #pragma unroll
-  for (int r = 0; r < NS; ++r)
+    for (int r = 0; r < NS; ++r) {
+      double acc = 0.0;
 #pragma unroll
-    for (int c = 0; c < NS; ++c) {
-      Mc[lane * NS * NS + r * NS + c] = R[r][c];
-      P[r][c] = R[r][c];
+      for (int c = 0; c < NS; ++c) acc = fma(P[r][c], x[c], acc);
+      y[r] = acc;
     }
-  power(P, K);
 #pragma unroll
-  for (int r = 0; r < NS; ++r)
+    for (int r = 0; r < NS; ++r) x[r] = y[r];
+    if (step == S)
 #pragma unroll
-    for (int c = 0; c < NS; ++c) Ms[lane * NS * NS + r * NS + c] = R[r][c];
+      for (int r = 0; r < NS; ++r) mc[r * NS] = x[r];
+  }
+#pragma unroll
+  for (int r = 0; r < NS; ++r) ms[r * NS] = x[r];
 }
 
 // The lane's matrix (or its transpose) in fp64. The kernels load it once before the look-back
@@ -131,7 +121,7 @@ template <int NS>
 __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per_eu(4))) linrec_fwd_lb(
     const float* __restrict__ A, const float* __restrict__ v, const float* __restrict__ x0, float* __restrict__ x,
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
-    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper) {
+    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   constexpr int S = steps_per_chunk<NS>(), NN = NS * NS;
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
@@ -214,7 +204,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
         for (int q = 0; q < NS; ++q) ej[q] = vj[q];
         matvec_add<NS>(sup, mc, sup, ej);
       }
-      if (sc > 0 && sc + 1 < nsuper) put_vec<NS>(agg + (sc * lanes + lane) * NS, sup);
+      if (lb_pub_agg(sc, lb_spacing) && sc + 1 < nsuper) put_vec<NS>(agg + (sc * lanes + lane) * NS, sup);
     }
     double St[NS];
 #pragma unroll
@@ -223,7 +213,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
       ap_look_back<NS>(St, agg, inc, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
                        k, lid, s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
-      if (sc + 1 < nsuper) {
+      if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) {
         double ms[NS][NS], o[NS];
         load_mat<NS>(ms, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN);
         matvec_add<NS>(o, ms, St, sup);
@@ -282,7 +272,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     const float* __restrict__ A, const float* __restrict__ g, const float* __restrict__ out,
     const float* __restrict__ x0, float* __restrict__ gv, float* __restrict__ gx0, const double* __restrict__ Mc,
     const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc, double* __restrict__ part,
-    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper) {
+    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   constexpr int S = steps_per_chunk<NS>(), NN = NS * NS;
   static_assert(64 * NN * sizeof(double) <= sizeof(LdsTile), "a wave's grad_A sums fit in its tile");
   __shared__ LdsTile s_lds[kLbWaves];
@@ -342,7 +332,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
         for (int q = 0; q < NS; ++q) fj[q] = vj[q];
         matvec_add<NS>(sup, mc, sup, fj);
       }
-      if (sc > 0 && sc + 1 < nsuper) put_vec<NS>(agg + (sc * lanes + lane) * NS, sup);
+      if (lb_pub_agg(nsuper - 1 - sc, lb_spacing) && sc > 0) put_vec<NS>(agg + (sc * lanes + lane) * NS, sup);
     }
     double R[NS];  // adjoint state entering the super-chunk from the right
 #pragma unroll
@@ -351,7 +341,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
       ap_look_back<NS>(R, agg, inc, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid,
                        s_lds, s_flag, s_pend, &s_any);
     if (k == 0 && live) {
-      if (sc > 0) {
+      if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) {
         double ms[NS][NS], o[NS];
         load_mat<NS>(ms, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN);
         matvec_add<NS>(o, ms, R, sup);
@@ -512,13 +502,13 @@ int fwd_impl(int64_t lanes, int64_t L, const float* A, const float* v, const flo
   const LrPlan p = lr_plan(lanes, L, NS);
   double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
   double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes)), dim3(256), 0, s, A, Mc, Ms, lanes, p.K, 0);
+  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes * NS)), dim3(256), 0, s, A, Mc, Ms, lanes, p.K, 0);
   lookback_reset_launch(ws, 2 * p.nsuper * lanes * NS, s);
   const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(linrec_fwd_lb<NS>, 64 * p.K, occ);
   hipLaunchKernelGGL((linrec_fwd_lb<NS>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, A, v, x0,
                      x, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
                      reinterpret_cast<double*>(ws + p.off_inc), reinterpret_cast<unsigned*>(ws), lanes, L, p.groups,
-                     p.K, p.nsuper);
+                     p.K, p.nsuper, lb_spacing_for(p.K));
   return tsf_launch_status();
 }
 
@@ -535,13 +525,13 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const flo
   double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
   double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
   double* part = reinterpret_cast<double*>(ws + p.off_part);
-  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes)), dim3(256), 0, s, A, Mc, Ms, lanes, p.K, 1);
+  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes * NS)), dim3(256), 0, s, A, Mc, Ms, lanes, p.K, 1);
   lookback_reset_launch(ws, 2 * p.nsuper * lanes * NS, s);
   const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(linrec_bwd_lb<NS>, 64 * p.K, occ);
   hipLaunchKernelGGL((linrec_bwd_lb<NS>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, A, g, out,
                      x0, gv, gx0, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
                      reinterpret_cast<double*>(ws + p.off_inc), part, reinterpret_cast<unsigned*>(ws), lanes, L,
-                     p.groups, p.K, p.nsuper);
+                     p.groups, p.K, p.nsuper, lb_spacing_for(p.K));
   hipLaunchKernelGGL(linrec_finish, dim3((unsigned)((lanes * NS * NS + 63) / 64)), dim3(1024), 0, s,
                      (const double*)part, gA, lanes * NS * NS, p.nsuper);
   return tsf_launch_status();
@@ -624,35 +614,37 @@ TSF_DEV void st_step(float* __restrict__ p, const double (&s)[NS]) {
   }
 }
 
-// M = P^e per lane, P = A or A^T (binary powering in fp64)
+// M = P^e per lane, P = A or A^T, one thread per (lane, column c): column c is P applied e times
+// to the unit vector e_c in fp64 (step-by-step, as linrec_transfer, for the same accuracy reason).
 template <int NS>
 __global__ void __launch_bounds__(64) lw_power(const float* __restrict__ A, double* __restrict__ M, int64_t lanes,
                                                 int e, int transpose) {
-  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (lane >= lanes) return;
-  double B[NS][NS], R[NS][NS], T[NS][NS];
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= lanes * NS) return;
+  const int64_t lane = idx / NS;
+  const int col = (int)(idx - lane * NS);
+  double P[NS][NS], x[NS];
   const float* a = A + lane * NS * NS;
-  for (int r = 0; r < NS; ++r)
-    for (int c = 0; c < NS; ++c) {
-      B[r][c] = (double)(transpose ? a[c * NS + r] : a[r * NS + c]);
-      R[r][c] = r == c ? 1.0 : 0.0;
-    }
-  auto mul = [&](double (&dst)[NS][NS], const double (&x)[NS][NS], const double (&y)[NS][NS]) {
-    for (int r = 0; r < NS; ++r)
-      for (int c = 0; c < NS; ++c) {
-        double acc = 0.0;
-        for (int j = 0; j < NS; ++j) acc = fma(x[r][j], y[j][c], acc);
-        T[r][c] = acc;
-      }
-    for (int r = 0; r < NS; ++r)
-      for (int c = 0; c < NS; ++c) dst[r][c] = T[r][c];
-  };
-  for (; e > 0; e >>= 1) {
-    if (e & 1) mul(R, R, B);
-    if (e > 1) mul(B, B, B);
+#pragma unroll
+  for (int r = 0; r < NS; ++r) {
+    x[r] = r == col ? 1.0 : 0.0;
+#pragma unroll
+    for (int c = 0; c < NS; ++c) P[r][c] = (double)(transpose ? a[c * NS + r] : a[r * NS + c]);
   }
-  for (int r = 0; r < NS; ++r)
-    for (int c = 0; c < NS; ++c) M[lane * NS * NS + r * NS + c] = R[r][c];
+  for (int step = 0; step < e; ++step) {
+    double y[NS];
+#pragma unroll
+    for (int r = 0; r < NS; ++r) {
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < NS; ++c) acc = fma(P[r][c], x[c], acc);
+      y[r] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < NS; ++r) x[r] = y[r];
+  }
+#pragma unroll
+  for (int r = 0; r < NS; ++r) M[lane * NS * NS + r * NS + col] = x[r];
 }
 
 // Forward chunk ends from a zero state: e [nchunks][lanes][NS]
@@ -957,7 +949,7 @@ int wide_fwd_impl(int64_t lanes, int64_t L, const float* A, const float* v, cons
   double* M = reinterpret_cast<double*>(ws + p.off_M);
   const dim3 grid((unsigned)((lanes + kWideThreads - 1) / kWideThreads), (unsigned)p.nchunks);
   const unsigned lb = (unsigned)((lanes + 63) / 64);
-  hipLaunchKernelGGL((lw_power<NS>), dim3(lb), dim3(64), 0, s, A, M, lanes, kWideT, 0);
+  hipLaunchKernelGGL((lw_power<NS>), dim3((unsigned)((lanes * NS + 63) / 64)), dim3(64), 0, s, A, M, lanes, kWideT, 0);
   hipLaunchKernelGGL((lw_sum_fwd<NS, VEC>), grid, dim3(kWideThreads), 0, s, A, v, e, lanes, L);
   hipLaunchKernelGGL((lw_carry_fwd<NS>), dim3(lb), dim3(64), 0, s, (const double*)M, x0, (const double*)e, carry,
                      lanes, p.nchunks);
@@ -980,7 +972,7 @@ int wide_bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, cons
   double* part = reinterpret_cast<double*>(ws + p.off_part);
   const dim3 grid((unsigned)((lanes + kWideThreads - 1) / kWideThreads), (unsigned)p.nchunks);
   const unsigned lb = (unsigned)((lanes + 63) / 64);
-  hipLaunchKernelGGL((lw_power<NS>), dim3(lb), dim3(64), 0, s, A, M, lanes, kWideT, 1);
+  hipLaunchKernelGGL((lw_power<NS>), dim3((unsigned)((lanes * NS + 63) / 64)), dim3(64), 0, s, A, M, lanes, kWideT, 1);
   hipLaunchKernelGGL((lw_sum_bwd<NS, VEC>), grid, dim3(kWideThreads), 0, s, A, g, f, lanes, L);
   hipLaunchKernelGGL((lw_carry_bwd<NS>), dim3(lb), dim3(64), 0, s, A, (const double*)M, (const double*)f, rc, gx0,
                      lanes, p.nchunks);

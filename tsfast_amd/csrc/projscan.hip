@@ -18,10 +18,11 @@
 // An MFMA result holds steps 4g .. 4g+3 of column j in lane (g, j) (g = lane / 16, j = lane % 16),
 // so the recurrence runs serially over a lane's 4 steps, then across the 4 lane groups (two
 // shift-and-combine stages through ds_bpermute), then from block to block.
-// Chunks are chained by decoupled look-back: a tile publishes its chunk's end state from a zero
-// start (agg), takes the state entering its chunk from the tiles before it in the same row
-// (walking back over published aggs to a published inc), and publishes the state leaving its
-// chunk (inc). Carries are fp64; the chunk-entering states are saved for the backward pass.
+// Chunks are chained by decoupled look-back with anchored publication (lookback.h): every eighth
+// chunk of a row in scan order publishes the state leaving it (inc), the others their end state
+// from a zero start (agg); a tile walks back over the aggs to the nearest anchor's inc, so the
+// state entering each chunk is composed the same way on every run. Carries are fp64; the
+// chunk-entering states are saved for the backward pass.
 #include <algorithm>
 
 #include "common.h"
@@ -128,7 +129,7 @@ __global__ void __launch_bounds__(256, 1)
                  const float2* __restrict__ lam, const float* __restrict__ c_re, const float* __restrict__ c_im,
                  const float2* __restrict__ x0, float* __restrict__ y, float2* __restrict__ x_last,
                  float2* __restrict__ saved, double2* __restrict__ agg, double2* __restrict__ inc,
-                 unsigned* __restrict__ counter, int B, int L, int H, int N, int O, int nchunks, int nsub) {
+                 unsigned* __restrict__ counter, int B, int L, int H, int N, int O, int nchunks, int nsub, int lb_spacing) {
   __shared__ __attribute__((aligned(16))) float s_xt[kMaxWaves][kBlk][kXtStride];
   __shared__ float s_y[2][kMaxWaves][kBlk][16 * OB];
   __shared__ unsigned s_tile[2];
@@ -229,10 +230,11 @@ __global__ void __launch_bounds__(256, 1)
     if (c == 0) {
       cin = (x0 != nullptr && s_lb < N) ? up2(x0[(int64_t)b * N + s_lb]) : Num<double2>::zero();
     } else {
-      if (c + 1 < nchunks) put(agg + (int64_t)c * cstride + widx, agg_v);
+      if (lb_pub_agg(c, lb_spacing) && c + 1 < nchunks) put(agg + (int64_t)c * cstride + widx, agg_v);
       cin = walk(agg, inc, cstride, widx, c, -1, nchunks, P64);
     }
-    if (c + 1 < nchunks) put(inc + (int64_t)c * cstride + widx, Num<double2>::fma(P64, cin, agg_v));
+    if (lb_pub_inc(c, lb_spacing) && c + 1 < nchunks)
+      put(inc + (int64_t)c * cstride + widx, Num<double2>::fma(P64, cin, agg_v));
     float2 carry[kSlots];
     {
       const float2 cf = down2(cin);
@@ -398,7 +400,7 @@ __global__ void __launch_bounds__(256, 1)
                  const float2* __restrict__ lam, const float* __restrict__ c_re, const float* __restrict__ c_im,
                  float* __restrict__ g_u, float2* __restrict__ g_x0, float* __restrict__ part, int64_t part_stride,
                  double2* __restrict__ agg, double2* __restrict__ inc, unsigned* __restrict__ counter, int B, int L,
-                 int H, int N, int O, int nsub) {
+                 int H, int N, int O, int nsub, int lb_spacing) {
   constexpr int HB = KS == 8 ? 2 : 1;  // 16-wide h blocks of g_u and grad W (H <= 16 HB)
   constexpr int OKS = 4 * OB;          // o per lane group in the g_x product (O <= 16 OB)
   __shared__ __attribute__((aligned(16))) float s_wu[kMaxWaves][16 * HB][kWuStride];
@@ -504,11 +506,11 @@ __global__ void __launch_bounds__(256, 1)
     const int64_t widx = (int64_t)b * NS + s_lb;
     double2 R = Num<double2>::zero();  // G at the first step of the next chunk
     if (c + 1 < nsub) {
-      if (c > 0) put(agg + (int64_t)c * cstride + widx, agg_v);
+      if (lb_pub_agg(cr, lb_spacing) && c > 0) put(agg + (int64_t)c * cstride + widx, agg_v);
       R = walk(agg, inc, cstride, widx, c, +1, nsub, cP32);
     }
     const double2 first = Num<double2>::fma(cP32, R, agg_v);  // G at this chunk's first step
-    if (c > 0) put(inc + (int64_t)c * cstride + widx, first);
+    if (lb_pub_inc(cr, lb_spacing) && c > 0) put(inc + (int64_t)c * cstride + widx, first);
     if (c == 0 && g_x0 != nullptr && s_lb < N) g_x0[(int64_t)b * N + s_lb] = down2(Num<double2>::mul(conj2(a_lb), first));
     float2 Rq[kSlots];
     {
@@ -800,7 +802,7 @@ void fwd_launch(const PsPlan& p, int64_t B, int64_t L, int64_t H, int64_t N, int
   hipLaunchKernelGGL((projscan_fwd<KS, OB>), dim3((unsigned)(p.tiles < cap ? p.tiles : cap)), dim3(threads), 0, s, u,
                      w_re, w_im, lam, c_re, c_im, x0, y, x_last, saved, reinterpret_cast<double2*>(ws + p.off_agg),
                      reinterpret_cast<double2*>(ws + p.off_inc), reinterpret_cast<unsigned*>(ws), (int)B, (int)L,
-                     (int)H, (int)N, (int)O, (int)p.nchunks, (int)p.nsub);
+                     (int)H, (int)N, (int)O, (int)p.nchunks, (int)p.nsub, lb_spacing_for(kAnchorSpacing));
 }
 
 template <int KS, int OB>
@@ -817,7 +819,7 @@ void bwd_launch(const PbPlan& p, int64_t B, int64_t L, int64_t H, int64_t N, int
   hipLaunchKernelGGL((projscan_bwd<KS, OB>), dim3((unsigned)grid), dim3(threads), 0, s, gy, g_xlast, saved, u, w_re,
                      w_im, lam, c_re, c_im, g_u, g_x0, part, p.part_stride,
                      reinterpret_cast<double2*>(ws + p.off_agg), reinterpret_cast<double2*>(ws + p.off_inc),
-                     reinterpret_cast<unsigned*>(ws), (int)B, (int)L, (int)H, (int)N, (int)O, (int)p.nsub);
+                     reinterpret_cast<unsigned*>(ws), (int)B, (int)L, (int)H, (int)N, (int)O, (int)p.nsub, lb_spacing_for(kAnchorSpacing));
   const int64_t outs = 2 * N * H + 2 * O * N + 2 * N;
   hipLaunchKernelGGL(projscan_bwd_reduce, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, part, p.part_stride,
                      grid, (int)N, p.nw * 64, (int)H, KS == 8 ? 32 : 16, (int)O, 16 * OB, g_w_re, g_w_im, g_c_re,

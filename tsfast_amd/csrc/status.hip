@@ -1,12 +1,20 @@
 // Status reporting for the C ABI (host code only).
 #include <stdio.h>
 
+#include <atomic>
+
 #include "common.h"
 #include "tsfast_hip.h"
 
 namespace {
 thread_local char g_msg[256];
 }
+
+namespace {
+std::atomic<int> g_deterministic{0};
+}
+
+int tsf_deterministic() { return g_deterministic.load(std::memory_order_relaxed); }
 
 int tsf_record_hip_error(hipError_t e) {
   if (e == hipSuccess) return TSF_OK;
@@ -17,6 +25,9 @@ int tsf_record_hip_error(hipError_t e) {
 extern "C" {
 
 int tsfast_hip_version(void) { return 1; }
+
+void tsfast_hip_set_deterministic(int on) { g_deterministic.store(on ? 1 : 0, std::memory_order_relaxed); }
+int tsfast_hip_get_deterministic(void) { return tsf_deterministic(); }
 
 const char* tsfast_hip_status_string(int status) {
   switch (status) {

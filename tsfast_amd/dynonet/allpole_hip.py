@@ -52,6 +52,7 @@ def supports(a: torch.Tensor, w: torch.Tensor, y0: torch.Tensor | None) -> str |
 @torch.library.custom_op("tsfast_hip::dynonet_allpole", mutates_args=())
 def _allpole_op(a: torch.Tensor, w: torch.Tensor, y0: torch.Tensor | None) -> torch.Tensor:
     lib = _lib.load()
+    _lib.sync_deterministic()
     a, w = a.contiguous(), w.contiguous()
     y0 = y0.contiguous() if y0 is not None else None
     for name, t in (("a", a), ("w", w), ("y0", y0)):
@@ -80,6 +81,7 @@ def _allpole_bwd_op(
     g: torch.Tensor, a: torch.Tensor, y: torch.Tensor, y0: torch.Tensor | None
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     lib = _lib.load()
+    _lib.sync_deterministic()
     g, a, y = g.contiguous(), a.contiguous(), y.contiguous()
     y0 = y0.contiguous() if y0 is not None else None
     for name, t in (("g", g), ("a", a), ("y", y), ("y0", y0)):

@@ -83,6 +83,7 @@ def _gblock_op(
     u: torch.Tensor, b: torch.Tensor, a: torch.Tensor, u_tail: torch.Tensor | None, x0: torch.Tensor | None
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     lib = _lib.load()
+    _lib.sync_deterministic()
     u, b, a = u.contiguous(), b.contiguous(), a.contiguous()
     u_tail = u_tail.contiguous() if u_tail is not None else None
     x0 = x0.contiguous() if x0 is not None else None
@@ -120,6 +121,7 @@ def _gblock_bwd_op(
     u_tail: torch.Tensor | None, x0: torch.Tensor | None, saved: torch.Tensor,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     lib = _lib.load()
+    _lib.sync_deterministic()
     gy = gy.contiguous()
     g_xlast = g_xlast.contiguous() if g_xlast is not None else None
     _lib.require(gy, "gy", (torch.float32,), u.device)

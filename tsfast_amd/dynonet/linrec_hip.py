@@ -60,6 +60,7 @@ def _workspace(lib, lanes, L, n, device):
 @torch.library.custom_op("tsfast_hip::linear_recurrence_hip", mutates_args=())
 def _linrec_op(A: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> torch.Tensor:
     lib = _lib.load()
+    _lib.sync_deterministic()
     A, v = A.contiguous(), v.contiguous()
     x0 = x0.contiguous() if x0 is not None else None
     for name, t in (("A", A), ("v", v), ("x0", x0)):
@@ -86,6 +87,7 @@ def _linrec_bwd_op(
     g: torch.Tensor, A: torch.Tensor, out: torch.Tensor, x0: torch.Tensor | None
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     lib = _lib.load()
+    _lib.sync_deterministic()
     g, A, out = g.contiguous(), A.contiguous(), out.contiguous()
     x0 = x0.contiguous() if x0 is not None else None
     for name, t in (("g", g), ("A", A), ("out", out), ("x0", x0)):

@@ -23,6 +23,7 @@ from .. import _lib
 
 _IO_DTYPES = {torch.float32: _lib.TSF_DTYPE_F32, torch.bfloat16: _lib.TSF_DTYPE_BF16}
 _PARAM_DTYPES = (torch.float32, torch.bfloat16)
+_SEG = 128  # steps per workgroup segment (conv.hip kSeg); tests pin it against the library's size query
 
 
 def supports(x, tail, weight, bias) -> str | None:
@@ -53,8 +54,18 @@ def supports(x, tail, weight, bias) -> str | None:
         return f"tail.shape {tuple(tail.shape)} != {(B, D, K - 1)}"
     if bias is not None and tuple(bias.shape) != (D,):
         return f"bias.shape {tuple(bias.shape)} != {(D,)}"
+    return _size_reason(B, L, D, x.stride(1), x.stride(2), x.element_size())
+
+
+def _size_reason(B: int, L: int, D: int, sxl: int, sxd: int, esz: int) -> str | None:
+    """The kernels' grid limits (conv.hip conv_args_status) and 32-bit per-row addressing
+    (conv_layout_status), repeated here so that supports() makes no library call."""
     if B > 65535:
         return f"batch {B} above 65535"
+    if -(-L // _SEG) > 65535:
+        return f"L={L} needs more than 65535 segments of {_SEG} steps"
+    if ((L + 8) * sxl + (D + 8) * sxd) * esz >= 1 << 32 or (L + 8) * D * esz >= 1 << 32:
+        return f"one batch row (L={L}, D={D}, strides {sxl}, {sxd}) exceeds the kernels' 32-bit row addressing"
     return None
 
 

@@ -44,6 +44,7 @@ def supports(lam: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> str
 def forward(lam: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> torch.Tensor:
     """Forward recurrence on the lane layout; returns the states ``[M, L, N]``."""
     lib = _lib.load()
+    _lib.sync_deterministic()
     M, L, N = v.shape
     for name, t in (("lam", lam), ("v", v), ("x0", x0)):
         _lib.require(t, name, (v.dtype,), v.device)
@@ -66,6 +67,7 @@ def backward(
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Adjoint sweep, returning ``(glam, gv, gx0)`` (gx0 empty when x0 is None)."""
     lib = _lib.load()
+    _lib.sync_deterministic()
     M, L, N = out.shape
     for name, t in (("g", g), ("lam", lam), ("out", out), ("x0", x0)):
         _lib.require(t, name, (out.dtype,), out.device)

@@ -57,6 +57,7 @@ def saved_floats(B: int, L: int, N: int) -> int:
 
 def _forward(u, W_re, W_im, lam, C_re, C_im, x0, train: bool):
     lib = _lib.load()
+    _lib.sync_deterministic()
     dev = u.device
     for name, t in (("u", u), ("W_re", W_re), ("W_im", W_im), ("C_re", C_re), ("C_im", C_im)):
         _lib.require(t, name, (torch.float32,), dev)
@@ -128,6 +129,7 @@ def _scan_bwd_op(
     W_im: torch.Tensor, lam: torch.Tensor, C_re: torch.Tensor, C_im: torch.Tensor, x0: torch.Tensor | None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     lib = _lib.load()
+    _lib.sync_deterministic()
     gy, g_xlast, saved, u, W_re, W_im, lam, C_re, C_im = _dense(gy, g_xlast, saved, u, W_re, W_im, lam, C_re, C_im)
     dev = u.device
     for name, t in (("gy", gy), ("saved", saved), ("u", u), ("W_re", W_re), ("W_im", W_im), ("C_re", C_re),

@@ -34,6 +34,7 @@ def supports(lam: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> str
 
 def forward(lam: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> torch.Tensor:
     lib = _lib.load()
+    _lib.sync_deterministic()
     M, L, N = v.shape
     for name, t in (("lam", lam), ("v", v), ("x0", x0)):
         _lib.require(t, name, (torch.float32,), v.device)
@@ -53,6 +54,7 @@ def backward(
     g: torch.Tensor, lam: torch.Tensor, out: torch.Tensor, x0: torch.Tensor | None
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     lib = _lib.load()
+    _lib.sync_deterministic()
     M, L, N = out.shape
     for name, t in (("g", g), ("lam", lam), ("out", out), ("x0", x0)):
         _lib.require(t, name, (torch.float32,), out.device)
