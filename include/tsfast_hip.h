@@ -13,6 +13,13 @@
  *   - the return value is a status: TSF_OK (0) on success, a negative TSF_ERR_* code otherwise;
  *     tsfast_hip_status_string() names it (for TSF_ERR_HIP, with the HIP runtime's message).
  *
+ * The single-pass look-back scans (diag, selective, all-pole with na <= 4, linear recurrence with
+ * n <= 4, G-block, projected) start their workspace with a 256-byte header: the tile counter in
+ * bytes 0..3 and, in bytes 64..67, a give-up flag (int32) that a look-back sets to 1 when it waited
+ * about a second without progress and gave up, its lanes then holding NaN (a GPU kept busy by
+ * other work). Each call clears the header on its stream before the scan, so after the call the
+ * flag tells a give-up apart from NaN that came with the inputs.
+ *
  * Complex tensors are interleaved (re, im) float pairs, i.e. torch.view_as_real layout.
  * bf16 tensors are raw 16-bit bfloat16 words (torch.bfloat16 storage).
  */

@@ -116,3 +116,19 @@ def test_compile_fullgraph_reference_path():
 
     f(lam, v).backward()
     assert v.grad is not None
+
+
+def test_lookback_give_up_check(monkeypatch):
+    """TSFAST_HIP_CHECK_LOOKBACK's check reads the workspace's give-up flag (byte offset 64, set by
+    a look-back that gave up waiting) and raises instead of letting its NaN pass as a result."""
+    from tsfast_amd import _lib
+
+    ws = torch.zeros(256, dtype=torch.uint8)
+    monkeypatch.setattr(_lib, "_CHECK_LOOKBACK", True)
+    _lib.check_lookback(ws, "scan")  # flag clear: no error
+    ws[_lib.LOOKBACK_ERR_OFFSET] = 1
+    assert _lib.lookback_gave_up(ws)
+    with pytest.raises(RuntimeError, match="gave up"):
+        _lib.check_lookback(ws, "scan")
+    monkeypatch.setattr(_lib, "_CHECK_LOOKBACK", False)
+    _lib.check_lookback(ws, "scan")  # debug mode off: never reads the flag

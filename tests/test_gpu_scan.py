@@ -153,3 +153,24 @@ def test_tbptt_chunked_equals_unchunked(gpu):
     want = O.diag_forward(_np(lam), _np(v), None)
     assert O.rel_err(_np(full), want) < TOL
     assert O.rel_err(_np(chunked), want) < TOL
+
+
+def test_lookback_give_up_flag_cleared_and_unset(gpu):
+    """Every scan's reset clears the workspace's give-up flag, and a scan whose look-backs all
+    complete leaves it clear (outputs checked against the oracle)."""
+    from tsfast_amd import _lib
+
+    lib = _lib.load()
+    lam, v, x0, _ = _make_diag((8, 5000, 64), (64,), torch.float32, seed=31)
+    lam_l, v_l, _ = _lanes(lam, v, None)
+    M, L, N = v.shape
+    nbytes = lib.tsfast_hip_diag_workspace_bytes(M, L, N, 0)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+    ws[_lib.LOOKBACK_ERR_OFFSET] = 1  # stale flag from an earlier (imagined) give-up
+    out = torch.empty_like(v_l, device=gpu)
+    lam_d, v_d = lam_l.to(gpu), v_l.to(gpu)
+    _lib.check(lib.tsfast_hip_diag_fwd(M, L, N, 0, _lib.ptr(lam_d), _lib.ptr(v_d), None, _lib.ptr(out), _lib.ptr(ws),
+                                       nbytes, _lib.stream_of(v_d)), "tsfast_hip_diag_fwd")
+    torch.cuda.synchronize()
+    assert not _lib.lookback_gave_up(ws)
+    assert O.rel_err(_np(out), O.diag_forward(_np(lam_l), _np(v_l))) < TOL

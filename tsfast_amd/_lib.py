@@ -107,6 +107,27 @@ def sync_deterministic() -> None:
         _det_mode = want
 
 
+_CHECK_LOOKBACK = os.environ.get("TSFAST_HIP_CHECK_LOOKBACK", "0") not in ("", "0")
+LOOKBACK_ERR_OFFSET = 64  # byte offset of the give-up flag in a look-back workspace (lookback.h kErrWord)
+
+
+def lookback_gave_up(ws: torch.Tensor) -> bool:
+    """Whether a look-back in the scan that used workspace ``ws`` gave up waiting (its lanes then
+    hold NaN). Synchronises with the device."""
+    return bool(ws[LOOKBACK_ERR_OFFSET : LOOKBACK_ERR_OFFSET + 4].view(torch.int32).item())
+
+
+def check_lookback(ws: torch.Tensor, what: str) -> None:
+    """With TSFAST_HIP_CHECK_LOOKBACK=1 in the environment (a debug mode: it synchronises after
+    every look-back scan), raise if the scan's look-back gave up rather than let its NaN pass as a
+    numerical result. Otherwise a no-op."""
+    if _CHECK_LOOKBACK and lookback_gave_up(ws):
+        raise RuntimeError(
+            f"{what}: a look-back wait gave up without progress (the GPU was probably shared with "
+            "work that kept the scan's workgroups from running); its outputs hold NaN"
+        )
+
+
 def available() -> bool:
     """True when the library file exists (does not load it)."""
     return LIB_PATH.exists()

@@ -396,7 +396,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
     for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && y0 && live && k == 0) ? (double)y0[lane * NA + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       ap_look_back<NA>(S, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
-                       k, lid, s_lds, s_flag, s_pend, &s_any);
+                       k, lid, s_lds, s_flag, s_pend, &s_any, counter);
     if (k == 0 && live) {
       if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) {
         double ms[NA][NA], o[NA];
@@ -510,7 +510,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     for (int q = 0; q < NA; ++q) R[q] = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
       ap_look_back<NA>(R, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K,
-                       k, lid, s_lds, s_flag, s_pend, &s_any);
+                       k, lid, s_lds, s_flag, s_pend, &s_any, counter);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) {
         double ms[NA][NA], o[NA];

@@ -223,7 +223,7 @@ template <int NA, int NV = 1>
 TSF_DEV void ap_look_back(double (&S)[NA * NV], const double* __restrict__ agg, const double* __restrict__ inc,
                           const double* __restrict__ MsLane, bool need, int64_t pos0, int64_t dj, int64_t nsuper,
                           int64_t lanes, int64_t lane, int K, int k, int lid, LdsTile* lds, int (*flag)[64],
-                          int* pend_s, int* any_s) {
+                          int* pend_s, int* any_s, unsigned* __restrict__ lb_counter) {
   constexpr int V = NA * NV;
   uint32_t spins = 0;
   if (k == 0) {
@@ -282,6 +282,7 @@ TSF_DEV void ap_look_back(double (&S)[NA * NV], const double* __restrict__ agg, 
         } else if (++spins > kSpinMax) {
 #pragma unroll
           for (int q = 0; q < V; ++q) S[q] = quiet_nan<double>();
+          lb_gave_up(lb_counter);
         } else {
           pending = true;
         }

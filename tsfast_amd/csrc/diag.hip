@@ -75,7 +75,7 @@ constexpr int kWindow = kMaxWaves;  // look-back slots examined per round
 template <typename W>
 TSF_DEV W look_back(const Map<W>* __restrict__ agg, const W* __restrict__ inc, bool need, int64_t pos0, int64_t dj,
                     int64_t nsuper, int64_t lanes, int64_t lane, int K, int k, int lid, Map<W> (*win)[64],
-                    int (*flag)[64], int64_t* pos_s, int* any_s) {
+                    int (*flag)[64], int64_t* pos_s, int* any_s, unsigned* __restrict__ lb_counter) {
   Map<W> acc = {Num<W>::one(), Num<W>::zero()};  // composition of the aggregates walked over
   W result = Num<W>::zero();
   uint32_t spins = 0;
@@ -143,6 +143,7 @@ TSF_DEV W look_back(const Map<W>* __restrict__ agg, const W* __restrict__ inc, b
         }
         if (p >= 0 && w == 0 && ++spins > kSpinMax) {
           result = quiet_nan<W>();
+          lb_gave_up(lb_counter);
           p = -1;
         }
         pending = p >= 0;
@@ -232,7 +233,7 @@ __global__ void __launch_bounds__(1024) diag_fwd(const T* __restrict__ lam, cons
     W s = x0 && live && k == 0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
     if (sc > 0)  // uniform over the workgroup
       s = look_back(agg, inc, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
-                    s_pos, &s_any);
+                    s_pos, &s_any, counter);
     if (k == 0 && live) {
       if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
       for (int j = 0; j < K; ++j) {
@@ -362,7 +363,7 @@ __global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, cons
     W R = Num<W>::zero();  // G entering the super-chunk from the right
     if (sc + 1 < nsuper)   // uniform over the workgroup
       R = look_back(agg, inc, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid, s_win, s_flag, s_pos,
-                    &s_any);
+                    &s_any, counter);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
       for (int j = K - 1; j >= 0; --j) {
@@ -510,7 +511,7 @@ __global__ void __launch_bounds__(1024) sel_fwd(const float* __restrict__ a, con
     double s = x0 && live && k == 0 ? (double)x0[lane] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       s = look_back(agg, inc, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
-                    s_pos, &s_any);
+                    s_pos, &s_any, counter);
     if (k == 0 && live) {
       if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
       for (int j = 0; j < K; ++j) {
@@ -616,7 +617,7 @@ __global__ void __launch_bounds__(1024) sel_bwd(const float* __restrict__ a, con
     double R = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
       R = look_back(agg, inc, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
-                    s_pos, &s_any);
+                    s_pos, &s_any, counter);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
       for (int j = K - 1; j >= 0; --j) {

@@ -188,7 +188,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
     for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[lane * NA + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       ap_look_back<NA>(S, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
-                       k, lid, s_lds, s_flag, s_pend, &s_any);
+                       k, lid, s_lds, s_flag, s_pend, &s_any, counter);
     if (k == 0 && live) {
       if (saved) {
 #pragma unroll
@@ -356,7 +356,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     for (int q = 0; q < V; ++q) Rv[q] = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
       ap_look_back<NA, 2>(Rv, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane,
-                          K, k, lid, s_lds, s_flag, s_pend, &s_any);
+                          K, k, lid, s_lds, s_flag, s_pend, &s_any, counter);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) {
         double ms[NA][NA], o[V];

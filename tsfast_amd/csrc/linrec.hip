@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     for (int q = 0; q < NS; ++q) St[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[lane * NS + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       ap_look_back<NS>(St, agg, inc, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
-                       k, lid, s_lds, s_flag, s_pend, &s_any);
+                       k, lid, s_lds, s_flag, s_pend, &s_any, counter);
     if (k == 0 && live) {
       if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) {
         double ms[NS][NS], o[NS];
@@ -339,7 +339,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     for (int q = 0; q < NS; ++q) R[q] = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
       ap_look_back<NS>(R, agg, inc, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid,
-                       s_lds, s_flag, s_pend, &s_any);
+                       s_lds, s_flag, s_pend, &s_any, counter);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) {
         double ms[NS][NS], o[NS];

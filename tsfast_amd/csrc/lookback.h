@@ -58,6 +58,15 @@ TSF_DEV bool lb_pub_agg(int64_t j, int spacing) { return spacing == 0 ? j > 0 : 
 TSF_DEV bool lb_pub_inc(int64_t j, int spacing) { return spacing == 0 || j % spacing == 0; }
 constexpr int kAnchorSpacing = 8;  // deterministic-mode spacing of the look-backs whose window moves
 
+// Give-up flag: the word kErrWord words after the tile counter (inside the kCounterBytes header
+// of the workspace, byte offset 64) is set to 1 by any look-back that gives up after kSpinMax
+// rounds without progress, whose lanes then carry NaN; lookback_reset clears it before every
+// scan, so after a scan it tells a give-up apart from NaNs that came with the inputs.
+constexpr int kErrWord = 16;
+TSF_DEV void lb_gave_up(unsigned* counter) {
+  __hip_atomic_store(counter + kErrWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 TSF_DEV unsigned take_tile(unsigned* counter) {
   return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -68,7 +77,10 @@ __global__ void __launch_bounds__(256) lookback_reset(uint64_t* __restrict__ wor
                                                       unsigned* __restrict__ counter) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) words[i] = kUnset;
-  if (blockIdx.x == 0 && threadIdx.x == 0) *counter = 0u;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    counter[0] = 0u;
+    counter[kErrWord] = 0u;
+  }
 }
 
 

@@ -93,7 +93,7 @@ TSF_DEV void block_scan(float2 (&x)[4], float2 lm, float2 lm4, float2 lm8, int l
 // without waiting, and every chunk waited on belongs to a tile taken earlier by a running
 // workgroup; a lane that makes no progress for kSpinMax rounds gives up with NaN.
 TSF_DEV double2 walk(const double2* __restrict__ agg, const double2* __restrict__ inc, int64_t cstride, int64_t widx,
-                     int c, int dir, int nc, double2 P) {
+                     int c, int dir, int nc, double2 P, unsigned* __restrict__ lb_counter) {
   double2 accP = Num<double2>::one(), acce = Num<double2>::zero();
   int r = c + dir;
   uint32_t spins = 0;
@@ -118,7 +118,10 @@ TSF_DEV double2 walk(const double2* __restrict__ agg, const double2* __restrict_
       acce = Num<double2>::fma(accP, va[i], acce);
       accP = Num<double2>::mul(accP, P);
     }
-    if (i == 0 && ++spins > kSpinMax) return quiet_nan<double2>();
+    if (i == 0 && ++spins > kSpinMax) {
+      lb_gave_up(lb_counter);
+      return quiet_nan<double2>();
+    }
     r += dir * i;
   }
 }
@@ -231,7 +234,7 @@ __global__ void __launch_bounds__(256, 1)
       cin = (x0 != nullptr && s_lb < N) ? up2(x0[(int64_t)b * N + s_lb]) : Num<double2>::zero();
     } else {
       if (lb_pub_agg(c, lb_spacing) && c + 1 < nchunks) put(agg + (int64_t)c * cstride + widx, agg_v);
-      cin = walk(agg, inc, cstride, widx, c, -1, nchunks, P64);
+      cin = walk(agg, inc, cstride, widx, c, -1, nchunks, P64, counter);
     }
     if (lb_pub_inc(c, lb_spacing) && c + 1 < nchunks)
       put(inc + (int64_t)c * cstride + widx, Num<double2>::fma(P64, cin, agg_v));
@@ -507,7 +510,7 @@ __global__ void __launch_bounds__(256, 1)
     double2 R = Num<double2>::zero();  // G at the first step of the next chunk
     if (c + 1 < nsub) {
       if (lb_pub_agg(cr, lb_spacing) && c > 0) put(agg + (int64_t)c * cstride + widx, agg_v);
-      R = walk(agg, inc, cstride, widx, c, +1, nsub, cP32);
+      R = walk(agg, inc, cstride, widx, c, +1, nsub, cP32, counter);
     }
     const double2 first = Num<double2>::fma(cP32, R, agg_v);  // G at this chunk's first step
     if (lb_pub_inc(cr, lb_spacing) && c > 0) put(inc + (int64_t)c * cstride + widx, first);

@@ -21,6 +21,7 @@ import torch
 from .. import _lib
 
 _MAX_NA = 16
+_LB_NA = 4  # highest order on the single-pass look-back path (allpole_core.h kLbNA)
 
 
 def supports(a: torch.Tensor, w: torch.Tensor, y0: torch.Tensor | None) -> str | None:
@@ -68,6 +69,8 @@ def _allpole_op(a: torch.Tensor, w: torch.Tensor, y0: torch.Tensor | None) -> to
         ),
         "tsfast_hip_allpole_fwd",
     )
+    if na <= _LB_NA:  # the single-pass look-back path (higher orders run two passes, no look-back)
+        _lib.check_lookback(ws, "tsfast_hip_allpole_fwd")
     return y
 
 
@@ -100,6 +103,8 @@ def _allpole_bwd_op(
         ),
         "tsfast_hip_allpole_bwd",
     )
+    if na <= _LB_NA:  # the single-pass look-back path (higher orders run two passes, no look-back)
+        _lib.check_lookback(ws, "tsfast_hip_allpole_bwd")
     return ga, gw, (gy0 if gy0 is not None else a.new_empty(0))
 
 

@@ -101,6 +101,7 @@ def _gblock_op(
         ),
         "tsfast_hip_gblock_fwd",
     )
+    _lib.check_lookback(ws, "tsfast_hip_gblock_fwd")
     return y, x_last, saved
 
 
@@ -141,6 +142,7 @@ def _gblock_bwd_op(
         ),
         "tsfast_hip_gblock_bwd",
     )
+    _lib.check_lookback(ws, "tsfast_hip_gblock_bwd")
     return gu, gu_tail, gb, ga, gx0
 
 

@@ -74,6 +74,8 @@ def _linrec_op(A: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> tor
         ),
         "tsfast_hip_linrec_fwd",
     )
+    if n <= 4:  # the single-pass look-back path (n = 5..8 run two passes, no look-back)
+        _lib.check_lookback(ws, "tsfast_hip_linrec_fwd")
     return x
 
 
@@ -104,6 +106,8 @@ def _linrec_bwd_op(
         ),
         "tsfast_hip_linrec_bwd",
     )
+    if n <= 4:  # the single-pass look-back path (n = 5..8 run two passes, no look-back)
+        _lib.check_lookback(ws, "tsfast_hip_linrec_bwd")
     return gA, gv, (gx0 if gx0 is not None else A.new_empty(0))
 
 

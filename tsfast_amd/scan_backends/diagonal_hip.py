@@ -59,6 +59,7 @@ def forward(lam: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> torc
         ),
         "tsfast_hip_diag_fwd",
     )
+    _lib.check_lookback(ws, "tsfast_hip_diag_fwd")
     return out
 
 
@@ -84,4 +85,5 @@ def backward(
         ),
         "tsfast_hip_diag_bwd",
     )
+    _lib.check_lookback(ws, "tsfast_hip_diag_bwd")
     return glam, gv, (gx0 if gx0 is not None else lam.new_empty(0))

@@ -79,6 +79,7 @@ def _forward(u, W_re, W_im, lam, C_re, C_im, x0, train: bool):
         ),
         "tsfast_hip_projscan_fwd",
     )
+    _lib.check_lookback(ws, "tsfast_hip_projscan_fwd")
     return y, x_last, saved
 
 
@@ -157,6 +158,7 @@ def _scan_bwd_op(
         ),
         "tsfast_hip_projscan_bwd",
     )
+    _lib.check_lookback(ws, "tsfast_hip_projscan_bwd")
     return g_u, g_W_re, g_W_im, g_lam, g_C_re, g_C_im, (g_x0 if g_x0 is not None else lam.new_empty(0))
 
 

@@ -47,6 +47,7 @@ def forward(lam: torch.Tensor, v: torch.Tensor, x0: torch.Tensor | None) -> torc
         ),
         "tsfast_hip_sel_fwd",
     )
+    _lib.check_lookback(ws, "tsfast_hip_sel_fwd")
     return out
 
 
@@ -70,4 +71,5 @@ def backward(
         ),
         "tsfast_hip_sel_bwd",
     )
+    _lib.check_lookback(ws, "tsfast_hip_sel_bwd")
     return glam, gv, (gx0 if gx0 is not None else lam.new_empty(0))
