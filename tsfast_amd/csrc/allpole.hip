@@ -328,7 +328,7 @@ __global__ void __launch_bounds__(kTile) allpole_bwd_apply(const float* __restri
 }
 
 template <int NA>
-__global__ void __launch_bounds__(64 * kLbWaves) allpole_fwd_lb(
+__global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per_eu(4))) allpole_fwd_lb(
     const float* __restrict__ a, const float* __restrict__ w, const float* __restrict__ y0, float* __restrict__ y,
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
     unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, int lb_spacing) {

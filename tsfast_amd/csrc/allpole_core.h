@@ -131,12 +131,14 @@ TSF_DEV void matvec_add(double (&out)[NA], const double (&m)[NA][NA], const doub
   for (int r = 0; r < NA; ++r) out[r] = t[r];
 }
 
-// y = C x for the companion matrix C of a (row 0 = -a, ones on the subdiagonal), in fp64.
+// y = C x for the companion matrix C of a (row 0 = -a, ones on the subdiagonal), in fp64. The sum
+// starts from the oldest entry, so only its last FMA waits on the previous step's new entry x[0]:
+// a chain of steps costs one FMA latency per step.
 template <int NA>
 TSF_DEV void companion_apply(double (&x)[NA], const double (&a)[NA]) {
   double y0 = 0.0;
 #pragma unroll
-  for (int c = 0; c < NA; ++c) y0 = fma(-a[c], x[c], y0);
+  for (int c = NA - 1; c >= 0; --c) y0 = fma(-a[c], x[c], y0);
 #pragma unroll
   for (int r = NA - 1; r > 0; --r) x[r] = x[r - 1];
   x[0] = y0;

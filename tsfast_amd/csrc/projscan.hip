@@ -18,11 +18,12 @@
 // An MFMA result holds steps 4g .. 4g+3 of column j in lane (g, j) (g = lane / 16, j = lane % 16),
 // so the recurrence runs serially over a lane's 4 steps, then across the 4 lane groups (two
 // shift-and-combine stages through ds_bpermute), then from block to block.
-// Chunks are chained by decoupled look-back with anchored publication (lookback.h): every eighth
-// chunk of a row in scan order publishes the state leaving it (inc), the others their end state
-// from a zero start (agg); a tile walks back over the aggs to the nearest anchor's inc, so the
-// state entering each chunk is composed the same way on every run. Carries are fp64; the
-// chunk-entering states are saved for the backward pass.
+// Chunks are chained by decoupled look-back (lookback.h): every chunk publishes its end state from
+// a zero start (agg) and the state leaving it (inc), and a tile walks back over the aggs to the
+// nearest published inc. In deterministic mode (tsfast_hip_set_deterministic) only every eighth
+// chunk of a row in scan order publishes an inc (anchored publication), so the state entering
+// each chunk is composed the same way on every run. Carries are fp64; the chunk-entering states
+// are saved for the backward pass.
 #include <algorithm>
 
 #include "common.h"
