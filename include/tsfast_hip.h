@@ -35,7 +35,7 @@ extern "C" {
 #define TSF_OK 0
 #define TSF_ERR_ARG (-1)         /* a size or pointer argument is invalid */
 #define TSF_ERR_WORKSPACE (-2)   /* workspace missing or smaller than the *_workspace_bytes query */
-#define TSF_ERR_UNSUPPORTED (-3) /* shape outside what the kernels are built for (e.g. N > 64) */
+#define TSF_ERR_UNSUPPORTED (-3) /* shape outside what the kernels are built for (e.g. H > 32 in the projected scan) */
 #define TSF_ERR_HIP (-4)         /* a HIP runtime call or kernel launch failed */
 #define TSF_ERR_SCRATCH (-5)     /* more scratch than a no-allocation entry point holds */
 

@@ -7,12 +7,13 @@
 // and S5.forward (architectures/s5.py:180-198) run. The reference materialises v and x
 // ([B, L, N] complex each); this pass reads u and writes y, and neither v nor x touches HBM.
 //
-// Work layout. A tile is one row b by a chunk of kChunk = 64 steps (4 blocks of 16) by all N
-// states; a workgroup has one wave per 64 states (N <= 256: at most 4 waves) and takes tiles in
-// scan order (chunk-major) from a counter. Both projections run on the fp32 matrix cores
-// (v_mfma_f32_16x16x4f32) with time as the row index of a 16 x 16 block:
+// Work layout. A tile is one row b by a chunk of kChunk = 32 steps (2 blocks of 16) by all N
+// states; a workgroup has one wave per 32 states (N <= 256: at most 8 waves, two per SIMD, so
+// each wave has 256 registers) and takes tiles in scan order (chunk-major) from a counter. Both
+// projections run on the fp32 matrix cores (v_mfma_f32_16x16x4f32) with time as the row index of
+// a 16 x 16 block:
 //   in-proj   V[t][s] = sum_h u[t][h] W[s][h]     A = the u block, B = W^T held in registers;
-//   read-out  Y[t][o] = sum_rho X[t][rho] Ct[rho][o] over the wave's 128 interleaved real state
+//   read-out  Y[t][o] = sum_rho X[t][rho] Ct[rho][o] over the wave's 64 interleaved real state
 //             rows rho (re, im; the im rows carry -C_im), A = the X block re-read through LDS in
 //             operand layout, B = Ct held in registers; the waves' partial Y are added in LDS.
 // An MFMA result holds steps 4g .. 4g+3 of column j in lane (g, j) (g = lane / 16, j = lane % 16),
@@ -38,11 +39,16 @@ namespace {
 using f4 = __attribute__((__vector_size__(4 * sizeof(float)))) float;
 
 constexpr int kBlk = 16;                  // steps per MFMA block
-constexpr int kBlocks = 4;                // blocks per chunk
-constexpr int kChunk = kBlk * kBlocks;    // steps per tile
-constexpr int kSlots = 4;                 // 16-state column blocks per wave
-constexpr int kMaxWaves = 4;              // N <= 256
-constexpr int kXtStride = 132;            // floats per row of a wave's transposed block in LDS
+constexpr int kBlocks = 2;                // blocks per chunk
+constexpr int kChunk = kBlk * kBlocks;    // steps per forward tile
+constexpr int kBwdBlocks = 2;             // blocks per backward tile
+constexpr int kSub = kBlk * kBwdBlocks;   // steps per backward tile (the saved-state interval)
+static_assert(kChunk % kSub == 0, "forward tiles cover whole saved-state intervals");
+constexpr int kSlots = 2;                 // 16-state column blocks per wave
+constexpr int kWaveStates = 16 * kSlots;  // states per wave
+constexpr int kRho = 2 * kWaveStates;     // interleaved real rows (re, im) of a wave's states
+constexpr int kMaxWaves = 8;              // N <= 256
+constexpr int kXtStride = kRho + 4;       // floats per row of a wave's transposed block in LDS
 constexpr uint32_t kOob = 0xFFFFFFF0u;    // buffer offset past every resource: loads return 0
 
 TSF_DEV f4 mfma(float a, float b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
@@ -57,11 +63,11 @@ TSF_DEV float2 from_group_below(float2 v, int lane, int d) {
   const float2 r = from_lane(v, lane - 16 * d);
   return lane >= 16 * d ? r : make_float2(0.0f, 0.0f);
 }
-TSF_DEV float2 pick(const float2 (&v)[4], int i) {
+template <int K>
+TSF_DEV float2 pick(const float2 (&v)[K], int i) {
   float2 r = v[0];
-  r = i == 1 ? v[1] : r;
-  r = i == 2 ? v[2] : r;
-  r = i == 3 ? v[3] : r;
+#pragma unroll
+  for (int k = 1; k < K; ++k) r = i == k ? v[k] : r;
   return r;
 }
 TSF_DEV double2 up2(float2 v) { return make_double2((double)v.x, (double)v.y); }
@@ -87,22 +93,23 @@ TSF_DEV void block_scan(float2 (&x)[4], float2 lm, float2 lm4, float2 lm8, int l
 }
 
 // Carry of chunk c for this lane's state, looked up over the chunks before it in scan order
-// (c - 1, c - 2, ... for dir = -1; c + 1, c + 2, ... for dir = +1; nc chunks), four at a time. A
+// (c - 1, c - 2, ... for dir = -1; c + 1, c + 2, ... for dir = +1; nc chunks), W at a time. A
 // published inc (the carry leaving that chunk) ends the walk; a published agg (that chunk's carry
 // from a zero start; every such chunk has the multiplier P) is composed and the walk moves on; an
 // unpublished word ends the round. The walk ends: the first chunk in scan order publishes its inc
 // without waiting, and every chunk waited on belongs to a tile taken earlier by a running
 // workgroup; a lane that makes no progress for kSpinMax rounds gives up with NaN.
+template <int W>
 TSF_DEV double2 walk(const double2* __restrict__ agg, const double2* __restrict__ inc, int64_t cstride, int64_t widx,
                      int c, int dir, int nc, double2 P, unsigned* __restrict__ lb_counter) {
   double2 accP = Num<double2>::one(), acce = Num<double2>::zero();
   int r = c + dir;
   uint32_t spins = 0;
   for (;;) {
-    double2 vi[4], va[4];
-    bool hi[4], ha[4];
+    double2 vi[W], va[W];
+    bool hi[W], ha[W];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < W; ++i) {
       const int rr = r + dir * i;
       hi[i] = ha[i] = false;
       if (rr >= 0 && rr < nc) {
@@ -111,7 +118,7 @@ TSF_DEV double2 walk(const double2* __restrict__ agg, const double2* __restrict_
       }
     }
     int i = 0;
-    for (; i < 4; ++i) {
+    for (; i < W; ++i) {
       const int rr = r + dir * i;
       if (rr < 0 || rr >= nc) break;
       if (hi[i]) return Num<double2>::fma(accP, vi[i], acce);
@@ -127,26 +134,34 @@ TSF_DEV double2 walk(const double2* __restrict__ agg, const double2* __restrict_
   }
 }
 
+// Dynamic LDS of the forward: per wave a transposed X block [kBlk][kXtStride], then the waves'
+// partial Y blocks, double-buffered [2][NW][kBlk][16 OB].
+template <int OB>
+constexpr size_t fwd_lds_bytes(int nw) {
+  return sizeof(float) * ((size_t)nw * kBlk * kXtStride + 2 * (size_t)nw * kBlk * 16 * OB);
+}
+
 template <int KS, int OB>
-__global__ void __launch_bounds__(256, 1)
+__global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(2)))
     projscan_fwd(const float* __restrict__ u, const float* __restrict__ w_re, const float* __restrict__ w_im,
                  const float2* __restrict__ lam, const float* __restrict__ c_re, const float* __restrict__ c_im,
                  const float2* __restrict__ x0, float* __restrict__ y, float2* __restrict__ x_last,
                  float2* __restrict__ saved, double2* __restrict__ agg, double2* __restrict__ inc,
                  unsigned* __restrict__ counter, int B, int L, int H, int N, int O, int nchunks, int nsub, int lb_spacing) {
-  __shared__ __attribute__((aligned(16))) float s_xt[kMaxWaves][kBlk][kXtStride];
-  __shared__ float s_y[2][kMaxWaves][kBlk][16 * OB];
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
   __shared__ unsigned s_tile[2];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, NW = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
-  const int64_t NS = (int64_t)NW * 64, cstride = (int64_t)B * NS, tiles = (int64_t)nchunks * B;
+  float* const s_xt = s_dyn + (size_t)w * kBlk * kXtStride;  // this wave's [kBlk][kXtStride]
+  float* const s_y = s_dyn + (size_t)NW * kBlk * kXtStride;  // [2][NW][kBlk][16 OB]
+  const int64_t NS = (int64_t)NW * kWaveStates, cstride = (int64_t)B * NS, tiles = (int64_t)nchunks * B;
   const Rsrc ru = make_rsrc(u, (uint32_t)((int64_t)B * L * H * 4));
 
   // in-proj B operands: W_p[s][h] for s = 64w + 16q + j, h = g KS + kk (p = 0 re, 1 im)
   float wB[kSlots][2][KS];
 #pragma unroll
   for (int q = 0; q < kSlots; ++q) {
-    const int s = 64 * w + 16 * q + j;
+    const int s = kWaveStates * w + 16 * q + j;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       const int h = g * KS + kk;
@@ -155,14 +170,16 @@ __global__ void __launch_bounds__(256, 1)
       wB[q][1][kk] = ok ? w_im[(int64_t)s * H + h] : 0.0f;
     }
   }
-  // read-out B operands: row rho = 32g + m is state 64w + rho/2, re (C_re) for even rho, im (-C_im) for odd
-  float cB[OB][32];
+  // read-out B operands: row rho = (kRho / 4) g + m is state kWaveStates w + rho/2, re (C_re) for
+  // even rho, im (-C_im) for odd
+  constexpr int kM = kRho / 4;  // MFMAs per 16-output block
+  float cB[OB][kM];
 #pragma unroll
   for (int ob = 0; ob < OB; ++ob) {
     const int o = 16 * ob + j;
 #pragma unroll
-    for (int m = 0; m < 32; ++m) {
-      const int rho = 32 * g + m, s = 64 * w + (rho >> 1);
+    for (int m = 0; m < kM; ++m) {
+      const int rho = kM * g + m, s = kWaveStates * w + (rho >> 1);
       const bool ok = o < O && s < N;
       cB[ob][m] = !ok ? 0.0f : (rho & 1) ? -c_im[(int64_t)o * N + s] : c_re[(int64_t)o * N + s];
     }
@@ -171,7 +188,7 @@ __global__ void __launch_bounds__(256, 1)
   float2 lm[kSlots], lm4[kSlots], lm8[kSlots], lmg[kSlots], lm16[kSlots];
 #pragma unroll
   for (int q = 0; q < kSlots; ++q) {
-    const int s = 64 * w + 16 * q + j;
+    const int s = kWaveStates * w + 16 * q + j;
     const float2 a = s < N ? lam[s] : make_float2(0.0f, 0.0f);
     lm[q] = a;
     lm4[q] = ipow(a, 4);
@@ -179,10 +196,12 @@ __global__ void __launch_bounds__(256, 1)
     lmg[q] = ipow(a, 4 * g + 1);
     lm16[q] = ipow(a, 16);
   }
-  // the lane's look-back state 64w + lane (slot g of column j)
-  const int s_lb = 64 * w + lane;
-  const double2 a_lb = s_lb < N ? up2(lam[s_lb]) : Num<double2>::zero();
-  const double2 P16 = ipow(a_lb, 16), P64 = ipow(a_lb, 64);
+  // the lane's look-back state kWaveStates w + lane (slot g of column j); lanes past the wave's
+  // states take no part in the look-back
+  const bool lb_lane = lane < kWaveStates;
+  const int s_lb = kWaveStates * w + lane;
+  const double2 a_lb = lb_lane && s_lb < N ? up2(lam[s_lb]) : Num<double2>::zero();
+  const double2 P16 = ipow(a_lb, 16), Pc = ipow(a_lb, kChunk);
 
   if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
   __syncthreads();
@@ -225,20 +244,22 @@ __global__ void __launch_bounds__(256, 1)
       }
     }
 
-    // look-back on lane (g, j) for state 64w + lane (slot g)
+    // look-back on lane (g, j) for state kWaveStates w + lane (slot g)
     double2 agg_v = Num<double2>::zero();
 #pragma unroll
     for (int k = 0; k < kBlocks; ++k) agg_v = Num<double2>::fma(P16, agg_v, up2(pick(e[k], g)));
     const int64_t widx = (int64_t)b * NS + s_lb;
-    double2 cin;
-    if (c == 0) {
-      cin = (x0 != nullptr && s_lb < N) ? up2(x0[(int64_t)b * N + s_lb]) : Num<double2>::zero();
-    } else {
-      if (lb_pub_agg(c, lb_spacing) && c + 1 < nchunks) put(agg + (int64_t)c * cstride + widx, agg_v);
-      cin = walk(agg, inc, cstride, widx, c, -1, nchunks, P64, counter);
+    double2 cin = Num<double2>::zero();
+    if (lb_lane) {
+      if (c == 0) {
+        if (x0 != nullptr && s_lb < N) cin = up2(x0[(int64_t)b * N + s_lb]);
+      } else {
+        if (lb_pub_agg(c, lb_spacing) && c + 1 < nchunks) put(agg + (int64_t)c * cstride + widx, agg_v);
+        cin = walk<2>(agg, inc, cstride, widx, c, -1, nchunks, Pc, counter);
+      }
+      if (lb_pub_inc(c, lb_spacing) && c + 1 < nchunks)
+        put(inc + (int64_t)c * cstride + widx, Num<double2>::fma(Pc, cin, agg_v));
     }
-    if (lb_pub_inc(c, lb_spacing) && c + 1 < nchunks)
-      put(inc + (int64_t)c * cstride + widx, Num<double2>::fma(P64, cin, agg_v));
     float2 carry[kSlots];
     {
       const float2 cf = down2(cin);
@@ -250,8 +271,8 @@ __global__ void __launch_bounds__(256, 1)
 #pragma unroll
     for (int k = 0; k < kBlocks; ++k) {
       // the state entering every half chunk is saved for the backward pass (its tiles are 32 steps)
-      const int sub = 2 * c + k / 2;
-      if (saved != nullptr && (k & 1) == 0 && sub < nsub && s_lb < N)
+      const int tk = t0 + kBlk * k, sub = tk / kSub;
+      if (saved != nullptr && tk % kSub == 0 && sub < nsub && lb_lane && s_lb < N)
         saved[((int64_t)b * nsub + sub) * N + s_lb] = pick(carry, g);
 #pragma unroll
       for (int q = 0; q < kSlots; ++q) {
@@ -267,7 +288,7 @@ __global__ void __launch_bounds__(256, 1)
       if (x_last != nullptr && tl >= 0 && tl < kBlk && g == (tl >> 2)) {
 #pragma unroll
         for (int q = 0; q < kSlots; ++q) {
-          const int s = 64 * w + 16 * q + j;
+          const int s = kWaveStates * w + 16 * q + j;
           if (s < N) x_last[(int64_t)b * N + s] = pick(x[k][q], tl & 3);
         }
       }
@@ -276,11 +297,11 @@ __global__ void __launch_bounds__(256, 1)
       for (int q = 0; q < kSlots; ++q)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          *reinterpret_cast<float2*>(&s_xt[w][4 * g + r][2 * (16 * q + j)]) = x[k][q][r];
-      float xa[32];
+          *reinterpret_cast<float2*>(&s_xt[(4 * g + r) * kXtStride + 2 * (16 * q + j)]) = x[k][q][r];
+      float xa[kM];
 #pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const f4 q4 = *reinterpret_cast<const f4*>(&s_xt[w][j][32 * g + 4 * v]);
+      for (int v = 0; v < kM / 4; ++v) {
+        const f4 q4 = *reinterpret_cast<const f4*>(&s_xt[j * kXtStride + kM * g + 4 * v]);
         xa[4 * v] = q4[0];
         xa[4 * v + 1] = q4[1];
         xa[4 * v + 2] = q4[2];
@@ -290,18 +311,20 @@ __global__ void __launch_bounds__(256, 1)
 #pragma unroll
       for (int ob = 0; ob < OB; ++ob) yacc[ob] = f4_zero();
 #pragma unroll
-      for (int m = 0; m < 32; ++m)
+      for (int m = 0; m < kM; ++m)
 #pragma unroll
         for (int ob = 0; ob < OB; ++ob) yacc[ob] = mfma(xa[m], cB[ob][m], yacc[ob]);
+      constexpr int kYw = kBlk * 16 * OB;  // floats of one wave's Y block
+      float* const sy = s_y + (size_t)(k & 1) * NW * kYw;
 #pragma unroll
       for (int ob = 0; ob < OB; ++ob)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s_y[k & 1][w][4 * g + r][16 * ob + j] = yacc[ob][r];
+        for (int r = 0; r < 4; ++r) sy[w * kYw + (4 * g + r) * 16 * OB + 16 * ob + j] = yacc[ob][r];
       __syncthreads();
       for (int idx = threadIdx.x; idx < kBlk * O; idx += blockDim.x) {
         const int tt = idx / O, o = idx - tt * O;
-        float sum = s_y[k & 1][0][tt][o];
-        for (int ww = 1; ww < NW; ++ww) sum += s_y[k & 1][ww][tt][o];
+        float sum = sy[tt * 16 * OB + o];
+        for (int ww = 1; ww < NW; ++ww) sum += sy[ww * kYw + tt * 16 * OB + o];
         const int t = t0 + kBlk * k + tt;
         if (t < L) y[((int64_t)b * L + t) * O + o] = sum;
       }
@@ -322,17 +345,17 @@ __global__ void __launch_bounds__(256) projscan_copy_state(const float2* __restr
 //   grad C_re = sum_t gy_t Re(x_t)^T,  grad C_im = -sum_t gy_t Im(x_t)^T,
 //   grad lam = sum_{b,t} G_t conj(x_{t-1}),  g_x0 = conj(lam) G_0.
 // A backward tile is one row by kSub = 32 steps (2 blocks) by all states, taken from the right
-// end. Phase A: g_x by MFMA (A = the gy block, B = conj(C)^T in registers), the reverse in-block
-// scans from zero, the tile's aggregate, a look-back over the later chunks of the row, the
-// fix-up of both G blocks. Phase B, block by block from the left: x recomputed (in-proj MFMA and
-// scan from the saved state entering the tile), grad lam on the VALU, grad C (A = gy^T loaded
-// in operand layout, B = x) and grad W (A = u^T, B = G) accumulated on the matrix cores over every
-// tile the workgroup takes, and g_u (A = G transposed through LDS, B = W rows in LDS), whose
-// per-wave partial sums are added in LDS. Each workgroup finally writes its grad W / C / lam sums
-// to its slot of the partial buffer, which projscan_bwd_reduce adds in a fixed order.
-constexpr int kBwdBlocks = 2;
-constexpr int kSub = kBlk * kBwdBlocks;  // steps per backward tile (the saved-state interval)
-constexpr int kWuStride = 132;           // floats per h row of a wave's W rows in LDS
+// end (one wave per 32 states, as in the forward). Phase A: g_x by MFMA (A = the gy block, B =
+// conj(C)^T reloaded from L2 each tile), the reverse in-block scans from zero, the tile's
+// aggregate, a look-back over the later chunks of the row, the fix-up of both G blocks. Phase B,
+// block by block from the left: x recomputed (in-proj MFMA with B = W^T read from the wave's W
+// rows in LDS at each use, and the scan from the saved state entering the tile), grad lam on the
+// VALU, grad C (A = gy^T loaded in operand layout, B = x) and grad W (A = u^T, B = G) accumulated
+// on the matrix cores over every tile the workgroup takes, and g_u (A = G transposed through LDS,
+// B = W rows in LDS), whose per-wave partial sums are added in LDS. Each workgroup finally writes
+// its grad W / C / lam sums to its slot of the partial buffer, which projscan_bwd_reduce adds in a
+// fixed order.
+constexpr int kWuStride = kRho + 4;      // floats per h row of a wave's W rows in LDS
 
 // conj(a) * x and conj(a) * x + b
 TSF_DEV float2 cmul_c(float2 a, float2 x) { return make_float2(fmaf(a.x, x.x, a.y * x.y), fmaf(a.x, x.y, -(a.y * x.x))); }
@@ -363,30 +386,15 @@ TSF_DEV void block_scan_rev(float2 (&x)[4], float2 lm, float2 lm4, float2 lm8, i
   }
 }
 
-// Matrix-core B operands read from the weights (L2-resident) when a phase starts, so that they
-// hold registers only while that phase runs. In-proj: W_p[s][h], s = 64w + 16q + j, h = g KS + kk.
-template <int KS>
-TSF_DEV void load_w_operands(float (&wB)[kSlots][2][KS], const float* __restrict__ w_re, const float* __restrict__ w_im,
-                             int w, int g, int j, int H, int N) {
-#pragma unroll
-  for (int q = 0; q < kSlots; ++q) {
-    const int s = 64 * w + 16 * q + j;
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      const int h = g * KS + kk;
-      const bool ok = s < N && h < H;
-      wB[q][0][kk] = ok ? w_re[(int64_t)s * H + h] : 0.0f;
-      wB[q][1][kk] = ok ? w_im[(int64_t)s * H + h] : 0.0f;
-    }
-  }
-}
+// The g_x product's B operands, read from the weights (L2-resident) when the phase starts, so that
+// they hold registers only while it runs.
 // g_x: conj(C)_p[o][s], o = g OKS + kk (p = 0: C_re, 1: -C_im)
 template <int OKS>
 TSF_DEV void load_c_operands(float (&cG)[kSlots][2][OKS], const float* __restrict__ c_re,
                              const float* __restrict__ c_im, int w, int g, int j, int O, int N) {
 #pragma unroll
   for (int q = 0; q < kSlots; ++q) {
-    const int s = 64 * w + 16 * q + j;
+    const int s = kWaveStates * w + 16 * q + j;
 #pragma unroll
     for (int kk = 0; kk < OKS; ++kk) {
       const int o = g * OKS + kk;
@@ -397,36 +405,49 @@ TSF_DEV void load_c_operands(float (&cG)[kSlots][2][OKS], const float* __restric
   }
 }
 
+// Dynamic LDS of the backward: per wave its W rows [16 HB][kWuStride] and a transposed G block
+// [kBlk][kXtStride], then the waves' partial g_u blocks, double-buffered [2][NW][kBlk][16 HB].
+template <int HB>
+constexpr size_t bwd_lds_bytes(int nw) {
+  return sizeof(float) *
+         ((size_t)nw * 16 * HB * kWuStride + (size_t)nw * kBlk * kXtStride + 2 * (size_t)nw * kBlk * 16 * HB);
+}
+template <int KS>
+constexpr int hb_for_ks() { return KS == 8 ? 2 : 1; }
+
 template <int KS, int OB>
-__global__ void __launch_bounds__(256, 1)
+__global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(2)))
     projscan_bwd(const float* __restrict__ gy, const float2* __restrict__ g_xlast, const float2* __restrict__ saved,
                  const float* __restrict__ u, const float* __restrict__ w_re, const float* __restrict__ w_im,
                  const float2* __restrict__ lam, const float* __restrict__ c_re, const float* __restrict__ c_im,
                  float* __restrict__ g_u, float2* __restrict__ g_x0, float* __restrict__ part, int64_t part_stride,
                  double2* __restrict__ agg, double2* __restrict__ inc, unsigned* __restrict__ counter, int B, int L,
                  int H, int N, int O, int nsub, int lb_spacing) {
-  constexpr int HB = KS == 8 ? 2 : 1;  // 16-wide h blocks of g_u and grad W (H <= 16 HB)
+  constexpr int HB = hb_for_ks<KS>();  // 16-wide h blocks of g_u and grad W (H <= 16 HB)
   constexpr int OKS = 4 * OB;          // o per lane group in the g_x product (O <= 16 OB)
-  __shared__ __attribute__((aligned(16))) float s_wu[kMaxWaves][16 * HB][kWuStride];
-  __shared__ __attribute__((aligned(16))) float s_xt[kMaxWaves][kBlk][kXtStride];
-  __shared__ float s_gu[2][kMaxWaves][kBlk][16 * HB];
+  constexpr int kM = kRho / 4;         // MFMAs per 16-wide h block of g_u
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
   __shared__ unsigned s_tile[2];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, NW = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
-  const int64_t NS = (int64_t)NW * 64, cstride = (int64_t)B * NS, tiles = (int64_t)nsub * B;
+  float* const s_wu = s_dyn + (size_t)w * 16 * HB * kWuStride;  // this wave's [16 HB][kWuStride]
+  float* const s_xt = s_dyn + (size_t)NW * 16 * HB * kWuStride + (size_t)w * kBlk * kXtStride;
+  float* const s_gu = s_dyn + (size_t)NW * (16 * HB * kWuStride + kBlk * kXtStride);  // [2][NW][kBlk][16 HB]
+  const int64_t NS = (int64_t)NW * kWaveStates, cstride = (int64_t)B * NS, tiles = (int64_t)nsub * B;
   const Rsrc ru = make_rsrc(u, (uint32_t)((int64_t)B * L * H * 4));
   const Rsrc rg = make_rsrc(gy, (uint32_t)((int64_t)B * L * O * 4));
 
-  // g_u B operands, wave-private in LDS: s_wu[w][h][rho] = W_p[64w + rho/2][h], p = rho & 1
-  for (int idx = lane; idx < 16 * HB * 128; idx += 64) {
-    const int h = idx >> 7, rho = idx & 127, s = 64 * w + (rho >> 1);
+  // the wave's W rows in LDS, zero outside [N, H]: s_wu[h][rho] = W_p[kWaveStates w + rho/2][h],
+  // p = rho & 1 (the B operands of both the in-proj recompute and g_u)
+  for (int idx = lane; idx < 16 * HB * kRho; idx += 64) {
+    const int h = idx / kRho, rho = idx - h * kRho, s = kWaveStates * w + (rho >> 1);
     const bool ok = s < N && h < H;
-    s_wu[w][h][rho] = !ok ? 0.0f : (rho & 1) ? w_im[(int64_t)s * H + h] : w_re[(int64_t)s * H + h];
+    s_wu[h * kWuStride + rho] = !ok ? 0.0f : (rho & 1) ? w_im[(int64_t)s * H + h] : w_re[(int64_t)s * H + h];
   }
   float2 lm[kSlots], lm4[kSlots], lm8[kSlots], lmg[kSlots], lmr[kSlots], lm16[kSlots];
 #pragma unroll
   for (int q = 0; q < kSlots; ++q) {
-    const int s = 64 * w + 16 * q + j;
+    const int s = kWaveStates * w + 16 * q + j;
     const float2 a = s < N ? lam[s] : make_float2(0.0f, 0.0f);
     lm[q] = a;
     lm4[q] = ipow(a, 4);
@@ -435,8 +456,9 @@ __global__ void __launch_bounds__(256, 1)
     lmr[q] = ipow(a, 13 - 4 * g);
     lm16[q] = ipow(a, 16);
   }
-  const int s_lb = 64 * w + lane;
-  const double2 a_lb = s_lb < N ? up2(lam[s_lb]) : Num<double2>::zero();
+  const bool lb_lane = lane < kWaveStates;
+  const int s_lb = kWaveStates * w + lane;
+  const double2 a_lb = lb_lane && s_lb < N ? up2(lam[s_lb]) : Num<double2>::zero();
   const double2 cP16 = conj2(ipow(a_lb, 16)), cP32 = conj2(ipow(a_lb, kSub));
 
   f4 accC[OB][kSlots][2], accW[HB][kSlots][2];
@@ -462,7 +484,12 @@ __global__ void __launch_bounds__(256, 1)
 
     // phase A: g_x by MFMA, reverse scans from zero at each block's end
     float cG[kSlots][2][OKS];
-    load_c_operands<OKS>(cG, c_re, c_im, w, g, j, O, N);
+    // reloaded per tile (L2 hits): the pointers pass through an empty asm so that the loads are not
+    // hoisted out of the tile loop and the operands do not stay live across phase B
+    const float* cre = c_re;
+    const float* cim = c_im;
+    asm volatile("" : "+s"(cre), "+s"(cim));
+    load_c_operands<OKS>(cG, cre, cim, w, g, j, O, N);
     float2 G[kBwdBlocks][kSlots][4];
     float2 eg[kBwdBlocks][kSlots];  // G at each block's first step from zero after its end
 #pragma unroll
@@ -492,7 +519,7 @@ __global__ void __launch_bounds__(256, 1)
 #pragma unroll
         for (int r = 0; r < 4; ++r) G[k][q][r] = make_float2(acc[q][0][r], acc[q][1][r]);
         if (last_here) {
-          const int s = 64 * w + 16 * q + j;
+          const int s = kWaveStates * w + 16 * q + j;
           const float2 gl_in = s < N ? g_xlast[(int64_t)b * N + s] : make_float2(0.0f, 0.0f);
 #pragma unroll
           for (int r = 0; r < 4; ++r)
@@ -503,19 +530,22 @@ __global__ void __launch_bounds__(256, 1)
       }
     }
 
-    // look-back on lane (g, j) for state 64w + lane over the later chunks of the row
+    // look-back on lane (g, j) for state kWaveStates w + lane over the later chunks of the row
     double2 agg_v = Num<double2>::zero();
 #pragma unroll
     for (int k = kBwdBlocks - 1; k >= 0; --k) agg_v = Num<double2>::fma(cP16, agg_v, up2(pick(eg[k], g)));
     const int64_t widx = (int64_t)b * NS + s_lb;
     double2 R = Num<double2>::zero();  // G at the first step of the next chunk
-    if (c + 1 < nsub) {
-      if (lb_pub_agg(cr, lb_spacing) && c > 0) put(agg + (int64_t)c * cstride + widx, agg_v);
-      R = walk(agg, inc, cstride, widx, c, +1, nsub, cP32, counter);
+    if (lb_lane) {
+      if (c + 1 < nsub) {
+        if (lb_pub_agg(cr, lb_spacing) && c > 0) put(agg + (int64_t)c * cstride + widx, agg_v);
+        R = walk<4>(agg, inc, cstride, widx, c, +1, nsub, cP32, counter);
+      }
+      const double2 first = Num<double2>::fma(cP32, R, agg_v);  // G at this chunk's first step
+      if (lb_pub_inc(cr, lb_spacing) && c > 0) put(inc + (int64_t)c * cstride + widx, first);
+      if (c == 0 && g_x0 != nullptr && s_lb < N)
+        g_x0[(int64_t)b * N + s_lb] = down2(Num<double2>::mul(conj2(a_lb), first));
     }
-    const double2 first = Num<double2>::fma(cP32, R, agg_v);  // G at this chunk's first step
-    if (lb_pub_inc(cr, lb_spacing) && c > 0) put(inc + (int64_t)c * cstride + widx, first);
-    if (c == 0 && g_x0 != nullptr && s_lb < N) g_x0[(int64_t)b * N + s_lb] = down2(Num<double2>::mul(conj2(a_lb), first));
     float2 Rq[kSlots];
     {
       const float2 rf = down2(R);
@@ -536,11 +566,9 @@ __global__ void __launch_bounds__(256, 1)
       }
 
     // phase B: x recomputed block by block; the parameter gradients and g_u
-    float wB[kSlots][2][KS];
-    load_w_operands<KS>(wB, w_re, w_im, w, g, j, H, N);
     float2 xc[kSlots];  // state entering the current block
     {
-      const float2 sv = s_lb < N ? saved[((int64_t)b * nsub + c) * N + s_lb] : make_float2(0.0f, 0.0f);
+      const float2 sv = lb_lane && s_lb < N ? saved[((int64_t)b * nsub + c) * N + s_lb] : make_float2(0.0f, 0.0f);
 #pragma unroll
       for (int q = 0; q < kSlots; ++q) xc[q] = from_lane(sv, 16 * q + j);
     }
@@ -557,6 +585,11 @@ __global__ void __launch_bounds__(256, 1)
           const uint32_t off = (t < L && h < H) ? (uint32_t)((((int64_t)b * L + t) * H + h) * 4) : kOob;
           ua[kk] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ru, off, 0, 0));
         }
+        // in-proj B operands W_p[s][h] (s = kWaveStates w + 16 q + j, h = g KS + kk) read from LDS
+        // at each use: the offset passes through an empty asm so the reads are not hoisted out of
+        // the loops and the 2 kSlots KS values do not stay live across the tile
+        int wofs = (g * KS) * kWuStride + 2 * j;
+        asm volatile("" : "+v"(wofs));
         f4 acc[kSlots][2];
 #pragma unroll
         for (int q = 0; q < kSlots; ++q) acc[q][0] = acc[q][1] = f4_zero();
@@ -564,8 +597,9 @@ __global__ void __launch_bounds__(256, 1)
         for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
           for (int q = 0; q < kSlots; ++q) {
-            acc[q][0] = mfma(ua[kk], wB[q][0][kk], acc[q][0]);
-            acc[q][1] = mfma(ua[kk], wB[q][1][kk], acc[q][1]);
+            const float2 wv = *reinterpret_cast<const float2*>(&s_wu[wofs + kk * kWuStride + 32 * q]);
+            acc[q][0] = mfma(ua[kk], wv.x, acc[q][0]);
+            acc[q][1] = mfma(ua[kk], wv.y, acc[q][1]);
           }
 #pragma unroll
         for (int q = 0; q < kSlots; ++q) {
@@ -630,35 +664,37 @@ __global__ void __launch_bounds__(256, 1)
       for (int q = 0; q < kSlots; ++q)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          *reinterpret_cast<float2*>(&s_xt[w][4 * g + r][2 * (16 * q + j)]) = G[k][q][r];
-      float xa[32];
+          *reinterpret_cast<float2*>(&s_xt[(4 * g + r) * kXtStride + 2 * (16 * q + j)]) = G[k][q][r];
+      float xa[kM];
 #pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const f4 q4 = *reinterpret_cast<const f4*>(&s_xt[w][j][32 * g + 4 * v]);
+      for (int v = 0; v < kM / 4; ++v) {
+        const f4 q4 = *reinterpret_cast<const f4*>(&s_xt[j * kXtStride + kM * g + 4 * v]);
         xa[4 * v] = q4[0];
         xa[4 * v + 1] = q4[1];
         xa[4 * v + 2] = q4[2];
         xa[4 * v + 3] = q4[3];
       }
+      constexpr int kGw = kBlk * 16 * HB;  // floats of one wave's g_u block
+      float* const sg = s_gu + (size_t)(k & 1) * NW * kGw;
 #pragma unroll
       for (int hb = 0; hb < HB; ++hb) {
         f4 gacc = f4_zero();
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const f4 wv = *reinterpret_cast<const f4*>(&s_wu[w][16 * hb + j][32 * g + 4 * v]);
+        for (int v = 0; v < kM / 4; ++v) {
+          const f4 wv = *reinterpret_cast<const f4*>(&s_wu[(16 * hb + j) * kWuStride + kM * g + 4 * v]);
           gacc = mfma(xa[4 * v], wv[0], gacc);
           gacc = mfma(xa[4 * v + 1], wv[1], gacc);
           gacc = mfma(xa[4 * v + 2], wv[2], gacc);
           gacc = mfma(xa[4 * v + 3], wv[3], gacc);
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s_gu[k & 1][w][4 * g + r][16 * hb + j] = gacc[r];
+        for (int r = 0; r < 4; ++r) sg[w * kGw + (4 * g + r) * 16 * HB + 16 * hb + j] = gacc[r];
       }
       __syncthreads();
       for (int idx = threadIdx.x; idx < kBlk * H; idx += blockDim.x) {
         const int tt = idx / H, h = idx - tt * H;
-        float sum = s_gu[k & 1][0][tt][h];
-        for (int ww = 1; ww < NW; ++ww) sum += s_gu[k & 1][ww][tt][h];
+        float sum = sg[tt * 16 * HB + h];
+        for (int ww = 1; ww < NW; ++ww) sum += sg[ww * kGw + tt * 16 * HB + h];
         const int t = tb + tt;
         if (t < L) g_u[((int64_t)b * L + t) * H + h] = sum;
       }
@@ -672,7 +708,7 @@ __global__ void __launch_bounds__(256, 1)
   float* pl = pc + 2 * NS * Op;
 #pragma unroll
   for (int q = 0; q < kSlots; ++q) {
-    const int64_t s = 64 * w + 16 * q + j;
+    const int64_t s = kWaveStates * w + 16 * q + j;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
 #pragma unroll
@@ -744,11 +780,11 @@ struct PsPlan {
 
 PsPlan ps_plan(int64_t B, int64_t L, int64_t N) {
   PsPlan p;
-  p.nw = (int)((N + 63) / 64);
+  p.nw = (int)((N + kWaveStates - 1) / kWaveStates);
   p.nchunks = (L + kChunk - 1) / kChunk;
   p.nsub = (L + kSub - 1) / kSub;
   p.tiles = p.nchunks * B;
-  p.words = p.nchunks * B * p.nw * 64;
+  p.words = p.nchunks * B * p.nw * kWaveStates;
   p.off_agg = kCounterBytes;
   p.off_inc = p.off_agg + sizeof(double2) * (size_t)p.words;
   p.bytes = p.off_inc + sizeof(double2) * (size_t)p.words;
@@ -759,7 +795,7 @@ int ks_for(int64_t H) { return H <= 4 ? 1 : H <= 8 ? 2 : H <= 16 ? 4 : 8; }
 int ob_for(int64_t O) { return O <= 16 ? 1 : 2; }
 
 // Backward: 32-step tiles, look-back words per half chunk, and one partial-sum slot per
-// workgroup (at most one resident workgroup per 64-state wave set on each compute unit).
+// workgroup (a compute unit holds at most kMaxWaves / nw of them: two waves per SIMD).
 struct PbPlan {
   int nw = 1, groups = 1;
   int64_t nsub = 0, tiles = 0, words = 0, part_stride = 0;
@@ -768,13 +804,13 @@ struct PbPlan {
 
 PbPlan pb_plan(int64_t B, int64_t L, int64_t H, int64_t N, int64_t O) {
   PbPlan p;
-  p.nw = (int)((N + 63) / 64);
+  p.nw = (int)((N + kWaveStates - 1) / kWaveStates);
   p.nsub = (L + kSub - 1) / kSub;
   p.tiles = p.nsub * B;
-  p.words = p.nsub * B * p.nw * 64;
-  const int64_t NS = p.nw * 64, Hp = ks_for(H) == 8 ? 32 : 16, Op = 16 * ob_for(O);
+  p.words = p.nsub * B * p.nw * kWaveStates;
+  const int64_t NS = p.nw * kWaveStates, Hp = ks_for(H) == 8 ? 32 : 16, Op = 16 * ob_for(O);
   p.part_stride = ((2 * NS * Hp + 2 * NS * Op + 2 * NS) + 63) / 64 * 64;
-  const int64_t cap = (int64_t)device_cus() * (4 / p.nw > 0 ? 4 / p.nw : 1);
+  const int64_t cap = (int64_t)device_cus() * (kMaxWaves / p.nw > 0 ? kMaxWaves / p.nw : 1);
   p.groups = (int)(p.tiles < cap ? (p.tiles > 0 ? p.tiles : 1) : cap);
   p.off_agg = kCounterBytes;
   p.off_inc = p.off_agg + sizeof(double2) * (size_t)p.words;
@@ -795,39 +831,71 @@ int ps_args_status(int64_t B, int64_t L, int64_t H, int64_t N, int64_t O) {
 
 #define TSF_PS_CASES(X) X(1, 1) X(1, 2) X(2, 1) X(2, 2) X(4, 1) X(4, 2) X(8, 1) X(8, 2)
 
-template <int KS, int OB>
-void fwd_launch(const PsPlan& p, int64_t B, int64_t L, int64_t H, int64_t N, int64_t O, const float* u,
-                const float* w_re, const float* w_im, const float2* lam, const float* c_re, const float* c_im,
-                const float2* x0, float* y, float2* x_last, float2* saved, char* ws, hipStream_t s) {
-  static int occ[5];
-  const int threads = 64 * p.nw;
-  lookback_reset_launch(ws, 4 * p.words, s);
-  const int64_t cap = resident_wgs(projscan_fwd<KS, OB>, threads, occ);
-  hipLaunchKernelGGL((projscan_fwd<KS, OB>), dim3((unsigned)(p.tiles < cap ? p.tiles : cap)), dim3(threads), 0, s, u,
-                     w_re, w_im, lam, c_re, c_im, x0, y, x_last, saved, reinterpret_cast<double2*>(ws + p.off_agg),
-                     reinterpret_cast<double2*>(ws + p.off_inc), reinterpret_cast<unsigned*>(ws), (int)B, (int)L,
-                     (int)H, (int)N, (int)O, (int)p.nchunks, (int)p.nsub, lb_spacing_for(kAnchorSpacing));
+// Persistent grid size for a kernel with dynamic LDS (per device, cached by wave count); raises the
+// kernel's dynamic-LDS limit first when it needs more than the default 64 KiB.
+template <typename F>
+int resident_wgs_lds(F kern, int threads, size_t lds, int (&cache)[64][kMaxWaves + 1], int64_t& out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return tsf_record_hip_error(e);
+  if (dev < 0 || dev >= 64) return TSF_ERR_UNSUPPORTED;
+  int& c = cache[dev][threads / 64];
+  if (c == 0) {
+    if (lds > 65536) {
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return tsf_record_hip_error(e);
+    }
+    int n = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds);
+    if (e != hipSuccess) return tsf_record_hip_error(e);
+    if (n < 1) return TSF_ERR_UNSUPPORTED;
+    c = n;
+  }
+  out = (int64_t)c * device_cus();
+  return TSF_OK;
 }
 
 template <int KS, int OB>
-void bwd_launch(const PbPlan& p, int64_t B, int64_t L, int64_t H, int64_t N, int64_t O, const float* gy,
+int fwd_launch(const PsPlan& p, int64_t B, int64_t L, int64_t H, int64_t N, int64_t O, const float* u,
+               const float* w_re, const float* w_im, const float2* lam, const float* c_re, const float* c_im,
+               const float2* x0, float* y, float2* x_last, float2* saved, char* ws, hipStream_t s) {
+  static int occ[64][kMaxWaves + 1];
+  const int threads = 64 * p.nw;
+  const size_t lds = fwd_lds_bytes<OB>(p.nw);
+  int64_t cap = 0;
+  const int st = resident_wgs_lds(projscan_fwd<KS, OB>, threads, lds, occ, cap);
+  if (st != TSF_OK) return st;
+  lookback_reset_launch(ws, 4 * p.words, s);
+  hipLaunchKernelGGL((projscan_fwd<KS, OB>), dim3((unsigned)(p.tiles < cap ? p.tiles : cap)), dim3(threads), lds, s, u,
+                     w_re, w_im, lam, c_re, c_im, x0, y, x_last, saved, reinterpret_cast<double2*>(ws + p.off_agg),
+                     reinterpret_cast<double2*>(ws + p.off_inc), reinterpret_cast<unsigned*>(ws), (int)B, (int)L,
+                     (int)H, (int)N, (int)O, (int)p.nchunks, (int)p.nsub, lb_spacing_for(kAnchorSpacing));
+  return TSF_OK;
+}
+
+template <int KS, int OB>
+int bwd_launch(const PbPlan& p, int64_t B, int64_t L, int64_t H, int64_t N, int64_t O, const float* gy,
                 const float2* g_xlast, const float2* saved, const float* u, const float* w_re, const float* w_im,
                 const float2* lam, const float* c_re, const float* c_im, float* g_u, float* g_w_re, float* g_w_im,
                 float* g_lam, float* g_c_re, float* g_c_im, float2* g_x0, char* ws, hipStream_t s) {
-  static int occ[5];
+  static int occ[64][kMaxWaves + 1];
   const int threads = 64 * p.nw;
+  const size_t lds = bwd_lds_bytes<hb_for_ks<KS>()>(p.nw);
+  int64_t cap = 0;
+  const int st = resident_wgs_lds(projscan_bwd<KS, OB>, threads, lds, occ, cap);
+  if (st != TSF_OK) return st;
   lookback_reset_launch(ws, 4 * p.words, s);
-  const int64_t cap = resident_wgs(projscan_bwd<KS, OB>, threads, occ);
   const int grid = (int)(p.groups < cap ? p.groups : cap);
   float* part = reinterpret_cast<float*>(ws + p.off_part);
-  hipLaunchKernelGGL((projscan_bwd<KS, OB>), dim3((unsigned)grid), dim3(threads), 0, s, gy, g_xlast, saved, u, w_re,
+  hipLaunchKernelGGL((projscan_bwd<KS, OB>), dim3((unsigned)grid), dim3(threads), lds, s, gy, g_xlast, saved, u, w_re,
                      w_im, lam, c_re, c_im, g_u, g_x0, part, p.part_stride,
                      reinterpret_cast<double2*>(ws + p.off_agg), reinterpret_cast<double2*>(ws + p.off_inc),
                      reinterpret_cast<unsigned*>(ws), (int)B, (int)L, (int)H, (int)N, (int)O, (int)p.nsub, lb_spacing_for(kAnchorSpacing));
   const int64_t outs = 2 * N * H + 2 * O * N + 2 * N;
   hipLaunchKernelGGL(projscan_bwd_reduce, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, part, p.part_stride,
-                     grid, (int)N, p.nw * 64, (int)H, KS == 8 ? 32 : 16, (int)O, 16 * OB, g_w_re, g_w_im, g_c_re,
+                     grid, (int)N, p.nw * kWaveStates, (int)H, KS == 8 ? 32 : 16, (int)O, 16 * OB, g_w_re, g_w_im, g_c_re,
                      g_c_im, g_lam);
+  return TSF_OK;
 }
 
 }  // namespace
@@ -871,9 +939,11 @@ int tsfast_hip_projscan_fwd(int64_t B, int64_t L, int64_t H, int64_t N, int64_t 
   float2* sv = reinterpret_cast<float2*>(saved);
   switch (ks_for(H) * 10 + ob_for(O)) {
 #define X(KS_, OB_)                                                                                            \
-  case KS_ * 10 + OB_:                                                                                         \
-    fwd_launch<KS_, OB_>(p, B, L, H, N, O, u, w_re, w_im, lamc, c_re, c_im, x0c, y, xl, sv, ws, s); \
-    break;
+  case KS_ * 10 + OB_: {                                                                                       \
+    const int rc = fwd_launch<KS_, OB_>(p, B, L, H, N, O, u, w_re, w_im, lamc, c_re, c_im, x0c, y, xl, sv, ws, s); \
+    if (rc != TSF_OK) return rc;                                                                               \
+    break;                                                                                                     \
+  }
     TSF_PS_CASES(X)
 #undef X
     default:
@@ -908,10 +978,12 @@ int tsfast_hip_projscan_bwd(int64_t B, int64_t L, int64_t H, int64_t N, int64_t 
   const float2* sv = reinterpret_cast<const float2*>(saved);
   switch (ks_for(H) * 10 + ob_for(O)) {
 #define X(KS_, OB_)                                                                                                 \
-  case KS_ * 10 + OB_:                                                                                              \
-    bwd_launch<KS_, OB_>(p, B, L, H, N, O, gy, gxl, sv, u, w_re, w_im, lamc, c_re, c_im, g_u, g_w_re, g_w_im, gl, \
-                         g_c_re, g_c_im, gx0, ws, s);                                                               \
-    break;
+  case KS_ * 10 + OB_: {                                                                                            \
+    const int rc = bwd_launch<KS_, OB_>(p, B, L, H, N, O, gy, gxl, sv, u, w_re, w_im, lamc, c_re, c_im, g_u, g_w_re, \
+                                        g_w_im, gl, g_c_re, g_c_im, gx0, ws, s);                                    \
+    if (rc != TSF_OK) return rc;                                                                                    \
+    break;                                                                                                          \
+  }
     TSF_PS_CASES(X)
 #undef X
     default:
