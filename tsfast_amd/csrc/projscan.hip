@@ -388,30 +388,63 @@ TSF_DEV void block_scan_rev(float2 (&x)[4], float2 lm, float2 lm4, float2 lm8, i
 
 // The g_x product's B operands, read from the weights (L2-resident) when the phase starts, so that
 // they hold registers only while it runs.
-// g_x: conj(C)_p[o][s], o = g OKS + kk (p = 0: C_re, 1: -C_im)
+// g_x: conj(C)_p[o][s], o = g OKS + kk (p = 0: C_re, 1: -C_im).
+// Read through buffer resources (o >= O falls past the end and reads 0) with 32-bit offsets from a
+// per-lane base that passes through an empty asm, so that neither the values nor their addresses
+// stay live across the tile loop.
 template <int OKS>
-TSF_DEV void load_c_operands(float (&cG)[kSlots][2][OKS], const float* __restrict__ c_re,
-                             const float* __restrict__ c_im, int w, int g, int j, int O, int N) {
+TSF_DEV void load_c_operands(float (&cG)[kSlots][2][OKS], const Rsrc& rre, const Rsrc& rim, int w, int g, int j,
+                             int N) {
+  int base = g * OKS * N + kWaveStates * w + j;
+  asm volatile("" : "+v"(base));
 #pragma unroll
   for (int q = 0; q < kSlots; ++q) {
-    const int s = kWaveStates * w + 16 * q + j;
+    const bool live = kWaveStates * w + 16 * q + j < N;
 #pragma unroll
     for (int kk = 0; kk < OKS; ++kk) {
-      const int o = g * OKS + kk;
-      const bool ok = s < N && o < O;
-      cG[q][0][kk] = ok ? c_re[(int64_t)o * N + s] : 0.0f;
-      cG[q][1][kk] = ok ? -c_im[(int64_t)o * N + s] : 0.0f;
+      const uint32_t off = live ? (uint32_t)(base + kk * N + 16 * q) * 4u : kOob;
+      cG[q][0][kk] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rre, off, 0, 0));
+      cG[q][1][kk] = -__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rim, off, 0, 0));
     }
   }
 }
 
+// Per-wave table of the powers of lam the backward's scans use, in LDS, read at each use rather
+// than held in registers across the tile loop: lam, lam^4, lam^8, lam^16 per (slot, column) and
+// lam^(4g+1), lam^(13-4g) per (slot, lane), float2 each.
+constexpr int kPwFloats = 2 * (4 * kSlots * 16 + 2 * kSlots * 64);
 // Dynamic LDS of the backward: per wave its W rows [16 HB][kWuStride] and a transposed G block
-// [kBlk][kXtStride], then the waves' partial g_u blocks, double-buffered [2][NW][kBlk][16 HB].
+// [kBlk][kXtStride], then the waves' partial g_u blocks, double-buffered [2][NW][kBlk][16 HB],
+// then the waves' power tables [NW][kPwFloats].
 template <int HB>
 constexpr size_t bwd_lds_bytes(int nw) {
-  return sizeof(float) *
-         ((size_t)nw * 16 * HB * kWuStride + (size_t)nw * kBlk * kXtStride + 2 * (size_t)nw * kBlk * 16 * HB);
+  return sizeof(float) * ((size_t)nw * 16 * HB * kWuStride + (size_t)nw * kBlk * kXtStride +
+                          2 * (size_t)nw * kBlk * 16 * HB + (size_t)nw * kPwFloats);
 }
+struct Pows {
+  float2 lm, lm4, lm8, lm16, lmx;  // lmx = lam^(4g+1) (forward-time fix-up) or lam^(13-4g) (reverse)
+};
+// Table layout in float2: [4][kSlots][16] (lam, lam^4, lam^8, lam^16 per column j), then
+// [2][kSlots][64] (lam^(4g+1), lam^(13-4g) per lane).
+TSF_DEV int pow_col(int kind, int q, int j) { return (kind * kSlots + q) * 16 + j; }
+TSF_DEV int pow_lane(int kind, int q, int lane) { return 4 * kSlots * 16 + (kind * kSlots + q) * 64 + lane; }
+// The powers of slot q for this lane. `zero` is 0 passed through an empty asm at the call site, so
+// the LDS reads stay where they are used instead of being hoisted out of the tile loop.
+TSF_DEV Pows read_pows(const float2* t, int zero, int q, int j, int lane, bool reverse) {
+  Pows p;
+  p.lm = t[zero + pow_col(0, q, j)];
+  p.lm4 = t[zero + pow_col(1, q, j)];
+  p.lm8 = t[zero + pow_col(2, q, j)];
+  p.lm16 = t[zero + pow_col(3, q, j)];
+  p.lmx = t[zero + pow_lane(reverse ? 1 : 0, q, lane)];
+  return p;
+}
+TSF_DEV int opaque_zero() {
+  int z = 0;
+  asm volatile("" : "+v"(z));
+  return z;
+}
+
 template <int KS>
 constexpr int hb_for_ks() { return KS == 8 ? 2 : 1; }
 
@@ -433,9 +466,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
   float* const s_wu = s_dyn + (size_t)w * 16 * HB * kWuStride;  // this wave's [16 HB][kWuStride]
   float* const s_xt = s_dyn + (size_t)NW * 16 * HB * kWuStride + (size_t)w * kBlk * kXtStride;
   float* const s_gu = s_dyn + (size_t)NW * (16 * HB * kWuStride + kBlk * kXtStride);  // [2][NW][kBlk][16 HB]
+  float2* const s_pw = reinterpret_cast<float2*>(s_gu + (size_t)2 * NW * kBlk * 16 * HB) + (size_t)w * kPwFloats / 2;
   const int64_t NS = (int64_t)NW * kWaveStates, cstride = (int64_t)B * NS, tiles = (int64_t)nsub * B;
   const Rsrc ru = make_rsrc(u, (uint32_t)((int64_t)B * L * H * 4));
   const Rsrc rg = make_rsrc(gy, (uint32_t)((int64_t)B * L * O * 4));
+  const Rsrc rcre = make_rsrc(c_re, (uint32_t)(O * N * 4)), rcim = make_rsrc(c_im, (uint32_t)(O * N * 4));
 
   // the wave's W rows in LDS, zero outside [N, H]: s_wu[h][rho] = W_p[kWaveStates w + rho/2][h],
   // p = rho & 1 (the B operands of both the in-proj recompute and g_u)
@@ -444,22 +479,22 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
     const bool ok = s < N && h < H;
     s_wu[h * kWuStride + rho] = !ok ? 0.0f : (rho & 1) ? w_im[(int64_t)s * H + h] : w_re[(int64_t)s * H + h];
   }
-  float2 lm[kSlots], lm4[kSlots], lm8[kSlots], lmg[kSlots], lmr[kSlots], lm16[kSlots];
+  // the wave's power table (read back by read_pows at each use)
 #pragma unroll
   for (int q = 0; q < kSlots; ++q) {
     const int s = kWaveStates * w + 16 * q + j;
     const float2 a = s < N ? lam[s] : make_float2(0.0f, 0.0f);
-    lm[q] = a;
-    lm4[q] = ipow(a, 4);
-    lm8[q] = ipow(a, 8);
-    lmg[q] = ipow(a, 4 * g + 1);
-    lmr[q] = ipow(a, 13 - 4 * g);
-    lm16[q] = ipow(a, 16);
+    if (g == 0) {
+      s_pw[pow_col(0, q, j)] = a;
+      s_pw[pow_col(1, q, j)] = ipow(a, 4);
+      s_pw[pow_col(2, q, j)] = ipow(a, 8);
+      s_pw[pow_col(3, q, j)] = ipow(a, 16);
+    }
+    s_pw[pow_lane(0, q, lane)] = ipow(a, 4 * g + 1);
+    s_pw[pow_lane(1, q, lane)] = ipow(a, 13 - 4 * g);
   }
   const bool lb_lane = lane < kWaveStates;
   const int s_lb = kWaveStates * w + lane;
-  const double2 a_lb = lb_lane && s_lb < N ? up2(lam[s_lb]) : Num<double2>::zero();
-  const double2 cP16 = conj2(ipow(a_lb, 16)), cP32 = conj2(ipow(a_lb, kSub));
 
   f4 accC[OB][kSlots][2], accW[HB][kSlots][2];
 #pragma unroll
@@ -484,12 +519,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
 
     // phase A: g_x by MFMA, reverse scans from zero at each block's end
     float cG[kSlots][2][OKS];
-    // reloaded per tile (L2 hits): the pointers pass through an empty asm so that the loads are not
-    // hoisted out of the tile loop and the operands do not stay live across phase B
-    const float* cre = c_re;
-    const float* cim = c_im;
-    asm volatile("" : "+s"(cre), "+s"(cim));
-    load_c_operands<OKS>(cG, cre, cim, w, g, j, O, N);
+    // reloaded per tile (L2 hits), so that they do not stay live across phase B
+    load_c_operands<OKS>(cG, rcre, rcim, w, g, j, N);
     float2 G[kBwdBlocks][kSlots][4];
     float2 eg[kBwdBlocks][kSlots];  // G at each block's first step from zero after its end
 #pragma unroll
@@ -525,12 +556,18 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
           for (int r = 0; r < 4; ++r)
             if (r == (tl & 3)) G[k][q][r] = cadd(G[k][q][r], gl_in);
         }
-        block_scan_rev(G[k][q], lm[q], lm4[q], lm8[q], lane);
+        const Pows pw = read_pows(s_pw, opaque_zero(), q, j, lane, true);
+        block_scan_rev(G[k][q], pw.lm, pw.lm4, pw.lm8, lane);
         eg[k][q] = from_lane(G[k][q][0], j);
       }
     }
 
-    // look-back on lane (g, j) for state kWaveStates w + lane over the later chunks of the row
+    // look-back on lane (g, j) for state kWaveStates w + lane over the later chunks of the row; the
+    // multipliers come from lam per tile (an L2 hit) instead of living across the tile loop
+    const float2* lam_t = lam;
+    asm volatile("" : "+s"(lam_t));
+    const double2 a_lb = lb_lane && s_lb < N ? up2(lam_t[s_lb]) : Num<double2>::zero();
+    const double2 cP16 = conj2(ipow(a_lb, 16)), cP32 = conj2(ipow(a_lb, kSub));
     double2 agg_v = Num<double2>::zero();
 #pragma unroll
     for (int k = kBwdBlocks - 1; k >= 0; --k) agg_v = Num<double2>::fma(cP16, agg_v, up2(pick(eg[k], g)));
@@ -556,13 +593,14 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
     for (int k = kBwdBlocks - 1; k >= 0; --k)
 #pragma unroll
       for (int q = 0; q < kSlots; ++q) {
-        float2 p = cmul_c(lmr[q], Rq[q]);
+        const Pows pw = read_pows(s_pw, opaque_zero(), q, j, lane, true);
+        float2 p = cmul_c(pw.lmx, Rq[q]);
 #pragma unroll
         for (int r = 3; r >= 0; --r) {
           G[k][q][r] = cadd(G[k][q][r], p);
-          p = cmul_c(lm[q], p);
+          p = cmul_c(pw.lm, p);
         }
-        Rq[q] = cfma_c(lm16[q], Rq[q], eg[k][q]);
+        Rq[q] = cfma_c(pw.lm16, Rq[q], eg[k][q]);
       }
 
     // phase B: x recomputed block by block; the parameter gradients and g_u
@@ -605,13 +643,14 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
         for (int q = 0; q < kSlots; ++q) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) X[q][r] = make_float2(acc[q][0][r], acc[q][1][r]);
-          block_scan(X[q], lm[q], lm4[q], lm8[q], lane);
+          const Pows pw = read_pows(s_pw, opaque_zero(), q, j, lane, false);
+          block_scan(X[q], pw.lm, pw.lm4, pw.lm8, lane);
           const float2 ex = from_lane(X[q][3], 48 + j);
-          float2 p = cmul(lmg[q], xc[q]);
+          float2 p = cmul(pw.lmx, xc[q]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             X[q][r] = cadd(X[q][r], p);
-            p = cmul(lm[q], p);
+            p = cmul(pw.lm, p);
           }
           // grad lam: G_t conj(x_{t-1}); x_{t-1} of a group's first step is the group below's last
           const float2 below = from_lane(X[q][3], lane - 16);
@@ -620,7 +659,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
 #pragma unroll
           for (int r = 1; r < 4; ++r) acc_l = cadd(acc_l, cmul_conj(G[k][q][r], X[q][r - 1]));
           gl[q] = cadd(gl[q], acc_l);
-          xc[q] = cfma(lm16[q], xc[q], ex);
+          xc[q] = cfma(pw.lm16, xc[q], ex);
         }
       }
       // grad C (A = gy^T: lane j -> o = 16 ob + j, group g -> step 4g + r; B = x)
@@ -723,24 +762,29 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
   }
 }
 
-// Adds the workgroups' partial sums in workgroup order: grad W_re / W_im [N, H], grad C_re /
-// C_im [O, N] (C_im's sums negated), grad lam [N] complex.
+// Adds the workgroups' partial sums: grad W_re / W_im [N, H], grad C_re / C_im [O, N] (C_im's
+// sums negated), grad lam [N] complex. A block of 256 threads takes 64 outputs, consecutive in the
+// partial buffer's layout (so every load of a wave is one contiguous row segment); thread slice k
+// (of 4) adds the workgroups k, k + 4, ... in order, and the four slice sums are added in slice
+// order, so the result does not depend on timing.
 __global__ void __launch_bounds__(256) projscan_bwd_reduce(const float* __restrict__ part, int64_t part_stride,
                                                            int groups, int N, int NS, int H, int Hp, int O, int Op,
                                                            float* __restrict__ g_w_re, float* __restrict__ g_w_im,
                                                            float* __restrict__ g_c_re, float* __restrict__ g_c_im,
                                                            float* __restrict__ g_lam) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  __shared__ float s_sum[4][64];
+  const int lo = threadIdx.x & 63, slice = threadIdx.x >> 6;
+  const int64_t i = blockIdx.x * (int64_t)64 + lo;
   const int64_t nW = 2 * (int64_t)N * H, nC = 2 * (int64_t)O * N, nL = 2 * (int64_t)N;
-  int64_t off;
-  float* dst;
+  int64_t off = 0;
+  float* dst = nullptr;
   float sign = 1.0f;
   if (i < nW) {
     const int64_t p = i / ((int64_t)N * H), rem = i - p * N * H, s = rem / H, h = rem - s * H;
     off = (p * NS + s) * Hp + h;
     dst = (p ? g_w_im : g_w_re) + s * H + h;
   } else if (i < nW + nC) {
-    const int64_t k = i - nW, p = k / ((int64_t)O * N), rem = k - p * O * N, o = rem / N, s = rem - o * N;
+    const int64_t k = i - nW, p = k / ((int64_t)O * N), rem = k - p * O * N, s = rem / O, o = rem - s * O;
     off = 2 * (int64_t)NS * Hp + (p * NS + s) * Op + o;
     dst = (p ? g_c_im : g_c_re) + o * N + s;
     sign = p ? -1.0f : 1.0f;
@@ -748,12 +792,15 @@ __global__ void __launch_bounds__(256) projscan_bwd_reduce(const float* __restri
     const int64_t k = i - nW - nC;
     off = 2 * (int64_t)NS * Hp + 2 * (int64_t)NS * Op + k;
     dst = g_lam + k;
-  } else {
-    return;
   }
   float sum = 0.0f;
-  for (int grp = 0; grp < groups; ++grp) sum += part[(int64_t)grp * part_stride + off];
-  *dst = sign * sum;
+  if (dst != nullptr) {
+#pragma unroll 4
+    for (int grp = slice; grp < groups; grp += 4) sum += part[(int64_t)grp * part_stride + off];
+  }
+  s_sum[slice][lo] = sum;
+  __syncthreads();
+  if (slice == 0 && dst != nullptr) *dst = sign * (((s_sum[0][lo] + s_sum[1][lo]) + s_sum[2][lo]) + s_sum[3][lo]);
 }
 
 // Gradients of an empty sequence (L = 0): the parameters get zeros, g_x0 = g_xlast (x_last = x0).
@@ -892,7 +939,7 @@ int bwd_launch(const PbPlan& p, int64_t B, int64_t L, int64_t H, int64_t N, int6
                      reinterpret_cast<double2*>(ws + p.off_agg), reinterpret_cast<double2*>(ws + p.off_inc),
                      reinterpret_cast<unsigned*>(ws), (int)B, (int)L, (int)H, (int)N, (int)O, (int)p.nsub, lb_spacing_for(kAnchorSpacing));
   const int64_t outs = 2 * N * H + 2 * O * N + 2 * N;
-  hipLaunchKernelGGL(projscan_bwd_reduce, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, part, p.part_stride,
+  hipLaunchKernelGGL(projscan_bwd_reduce, dim3((unsigned)((outs + 63) / 64)), dim3(256), 0, s, part, p.part_stride,
                      grid, (int)N, p.nw * kWaveStates, (int)H, KS == 8 ? 32 : 16, (int)O, 16 * OB, g_w_re, g_w_im, g_c_re,
                      g_c_im, g_lam);
   return TSF_OK;
