@@ -30,6 +30,12 @@ _DIAG_SHAPES = [
     ((32, 1000, 64), (32, 64)),  # config 1
     ((4, 4096, 256), (256,)),  # config 2, batch reduced
     ((16, 2048, 256), (256,)),  # enough lanes for the 32-step real chunk tiles
+    # bounds of the whole-sequence tiles (one workgroup per lane group covers L <= 16 chunks:
+    # 1024 real steps, 512 complex forward, 256 complex backward) and ragged lane groups
+    ((2, 1024, 64), (64,)),
+    ((2, 1025, 64), (64,)),
+    ((2, 512, 32), (32,)),
+    ((3, 256, 70), (70,)),
 ]
 
 
@@ -153,6 +159,40 @@ def test_tbptt_chunked_equals_unchunked(gpu):
     want = O.diag_forward(_np(lam), _np(v), None)
     assert O.rel_err(_np(full), want) < TOL
     assert O.rel_err(_np(chunked), want) < TOL
+
+
+@pytest.mark.parametrize("cplx", [0, 1])
+def test_whole_sequence_tiles_clear_the_flag(gpu, cplx):
+    """A call served by whole-sequence tiles (no look-back, no reset kernel) leaves the workspace's
+    give-up flag clear even when the buffer held a stale one, in both directions."""
+    from tsfast_amd import _lib
+
+    lib = _lib.load()
+    dtype = torch.complex64 if cplx else torch.float32
+    lam, v, x0, gout = _make_diag((4, 200, 64), (64,), dtype, seed=33)
+    lam_l, _, _ = _lanes(lam, v, x0)
+    M, L, N = v.shape
+    nbytes = lib.tsfast_hip_diag_workspace_bytes(M, L, N, cplx)
+    lam_d, v_d, x0_d, g_d = (t.to(gpu) for t in (lam_l, v, x0, gout))
+    out = torch.empty_like(v_d)
+    gv, glam, gx0 = torch.empty_like(v_d), torch.empty_like(lam_d), torch.empty_like(x0_d)
+    for call in ("fwd", "bwd"):
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+        ws[_lib.LOOKBACK_ERR_OFFSET] = 1
+        if call == "fwd":
+            st = lib.tsfast_hip_diag_fwd(M, L, N, cplx, _lib.ptr(lam_d), _lib.ptr(v_d), _lib.ptr(x0_d), _lib.ptr(out),
+                                         _lib.ptr(ws), nbytes, _lib.stream_of(v_d))
+        else:
+            st = lib.tsfast_hip_diag_bwd(M, L, N, cplx, _lib.ptr(g_d), _lib.ptr(lam_d), _lib.ptr(out), _lib.ptr(x0_d),
+                                         _lib.ptr(gv), _lib.ptr(glam), _lib.ptr(gx0), _lib.ptr(ws), nbytes,
+                                         _lib.stream_of(v_d))
+        _lib.check(st, f"tsfast_hip_diag_{call}")
+        torch.cuda.synchronize()
+        assert not _lib.lookback_gave_up(ws), call
+    want = O.diag_forward(_np(lam_l), _np(v), _np(x0))
+    glam_w, gv_w, gx0_w = O.diag_backward(_np(gout), _np(lam_l), want, _np(x0))
+    assert O.rel_err(_np(out), want) < TOL
+    assert O.rel_err(_np(gv), gv_w) < TOL and O.rel_err(_np(glam), glam_w) < TOL and O.rel_err(_np(gx0), gx0_w) < TOL
 
 
 def test_lookback_give_up_flag_cleared_and_unset(gpu):

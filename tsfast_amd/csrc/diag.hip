@@ -406,6 +406,162 @@ __global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, cons
   }
 }
 
+// ---------------------------------------------------------------- whole-sequence tiles
+// When K <= 16 chunks of TC steps cover the sequence, one workgroup of K waves takes a 64-lane
+// group's whole sequence (wave k the k-th chunk): no look-back, no workspace words and no reset
+// launch, so each direction is a single kernel. After one barrier every wave composes the
+// summaries of the chunks before it (forward) or after it (backward) from LDS into its entering
+// state, at most K - 1 fp64 folds.
+template <typename T, int TC>
+__global__ void __launch_bounds__(1024) diag_whole_fwd(const T* __restrict__ lam, const T* __restrict__ v,
+                                                       const T* __restrict__ x0, T* __restrict__ out,
+                                                       unsigned* __restrict__ ws_head, int64_t lanes, int64_t L,
+                                                       int64_t N) {
+  using W = typename Wide<T>::type;
+  __shared__ W s_e[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
+  const int64_t lane = (int64_t)blockIdx.x * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t t0 = (int64_t)k * TC;
+  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) ws_head[kErrWord] = 0;  // no look-back: nothing can give up
+  W a = Num<W>::zero(), e = Num<W>::zero();
+  T vb[TC];
+  int64_t base = 0;
+  if (live) {
+    a = Wide<T>::up(lam[lane]);
+    const int64_t m = lane / N, n = lane - m * N;
+    base = (m * L + t0) * N + n;
+    const T* vp = v + base;
+    if (len == TC) {
+#pragma unroll
+      for (int i = 0; i < TC; ++i) vb[i] = vp[i * N];
+#pragma unroll
+      for (int i = 0; i < TC; ++i) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < TC; ++i)
+        if (i < len) vb[i] = vp[i * N];
+#pragma unroll
+      for (int i = 0; i < TC; ++i)
+        if (i < len) e = Num<W>::fma(a, e, Wide<T>::up(vb[i]));
+    }
+  }
+  s_e[k][lid] = e;
+  __syncthreads();
+  if (!live || len == 0) return;
+  const W Pc = ipow(a, TC);  // every chunk before a non-empty one is full
+  W x = x0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
+  for (int j = 0; j < k; ++j) x = Num<W>::fma(Pc, x, s_e[j][lid]);
+  T* op = out + base;
+  if (len == TC) {
+#pragma unroll
+    for (int i = 0; i < TC; ++i) {
+      x = Num<W>::fma(a, x, Wide<T>::up(vb[i]));
+      op[i * N] = Wide<T>::down(x);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TC; ++i)
+      if (i < len) {
+        x = Num<W>::fma(a, x, Wide<T>::up(vb[i]));
+        op[i * N] = Wide<T>::down(x);
+      }
+  }
+}
+
+// Backward of the whole-sequence tile: each wave summarises its chunk's adjoint from a zero state
+// (f = G at the chunk's first step), then re-runs it half a chunk at a time from the G entering
+// from the right, writing gv and accumulating glam = sum_t G_t conj(x_{t-1}). The re-run reloads
+// its g values (L2 hits) together with x, through a pointer the compiler cannot see through, so
+// at most one chunk of values is live at a time; the K per-chunk glam sums are added in order.
+template <typename T, int TC>
+__global__ void __launch_bounds__(1024) diag_whole_bwd(const T* __restrict__ lam, const T* __restrict__ g,
+                                                       const T* __restrict__ out, const T* __restrict__ x0,
+                                                       T* __restrict__ gv, T* __restrict__ glam, T* __restrict__ gx0,
+                                                       unsigned* __restrict__ ws_head, int64_t lanes, int64_t L,
+                                                       int64_t N) {
+  using W = typename Wide<T>::type;
+  constexpr int H2 = TC / 2;
+  __shared__ W s_f[kMaxWaves][64];
+  __shared__ W s_acc[kMaxWaves][64];
+  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6, K = blockDim.x >> 6;
+  const int64_t lane = (int64_t)blockIdx.x * 64 + lid;
+  const bool live = lane < lanes;
+  const int64_t t0 = (int64_t)k * TC;
+  const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) ws_head[kErrWord] = 0;  // no look-back: nothing can give up
+  W ac = Num<W>::zero(), f = Num<W>::zero();
+  int64_t base = 0;
+  if (live) {
+    ac = Num<W>::conj(Wide<T>::up(lam[lane]));
+    const int64_t m = lane / N, n = lane - m * N;
+    base = (m * L + t0) * N + n;
+    const T* gp = g + base;
+    T gb[TC];
+    if (len == TC) {
+#pragma unroll
+      for (int i = 0; i < TC; ++i) gb[i] = gp[i * N];
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < TC; ++i) gb[i] = gp[(i < len ? i : len - 1) * N];  // clamped, branch-free
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i)
+        if (i < len) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
+    }
+  }
+  s_f[k][lid] = f;
+  __syncthreads();
+  W acc = Num<W>::zero();
+  if (live && len > 0) {
+    const W Pc = ipow(ac, TC);  // every chunk before a non-empty one is full
+    W G = Num<W>::zero();       // G entering the chunk from the right
+    for (int j = K - 1; j > k; --j) G = Num<W>::fma(Pc, G, s_f[j][lid]);
+    T* gvp = gv + base;
+#pragma unroll
+    for (int h = 1; h >= 0; --h) {
+      const T* gp = g + base;
+      const T* xp = out + base;
+      asm volatile("" : "+v"(gp), "+v"(xp));
+      T gh[H2], xh[H2];  // g_t and x_{t-1} (x0, or zero without it, before the first step)
+      if (len == TC && t0 > 0) {
+#pragma unroll
+        for (int i = 0; i < H2; ++i) {
+          gh[i] = gp[(h * H2 + i) * N];
+          xh[i] = xp[(h * H2 + i - 1) * N];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < H2; ++i) {  // clamped into the chunk, branch-free
+          const int ii = h * H2 + i < len ? h * H2 + i : len - 1;
+          gh[i] = gp[ii * N];
+          xh[i] = xp[(t0 + ii > 0 ? ii - 1 : 0) * N];
+        }
+        if (t0 == 0 && h == 0) xh[0] = x0 ? x0[lane] : T{};
+      }
+#pragma unroll
+      for (int i = H2 - 1; i >= 0; --i) {
+        const int ii = h * H2 + i;
+        if (ii < len) {
+          G = Num<W>::fma(ac, G, Wide<T>::up(gh[i]));
+          gvp[ii * N] = Wide<T>::down(G);
+          acc = Num<W>::fma(G, Num<W>::conj(Wide<T>::up(xh[i])), acc);
+        }
+      }
+    }
+    if (k == 0 && gx0) gx0[lane] = Wide<T>::down(Num<W>::mul(ac, G));
+  }
+  s_acc[k][lid] = acc;
+  __syncthreads();
+  if (k == 0 && live) {
+    W sum = s_acc[0][lid];
+    for (int j = 1; j < K; ++j) sum = Num<W>::add(sum, s_acc[j][lid]);
+    glam[lane] = Wide<T>::down(sum);
+  }
+}
+
 // glam = sum over super-chunks of the partials, in a fixed order (deterministic run to run):
 // wave k adds the k-th of 16 contiguous segments, wave 0 adds the 16 segment sums in order.
 template <typename T>
@@ -714,6 +870,12 @@ unsigned persistent_grid(const DiagTile& t, F kern, int* cache) {
 }
 
 
+// Whole-sequence tiling (diag_whole_fwd / diag_whole_bwd): steps per wave, and whether K <= 16
+// such chunks cover the sequence.
+constexpr int whole_tc(bool cplx, bool bwd) { return cplx ? (bwd ? 16 : 32) : 64; }
+inline bool whole_fits(int64_t L, int tc) { return L <= (int64_t)kMaxWaves * tc; }
+inline dim3 whole_block(int64_t L, int tc) { return dim3((unsigned)(64 * ((L + tc - 1) / tc))); }
+
 template <typename T, int TC>
 void diag_fwd_launch(const DiagTile& t, const T* lam, const T* v, const T* x0, T* out, char* ws, int64_t L, int64_t N,
                      hipStream_t s) {
@@ -814,6 +976,9 @@ int noalloc_scratch(hipStream_t s, char** out) {
 extern "C" {
 
 int64_t tsfast_hip_diag_workspace_bytes(int64_t M, int64_t L, int64_t N, int is_complex) {
+  // whole-sequence tiles in both directions: only the header (its look-back flag word) is used
+  if (whole_fits(L, whole_tc(is_complex != 0, false)) && whole_fits(L, whole_tc(is_complex != 0, true)))
+    return kCounterBytes;
   const DiagTile f = const_tile(M * N, L, is_complex != 0, false), b = const_tile(M * N, L, is_complex != 0, true);
   // counter, then fp64 look-back maps and states and glam partials, 4 words per lane and
   // super-chunk (complex128 when complex), for the larger of the forward / backward tilings
@@ -826,9 +991,22 @@ int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   if (M == 0 || L == 0 || N == 0) return TSF_OK;
   if (!lam || !v || !out) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (whole_fits(L, whole_tc(is_complex != 0, false))) {
+    const int64_t groups = (M * N + 63) / 64;
+    if (groups > INT32_MAX) return TSF_ERR_UNSUPPORTED;
+    if (is_complex)
+      hipLaunchKernelGGL((diag_whole_fwd<float2, whole_tc(true, false)>), dim3((unsigned)groups),
+                         whole_block(L, whole_tc(true, false)), 0, s, (const float2*)lam, (const float2*)v,
+                         (const float2*)x0, (float2*)out, (unsigned*)workspace, M * N, L, N);
+    else
+      hipLaunchKernelGGL((diag_whole_fwd<float, whole_tc(false, false)>), dim3((unsigned)groups),
+                         whole_block(L, whole_tc(false, false)), 0, s, (const float*)lam, (const float*)v,
+                         (const float*)x0, (float*)out, (unsigned*)workspace, M * N, L, N);
+    return tsf_launch_status();
+  }
   const DiagTile t = const_tile(M * N, L, is_complex != 0, false);
   if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   if (is_complex)
     diag_fwd_launch<float2, 16>(t, (const float2*)lam, (const float2*)v, (const float2*)x0, (float2*)out, ws, L, N, s);
@@ -856,6 +1034,21 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   }
   if (!g || !out || !gv) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
+  if (whole_fits(L, whole_tc(is_complex != 0, true))) {
+    const int64_t groups = (lanes + 63) / 64;
+    if (groups > INT32_MAX) return TSF_ERR_UNSUPPORTED;
+    if (is_complex)
+      hipLaunchKernelGGL((diag_whole_bwd<float2, whole_tc(true, true)>), dim3((unsigned)groups),
+                         whole_block(L, whole_tc(true, true)), 0, s, (const float2*)lam, (const float2*)g,
+                         (const float2*)out, (const float2*)x0, (float2*)gv, (float2*)glam, (float2*)gx0,
+                         (unsigned*)workspace, lanes, L, N);
+    else
+      hipLaunchKernelGGL((diag_whole_bwd<float, whole_tc(false, true)>), dim3((unsigned)groups),
+                         whole_block(L, whole_tc(false, true)), 0, s, (const float*)lam, (const float*)g,
+                         (const float*)out, (const float*)x0, (float*)gv, (float*)glam, (float*)gx0,
+                         (unsigned*)workspace, lanes, L, N);
+    return tsf_launch_status();
+  }
   const DiagTile t = const_tile(lanes, L, is_complex != 0, true);
   if (!grid_fits(t)) return TSF_ERR_UNSUPPORTED;
   char* ws = static_cast<char*>(workspace);
