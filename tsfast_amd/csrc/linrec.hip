@@ -44,28 +44,6 @@ constexpr int steps_per_chunk() {
   return kTileT / NS;
 }
 
-// x <- P x in fp64, each row's dot product summed as a pairwise tree (products of column pairs,
-// then pairwise adds), so a chain of steps waits about 2 + log2(NS / 2) operations per step
-// instead of NS.
-template <int NS>
-TSF_DEV void matvec_tree(const double (&P)[NS][NS], double (&x)[NS]) {
-  double y[NS];
-#pragma unroll
-  for (int r = 0; r < NS; ++r) {
-    double part[(NS + 1) / 2];
-#pragma unroll
-    for (int i = 0; i < NS / 2; ++i) part[i] = fma(P[r][2 * i], x[2 * i], P[r][2 * i + 1] * x[2 * i + 1]);
-    if constexpr (NS % 2 == 1) part[NS / 2] = P[r][NS - 1] * x[NS - 1];
-#pragma unroll
-    for (int w = 1; w < (NS + 1) / 2; w *= 2)
-#pragma unroll
-      for (int i = 0; i + w < (NS + 1) / 2; i += 2 * w) part[i] += part[i + w];
-    y[r] = part[0];
-  }
-#pragma unroll
-  for (int r = 0; r < NS; ++r) x[r] = y[r];
-}
-
 // Transfer matrices per lane: Mc = P^S and Ms = P^(S K) with P = A (forward) or A^T (adjoint),
 // one thread per (lane, column c): column c is P applied S K times to the unit vector e_c, in
 // fp64. (Repeated squaring would compound rounding errors through the transient growth of
@@ -90,7 +68,16 @@ __global__ void __launch_bounds__(256) linrec_transfer(const float* __restrict__
   double* mc = Mc + lane * NS * NS + col;
   double* ms = Ms + lane * NS * NS + col;
   for (int step = 1; step <= S * K; ++step) {
-    matvec_tree<NS>(P, x);
+    double y[NS];
+#pragma unroll
+    for (int r = 0; r < NS; ++r) {
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < NS; ++c) acc = fma(P[r][c], x[c], acc);
+      y[r] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < NS; ++r) x[r] = y[r];
     if (step == S)
 #pragma unroll
       for (int r = 0; r < NS; ++r) mc[r * NS] = x[r];
@@ -644,7 +631,18 @@ __global__ void __launch_bounds__(64) lw_power(const float* __restrict__ A, doub
 #pragma unroll
     for (int c = 0; c < NS; ++c) P[r][c] = (double)(transpose ? a[c * NS + r] : a[r * NS + c]);
   }
-  for (int step = 0; step < e; ++step) matvec_tree<NS>(P, x);
+  for (int step = 0; step < e; ++step) {
+    double y[NS];
+#pragma unroll
+    for (int r = 0; r < NS; ++r) {
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < NS; ++c) acc = fma(P[r][c], x[c], acc);
+      y[r] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < NS; ++r) x[r] = y[r];
+  }
 #pragma unroll
   for (int r = 0; r < NS; ++r) M[lane * NS * NS + r * NS + col] = x[r];
 }
