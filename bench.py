@@ -23,7 +23,8 @@ companion-matrix doubling scan and its adjoint (oracle/torch_reference.py, a res
 reference CPU path of dynonet/core.py:23-88) for config 4.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 3] [--io bf16|fp32] [--no-cpu]
-       (or one of --selective, --conv, --gblock, --linrec for the other rows' workloads)
+       (or one of --selective, --conv, --gblock, --linrec, --projected, --adjoint for the other
+       rows' workloads)
 """
 
 from __future__ import annotations
@@ -784,6 +785,44 @@ def run_linrec(args, line):
     return ms, fwd_b + bwd_b, kernels, cpu
 
 
+def run_adjoint(args, line):
+    """The chunked NeuralStateSpace adjoint scan (ssm/backend_metal.py:446-479, kernels :285-357)
+    at an NSS-sized backward with the reference's own chunking: B 16 (its largest scan batch),
+    L 4096, n 32 (its largest scan state), C = min(ceil(512 / B), L // 64) chunks. The chunk
+    summaries run on the fp64 matrix cores, so the roofline is fp64 MFMA (78.6 TFLOP/s)."""
+    import torch
+
+    from tsfast_amd.ssm import adjoint_hip
+
+    B, L, n = 16, 4096, 32
+    C = max(1, min(-(-512 // B), L // 64))
+    cl = -(-L // C)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    jt = torch.randn(B, L, n, n, device="cuda", generator=g) * (0.9 / n**0.5)
+    gout = torch.randn(B, L, n, device="cuda", generator=g)
+
+    def step(ev):
+        mark(ev)
+        adjoint_hip.run(jt, gout, cl)
+        mark(ev)
+
+    ms, (call_ms,) = time_steps(step, args.steps, args.warmup)
+    flops = 2 * B * (L - 1) * n * n * (n + 1)  # [P | s] <- A [P | s] per step
+    line.update(
+        metric="ms per call + achieved fp64 TFLOP/s, chunked NSS adjoint scan (ssm_bwd_summary + ssm_bwd_scan)",
+        unit="TFLOP/s",
+        config={"workload": f"chunked adjoint of gy_t = gout_t + jt[t+1] gy_t+1: batch {B}, L {L}, n {n}, "
+                            f"{C} chunks of {cl} steps (the reference's chunking), jt {B * L * n * n * 4 / 2**20:.0f} MiB",
+                "B": B, "L": L, "n": n, "chunks": C, "chunk_len": cl},
+        call_ms=round(call_ms, 4),
+        algorithmic_flops={"call": flops},
+        _mfma_peak_tflops=78.6,
+    )
+    line["dtype"] = "f64"  # fp32 inputs, fp64 summaries on the matrix cores
+    kernels = {"call": ("mas_summary + mas_carry (fp64 MFMA chunk summaries, sequential carry)", call_ms, flops)}
+    return ms, flops, kernels, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -801,6 +840,8 @@ def main():
                     help="measure the constant-matrix linear_recurrence on config 4's companion-matrix route")
     ap.add_argument("--projected", action="store_true",
                     help="measure the fused projected complex diagonal scan (LRU/S5 core) at config 2's shape")
+    ap.add_argument("--adjoint", action="store_true",
+                    help="measure the chunked NSS adjoint scan (n 32, the reference's chunking)")
     ap.add_argument("--order", type=int, default=3,
                     help="with --linrec: the denominator order n (state size 1..8; config 4 is 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
@@ -850,7 +891,7 @@ def main():
         "data": "synthetic",
     }
     runner = (run_conv if args.conv else run_selective if args.selective else run_gblock if args.gblock
-              else run_linrec if args.linrec else run_projected if args.projected
+              else run_linrec if args.linrec else run_projected if args.projected else run_adjoint if args.adjoint
               else {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config])
     ms, total_bytes, kernels, cpu = runner(args, line)
     mfma_peak = line.pop("_mfma_peak_tflops", None)

@@ -256,6 +256,20 @@ int tsfast_hip_projscan_bwd(int64_t B, int64_t L, int64_t H, int64_t N, int64_t 
                             float* g_w_re, float* g_w_im, void* g_lam, float* g_c_re, float* g_c_im, void* g_x0,
                             void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------------------------
+ * Chunked adjoint of a time-varying matrix recurrence (the sequence-parallel part of a
+ * NeuralStateSpace backward). Replaces the pair ssm_bwd_summary + ssm_bwd_scan
+ * (tsfast/models/architectures/ssm/backend_metal.py:285-357) as `backward` calls it (:466-476):
+ *   jt [B, L, n, n] float32 (per-step matrices A_t, row-major), gout [B, L, n] float32;
+ *   gy_t = gout_t + A_{t+1} gy_{t+1}, gy_{L-1} = gout_{L-1};
+ *   chunks of CL steps, C = ceil(L / CL); writes bnd [B, C + 1, n] float32, bnd[b, c] = gy at the
+ *   first step of chunk c, bnd[b, C] = 0.
+ * 1 <= n <= 32 (TSF_ERR_UNSUPPORTED above). Summaries in fp64 on the matrix cores; the workspace
+ * holds them ([B, C, n, n + 1] doubles). */
+int64_t tsfast_hip_mat_adjoint_workspace_bytes(int64_t B, int64_t L, int64_t n, int64_t CL);
+int tsfast_hip_mat_adjoint_bounds(int64_t B, int64_t L, int64_t n, int64_t CL, const float* jt, const float* gout,
+                                  float* bnd, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,7 +18,9 @@ diagonal one, delta -> 0 makes Mamba the identity map on the state, N = 1 reduce
 scalar recurrence); the G-block functions compose the FIR and all-pole restatements and are
 checked against autograd through the reference's grouped-conv1d formulation; the constant-matrix
 recurrence is checked against matrix-power closed forms, torch float64 autograd through a loop,
-and its diagonal and companion special cases (the diagonal scan and the all-pole filter).
+and its diagonal and companion special cases (the diagonal scan and the all-pole filter); the
+chunked matrix adjoint is checked against the step-by-step adjoint recurrence and its diagonal
+special case (the selective scan's adjoint).
 """
 
 from __future__ import annotations
@@ -46,6 +48,7 @@ __all__ = [
     "real_out_proj",
     "projscan_forward",
     "projscan_backward",
+    "mat_adjoint_bounds",
 ]
 
 
@@ -458,3 +461,40 @@ def projscan_backward(gy, g_xlast, u, W_re, W_im, lam, C_re, C_im, x, x0=None):
     g_C_re = np.einsum("blo,bln->on", gy, x.real)
     g_C_im = -np.einsum("blo,bln->on", gy, x.imag)
     return g_u, g_W_re, g_W_im, glam_rows.sum(0), g_C_re, g_C_im, gx0
+
+
+# --------------------------------------------------------------------------- NSS chunked adjoint
+def mat_adjoint_bounds(jt, gout, cl):
+    """Chunk boundaries of ``gy_t = gout_t + jt[t+1] gy_{t+1}`` (``gy_{L-1} = gout_{L-1}``).
+
+    Restates ``ssm_bwd_summary`` and ``ssm_bwd_scan``
+    (tsfast/models/architectures/ssm/backend_metal.py:285-357) with the chunking of ``backward``
+    (:466-476): chunk ``c`` covers steps ``[c cl, min((c + 1) cl, L))``; its summary ``(P, s)``
+    starts from ``(I, 0)`` and, right to left over its steps, becomes ``(A P, gout_t + A s)`` with
+    ``A = jt[t + 1]``, or ``(0, gout_t)`` at ``t = L - 1``; then ``v`` runs over the chunks from
+    the right from zero, ``v <- s_c + P_c v``, and ``bnd[:, c] = v``, ``bnd[:, C] = 0``.
+    Returns ``bnd [B, C + 1, n]`` in float64."""
+    jt, gout = _hi(jt), _hi(gout)
+    B, L, n = gout.shape
+    C = -(-L // int(cl)) if L > 0 else 0
+    pc = np.zeros((B, C, n, n))
+    sc = np.zeros((B, C, n))
+    for c in range(C):
+        t0, t1 = c * cl, min((c + 1) * cl, L)
+        P = np.broadcast_to(np.eye(n), (B, n, n)).copy()
+        sv = np.zeros((B, n))
+        for t in range(t1 - 1, t0 - 1, -1):
+            if t + 1 < L:
+                A = jt[:, t + 1]
+                P = A @ P
+                sv = gout[:, t] + np.einsum("bim,bm->bi", A, sv)
+            else:
+                P = np.zeros((B, n, n))
+                sv = gout[:, t].copy()
+        pc[:, c], sc[:, c] = P, sv
+    bnd = np.zeros((B, C + 1, n))
+    v = np.zeros((B, n))
+    for c in range(C - 1, -1, -1):
+        v = sc[:, c] + np.einsum("bim,bm->bi", pc[:, c], v)
+        bnd[:, c] = v
+    return bnd

@@ -777,3 +777,69 @@ def test_projscan_check_rejects_forward():
 )
 def test_projscan_check_rejects_backward(mutant):
     assert not check_projscan(O.projscan_forward, mutant)
+
+
+# ------------------------------------------------------------------------ NSS chunked adjoint
+def _adjoint_steps(jt, gout):
+    """The adjoint at every step by its definition, gy_t = gout_t + jt[t+1] gy_{t+1}."""
+    B, L, n = gout.shape
+    gy = np.zeros((B, L, n))
+    nxt = np.zeros((B, n))
+    for t in range(L - 1, -1, -1):
+        gy[:, t] = gout[:, t] + (np.einsum("bij,bj->bi", jt[:, t + 1], nxt) if t + 1 < L else 0.0)
+        nxt = gy[:, t]
+    return gy
+
+
+def check_mat_adjoint(fn):
+    """Boundaries against the step-by-step adjoint (gy at every chunk's first step, zero past the
+    end) on ragged chunkings, and the diagonal special case against the selective scan's adjoint
+    (G_t = g_t + a_{t+1} G_{t+1} with a_t the diagonal of jt[t])."""
+    rng = _rng(16)
+    for B, L, n, cl in ((2, 37, 3, 8), (1, 5, 4, 5), (3, 64, 2, 64), (2, 33, 5, 1), (1, 20, 1, 7), (2, 50, 6, 100)):
+        jt = rng.standard_normal((B, L, n, n)) * (0.9 / np.sqrt(n))
+        gout = rng.standard_normal((B, L, n))
+        C = -(-L // cl)
+        want = np.zeros((B, C + 1, n))
+        want[:, :C] = _adjoint_steps(jt, gout)[:, ::cl][:, :C]
+        got = np.asarray(fn(jt, gout, cl))
+        if got.shape != want.shape or O.rel_err(got, want) > TOL:
+            return False
+    B, L, n, cl = 2, 40, 4, 6
+    a = rng.uniform(0.2, 0.95, (B, L, n))
+    jt = np.zeros((B, L, n, n))
+    for i in range(n):
+        jt[:, :, i, i] = a[:, :, i]
+    gout = rng.standard_normal((B, L, n))
+    _, gv, _ = O.selective_backward(gout, a, np.zeros((B, L, n)))
+    got = np.asarray(fn(jt, gout, cl))
+    return O.rel_err(got[:, :-1], gv[:, ::cl]) <= TOL and not np.any(got[:, -1])
+
+
+def test_mat_adjoint_step_recurrence_and_diagonal_case():
+    assert check_mat_adjoint(O.mat_adjoint_bounds)
+
+
+def _mat_adjoint_transposed(jt, gout, cl):
+    return O.mat_adjoint_bounds(np.swapaxes(jt, -1, -2), gout, cl)
+
+
+def _mat_adjoint_current_step(jt, gout, cl):  # A_t instead of A_{t+1}
+    return O.mat_adjoint_bounds(np.roll(jt, 1, axis=1), gout, cl)
+
+
+def _mat_adjoint_chunk_end_dropped(jt, gout, cl):  # each chunk's last gout left out
+    g = np.array(gout, copy=True)
+    g[:, cl - 1 :: cl] = 0.0
+    return O.mat_adjoint_bounds(jt, g, cl)
+
+
+def _mat_adjoint_shifted(jt, gout, cl):  # the boundary of the next chunk
+    return np.roll(O.mat_adjoint_bounds(jt, gout, cl), -1, axis=1)
+
+
+@pytest.mark.parametrize(
+    "mutant", [_mat_adjoint_transposed, _mat_adjoint_current_step, _mat_adjoint_chunk_end_dropped, _mat_adjoint_shifted]
+)
+def test_mat_adjoint_check_rejects(mutant):
+    assert not check_mat_adjoint(mutant)

@@ -64,6 +64,8 @@ _SIGNATURES: dict[str, tuple[list, object]] = {
     "tsfast_hip_projscan_fwd": ([_i64] * 5 + [_ptr] * 11 + [_i64, _ptr], _int),
     "tsfast_hip_projscan_bwd_workspace_bytes": ([_i64] * 5, _i64),
     "tsfast_hip_projscan_bwd": ([_i64] * 5 + [_ptr] * 17 + [_i64, _ptr], _int),
+    "tsfast_hip_mat_adjoint_workspace_bytes": ([_i64] * 4, _i64),
+    "tsfast_hip_mat_adjoint_bounds": ([_i64] * 4 + [_ptr] * 4 + [_i64, _ptr], _int),
 }
 
 TSF_DTYPE_F32 = 0
