@@ -16,7 +16,8 @@
 // stream through LDS four steps at a time with coalesced loads, the next batch in flight while the
 // current one is used.
 // fp64 keeps a chunk's product of up to a few hundred matrices at fp64 rounding (fp32 inputs).
-// Carry kernel: one wave per row b, one lane per state row, the next chunk's summary prefetched.
+// Carry kernel: one workgroup per row b, four lanes per state row, the next eight chunks' summaries
+// in flight.
 #include <algorithm>
 
 #include "common.h"
@@ -64,13 +65,26 @@ __global__ void __launch_bounds__(64 * NBC) mas_summary(const float* __restrict_
   // instantiation the host picks.
   const int fi = threadIdx.x / n, fr = threadIdx.x - fi * n;
   const bool mover = fi < kMasBatch;
+  const bool vec4 = (n & 3) == 0 && (reinterpret_cast<uintptr_t>(jt) & 15) == 0;
   float reg[R], greg = 0.0f;
   auto fetch = [&](int64_t k) __attribute__((always_inline)) {
     const int64_t t = t1 - 1 - kMasBatch * k - fi;
     const bool ok = mover && t >= t0;
     const float* row = jt + ((b * L + t + 1) * n + fr) * n;
+    const bool have = ok && t + 1 < L;
+    if (vec4) {  // n % 4 == 0 and 16-byte aligned rows: whole float4s
 #pragma unroll
-    for (int q = 0; q < R; ++q) reg[q] = (ok && t + 1 < L && q < n) ? row[q] : 0.0f;
+      for (int q = 0; q < R; q += 4) {
+        const float4 v = (have && q < n) ? *reinterpret_cast<const float4*>(row + q) : make_float4(0.f, 0.f, 0.f, 0.f);
+        reg[q] = v.x;
+        reg[q + 1] = v.y;
+        reg[q + 2] = v.z;
+        reg[q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < R; ++q) reg[q] = (have && q < n) ? row[q] : 0.0f;
+    }
     greg = ok ? gout[(b * L + t) * n + fr] : 0.0f;
   };
   auto stash = [&](int buf) __attribute__((always_inline)) {
@@ -133,40 +147,50 @@ __global__ void __launch_bounds__(64 * NBC) mas_summary(const float* __restrict_
   }
 }
 
-// bnd[b, c] = s_c + P_c bnd[b, c + 1] from the right, bnd[b, C] = 0. One wave per row b; lane i
-// owns state row i and holds the next chunk's row of P in registers while it folds the current.
+// bnd[b, c] = s_c + P_c bnd[b, c + 1] from the right, bnd[b, C] = 0. One workgroup per row b of
+// 4 NP threads: four lanes per state row i, each summing NP / 4 columns of P_c's row (the four
+// partials meet through two lane swaps). A lane keeps the row parts of the next kRing chunks in a
+// register ring, so each chunk's loads are issued kRing chunks before they are needed.
+constexpr int kRing = 8;
 template <int NP>
-__global__ void __launch_bounds__(64) mas_carry(const double* __restrict__ pc, const double* __restrict__ sc,
-                                                float* __restrict__ bnd, int n, int64_t C) {
+__global__ void __launch_bounds__(4 * NP) mas_carry(const double* __restrict__ pc, const double* __restrict__ sc,
+                                                    float* __restrict__ bnd, int n, int64_t C) {
+  constexpr int CP = NP / 4;
   __shared__ double s_v[2][NP];
-  const int i = threadIdx.x;
+  const int tid = threadIdx.x, i = tid >> 2, h = tid & 3;
   const int64_t b = blockIdx.x;
   const bool live = i < n;
-  if (i < NP) s_v[0][i] = 0.0;
-  if (live) bnd[(b * (C + 1) + C) * n + i] = 0.0f;
-  __syncthreads();
-  double row[NP], s = 0.0;
-  auto load = [&](int64_t c, double (&dst)[NP], double& sd) __attribute__((always_inline)) {
-    const double* p = pc + ((b * C + c) * n + (live ? i : 0)) * n;
+  if (tid < NP) s_v[0][tid] = 0.0;
+  if (h == 0 && live) bnd[(b * (C + 1) + C) * n + i] = 0.0f;
+  double ring[kRing][CP], sring[kRing];
+  auto load = [&](int64_t c, int slot) __attribute__((always_inline)) {
+    const double* p = pc + ((b * C + c) * n + (live ? i : 0)) * n + h * CP;
 #pragma unroll
-    for (int m = 0; m < NP; ++m) dst[m] = (live && m < n) ? p[m] : 0.0;
-    sd = live ? sc[(b * C + c) * n + i] : 0.0;
+    for (int m = 0; m < CP; ++m) ring[slot][m] = (live && c >= 0 && h * CP + m < n) ? p[m] : 0.0;
+    sring[slot] = (live && h == 0 && c >= 0) ? sc[(b * C + c) * n + i] : 0.0;
   };
-  double nrow[NP], ns = 0.0;
-  if (C > 0) load(C - 1, nrow, ns);
+#pragma unroll
+  for (int d = 0; d < kRing; ++d) load(C - 1 - d, d);
+  __syncthreads();
   int cur = 0;
-  for (int64_t c = C - 1; c >= 0; --c) {
+  for (int64_t c0 = C - 1; c0 >= 0; c0 -= kRing) {
 #pragma unroll
-    for (int m = 0; m < NP; ++m) row[m] = nrow[m];
-    s = ns;
-    if (c > 0) load(c - 1, nrow, ns);
-    double v = s;
+    for (int d = 0; d < kRing; ++d) {
+      const int64_t c = c0 - d;
+      if (c < 0) break;  // uniform over the workgroup
+      double part = sring[d];
 #pragma unroll
-    for (int m = 0; m < NP; ++m) v = fma(row[m], s_v[cur][m], v);
-    if (i < NP) s_v[cur ^ 1][i] = live ? v : 0.0;
-    if (live) bnd[(b * (C + 1) + c) * n + i] = (float)v;
-    __syncthreads();
-    cur ^= 1;
+      for (int m = 0; m < CP; ++m) part = fma(ring[d][m], s_v[cur][h * CP + m], part);
+      part += __shfl_xor(part, 1);
+      part += __shfl_xor(part, 2);
+      load(c - kRing, d);  // the ring slot now holds the chunk kRing further left
+      if (h == 0 && live) {
+        s_v[cur ^ 1][i] = part;
+        bnd[(b * (C + 1) + c) * n + i] = (float)part;
+      }
+      __syncthreads();
+      cur ^= 1;
+    }
   }
 }
 
@@ -229,7 +253,7 @@ int tsfast_hip_mat_adjoint_bounds(int64_t B, int64_t L, int64_t n, int64_t CL, c
     hipLaunchKernelGGL(mas_carry<16>, dim3((unsigned)B), dim3(64), 0, s, (const double*)pc, (const double*)sc, bnd, nn,
                        C);
   else
-    hipLaunchKernelGGL(mas_carry<32>, dim3((unsigned)B), dim3(64), 0, s, (const double*)pc, (const double*)sc, bnd, nn,
+    hipLaunchKernelGGL(mas_carry<32>, dim3((unsigned)B), dim3(128), 0, s, (const double*)pc, (const double*)sc, bnd, nn,
                        C);
   return tsf_launch_status();
 }
