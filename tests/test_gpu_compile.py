@@ -151,3 +151,20 @@ def test_compile_linear_dynamical_operator_with_state(gpu):
         return y + 1e-2 * (state["x"].sum() + state["u"].sum())
 
     _compare(section, leaves)
+
+
+def test_compile_projected_diagonal_recurrence(gpu):
+    """The fused LRU/S5 layer core (tsfast_hip::projected_scan_train / _bwd) under fullgraph."""
+    g = torch.Generator().manual_seed(9)
+    B, L, H, N, O = 2, 400, 6, 40, 5
+    leaves = [t.to(gpu).requires_grad_() for t in (
+        torch.randn(B, L, H, generator=g), torch.randn(N, H, generator=g) / H**0.5, torch.randn(N, H, generator=g) / H**0.5,
+        torch.polar(torch.rand(N, generator=g) * 0.099 + 0.9, torch.rand(N, generator=g) * 0.3),
+        torch.randn(O, N, generator=g) / N**0.5, torch.randn(O, N, generator=g) / N**0.5,
+        torch.randn(B, N, dtype=torch.complex64, generator=g))]
+
+    def fn(u, W_re, W_im, lam, C_re, C_im, x0):
+        y, x_last = scan.projected_diagonal_recurrence(u, W_re, W_im, lam, C_re, C_im, x0)
+        return y + torch.view_as_real(x_last).sum()
+
+    _compare(fn, leaves)
