@@ -36,6 +36,10 @@ _DIAG_SHAPES = [
     ((2, 1025, 64), (64,)),
     ((2, 512, 32), (32,)),
     ((3, 256, 70), (70,)),
+    # whole-sequence lane groups: 64 lanes once they fill 256 workgroups (16384 lanes), 16 below;
+    # 500 lanes = 32 groups of 16 (XCD-contiguous group order) with a ragged last group
+    ((64, 200, 256), (256,)),
+    ((5, 200, 100), (100,)),
 ]
 
 

@@ -27,6 +27,7 @@ namespace {
 
 // All kernels load fp32 (or complex64) and carry the recurrence in fp64 (complex128): W below.
 constexpr int kMaxWaves = 16;
+constexpr unsigned kXcds = 8;  // XCDs of an MI355X, each with its own L2
 
 // ---------------------------------------------------------------- affine maps and look-back
 template <typename W>
@@ -407,20 +408,29 @@ __global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, cons
 }
 
 // ---------------------------------------------------------------- whole-sequence tiles
-// When K <= 16 chunks of TC steps cover the sequence, one workgroup of K waves takes a 64-lane
-// group's whole sequence (wave k the k-th chunk): no look-back, no workspace words and no reset
-// launch, so each direction is a single kernel. After one barrier every wave composes the
-// summaries of the chunks before it (forward) or after it (backward) from LDS into its entering
-// state, at most K - 1 fp64 folds.
-template <typename T, int TC>
-__global__ void __launch_bounds__(1024) diag_whole_fwd(const T* __restrict__ lam, const T* __restrict__ v,
-                                                       const T* __restrict__ x0, T* __restrict__ out,
-                                                       unsigned* __restrict__ ws_head, int64_t lanes, int64_t L,
-                                                       int64_t N) {
+// When K <= 16 chunks of TC steps cover the sequence, one workgroup of K x LG threads takes an
+// LG-lane group's whole sequence (threads k*LG .. k*LG + LG-1 the k-th chunk): no look-back, no
+// workspace words and no reset launch, so each direction is a single kernel. After one barrier
+// every chunk composes the summaries of the chunks before it (forward) or after it (backward)
+// from LDS into its entering state, at most K - 1 fp64 folds. Narrow groups (LG = 16) give a
+// small scan more workgroups than there are lane groups of 64; whole_group() hands each XCD a
+// contiguous range of groups, so the groups whose rows share a 128-byte line share an L2.
+TSF_DEV int64_t whole_group() {
+  const unsigned total = gridDim.x;
+  unsigned lin = blockIdx.x;
+  if (total % kXcds == 0) lin = (lin % kXcds) * (total / kXcds) + lin / kXcds;
+  return lin;
+}
+
+template <typename T, int TC, int LG>
+__global__ void __launch_bounds__(LG * kMaxWaves) diag_whole_fwd(const T* __restrict__ lam, const T* __restrict__ v,
+                                                                 const T* __restrict__ x0, T* __restrict__ out,
+                                                                 unsigned* __restrict__ ws_head, int64_t lanes,
+                                                                 int64_t L, int64_t N) {
   using W = typename Wide<T>::type;
-  __shared__ W s_e[kMaxWaves][64];
-  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int64_t lane = (int64_t)blockIdx.x * 64 + lid;
+  __shared__ W s_e[kMaxWaves][LG];
+  const int lid = threadIdx.x % LG, k = threadIdx.x / LG;
+  const int64_t lane = whole_group() * LG + lid;
   const bool live = lane < lanes;
   const int64_t t0 = (int64_t)k * TC;
   const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
@@ -470,36 +480,60 @@ __global__ void __launch_bounds__(1024) diag_whole_fwd(const T* __restrict__ lam
   }
 }
 
-// Backward of the whole-sequence tile: each wave summarises its chunk's adjoint from a zero state
-// (f = G at the chunk's first step), then re-runs it half a chunk at a time from the G entering
-// from the right, writing gv and accumulating glam = sum_t G_t conj(x_{t-1}). The re-run reloads
-// its g values (L2 hits) together with x, through a pointer the compiler cannot see through, so
-// at most one chunk of values is live at a time; the K per-chunk glam sums are added in order.
-template <typename T, int TC>
-__global__ void __launch_bounds__(1024) diag_whole_bwd(const T* __restrict__ lam, const T* __restrict__ g,
-                                                       const T* __restrict__ out, const T* __restrict__ x0,
-                                                       T* __restrict__ gv, T* __restrict__ glam, T* __restrict__ gx0,
-                                                       unsigned* __restrict__ ws_head, int64_t lanes, int64_t L,
-                                                       int64_t N) {
+// Backward of the whole-sequence tile: each chunk summarises its adjoint from a zero state
+// (f = G at the chunk's first step), then re-runs it from the G entering from the right, writing
+// gv and accumulating glam = sum_t G_t conj(x_{t-1}). With 64-lane groups (16 waves, 128 VGPRs)
+// the re-run goes half a chunk at a time and reloads its g values (L2 hits) together with x,
+// through a pointer the compiler cannot see through, so at most one chunk of values is live at
+// a time; narrower groups have the registers to load the chunk's g and x values together before
+// the barrier (one round trip to memory). The K per-chunk glam sums are added in order.
+template <typename T, int TC, int LG>
+__global__ void __launch_bounds__(LG * kMaxWaves) diag_whole_bwd(const T* __restrict__ lam, const T* __restrict__ g,
+                                                                 const T* __restrict__ out, const T* __restrict__ x0,
+                                                                 T* __restrict__ gv, T* __restrict__ glam,
+                                                                 T* __restrict__ gx0, unsigned* __restrict__ ws_head,
+                                                                 int64_t lanes, int64_t L, int64_t N) {
   using W = typename Wide<T>::type;
   constexpr int H2 = TC / 2;
-  __shared__ W s_f[kMaxWaves][64];
-  __shared__ W s_acc[kMaxWaves][64];
-  const int lid = threadIdx.x & 63, k = threadIdx.x >> 6, K = blockDim.x >> 6;
-  const int64_t lane = (int64_t)blockIdx.x * 64 + lid;
+  constexpr bool kKeep = LG < 64;
+  __shared__ W s_f[kMaxWaves][LG];
+  __shared__ W s_acc[kMaxWaves][LG];
+  const int lid = threadIdx.x % LG, k = threadIdx.x / LG, K = blockDim.x / LG;
+  const int64_t lane = whole_group() * LG + lid;
   const bool live = lane < lanes;
   const int64_t t0 = (int64_t)k * TC;
   const int len = (L - t0) >= TC ? TC : (L - t0) > 0 ? (int)(L - t0) : 0;
   if (blockIdx.x == 0 && threadIdx.x == 0) ws_head[kErrWord] = 0;  // no look-back: nothing can give up
   W ac = Num<W>::zero(), f = Num<W>::zero();
   int64_t base = 0;
+  T gb[TC];
+  T xb[kKeep ? TC : 1];  // narrow groups: x_{t-1} of the whole chunk, loaded with g
   if (live) {
     ac = Num<W>::conj(Wide<T>::up(lam[lane]));
     const int64_t m = lane / N, n = lane - m * N;
     base = (m * L + t0) * N + n;
     const T* gp = g + base;
-    T gb[TC];
-    if (len == TC) {
+    if (kKeep) {
+      const T* xp = out + base;
+      if (len == TC && t0 > 0) {
+#pragma unroll
+        for (int i = 0; i < TC; ++i) {
+          gb[i] = gp[i * N];
+          xb[i] = xp[(i - 1) * N];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < TC; ++i) {  // clamped into the chunk, branch-free
+          const int ii = i < len ? i : len - 1;
+          gb[i] = gp[ii * N];
+          xb[i] = xp[(t0 + ii > 0 ? ii - 1 : 0) * N];
+        }
+        if (t0 == 0) xb[0] = x0 ? x0[lane] : T{};
+      }
+#pragma unroll
+      for (int i = TC - 1; i >= 0; --i)
+        if (len == TC || i < len) f = Num<W>::fma(ac, f, Wide<T>::up(gb[i]));
+    } else if (len == TC) {
 #pragma unroll
       for (int i = 0; i < TC; ++i) gb[i] = gp[i * N];
 #pragma unroll
@@ -520,34 +554,44 @@ __global__ void __launch_bounds__(1024) diag_whole_bwd(const T* __restrict__ lam
     W G = Num<W>::zero();       // G entering the chunk from the right
     for (int j = K - 1; j > k; --j) G = Num<W>::fma(Pc, G, s_f[j][lid]);
     T* gvp = gv + base;
+    if (kKeep) {
 #pragma unroll
-    for (int h = 1; h >= 0; --h) {
-      const T* gp = g + base;
-      const T* xp = out + base;
-      asm volatile("" : "+v"(gp), "+v"(xp));
-      T gh[H2], xh[H2];  // g_t and x_{t-1} (x0, or zero without it, before the first step)
-      if (len == TC && t0 > 0) {
-#pragma unroll
-        for (int i = 0; i < H2; ++i) {
-          gh[i] = gp[(h * H2 + i) * N];
-          xh[i] = xp[(h * H2 + i - 1) * N];
+      for (int i = TC - 1; i >= 0; --i)
+        if (i < len) {
+          G = Num<W>::fma(ac, G, Wide<T>::up(gb[i]));
+          gvp[i * N] = Wide<T>::down(G);
+          acc = Num<W>::fma(G, Num<W>::conj(Wide<T>::up(xb[i])), acc);
         }
-      } else {
+    } else {
 #pragma unroll
-        for (int i = 0; i < H2; ++i) {  // clamped into the chunk, branch-free
-          const int ii = h * H2 + i < len ? h * H2 + i : len - 1;
-          gh[i] = gp[ii * N];
-          xh[i] = xp[(t0 + ii > 0 ? ii - 1 : 0) * N];
+      for (int h = 1; h >= 0; --h) {
+        const T* gp = g + base;
+        const T* xp = out + base;
+        asm volatile("" : "+v"(gp), "+v"(xp));
+        T gh[H2], xh[H2];  // g_t and x_{t-1} (x0, or zero without it, before the first step)
+        if (len == TC && t0 > 0) {
+#pragma unroll
+          for (int i = 0; i < H2; ++i) {
+            gh[i] = gp[(h * H2 + i) * N];
+            xh[i] = xp[(h * H2 + i - 1) * N];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < H2; ++i) {  // clamped into the chunk, branch-free
+            const int ii = h * H2 + i < len ? h * H2 + i : len - 1;
+            gh[i] = gp[ii * N];
+            xh[i] = xp[(t0 + ii > 0 ? ii - 1 : 0) * N];
+          }
+          if (t0 == 0 && h == 0) xh[0] = x0 ? x0[lane] : T{};
         }
-        if (t0 == 0 && h == 0) xh[0] = x0 ? x0[lane] : T{};
-      }
 #pragma unroll
-      for (int i = H2 - 1; i >= 0; --i) {
-        const int ii = h * H2 + i;
-        if (ii < len) {
-          G = Num<W>::fma(ac, G, Wide<T>::up(gh[i]));
-          gvp[ii * N] = Wide<T>::down(G);
-          acc = Num<W>::fma(G, Num<W>::conj(Wide<T>::up(xh[i])), acc);
+        for (int i = H2 - 1; i >= 0; --i) {
+          const int ii = h * H2 + i;
+          if (ii < len) {
+            G = Num<W>::fma(ac, G, Wide<T>::up(gh[i]));
+            gvp[ii * N] = Wide<T>::down(G);
+            acc = Num<W>::fma(G, Num<W>::conj(Wide<T>::up(xh[i])), acc);
+          }
         }
       }
     }
@@ -874,7 +918,38 @@ unsigned persistent_grid(const DiagTile& t, F kern, int* cache) {
 // such chunks cover the sequence.
 constexpr int whole_tc(bool cplx, bool bwd) { return cplx ? (bwd ? 16 : 32) : 64; }
 inline bool whole_fits(int64_t L, int tc) { return L <= (int64_t)kMaxWaves * tc; }
-inline dim3 whole_block(int64_t L, int tc) { return dim3((unsigned)(64 * ((L + tc - 1) / tc))); }
+inline dim3 whole_block(int64_t L, int tc, int lg) { return dim3((unsigned)(lg * ((L + tc - 1) / tc))); }
+// Lanes per whole-sequence group: 64 (256-byte row segments of fp32) when that already gives
+// every CU a workgroup, else 16 (four times the workgroups; 64-byte segments, paired in L2).
+inline int whole_lg(int64_t lanes) {
+  return (lanes + 63) / 64 >= 256 ? 64 : 16;
+}
+
+template <typename T, int TC>
+void whole_fwd_launch(int64_t lanes, int64_t L, int64_t N, const T* lam, const T* v, const T* x0, T* out,
+                      unsigned* ws, hipStream_t s) {
+  const int lg = whole_lg(lanes);
+  const unsigned groups = (unsigned)((lanes + lg - 1) / lg);
+  if (lg == 64)
+    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 64>), dim3(groups), whole_block(L, TC, 64), 0, s, lam, v, x0, out, ws,
+                       lanes, L, N);
+  else
+    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 16>), dim3(groups), whole_block(L, TC, 16), 0, s, lam, v, x0, out, ws,
+                       lanes, L, N);
+}
+
+template <typename T, int TC>
+void whole_bwd_launch(int64_t lanes, int64_t L, int64_t N, const T* lam, const T* g, const T* out, const T* x0,
+                      T* gv, T* glam, T* gx0, unsigned* ws, hipStream_t s) {
+  const int lg = whole_lg(lanes);
+  const unsigned groups = (unsigned)((lanes + lg - 1) / lg);
+  if (lg == 64)
+    hipLaunchKernelGGL((diag_whole_bwd<T, TC, 64>), dim3(groups), whole_block(L, TC, 64), 0, s, lam, g, out, x0, gv,
+                       glam, gx0, ws, lanes, L, N);
+  else
+    hipLaunchKernelGGL((diag_whole_bwd<T, TC, 16>), dim3(groups), whole_block(L, TC, 16), 0, s, lam, g, out, x0, gv,
+                       glam, gx0, ws, lanes, L, N);
+}
 
 template <typename T, int TC>
 void diag_fwd_launch(const DiagTile& t, const T* lam, const T* v, const T* x0, T* out, char* ws, int64_t L, int64_t N,
@@ -993,16 +1068,13 @@ int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (whole_fits(L, whole_tc(is_complex != 0, false))) {
-    const int64_t groups = (M * N + 63) / 64;
-    if (groups > INT32_MAX) return TSF_ERR_UNSUPPORTED;
+    if ((M * N + 15) / 16 > INT32_MAX) return TSF_ERR_UNSUPPORTED;
     if (is_complex)
-      hipLaunchKernelGGL((diag_whole_fwd<float2, whole_tc(true, false)>), dim3((unsigned)groups),
-                         whole_block(L, whole_tc(true, false)), 0, s, (const float2*)lam, (const float2*)v,
-                         (const float2*)x0, (float2*)out, (unsigned*)workspace, M * N, L, N);
+      whole_fwd_launch<float2, whole_tc(true, false)>(M * N, L, N, (const float2*)lam, (const float2*)v,
+                                                      (const float2*)x0, (float2*)out, (unsigned*)workspace, s);
     else
-      hipLaunchKernelGGL((diag_whole_fwd<float, whole_tc(false, false)>), dim3((unsigned)groups),
-                         whole_block(L, whole_tc(false, false)), 0, s, (const float*)lam, (const float*)v,
-                         (const float*)x0, (float*)out, (unsigned*)workspace, M * N, L, N);
+      whole_fwd_launch<float, whole_tc(false, false)>(M * N, L, N, (const float*)lam, (const float*)v,
+                                                      (const float*)x0, (float*)out, (unsigned*)workspace, s);
     return tsf_launch_status();
   }
   const DiagTile t = const_tile(M * N, L, is_complex != 0, false);
@@ -1035,18 +1107,15 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   if (!g || !out || !gv) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
   if (whole_fits(L, whole_tc(is_complex != 0, true))) {
-    const int64_t groups = (lanes + 63) / 64;
-    if (groups > INT32_MAX) return TSF_ERR_UNSUPPORTED;
+    if ((lanes + 15) / 16 > INT32_MAX) return TSF_ERR_UNSUPPORTED;
     if (is_complex)
-      hipLaunchKernelGGL((diag_whole_bwd<float2, whole_tc(true, true)>), dim3((unsigned)groups),
-                         whole_block(L, whole_tc(true, true)), 0, s, (const float2*)lam, (const float2*)g,
-                         (const float2*)out, (const float2*)x0, (float2*)gv, (float2*)glam, (float2*)gx0,
-                         (unsigned*)workspace, lanes, L, N);
+      whole_bwd_launch<float2, whole_tc(true, true)>(lanes, L, N, (const float2*)lam, (const float2*)g,
+                                                     (const float2*)out, (const float2*)x0, (float2*)gv,
+                                                     (float2*)glam, (float2*)gx0, (unsigned*)workspace, s);
     else
-      hipLaunchKernelGGL((diag_whole_bwd<float, whole_tc(false, true)>), dim3((unsigned)groups),
-                         whole_block(L, whole_tc(false, true)), 0, s, (const float*)lam, (const float*)g,
-                         (const float*)out, (const float*)x0, (float*)gv, (float*)glam, (float*)gx0,
-                         (unsigned*)workspace, lanes, L, N);
+      whole_bwd_launch<float, whole_tc(false, true)>(lanes, L, N, (const float*)lam, (const float*)g,
+                                                     (const float*)out, (const float*)x0, (float*)gv, (float*)glam,
+                                                     (float*)gx0, (unsigned*)workspace, s);
     return tsf_launch_status();
   }
   const DiagTile t = const_tile(lanes, L, is_complex != 0, true);
