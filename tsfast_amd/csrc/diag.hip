@@ -408,7 +408,7 @@ __global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, cons
 }
 
 // ---------------------------------------------------------------- whole-sequence tiles
-// When K <= 16 chunks of TC steps cover the sequence, one workgroup of K x LG threads takes an
+// When K <= KMAX chunks of TC steps cover the sequence, one workgroup of K x LG threads takes an
 // LG-lane group's whole sequence (threads k*LG .. k*LG + LG-1 the k-th chunk): no look-back, no
 // workspace words and no reset launch, so each direction is a single kernel. After one barrier
 // every chunk composes the summaries of the chunks before it (forward) or after it (backward)
@@ -422,13 +422,13 @@ TSF_DEV int64_t whole_group() {
   return lin;
 }
 
-template <typename T, int TC, int LG>
-__global__ void __launch_bounds__(LG * kMaxWaves) diag_whole_fwd(const T* __restrict__ lam, const T* __restrict__ v,
+template <typename T, int TC, int LG, int KMAX>
+__global__ void __launch_bounds__(LG * KMAX) diag_whole_fwd(const T* __restrict__ lam, const T* __restrict__ v,
                                                                  const T* __restrict__ x0, T* __restrict__ out,
                                                                  unsigned* __restrict__ ws_head, int64_t lanes,
                                                                  int64_t L, int64_t N) {
   using W = typename Wide<T>::type;
-  __shared__ W s_e[kMaxWaves][LG];
+  __shared__ W s_e[KMAX][LG];
   const int lid = threadIdx.x % LG, k = threadIdx.x / LG;
   const int64_t lane = whole_group() * LG + lid;
   const bool live = lane < lanes;
@@ -487,17 +487,17 @@ __global__ void __launch_bounds__(LG * kMaxWaves) diag_whole_fwd(const T* __rest
 // through a pointer the compiler cannot see through, so at most one chunk of values is live at
 // a time; narrower groups have the registers to load the chunk's g and x values together before
 // the barrier (one round trip to memory). The K per-chunk glam sums are added in order.
-template <typename T, int TC, int LG>
-__global__ void __launch_bounds__(LG * kMaxWaves) diag_whole_bwd(const T* __restrict__ lam, const T* __restrict__ g,
+template <typename T, int TC, int LG, int KMAX>
+__global__ void __launch_bounds__(LG * KMAX) diag_whole_bwd(const T* __restrict__ lam, const T* __restrict__ g,
                                                                  const T* __restrict__ out, const T* __restrict__ x0,
                                                                  T* __restrict__ gv, T* __restrict__ glam,
                                                                  T* __restrict__ gx0, unsigned* __restrict__ ws_head,
                                                                  int64_t lanes, int64_t L, int64_t N) {
   using W = typename Wide<T>::type;
   constexpr int H2 = TC / 2;
-  constexpr bool kKeep = LG < 64;
-  __shared__ W s_f[kMaxWaves][LG];
-  __shared__ W s_acc[kMaxWaves][LG];
+  constexpr bool kKeep = LG * KMAX <= 256;
+  __shared__ W s_f[KMAX][LG];
+  __shared__ W s_acc[KMAX][LG];
   const int lid = threadIdx.x % LG, k = threadIdx.x / LG, K = blockDim.x / LG;
   const int64_t lane = whole_group() * LG + lid;
   const bool live = lane < lanes;
@@ -914,41 +914,51 @@ unsigned persistent_grid(const DiagTile& t, F kern, int* cache) {
 }
 
 
-// Whole-sequence tiling (diag_whole_fwd / diag_whole_bwd): steps per wave, and whether K <= 16
-// such chunks cover the sequence.
+// Whole-sequence tiling (diag_whole_fwd / diag_whole_bwd): TC steps per chunk; lane groups of 64
+// (256-byte row segments of fp32) when they already give every CU a workgroup, else of 16 (four
+// times the workgroups; 64-byte segments, paired in L2). A workgroup holds up to 1024 threads:
+// 16 chunks of 64 lanes, or 64 chunks of 16 lanes (16 chunks when they cover the sequence, so
+// that 256 threads may keep a chunk's values in registers). Longer sequences take the look-back.
 constexpr int whole_tc(bool cplx, bool bwd) { return cplx ? (bwd ? 16 : 32) : 64; }
-inline bool whole_fits(int64_t L, int tc) { return L <= (int64_t)kMaxWaves * tc; }
-inline dim3 whole_block(int64_t L, int tc, int lg) { return dim3((unsigned)(lg * ((L + tc - 1) / tc))); }
-// Lanes per whole-sequence group: 64 (256-byte row segments of fp32) when that already gives
-// every CU a workgroup, else 16 (four times the workgroups; 64-byte segments, paired in L2).
-inline int whole_lg(int64_t lanes) {
-  return (lanes + 63) / 64 >= 256 ? 64 : 16;
+struct WholeTile {
+  int lg = 0, kmax = 0;  // kmax == 0: the sequence is too long for one workgroup
+};
+inline WholeTile whole_tile(int64_t lanes, int64_t L, int tc, bool bwd) {
+  const int64_t chunks = (L + tc - 1) / tc;
+  if ((lanes + 63) / 64 >= 256) return chunks <= 16 ? WholeTile{64, 16} : WholeTile{};
+  if (chunks <= 16) return {16, 16};
+  // 64 chunks of 16 lanes: forward only, and only while one round of workgroups covers the
+  // lanes (the backward of so long a chunk run reloads its values, slower than the look-back)
+  if (!bwd && chunks <= 64 && (lanes + 15) / 16 <= 256) return {16, 64};
+  return {};
+}
+inline bool whole_both(int64_t lanes, int64_t L, bool cplx) {
+  return whole_tile(lanes, L, whole_tc(cplx, false), false).kmax > 0 &&
+         whole_tile(lanes, L, whole_tc(cplx, true), true).kmax > 0;
 }
 
 template <typename T, int TC>
-void whole_fwd_launch(int64_t lanes, int64_t L, int64_t N, const T* lam, const T* v, const T* x0, T* out,
-                      unsigned* ws, hipStream_t s) {
-  const int lg = whole_lg(lanes);
-  const unsigned groups = (unsigned)((lanes + lg - 1) / lg);
-  if (lg == 64)
-    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 64>), dim3(groups), whole_block(L, TC, 64), 0, s, lam, v, x0, out, ws,
-                       lanes, L, N);
+void whole_fwd_launch(const WholeTile& w, int64_t lanes, int64_t L, int64_t N, const T* lam, const T* v, const T* x0,
+                      T* out, unsigned* ws, hipStream_t s) {
+  const dim3 grid((unsigned)((lanes + w.lg - 1) / w.lg)), block((unsigned)(w.lg * ((L + TC - 1) / TC)));
+  if (w.lg == 64)
+    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 64, 16>), grid, block, 0, s, lam, v, x0, out, ws, lanes, L, N);
+  else if (w.kmax == 16)
+    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 16, 16>), grid, block, 0, s, lam, v, x0, out, ws, lanes, L, N);
   else
-    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 16>), dim3(groups), whole_block(L, TC, 16), 0, s, lam, v, x0, out, ws,
-                       lanes, L, N);
+    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 16, 64>), grid, block, 0, s, lam, v, x0, out, ws, lanes, L, N);
 }
 
 template <typename T, int TC>
-void whole_bwd_launch(int64_t lanes, int64_t L, int64_t N, const T* lam, const T* g, const T* out, const T* x0,
-                      T* gv, T* glam, T* gx0, unsigned* ws, hipStream_t s) {
-  const int lg = whole_lg(lanes);
-  const unsigned groups = (unsigned)((lanes + lg - 1) / lg);
-  if (lg == 64)
-    hipLaunchKernelGGL((diag_whole_bwd<T, TC, 64>), dim3(groups), whole_block(L, TC, 64), 0, s, lam, g, out, x0, gv,
-                       glam, gx0, ws, lanes, L, N);
+void whole_bwd_launch(const WholeTile& w, int64_t lanes, int64_t L, int64_t N, const T* lam, const T* g, const T* out,
+                      const T* x0, T* gv, T* glam, T* gx0, unsigned* ws, hipStream_t s) {
+  const dim3 grid((unsigned)((lanes + w.lg - 1) / w.lg)), block((unsigned)(w.lg * ((L + TC - 1) / TC)));
+  if (w.lg == 64)
+    hipLaunchKernelGGL((diag_whole_bwd<T, TC, 64, 16>), grid, block, 0, s, lam, g, out, x0, gv, glam, gx0, ws, lanes,
+                       L, N);
   else
-    hipLaunchKernelGGL((diag_whole_bwd<T, TC, 16>), dim3(groups), whole_block(L, TC, 16), 0, s, lam, g, out, x0, gv,
-                       glam, gx0, ws, lanes, L, N);
+    hipLaunchKernelGGL((diag_whole_bwd<T, TC, 16, 16>), grid, block, 0, s, lam, g, out, x0, gv, glam, gx0, ws, lanes,
+                       L, N);
 }
 
 template <typename T, int TC>
@@ -1052,8 +1062,7 @@ extern "C" {
 
 int64_t tsfast_hip_diag_workspace_bytes(int64_t M, int64_t L, int64_t N, int is_complex) {
   // whole-sequence tiles in both directions: only the header (its look-back flag word) is used
-  if (whole_fits(L, whole_tc(is_complex != 0, false)) && whole_fits(L, whole_tc(is_complex != 0, true)))
-    return kCounterBytes;
+  if (whole_both(M * N, L, is_complex != 0)) return kCounterBytes;
   const DiagTile f = const_tile(M * N, L, is_complex != 0, false), b = const_tile(M * N, L, is_complex != 0, true);
   // counter, then fp64 look-back maps and states and glam partials, 4 words per lane and
   // super-chunk (complex128 when complex), for the larger of the forward / backward tilings
@@ -1067,13 +1076,14 @@ int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   if (!lam || !v || !out) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (whole_fits(L, whole_tc(is_complex != 0, false))) {
+  const WholeTile wf = whole_tile(M * N, L, whole_tc(is_complex != 0, false), false);
+  if (wf.kmax > 0) {
     if ((M * N + 15) / 16 > INT32_MAX) return TSF_ERR_UNSUPPORTED;
     if (is_complex)
-      whole_fwd_launch<float2, whole_tc(true, false)>(M * N, L, N, (const float2*)lam, (const float2*)v,
+      whole_fwd_launch<float2, whole_tc(true, false)>(wf, M * N, L, N, (const float2*)lam, (const float2*)v,
                                                       (const float2*)x0, (float2*)out, (unsigned*)workspace, s);
     else
-      whole_fwd_launch<float, whole_tc(false, false)>(M * N, L, N, (const float*)lam, (const float*)v,
+      whole_fwd_launch<float, whole_tc(false, false)>(wf, M * N, L, N, (const float*)lam, (const float*)v,
                                                       (const float*)x0, (float*)out, (unsigned*)workspace, s);
     return tsf_launch_status();
   }
@@ -1106,14 +1116,15 @@ int tsfast_hip_diag_bwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   }
   if (!g || !out || !gv) return TSF_ERR_ARG;
   if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
-  if (whole_fits(L, whole_tc(is_complex != 0, true))) {
+  const WholeTile wb = whole_tile(lanes, L, whole_tc(is_complex != 0, true), true);
+  if (wb.kmax > 0) {
     if ((lanes + 15) / 16 > INT32_MAX) return TSF_ERR_UNSUPPORTED;
     if (is_complex)
-      whole_bwd_launch<float2, whole_tc(true, true)>(lanes, L, N, (const float2*)lam, (const float2*)g,
+      whole_bwd_launch<float2, whole_tc(true, true)>(wb, lanes, L, N, (const float2*)lam, (const float2*)g,
                                                      (const float2*)out, (const float2*)x0, (float2*)gv,
                                                      (float2*)glam, (float2*)gx0, (unsigned*)workspace, s);
     else
-      whole_bwd_launch<float, whole_tc(false, true)>(lanes, L, N, (const float*)lam, (const float*)g,
+      whole_bwd_launch<float, whole_tc(false, true)>(wb, lanes, L, N, (const float*)lam, (const float*)g,
                                                      (const float*)out, (const float*)x0, (float*)gv, (float*)glam,
                                                      (float*)gx0, (unsigned*)workspace, s);
     return tsf_launch_status();
