@@ -158,9 +158,12 @@ TSF_DEV void companion_powers_col(const float* __restrict__ arow, double* __rest
     a[c] = (double)arow[c];
     x[c] = c == col ? 1.0 : 0.0;
   }
-  for (int step = 1; step <= 32 * K; ++step) {
-    companion_apply<NA>(x, a);
-    if (step == 32)
+  // 32-step blocks, unrolled: each step waits on one FMA (the newest state's term), and the
+  // others are scheduled around it
+  for (int blk = 0; blk < K; ++blk) {
+#pragma unroll
+    for (int step = 0; step < 32; ++step) companion_apply<NA>(x, a);
+    if (blk == 0)
 #pragma unroll
       for (int r = 0; r < NA; ++r) Mc_out[r * NA + col] = x[r];
   }
