@@ -67,18 +67,22 @@ __global__ void __launch_bounds__(256) linrec_transfer(const float* __restrict__
   }
   double* mc = Mc + lane * NS * NS + col;
   double* ms = Ms + lane * NS * NS + col;
-  for (int step = 1; step <= S * K; ++step) {
-    double y[NS];
+  // blocks of S steps, unrolled (no per-step branch; independent work scheduled around the chain)
+  for (int blk = 0; blk < K; ++blk) {
 #pragma unroll
-    for (int r = 0; r < NS; ++r) {
-      double acc = 0.0;
+    for (int step = 0; step < S; ++step) {
+      double y[NS];
 #pragma unroll
-      for (int c = 0; c < NS; ++c) acc = fma(P[r][c], x[c], acc);
-      y[r] = acc;
+      for (int r = 0; r < NS; ++r) {
+        double acc = 0.0;
+#pragma unroll
+        for (int c = 0; c < NS; ++c) acc = fma(P[r][c], x[c], acc);
+        y[r] = acc;
+      }
+#pragma unroll
+      for (int r = 0; r < NS; ++r) x[r] = y[r];
     }
-#pragma unroll
-    for (int r = 0; r < NS; ++r) x[r] = y[r];
-    if (step == S)
+    if (blk == 0)
 #pragma unroll
       for (int r = 0; r < NS; ++r) mc[r * NS] = x[r];
   }
@@ -631,6 +635,7 @@ __global__ void __launch_bounds__(64) lw_power(const float* __restrict__ A, doub
 #pragma unroll
     for (int c = 0; c < NS; ++c) P[r][c] = (double)(transpose ? a[c * NS + r] : a[r * NS + c]);
   }
+#pragma unroll 8
   for (int step = 0; step < e; ++step) {
     double y[NS];
 #pragma unroll
