@@ -90,14 +90,17 @@ TSF_DEV void fir(float (&w)[kTileT], const float (&uw)[kTileT + NBT - 1], const 
   }
 }
 
+// The coefficients of pair lid % P, the pair that lane l0 + lid holds in every tile (l0 a multiple
+// of 64 and I * O dividing 64): loaded once per workgroup. Lanes beyond the tensor see zero inputs,
+// so their coefficients do not matter.
 template <int NA, int NBT>
-TSF_DEV void load_coeffs(double (&av)[NA], float (&bk)[NBT], const float* __restrict__ bcoef,
-                         const float* __restrict__ acoef, const GbLane& g, int I, int nb) {
-  const int pair = g.o * I + g.j;  // [O, I, .] parameter layout
+TSF_DEV void load_pair_coeffs(double (&av)[NA], float (&bk)[NBT], const float* __restrict__ bcoef,
+                              const float* __restrict__ acoef, int lid, int I, int O, int nb) {
+  const int p = lid % (I * O), pair = (p % O) * I + p / O;  // [O, I, .] parameter layout
 #pragma unroll
-  for (int q = 0; q < NA; ++q) av[q] = g.live ? (double)acoef[pair * NA + q] : 0.0;
+  for (int q = 0; q < NA; ++q) av[q] = (double)acoef[pair * NA + q];
 #pragma unroll
-  for (int k = 0; k < NBT; ++k) bk[k] = (g.live && k < nb) ? bcoef[pair * nb + k] : 0.0f;
+  for (int k = 0; k < NBT; ++k) bk[k] = k < nb ? bcoef[pair * nb + k] : 0.0f;
 }
 
 // Transfer matrices per lane from its pair's coefficients a [O, I, NA] (lane = b * P + j * O + o).
@@ -131,6 +134,11 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
   const int P = I * O, R = kTile / P;
   const int64_t lanes = B * P;
   const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
+  // the pair's coefficients and transfer matrices are the same in every tile (load_pair_coeffs)
+  double av[NA];
+  float bk[NBT];
+  load_pair_coeffs<NA, NBT>(av, bk, bcoef, acoef, lid, I, O, nb);
+  if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, 0, lanes);
   if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
   __syncthreads();
   for (int buf = 0;; buf ^= 1) {
@@ -143,9 +151,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
     const bool live = g.live;
     const int64_t t0 = sc * SL + (int64_t)k * kTileT;
     const int n = (L - t0) >= kTileT ? kTileT : (L - t0) > 0 ? (int)(L - t0) : 0;
-    double av[NA], s[NA];
-    float bk[NBT];
-    load_coeffs<NA, NBT>(av, bk, bcoef, acoef, g, I, nb);
+    double s[NA];
 #pragma unroll
     for (int q = 0; q < NA; ++q) s[q] = 0.0;
     float xb[kTileT];
@@ -162,7 +168,6 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
           if (i < n) step<NA>(av, s, (double)xb[i]);
       }
     }
-    if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, l0, lanes);
     double* vk = vec_area<NA>(s_lds, k) + lid * NA;
 #pragma unroll
     for (int q = 0; q < NA; ++q) vk[q] = s[q];
@@ -278,10 +283,20 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
   __shared__ int s_any;
   __shared__ unsigned s_tile[2];
   __shared__ double s_mat[MatStage<NA>::kDoubles];
+  // each wave's u window, kept from the forward recompute for the sweep's grad b (NBT <= 8: 80 KB)
+  constexpr int kUW = kTileT + NBT - 1;
+  constexpr bool kStashU = NBT <= 8;
+  __shared__ float s_uw[kStashU ? kLbWaves : 1][kStashU ? 64 : 1][kStashU ? kUW : 1];
+  __shared__ double s_st[64][NA];  // the super-chunk's saved entering state, prefetched by wave 0
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int P = I * O, R = kTile / P;
   const int64_t lanes = B * P;
   const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
+  // the pair's coefficients and transfer matrices are the same in every tile (load_pair_coeffs)
+  double av[NA];
+  float bk[NBT];
+  load_pair_coeffs<NA, NBT>(av, bk, bcoef, acoef, lid, I, O, nb);
+  if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, 0, lanes);
   if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
   __syncthreads();
   for (int buf = 0;; buf ^= 1) {
@@ -294,9 +309,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     const bool live = g.live;
     const int64_t t0 = sc * SL + (int64_t)k * kTileT;
     const int n = (L - t0) >= kTileT ? kTileT : (L - t0) > 0 ? (int)(L - t0) : 0;
-    double av[NA], s[NA];
-    float bk[NBT];
-    load_coeffs<NA, NBT>(av, bk, bcoef, acoef, g, I, nb);
+    double s[NA];
     // The phases are ordered so that no 32-step window is live across the look-back: the adjoint
     // summaries and look-back first (g window dropped after the summaries), then the forward
     // recompute of y_p, then the sweep over a reloaded g window.
@@ -312,6 +325,14 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     };
     double* vk = vec_area<NA>(s_lds, k) + lid * V;
     double sG[NA], sC[NA];
+    // wave 0 issues the load of the super-chunk's saved entering state with its g window, so that
+    // its latency overlaps theirs; parked in LDS for the state composition below
+    double st_pre[NA];
+    if (k == 0) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q)
+        st_pre[q] = !live ? 0.0 : sc == 0 ? (x0 ? (double)x0[lane * NA + q] : 0.0) : saved[(sc * lanes + lane) * NA + q];
+    }
     {
       // --- zero-state summaries of both adjoint recurrences over the chunk, right to left
       float gw[kTileT + NBT - 1];
@@ -328,11 +349,14 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
           step<NA>(av, sC, (double)h);
         }
     }
-    if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, l0, lanes);
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
       vk[q] = sG[q];
       vk[NA + q] = sC[q];
+    }
+    if (k == 0) {
+#pragma unroll
+      for (int q = 0; q < NA; ++q) s_st[lid][q] = st_pre[q];
     }
     if (threadIdx.x == 0) s_tile[buf ^ 1] = next;
     __syncthreads();
@@ -390,6 +414,10 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     if (n > 0) {
       float uw[kTileT + NBT - 1];
       load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
+      if constexpr (kStashU) {
+#pragma unroll
+        for (int i = 0; i < kUW; ++i) s_uw[k][lid][i] = uw[i];
+      }
       fir<NBT>(xb, uw, bk);
 #pragma unroll
       for (int i = 0; i < kTileT; ++i)
@@ -402,7 +430,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     if (k == 0 && live) {
       double st[NA];
 #pragma unroll
-      for (int q = 0; q < NA; ++q) st[q] = sc == 0 ? (x0 ? (double)x0[lane * NA + q] : 0.0) : saved[(sc * lanes + lane) * NA + q];
+      for (int q = 0; q < NA; ++q) st[q] = s_st[lid][q];
       double mc[NA][NA];
       load_mat<NA>(mc, MatStage<NA>::kLds ? &s_mat[lid * NA * NA] : Mc + lane * NA * NA);
       for (int jj = 0; jj < K; ++jj) {
@@ -471,7 +499,12 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
       for (int m = 0; m < (NBT > 1 ? NBT - 1 : 1); ++m) gt[m] = 0.0f;
       {
         float uw[kTileT + NBT - 1];
-        load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
+        if constexpr (kStashU) {
+#pragma unroll
+          for (int i = 0; i < kUW; ++i) uw[i] = s_uw[k][lid][i];  // this wave's own, same lane
+        } else {
+          load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
+        }
 #pragma unroll
         for (int i = 0; i < kTileT; ++i)
           if (i < n) {
@@ -515,21 +548,27 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
       for (int kk = 0; kk < NBT; ++kk) pb[kk] = gbk[kk];
     }
     __syncthreads();
-    if (k == 0 && live) {
+    // wave w of the K sums partial values w, w + K, ... of its lane over the K chunks, in chunk
+    // order (the chunks' reads issued together)
+    if (live) {
+      for (int v = k; v < NA + NBT; v += K) {
+        double pv[kLbWaves];
 #pragma unroll
-      for (int q = 0; q < NA; ++q) {
+        for (int jj = 0; jj < kLbWaves; ++jj)
+          pv[jj] = jj >= K   ? 0.0
+                   : v < NA ? (part_a_area<NA, NBT>(s_lds, jj) + lid * NA)[v]
+                            : (double)(part_b_area<NA, NBT>(s_lds, jj) + lid * NBT)[v - NA];
         double t = 0.0;
-        for (int jj = 0; jj < K; ++jj) t += (part_a_area<NA, NBT>(s_lds, jj) + lid * NA)[q];
-        part_ga[(sc * lanes + lane) * NA + q] = t;
-      }
 #pragma unroll
-      for (int kk = 0; kk < NBT; ++kk) {
-        double t = 0.0;
-        for (int jj = 0; jj < K; ++jj) t += (double)(part_b_area<NA, NBT>(s_lds, jj) + lid * NBT)[kk];
-        part_gb[(sc * lanes + lane) * NBT + kk] = t;
+        for (int jj = 0; jj < kLbWaves; ++jj)
+          if (jj < K) t += pv[jj];
+        if (v < NA)
+          part_ga[(sc * lanes + lane) * NA + v] = t;
+        else
+          part_gb[(sc * lanes + lane) * NBT + (v - NA)] = t;
       }
     }
-    __syncthreads();  // wave 0's reads of every tile precede the next tile's writes into them
+    __syncthreads();  // every wave's reads of the tile precede the next tile's writes into them
   }
 }
 
