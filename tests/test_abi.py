@@ -41,6 +41,21 @@ def test_status_strings(lib):
     assert lib.tsfast_hip_version() >= 1
 
 
+def test_whole_sequence_tiling_needs_only_the_header(lib):
+    """Diagonal scans whose both directions fit one workgroup per lane group (whole-sequence
+    tiles: no look-back words) need only the 256-byte header; any longer sequence needs the
+    look-back words. Chunks are 64 real steps (complex: 32 forward, 16 backward); groups are
+    64 lanes from 16384 lanes up (16 chunks), else 16 lanes (16 chunks; the forward alone may
+    take 64 when 256 groups cover the lanes)."""
+    ws = lib.tsfast_hip_diag_workspace_bytes
+    assert ws(32, 1000, 64, 0) == 256  # config 1: 2048 lanes, 16 chunks
+    assert ws(64, 1024, 256, 0) == 256  # 16384 lanes in 64-lane groups, 16 chunks
+    assert ws(64, 1025, 256, 0) > 256  # 17 chunks
+    assert ws(2, 1024, 64, 0) == 256 and ws(2, 1025, 64, 0) > 256
+    assert ws(8, 4096, 128, 0) > 256  # config 5: the forward alone is whole-sequence
+    assert ws(2, 256, 32, 1) == 256 and ws(2, 257, 32, 1) > 256  # complex backward: 16 x 16 steps
+
+
 def test_size_queries(lib):
     assert lib.tsfast_hip_diag_workspace_bytes(32, 1000, 64, 0) > 0
     # a 256-byte tile counter, then 4 words per lane and super-chunk (complex: 16-byte words)
