@@ -55,6 +55,10 @@ _SHAPES = [
     (5, 1000, 2, 2, 5, 1),
     (6, 2049, 1, 8, 2, 3),
     (4, 4096, 8, 8, 8, 3),  # config-4 channel structure, reduced batch and length
+    # lanes beyond one tile, not a multiple of 64: the second tile holds a partial lane group
+    # whose pairs (lane % P) repeat the first tile's (coefficients and transfer matrices staged once)
+    (5, 700, 4, 4, 8, 3),  # 80 lanes, matrices in LDS
+    (9, 500, 2, 4, 4, 4),  # 72 lanes, na 4: matrices read from global memory
 ]
 
 
