@@ -67,7 +67,10 @@ int tsfast_hip_version(void);
  * Layout: lam [M, N], v/out/g/gv [M, L, N], x0/gx0/glam [M, N]; float32 or complex64.
  * Single-pass kernels with an inter-workgroup look-back: the workspace holds the tile counter and
  * the published super-chunk states; each call re-initialises it on its stream (no caller set-up),
- * so two calls in flight at once must not share one workspace.
+ * so two calls in flight at once must not share one workspace. A sequence short enough for one
+ * workgroup per lane group in a direction (whole-sequence tiles: up to 16 chunks of 64 real
+ * steps, or 32 / 16 complex steps forward / backward; a forward on 16-lane groups up to 64
+ * chunks) runs without a look-back; when both directions do, the workspace is just the header.
  */
 int64_t tsfast_hip_diag_workspace_bytes(int64_t M, int64_t L, int64_t N, int is_complex);
 int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const void* lam, const void* v,
