@@ -247,7 +247,8 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
         const int64_t bb = b0 + rb;
         if (i < n && bb < B) {
           float acc = 0.0f;
-          for (int jj = 0; jj < I; ++jj) acc += tl[rb * P + jj * O + o][i];
+#pragma unroll 8
+          for (int jj = 0; jj < I; ++jj) acc += tl[rb * P + jj * O + o][i];  // reads go out together
           y[(bb * L + t0 + i) * O + o] = acc;
         }
       }
@@ -489,7 +490,8 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
         const int64_t bb = b0 + rb;
         if (i < n && bb < B) {
           float acc = 0.0f;
-          for (int o = 0; o < O; ++o) acc += tl[rb * P + jj * O + o][i];
+#pragma unroll 8
+          for (int o = 0; o < O; ++o) acc += tl[rb * P + jj * O + o][i];  // reads go out together
           gu[(bb * L + t0 + i) * I + jj] = acc;
         }
       }
@@ -531,6 +533,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
           const int64_t bb = b0 + rb;
           if (bb < B) {
             float acc = 0.0f;
+#pragma unroll 8
             for (int o = 0; o < O; ++o) acc += tl[rb * P + jj * O + o][m + NBT - nb];
             gu_tail[(bb * (nb - 1) + m) * I + jj] = acc;
           }
