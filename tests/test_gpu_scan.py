@@ -40,6 +40,7 @@ _DIAG_SHAPES = [
     # 500 lanes = 32 groups of 16 (XCD-contiguous group order) with a ragged last group
     ((64, 200, 256), (256,)),
     ((5, 200, 100), (100,)),
+    ((48, 500, 256), (256,)),  # 12288 lanes: 768 16-lane workgroups, several rounds per CU
     # forward on whole-sequence tiles of up to 64 chunks (16-lane groups, L <= 4096), backward on
     # the look-back: ragged lanes and last chunk; and a long look-back with 128 super-chunks
     ((3, 3000, 70), (70,)),
