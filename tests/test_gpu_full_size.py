@@ -118,14 +118,16 @@ def test_config3_full_size(gpu):
     assert O.rel_err(_np64(gz[b : b + 1, :, ds]), wgz) < tol
 
 
-def test_config3_full_width_row_all_grads(gpu):
-    """One batch row of config 3 at its full length and width (L4096, D1536, N16, bf16 I/O)
-    against the fp64 oracle, every output and gradient included: gBt / gCt sum over all 48
-    32-channel tiles of the backward's partial buffer and gA / gDp over the whole sequence, so
-    the cross-tile reduction is checked at the headline width, not only at D = 256."""
+@pytest.mark.parametrize("io", ["bf16", "fp32"])
+def test_config3_full_width_row_all_grads(gpu, io):
+    """One batch row of config 3 at its full length and width (L4096, D1536, N16) against the
+    fp64 oracle, every output and gradient included: gBt / gCt sum over every channel tile of
+    the backward's partial buffer and gA / gDp over the whole sequence, so the cross-tile
+    reduction is checked at the headline width, not only at D = 256. bf16 I/O (the benchmark's
+    regime, bar 2e-2) and fp32 I/O (the reference's own regime, bar 1e-5)."""
     g = torch.Generator().manual_seed(5)
     L, D, N = 4096, 1536, 16
-    bf = torch.bfloat16
+    bf = torch.bfloat16 if io == "bf16" else torch.float32
     A = -torch.exp(torch.log(torch.arange(1, N + 1, dtype=torch.float32))).expand(D, N).contiguous()
     draw = (torch.randn(1, L, D, generator=g) - 4.0).to(bf)
     Bt = torch.randn(1, L, N, generator=g).to(bf)
@@ -139,7 +141,7 @@ def test_config3_full_width_row_all_grads(gpu):
     np_args = [_np64(t) for t in (draw, A, Bt, Ct, u, z, Dp)]
     want_out, want_h = O.mamba_forward(*np_args)
     want = O.mamba_backward(_np64(gout), None, *np_args)
-    tol = 2e-2
+    tol = 2e-2 if io == "bf16" else 1e-5
     assert O.rel_err(_np64(out), want_out) < tol
     assert O.rel_err(_np64(h_last.view(1, D, N)), want_h) < tol
     for name, got, w in zip(("draw", "A", "Bt", "Ct", "u", "z", "Dp"), grads[:7], want[:7]):

@@ -55,12 +55,22 @@ int ns_for(int64_t N) {
 #ifndef TSF_MAMBA_FWD_RD
 #define TSF_MAMBA_FWD_RD 4
 #endif
+// Channels per workgroup of the forward and of the backward (16 or 32).
+#ifndef TSF_MAMBA_FWD_DT
+#define TSF_MAMBA_FWD_DT 32
+#endif
+#ifndef TSF_MAMBA_BWD_DT
+#define TSF_MAMBA_BWD_DT 32
+#endif
+#ifndef TSF_MAMBA_BWD_HG
+#define TSF_MAMBA_BWD_HG 0
+#endif
 
 template <int NS>
 struct MCfg {
   static constexpr int NG = NS >= 8 ? 8 : NS;  // lanes per channel
   static constexpr int NPT = NS / NG;          // states per lane
-  static constexpr int DT = 32;                // channels per workgroup
+  static constexpr int DT = TSF_MAMBA_FWD_DT;  // channels per workgroup
   static constexpr int TH = DT * NG;           // threads per workgroup
   // checkpoint interval = backward recompute chunk (lam_t and h_t of a chunk live in VGPRs)
   static constexpr int CHK = NPT <= 2 ? 8 : (NPT == 4 ? 8 : 4);
@@ -191,6 +201,8 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
   // y partial per lane (state group); odd groups store channel dl at column dl ^ 16, so the two
   // lanes of a state pair (same channel, rows 32 floats apart) write to different banks
   __shared__ float s_y[TF][NG][DT];
+  // with 32-channel tiles the two lanes of a state pair sit in one half-wave, 32 floats apart
+  constexpr int kSwz = DT >= 32 ? 16 : 0;
 
   const int tid = threadIdx.x;
   int64_t tile, b;
@@ -328,7 +340,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
           h[j] = fmaf(lam, h[j], sv[cur][r].y * bcv[cur][r][j].x);
           y = fmaf(h[j], bcv[cur][r][j].y, y);
         }
-        s_y[i][ng][dl ^ ((ng & 1) << 4)] = y;
+        s_y[i][ng][dl ^ ((ng & 1) * kSwz)] = y;
       }
       // checkpoint slot k holds the state after step (k + 1) * CHK - 1 (layout [B, NC, N, D])
       const int ie = i0 + kRd - 1;
@@ -348,7 +360,7 @@ __global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
       if (((TF * DT) % TH == 0 || idx < TF * DT) && t < len && oact) {
         float yp[NG];
 #pragma unroll
-        for (int g = 0; g < NG; ++g) yp[g] = s_y[t][g][od ^ ((g & 1) << 4)];
+        for (int g = 0; g < NG; ++g) yp[g] = s_y[t][g][od ^ ((g & 1) * kSwz)];
         const float y = tree_sum<NG>(yp);
         const float zz = o_z[k];
         const uint32_t o = (t0 + (uint32_t)t) * Du + (uint32_t)od;
@@ -590,7 +602,9 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
     // used within one iteration, so no pending load is carried around the loop
     if (c > 0) load_chunk(c - 1);
 
-    // A: recompute this chunk's states into registers: lam_t, lam_t h_{t-1} and h_t
+    // A: recompute this chunk's states into registers: lam_t, lam_t h_{t-1} and h_t (the chunk's
+    // (delta, delta u) stay in registers for B: one LDS read per step instead of two)
+    float2 scb[CHK];
     {
       float hs[NPT];
 #pragma unroll
@@ -598,6 +612,7 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
 #pragma unroll
       for (int i = 0; i < CHK; ++i) {
         const float2 sc = s_dx[i][dl];
+        scb[i] = sc;
 #pragma unroll
         for (int j = 0; j < NPT; ++j) {
           const int s = i * NPT + j;
@@ -612,7 +627,7 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
     // B: adjoint sweep backwards through the chunk
 #pragma unroll
     for (int i = CHK - 1; i >= 0; --i) {
-      const float2 sc = s_dx[i][dl];  // (delta, delta * u)
+      const float2 sc = scb[i];  // (delta, delta * u), kept from A
       const float gyv = s_gw[wb][i][dl];
       float aq = 0.0f, gb = 0.0f;
 #pragma unroll
@@ -625,7 +640,7 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
         aq = fmaf(Av[j], Q, aq);
         gb = fmaf(row_bcast(bv[s / 16], s % 16), G[j], gb);
         s_dp[i][j * NG + ng][dl] = G[j] * sc.y;
-        s_dp[i][NS + j * NG + ng][dl] = hb[i][j];
+        s_dp[i][NS + j * NG + ng][dl] = TSF_MAMBA_BWD_HG ? hb[i][j] * gyv : hb[i][j];
       }
       s_np[i][0][ng][dl] = aq;
       s_np[i][1][ng][dl] = gb;
@@ -662,7 +677,7 @@ __global__ void __launch_bounds__((BCfg<NS, DT_>::TH), (BCfg<NS, DT_>::OCC)) mam
       const float4* row = reinterpret_cast<const float4*>(&s_dp[ii][col][0]);
       constexpr int NQ = DT / 4;
       float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (half == 0) {
+      if (half == 0 || TSF_MAMBA_BWD_HG) {
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
           const float4 v = row[(q + (c >> 1)) % NQ];
@@ -791,7 +806,7 @@ int launch_fwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
 // Channel tile of the backward. (A 96-channel tile, one 12-wave workgroup per CU with a third of
 // the grad-B/C partials, measured 16% slower at config 3: with one workgroup per CU nothing runs
 // while its waves wait at the chunk barriers.)
-constexpr int kBwdDT = 32;
+constexpr int kBwdDT = TSF_MAMBA_BWD_DT;
 
 // Backward workspace: grad-B/C partials [nT, B, L, 2*NS] in the I/O type (padded to 256 bytes),
 // then the fp32 per-row partials of gA [B, D, N] and gDp [B, D].

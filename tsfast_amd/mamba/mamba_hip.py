@@ -289,7 +289,11 @@ def run(draw, A, Bt, Ct, u, z, Dp, h0):
     evolve independently, and the output is linear in the per-state sum ``h . C`` for fixed
     draw, u, z (``out = (sum over groups of h_g . C_g + Dp u) * silu(z)``), so the groups' outputs
     add up to the output (the D skip goes with the first group only), and their gradients add up
-    the same way through autograd. Group outputs are summed in float32 and rounded once.
+    the same way through autograd. Each group's launch rounds its output (and its gradients of
+    the I/O tensors) to the I/O dtype; the outputs are then added in float32 and rounded again,
+    and autograd adds the groups' gradients in the I/O dtype. With float32 I/O that is ordinary
+    float32 rounding; with bfloat16 I/O it is up to one bfloat16 rounding per group on top of the
+    final one, inside the 2e-2 bar of bf16 I/O (the GPU tests at N 96 and 130 check it).
     """
     N = A.shape[-1]
     if N <= _MAX_N:
