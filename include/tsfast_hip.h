@@ -56,6 +56,19 @@ const char* tsfast_hip_status_string(int status);
  * torch.are_deterministic_algorithms_enabled(). */
 void tsfast_hip_set_deterministic(int on);
 int tsfast_hip_get_deterministic(void);
+/* Look-back failure reporting. Every look-back wait is bounded: a scan whose wait makes no
+ * progress for the spin limit gives up, writes NaN into the lanes concerned, sets the
+ * workspace's give-up word (byte 64) and writes the scan's call number into the library's alarm
+ * word, a word in mapped host memory. tsfast_hip_lookback_gave_up reads that word without
+ * synchronising with the device: 1 if it names a scan call not yet reported (a give-up shows
+ * there once its kernel has ended), 0 if not, -1 if the word could not be allocated; with
+ * `clear` nonzero the call it names counts as reported from then on, so each failing call is
+ * reported once. tsfast_hip_set_lookback_spin_limit sets the polls without progress allowed before a
+ * give-up (default 2^20, taken by each scan's reset kernel when it is enqueued) and returns the
+ * previous limit; a small limit lets a test force a give-up while every kernel still exits.
+ * No counterpart in the reference, whose scans never wait on other workgroups. */
+int tsfast_hip_lookback_gave_up(int clear);
+int64_t tsfast_hip_set_lookback_spin_limit(int64_t polls);
 /* Library version, for the Python loader's sanity check. */
 int tsfast_hip_version(void);
 

@@ -223,3 +223,104 @@ def test_lookback_give_up_flag_cleared_and_unset(gpu):
     torch.cuda.synchronize()
     assert not _lib.lookback_gave_up(ws)
     assert O.rel_err(_np(out), O.diag_forward(_np(lam_l), _np(v_l))) < TOL
+
+
+# The reference suite's coefficient draws (tests/test_scan_diagonal_backends.py:33-40: real
+# lam ~ U(0, 0.85); complex |lam| ~ U(0, 0.85) with phase ~ U(0, 3)), plus negative real
+# coefficients and complex ones near the unit circle with large phases, on shapes that take the
+# look-back (real L > 1024, complex L > 512: fp64 powers of lam composed across super-chunks,
+# underflowing fast for small |lam|) and on whole-sequence tiles. Lane 0 of every draw has
+# lam = 0 exactly (x_t = v_t).
+_DRAW_SHAPES = [
+    ((2, 1025, 64), (64,)),
+    ((1, 8192, 24), (24,)),
+    ((6, 8192, 100), (100,)),
+    ((3, 3000, 70), (70,)),
+    ((16, 2048, 256), (256,)),
+    ((4, 4096, 256), (256,)),
+    ((32, 1000, 64), (32, 64)),
+    ((2, 512, 32), (32,)),
+    ((48, 500, 256), (256,)),
+]
+
+
+def _draw_lam(kind, shape, g):
+    u = torch.rand(*shape, generator=g)
+    if kind == "ref_real":
+        lam = u * 0.85
+    elif kind == "neg_real":
+        lam = -(u * 0.9 + 0.05)
+    elif kind == "neg_real_near_one":
+        lam = -(u * 0.099 + 0.9)
+    elif kind == "ref_complex":
+        lam = torch.polar(u * 0.85, torch.rand(*shape, generator=g) * 3.0)
+    else:  # "wide_complex": near the unit circle, phases up to 3 rad
+        lam = torch.polar(u * 0.099 + 0.9, torch.rand(*shape, generator=g) * 3.0)
+    lam[..., 0] = 0
+    return lam
+
+
+@pytest.mark.parametrize("kind", ["ref_real", "neg_real", "neg_real_near_one", "ref_complex", "wide_complex"])
+@pytest.mark.parametrize("v_shape,lam_shape", _DRAW_SHAPES)
+def test_diag_reference_coefficient_draws(gpu, kind, v_shape, lam_shape):
+    g = torch.Generator().manual_seed(sum(v_shape) + len(kind))
+    cplx = kind.endswith("complex")
+    dt = torch.complex64 if cplx else torch.float32
+    lam = _draw_lam(kind, lam_shape, g)
+    v = torch.randn(*v_shape, dtype=dt, generator=g)
+    x0 = torch.randn(v_shape[0], v_shape[-1], dtype=dt, generator=g)
+    gout = torch.randn(*v_shape, dtype=dt, generator=g)
+    lam_d = lam.to(gpu).requires_grad_()
+    v_d, x0_d = v.to(gpu).requires_grad_(), x0.to(gpu).requires_grad_()
+    with dispatch.use_backend("hip"):
+        assert dispatch.resolve("scan.diagonal", scan._BACKENDS["diagonal"], ("hip",), _lanes(lam_d, v_d, x0_d)) is diagonal_hip
+        out = scan.diagonal_recurrence(lam_d, v_d, x0_d)
+        out.backward(gout.to(gpu))
+    lam_l, _, _ = _lanes(lam, v, x0)
+    want = O.diag_forward(_np(lam_l), _np(v), _np(x0))
+    glam_w, gv_w, gx0_w = O.diag_backward(_np(gout), _np(lam_l), want, _np(x0))
+    if lam.dim() == 1:
+        glam_w = glam_w.sum(0)
+    assert O.rel_err(_np(out), want) < TOL, "out"
+    assert O.rel_err(_np(v_d.grad), gv_w) < TOL, "gv"
+    assert O.rel_err(_np(lam_d.grad), glam_w) < TOL, "glam"
+    assert O.rel_err(_np(x0_d.grad), gx0_w) < TOL, "gx0"
+
+
+def test_forced_give_up_raises_without_debug_mode(gpu):
+    """A look-back that gives up is reported by default (no TSFAST_HIP_CHECK_LOOKBACK): the host
+    forces it with a zero spin limit (a wait ends at its first round without progress, so every
+    kernel still exits), and the give-up reaches the Python layer through the library's alarm
+    word, as a RuntimeError from the call that launched it or from the next check, and only once
+    per failing call. Scans then run normally again."""
+    from tsfast_amd import _lib
+
+    _lib.raise_if_lookback_gave_up("before")  # no earlier give-up pending
+    assert _lib.load().tsfast_hip_lookback_gave_up(0) == 0
+    g = torch.Generator().manual_seed(41)
+    lam = (torch.rand(8, 64, generator=g) * 0.099 + 0.9).to(gpu)
+    v = torch.randn(8, 100_000, 64, generator=g).to(gpu)  # 12800 look-back tiles
+    lib = _lib.load()
+    prev = lib.tsfast_hip_set_lookback_spin_limit(0)
+    raised = False
+    out = None
+    try:
+        out = diagonal_hip.forward(lam, v, None)
+    except RuntimeError as e:
+        raised = "gave up" in str(e)
+    finally:
+        lib.tsfast_hip_set_lookback_spin_limit(prev)
+    torch.cuda.synchronize()
+    if not raised:
+        assert torch.isnan(out).any()  # the lanes whose wait gave up
+        with pytest.raises(RuntimeError, match="gave up"):
+            _lib.raise_if_lookback_gave_up("after")
+    # reported once: the same call's later give-ups do not raise again
+    assert lib.tsfast_hip_lookback_gave_up(0) == 0
+    _lib.raise_if_lookback_gave_up("again")
+    # normal limit again: a clean scan that matches the oracle and raises nothing
+    small_v = v[:2, :5000].contiguous()
+    out2 = diagonal_hip.forward(lam[:2], small_v, None)
+    torch.cuda.synchronize()
+    _lib.raise_if_lookback_gave_up("clean")
+    assert O.rel_err(_np(out2), O.diag_forward(_np(lam[:2]), _np(small_v))) < TOL

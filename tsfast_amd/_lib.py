@@ -30,6 +30,8 @@ _SIGNATURES: dict[str, tuple[list, object]] = {
     "tsfast_hip_status_string": ([_int], ctypes.c_char_p),
     "tsfast_hip_set_deterministic": ([_int], None),
     "tsfast_hip_get_deterministic": ([], _int),
+    "tsfast_hip_lookback_gave_up": ([_int], _int),
+    "tsfast_hip_set_lookback_spin_limit": ([_i64], _i64),
     "tsfast_hip_diag_workspace_bytes": ([_i64, _i64, _i64, _int], _i64),
     "tsfast_hip_diag_fwd": ([_i64, _i64, _i64, _int] + [_ptr] * 5 + [_i64, _ptr], _int),
     "tsfast_hip_diag_bwd": ([_i64, _i64, _i64, _int] + [_ptr] * 8 + [_i64, _ptr], _int),
@@ -91,6 +93,9 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
                 fn.restype = restype
+            if torch.cuda.is_available():
+                # allocate the look-back alarm word now, not inside a later graph capture
+                lib.tsfast_hip_lookback_gave_up(0)
             _lib = lib
     return _lib
 
@@ -119,15 +124,40 @@ def lookback_gave_up(ws: torch.Tensor) -> bool:
     return bool(ws[LOOKBACK_ERR_OFFSET : LOOKBACK_ERR_OFFSET + 4].view(torch.int32).item())
 
 
+def _alarm(clear: bool) -> int:
+    """1 if the library's look-back alarm word names a scan call that gave up and has not been
+    reported, else 0 (-1 if the word is unavailable; 0 without a GPU, where no scan can have
+    run); ``clear`` marks that call reported."""
+    if not torch.cuda.is_available():
+        return 0
+    return load().tsfast_hip_lookback_gave_up(1 if clear else 0)
+
+
+def raise_if_lookback_gave_up(what: str) -> None:
+    """Raise if a look-back scan of this process gave up and has not been reported yet, reading
+    the library's alarm word in mapped host memory (no device synchronisation). A give-up shows
+    there once its kernel has ended, so it is reported, once, by the first check after that:
+    the call that launched it, or a later one."""
+    if _alarm(clear=True) > 0:
+        raise RuntimeError(
+            f"{what}: a look-back wait in this or an earlier scan call gave up without progress (the "
+            "GPU was probably shared with work that kept the scan's workgroups from running); the "
+            "outputs of that call hold NaN"
+        )
+
+
 def check_lookback(ws: torch.Tensor, what: str) -> None:
-    """With TSFAST_HIP_CHECK_LOOKBACK=1 in the environment (a debug mode: it synchronises after
-    every look-back scan), raise if the scan's look-back gave up rather than let its NaN pass as a
-    numerical result. Otherwise a no-op."""
+    """Called after every look-back scan is enqueued: raises if a look-back gave up (this call's,
+    if its kernels have ended, or an earlier call's) rather than let its NaN pass as a numerical
+    result. With TSFAST_HIP_CHECK_LOOKBACK=1 in the environment (a debug mode) it first
+    synchronises, so that this call's own give-up is always the one reported."""
     if _CHECK_LOOKBACK and lookback_gave_up(ws):
+        _alarm(clear=True)
         raise RuntimeError(
             f"{what}: a look-back wait gave up without progress (the GPU was probably shared with "
             "work that kept the scan's workgroups from running); its outputs hold NaN"
         )
+    raise_if_lookback_gave_up(what)
 
 
 def available() -> bool:

@@ -205,7 +205,7 @@ TSF_DEV void put_vec(double* p, const double (&x)[NA]) {
 // Horner's rule back from that inc (s <- Ms s + agg). Otherwise the round is repeated. Every
 // wait ends: the nearest super-chunk publishes its inc once its own look-back ends, and the first
 // one in scan order publishes its inc without looking back (the window never has to move); a
-// lane without progress for kSpinMax rounds gives up with NaN.
+// lane without progress for the header's spin-limit rounds gives up with NaN.
 // out = m x + b applied to each of the NV blocks of NA values.
 template <int NA, int NV>
 TSF_DEV void block_matvec_add(double (&out)[NA * NV], const double (&m)[NA][NA], const double (&x)[NA * NV],
@@ -231,6 +231,7 @@ TSF_DEV void ap_look_back(double (&S)[NA * NV], const double* __restrict__ agg, 
                           int* pend_s, int* any_s, unsigned* __restrict__ lb_counter) {
   constexpr int V = NA * NV;
   uint32_t spins = 0;
+  const uint32_t spin_max = lb_spin_limit(lb_counter);
   if (k == 0) {
     int p = 0;
     if (need) {
@@ -284,7 +285,7 @@ TSF_DEV void ap_look_back(double (&S)[NA * NV], const double* __restrict__ agg, 
             for (int q = 0; q < V; ++q) ag[q] = sv[q];
             block_matvec_add<NA, NV>(S, ms, S, ag);
           }
-        } else if (++spins > kSpinMax) {
+        } else if (++spins > spin_max) {
 #pragma unroll
           for (int q = 0; q < V; ++q) S[q] = quiet_nan<double>();
           lb_gave_up(lb_counter);

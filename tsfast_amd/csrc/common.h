@@ -259,3 +259,8 @@ int tsf_record_hip_error(hipError_t e);
 inline int tsf_launch_status() { return tsf_record_hip_error(hipGetLastError()); }
 // Process-wide deterministic mode of the look-back scans (tsfast_hip_set_deterministic).
 int tsf_deterministic();
+// Look-back failure reporting (csrc/status.hip): the device address of the host-mapped alarm
+// word that a give-up sets (nullptr when it could not be allocated) and the current wait bound.
+unsigned* tsf_lookback_alarm();
+uint32_t tsf_lookback_spin_limit();
+uint32_t tsf_next_epoch();  // call number of the next look-back scan (never 0)

@@ -71,7 +71,7 @@ constexpr int kWindow = kMaxWaves;  // look-back slots examined per round
 // moves on, an unpublished slot ends the round (the next round starts there). The walk always
 // ends: the first tile in scan order publishes its inc without looking back, and every tile
 // waited on was taken from the counter earlier by a workgroup that is running; a lane that
-// makes no progress for kSpinMax rounds gives up with NaN. Returns the entering state in wave
+// makes no progress for the header's spin-limit rounds gives up with NaN. Returns the entering state in wave
 // 0's lanes. LDS: win/flag [kWindow][64], pos [64] and one flag word, owned by the caller.
 template <typename W>
 TSF_DEV W look_back(const Map<W>* __restrict__ agg, const W* __restrict__ inc, bool need, int64_t pos0, int64_t dj,
@@ -80,6 +80,7 @@ TSF_DEV W look_back(const Map<W>* __restrict__ agg, const W* __restrict__ inc, b
   Map<W> acc = {Num<W>::one(), Num<W>::zero()};  // composition of the aggregates walked over
   W result = Num<W>::zero();
   uint32_t spins = 0;
+  const uint32_t spin_max = lb_spin_limit(lb_counter);
   if (k == 0) {
     // direct probe of the nearest tile by wave 0: in the steady state of a long scan its inc is
     // already published, and the window rounds below are skipped
@@ -142,7 +143,7 @@ TSF_DEV W look_back(const Map<W>* __restrict__ agg, const W* __restrict__ inc, b
           acc = then(win[w][lid], acc);
           p += dj;
         }
-        if (p >= 0 && w == 0 && ++spins > kSpinMax) {
+        if (p >= 0 && w == 0 && ++spins > spin_max) {
           result = quiet_nan<W>();
           lb_gave_up(lb_counter);
           p = -1;
@@ -1056,6 +1057,14 @@ int noalloc_scratch(hipStream_t s, char** out) {
   return TSF_OK;
 }
 
+// Workspace bytes the forward alone touches: the header (the give-up word) on whole-sequence
+// tiles, else the header and its look-back words (maps and states, 3 fp64 words per lane and
+// super-chunk, complex128 when complex).
+int64_t diag_fwd_workspace_bytes(int64_t M, int64_t L, int64_t N, bool cplx) {
+  if (whole_tile(M * N, L, whole_tc(cplx, false), false).kmax > 0) return kCounterBytes;
+  return kCounterBytes + lookback_bytes(const_tile(M * N, L, cplx, false), cplx ? 16 : 8);
+}
+
 }  // namespace
 
 extern "C" {
@@ -1074,7 +1083,7 @@ int tsfast_hip_diag_fwd(int64_t M, int64_t L, int64_t N, int is_complex, const v
   if (M < 0 || L < 0 || N < 0) return TSF_ERR_ARG;
   if (M == 0 || L == 0 || N == 0) return TSF_OK;
   if (!lam || !v || !out) return TSF_ERR_ARG;
-  if (workspace_bytes < tsfast_hip_diag_workspace_bytes(M, L, N, is_complex) || !workspace) return TSF_ERR_WORKSPACE;
+  if (workspace_bytes < diag_fwd_workspace_bytes(M, L, N, is_complex != 0) || !workspace) return TSF_ERR_WORKSPACE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const WholeTile wf = whole_tile(M * N, L, whole_tc(is_complex != 0, false), false);
   if (wf.kmax > 0) {
@@ -1151,7 +1160,7 @@ int tsfast_hip_diag_fwd_noalloc(int64_t M, int64_t L, int64_t N, int is_complex,
   if (M < 0 || L < 0 || N < 0) return TSF_ERR_ARG;
   if (M == 0 || L == 0 || N == 0) return TSF_OK;
   if (!lam || !v || !out) return TSF_ERR_ARG;
-  const int64_t need = tsfast_hip_diag_workspace_bytes(M, L, N, is_complex);
+  const int64_t need = diag_fwd_workspace_bytes(M, L, N, is_complex != 0);
   if (need > kNoAllocScratchBytes) return TSF_ERR_SCRATCH;
   char* ws = nullptr;
   const int st = noalloc_scratch(static_cast<hipStream_t>(stream), &ws);

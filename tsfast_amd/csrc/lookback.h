@@ -9,7 +9,9 @@
 // the XCDs) and validated on its own, so no fence has to order data against a flag.
 constexpr uint64_t kUnset = 0x7FF00000DEADBEEFull;
 // Polls without progress before a look-back gives up and yields NaN (about a second): every
-// wait ends even if an invariant below were broken, and the NaN shows in the outputs.
+// wait ends even if an invariant below were broken, and the NaN shows in the outputs. The bound
+// a scan uses is the library's current limit (tsfast_hip_set_lookback_spin_limit, default
+// kSpinMax), which the reset kernel writes into the workspace header.
 constexpr uint32_t kSpinMax = 1u << 20;
 
 TSF_DEV void put_word(double* p, double x) {
@@ -62,10 +64,21 @@ constexpr int kAnchorSpacing = 8;  // deterministic-mode spacing of the look-bac
 // of the workspace, byte offset 64) is set to 1 by any look-back that gives up after kSpinMax
 // rounds without progress, whose lanes then carry NaN; lookback_reset clears it before every
 // scan, so after a scan it tells a give-up apart from NaNs that came with the inputs.
+// A give-up also writes the scan's call number (kEpochWord, nonzero) into the library's alarm
+// word, a 4-byte word in mapped host memory whose device address the reset kernel writes into the
+// header at word kAlarmWord (8 bytes; zero when the library has no alarm word), so that the host
+// sees it without a device synchronisation and reports each failing call once
+// (tsfast_hip_lookback_gave_up). The header's word kSpinWord holds the wait bound.
 constexpr int kErrWord = 16;
+constexpr int kSpinWord = 17;
+constexpr int kAlarmWord = 18;  // 8-byte aligned: byte offset 72
+constexpr int kEpochWord = 20;
 TSF_DEV void lb_gave_up(unsigned* counter) {
   __hip_atomic_store(counter + kErrWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned* alarm = reinterpret_cast<unsigned*>(*reinterpret_cast<const uint64_t*>(counter + kAlarmWord));
+  if (alarm) __hip_atomic_store(alarm, counter[kEpochWord], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
+TSF_DEV uint32_t lb_spin_limit(const unsigned* counter) { return counter[kSpinWord]; }
 
 TSF_DEV unsigned take_tile(unsigned* counter) {
   return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -74,12 +87,16 @@ TSF_DEV unsigned take_tile(unsigned* counter) {
 // Resets the look-back words to kUnset and the tile counter to zero before every scan (a
 // kernel rather than a memset node, so that a captured graph replays it reliably).
 __global__ void __launch_bounds__(256) lookback_reset(uint64_t* __restrict__ words, int64_t n,
-                                                      unsigned* __restrict__ counter) {
+                                                      unsigned* __restrict__ counter, unsigned* alarm,
+                                                      uint32_t spin_limit, uint32_t epoch) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) words[i] = kUnset;
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     counter[0] = 0u;
     counter[kErrWord] = 0u;
+    counter[kSpinWord] = spin_limit;
+    counter[kEpochWord] = epoch;
+    *reinterpret_cast<uint64_t*>(counter + kAlarmWord) = reinterpret_cast<uint64_t>(alarm);
   }
 }
 
@@ -109,5 +126,6 @@ void lookback_reset_launch(char* ws, int64_t words, hipStream_t s) {
   if (blocks < 1) blocks = 1;
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(lookback_reset, dim3((unsigned)blocks), dim3(256), 0, s,
-                     reinterpret_cast<uint64_t*>(ws + kCounterBytes), words, reinterpret_cast<unsigned*>(ws));
+                     reinterpret_cast<uint64_t*>(ws + kCounterBytes), words, reinterpret_cast<unsigned*>(ws),
+                     tsf_lookback_alarm(), tsf_lookback_spin_limit(), tsf_next_epoch());
 }

@@ -98,13 +98,14 @@ TSF_DEV void block_scan(float2 (&x)[4], float2 lm, float2 lm4, float2 lm8, int l
 // from a zero start; every such chunk has the multiplier P) is composed and the walk moves on; an
 // unpublished word ends the round. The walk ends: the first chunk in scan order publishes its inc
 // without waiting, and every chunk waited on belongs to a tile taken earlier by a running
-// workgroup; a lane that makes no progress for kSpinMax rounds gives up with NaN.
+// workgroup; a lane that makes no progress for the header's spin-limit rounds gives up with NaN.
 template <int W>
 TSF_DEV double2 walk(const double2* __restrict__ agg, const double2* __restrict__ inc, int64_t cstride, int64_t widx,
                      int c, int dir, int nc, double2 P, unsigned* __restrict__ lb_counter) {
   double2 accP = Num<double2>::one(), acce = Num<double2>::zero();
   int r = c + dir;
   uint32_t spins = 0;
+  const uint32_t spin_max = lb_spin_limit(lb_counter);
   for (;;) {
     double2 vi[W], va[W];
     bool hi[W], ha[W];
@@ -126,7 +127,7 @@ TSF_DEV double2 walk(const double2* __restrict__ agg, const double2* __restrict_
       acce = Num<double2>::fma(accP, va[i], acce);
       accP = Num<double2>::mul(accP, P);
     }
-    if (i == 0 && ++spins > kSpinMax) {
+    if (i == 0 && ++spins > spin_max) {
       lb_gave_up(lb_counter);
       return quiet_nan<double2>();
     }
