@@ -140,14 +140,39 @@ def test_mamba_saved_floats_formula_matches_the_library(lib):
 
 
 def test_conv_supports_mirrors_the_kernel_grid_limit(lib):
-    """conv_hip's size screen repeats the kernels' limits (B and the number of 128-step segments
-    each at most 65535), so a shape the library rejects falls back through dispatch instead of
-    raising in the op."""
+    """conv_hip's size screen repeats the kernels' limit (a one-dimensional grid of at most
+    2^24 - 1 workgroups; batch and sequence length have no cap of their own), so a shape the
+    library rejects falls back through dispatch instead of raising in the op."""
     from tsfast_amd.mamba import conv_hip
 
     D, K = 64, 4
-    for B, L in ((1, 1), (1, 128), (1, 65535 * 128 - 1), (1, 65535 * 128), (1, 65535 * 128 + 1), (1, 65536 * 128),
-                 (65535, 8), (65536, 8)):
+    cases = ((1, 1), (1, 128), (1, 65536 * 128), (65536, 8), (70000, 3), (2**24 - 1, 8), (2**24, 8),
+             (2**23 - 1, 65), (2**23, 65), (2**20, 1024), (2**18, 1024))
+    for B, L in cases:
         c_ok = lib.tsfast_hip_conv_silu_workspace_bytes(B, L, D, K) >= 0
         py_ok = conv_hip._size_reason(B, L, D, D, 1, 2) is None
         assert py_ok == c_ok, (B, L)
+    assert conv_hip._size_reason(70000, 3, D, D, 1, 2) is None
+    assert conv_hip._size_reason(2**24, 8, D, D, 1, 2) is not None
+
+
+@pytest.mark.parametrize(
+    "B,L,H,N,O",
+    [
+        (64, 4096, 32, 256, 32),
+        (1, 2**24, 32, 16, 31),  # u just under 2 GiB, y under
+        (1, 2**24, 31, 16, 32),  # y at 2 GiB: O > H on a long sequence
+        (1, 2**24, 32, 16, 32),  # both at 2 GiB
+        (2, 3, 33, 8, 8),
+        (2, 3, 8, 257, 8),
+        (2, 3, 8, 8, 33),
+        (2**30, 1, 1, 1, 1),
+    ],
+)
+def test_projected_supports_mirrors_the_library_size_check(lib, B, L, H, N, O):
+    """projected_hip's shape screen accepts exactly what tsfast_hip_projscan_workspace_bytes
+    accepts, so a call that passes supports() never meets a -1 workspace query."""
+    from tsfast_amd.scan_backends import projected_hip
+
+    ok_lib = lib.tsfast_hip_projscan_workspace_bytes(B, L, H, N, O) >= 0
+    assert (projected_hip.shape_reason(B, L, H, N, O) is None) == ok_lib

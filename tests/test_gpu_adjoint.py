@@ -42,6 +42,8 @@ def _inputs(B, L, n, seed, radius=0.9):
         (2, 50, 8, 1),
         (3, 40, 12, 200),
         (1, 4096, 32, 256),
+        (2, 200, 7, 16),
+        (2, 200, 20, 24),
     ],
 )
 def test_mat_adjoint_matches_oracle(gpu, B, L, n, cl):

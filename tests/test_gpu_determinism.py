@@ -157,11 +157,11 @@ def test_gblock_bitwise_repeatable(gpu):
 
 
 def test_projected_scan_repeatable(gpu):
-    """y, the returned state, g_u and g_x0 are bitwise repeatable. The parameter gradients
-    (grad W, grad lam, grad C) are sums a workgroup accumulates over the tiles it takes from the
-    tile counter, which depends on timing (a fixed tile-to-workgroup map could stall when not all
-    workgroups are resident); the final sum over workgroups runs in a fixed order, and runs agree
-    to float32 rounding."""
+    """Every output and gradient is bitwise repeatable: y and the returned state from the fused
+    forward's anchored look-back, and all seven gradients from the backward, which in this mode
+    differentiates the three-step composition (the fused backward's parameter gradients are
+    sums a workgroup accumulates over the tiles it takes from a counter, whose order depends on
+    timing). The deterministic gradients also agree with the fused backward's to 1e-5."""
     g = torch.Generator().manual_seed(6)
     B, L, H, N, O = 4, 8192, 32, 256, 32
     u = torch.randn(B, L, H, generator=g)
@@ -174,15 +174,20 @@ def test_projected_scan_repeatable(gpu):
 
     def call(u, W_re, W_im, lam, C_re, C_im, x0, gy):
         y, x_last, saved = projected_hip._scan_train_op(u, W_re, W_im, lam, C_re, C_im, x0)
-        return (y, x_last, *projected_hip._scan_bwd_op(gy, None, saved, u, W_re, W_im, lam, C_re, C_im, x0))
+        return (y, x_last, *projected_hip.backward(gy, None, saved, u, W_re, W_im, lam, C_re, C_im, x0))
 
-    outs = _repeat(call, *ins)
-    exact = [0, 1, 2, 8]  # y, x_last, g_u, g_x0
-    _assert_same([[o[i] for i in exact] for o in outs])
-    for rep in outs[1:]:
-        for i in (3, 4, 5, 6, 7):  # g_W_re, g_W_im, g_lam, g_C_re, g_C_im
-            a, b = outs[0][i], rep[i]
-            assert (a - b).abs().max() <= 1e-5 * a.abs().max(), i
+    fused = _default_mode(call, *ins)  # the fused backward kernel
+    noise = torch.randn(1 << 22, device=gpu)
+    outs = []
+    for r in range(3):
+        for _ in range(r * 3):
+            noise.mul_(1.0001)
+        outs.append([t.clone() for t in call(*ins)])
+    torch.cuda.synchronize()
+    _assert_same(outs)
+    for i, (a, b) in enumerate(zip(outs[0], fused)):
+        if b.numel():
+            assert ((a - b).abs().max() / b.abs().max()).item() < 1e-5, f"output {i}: composition vs fused"
 
 
 def test_mamba_and_conv_bitwise_repeatable(gpu):

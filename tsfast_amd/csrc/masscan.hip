@@ -160,7 +160,9 @@ __global__ void __launch_bounds__(4 * NP) mas_carry(const double* __restrict__ p
   const int tid = threadIdx.x, i = tid >> 2, h = tid & 3;
   const int64_t b = blockIdx.x;
   const bool live = i < n;
-  if (tid < NP) s_v[0][tid] = 0.0;
+  // both buffers start at zero: columns n..NP-1 of either one are read (times a zero P entry) in
+  // every chunk, so no earlier kernel's LDS contents (possibly NaN or Inf bits) may remain there
+  if (tid < 2 * NP) s_v[tid / NP][tid % NP] = 0.0;
   if (h == 0 && live) bnd[(b * (C + 1) + C) * n + i] = 0.0f;
   double ring[kRing][CP], sring[kRing];
   auto load = [&](int64_t c, int slot) __attribute__((always_inline)) {

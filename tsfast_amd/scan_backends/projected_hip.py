@@ -43,10 +43,20 @@ def supports(u, W_re, W_im, lam, C_re, C_im, x0) -> str | None:
         return f"C shapes {tuple(C_re.shape)}/{tuple(C_im.shape)} != {(O, N)}"
     if x0 is not None and tuple(x0.shape) != (B, N):
         return f"x0 shape {tuple(x0.shape)} != {(B, N)}"
+    return shape_reason(B, L, H, N, O)
+
+
+def shape_reason(B: int, L: int, H: int, N: int, O: int) -> str | None:
+    """The kernel's size limits (``ps_args_status`` in ``csrc/projscan.hip``): widths, and u / y /
+    gy read through buffer resources with 32-bit byte offsets, chunk and row indices in int."""
     if H > _MAX_H or N > _MAX_N or O > _MAX_O:
         return f"H={H}, N={N}, O={O} beyond the kernel's H <= {_MAX_H}, N <= {_MAX_N}, O <= {_MAX_O}"
     if B * L * H * 4 >= 2**31:
         return f"u of {B * L * H * 4} bytes beyond the kernel's 2 GiB buffer addressing"
+    if B * L * O * 4 >= 2**31:
+        return f"y of {B * L * O * 4} bytes beyond the kernel's 2 GiB buffer addressing"
+    if B > (2**31 - 1) // 2 or L > (2**31 - 1) // 2:
+        return f"B={B} or L={L} beyond the kernel's int chunk and row indices"
     return None
 
 
@@ -124,6 +134,38 @@ def _(u, W_re, W_im, lam, C_re, C_im, x0):
     return _fake_outs(u, lam, C_re, train=True)
 
 
+def _composition_bwd(gy, g_xlast, u, W_re, W_im, lam, C_re, C_im, x0):
+    """Every gradient of the projected scan through the three-step composition
+    ``complex_in_proj -> diagonal_recurrence -> real_out_proj`` (the reference's own formulation,
+    ``models/_core/scan.py:221-243, 272-313``), differentiated by autograd. Used under
+    ``torch.use_deterministic_algorithms(True)``: the fused backward adds its parameter gradients
+    (grad W, grad lam, grad C) per workgroup over the tiles the workgroup takes from a counter,
+    and which tiles those are depends on timing, while the composition's GEMMs and the diagonal
+    scan's anchored look-back give the same bits on every run."""
+    from ..scan import complex_in_proj, diagonal_recurrence, real_out_proj
+
+    B, L, _ = u.shape
+    if L == 0:
+        zeros = [torch.zeros_like(t) for t in (u, W_re, W_im, lam, C_re, C_im)]
+        g_x0 = lam.new_empty(0)
+        if x0 is not None:
+            g_x0 = g_xlast.clone() if g_xlast is not None else torch.zeros_like(x0)
+        return (*zeros, g_x0)
+    with torch.enable_grad():
+        leaves = [t.detach().requires_grad_() for t in (u, W_re, W_im, lam, C_re, C_im)]
+        if x0 is not None:
+            leaves.append(x0.detach().requires_grad_())
+        x = diagonal_recurrence(leaves[3], complex_in_proj(leaves[0], leaves[1], leaves[2]),
+                                leaves[6] if x0 is not None else None)
+        outs, ups = [real_out_proj(x, leaves[4], leaves[5])], [gy]
+        if g_xlast is not None:
+            outs.append(x[:, -1, :])
+            ups.append(g_xlast)
+        grads = torch.autograd.grad(outs, leaves, ups, allow_unused=True)
+    grads = [torch.zeros_like(t) if g is None else g for g, t in zip(grads, leaves)]
+    return (*grads[:6], grads[6] if x0 is not None else lam.new_empty(0))
+
+
 @torch.library.custom_op("tsfast_hip::projected_scan_bwd", mutates_args=())
 def _scan_bwd_op(
     gy: torch.Tensor, g_xlast: torch.Tensor | None, saved: torch.Tensor, u: torch.Tensor, W_re: torch.Tensor,
@@ -169,6 +211,16 @@ def _(gy, g_xlast, saved, u, W_re, W_im, lam, C_re, C_im, x0):
             torch.empty_like(C_re), torch.empty_like(C_im), g_x0)
 
 
+def backward(gy, g_xlast, saved, u, W_re, W_im, lam, C_re, C_im, x0):
+    """Every gradient of the projected scan: ``(g_u, g_W_re, g_W_im, g_lam, g_C_re, g_C_im,
+    g_x0)`` (``g_x0`` empty when ``x0`` is None). The fused backward kernel, or under
+    ``torch.use_deterministic_algorithms(True)`` the composition's autograd
+    (``_composition_bwd``), whose bits do not depend on timing."""
+    if torch.are_deterministic_algorithms_enabled():
+        return _composition_bwd(*_dense(gy, g_xlast, u, W_re, W_im, lam, C_re, C_im, x0))
+    return _scan_bwd_op(gy, g_xlast, saved, u, W_re, W_im, lam, C_re, C_im, x0)
+
+
 def _scan_setup(ctx, inputs, output):
     u, W_re, W_im, lam, C_re, C_im, x0 = inputs
     ctx.save_for_backward(u, W_re, W_im, lam, C_re, C_im, x0, output[2])
@@ -178,7 +230,7 @@ def _scan_backward(ctx, gy, g_xlast, g_saved):
     u, W_re, W_im, lam, C_re, C_im, x0, saved = ctx.saved_tensors
     if gy is None:
         gy = u.new_zeros(u.shape[0], u.shape[1], C_re.shape[0])
-    g_u, g_W_re, g_W_im, g_lam, g_C_re, g_C_im, g_x0 = _scan_bwd_op(
+    g_u, g_W_re, g_W_im, g_lam, g_C_re, g_C_im, g_x0 = backward(
         gy, g_xlast, saved, u, W_re, W_im, lam, C_re, C_im, x0
     )
     return g_u, g_W_re, g_W_im, g_lam, g_C_re, g_C_im, (g_x0 if x0 is not None else None)
