@@ -100,3 +100,53 @@ def test_allpole_chunked_state_shorter_than_na(gpu):
             prev = y0 if y0 is not None else torch.zeros(lanes, na, device=gpu)
             y0 = y.flip(-1)[:, :na] if n >= na else torch.cat((y.flip(-1), prev[:, : na - n]), -1)
     assert O.rel_err(_np(torch.cat(parts, -1)), _np(full)) < TOL
+
+
+def _ref_draw(P, na, g, L):
+    """The reference suite's coefficients, a = 0.25 N(0, 1) per pair
+    (tests/test_scan_allpole_backend.py:61). On sequences longer than 600 steps a pair whose
+    filter has a pole at radius >= 0.999 is drawn again, so the outputs stay finite in fp32."""
+    rows = []
+    for _ in range(P):
+        while True:
+            a = torch.randn(na, generator=g) * 0.25
+            if L <= 600 or np.max(np.abs(np.roots(np.r_[1.0, a.double().numpy()]))) < 0.999:
+                break
+        rows.append(a)
+    return torch.stack(rows)
+
+
+@pytest.mark.parametrize(
+    "B,P,L,na",
+    [
+        (32, 8, 200, 2), (4, 32, 100, 8), (3, 5, 7, 3), (2, 4, 1, 2), (2, 4, 2, 4), (1, 1, 513, 1),
+        (2, 3, 60, 16),
+        (3, 50, 5000, 3), (2, 100, 3333, 4), (1, 70, 20000, 1), (5, 13, 4100, 2), (4, 20, 2000, 6),
+    ],
+)
+@pytest.mark.parametrize("with_y0", [True, False])
+def test_allpole_reference_coefficient_draws(gpu, B, P, L, na, with_y0):
+    """The reference's coefficient draws (not constructed stable poles) on its own shapes and on
+    the look-back and two-pass paths."""
+    g = torch.Generator().manual_seed(7 * B * L + na)
+    a = _ref_draw(P, na, g, L)
+    w = torch.randn(B, P, L, generator=g)
+    y0 = torch.randn(B, P, na, generator=g) if with_y0 else None
+    gout = torch.randn(B, P, L, generator=g)
+    a_d, w_d = a.to(gpu).requires_grad_(), w.to(gpu).requires_grad_()
+    y0_d = y0.to(gpu).requires_grad_() if y0 is not None else None
+    with dispatch.use_backend("hip"):
+        assert dispatch.resolve("dynonet.allpole", dcore._ALLPOLE_BACKENDS, ("hip",), (a_d, w_d, y0_d)) is allpole_hip
+        y = dcore.allpole(a_d, w_d, y0_d)
+        y.backward(gout.to(gpu))
+    lanes = B * P
+    a_l = _np(a.expand(B, P, na).reshape(lanes, na))
+    y0_l = None if y0 is None else _np(y0.reshape(lanes, na))
+    want = O.allpole_forward(a_l, _np(w.reshape(lanes, L)), y0_l)
+    ga, gw, gy0 = O.allpole_backward(_np(gout.reshape(lanes, L)), a_l, want, y0_l)
+    assert np.isfinite(want).all()
+    assert O.rel_err(_np(y).reshape(lanes, L), want) < TOL, "y"
+    assert O.rel_err(_np(w_d.grad).reshape(lanes, L), gw) < TOL, "gw"
+    assert O.rel_err(_np(a_d.grad), ga.reshape(B, P, na).sum(0)) < TOL, "ga"
+    if y0 is not None:
+        assert O.rel_err(_np(y0_d.grad).reshape(lanes, na), gy0) < TOL, "gy0"

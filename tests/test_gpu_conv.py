@@ -50,6 +50,8 @@ _SHAPES = [
     (1, 300, 16, 7, False, True),  # K = 7: 21-row tiles, several segments
     (3, 700, 264, 4, True, True),  # two channel blocks, the second nearly empty
     (2, 1024, 1536, 4, True, True),  # config-3 channel count, reduced batch and length
+    (70000, 3, 8, 4, True, True),  # more batch rows than a grid dimension's 65535 (1-D grid)
+    (70000, 3, 12, 3, True, False),  # the same on the scalar (one channel per thread) path
 ]
 
 

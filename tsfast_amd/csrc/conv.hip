@@ -151,18 +151,31 @@ TSF_DEV float xbuf_at(const TIO* __restrict__ xrow, const TIO* __restrict__ tail
   return tail ? to_f32(tail[(b * D + d) * (K - 1) + (K - 1 + s)]) : 0.0f;
 }
 
+// Workgroup coordinates from a one-dimensional grid of nx * ny * B workgroups (x fastest, then
+// y, then the batch row, the order a three-dimensional grid dispatches in), so that neither the
+// batch nor the segment count is bounded by a grid dimension's 65535 limit.
+struct Wg3 {
+  int64_t x, y, z;
+};
+TSF_DEV Wg3 wg3(uint32_t nx, uint32_t ny) {
+  const uint32_t lin = blockIdx.x;
+  const uint32_t r = lin / nx;
+  return {(int64_t)(lin - r * nx), (int64_t)(r % ny), (int64_t)(r / ny)};
+}
+
 // ------------------------------------------------------------------------------------ forward
 template <typename TIO, int K, bool VECL>
 __global__ void __launch_bounds__(kCh) conv_silu_fwd_kernel(const TIO* __restrict__ x, const TIO* __restrict__ tail,
                                                             const float* __restrict__ w,
                                                             const float* __restrict__ bias, TIO* __restrict__ out,
                                                             int64_t L, int64_t D, int64_t sxb, int64_t sxl,
-                                                            int64_t sxd) {
+                                                            int64_t sxd, uint32_t nx, uint32_t ny) {
   constexpr int TR = TSF_CONV_FWD_TM * Tile<K>::TR;  // one input tile only: more rows between barriers
   __shared__ __align__(16) TIO s_x[TR][kCh];
   const int tid = threadIdx.x;
-  const int64_t c0 = (int64_t)blockIdx.x * kCh, d = c0 + tid, b = blockIdx.z;
-  const int64_t t0 = (int64_t)blockIdx.y * kSeg;
+  const Wg3 wg = wg3(nx, ny);
+  const int64_t c0 = wg.x * kCh, d = c0 + tid, b = wg.z;
+  const int64_t t0 = wg.y * kSeg;
   const bool live = d < D;
   const int64_t nrow = (L - t0) < kSeg ? (L - t0) : kSeg;  // stream rows: the segment's steps
   const TIO* xrow = x + b * sxb;
@@ -207,14 +220,16 @@ template <typename TIO, int K, bool VECL>
 __global__ void __launch_bounds__(kCh) conv_silu_bwd_kernel(
     const TIO* __restrict__ x, const TIO* __restrict__ tail, const float* __restrict__ w,
     const float* __restrict__ bias, const TIO* __restrict__ gy, TIO* __restrict__ gx, TIO* __restrict__ gtail,
-    float* __restrict__ part, int64_t L, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd) {
+    float* __restrict__ part, int64_t L, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd, uint32_t nx,
+    uint32_t ny) {
   constexpr int TR = TSF_CONV_BWD_TM * Tile<K>::TR;
   constexpr int KP = K + 1;
   __shared__ __align__(16) TIO s_x[TR][kCh];
   __shared__ __align__(16) TIO s_g[TR][kCh];
   const int tid = threadIdx.x;
-  const int64_t c0 = (int64_t)blockIdx.x * kCh, d = c0 + tid, b = blockIdx.z;
-  const int64_t t0 = (int64_t)blockIdx.y * kSeg;
+  const Wg3 wg = wg3(nx, ny);
+  const int64_t c0 = wg.x * kCh, d = c0 + tid, b = wg.z;
+  const int64_t t0 = wg.y * kSeg;
   const bool live = d < D;
   const int64_t own = (L - t0) < kSeg ? (L - t0) : kSeg;  // the segment's own steps
   const int64_t nrow = own + K - 1;                        // stream rows, with the right halo
@@ -289,7 +304,7 @@ __global__ void __launch_bounds__(kCh) conv_silu_bwd_kernel(
     }
   }
   if (live) {
-    float* pr = part + (((int64_t)b * gridDim.y + blockIdx.y) * D + d) * KP;
+    float* pr = part + ((b * ny + wg.y) * D + d) * KP;
 #pragma unroll
     for (int k = 0; k < KP; ++k) pr[k] = acc[k];
   }
@@ -342,12 +357,13 @@ struct Coord {
   bool live;
 };
 template <int VEC>
-TSF_DEV Coord coord(int64_t D, int64_t runs) {
+TSF_DEV Coord coord(int64_t D, int64_t runs, uint32_t nx, uint32_t ny) {
+  const Wg3 wg = wg3(nx, ny);
   const int64_t cgs = (D + VEC - 1) / VEC;
-  const int64_t cg = (int64_t)blockIdx.x * kCgWg + (threadIdx.x % kCgWg);
-  const int64_t run = (int64_t)blockIdx.y * kRunsWg + threadIdx.x / kCgWg;
+  const int64_t cg = wg.x * kCgWg + (threadIdx.x % kCgWg);
+  const int64_t run = wg.y * kRunsWg + threadIdx.x / kCgWg;
   Coord c;
-  c.b = blockIdx.z;
+  c.b = wg.z;
   c.run = run;
   c.d0 = cg * VEC;
   c.live = cg < cgs && run < runs;
@@ -375,8 +391,8 @@ template <typename TIO, int K, int VEC>
 __global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_fwd_reg(
     const TIO* __restrict__ x, const TIO* __restrict__ tail, const float* __restrict__ w,
     const float* __restrict__ bias, TIO* __restrict__ out, int64_t L, int64_t D, int64_t sxb, int64_t sxl,
-    int64_t sxd, int64_t runs) {
-  const Coord c = coord<VEC>(D, runs);
+    int64_t sxd, int64_t runs, uint32_t nx, uint32_t ny) {
+  const Coord c = coord<VEC>(D, runs, nx, ny);
   if (!c.live) return;
   float wk[K][VEC], bv[VEC];
 #pragma unroll
@@ -422,15 +438,17 @@ template <typename TIO, int K, int VEC>
 __global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_bwd_reg(
     const TIO* __restrict__ x, const TIO* __restrict__ tail, const float* __restrict__ w,
     const float* __restrict__ bias, const TIO* __restrict__ gy, TIO* __restrict__ gx, TIO* __restrict__ gtail,
-    float* __restrict__ part, int64_t L, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd, int64_t runs) {
+    float* __restrict__ part, int64_t L, int64_t D, int64_t sxb, int64_t sxl, int64_t sxd, int64_t runs,
+    uint32_t nx, uint32_t ny) {
   constexpr int KP = K + 1;
   constexpr int NP = kRunB + K - 1;  // steps whose gpre a run needs: t0 .. t0+kRunB+K-2
   __shared__ float s_part[kRunsWg][KP][kCgWg * VEC];
   const int wv = threadIdx.x / kCgWg, ln = threadIdx.x % kCgWg;
-  const int64_t cg = (int64_t)blockIdx.x * kCgWg + ln;
-  const int64_t b = blockIdx.z;
+  const Wg3 wg = wg3(nx, ny);
+  const int64_t cg = wg.x * kCgWg + ln;
+  const int64_t b = wg.z;
   const int64_t d0 = cg * VEC;
-  const int64_t run0 = ((int64_t)blockIdx.y * kRunsWg + wv) * kRpt;
+  const int64_t run0 = (wg.y * kRunsWg + wv) * kRpt;
   const TIO* xrow = x + b * sxb;
   const TIO* gyrow = gy + b * L * D;
   TIO* gxrow = gx + b * L * D;
@@ -514,15 +532,15 @@ __global__ void __launch_bounds__(kCgWg* kRunsWg) conv_silu_bwd_reg(
 #pragma unroll
     for (int ch = 0; ch < VEC; ++ch) s_part[wv][k][ln * VEC + ch] = acc[k][ch];
   __syncthreads();
-  const int64_t groups = gridDim.y;
+  const int64_t groups = ny;
   for (int idx = threadIdx.x; idx < KP * kCgWg * VEC; idx += kCgWg * kRunsWg) {
     const int k = idx / (kCgWg * VEC), dd = idx % (kCgWg * VEC);
-    const int64_t d = (int64_t)blockIdx.x * kCgWg * VEC + dd;
+    const int64_t d = wg.x * kCgWg * VEC + dd;
     if (d < D) {
       float s = 0.0f;
 #pragma unroll
       for (int r = 0; r < kRunsWg; ++r) s += s_part[r][k][dd];
-      part[((int64_t)blockIdx.z * groups + blockIdx.y) * D * KP + d * KP + k] = s;
+      part[(wg.z * groups + wg.y) * D * KP + d * KP + k] = s;
     }
   }
 }
@@ -589,13 +607,14 @@ template <typename TIO, int K>
 void fwd_k(bool vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
            const void* tail, const float* w, const float* bias, void* out, hipStream_t s) {
   const ConvPlan p = conv_plan(L, D);
-  const dim3 grid((unsigned)p.cblocks, (unsigned)p.nseg, (unsigned)B);
+  const dim3 grid((unsigned)(p.cblocks * p.nseg * B));
+  const uint32_t nx = (uint32_t)p.cblocks, ny = (uint32_t)p.nseg;
   if (vec)
     hipLaunchKernelGGL((conv_silu_fwd_kernel<TIO, K, true>), grid, dim3(kCh), 0, s, (const TIO*)x, (const TIO*)tail, w,
-                       bias, (TIO*)out, L, D, sxb, sxl, sxd);
+                       bias, (TIO*)out, L, D, sxb, sxl, sxd, nx, ny);
   else
     hipLaunchKernelGGL((conv_silu_fwd_kernel<TIO, K, false>), grid, dim3(kCh), 0, s, (const TIO*)x, (const TIO*)tail,
-                       w, bias, (TIO*)out, L, D, sxb, sxl, sxd);
+                       w, bias, (TIO*)out, L, D, sxb, sxl, sxd, nx, ny);
 }
 
 template <typename TIO, int K>
@@ -603,13 +622,14 @@ void bwd_k(bool vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb
            const void* tail, const float* w, const float* bias, const void* gy, void* gx, void* gtail, float* gw,
            float* gb, float* part, hipStream_t s) {
   const ConvPlan p = conv_plan(L, D);
-  const dim3 grid((unsigned)p.cblocks, (unsigned)p.nseg, (unsigned)B);
+  const dim3 grid((unsigned)(p.cblocks * p.nseg * B));
+  const uint32_t nx = (uint32_t)p.cblocks, ny = (uint32_t)p.nseg;
   if (vec)
     hipLaunchKernelGGL((conv_silu_bwd_kernel<TIO, K, true>), grid, dim3(kCh), 0, s, (const TIO*)x, (const TIO*)tail, w,
-                       bias, (const TIO*)gy, (TIO*)gx, (TIO*)gtail, part, L, D, sxb, sxl, sxd);
+                       bias, (const TIO*)gy, (TIO*)gx, (TIO*)gtail, part, L, D, sxb, sxl, sxd, nx, ny);
   else
     hipLaunchKernelGGL((conv_silu_bwd_kernel<TIO, K, false>), grid, dim3(kCh), 0, s, (const TIO*)x, (const TIO*)tail,
-                       w, bias, (const TIO*)gy, (TIO*)gx, (TIO*)gtail, part, L, D, sxb, sxl, sxd);
+                       w, bias, (const TIO*)gy, (TIO*)gx, (TIO*)gtail, part, L, D, sxb, sxl, sxd, nx, ny);
   const int64_t n = D * (K + 1);
   hipLaunchKernelGGL(conv_reduce_params, dim3((unsigned)((n + 63) / 64)), dim3(64 * kRedWaves), 0, s,
                      (const float*)part, gw, gb, B * p.nseg, D, K);
@@ -641,9 +661,10 @@ template <typename TIO, int K, int VEC>
 void launch_fwd(int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int64_t sxl, int64_t sxd,
                 const void* tail, const float* w, const float* bias, void* out, hipStream_t s) {
   const RegPlan p = reg_plan(L, D, VEC, kRun, kRunsWg);
-  dim3 grid((unsigned)p.cg_blocks, (unsigned)p.run_groups, (unsigned)B);
+  const dim3 grid((unsigned)(p.cg_blocks * p.run_groups * B));
   hipLaunchKernelGGL((conv_silu_fwd_reg<TIO, K, VEC>), grid, dim3(kCgWg * kRunsWg), 0, s, (const TIO*)x,
-                     (const TIO*)tail, w, bias, (TIO*)out, L, D, sxb, sxl, sxd, p.runs);
+                     (const TIO*)tail, w, bias, (TIO*)out, L, D, sxb, sxl, sxd, p.runs, (uint32_t)p.cg_blocks,
+                     (uint32_t)p.run_groups);
 }
 
 template <typename TIO, int K, int VEC>
@@ -651,10 +672,10 @@ void launch_bwd(int64_t B, int64_t L, int64_t D, const void* x, int64_t sxb, int
                 const void* tail, const float* w, const float* bias, const void* gy, void* gx, void* gtail,
                 float* gw, float* gb, float* part, hipStream_t s) {
   const RegPlan p = reg_plan(L, D, VEC, kRunB, kRunsWg * kRpt);
-  dim3 grid((unsigned)p.cg_blocks, (unsigned)p.run_groups, (unsigned)B);
+  const dim3 grid((unsigned)(p.cg_blocks * p.run_groups * B));
   hipLaunchKernelGGL((conv_silu_bwd_reg<TIO, K, VEC>), grid, dim3(kCgWg * kRunsWg), 0, s, (const TIO*)x,
                      (const TIO*)tail, w, bias, (const TIO*)gy, (TIO*)gx, (TIO*)gtail, part, L, D, sxb, sxl, sxd,
-                     p.runs);
+                     p.runs, (uint32_t)p.cg_blocks, (uint32_t)p.run_groups);
   const int64_t n = D * (K + 1);
   hipLaunchKernelGGL(conv_reduce_params, dim3((unsigned)((n + 63) / 64)), dim3(64 * kRedWaves), 0, s,
                      (const float*)part, gw, gb, B * p.run_groups, D, K);
@@ -692,9 +713,15 @@ void bwd_reg(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sx
   }
 
 // TSF_OK when the sizes are valid and supported, else the status to return
+// The grids are one-dimensional with 256-thread workgroups (kernels index it in 32 bits): at most
+// 2^24 - 1 workgroups. The register-tile forward with one channel per thread has the most,
+// ceil(D / 64) * ceil(ceil(L / 16) / 4) per batch row.
+constexpr int64_t kMaxWgs = (1 << 24) - 1;
 int conv_args_status(int64_t B, int64_t L, int64_t D, int64_t K) {
   if (B < 0 || L < 0 || D < 0 || K < 2) return TSF_ERR_ARG;
-  if (K > 8 || B > 65535 || (L + kSeg - 1) / kSeg > 65535) return TSF_ERR_UNSUPPORTED;
+  if (K > 8) return TSF_ERR_UNSUPPORTED;
+  const int64_t per_row = ((D + kCgWg - 1) / kCgWg) * ((((L + kRun - 1) / kRun) + kRunsWg - 1) / kRunsWg);
+  if (per_row > 0 && B > kMaxWgs / per_row) return TSF_ERR_UNSUPPORTED;
   return TSF_OK;
 }
 

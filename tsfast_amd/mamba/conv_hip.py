@@ -58,12 +58,13 @@ def supports(x, tail, weight, bias) -> str | None:
 
 
 def _size_reason(B: int, L: int, D: int, sxl: int, sxd: int, esz: int) -> str | None:
-    """The kernels' grid limits (conv.hip conv_args_status) and 32-bit per-row addressing
-    (conv_layout_status), repeated here so that supports() makes no library call."""
-    if B > 65535:
-        return f"batch {B} above 65535"
-    if -(-L // _SEG) > 65535:
-        return f"L={L} needs more than 65535 segments of {_SEG} steps"
+    """The kernels' grid limit (conv.hip conv_args_status: a one-dimensional grid of at most
+    2^24 - 1 workgroups, the most of which the one-channel register-tile forward launches) and
+    32-bit per-row addressing (conv_layout_status), repeated here so that supports() makes no
+    library call."""
+    per_row = -(-D // 64) * -(-(-(-L // 16)) // 4)
+    if per_row > 0 and B > ((1 << 24) - 1) // per_row:
+        return f"B={B}, L={L}, D={D} needs more than 2^24 - 1 workgroups"
     if ((L + 8) * sxl + (D + 8) * sxd) * esz >= 1 << 32 or (L + 8) * D * esz >= 1 << 32:
         return f"one batch row (L={L}, D={D}, strides {sxl}, {sxd}) exceeds the kernels' 32-bit row addressing"
     return None
