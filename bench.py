@@ -227,8 +227,11 @@ def mark(ev):
         ev.append(e)
 
 
-def cpu_time(fn, budget_s=20.0, reps=5):
-    fn()  # warmup
+def cpu_time(fn, budget_s=20.0, reps=5, warmup=3):
+    """The CPU protocol of the baseline notes: `warmup` untimed runs, then the median of up to
+    `reps` timed runs (fewer if they exceed `budget_s`); returns (median seconds, runs)."""
+    for _ in range(warmup):
+        fn()
     times = []
     t_start = time.perf_counter()
     while len(times) < reps and (time.perf_counter() - t_start) < budget_s:
@@ -276,17 +279,18 @@ def run_mamba(args, line):
             lib = CB.load(prefer_native=True)
             threads = os.cpu_count() or 1
             lib.cpu_set_threads(threads)
-            xs = mamba_inputs(1, L, D, N, io_dtype, "cpu")
+            xs = mamba_inputs(B, L, D, N, io_dtype, "cpu")
             a = {k: v.float().numpy() for k, v in xs.items()}
+            del xs
             margs = [a[k] for k in ("draw", "A", "Bt", "Ct", "u", "z", "Dp")]
-            med, n = cpu_time(lambda: CB.mamba_fwd_bwd(*margs, a["gout"]))
-            sf, sb = mamba_bytes(1, L, D, N, 2 if io_dtype == torch.bfloat16 else 4)
+            med, n = cpu_time(lambda: CB.mamba_fwd_bwd(*margs, a["gout"]), budget_s=60.0)
+            sf, sb = mamba_bytes(B, L, D, N, 2 if io_dtype == torch.bfloat16 else 4)
             return {
                 "value": round((sf + sb) / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": (f"one batch row (B=1, L={L}, D={D}, N={N}) of config 3, fp32 (reference CPU regime, "
-                           f"oracle/cpu_baseline.cpp after mamba/backend_c.py), fwd+bwd median of {n} runs = "
-                           f"{med * 1e3:.1f} ms; full config 3 would take ~{med * B * 1e3:.0f} ms; "
-                           f"build {CB.lib_path().name}"),
+                "sample": (f"the whole config 3 workload (B={B}, L={L}, D={D}, N={N}) in fp32 (the reference CPU "
+                           f"kernel's regime: the bf16 inputs upcast; oracle/cpu_baseline.cpp after "
+                           f"mamba/backend_c.py, its exp included), fwd+bwd with the partial sums, 3 warmup runs, "
+                           f"median of {n} = {med * 1e3:.1f} ms; build {CB.lib_path().name}"),
                 "ms_per_step_sample": round(med * 1e3, 3),
             }
         cpu = cpu_leg

@@ -27,8 +27,32 @@ namespace {
 constexpr int BD = 8;
 constexpr int CHK = 16;
 
-inline float softplusf(float x) { return x > 20.0f ? x : std::log1p(std::exp(x)); }
-inline float sigmoidf(float x) { return 1.0f / (1.0f + std::exp(-x)); }
+// The reference CPU kernel's own exp (mamba/backend_c.py:55-74), so that this column times the
+// reference's CPU arithmetic: clamp to [-88, 88]; x = k ln2 + r with k = round(x / ln2), ln2
+// taken as the float 0.693359375 minus 2.12194440e-4 (a Cody-Waite split: k * 0.693359375 is
+// exact in float for |k| <= 128); e^r by its Taylor series through r^6 / 6!; 2^k from the
+// exponent bits. Plain arithmetic keeps the state loop vectorisable, as in the reference.
+inline float ref_expf(float x) {
+  x = std::min(88.0f, std::max(-88.0f, x));
+  const float t = x * 1.44269504088896341f;
+  const int32_t k = (int32_t)(t >= 0.0f ? t + 0.5f : t - 0.5f);
+  const float kf = (float)k;
+  const float r = (x - kf * 0.693359375f) + kf * 2.12194440e-4f;
+  // sum_{n<=6} r^n / n!, Horner form from the highest power
+  float p = 1.0f / 720.0f;
+  p = p * r + 1.0f / 120.0f;
+  p = p * r + 1.0f / 24.0f;
+  p = p * r + 1.0f / 6.0f;
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  int32_t bits = (k + 127) << 23;
+  float scale;
+  std::memcpy(&scale, &bits, sizeof(scale));
+  return p * scale;
+}
+inline float softplusf(float x) { return x > 20.0f ? x : std::log1p(ref_expf(x)); }
+inline float sigmoidf(float x) { return 1.0f / (1.0f + ref_expf(-x)); }
 
 template <int N>
 void mamba_fwd_t(int64_t B, int64_t L, int64_t D, const float* draw, const float* A, const float* Bt,
@@ -53,7 +77,7 @@ void mamba_fwd_t(int64_t B, int64_t L, int64_t D, const float* draw, const float
         float acc = 0.0f;
 #pragma omp simd reduction(+ : acc)
         for (int n = 0; n < N; ++n) {
-          const float hv = std::exp(dl * a[n]) * h[j][n] + du * bt[n];
+          const float hv = ref_expf(dl * a[n]) * h[j][n] + du * bt[n];
           h[j][n] = hv;
           acc += hv * ct[n];
         }
@@ -107,7 +131,7 @@ void mamba_bwd_t(int64_t B, int64_t L, int64_t D, const float* draw, const float
           dbuf[i][j] = dl;
 #pragma omp simd
           for (int n = 0; n < N; ++n) {
-            hs[j][n] = std::exp(dl * a[n]) * hs[j][n] + du * bt[n];
+            hs[j][n] = ref_expf(dl * a[n]) * hs[j][n] + du * bt[n];
             hbuf[i][j][n] = hs[j][n];
           }
         }
@@ -133,7 +157,7 @@ void mamba_bwd_t(int64_t B, int64_t L, int64_t D, const float* draw, const float
           if (t + 1 < L) {
             const float dn = softplusf(draw[row + j + D]);
 #pragma omp simd
-            for (int n = 0; n < N; ++n) G[j][n] = gy * ct[n] + std::exp(dn * a[n]) * G[j][n];
+            for (int n = 0; n < N; ++n) G[j][n] = gy * ct[n] + ref_expf(dn * a[n]) * G[j][n];
           } else {
             for (int n = 0; n < N; ++n) G[j][n] = gy * ct[n] + G[j][n];
           }
@@ -160,7 +184,7 @@ void mamba_bwd_t(int64_t B, int64_t L, int64_t D, const float* draw, const float
       for (int j = 0; j < nd; ++j) {
         const float* a = A + (d0 + j) * N;
         const float d_0 = L > 0 ? softplusf(draw[b * L * D + d0 + j]) : 0.0f;
-        for (int n = 0; n < N; ++n) gh0[(b * D + d0 + j) * N + n] = std::exp(d_0 * a[n]) * G[j][n];
+        for (int n = 0; n < N; ++n) gh0[(b * D + d0 + j) * N + n] = ref_expf(d_0 * a[n]) * G[j][n];
       }
     }
   }
@@ -312,6 +336,11 @@ extern "C" {
 
 int cpu_num_threads(void) { return omp_get_max_threads(); }
 void cpu_set_threads(int n) { omp_set_num_threads(n); }
+
+// ref_expf elementwise (for its accuracy pin in the tests)
+void cpu_ref_expf(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = ref_expf(x[i]);
+}
 
 int cpu_mamba_chk(void) { return CHK; }
 int cpu_mamba_bd(void) { return BD; }

@@ -79,12 +79,22 @@ def load(prefer_native: bool = True) -> ctypes.CDLL:
         getattr(lib, name).restype = i32
     lib.cpu_set_threads.argtypes = [i32]
     lib.cpu_set_threads.restype = None
+    lib.cpu_ref_expf.argtypes = [ptr, ptr, i64]
+    lib.cpu_ref_expf.restype = None
     _lib, _lib_path = lib, path
     return lib
 
 
 def lib_path() -> Path | None:
     return _lib_path
+
+
+def ref_expf(x: np.ndarray) -> np.ndarray:
+    """The port's restatement of the reference CPU kernel's exp (backend_c.py:55-74), elementwise."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    load().cpu_ref_expf(_p(x), _p(y), x.size)
+    return y
 
 
 def _p(a: np.ndarray | None):

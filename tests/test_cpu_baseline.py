@@ -1,6 +1,8 @@
 """The CPU-baseline port (oracle/cpu_baseline.cpp) computes the same thing as the fp64 oracle,
 so the bench's CPU column times the right work."""
 
+import math
+
 import numpy as np
 import pytest
 
@@ -97,3 +99,26 @@ def test_torch_reference_conv_matches_oracle():
     x, tail, w, b = (rng.standard_normal(s) for s in ((B, L, D), (B, D, K - 1), (D, 1, K), (D,)))
     y = TR.causal_depthwise_silu(*(torch.tensor(t) for t in (x, tail, w, b)))
     assert O.rel_err(y.numpy(), O.conv_silu_forward(x, tail, w[:, 0], b)) < 1e-12
+
+
+def test_ref_expf_is_the_reference_cpu_exp(lib):
+    """The port's exp restates the reference CPU kernel's (range reduction to 2^k, Taylor series
+    through r^6 / 6!, clamp to [-88, 88]; backend_c.py:55-74): within 2e-7 relative of the true
+    exponential on [-1, 1] (k = 0 or +-1), within 5e-6 wherever 2^k is a normal float (built with
+    the reference's -ffast-math, the compiler may fold the two-part ln 2 of the reduction into one
+    rounded product, so r carries up to half an ulp of x), exact at 0, clamped above 88, and zero
+    where k reaches -127 (the exponent-bits scale is then 0). A series cut one term short
+    (r^5 / 5!) misses the [-1, 1] bound."""
+    x = np.linspace(-1, 1, 20_001).astype(np.float32)
+    got = CB.ref_expf(x).astype(np.float64)
+    want = np.exp(x.astype(np.float64))
+    assert np.max(np.abs(got / want - 1)) < 2e-7
+    xw = np.linspace(-87.0, 87.9, 200_001).astype(np.float32)
+    assert np.max(np.abs(CB.ref_expf(xw).astype(np.float64) / np.exp(xw.astype(np.float64)) - 1)) < 5e-6
+    assert CB.ref_expf(np.zeros(1))[0] == 1.0
+    assert CB.ref_expf(np.array([100.0]))[0] == CB.ref_expf(np.array([88.0]))[0]
+    assert CB.ref_expf(np.array([-88.0]))[0] == 0.0 and CB.ref_expf(np.array([-1000.0]))[0] == 0.0
+    # the mutant: drop the r^6 term of the same reduction
+    r = x.astype(np.float64) - np.round(x.astype(np.float64) / np.log(2)) * np.log(2)
+    short = np.exp(x.astype(np.float64) - r) * sum(r**n / math.factorial(n) for n in range(6))
+    assert np.max(np.abs(short / want - 1)) > 2e-7
