@@ -201,7 +201,8 @@ int tsfast_hip_conv_silu_bwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_
  * :219-222, the tsfast::dynonet_allpole op at :225-235 and a sum at :250), per pair p = j*O + o:
  *   w_p[t] = sum_k b[o,j,k] u[t-k, j],  y_p[t] = w_p[t] - sum_i a[o,j,i] y_p[t-i],
  *   y[t, o] = sum_j y_p[t],  x_last[p, q] = y_p[L-1-q] (x0 beyond the start).
- * float32 in and out, fp64 state; 1 <= na <= 4, 1 <= nb <= 16, I*O dividing 64, else
+ * float32 in and out, fp64 state; 1 <= na <= 4, 1 <= nb <= 16, I*O <= 64 (a caller splits a
+ * larger block into groups of whole inputs or outputs and adds their outputs), else
  * TSF_ERR_UNSUPPORTED. Layout: u/gu [B, L, I], y/gy [B, L, O] (channel-last, contiguous),
  * b/gb [O, I, nb], a/ga [O, I, na], u_tail/gu_tail [B, nb-1, I] (the carried FIR input; NULL =
  * zeros), x0/gx0/x_last/g_xlast [B, I*O, na] newest first (NULL x0 = zeros; x_last, g_xlast may

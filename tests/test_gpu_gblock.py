@@ -3,8 +3,10 @@
 The oracle (oracle/scan_oracle.py::gblock_forward/backward) is pinned against float64 autograd
 through the reference's own formulation (grouped conv1d, a sequential all-pole loop, the sum
 over inputs; tests/test_oracle.py). Shapes cover every tap padding (nb 1..16 -> 2, 4, 8, 16),
-every order na 1..4, pair counts 1..64 (64 / (I*O) batch rows per tile), sequences shorter
-than na and than one chunk, many super-chunks, and absent initial state. Bar: max relative
+every order na 1..4, pair counts that divide 64 (64 / (I*O) batch rows per tile) and that do
+not (a batch row padded to the next power of two: 3, 15, 24 and 40 pairs), more than 64 pairs
+(run as groups of inputs, and of outputs past 64), sequences shorter than na and than one chunk,
+many super-chunks, and absent initial state. Bar: max relative
 error <= 1e-5 for outputs, the returned state and every gradient (fp32 I/O, fp64 state).
 """
 
@@ -59,6 +61,16 @@ _SHAPES = [
     # whose pairs (lane % P) repeat the first tile's (coefficients and transfer matrices staged once)
     (5, 700, 4, 4, 8, 3),  # 80 lanes, matrices in LDS
     (9, 500, 2, 4, 4, 4),  # 72 lanes, na 4: matrices read from global memory
+    # pair counts that do not divide 64: each batch row padded to the next power of two
+    (3, 900, 3, 8, 8, 2),  # 24 pairs (DynoNet(input_size=3)'s first block): 32 lanes per row
+    (4, 600, 8, 3, 8, 2),  # 24 pairs, input-major with 3 outputs
+    (5, 700, 5, 3, 6, 3),  # 15 pairs: 80 lanes, a partial second tile
+    (7, 333, 3, 1, 4, 4),  # 3 pairs, na 4
+    (3, 500, 5, 8, 8, 3),  # 40 pairs: 24 idle lanes per row
+    (2, 5000, 3, 5, 16, 4),  # 15 pairs, 16 taps, many super-chunks
+    # more than 64 pairs: groups of inputs (and of outputs past 64 outputs)
+    (2, 400, 9, 8, 8, 2),  # 72 pairs: inputs 0..7 and 8
+    (2, 300, 2, 70, 4, 1),  # 140 pairs: 64 + 6 outputs, one input per group
 ]
 
 
@@ -106,6 +118,20 @@ def test_gblock_operator_dispatch_and_chunked_state(gpu):
     assert torch.equal(st2["u"], st_full["u"])
 
 
+def test_dynonet_default_blocks_take_the_fused_kernel(gpu):
+    """DynoNet(input_size=3, output_size=2) builds G-blocks of 3 x 8, 8 x 2 and 3 x 2 pairs
+    (dynonet/core.py:304-306): every one resolves to the fused kernel and matches the oracle."""
+    for I, O_ in ((3, 8), (8, 2), (3, 2)):
+        B, L, nb, na = 2, 500, 8, 2
+        u, b, a, _, _, _, _ = _make(B, L, I, O_, nb, na, seed=I * 10 + O_)
+        u, b, a = u.to(gpu), b.to(gpu), a.to(gpu)
+        zeros = (u.new_zeros(B, nb - 1, I), u.new_zeros(B, I * O_, na))
+        assert dispatch.resolve("dynonet.gblock", dcore._GBLOCK_BACKENDS, ("hip",), (u, b, a, *zeros)) is gblock_hip
+        y = dcore.linear_dynamical_operator(u, b, a)
+        want, _, _ = O.gblock_forward(_np(u), _np(b), _np(a), np.zeros((B, nb - 1, I)), np.zeros((B, I * O_, na)))
+        assert O.rel_err(_np(y), want) < TOL
+
+
 def test_gblock_matches_unfused_path(gpu):
     """The fused kernel and the reference's three-stage path (conv1d, all-pole op, sum) agree."""
     B, L, I, O_, nb, na = 4, 1500, 8, 8, 8, 3
@@ -125,7 +151,8 @@ def test_gblock_supports_reasons(gpu):
     u = torch.randn(2, 10, 3, device=gpu)
     b = torch.randn(5, 3, 4, device=gpu)
     a = torch.randn(5, 3, 2, device=gpu)
-    assert "divide 64" in gblock_hip.supports(u, b, a, None, None)
+    assert gblock_hip.supports(u, b, a, None, None) is None  # 15 pairs
+    assert "taps" in gblock_hip.supports(u, torch.randn(5, 3, 17, device=gpu), a, None, None)
     b2, a2 = torch.randn(2, 3, 4, device=gpu), torch.randn(2, 3, 5, device=gpu)
     assert "order" in gblock_hip.supports(u[..., :2], b2[:, :2], a2[:, :2], None, None)
     assert "GPU-only" in gblock_hip.supports(u.cpu(), b.cpu(), a.cpu(), None, None)

@@ -12,7 +12,8 @@
 // Neither the FIR output w nor the per-pair outputs y_p (each [B, P, L], P times the size of u)
 // ever reach HBM: the forward reads u and writes y; the backward reads u and gy and writes gu.
 // Both run the single-pass look-back scheme of the all-pole kernels (allpole_core.h) over lanes
-// lane = b * P + p, 64 lanes (64 / P whole batch rows) to a tile:
+// lane = b * Pp + p, where Pp is P rounded up to a power of two (a batch row's lanes p >= P are
+// idle: zero inputs, nothing stored), 64 lanes (64 / Pp whole batch rows) to a tile:
 //   forward   each wave loads its lanes' u window (its 32-step chunk plus the nb - 1 step FIR
 //             halo, straight from u: the lanes of one batch row read a few contiguous bytes per
 //             step), forms w, runs the all-pole scan with look-back, saves each super-chunk's
@@ -25,7 +26,7 @@
 //             gradient; forming it from B^T g needs only the gy halo to the right, not another
 //             tile's G. grad a = -sum G_t y_{t-i} and grad b = sum G_t u_{t-k} are reduced per
 //             tile; gu (sum of c over o) and the tail gradient go through LDS.
-// Orders na <= 4, nb <= 16 (taps padded to NBT in {2, 4, 8, 16} with zeros), I * O dividing 64.
+// Orders na <= 4, nb <= 16 (taps padded to NBT in {2, 4, 8, 16} with zeros), I * O <= 64.
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -37,20 +38,31 @@ namespace {
 
 constexpr int kGbMaxNB = 16;
 
+// lane = b * Pp + p in the padded lane space; rl = b * P + p indexes the caller's per-pair state
+// tensors (x0, x_last and their gradients, [B, P, na]).
 struct GbLane {
-  int64_t b;
+  int64_t b, rl;
   int p, j, o;
   bool live;
 };
-TSF_DEV GbLane gb_lane(int64_t lane, int64_t lanes, int P, int O) {
+TSF_DEV GbLane gb_lane(int64_t lane, int64_t lanes, int P, int Pp, int O) {
   GbLane g;
-  g.live = lane < lanes;
-  const int64_t l = g.live ? lane : 0;
-  g.b = l / P;
-  g.p = (int)(l - g.b * P);
+  const int64_t l = lane < lanes ? lane : 0;
+  g.b = l / Pp;
+  g.p = (int)(l - g.b * Pp);
+  g.live = lane < lanes && g.p < P;
+  if (!g.live) g.p = 0;
   g.j = g.p / O;
   g.o = g.p - g.j * O;
+  g.rl = g.b * P + g.p;
   return g;
+}
+
+// P pairs per batch row rounded up to a power of two (P <= 64), so 64 / Pp batch rows fill a tile.
+TSF_HOST_DEV int padded_pairs(int P) {
+  int pp = 1;
+  while (pp < P) pp *= 2;
+  return pp;
 }
 
 // The lane's FIR input u_s for s in [t0 - (NBT - 1), t0 + kTileT): u [B, L, I] for s in [0, L),
@@ -90,28 +102,33 @@ TSF_DEV void fir(float (&w)[kTileT], const float (&uw)[kTileT + NBT - 1], const 
   }
 }
 
-// The coefficients of pair lid % P, the pair that lane l0 + lid holds in every tile (l0 a multiple
-// of 64 and I * O dividing 64): loaded once per workgroup. Lanes beyond the tensor see zero inputs,
-// so their coefficients do not matter.
+// The coefficients of pair lid % Pp, the pair that lane l0 + lid holds in every tile (l0 a multiple
+// of 64 and Pp dividing 64): loaded once per workgroup. Idle lanes (padding or beyond the tensor)
+// see zero inputs and store nothing; they take pair 0's coefficients.
 template <int NA, int NBT>
 TSF_DEV void load_pair_coeffs(double (&av)[NA], float (&bk)[NBT], const float* __restrict__ bcoef,
-                              const float* __restrict__ acoef, int lid, int I, int O, int nb) {
-  const int p = lid % (I * O), pair = (p % O) * I + p / O;  // [O, I, .] parameter layout
+                              const float* __restrict__ acoef, int lid, int I, int O, int nb, int Pp) {
+  int p = lid % Pp;
+  if (p >= I * O) p = 0;
+  const int pair = (p % O) * I + p / O;  // [O, I, .] parameter layout
 #pragma unroll
   for (int q = 0; q < NA; ++q) av[q] = (double)acoef[pair * NA + q];
 #pragma unroll
   for (int k = 0; k < NBT; ++k) bk[k] = k < nb ? bcoef[pair * nb + k] : 0.0f;
 }
 
-// Transfer matrices per lane from its pair's coefficients a [O, I, NA] (lane = b * P + j * O + o).
-// One thread per (lane, column).
+// Transfer matrices per lane from its pair's coefficients a [O, I, NA] (lane = b * Pp + j * O + o;
+// padding lanes take pair 0's). One thread per (lane, column).
 template <int NA>
 __global__ void __launch_bounds__(64) gblock_transfer(const float* __restrict__ acoef, double* __restrict__ Mc,
-                                                      double* __restrict__ Ms, int64_t lanes, int I, int O, int K) {
+                                                      double* __restrict__ Ms, int64_t lanes, int I, int O, int Pp,
+                                                      int K) {
   const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (idx >= lanes * NA) return;
   const int64_t lane = idx / NA;
-  const int P = I * O, p = (int)(lane % P), j = p / O, o = p % O;
+  int p = (int)(lane % Pp);
+  if (p >= I * O) p = 0;
+  const int j = p / O, o = p % O;
   companion_powers_col<NA>(acoef + (o * I + j) * NA, Mc + lane * NA * NA, Ms + lane * NA * NA, K,
                            (int)(idx - lane * NA));
 }
@@ -122,7 +139,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
     const float* __restrict__ u, const float* __restrict__ bcoef, const float* __restrict__ acoef,
     const float* __restrict__ u_tail, const float* __restrict__ x0, float* __restrict__ y, float* __restrict__ x_last,
     double* __restrict__ saved, const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg,
-    double* __restrict__ inc, unsigned* __restrict__ counter, int64_t B, int64_t L, int I, int O, int nb,
+    double* __restrict__ inc, unsigned* __restrict__ counter, int64_t B, int64_t L, int I, int O, int Pp, int nb,
     int64_t groups, int K, int64_t nsuper, int lb_spacing) {
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
@@ -131,13 +148,13 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
   __shared__ unsigned s_tile[2];
   __shared__ double s_mat[MatStage<NA>::kDoubles];
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int P = I * O, R = kTile / P;
-  const int64_t lanes = B * P;
+  const int P = I * O, R = kTile / Pp;
+  const int64_t lanes = B * Pp;
   const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
   // the pair's coefficients and transfer matrices are the same in every tile (load_pair_coeffs)
   double av[NA];
   float bk[NBT];
-  load_pair_coeffs<NA, NBT>(av, bk, bcoef, acoef, lid, I, O, nb);
+  load_pair_coeffs<NA, NBT>(av, bk, bcoef, acoef, lid, I, O, nb, Pp);
   if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, 0, lanes);
   if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
   __syncthreads();
@@ -147,7 +164,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
     unsigned next = 0;
     if (threadIdx.x == 0) next = take_tile(counter);
     const int64_t sc = tile / groups, l0 = (tile - sc * groups) * kTile, lane = l0 + lid;
-    const GbLane g = gb_lane(lane, lanes, P, O);
+    const GbLane g = gb_lane(lane, lanes, P, Pp, O);
     const bool live = g.live;
     const int64_t t0 = sc * SL + (int64_t)k * kTileT;
     const int n = (L - t0) >= kTileT ? kTileT : (L - t0) > 0 ? (int)(L - t0) : 0;
@@ -190,7 +207,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
     }
     double S[NA];
 #pragma unroll
-    for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[lane * NA + q] : 0.0;
+    for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[g.rl * NA + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       ap_look_back<NA>(S, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
                        k, lid, s_lds, s_flag, s_pend, &s_any, counter);
@@ -233,7 +250,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
       // the delay line after the sequence's last step is the returned state (newest first)
       if (x_last && live && t0 + n == L) {
 #pragma unroll
-        for (int q = 0; q < NA; ++q) x_last[lane * NA + q] = (float)s[q];
+        for (int q = 0; q < NA; ++q) x_last[g.rl * NA + q] = (float)s[q];
       }
       // y[b, t, o] = sum_j y_{j*O+o}[t]: the pairs' rows meet in the wave's LDS tile
       float(*tl)[kTileT + 1] = s_lds[k];
@@ -241,14 +258,14 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
 #pragma unroll
       for (int i = 0; i < kTileT; ++i) tl[lid][i] = xb[i];
       __builtin_amdgcn_wave_barrier();
-      const int64_t b0 = l0 / P;
+      const int64_t b0 = l0 / Pp;
       for (int qi = lid; qi < R * kTileT * O; qi += kTile) {
         const int o = qi % O, i = (qi / O) % kTileT, rb = qi / (O * kTileT);
         const int64_t bb = b0 + rb;
         if (i < n && bb < B) {
           float acc = 0.0f;
 #pragma unroll 8
-          for (int jj = 0; jj < I; ++jj) acc += tl[rb * P + jj * O + o][i];  // reads go out together
+          for (int jj = 0; jj < I; ++jj) acc += tl[rb * Pp + jj * O + o][i];  // reads go out together
           y[(bb * L + t0 + i) * O + o] = acc;
         }
       }
@@ -275,7 +292,8 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     const float* __restrict__ x0, const double* __restrict__ saved, const double* __restrict__ Mc,
     const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc, unsigned* __restrict__ counter,
     float* __restrict__ gu, float* __restrict__ gu_tail, double* __restrict__ part_ga, double* __restrict__ part_gb,
-    double* __restrict__ gh, int64_t B, int64_t L, int I, int O, int nb, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
+    double* __restrict__ gh, int64_t B, int64_t L, int I, int O, int Pp, int nb, int64_t groups, int K, int64_t nsuper,
+    int lb_spacing) {
   static_assert(64 * (NA * sizeof(double) + NBT * sizeof(float)) <= sizeof(LdsTile), "partials fit in a tile");
   constexpr int V = 2 * NA;  // adjoint state: G then c
   __shared__ LdsTile s_lds[kLbWaves];
@@ -290,13 +308,13 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
   __shared__ float s_uw[kStashU ? kLbWaves : 1][kStashU ? 64 : 1][kStashU ? kUW : 1];
   __shared__ double s_st[64][NA];  // the super-chunk's saved entering state, prefetched by wave 0
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
-  const int P = I * O, R = kTile / P;
-  const int64_t lanes = B * P;
+  const int P = I * O, R = kTile / Pp;
+  const int64_t lanes = B * Pp;
   const int64_t tiles = groups * nsuper, SL = (int64_t)K * kTileT;
   // the pair's coefficients and transfer matrices are the same in every tile (load_pair_coeffs)
   double av[NA];
   float bk[NBT];
-  load_pair_coeffs<NA, NBT>(av, bk, bcoef, acoef, lid, I, O, nb);
+  load_pair_coeffs<NA, NBT>(av, bk, bcoef, acoef, lid, I, O, nb, Pp);
   if constexpr (MatStage<NA>::kLds) stage_mats<NA>(s_mat, Mc, Ms, 0, lanes);
   if (threadIdx.x == 0) s_tile[0] = take_tile(counter);
   __syncthreads();
@@ -306,7 +324,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     unsigned next = 0;
     if (threadIdx.x == 0) next = take_tile(counter);
     const int64_t r = tile / groups, sc = nsuper - 1 - r, l0 = (tile - r * groups) * kTile, lane = l0 + lid;
-    const GbLane g = gb_lane(lane, lanes, P, O);
+    const GbLane g = gb_lane(lane, lanes, P, Pp, O);
     const bool live = g.live;
     const int64_t t0 = sc * SL + (int64_t)k * kTileT;
     const int n = (L - t0) >= kTileT ? kTileT : (L - t0) > 0 ? (int)(L - t0) : 0;
@@ -320,7 +338,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
       for (int i = 0; i < kTileT + NBT - 1; ++i) {
         const int64_t s2 = t0 + i;
         float v = (live && s2 < L) ? grow[s2 * O] : 0.0f;
-        if (g_xlast && live && s2 < L && s2 >= L - NA) v += g_xlast[lane * NA + (L - 1 - s2)];
+        if (g_xlast && live && s2 < L && s2 >= L - NA) v += g_xlast[g.rl * NA + (L - 1 - s2)];
         gw_[i] = v;
       }
     };
@@ -332,7 +350,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     if (k == 0) {
 #pragma unroll
       for (int q = 0; q < NA; ++q)
-        st_pre[q] = !live ? 0.0 : sc == 0 ? (x0 ? (double)x0[lane * NA + q] : 0.0) : saved[(sc * lanes + lane) * NA + q];
+        st_pre[q] = !live ? 0.0 : sc == 0 ? (x0 ? (double)x0[g.rl * NA + q] : 0.0) : saved[(sc * lanes + lane) * NA + q];
     }
     {
       // --- zero-state summaries of both adjoint recurrences over the chunk, right to left
@@ -484,14 +502,14 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
 #pragma unroll
       for (int i = 0; i < kTileT; ++i) tl[lid][i] = xb[i];
       __builtin_amdgcn_wave_barrier();
-      const int64_t b0 = l0 / P;
+      const int64_t b0 = l0 / Pp;
       for (int qi = lid; qi < R * kTileT * I; qi += kTile) {
         const int jj = qi % I, i = (qi / I) % kTileT, rb = qi / (I * kTileT);
         const int64_t bb = b0 + rb;
         if (i < n && bb < B) {
           float acc = 0.0f;
 #pragma unroll 8
-          for (int o = 0; o < O; ++o) acc += tl[rb * P + jj * O + o][i];  // reads go out together
+          for (int o = 0; o < O; ++o) acc += tl[rb * Pp + jj * O + o][i];  // reads go out together
           gu[(bb * L + t0 + i) * I + jj] = acc;
         }
       }
@@ -534,7 +552,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
           if (bb < B) {
             float acc = 0.0f;
 #pragma unroll 8
-            for (int o = 0; o < O; ++o) acc += tl[rb * P + jj * O + o][m + NBT - nb];
+            for (int o = 0; o < O; ++o) acc += tl[rb * Pp + jj * O + o][m + NBT - nb];
             gu_tail[(bb * (nb - 1) + m) * I + jj] = acc;
           }
         }
@@ -583,12 +601,15 @@ __global__ void __launch_bounds__(1024) gblock_finish_lane(
     const float* __restrict__ acoef, const float* __restrict__ x0, const float* __restrict__ g_xlast,
     const double* __restrict__ gh, const double* __restrict__ part_ga, const double* __restrict__ part_gb,
     double* __restrict__ ga_lane, double* __restrict__ gb_lane, float* __restrict__ gx0, int64_t lanes, int I, int O,
-    int64_t L, int64_t n) {
+    int Pp, int64_t L, int64_t n) {
   __shared__ double s_p[16][64];
   __shared__ double s_tot[NA + NBT][64];
   const int lid = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int64_t lane = blockIdx.x * 64 + lid;
-  const bool live = lane < lanes;
+  const int P = I * O;
+  const int p = (int)(lane % Pp);
+  const bool live = lane < lanes && p < P;
+  const int64_t rl = lane / Pp * P + p;  // the caller's [B, P, na] row
   const int64_t seg = (n + 15) / 16;
   const int64_t r0 = k * seg, r1 = (r0 + seg < n) ? r0 + seg : n;
   for (int q = 0; q < NA + NBT; ++q) {
@@ -606,8 +627,7 @@ __global__ void __launch_bounds__(1024) gblock_finish_lane(
     __syncthreads();
   }
   if (k != 0 || !live) return;  // no barrier follows
-  const int P = I * O;
-  const int p = (int)(lane % P), j = p / O, o = p % O;
+  const int j = p / O, o = p % O;
   const int pair = o * I + j;
   double Gh[NA];  // G_0 .. G_{NA-1}, zero past the end of the sequence
 #pragma unroll
@@ -617,7 +637,7 @@ __global__ void __launch_bounds__(1024) gblock_finish_lane(
     double t = s_tot[q][lid];
     if (x0) {
 #pragma unroll
-      for (int jj = 1; jj <= q + 1; ++jj) t = fma(Gh[q + 1 - jj], (double)x0[lane * NA + jj - 1], t);
+      for (int jj = 1; jj <= q + 1; ++jj) t = fma(Gh[q + 1 - jj], (double)x0[rl * NA + jj - 1], t);
     }
     ga_lane[lane * NA + q] = -t;
   }
@@ -631,8 +651,8 @@ __global__ void __launch_bounds__(1024) gblock_finish_lane(
       for (int i = jj + 1; i <= NA; ++i) t = fma((double)acoef[pair * NA + i - 1], Gh[i - 1 - jj], t);
       t = -t;
       // x_last[q] = x0[q - L] for q >= L: that part of the x_last gradient reaches x0 directly
-      if (g_xlast && jj + L < NA) t += (double)g_xlast[lane * NA + jj + L];
-      gx0[lane * NA + jj] = (float)t;
+      if (g_xlast && jj + L < NA) t += (double)g_xlast[rl * NA + jj + L];
+      gx0[rl * NA + jj] = (float)t;
     }
   }
 }
@@ -641,7 +661,8 @@ __global__ void __launch_bounds__(1024) gblock_finish_lane(
 template <int NA, int NBT>
 __global__ void __launch_bounds__(256) gblock_finish_pairs(const double* __restrict__ ga_lane,
                                                             const double* __restrict__ gb_lane, float* __restrict__ ga,
-                                                            float* __restrict__ gb, int64_t B, int I, int O, int nb) {
+                                                            float* __restrict__ gb, int64_t B, int I, int O, int Pp,
+                                                            int nb) {
   const int P = I * O;
   const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (idx >= (int64_t)P * (NA + nb)) return;
@@ -650,7 +671,7 @@ __global__ void __launch_bounds__(256) gblock_finish_pairs(const double* __restr
   double t = 0.0;
 #pragma unroll 8
   for (int64_t b = 0; b < B; ++b)
-    t += q < NA ? ga_lane[(b * P + p) * NA + q] : gb_lane[(b * P + p) * NBT + (q - NA)];
+    t += q < NA ? ga_lane[(b * Pp + p) * NA + q] : gb_lane[(b * Pp + p) * NBT + (q - NA)];
   if (q < NA)
     ga[pair * NA + q] = (float)t;
   else
@@ -677,7 +698,8 @@ int nbt_for(int64_t nb) { return nb <= 2 ? 2 : nb <= 4 ? 4 : nb <= 8 ? 8 : 16; }
 // per-lane grad a / grad b [lanes][na | NBT], and the transfer matrices Mc, Ms [lanes][na][na].
 struct GbPlan {
   LbPlan lb;
-  int64_t lanes = 0;
+  int64_t lanes = 0;  // B * Pp: batch rows padded to a power-of-two pair count
+  int pp = 1;
   int nbt = 2;
   size_t off_agg = 0, off_inc = 0, off_pa = 0, off_pb = 0, off_gh = 0, off_gal = 0, off_gbl = 0, off_Mc = 0,
          off_Ms = 0, bytes = 0;
@@ -685,7 +707,8 @@ struct GbPlan {
 
 GbPlan gb_plan(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na) {
   GbPlan p;
-  p.lanes = B * I * O;
+  p.pp = padded_pairs((int)(I * O));
+  p.lanes = B * p.pp;
   p.nbt = nbt_for(nb);
   p.lb = lb_plan(p.lanes, L, na);
   const size_t f = 8, rows = (size_t)p.lb.nsuper * p.lanes;
@@ -704,7 +727,7 @@ GbPlan gb_plan(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t n
 
 int gb_args_status(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, int64_t na) {
   if (B < 0 || L < 0 || I < 1 || O < 1 || nb < 1 || na < 1) return TSF_ERR_ARG;
-  if (na > kLbNA || nb > kGbMaxNB || kTile % (I * O) != 0) return TSF_ERR_UNSUPPORTED;
+  if (na > kLbNA || nb > kGbMaxNB || I * O > kTile) return TSF_ERR_UNSUPPORTED;
   if (B * I * O * (L > 0 ? L : 1) >= ((int64_t)1 << 40)) return TSF_ERR_UNSUPPORTED;
   return TSF_OK;
 }
@@ -716,13 +739,15 @@ void fwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
   static int occ[kMaxNA + 1];
   double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
   double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-  hipLaunchKernelGGL((gblock_transfer<NA>), transfer_grid(p.lanes, NA), dim3(64), 0, s, acoef, Mc, Ms, p.lanes, I, O, p.lb.K);
+  hipLaunchKernelGGL((gblock_transfer<NA>), transfer_grid(p.lanes, NA), dim3(64), 0, s, acoef, Mc, Ms, p.lanes, I, O,
+                     p.pp, p.lb.K);
   lookback_reset_launch(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, s);
   const int64_t tiles = p.lb.groups * p.lb.nsuper, cap = resident_wgs(gblock_fwd_lb<NA, NBT>, 64 * p.lb.K, occ);
   hipLaunchKernelGGL((gblock_fwd_lb<NA, NBT>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.lb.K), 0, s, u,
                      bcoef, acoef, u_tail, x0, y, x_last, saved, (const double*)Mc, (const double*)Ms,
                      reinterpret_cast<double*>(ws + p.off_agg), reinterpret_cast<double*>(ws + p.off_inc),
-                     reinterpret_cast<unsigned*>(ws), B, L, I, O, nb, p.lb.groups, p.lb.K, p.lb.nsuper, lb_spacing_for(p.lb.K));
+                     reinterpret_cast<unsigned*>(ws), B, L, I, O, p.pp, nb, p.lb.groups, p.lb.K, p.lb.nsuper,
+                     lb_spacing_for(p.lb.K));
 }
 
 template <int NA, int NBT>
@@ -738,14 +763,14 @@ void bwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
     double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
     double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
     hipLaunchKernelGGL((gblock_transfer<NA>), transfer_grid(p.lanes, NA), dim3(64), 0, s, acoef, Mc, Ms, p.lanes, I, O,
-                       p.lb.K);
+                       p.pp, p.lb.K);
     lookback_reset_launch(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, s);
     const int64_t tiles = p.lb.groups * p.lb.nsuper, cap = resident_wgs(gblock_bwd_lb<NA, NBT>, 64 * p.lb.K, occ);
     hipLaunchKernelGGL((gblock_bwd_lb<NA, NBT>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.lb.K), 0, s,
                        gy, g_xlast, u, bcoef, acoef, u_tail, x0, saved, (const double*)Mc, (const double*)Ms,
                        reinterpret_cast<double*>(ws + p.off_agg), reinterpret_cast<double*>(ws + p.off_inc),
-                       reinterpret_cast<unsigned*>(ws), gu, gu_tail, pa, pb, gh, B, L, I, O, nb, p.lb.groups, p.lb.K,
-                       p.lb.nsuper, lb_spacing_for(p.lb.K));
+                       reinterpret_cast<unsigned*>(ws), gu, gu_tail, pa, pb, gh, B, L, I, O, p.pp, nb, p.lb.groups,
+                       p.lb.K, p.lb.nsuper, lb_spacing_for(p.lb.K));
   } else if (gu_tail && nb > 1) {
     const int64_t nt = B * (nb - 1) * I;
     hipLaunchKernelGGL(gblock_zero, grid_for(nt), dim3(256), 0, s, gu_tail, nt);
@@ -754,10 +779,10 @@ void bwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
   double* gbl = reinterpret_cast<double*>(ws + p.off_gbl);
   hipLaunchKernelGGL((gblock_finish_lane<NA, NBT>), dim3((unsigned)p.lb.groups > 0 ? (unsigned)p.lb.groups : 1u),
                      dim3(1024), 0, s, acoef, x0, g_xlast, (const double*)gh, (const double*)pa, (const double*)pb, gal,
-                     gbl, gx0, p.lanes, I, O, L, L > 0 ? p.lb.nsuper : (int64_t)0);
+                     gbl, gx0, p.lanes, I, O, p.pp, L, L > 0 ? p.lb.nsuper : (int64_t)0);
   const int64_t np = (int64_t)I * O * (NA + nb);
   hipLaunchKernelGGL((gblock_finish_pairs<NA, NBT>), grid_for(np), dim3(256), 0, s, (const double*)gal,
-                     (const double*)gbl, ga, gb, B, I, O, nb);
+                     (const double*)gbl, ga, gb, B, I, O, p.pp, nb);
 }
 
 #define TSF_GB_CASES(X) \

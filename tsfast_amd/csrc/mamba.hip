@@ -66,19 +66,36 @@ int ns_for(int64_t N) {
 #define TSF_MAMBA_BWD_HG 0
 #endif
 
+// Lanes per channel of the forward (8 or 16) and its steps per LDS round (0: the default).
+#ifndef TSF_MAMBA_FWD_NG
+#define TSF_MAMBA_FWD_NG 8
+#endif
+#ifndef TSF_MAMBA_FWD_TF
+#define TSF_MAMBA_FWD_TF 0
+#endif
+
+// Backward lane split and the checkpoint interval shared by both directions.
 template <int NS>
 struct MCfg {
   static constexpr int NG = NS >= 8 ? 8 : NS;  // lanes per channel
   static constexpr int NPT = NS / NG;          // states per lane
-  static constexpr int DT = TSF_MAMBA_FWD_DT;  // channels per workgroup
-  static constexpr int TH = DT * NG;           // threads per workgroup
   // checkpoint interval = backward recompute chunk (lam_t and h_t of a chunk live in VGPRs)
   static constexpr int CHK = NPT <= 2 ? 8 : (NPT == 4 ? 8 : 4);
-  static constexpr int TF = NPT <= 2 ? 32 : 2 * CHK;  // forward steps per LDS round
-  static constexpr int TB = CHK < 8 ? CHK : 8;  // backward flush sub-block
-  static constexpr int IT_F = (TF * DT + TH - 1) / TH;   // owned (t, d) items per thread, forward
-  static constexpr int IT_B = (CHK * DT + TH - 1) / TH;  // owned (t, d) items per thread, backward
-  static constexpr int BC_F = (TF * NS + TH - 1) / TH;   // B/C tile elements per thread, forward
+};
+
+// Forward tiling: DT channels per workgroup, NG lanes per channel with NPT states each.
+template <int NS>
+struct FCfg {
+  static constexpr int NG = NS >= TSF_MAMBA_FWD_NG ? TSF_MAMBA_FWD_NG : NS;
+  static constexpr int NPT = NS / NG;
+  static constexpr int DT = TSF_MAMBA_FWD_DT;
+  static constexpr int TH = DT * NG;
+  static constexpr int CHK = MCfg<NS>::CHK;
+  static constexpr int TF = TSF_MAMBA_FWD_TF > 0 ? TSF_MAMBA_FWD_TF : (NPT <= 2 ? 32 : 2 * CHK);
+  static constexpr int IT_F = (TF * DT + TH - 1) / TH;  // owned (t, d) items per thread
+  static constexpr int BC_F = (TF * NS + TH - 1) / TH;  // B/C tile elements per thread
+  static constexpr int WAVES = TH / 64;
+  static constexpr int OCC = (12 / WAVES) > 1 ? (12 / WAVES) : 1;  // workgroups per CU aimed at
 };
 
 template <typename TIO>
@@ -188,12 +205,12 @@ TSF_DEV float row_bcast(float x, int k) {
 // ------------------------------------------------------------------------------------ forward
 // SAVE: training forward (writes the checkpoints and y to chk); chk is unused otherwise.
 template <typename TIO, int NS, bool SAVE>
-__global__ void __launch_bounds__(MCfg<NS>::TH) mamba_fwd_kernel(
+__global__ void __launch_bounds__(FCfg<NS>::TH, FCfg<NS>::WAVES >= 8 ? 3 : 1) mamba_fwd_kernel(
     const TIO* __restrict__ draw, const float* __restrict__ A, const TIO* __restrict__ Bt,
     const TIO* __restrict__ Ct, const TIO* __restrict__ u, const TIO* __restrict__ z, const float* __restrict__ Dp,
     const float* __restrict__ h0, TIO* __restrict__ out, float* __restrict__ h_last, float* __restrict__ chk,
     int64_t L, int64_t D, int N, int64_t NC, unsigned cus) {
-  using C = MCfg<NS>;
+  using C = FCfg<NS>;
   constexpr int NPT = C::NPT, NG = C::NG, DT = C::DT, TH = C::TH, CHK = C::CHK, TF = C::TF;
   constexpr int IT = C::IT_F, BCI = C::BC_F;
   __shared__ float2 s_sc[TF][DT];       // (delta, delta * u)
@@ -789,7 +806,7 @@ template <typename TIO, int NS>
 int launch_fwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, const float* A, const void* Bt,
                const void* Ct, const void* u, const void* z, const float* Dp, const float* h0, void* out,
                float* h_last, float* chk, hipStream_t s) {
-  using C = MCfg<NS>;
+  using C = FCfg<NS>;
   const int64_t NC = (L + C::CHK - 1) / C::CHK;
   dim3 grid((unsigned)((D + C::DT - 1) / C::DT * B));
   if (chk)

@@ -12,7 +12,9 @@ outputs from per-super-chunk states the forward saves (a few MB).
 ``dynonet_gblock_bwd`` custom ops. Shapes follow the reference: ``u [B, L, I]``, ``b_coeff
 [O, I, nb]``, ``a_coeff [O, I, na]``, ``u_tail [B, nb-1, I]``, ``x0 [B, I*O, na]`` (pairs input-major,
 newest first); ``y [B, L, O]``, ``x_last [B, I*O, na]``. float32; ``1 <= na <= 4``, ``nb <= 16``,
-``I*O`` dividing 64.
+any number of channel pairs. One launch per direction serves up to 64 pairs (a batch row's pairs
+padded to a power of two inside the kernels); a larger block runs as groups of whole inputs (and,
+past 64 outputs, of outputs) of at most 64 pairs each, whose outputs and gradients add up.
 """
 
 from __future__ import annotations
@@ -25,6 +27,7 @@ from .. import _lib
 
 _MAX_NA = 4
 _MAX_NB = 16
+_MAX_PAIRS = 64  # pairs one launch serves (a tile of 64 lanes holds whole batch rows)
 
 
 def supports(u, b_coeff, a_coeff, u_tail, x0) -> str | None:
@@ -50,8 +53,6 @@ def supports(u, b_coeff, a_coeff, u_tail, x0) -> str | None:
         return f"denominator order {na} outside [1, {_MAX_NA}]"
     if not 1 <= nb <= _MAX_NB:
         return f"numerator taps {nb} outside [1, {_MAX_NB}]"
-    if 64 % (I * O) != 0:
-        return f"{I} x {O} channel pairs do not divide 64"
     if u_tail is not None and tuple(u_tail.shape) != (B, nb - 1, I):
         return f"u_tail.shape {tuple(u_tail.shape)} != {(B, nb - 1, I)}"
     if x0 is not None and tuple(x0.shape) != (B, I * O, na):
@@ -175,11 +176,42 @@ def _gblock_backward(ctx, gy, g_xlast, g_saved):
 _gblock_op.register_autograd(_gblock_backward, setup_context=_gblock_setup)
 
 
+def _groups(I: int, O: int) -> tuple[list[range], list[range]]:
+    """Input and output ranges whose pair counts fit one launch (``_MAX_PAIRS``)."""
+    go = min(O, _MAX_PAIRS)
+    gi = max(1, _MAX_PAIRS // go)
+    return ([range(i, min(i + gi, I)) for i in range(0, I, gi)], [range(o, min(o + go, O)) for o in range(0, O, go)])
+
+
 def run(u, b_coeff, a_coeff, u_tail, x0):
     """Fused G-block: ``y [B, L, O]`` and the all-pole state ``x_last [B, I*O, na]`` (newest first).
 
     ``u_tail`` (the last ``nb - 1`` inputs before ``u``) and ``x0`` may be None (zero initial
-    conditions). Differentiable in all inputs (``tsfast_hip::dynonet_gblock``).
+    conditions). Differentiable in all inputs (``tsfast_hip::dynonet_gblock``). More than 64
+    pairs run as groups (``_groups``): the pair outputs of a group of inputs sum into y like any
+    other pairs, so y adds the groups' outputs and each pair's state comes from its own group.
     """
-    y, x_last, _ = _gblock_op(u, b_coeff, a_coeff, u_tail, x0)
+    I, O = u.shape[-1], b_coeff.shape[0]
+    if I * O <= _MAX_PAIRS:
+        y, x_last, _ = _gblock_op(u, b_coeff, a_coeff, u_tail, x0)
+        return y, x_last
+    B, na = u.shape[0], a_coeff.shape[-1]
+    in_groups, out_groups = _groups(I, O)
+    x0v = None if x0 is None else x0.view(B, I, O, na)
+    y_cols, x_rows = [], [[None] * len(out_groups) for _ in in_groups]
+    for oi, og in enumerate(out_groups):
+        o0, o1 = og.start, og.stop
+        y_part = None
+        for ii, ig in enumerate(in_groups):
+            i0, i1 = ig.start, ig.stop
+            x0g = None if x0v is None else x0v[:, i0:i1, o0:o1].reshape(B, (i1 - i0) * (o1 - o0), na)
+            yg, xg, _ = _gblock_op(
+                u[..., i0:i1], b_coeff[o0:o1, i0:i1], a_coeff[o0:o1, i0:i1],
+                None if u_tail is None else u_tail[..., i0:i1], x0g,
+            )
+            y_part = yg if y_part is None else y_part + yg
+            x_rows[ii][oi] = xg.view(B, i1 - i0, o1 - o0, na)
+        y_cols.append(y_part)
+    y = torch.cat(y_cols, dim=-1) if len(y_cols) > 1 else y_cols[0]
+    x_last = torch.cat([torch.cat(row, dim=2) for row in x_rows], dim=1).reshape(B, I * O, na)
     return y, x_last
