@@ -759,10 +759,15 @@ def run_linrec(args, line):
     if n <= 4:
         kernels = {"fwd": ("linrec_fwd_lb look-back scan + transfer + reset", fwd_ms, fwd_b),
                    "bwd": ("linrec_bwd_lb look-back scan + transfer + reset + finish", bwd_ms, bwd_b)}
-    else:
+    elif n <= 8:
         kernels = {"fwd": ("lw_sum_fwd + lw_carry_fwd + lw_apply_fwd two-pass scan + lw_power", fwd_ms, fwd_b),
                    "bwd": ("lw_sum_bwd + lw_carry_bwd + lw_apply_bwd two-pass scan + lw_power + finish", bwd_ms,
                            bwd_b)}
+    else:
+        kernels = {"fwd": ("lsp_sum_fwd + lsp_carry_fwd + lsp_apply_fwd spread two-pass scan + lsp_power", fwd_ms,
+                           fwd_b),
+                   "bwd": ("lsp_sum_bwd + lsp_carry_bwd + lsp_apply_bwd spread two-pass scan + lsp_power + finish",
+                           bwd_ms, bwd_b)}
     cpu = None
     if not args.no_cpu:
         def cpu_leg():
@@ -847,7 +852,7 @@ def main():
     ap.add_argument("--adjoint", action="store_true",
                     help="measure the chunked NSS adjoint scan (n 32, the reference's chunking)")
     ap.add_argument("--order", type=int, default=3,
-                    help="with --linrec: the denominator order n (state size 1..8; config 4 is 3)")
+                    help="with --linrec: the denominator order n (state size 1..16; config 4 is 3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument(
         "--copy-calibration",

@@ -228,9 +228,10 @@ int tsfast_hip_gblock_bwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb
  * G_t = A^T G_{t+1} + g_t, grad_A = sum_t G_t x_{t-1}^T, grad_x0 = A^T G_1; the reference runs
  * both as log-doubling scans, :23-37). Lanes are the flattened leading dims:
  * A/gA [lanes, n, n] row-major, v/x/g/gv [lanes, L, n] contiguous, x0/gx0 [lanes, n].
- * float32 in and out, fp64 state; 1 <= n <= 8, else TSF_ERR_UNSUPPORTED (n <= 4: a single-pass
- * look-back scan; n = 5..8: chunk summaries, a per-lane carry and a re-run, with L at most
- * 65535 * 256). The workspace holds the scan's intermediate state, re-initialised by each call
+ * float32 in and out, fp64 state; 1 <= n <= 16, else TSF_ERR_UNSUPPORTED (n <= 4: a single-pass
+ * look-back scan; n = 5..16: chunk summaries, a per-lane carry and a re-run, with L at most
+ * 65535 * 256; n = 9..16 run each lane and chunk on a group of 16 threads, one state component
+ * each). The workspace holds the scan's intermediate state, re-initialised by each call
  * on its stream: two calls in flight must not share one.
  */
 int64_t tsfast_hip_linrec_workspace_bytes(int64_t lanes, int64_t L, int64_t n);

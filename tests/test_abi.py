@@ -79,14 +79,17 @@ def test_size_queries(lib):
     assert lib.tsfast_hip_linrec_workspace_bytes(64, 100, 2) == 256 + 8 * (4 * 64 * (2 + 2 + 4) + 2 * 64 * 4)
     # n = 5..8: e/f and carries [chunks][lanes][n], the lane matrices and the grad_A partials
     assert lib.tsfast_hip_linrec_workspace_bytes(4, 300, 5) == 8 * (2 * 2 * 4 * 5 + 4 * 25 + 2 * 4 * 25)
-    assert lib.tsfast_hip_linrec_workspace_bytes(4, 16, 9) == -1  # n above 8
+    # n = 9..16 (spread path): the same areas with the same 256-step chunks
+    assert lib.tsfast_hip_linrec_workspace_bytes(4, 300, 12) == 8 * (2 * 2 * 4 * 12 + 4 * 144 + 2 * 4 * 144)
+    assert lib.tsfast_hip_linrec_workspace_bytes(4, 16, 17) == -1  # n above 16
 
 
 def test_argument_errors_before_any_launch(lib):
     # negative sizes and unsupported orders are rejected on the host, before touching a device
     assert lib.tsfast_hip_diag_fwd(-1, 1, 1, 0, None, None, None, None, None, 0, None) == -1
     assert lib.tsfast_hip_allpole_fwd(4, 16, 17, None, None, None, None, None, 0, None) == -3
-    assert lib.tsfast_hip_linrec_fwd(4, 16, 9, None, None, None, None, None, 0, None) == -3
+    assert lib.tsfast_hip_linrec_fwd(4, 16, 17, None, None, None, None, None, 0, None) == -3
+    assert lib.tsfast_hip_linrec_fwd(4, 16, 9, None, None, None, None, None, 0, None) == -1  # NULL inputs
     assert lib.tsfast_hip_linrec_bwd(-1, 16, 2, *([None] * 8), 0, None) == -1
     assert lib.tsfast_hip_mamba_fwd(1, 1, 1, 65, 0, *([None] * 12)) == -3
     assert lib.tsfast_hip_conv_silu_fwd(1, 8, 4, 1, 0, *([None, 0, 0, 0] + [None] * 5)) == -1  # K < 2

@@ -320,3 +320,47 @@ def test_linrec_order8_config4_route_full_size(gpu):
     gA, gv, _ = O.linrec_backward(g_s, A_s, want)
     assert O.rel_err(_np64(A_d.grad[pick.to(gpu)]), gA) < 1e-5
     assert O.rel_err(_np64(v_d.grad[pick.to(gpu)]), gv) < 1e-5
+
+
+def test_linrec_order16_config4_route_full_size(gpu):
+    """The spread n = 16 path on config 4's route at full size (4096 lanes x L16384, companion
+    matrices of order-16 denominators driven by (w_t, 0, ...): 256 workgroups of 16 lanes x 64
+    chunks). Lanes are independent, so 48 lanes spread over every block of 256 (each block's
+    first, middle and last lane, which fall in different 16-lane workgroups) are checked against
+    the oracle over the full length, x and every gradient. Inputs are drawn on the GPU and the
+    checked lanes copied back."""
+    from tsfast_amd.dynonet import core as dcore
+    from tsfast_amd.dynonet import linrec_hip
+
+    g = torch.Generator().manual_seed(16)
+    lanes, L, n = 4096, 16384, 16
+    # eight conjugate pole pairs per lane, |p| ~ U(0.5, 0.95), angles ~ U(0, pi); lanes whose
+    # fp32-rounded filter is not stable (spectral radius >= 0.99) get their poles pulled inwards
+    rho = (torch.rand(lanes, n // 2, generator=g, dtype=torch.float64) * 0.45 + 0.5).numpy()
+    th = (torch.rand(lanes, n // 2, generator=g, dtype=torch.float64) * np.pi).numpy()
+    for _ in range(30):
+        poles = np.concatenate([rho * np.exp(1j * th), rho * np.exp(-1j * th)], axis=1)
+        a = torch.tensor(np.array([np.real(np.poly(p))[1:] for p in poles]), dtype=torch.float32)
+        radius = np.abs(np.linalg.eigvals(dcore.companion(a).double().numpy())).max(-1)
+        if (radius < 0.99).all():
+            break
+        rho = np.where((radius >= 0.99)[:, None], rho * 0.97, rho)
+    assert (radius < 0.99).all()
+    A = dcore.companion(a).contiguous()
+    gg = torch.Generator(device=gpu).manual_seed(17)
+    w = torch.randn(lanes, L, 1, device=gpu, generator=gg)
+    v_d = torch.nn.functional.pad(w, (0, n - 1)).contiguous().requires_grad_()
+    del w
+    gx = torch.randn(lanes, L, n, device=gpu, generator=gg)
+    A_d = A.to(gpu).requires_grad_()
+    assert linrec_hip.supports(A_d, v_d, None) is None
+    x = linrec_hip.run(A_d, v_d, None)
+    x.backward(gx)
+    pick = torch.tensor(sorted({b * 256 + o for b in range(16) for o in (0, 128, 255)}), device=gpu)
+    A_s = A[pick.cpu()].double().numpy()
+    v_s, g_s = v_d.detach()[pick].double().cpu().numpy(), gx[pick].double().cpu().numpy()
+    want = O.linrec_forward(A_s, v_s)
+    assert O.rel_err(_np64(x[pick]), want) < 1e-5
+    gA, gv, _ = O.linrec_backward(g_s, A_s, want)
+    assert O.rel_err(_np64(A_d.grad[pick]), gA) < 1e-5
+    assert O.rel_err(_np64(v_d.grad[pick]), gv) < 1e-5

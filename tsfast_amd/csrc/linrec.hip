@@ -1021,12 +1021,307 @@ int wide_bwd(int64_t lanes, int64_t L, const float* g, const float* A, const flo
 
 #define TSF_WIDE_CASES(X) X(5) X(6) X(7) X(8)
 
+// ------------------------------------------------------------------------------ n = 9..16
+// Spread two-pass path: the phases of the n = 5..8 path (chunk summaries from a zero state, a
+// sequential carry over the chunks with M = P^kWideT, every chunk re-run from its entering state),
+// with one (lane, chunk) per group of 16 threads, a DPP row. Thread r of a group holds component r
+// of the state (fp64) and row r of the step matrix (fp64, zero beyond n), and a step
+//     s_r <- sum_c P[r][c] s_c + x_r
+// takes the other components s_c by row broadcasts (two 32-bit row_newbcast moves per fp64
+// value), in the n = 5..8 path's summation order (c = 0 .. n-1 onto x_r). Per step a group reads
+// or writes one contiguous segment of n floats (coalesced), and the adjoint's grad_A partial
+// sum_t G_t x_{t-1}^T is accumulated row by row, thread r holding row r. Components r >= n stay
+// zero: their matrix rows and inputs are zero, and nothing is stored for them.
+constexpr int kSpread = 16;     // threads per group = the padded state size
+constexpr int kMaxSpreadNS = 16;
+constexpr int kSpreadPf = 8;    // steps fetched ahead by the chunk kernels
+
+template <int K>
+TSF_DEV uint32_t row_lane_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x150 + K, 0xF, 0xF, true);
+}
+// the value x holds in lane K (0..15) of this thread's 16-lane row
+template <int K>
+TSF_DEV double row_lane(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint64_t lo = row_lane_u32<K>((uint32_t)b), hi = row_lane_u32<K>((uint32_t)(b >> 32));
+  return __longlong_as_double((long long)((hi << 32) | lo));
+}
+template <int K>
+TSF_DEV float row_lane(float x) {
+  return __uint_as_float(row_lane_u32<K>(__float_as_uint(x)));
+}
+
+// acc + sum_c p[c] * (s of lane c), c = 0 .. 15 in order
+template <int C = 0>
+TSF_DEV double spread_dot(const double (&p)[kSpread], double s, double acc) {
+  if constexpr (C == kSpread) {
+    return acc;
+  } else {
+    return spread_dot<C + 1>(p, s, fma(p[C], row_lane<C>(s), acc));
+  }
+}
+// acc[c] += g * (x of lane c), c = 0 .. 15
+template <int C = 0>
+TSF_DEV void spread_outer(double (&acc)[kSpread], double g, float x) {
+  if constexpr (C < kSpread) {
+    acc[C] = fma(g, (double)row_lane<C>(x), acc[C]);
+    spread_outer<C + 1>(acc, g, x);
+  }
+}
+
+// Row r of P = A (forward) or A^T (adjoint) of one lane, fp64, zero beyond n.
+TSF_DEV void spread_row(double (&p)[kSpread], const float* __restrict__ A, int64_t lane, int n, int r, bool live,
+                        bool transpose) {
+  const float* a = A + lane * n * n;
+#pragma unroll
+  for (int c = 0; c < kSpread; ++c)
+    p[c] = (live && r < n && c < n) ? (double)a[transpose ? c * n + r : r * n + c] : 0.0;
+}
+
+// M = P^e per lane, fp64 [lanes][n][n]: a workgroup per lane, group c runs column c (P applied e
+// times to the unit vector e_c, step by step as lw_power).
+__global__ void __launch_bounds__(256) lsp_power(const float* __restrict__ A, double* __restrict__ M, int64_t lanes,
+                                                 int n, int e, int transpose) {
+  const int64_t lane = blockIdx.x;
+  const int r = threadIdx.x & 15, col = threadIdx.x >> 4;
+  double p[kSpread];
+  spread_row(p, A, lane, n, r, true, transpose != 0);
+  double x = r == col ? 1.0 : 0.0;
+  for (int step = 0; step < e; ++step) x = spread_dot(p, x, 0.0);
+  if (r < n && col < n) M[(lane * n + r) * n + col] = x;
+}
+
+// One (lane, chunk) per group: group g of workgroup (bx, chunk) is lane bx * 16 + g.
+struct SpreadIdx {
+  int64_t lane, c, t0, t1;
+  int r;
+  bool live;
+};
+TSF_DEV SpreadIdx spread_idx(int64_t lanes, int64_t L) {
+  SpreadIdx q;
+  q.r = threadIdx.x & 15;
+  q.lane = blockIdx.x * (int64_t)16 + (threadIdx.x >> 4);
+  q.live = q.lane < lanes;
+  q.c = blockIdx.y;
+  q.t0 = q.c * kWideT;
+  q.t1 = (q.t0 + kWideT < L) ? q.t0 + kWideT : L;
+  return q;
+}
+
+// Forward chunk ends from a zero state: e [nchunks][lanes][n]
+__global__ void __launch_bounds__(256) lsp_sum_fwd(const float* __restrict__ A, const float* __restrict__ v,
+                                                   double* __restrict__ e, int64_t lanes, int64_t L, int n) {
+  const SpreadIdx q = spread_idx(lanes, L);
+  const bool ld = q.live && q.r < n;
+  double p[kSpread];
+  spread_row(p, A, q.lane, n, q.r, q.live, false);
+  const float* row = v + (q.live ? q.lane : 0) * L * n + q.r;
+  float d[kSpreadPf];
+#pragma unroll
+  for (int k = 0; k < kSpreadPf; ++k) d[k] = (ld && q.t0 + k < q.t1) ? row[(q.t0 + k) * n] : 0.0f;
+  double s = 0.0;
+  for (int64_t tb = q.t0; tb < q.t1; tb += kSpreadPf) {
+#pragma unroll
+    for (int k = 0; k < kSpreadPf; ++k) {
+      const int64_t t = tb + k;
+      if (t < q.t1) {  // uniform over the workgroup (one chunk)
+        s = spread_dot(p, s, (double)d[k]);
+        d[k] = (ld && t + kSpreadPf < q.t1) ? row[(t + kSpreadPf) * n] : 0.0f;
+      }
+    }
+  }
+  if (ld) e[(q.c * lanes + q.lane) * n + q.r] = s;
+}
+
+// Entering state of every chunk: carry[c] = M carry[c-1] + e[c-1], carry[0] = x0 (or 0); a group
+// per lane.
+__global__ void __launch_bounds__(256) lsp_carry_fwd(const double* __restrict__ M, const float* __restrict__ x0,
+                                                     const double* __restrict__ e, double* __restrict__ carry,
+                                                     int64_t lanes, int64_t nchunks, int n) {
+  const int r = threadIdx.x & 15;
+  const int64_t lane = blockIdx.x * (int64_t)16 + (threadIdx.x >> 4);
+  const bool live = lane < lanes, ld = live && r < n;
+  double m[kSpread];
+#pragma unroll
+  for (int c = 0; c < kSpread; ++c) m[c] = (ld && c < n) ? M[(lane * n + r) * n + c] : 0.0;
+  double s = (ld && x0) ? (double)x0[lane * n + r] : 0.0;
+  for (int64_t c = 0; c < nchunks; ++c) {
+    if (ld) carry[(c * lanes + lane) * n + r] = s;
+    s = spread_dot(m, s, ld ? e[(c * lanes + lane) * n + r] : 0.0);
+  }
+}
+
+// Every chunk re-run from its entering state, writing x.
+__global__ void __launch_bounds__(256) lsp_apply_fwd(const float* __restrict__ A, const float* __restrict__ v,
+                                                     const double* __restrict__ carry, float* __restrict__ x,
+                                                     int64_t lanes, int64_t L, int n) {
+  const SpreadIdx q = spread_idx(lanes, L);
+  const bool ld = q.live && q.r < n;
+  double p[kSpread];
+  spread_row(p, A, q.lane, n, q.r, q.live, false);
+  const int64_t off = (q.live ? q.lane : 0) * L * n + q.r;
+  const float* row = v + off;
+  float* orow = x + off;
+  float d[kSpreadPf];
+#pragma unroll
+  for (int k = 0; k < kSpreadPf; ++k) d[k] = (ld && q.t0 + k < q.t1) ? row[(q.t0 + k) * n] : 0.0f;
+  double s = ld ? carry[(q.c * lanes + q.lane) * n + q.r] : 0.0;
+  for (int64_t tb = q.t0; tb < q.t1; tb += kSpreadPf) {
+#pragma unroll
+    for (int k = 0; k < kSpreadPf; ++k) {
+      const int64_t t = tb + k;
+      if (t < q.t1) {
+        s = spread_dot(p, s, (double)d[k]);
+        if (ld) orow[t * n] = (float)s;
+        d[k] = (ld && t + kSpreadPf < q.t1) ? row[(t + kSpreadPf) * n] : 0.0f;
+      }
+    }
+  }
+}
+
+// Adjoint chunk starts from a zero right-end state: f [nchunks][lanes][n]
+__global__ void __launch_bounds__(256) lsp_sum_bwd(const float* __restrict__ A, const float* __restrict__ g,
+                                                   double* __restrict__ f, int64_t lanes, int64_t L, int n) {
+  const SpreadIdx q = spread_idx(lanes, L);
+  const bool ld = q.live && q.r < n;
+  double p[kSpread];
+  spread_row(p, A, q.lane, n, q.r, q.live, true);
+  const float* row = g + (q.live ? q.lane : 0) * L * n + q.r;
+  float d[kSpreadPf];
+#pragma unroll
+  for (int k = 0; k < kSpreadPf; ++k) d[k] = (ld && q.t1 - 1 - k >= q.t0) ? row[(q.t1 - 1 - k) * n] : 0.0f;
+  double G = 0.0;
+  for (int64_t tb = q.t1 - 1; tb >= q.t0; tb -= kSpreadPf) {
+#pragma unroll
+    for (int k = 0; k < kSpreadPf; ++k) {
+      const int64_t t = tb - k;
+      if (t >= q.t0) {
+        G = spread_dot(p, G, (double)d[k]);
+        d[k] = (ld && t - kSpreadPf >= q.t0) ? row[(t - kSpreadPf) * n] : 0.0f;
+      }
+    }
+  }
+  if (ld) f[(q.c * lanes + q.lane) * n + q.r] = G;
+}
+
+// Adjoint entering every chunk from the right: rc[c] = G at the first step of chunk c + 1 (zero
+// for the last chunk), rc[c-1] = f[c] + M rc[c]; then grad_x0 = A^T G_0 with G_0 = f[0] + M rc[0].
+__global__ void __launch_bounds__(256) lsp_carry_bwd(const float* __restrict__ A, const double* __restrict__ M,
+                                                     const double* __restrict__ f, double* __restrict__ rc,
+                                                     float* __restrict__ gx0, int64_t lanes, int64_t nchunks, int n) {
+  const int r = threadIdx.x & 15;
+  const int64_t lane = blockIdx.x * (int64_t)16 + (threadIdx.x >> 4);
+  const bool live = lane < lanes, ld = live && r < n;
+  double m[kSpread];
+#pragma unroll
+  for (int c = 0; c < kSpread; ++c) m[c] = (ld && c < n) ? M[(lane * n + r) * n + c] : 0.0;
+  double R = 0.0;
+  for (int64_t c = nchunks - 1; c >= 0; --c) {
+    if (ld) rc[(c * lanes + lane) * n + r] = R;
+    R = spread_dot(m, R, ld ? f[(c * lanes + lane) * n + r] : 0.0);
+  }
+  if (gx0) {  // R now holds G_0; grad_x0 = A^T G_0
+    double p[kSpread];
+    spread_row(p, A, lane, n, r, live, true);
+    const double gx = spread_dot(p, R, 0.0);
+    if (ld) gx0[lane * n + r] = (float)gx;
+  }
+}
+
+// Every chunk re-run backwards from its right-end adjoint, writing grad_v and the chunk's grad_A
+// partial sum_t G_t x_{t-1}^T (x_{-1} = x0 or 0) into part [nchunks][lanes][n][n].
+__global__ void __launch_bounds__(256) lsp_apply_bwd(const float* __restrict__ A, const float* __restrict__ g,
+                                                     const float* __restrict__ out, const float* __restrict__ x0,
+                                                     const double* __restrict__ rc, float* __restrict__ gv,
+                                                     double* __restrict__ part, int64_t lanes, int64_t L, int n) {
+  const SpreadIdx q = spread_idx(lanes, L);
+  const bool ld = q.live && q.r < n;
+  double p[kSpread], acc[kSpread];
+  spread_row(p, A, q.lane, n, q.r, q.live, true);
+#pragma unroll
+  for (int c = 0; c < kSpread; ++c) acc[c] = 0.0;
+  const int64_t off = (q.live ? q.lane : 0) * L * n + q.r;
+  const float* grow = g + off;
+  const float* xrow = out + off;
+  float* orow = gv + off;
+  const float x_init = (ld && x0) ? x0[q.lane * n + q.r] : 0.0f;  // x_{-1}
+  // slot k holds g_t and x_{t-1} of a step t with (t1 - 1 - t) % kSpreadPf == k
+  float dg[kSpreadPf], dx[kSpreadPf];
+  auto fetch = [&](int k, int64_t t) __attribute__((always_inline)) {
+    dg[k] = ld ? grow[t * n] : 0.0f;
+    dx[k] = !ld ? 0.0f : t > 0 ? xrow[(t - 1) * n] : x_init;
+  };
+#pragma unroll
+  for (int k = 0; k < kSpreadPf; ++k)
+    if (q.t1 - 1 - k >= q.t0) fetch(k, q.t1 - 1 - k);
+  double G = ld ? rc[(q.c * lanes + q.lane) * n + q.r] : 0.0;
+  for (int64_t tb = q.t1 - 1; tb >= q.t0; tb -= kSpreadPf) {
+#pragma unroll
+    for (int k = 0; k < kSpreadPf; ++k) {
+      const int64_t t = tb - k;
+      if (t >= q.t0) {
+        G = spread_dot(p, G, (double)dg[k]);
+        if (ld) orow[t * n] = (float)G;
+        spread_outer(acc, G, dx[k]);
+        if (t - kSpreadPf >= q.t0) fetch(k, t - kSpreadPf);
+      }
+    }
+  }
+  if (ld) {
+    double* pr = part + ((q.c * lanes + q.lane) * n + q.r) * n;
+#pragma unroll
+    for (int c = 0; c < kSpread; ++c)
+      if (c < n) pr[c] = acc[c];
+  }
+}
+
+int spread_fwd(int64_t lanes, int64_t L, int n, const float* A, const float* v, const float* x0, float* x, char* ws,
+               hipStream_t s) {
+  const LwPlan p = lw_plan(lanes, L, n);
+  double* e = reinterpret_cast<double*>(ws + p.off_e);
+  double* carry = reinterpret_cast<double*>(ws + p.off_carry);
+  double* M = reinterpret_cast<double*>(ws + p.off_M);
+  const unsigned lg = (unsigned)((lanes + 15) / 16);
+  const dim3 grid(lg, (unsigned)p.nchunks);
+  hipLaunchKernelGGL(lsp_power, dim3((unsigned)lanes), dim3(256), 0, s, A, M, lanes, n, kWideT, 0);
+  hipLaunchKernelGGL(lsp_sum_fwd, grid, dim3(256), 0, s, A, v, e, lanes, L, n);
+  hipLaunchKernelGGL(lsp_carry_fwd, dim3(lg), dim3(256), 0, s, (const double*)M, x0, (const double*)e, carry, lanes,
+                     p.nchunks, n);
+  hipLaunchKernelGGL(lsp_apply_fwd, grid, dim3(256), 0, s, A, v, (const double*)carry, x, lanes, L, n);
+  return tsf_launch_status();
+}
+
+int spread_bwd(int64_t lanes, int64_t L, int n, const float* g, const float* A, const float* out, const float* x0,
+               float* gA, float* gv, float* gx0, char* ws, hipStream_t s) {
+  if (L == 0) {
+    hipLaunchKernelGGL(linrec_zero, dim3(blocks_for(lanes * n * n)), dim3(256), 0, s, gA, lanes * n * n);
+    if (gx0) hipLaunchKernelGGL(linrec_zero, dim3(blocks_for(lanes * n)), dim3(256), 0, s, gx0, lanes * n);
+    return tsf_launch_status();
+  }
+  const LwPlan p = lw_plan(lanes, L, n);
+  double* f = reinterpret_cast<double*>(ws + p.off_e);
+  double* rc = reinterpret_cast<double*>(ws + p.off_carry);
+  double* M = reinterpret_cast<double*>(ws + p.off_M);
+  double* part = reinterpret_cast<double*>(ws + p.off_part);
+  const unsigned lg = (unsigned)((lanes + 15) / 16);
+  const dim3 grid(lg, (unsigned)p.nchunks);
+  hipLaunchKernelGGL(lsp_power, dim3((unsigned)lanes), dim3(256), 0, s, A, M, lanes, n, kWideT, 1);
+  hipLaunchKernelGGL(lsp_sum_bwd, grid, dim3(256), 0, s, A, g, f, lanes, L, n);
+  hipLaunchKernelGGL(lsp_carry_bwd, dim3(lg), dim3(256), 0, s, A, (const double*)M, (const double*)f, rc, gx0, lanes,
+                     p.nchunks, n);
+  hipLaunchKernelGGL(lsp_apply_bwd, grid, dim3(256), 0, s, A, g, out, x0, (const double*)rc, gv, part, lanes, L, n);
+  hipLaunchKernelGGL(linrec_finish, dim3((unsigned)((lanes * n * n + 63) / 64)), dim3(1024), 0, s,
+                     (const double*)part, gA, lanes * n * n, p.nchunks);
+  return tsf_launch_status();
+}
+
 }  // namespace
 
 extern "C" {
 
 int64_t tsfast_hip_linrec_workspace_bytes(int64_t lanes, int64_t L, int64_t n) {
-  if (lanes < 0 || L < 0 || n < 1 || n > kMaxWideNS) return -1;
+  if (lanes < 0 || L < 0 || n < 1 || n > kMaxSpreadNS) return -1;
   if (n > kMaxNS) return (int64_t)lw_plan(lanes, L, n).bytes;
   return (int64_t)lr_plan(lanes, L, n).bytes;
 }
@@ -1034,8 +1329,9 @@ int64_t tsfast_hip_linrec_workspace_bytes(int64_t lanes, int64_t L, int64_t n) {
 int tsfast_hip_linrec_fwd(int64_t lanes, int64_t L, int64_t n, const float* A, const float* v, const float* x0,
                           float* x, void* workspace, int64_t workspace_bytes, void* stream) {
   if (lanes < 0 || L < 0) return TSF_ERR_ARG;
-  if (n < 1 || n > kMaxWideNS) return TSF_ERR_UNSUPPORTED;
+  if (n < 1 || n > kMaxSpreadNS) return TSF_ERR_UNSUPPORTED;
   if (lanes == 0 || L == 0) return TSF_OK;
+  if (n > kMaxWideNS && lanes > (int64_t)UINT32_MAX) return TSF_ERR_UNSUPPORTED;
   if (n > kMaxNS && !lw_grid_fits(lanes, L)) return TSF_ERR_UNSUPPORTED;
   if (!A || !v || !x) return TSF_ERR_ARG;
   if (!workspace || workspace_bytes < tsfast_hip_linrec_workspace_bytes(lanes, L, n)) return TSF_ERR_WORKSPACE;
@@ -1052,16 +1348,18 @@ int tsfast_hip_linrec_fwd(int64_t lanes, int64_t L, int64_t n, const float* A, c
     return wide_fwd<K>(lanes, L, A, v, x0, x, ws, s);
     TSF_WIDE_CASES(X)
 #undef X
+    default:
+      return spread_fwd(lanes, L, (int)n, A, v, x0, x, ws, s);
   }
-  return TSF_ERR_UNSUPPORTED;
 }
 
 int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, const float* A, const float* out,
                           const float* x0, float* gA, float* gv, float* gx0, void* workspace, int64_t workspace_bytes,
                           void* stream) {
   if (lanes < 0 || L < 0) return TSF_ERR_ARG;
-  if (n < 1 || n > kMaxWideNS) return TSF_ERR_UNSUPPORTED;
+  if (n < 1 || n > kMaxSpreadNS) return TSF_ERR_UNSUPPORTED;
   if (lanes == 0) return TSF_OK;
+  if (n > kMaxWideNS && lanes > (int64_t)UINT32_MAX) return TSF_ERR_UNSUPPORTED;
   if (n > kMaxNS && !lw_grid_fits(lanes, L)) return TSF_ERR_UNSUPPORTED;
   if (!A || !gA || (L > 0 && (!g || !out || !gv))) return TSF_ERR_ARG;
   if (x0 && !gx0) return TSF_ERR_ARG;
@@ -1079,8 +1377,9 @@ int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, c
     return wide_bwd<K>(lanes, L, g, A, out, x0, gA, gv, gx0, ws, s);
     TSF_WIDE_CASES(X)
 #undef X
+    default:
+      return spread_bwd(lanes, L, (int)n, g, A, out, x0, gA, gv, gx0, ws, s);
   }
-  return TSF_ERR_UNSUPPORTED;
 }
 
 }  // extern "C"

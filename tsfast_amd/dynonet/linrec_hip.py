@@ -10,7 +10,8 @@ and writes the states once. ``supports(A, v, x0)`` and ``run(A, v, x0) -> x``, d
 
 Shapes follow the reference: ``A [..., n, n]``, ``v [..., L, n]``, ``x0 [..., n]`` with common
 leading dims (``linear_recurrence`` broadcasts them first); states ``x_1 .. x_L`` as ``[..., L, n]``.
-float32, ``1 <= n <= 8`` (``n <= 4`` a single-pass look-back scan, ``5..8`` a two-pass scan).
+float32, ``1 <= n <= 16`` (``n <= 4`` a single-pass look-back scan, ``5..8`` a two-pass scan with a
+thread per lane and chunk, ``9..16`` a two-pass scan with a 16-thread group per lane and chunk).
 """
 
 from __future__ import annotations
@@ -23,7 +24,7 @@ import torch
 
 from .. import _lib
 
-_MAX_N = 8
+_MAX_N = 16
 _MAX_WIDE_L = 65535 * 256  # two-pass path (n > 4): chunks of 256 steps, one grid row each
 
 
