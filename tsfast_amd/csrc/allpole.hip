@@ -331,7 +331,7 @@ template <int NA>
 __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per_eu(4))) allpole_fwd_lb(
     const float* __restrict__ a, const float* __restrict__ w, const float* __restrict__ y0, float* __restrict__ y,
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
-    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
+    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, LbCfg lb_spacing) {
   constexpr int NN = NA * NA;
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
@@ -396,7 +396,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && y0 && live && k == 0) ? (double)y0[lane * NA + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       ap_look_back<NA>(S, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
-                       k, lid, s_lds, s_flag, s_pend, &s_any, counter);
+                       k, lid, s_lds, s_flag, s_pend, &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) {
         double ms[NA][NA], o[NA];
@@ -445,7 +445,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     const float* __restrict__ a, const float* __restrict__ g, const float* __restrict__ y,
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
     unsigned* __restrict__ counter, float* __restrict__ gw, double* __restrict__ part, int64_t lanes, int64_t L,
-    int64_t groups, int K, int64_t nsuper, int lb_spacing) {
+    int64_t groups, int K, int64_t nsuper, LbCfg lb_spacing) {
   constexpr int NN = NA * NA;
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
@@ -510,7 +510,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     for (int q = 0; q < NA; ++q) R[q] = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
       ap_look_back<NA>(R, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K,
-                       k, lid, s_lds, s_flag, s_pend, &s_any, counter);
+                       k, lid, s_lds, s_flag, s_pend, &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) {
         double ms[NA][NA], o[NA];

@@ -205,7 +205,7 @@ TSF_DEV void put_vec(double* p, const double (&x)[NA]) {
 // Horner's rule back from that inc (s <- Ms s + agg). Otherwise the round is repeated. Every
 // wait ends: the nearest super-chunk publishes its inc once its own look-back ends, and the first
 // one in scan order publishes its inc without looking back (the window never has to move); a
-// lane without progress for the header's spin-limit rounds gives up with NaN.
+// lane without progress for spin_max rounds gives up with NaN.
 // out = m x + b applied to each of the NV blocks of NA values.
 template <int NA, int NV>
 TSF_DEV void block_matvec_add(double (&out)[NA * NV], const double (&m)[NA][NA], const double (&x)[NA * NV],
@@ -228,10 +228,9 @@ template <int NA, int NV = 1>
 TSF_DEV void ap_look_back(double (&S)[NA * NV], const double* __restrict__ agg, const double* __restrict__ inc,
                           const double* __restrict__ MsLane, bool need, int64_t pos0, int64_t dj, int64_t nsuper,
                           int64_t lanes, int64_t lane, int K, int k, int lid, LdsTile* lds, int (*flag)[64],
-                          int* pend_s, int* any_s, unsigned* __restrict__ lb_counter) {
+                          int* pend_s, int* any_s, unsigned* __restrict__ lb_counter, uint32_t spin_max) {
   constexpr int V = NA * NV;
   uint32_t spins = 0;
-  const uint32_t spin_max = lb_spin_limit(lb_counter);
   if (k == 0) {
     int p = 0;
     if (need) {

@@ -71,16 +71,16 @@ constexpr int kWindow = kMaxWaves;  // look-back slots examined per round
 // moves on, an unpublished slot ends the round (the next round starts there). The walk always
 // ends: the first tile in scan order publishes its inc without looking back, and every tile
 // waited on was taken from the counter earlier by a workgroup that is running; a lane that
-// makes no progress for the header's spin-limit rounds gives up with NaN. Returns the entering state in wave
+// makes no progress for spin_max rounds gives up with NaN. Returns the entering state in wave
 // 0's lanes. LDS: win/flag [kWindow][64], pos [64] and one flag word, owned by the caller.
 template <typename W>
 TSF_DEV W look_back(const Map<W>* __restrict__ agg, const W* __restrict__ inc, bool need, int64_t pos0, int64_t dj,
                     int64_t nsuper, int64_t lanes, int64_t lane, int K, int k, int lid, Map<W> (*win)[64],
-                    int (*flag)[64], int64_t* pos_s, int* any_s, unsigned* __restrict__ lb_counter) {
+                    int (*flag)[64], int64_t* pos_s, int* any_s, unsigned* __restrict__ lb_counter,
+                    uint32_t spin_max) {
   Map<W> acc = {Num<W>::one(), Num<W>::zero()};  // composition of the aggregates walked over
   W result = Num<W>::zero();
   uint32_t spins = 0;
-  const uint32_t spin_max = lb_spin_limit(lb_counter);
   if (k == 0) {
     // direct probe of the nearest tile by wave 0: in the steady state of a long scan its inc is
     // already published, and the window rounds below are skipped
@@ -175,7 +175,7 @@ __global__ void __launch_bounds__(1024) diag_fwd(const T* __restrict__ lam, cons
                                                  Map<typename Wide<T>::type>* __restrict__ agg,
                                                  typename Wide<T>::type* __restrict__ inc, unsigned* __restrict__ counter,
                                                  int64_t lanes, int64_t L, int64_t N, int64_t groups, int K,
-                                                 int64_t nsuper, int lb_spacing) {
+                                                 int64_t nsuper, LbCfg lb_spacing) {
   using W = typename Wide<T>::type;
   __shared__ W s_e[kMaxWaves][64];
   // the look-back window, then (once the look-back is done) the state entering each chunk
@@ -235,7 +235,7 @@ __global__ void __launch_bounds__(1024) diag_fwd(const T* __restrict__ lam, cons
     W s = x0 && live && k == 0 ? Wide<T>::up(x0[lane]) : Num<W>::zero();
     if (sc > 0)  // uniform over the workgroup
       s = look_back(agg, inc, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
-                    s_pos, &s_any, counter);
+                    s_pos, &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
       for (int j = 0; j < K; ++j) {
@@ -276,7 +276,7 @@ __global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, cons
                                                  typename Wide<T>::type* __restrict__ inc, unsigned* __restrict__ counter,
                                                  T* __restrict__ gv, typename Wide<T>::type* __restrict__ part,
                                                  T* __restrict__ glam, T* __restrict__ gx0, int64_t lanes, int64_t L,
-                                                 int64_t N, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
+                                                 int64_t N, int64_t groups, int K, int64_t nsuper, LbCfg lb_spacing) {
   using W = typename Wide<T>::type;
   __shared__ W s_f[kMaxWaves][64];
   // the look-back window, then G entering each chunk from the right (s_start) and the glam
@@ -365,7 +365,7 @@ __global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, cons
     W R = Num<W>::zero();  // G entering the super-chunk from the right
     if (sc + 1 < nsuper)   // uniform over the workgroup
       R = look_back(agg, inc, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid, s_win, s_flag, s_pos,
-                    &s_any, counter);
+                    &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
       for (int j = K - 1; j >= 0; --j) {
@@ -648,7 +648,7 @@ __global__ void __launch_bounds__(1024) sel_fwd(const float* __restrict__ a, con
                                                 const float* __restrict__ x0, float* __restrict__ out,
                                                 Map<double>* __restrict__ agg, double* __restrict__ inc,
                                                 unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t N,
-                                                int64_t groups, int K, int64_t nsuper, int lb_spacing) {
+                                                int64_t groups, int K, int64_t nsuper, LbCfg lb_spacing) {
   __shared__ double2 s_m[kMaxWaves][64];  // chunk maps (P, e)
   // the look-back window, then the state entering each chunk
   __shared__ Map<double> s_win[kMaxWaves][64];
@@ -712,7 +712,7 @@ __global__ void __launch_bounds__(1024) sel_fwd(const float* __restrict__ a, con
     double s = x0 && live && k == 0 ? (double)x0[lane] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       s = look_back(agg, inc, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
-                    s_pos, &s_any, counter);
+                    s_pos, &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) put(inc + sc * lanes + lane, apply(sup, s));
       for (int j = 0; j < K; ++j) {
@@ -750,7 +750,7 @@ __global__ void __launch_bounds__(1024) sel_bwd(const float* __restrict__ a, con
                                                 Map<double>* __restrict__ agg, double* __restrict__ inc,
                                                 unsigned* __restrict__ counter, float* __restrict__ glam,
                                                 float* __restrict__ gv, float* __restrict__ gx0, int64_t lanes,
-                                                int64_t L, int64_t N, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
+                                                int64_t L, int64_t N, int64_t groups, int K, int64_t nsuper, LbCfg lb_spacing) {
   __shared__ double2 s_m[kMaxWaves][64];
   // the look-back window, then G entering each chunk from the right
   __shared__ Map<double> s_win[kMaxWaves][64];
@@ -818,7 +818,7 @@ __global__ void __launch_bounds__(1024) sel_bwd(const float* __restrict__ a, con
     double R = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
       R = look_back(agg, inc, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid, s_win, s_flag,
-                    s_pos, &s_any, counter);
+                    s_pos, &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) put(inc + sc * lanes + lane, apply(sup, R));
       for (int j = K - 1; j >= 0; --j) {

@@ -140,7 +140,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
     const float* __restrict__ u_tail, const float* __restrict__ x0, float* __restrict__ y, float* __restrict__ x_last,
     double* __restrict__ saved, const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg,
     double* __restrict__ inc, unsigned* __restrict__ counter, int64_t B, int64_t L, int I, int O, int Pp, int nb,
-    int64_t groups, int K, int64_t nsuper, int lb_spacing) {
+    int64_t groups, int K, int64_t nsuper, LbCfg lb_spacing) {
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
   __shared__ int s_pend[64];
@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_fwd_lb(
     for (int q = 0; q < NA; ++q) S[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[g.rl * NA + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       ap_look_back<NA>(S, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
-                       k, lid, s_lds, s_flag, s_pend, &s_any, counter);
+                       k, lid, s_lds, s_flag, s_pend, &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (saved) {
 #pragma unroll
@@ -293,7 +293,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc, unsigned* __restrict__ counter,
     float* __restrict__ gu, float* __restrict__ gu_tail, double* __restrict__ part_ga, double* __restrict__ part_gb,
     double* __restrict__ gh, int64_t B, int64_t L, int I, int O, int Pp, int nb, int64_t groups, int K, int64_t nsuper,
-    int lb_spacing) {
+    LbCfg lb_spacing) {
   static_assert(64 * (NA * sizeof(double) + NBT * sizeof(float)) <= sizeof(LdsTile), "partials fit in a tile");
   constexpr int V = 2 * NA;  // adjoint state: G then c
   __shared__ LdsTile s_lds[kLbWaves];
@@ -399,7 +399,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     for (int q = 0; q < V; ++q) Rv[q] = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
       ap_look_back<NA, 2>(Rv, agg, inc, MatStage<NA>::kLds ? &s_mat[64 * NA * NA + lid * NA * NA] : Ms + lane * NA * NA, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane,
-                          K, k, lid, s_lds, s_flag, s_pend, &s_any, counter);
+                          K, k, lid, s_lds, s_flag, s_pend, &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) {
         double ms[NA][NA], o[V];

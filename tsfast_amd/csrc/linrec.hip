@@ -125,7 +125,7 @@ template <int NS>
 __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per_eu(4))) linrec_fwd_lb(
     const float* __restrict__ A, const float* __restrict__ v, const float* __restrict__ x0, float* __restrict__ x,
     const double* __restrict__ Mc, const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc,
-    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
+    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, LbCfg lb_spacing) {
   constexpr int S = steps_per_chunk<NS>(), NN = NS * NS;
   __shared__ LdsTile s_lds[kLbWaves];
   __shared__ int s_flag[kLbWaves][64];
@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     for (int q = 0; q < NS; ++q) St[q] = (sc == 0 && x0 && live && k == 0) ? (double)x0[lane * NS + q] : 0.0;
     if (sc > 0)  // uniform over the workgroup
       ap_look_back<NS>(St, agg, inc, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc - 1, (int64_t)-1, nsuper, lanes, lane, K,
-                       k, lid, s_lds, s_flag, s_pend, &s_any, counter);
+                       k, lid, s_lds, s_flag, s_pend, &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (lb_pub_inc(sc, lb_spacing) && sc + 1 < nsuper) {
         double ms[NS][NS], o[NS];
@@ -276,7 +276,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     const float* __restrict__ A, const float* __restrict__ g, const float* __restrict__ out,
     const float* __restrict__ x0, float* __restrict__ gv, float* __restrict__ gx0, const double* __restrict__ Mc,
     const double* __restrict__ Ms, double* __restrict__ agg, double* __restrict__ inc, double* __restrict__ part,
-    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, int lb_spacing) {
+    unsigned* __restrict__ counter, int64_t lanes, int64_t L, int64_t groups, int K, int64_t nsuper, LbCfg lb_spacing) {
   constexpr int S = steps_per_chunk<NS>(), NN = NS * NS;
   static_assert(64 * NN * sizeof(double) <= sizeof(LdsTile), "a wave's grad_A sums fit in its tile");
   __shared__ LdsTile s_lds[kLbWaves];
@@ -343,7 +343,7 @@ __global__ void __launch_bounds__(64 * kLbWaves) __attribute__((amdgpu_waves_per
     for (int q = 0; q < NS; ++q) R[q] = 0.0;
     if (sc + 1 < nsuper)  // uniform over the workgroup
       ap_look_back<NS>(R, agg, inc, MatStage<NS>::kLds ? &s_mat[64 * NN + lid * NN] : Ms + lane * NN, k == 0 && live, sc + 1, (int64_t)1, nsuper, lanes, lane, K, k, lid,
-                       s_lds, s_flag, s_pend, &s_any, counter);
+                       s_lds, s_flag, s_pend, &s_any, counter, lb_spacing.spin_max);
     if (k == 0 && live) {
       if (lb_pub_inc(nsuper - 1 - sc, lb_spacing) && sc > 0) {
         double ms[NS][NS], o[NS];

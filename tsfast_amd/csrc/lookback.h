@@ -58,6 +58,18 @@ TSF_DEV double2 quiet_nan<double2>() {
 //    the slots a look-back examines.
 TSF_DEV bool lb_pub_agg(int64_t j, int spacing) { return spacing == 0 ? j > 0 : j % spacing != 0; }
 TSF_DEV bool lb_pub_inc(int64_t j, int spacing) { return spacing == 0 || j % spacing == 0; }
+
+// What a launch tells its look-back kernel: the anchor spacing (0 unless the deterministic mode
+// is on) and the wait bound, the rounds without progress after which a look-back gives up
+// (tsfast_hip_set_lookback_spin_limit). Both are kernel arguments: a bound read from memory would
+// make each round's comparison wait for every outstanding memory operation of the wave,
+// the look-back's own published stores included.
+struct LbCfg {
+  int spacing;
+  uint32_t spin_max;
+};
+TSF_DEV bool lb_pub_agg(int64_t j, LbCfg c) { return lb_pub_agg(j, c.spacing); }
+TSF_DEV bool lb_pub_inc(int64_t j, LbCfg c) { return lb_pub_inc(j, c.spacing); }
 constexpr int kAnchorSpacing = 8;  // deterministic-mode spacing of the look-backs whose window moves
 
 // Give-up flag: the word kErrWord words after the tile counter (inside the kCounterBytes header
@@ -68,9 +80,8 @@ constexpr int kAnchorSpacing = 8;  // deterministic-mode spacing of the look-bac
 // word, a 4-byte word in mapped host memory whose device address the reset kernel writes into the
 // header at word kAlarmWord (8 bytes; zero when the library has no alarm word), so that the host
 // sees it without a device synchronisation and reports each failing call once
-// (tsfast_hip_lookback_gave_up). The header's word kSpinWord holds the wait bound.
+// (tsfast_hip_lookback_gave_up).
 constexpr int kErrWord = 16;
-constexpr int kSpinWord = 17;
 constexpr int kAlarmWord = 18;  // 8-byte aligned: byte offset 72
 constexpr int kEpochWord = 20;
 TSF_DEV void lb_gave_up(unsigned* counter) {
@@ -78,7 +89,6 @@ TSF_DEV void lb_gave_up(unsigned* counter) {
   unsigned* alarm = reinterpret_cast<unsigned*>(*reinterpret_cast<const uint64_t*>(counter + kAlarmWord));
   if (alarm) __hip_atomic_store(alarm, counter[kEpochWord], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
-TSF_DEV uint32_t lb_spin_limit(const unsigned* counter) { return counter[kSpinWord]; }
 
 TSF_DEV unsigned take_tile(unsigned* counter) {
   return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -88,13 +98,12 @@ TSF_DEV unsigned take_tile(unsigned* counter) {
 // kernel rather than a memset node, so that a captured graph replays it reliably).
 __global__ void __launch_bounds__(256) lookback_reset(uint64_t* __restrict__ words, int64_t n,
                                                       unsigned* __restrict__ counter, unsigned* alarm,
-                                                      uint32_t spin_limit, uint32_t epoch) {
+                                                      uint32_t epoch) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) words[i] = kUnset;
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     counter[0] = 0u;
     counter[kErrWord] = 0u;
-    counter[kSpinWord] = spin_limit;
     counter[kEpochWord] = epoch;
     *reinterpret_cast<uint64_t*>(counter + kAlarmWord) = reinterpret_cast<uint64_t>(alarm);
   }
@@ -117,9 +126,11 @@ int64_t resident_wgs(F kern, int threads, int* cache) {
   return (int64_t)c * device_cus();
 }
 
-// The anchor spacing a launch passes to its kernel: 0 unless the deterministic mode is on
-// (tsfast_hip_set_deterministic), then `deterministic_spacing`.
-inline int lb_spacing_for(int deterministic_spacing) { return tsf_deterministic() ? deterministic_spacing : 0; }
+// The look-back arguments of a launch: anchor spacing 0 unless the deterministic mode is on
+// (tsfast_hip_set_deterministic), then `deterministic_spacing`; the library's current wait bound.
+inline LbCfg lb_spacing_for(int deterministic_spacing) {
+  return LbCfg{tsf_deterministic() ? deterministic_spacing : 0, tsf_lookback_spin_limit()};
+}
 
 void lookback_reset_launch(char* ws, int64_t words, hipStream_t s) {
   int64_t blocks = (words + 255) / 256;
@@ -127,5 +138,5 @@ void lookback_reset_launch(char* ws, int64_t words, hipStream_t s) {
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(lookback_reset, dim3((unsigned)blocks), dim3(256), 0, s,
                      reinterpret_cast<uint64_t*>(ws + kCounterBytes), words, reinterpret_cast<unsigned*>(ws),
-                     tsf_lookback_alarm(), tsf_lookback_spin_limit(), tsf_next_epoch());
+                     tsf_lookback_alarm(), tsf_next_epoch());
 }

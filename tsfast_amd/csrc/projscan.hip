@@ -98,14 +98,13 @@ TSF_DEV void block_scan(float2 (&x)[4], float2 lm, float2 lm4, float2 lm8, int l
 // from a zero start; every such chunk has the multiplier P) is composed and the walk moves on; an
 // unpublished word ends the round. The walk ends: the first chunk in scan order publishes its inc
 // without waiting, and every chunk waited on belongs to a tile taken earlier by a running
-// workgroup; a lane that makes no progress for the header's spin-limit rounds gives up with NaN.
+// workgroup; a lane that makes no progress for spin_max rounds gives up with NaN.
 template <int W>
 TSF_DEV double2 walk(const double2* __restrict__ agg, const double2* __restrict__ inc, int64_t cstride, int64_t widx,
-                     int c, int dir, int nc, double2 P, unsigned* __restrict__ lb_counter) {
+                     int c, int dir, int nc, double2 P, unsigned* __restrict__ lb_counter, uint32_t spin_max) {
   double2 accP = Num<double2>::one(), acce = Num<double2>::zero();
   int r = c + dir;
   uint32_t spins = 0;
-  const uint32_t spin_max = lb_spin_limit(lb_counter);
   for (;;) {
     double2 vi[W], va[W];
     bool hi[W], ha[W];
@@ -148,7 +147,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
                  const float2* __restrict__ lam, const float* __restrict__ c_re, const float* __restrict__ c_im,
                  const float2* __restrict__ x0, float* __restrict__ y, float2* __restrict__ x_last,
                  float2* __restrict__ saved, double2* __restrict__ agg, double2* __restrict__ inc,
-                 unsigned* __restrict__ counter, int B, int L, int H, int N, int O, int nchunks, int nsub, int lb_spacing) {
+                 unsigned* __restrict__ counter, int B, int L, int H, int N, int O, int nchunks, int nsub, LbCfg lb_spacing) {
   extern __shared__ __attribute__((aligned(16))) float s_dyn[];
   __shared__ unsigned s_tile[2];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, NW = blockDim.x >> 6;
@@ -256,7 +255,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
         if (x0 != nullptr && s_lb < N) cin = up2(x0[(int64_t)b * N + s_lb]);
       } else {
         if (lb_pub_agg(c, lb_spacing) && c + 1 < nchunks) put(agg + (int64_t)c * cstride + widx, agg_v);
-        cin = walk<2>(agg, inc, cstride, widx, c, -1, nchunks, Pc, counter);
+        cin = walk<2>(agg, inc, cstride, widx, c, -1, nchunks, Pc, counter, lb_spacing.spin_max);
       }
       if (lb_pub_inc(c, lb_spacing) && c + 1 < nchunks)
         put(inc + (int64_t)c * cstride + widx, Num<double2>::fma(Pc, cin, agg_v));
@@ -456,7 +455,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
                  const float2* __restrict__ lam, const float* __restrict__ c_re, const float* __restrict__ c_im,
                  float* __restrict__ g_u, float2* __restrict__ g_x0, float* __restrict__ part, int64_t part_stride,
                  double2* __restrict__ agg, double2* __restrict__ inc, unsigned* __restrict__ counter, int B, int L,
-                 int H, int N, int O, int nsub, int lb_spacing) {
+                 int H, int N, int O, int nsub, LbCfg lb_spacing) {
   constexpr int HB = hb_for_ks<KS>();  // 16-wide h blocks of g_u and grad W (H <= 16 HB)
   constexpr int OKS = 4 * OB;          // o per lane group in the g_x product (O <= 16 OB)
   constexpr int kM = kRho / 4;         // MFMAs per 16-wide h block of g_u
@@ -577,7 +576,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_pe
     if (lb_lane) {
       if (c + 1 < nsub) {
         if (lb_pub_agg(cr, lb_spacing) && c > 0) put(agg + (int64_t)c * cstride + widx, agg_v);
-        R = walk<4>(agg, inc, cstride, widx, c, +1, nsub, cP32, counter);
+        R = walk<4>(agg, inc, cstride, widx, c, +1, nsub, cP32, counter, lb_spacing.spin_max);
       }
       const double2 first = Num<double2>::fma(cP32, R, agg_v);  // G at this chunk's first step
       if (lb_pub_inc(cr, lb_spacing) && c > 0) put(inc + (int64_t)c * cstride + widx, first);
