@@ -64,7 +64,7 @@ int tsfast_hip_get_deterministic(void);
  * there once its kernel has ended), 0 if not, -1 if the word could not be allocated; with
  * `clear` nonzero the call it names counts as reported from then on, so each failing call is
  * reported once. tsfast_hip_set_lookback_spin_limit sets the polls without progress allowed before a
- * give-up (default 2^20, taken by each scan's reset kernel when it is enqueued) and returns the
+ * give-up (default 2^20, passed to each scan's kernels when they are enqueued) and returns the
  * previous limit; a small limit lets a test force a give-up while every kernel still exits.
  * No counterpart in the reference, whose scans never wait on other workgroups. */
 int tsfast_hip_lookback_gave_up(int clear);
