@@ -553,21 +553,30 @@ def gblock_inputs(dev, B=64, L=16384, I=8, O=8, nb=8, na=3):
     a = torch.empty(O, I, na)
     for o in range(O):
         for j in range(I):
-            r = (torch.rand(na, generator=g) * 0.48 + 0.5).numpy()
-            a[o, j] = torch.tensor(np.poly(r)[1:], dtype=torch.float32)
+            r = (torch.rand(na, generator=g) * 0.48 + 0.5).double().numpy()
+            # higher orders (--order): keep the fp32-rounded filter stable (spectral radius < 0.99)
+            for _ in range(60):
+                ai = np.poly(r)[1:].astype(np.float32)
+                cm = np.eye(na, k=-1)
+                cm[0] = -ai.astype(np.float64)
+                if na == 1 or np.abs(np.linalg.eigvals(cm)).max() < 0.99:
+                    break
+                r = r * 0.97
+            a[o, j] = torch.tensor(ai, dtype=torch.float32)
     gy = torch.randn(B, L, O, generator=g)
     return u.to(dev), b.to(dev), a.to(dev), gy.to(dev)
 
 
 def run_gblock(args, line):
     """The fused dynoNet G-block (FIR + all-pole + input sum) at config 4's channel structure, with
-    the reference's unfused three-stage path (conv1d, all-pole op, sum) timed in the same run."""
+    the reference's unfused three-stage path (conv1d, all-pole op, sum) timed in the same run.
+    ``--order`` above 4 times the staged path (this library's FIR op, all-pole op and sum)."""
     import torch
 
     from tsfast_amd.dynonet import core as dcore
     from tsfast_amd.dynonet import gblock_hip
 
-    u, b, a, gy = gblock_inputs("cuda")
+    u, b, a, gy = gblock_inputs("cuda", na=args.order)
     B, L, I = u.shape
     O, _, nb = b.shape
     na = a.shape[-1]
@@ -575,12 +584,22 @@ def run_gblock(args, line):
     tail = u.new_zeros(B, nb - 1, I)
     x0 = u.new_zeros(B, P, na)
 
+    fused = na <= 4
+
     def step(ev):
-        mark(ev)
-        y, x_last, saved = gblock_hip._gblock_op(u, b, a, tail, x0)
-        mark(ev)
-        gblock_hip._gblock_bwd_op(gy, None, u, b, a, tail, x0, saved)
-        mark(ev)
+        if fused:
+            mark(ev)
+            y, x_last, saved = gblock_hip._gblock_op(u, b, a, tail, x0)
+            mark(ev)
+            gblock_hip._gblock_bwd_op(gy, None, u, b, a, tail, x0, saved)
+            mark(ev)
+        else:
+            uu, bb, aa = (t.detach().requires_grad_() for t in (u, b, a))
+            mark(ev)
+            y, x_last = gblock_hip.run(uu, bb, aa, tail, x0)
+            mark(ev)
+            torch.autograd.backward(y, gy)
+            mark(ev)
 
     ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
 
@@ -612,8 +631,12 @@ def run_gblock(args, line):
                     "path": "F.conv1d + tsfast_hip::dynonet_allpole + sum over inputs (the reference's stages)"},
     )
     line["dtype"] = "f64"  # fp32 I/O, fp64 recurrence inside
-    kernels = {"fwd": ("gblock_fwd_lb look-back scan + transfer + reset", fwd_ms, fwd_b),
-               "bwd": ("gblock_bwd_lb look-back scan + transfer + reset + finish", bwd_ms, bwd_b)}
+    if fused:
+        kernels = {"fwd": ("gblock_fwd_lb look-back scan + transfer + reset", fwd_ms, fwd_b),
+                   "bwd": ("gblock_bwd_lb look-back scan + transfer + reset + finish", bwd_ms, bwd_b)}
+    else:
+        kernels = {"fwd": ("gb_fir_fwd + all-pole two-pass scan + input sum (staged)", fwd_ms, fwd_b),
+                   "bwd": ("all-pole two-pass adjoint + gb_fir_bwd + gb_fir_reduce (staged)", bwd_ms, bwd_b)}
     cpu = None
     if not args.no_cpu:
         def cpu_leg():
@@ -852,7 +875,8 @@ def main():
     ap.add_argument("--adjoint", action="store_true",
                     help="measure the chunked NSS adjoint scan (n 32, the reference's chunking)")
     ap.add_argument("--order", type=int, default=3,
-                    help="with --linrec: the denominator order n (state size 1..16; config 4 is 3)")
+                    help="with --linrec: the denominator order n (state size 1..16; config 4 is 3); with "
+                         "--gblock: the G-block's denominator order (1..16; above 4 the staged path)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument(
         "--copy-calibration",

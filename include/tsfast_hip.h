@@ -220,6 +220,19 @@ int tsfast_hip_gblock_bwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb
                           const float* g_xlast, const float* u, const float* b, const float* a, const float* u_tail,
                           const float* x0, const double* saved, float* gu, float* gu_tail, float* gb, float* ga,
                           float* gx0, void* workspace, int64_t workspace_bytes, void* stream);
+/* The G-block's FIR stage alone, for blocks the fused kernels decline (denominator orders above 4):
+ * the grouped causal convolution F.conv1d(cat(u_tail, u), flipped taps, groups=I) of
+ * dynonet/core.py:219-222, w[b, j*O + o, t] = sum_{k < nb} b[o, j, k] u[b, t - k, j] (u before the
+ * sequence from u_tail, zero when NULL), written in the all-pole lane layout w [B, I*O, L]; the
+ * pairs then run tsfast_hip_allpole_fwd/bwd and are summed over inputs by the caller. The
+ * backward gives gu [B, L, I], gu_tail [B, nb-1, I] (may be NULL) and gb [O, I, nb] (summed over
+ * batch and time in a fixed order; the workspace holds fp64 per-tile partials). 1 <= nb <= 64. */
+int64_t tsfast_hip_gblock_fir_workspace_bytes(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb);
+int tsfast_hip_gblock_fir_fwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, const float* u, const float* b,
+                              const float* u_tail, float* w, void* stream);
+int tsfast_hip_gblock_fir_bwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, const float* gw,
+                              const float* u, const float* b, const float* u_tail, float* gu, float* gu_tail,
+                              float* gb, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * Constant-matrix linear recurrence  x_t = A x_{t-1} + v_t  (x_0 = x0, zero when NULL), the

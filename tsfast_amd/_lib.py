@@ -58,6 +58,9 @@ _SIGNATURES: dict[str, tuple[list, object]] = {
     "tsfast_hip_gblock_saved_doubles": ([_i64] * 5, _i64),
     "tsfast_hip_gblock_fwd": ([_i64] * 6 + [_ptr] * 9 + [_i64, _ptr], _int),
     "tsfast_hip_gblock_bwd": ([_i64] * 6 + [_ptr] * 14 + [_i64, _ptr], _int),
+    "tsfast_hip_gblock_fir_workspace_bytes": ([_i64] * 5, _i64),
+    "tsfast_hip_gblock_fir_fwd": ([_i64] * 5 + [_ptr] * 5, _int),
+    "tsfast_hip_gblock_fir_bwd": ([_i64] * 5 + [_ptr] * 8 + [_i64, _ptr], _int),
     "tsfast_hip_linrec_workspace_bytes": ([_i64] * 3, _i64),
     "tsfast_hip_linrec_fwd": ([_i64] * 3 + [_ptr] * 5 + [_i64, _ptr], _int),
     "tsfast_hip_linrec_bwd": ([_i64] * 3 + [_ptr] * 8 + [_i64, _ptr], _int),

@@ -785,6 +785,142 @@ void bwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
                      (const double*)gbl, ga, gb, B, I, O, p.pp, nb);
 }
 
+// ------------------------------------------------------------------------------- FIR stage
+// The G-block's FIR stage on its own, for denominators above the fused kernels' orders (the
+// all-pole stage then runs as tsfast_hip::dynonet_allpole on the pair lanes, and the pairs are
+// summed over inputs): the grouped causal convolution of dynonet/core.py:219-222,
+//   w[b, j*O + o, t] = sum_{k < nb} b[o, j, k] u[b, t - k, j]     (u[b, -m, j] = u_tail[b, nb-1-m, j])
+// with w in the all-pole lane layout [B, I*O, L] (time contiguous). A workgroup takes one batch
+// row, one input channel and 256 steps: the steps' u values and their nb - 1 step halo go through
+// LDS once (u is channel-last, so a row of steps is strided), and each thread forms its step for
+// every output channel from the same nb registers; coefficients are uniform (scalar) loads.
+constexpr int kFirT = 256;
+constexpr int kFirMaxNB = 64;
+
+struct FirTile {
+  int64_t b, t0;
+  int j;
+};
+TSF_DEV FirTile fir_tile(int64_t tiles_t, int I) {
+  FirTile f;
+  const int64_t g = blockIdx.x;
+  const int64_t tt = g % tiles_t, rest = g / tiles_t;
+  f.j = (int)(rest % I);
+  f.b = rest / I;
+  f.t0 = tt * kFirT;
+  return f;
+}
+// u_ext[b, t, j] for t in [-(nb - 1), L): u, then the carried tail (zero without it)
+TSF_DEV float fir_u(const float* __restrict__ u, const float* __restrict__ u_tail, int64_t b, int64_t t, int j,
+                    int64_t L, int I, int nb) {
+  if (t >= 0) return t < L ? u[(b * L + t) * I + j] : 0.0f;
+  if (!u_tail || t < -(int64_t)(nb - 1)) return 0.0f;
+  return u_tail[(b * (nb - 1) + (nb - 1 + t)) * I + j];
+}
+
+__global__ void __launch_bounds__(kFirT) gb_fir_fwd(const float* __restrict__ u, const float* __restrict__ bcoef,
+                                                    const float* __restrict__ u_tail, float* __restrict__ w,
+                                                    int64_t L, int I, int O, int nb, int64_t tiles_t) {
+  __shared__ float s_u[kFirT + kFirMaxNB - 1];
+  const FirTile f = fir_tile(tiles_t, I);
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kFirT + nb - 1; i += kFirT) s_u[i] = fir_u(u, u_tail, f.b, f.t0 - (nb - 1) + i, f.j, L, I, nb);
+  __syncthreads();
+  const int64_t t = f.t0 + tid;
+  if (t >= L) return;
+  float uk[kFirMaxNB];  // uk[k] = u_ext[t - k]
+#pragma unroll
+  for (int k = 0; k < kFirMaxNB; ++k)
+    if (k < nb) uk[k] = s_u[tid + nb - 1 - k];
+  const int P = I * O;
+  for (int o = 0; o < O; ++o) {
+    const float* bk = bcoef + ((int64_t)o * I + f.j) * nb;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kFirMaxNB; ++k)
+      if (k < nb) acc = fmaf(bk[k], uk[k], acc);
+    w[((f.b * P + (int64_t)f.j * O + o) * L) + t] = acc;
+  }
+}
+
+// FIR adjoint, one workgroup per (batch row, input channel, 256 steps) as the forward:
+//   gu[b, t, j]      = sum_o sum_k b[o, j, k] gw[b, j*O + o, t + k]      (gw zero from L on)
+//   gu_tail[b, m, j] = the same sum at t = m - (nb - 1) < 0
+//   part[., o, k]    = sum over the tile's steps of gw[b, j*O + o, t] u_ext[b, t - k, j]  (fp64)
+// Output channels go through LDS in blocks of kFirOB rows of gw (with the nb - 1 step halo on the
+// right); the grad-b partials are summed over tiles and batch rows by gb_fir_reduce.
+constexpr int kFirOB = 16;
+__global__ void __launch_bounds__(kFirT) gb_fir_bwd(const float* __restrict__ gw, const float* __restrict__ u,
+                                                    const float* __restrict__ bcoef, const float* __restrict__ u_tail,
+                                                    float* __restrict__ gu, float* __restrict__ gu_tail,
+                                                    double* __restrict__ part, int64_t L, int I, int O, int nb,
+                                                    int64_t tiles_t) {
+  __shared__ float s_u[kFirT + kFirMaxNB - 1];
+  __shared__ float s_g[kFirOB][kFirT + kFirMaxNB - 1];
+  const FirTile f = fir_tile(tiles_t, I);
+  const int tid = threadIdx.x;
+  const int P = I * O;
+  for (int i = tid; i < kFirT + nb - 1; i += kFirT) s_u[i] = fir_u(u, u_tail, f.b, f.t0 - (nb - 1) + i, f.j, L, I, nb);
+  const int64_t t = f.t0 + tid;
+  const int nt = (int)((L - f.t0) < kFirT ? (L - f.t0) : kFirT);  // steps of this tile
+  const bool tail = f.t0 == 0 && gu_tail && nb > 1 && tid < nb - 1;
+  float acc = 0.0f, acc_tail = 0.0f;
+  double* pw = part + (((f.b * tiles_t + f.t0 / kFirT) * I + f.j) * O) * nb;
+  for (int o0 = 0; o0 < O; o0 += kFirOB) {
+    const int ob = (O - o0) < kFirOB ? (O - o0) : kFirOB;
+    __syncthreads();  // the previous block's readers are done
+    for (int e = tid; e < ob * (kFirT + nb - 1); e += kFirT) {
+      const int r = e / (kFirT + nb - 1), i = e - r * (kFirT + nb - 1);
+      const int64_t tt = f.t0 + i;
+      s_g[r][i] = tt < L ? gw[(f.b * P + (int64_t)f.j * O + o0 + r) * L + tt] : 0.0f;
+    }
+    __syncthreads();
+    for (int r = 0; r < ob; ++r) {
+      const float* bk = bcoef + ((int64_t)(o0 + r) * I + f.j) * nb;
+      for (int k = 0; k < nb; ++k) acc = fmaf(bk[k], s_g[r][tid + k], acc);
+      if (tail) {
+        // gu_tail[m] with m = tid: t = m - (nb - 1), so gw index t + k >= 0 means k >= nb - 1 - m
+        for (int k = nb - 1 - tid; k < nb; ++k) acc_tail = fmaf(bk[k], s_g[r][tid - (nb - 1) + k], acc_tail);
+      }
+    }
+    // grad-b partials of this block: one (o, k) per thread at a time, a dot product over the steps
+    for (int e = tid; e < ob * nb; e += kFirT) {
+      const int r = e / nb, k = e - r * nb;
+      double d = 0.0;
+      for (int i = 0; i < nt; ++i) d = fma((double)s_g[r][i], (double)s_u[i + nb - 1 - k], d);
+      pw[(o0 + r) * nb + k] = d;
+    }
+  }
+  if (t < L) gu[(f.b * L + t) * I + f.j] = acc;
+  if (tail) gu_tail[(f.b * (nb - 1) + tid) * I + f.j] = acc_tail;
+}
+
+// grad b [O, I, nb]: per entry, the sum of the partials over batch rows and tiles in a fixed
+// order (a workgroup per entry: strided partial sums, then a tree in LDS).
+__global__ void __launch_bounds__(256) gb_fir_reduce(const double* __restrict__ part, float* __restrict__ gb,
+                                                     int64_t rows, int I, int O, int nb) {
+  __shared__ double s_r[256];
+  const int64_t e = blockIdx.x;  // (o, j, k) with the [O, I, nb] layout of b
+  const int k = (int)(e % nb), j = (int)((e / nb) % I), o = (int)(e / ((int64_t)nb * I));
+  double acc = 0.0;
+  for (int64_t r = threadIdx.x; r < rows; r += 256) acc += part[((r * I + j) * O + o) * nb + k];
+  s_r[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) s_r[threadIdx.x] += s_r[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) gb[e] = (float)s_r[0];
+}
+
+int fir_args_status(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb) {
+  if (B < 0 || L < 0 || I < 1 || O < 1 || nb < 1) return TSF_ERR_ARG;
+  if (nb > kFirMaxNB) return TSF_ERR_UNSUPPORTED;
+  const int64_t tiles = B * I * ((L + kFirT - 1) / kFirT);
+  if (tiles > INT32_MAX || I * O > INT32_MAX / 2) return TSF_ERR_UNSUPPORTED;
+  return TSF_OK;
+}
+
 #define TSF_GB_CASES(X) \
   X(1, 2) X(1, 4) X(1, 8) X(1, 16) X(2, 2) X(2, 4) X(2, 8) X(2, 16) X(3, 2) X(3, 4) X(3, 8) X(3, 16) X(4, 2) X(4, 4) X(4, 8) X(4, 16)
 
@@ -855,6 +991,46 @@ int tsfast_hip_gblock_bwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb
     default:
       return TSF_ERR_UNSUPPORTED;
   }
+  return tsf_launch_status();
+}
+
+int64_t tsfast_hip_gblock_fir_workspace_bytes(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb) {
+  if (fir_args_status(B, L, I, O, nb) != TSF_OK) return -1;
+  return 8 * B * ((L + kFirT - 1) / kFirT) * I * O * nb;
+}
+
+int tsfast_hip_gblock_fir_fwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, const float* u, const float* b,
+                              const float* u_tail, float* w, void* stream) {
+  const int st = fir_args_status(B, L, I, O, nb);
+  if (st != TSF_OK) return st;
+  if (B == 0 || L == 0) return TSF_OK;
+  if (!u || !b || !w) return TSF_ERR_ARG;
+  const int64_t tiles_t = (L + kFirT - 1) / kFirT;
+  hipLaunchKernelGGL(gb_fir_fwd, dim3((unsigned)(B * I * tiles_t)), dim3(kFirT), 0, static_cast<hipStream_t>(stream),
+                     u, b, u_tail, w, L, (int)I, (int)O, (int)nb, tiles_t);
+  return tsf_launch_status();
+}
+
+int tsfast_hip_gblock_fir_bwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb, const float* gw,
+                              const float* u, const float* b, const float* u_tail, float* gu, float* gu_tail,
+                              float* gb, void* workspace, int64_t workspace_bytes, void* stream) {
+  const int st = fir_args_status(B, L, I, O, nb);
+  if (st != TSF_OK) return st;
+  if (!b || !gb || (L > 0 && B > 0 && (!gw || !u || !gu))) return TSF_ERR_ARG;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t tiles_t = (L + kFirT - 1) / kFirT, rows = B * tiles_t;
+  if (rows == 0) {  // no steps: grad b and the tail gradient are zero
+    hipLaunchKernelGGL(gblock_zero, grid_for(O * I * nb), dim3(256), 0, s, gb, O * I * nb);
+    if (gu_tail && nb > 1 && B > 0)
+      hipLaunchKernelGGL(gblock_zero, grid_for(B * (nb - 1) * I), dim3(256), 0, s, gu_tail, B * (nb - 1) * I);
+    return tsf_launch_status();
+  }
+  if (!workspace || workspace_bytes < tsfast_hip_gblock_fir_workspace_bytes(B, L, I, O, nb)) return TSF_ERR_WORKSPACE;
+  double* part = static_cast<double*>(workspace);
+  hipLaunchKernelGGL(gb_fir_bwd, dim3((unsigned)(B * I * tiles_t)), dim3(kFirT), 0, s, gw, u, b, u_tail, gu, gu_tail,
+                     part, L, (int)I, (int)O, (int)nb, tiles_t);
+  hipLaunchKernelGGL(gb_fir_reduce, dim3((unsigned)(O * I * nb)), dim3(256), 0, s, (const double*)part, gb, rows,
+                     (int)I, (int)O, (int)nb);
   return tsf_launch_status();
 }
 

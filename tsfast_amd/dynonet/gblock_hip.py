@@ -11,10 +11,13 @@ outputs from per-super-chunk states the forward saves (a few MB).
 (y, x_last)``, differentiable in all inputs through the ``tsfast_hip::dynonet_gblock`` /
 ``dynonet_gblock_bwd`` custom ops. Shapes follow the reference: ``u [B, L, I]``, ``b_coeff
 [O, I, nb]``, ``a_coeff [O, I, na]``, ``u_tail [B, nb-1, I]``, ``x0 [B, I*O, na]`` (pairs input-major,
-newest first); ``y [B, L, O]``, ``x_last [B, I*O, na]``. float32; ``1 <= na <= 4``, ``nb <= 16``,
-any number of channel pairs. One launch per direction serves up to 64 pairs (a batch row's pairs
-padded to a power of two inside the kernels); a larger block runs as groups of whole inputs (and,
-past 64 outputs, of outputs) of at most 64 pairs each, whose outputs and gradients add up.
+newest first); ``y [B, L, O]``, ``x_last [B, I*O, na]``. float32, any number of channel pairs.
+Orders ``na <= 4`` with ``nb <= 16`` run the fused kernels: one launch per direction serves up to
+64 pairs (a batch row's pairs padded to a power of two inside the kernels); a larger block runs as
+groups of whole inputs (and, past 64 outputs, of outputs) of at most 64 pairs each, whose outputs
+and gradients add up. Orders ``5 <= na <= 16`` (or ``nb`` up to 64) run the three stages on this
+library's kernels: the FIR stage (``tsfast_hip::dynonet_fir``, writing ``w`` in the all-pole lane
+layout), the all-pole op on the pair lanes (``allpole_hip``), and a sum over inputs.
 """
 
 from __future__ import annotations
@@ -25,9 +28,11 @@ import torch
 
 from .. import _lib
 
-_MAX_NA = 4
+_MAX_NA = 4  # orders of the fused kernels
 _MAX_NB = 16
 _MAX_PAIRS = 64  # pairs one launch serves (a tile of 64 lanes holds whole batch rows)
+_MAX_NA_STAGED = 16  # orders of the staged path (the all-pole kernels' range)
+_MAX_NB_STAGED = 64  # taps of the FIR kernel
 
 
 def supports(u, b_coeff, a_coeff, u_tail, x0) -> str | None:
@@ -49,10 +54,10 @@ def supports(u, b_coeff, a_coeff, u_tail, x0) -> str | None:
     na = a_coeff.shape[-1]
     if I_b != I or tuple(a_coeff.shape[:2]) != (O, I):
         return f"coefficient shapes {tuple(b_coeff.shape)}, {tuple(a_coeff.shape)} do not match {I} inputs"
-    if not 1 <= na <= _MAX_NA:
-        return f"denominator order {na} outside [1, {_MAX_NA}]"
-    if not 1 <= nb <= _MAX_NB:
-        return f"numerator taps {nb} outside [1, {_MAX_NB}]"
+    if not 1 <= na <= _MAX_NA_STAGED:
+        return f"denominator order {na} outside [1, {_MAX_NA_STAGED}]"
+    if not 1 <= nb <= _MAX_NB_STAGED:
+        return f"numerator taps {nb} outside [1, {_MAX_NB_STAGED}]"
     if u_tail is not None and tuple(u_tail.shape) != (B, nb - 1, I):
         return f"u_tail.shape {tuple(u_tail.shape)} != {(B, nb - 1, I)}"
     if x0 is not None and tuple(x0.shape) != (B, I * O, na):
@@ -183,6 +188,104 @@ def _groups(I: int, O: int) -> tuple[list[range], list[range]]:
     return ([range(i, min(i + gi, I)) for i in range(0, I, gi)], [range(o, min(o + go, O)) for o in range(0, O, go)])
 
 
+def _fused(na: int, nb: int) -> bool:
+    return na <= _MAX_NA and nb <= _MAX_NB
+
+
+# ------------------------------------------------------------------------------ staged path
+@torch.library.custom_op("tsfast_hip::dynonet_fir", mutates_args=())
+def _fir_op(u: torch.Tensor, b: torch.Tensor, u_tail: torch.Tensor | None) -> torch.Tensor:
+    lib = _lib.load()
+    u, b = u.contiguous(), b.contiguous()
+    u_tail = u_tail.contiguous() if u_tail is not None else None
+    for name, t in (("u", u), ("b_coeff", b), ("u_tail", u_tail)):
+        _lib.require(t, name, (torch.float32,), u.device)
+    B, L, I = u.shape
+    O, _, nb = b.shape
+    w = torch.empty(B, I * O, L, device=u.device, dtype=torch.float32)
+    _lib.check(
+        lib.tsfast_hip_gblock_fir_fwd(B, L, I, O, nb, _lib.ptr(u), _lib.ptr(b), _lib.ptr(u_tail), _lib.ptr(w),
+                                      _lib.stream_of(u)),
+        "tsfast_hip_gblock_fir_fwd",
+    )
+    return w
+
+
+@_fir_op.register_fake
+def _(u, b, u_tail):
+    B, L, I = u.shape
+    return u.new_empty(B, I * b.shape[0], L)
+
+
+@torch.library.custom_op("tsfast_hip::dynonet_fir_bwd", mutates_args=())
+def _fir_bwd_op(
+    gw: torch.Tensor, u: torch.Tensor, b: torch.Tensor, u_tail: torch.Tensor | None
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    gw = gw.contiguous()
+    _lib.require(gw, "gw", (torch.float32,), u.device)
+    B, L, I = u.shape
+    O, _, nb = b.shape
+    gu = torch.empty_like(u)
+    gu_tail = torch.zeros(B, nb - 1, I, device=u.device, dtype=torch.float32)
+    gb = torch.empty_like(b)
+    n = lib.tsfast_hip_gblock_fir_workspace_bytes(B, L, I, O, nb)
+    if n < 0:
+        raise RuntimeError("tsfast_hip_gblock_fir_workspace_bytes: unsupported shape")
+    ws = _lib.workspace(n, u.device)
+    _lib.check(
+        lib.tsfast_hip_gblock_fir_bwd(
+            B, L, I, O, nb, _lib.ptr(gw), _lib.ptr(u), _lib.ptr(b), _lib.ptr(u_tail), _lib.ptr(gu),
+            _lib.ptr(gu_tail), _lib.ptr(gb), _lib.ptr(ws), n, _lib.stream_of(u),
+        ),
+        "tsfast_hip_gblock_fir_bwd",
+    )
+    return gu, gu_tail, gb
+
+
+@_fir_bwd_op.register_fake
+def _(gw, u, b, u_tail):
+    B, _, I = u.shape
+    return torch.empty_like(u), u.new_empty(B, b.shape[-1] - 1, I), torch.empty_like(b)
+
+
+def _fir_setup(ctx, inputs, output):
+    u, b, u_tail = inputs
+    ctx.has_tail = u_tail is not None
+    ctx.save_for_backward(u, b, u_tail)
+
+
+def _fir_backward(ctx, gw):
+    u, b, u_tail = ctx.saved_tensors
+    gu, gu_tail, gb = _fir_bwd_op(gw, u.contiguous(), b.contiguous(),
+                                  u_tail.contiguous() if u_tail is not None else None)
+    return gu, gb, (gu_tail if ctx.has_tail else None)
+
+
+_fir_op.register_autograd(_fir_backward, setup_context=_fir_setup)
+
+
+def _run_staged(u, b_coeff, a_coeff, u_tail, x0):
+    """FIR stage, all-pole op on the pair lanes and the sum over inputs, as the reference's three
+    stages (dynonet/core.py:219-250) but on this library's kernels; every step is differentiable."""
+    from . import allpole_hip
+
+    B, L, I = u.shape
+    O, _, nb = b_coeff.shape
+    na = a_coeff.shape[-1]
+    P = I * O
+    w = _fir_op(u, b_coeff, u_tail)  # [B, P, L], pair p = j * O + o
+    a_pairs = a_coeff.permute(1, 0, 2).reshape(P, na)
+    y_pairs = allpole_hip.run(a_pairs, w, x0)
+    if L >= na:
+        x_last = y_pairs[..., L - na :].flip(-1)
+    else:
+        head = x0[..., : na - L] if x0 is not None else y_pairs.new_zeros(B, P, na - L)
+        x_last = torch.cat((y_pairs.flip(-1), head), dim=-1)
+    y = y_pairs.view(B, I, O, L).sum(1).transpose(1, 2)
+    return y, x_last
+
+
 def run(u, b_coeff, a_coeff, u_tail, x0):
     """Fused G-block: ``y [B, L, O]`` and the all-pole state ``x_last [B, I*O, na]`` (newest first).
 
@@ -192,6 +295,8 @@ def run(u, b_coeff, a_coeff, u_tail, x0):
     other pairs, so y adds the groups' outputs and each pair's state comes from its own group.
     """
     I, O = u.shape[-1], b_coeff.shape[0]
+    if not _fused(a_coeff.shape[-1], b_coeff.shape[-1]):
+        return _run_staged(u, b_coeff, a_coeff, u_tail, x0)
     if I * O <= _MAX_PAIRS:
         y, x_last, _ = _gblock_op(u, b_coeff, a_coeff, u_tail, x0)
         return y, x_last
