@@ -30,6 +30,7 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--config 3] [--io b
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -196,20 +197,28 @@ def allpole_inputs(device, P=64, B=64, L=16384, na=3):
 # --------------------------------------------------------------------------- timing
 def time_steps(step, steps, warmup):
     """W untimed steps, then K timed steps between device synchronisations; step(ev) records
-    events at phase boundaries. Returns (ms per step, [mean ms per phase])."""
+    events at phase boundaries. Returns (ms per step, [mean ms per phase]). Python's cyclic
+    collector is run before and held off during the steps (as timeit does): a full collection
+    stalls the host for tens of milliseconds, starving the GPU of launches, and where it falls
+    depends on allocation counts that differ between a first and a later process."""
     import torch
 
-    for _ in range(warmup):
-        step(None)
-    torch.cuda.synchronize()
-    events = []
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        ev = []
-        step(ev)
-        events.append(ev)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
+    gc.collect()
+    gc.disable()
+    try:
+        for _ in range(warmup):
+            step(None)
+        torch.cuda.synchronize()
+        events = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ev = []
+            step(ev)
+            events.append(ev)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    finally:
+        gc.enable()
     phases = []
     if events and events[0]:
         for p in range(len(events[0]) - 1):

@@ -11,7 +11,7 @@ constexpr uint64_t kUnset = 0x7FF00000DEADBEEFull;
 // Polls without progress before a look-back gives up and yields NaN (about a second): every
 // wait ends even if an invariant below were broken, and the NaN shows in the outputs. The bound
 // a scan uses is the library's current limit (tsfast_hip_set_lookback_spin_limit, default
-// kSpinMax), which the reset kernel writes into the workspace header.
+// kSpinMax), passed to its kernels at enqueue (LbCfg below).
 constexpr uint32_t kSpinMax = 1u << 20;
 
 TSF_DEV void put_word(double* p, double x) {
