@@ -16,10 +16,12 @@
 // to M s + e, with M a power of the companion matrix C and e the chunk's zero-state end. Orders
 // NA <= 4 run single-pass kernels with a decoupled look-back between workgroups (every input
 // element read once; described at allpole_fwd_lb). Higher orders, whose NA x NA matrices do not
-// fit in registers, run a two-pass scan with chunks of T_c steps, one thread per (lane, chunk):
-//   1. transfer   per lane: M = C^{T_c} (built step by step up to C^256), stored in the workspace;
+// fit in registers, run a two-pass scan with chunks of T_c steps (at most 256 when the sequence
+// takes more than one chunk), one thread per (lane, chunk) in the streaming passes:
+//   1. transfer   per (lane, column): M = C^{T_c}, C applied T_c times to a unit vector;
 //   2. chunk_end  per (lane, chunk): e_c from a zero entering state;
-//   3. carry      per lane: entering states S_c = M S_{c-1} + e_{c-1}, sequential over chunks;
+//   3. carry      per lane (16 threads, one state component each): entering states
+//                 S_c = M S_{c-1} + e_{c-1}, sequential over chunks;
 //   4. apply      per (lane, chunk): run the chunk from S_c and write y.
 // The adjoint G_t = g_t - sum_i a_i G_{t+i} is the same filter run backwards, so the backward
 // reuses the matrices with the chunk order reversed and accumulates grad_a partials per chunk;
@@ -34,9 +36,36 @@ namespace {
 #include "allpole_core.h"
 
 
-// M = C^{T_c} per lane. Powers up to C^256 are built step by step from the unit vectors (fp64;
-// see companion_powers for why not by squaring); a longer chunk takes (C^256)^q C^r, squaring only
-// C^256, whose transient growth has decayed for the stable filters this scan serves.
+// M = C^{T_c} for chunks of at most kColsT steps, one thread per (lane, column): column col is C
+// applied T_c times to the unit vector e_col, step by step in fp64 (see companion_powers_col for
+// why not by squaring), in unrolled 32-step blocks.
+constexpr int64_t kColsT = 256;
+template <int NA>
+__global__ void __launch_bounds__(64) allpole_transfer_cols(const float* __restrict__ a, double* __restrict__ M,
+                                                            int64_t lanes, int T_c) {
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= lanes * NA) return;
+  const int64_t lane = idx / NA;
+  const int col = (int)(idx - lane * NA);
+  double ac[NA], x[NA];
+#pragma unroll
+  for (int c = 0; c < NA; ++c) {
+    ac[c] = (double)a[lane * NA + c];
+    x[c] = c == col ? 1.0 : 0.0;
+  }
+  int t = 0;
+  for (; t + 32 <= T_c; t += 32)
+#pragma unroll
+    for (int step = 0; step < 32; ++step) companion_apply<NA>(x, ac);
+  for (; t < T_c; ++t) companion_apply<NA>(x, ac);
+#pragma unroll
+  for (int r = 0; r < NA; ++r) M[(lane * NA + r) * NA + col] = x[r];
+}
+
+// M = C^{T_c} per lane for chunks longer than kColsT (only sequences of more than 65535 x 256
+// steps). Powers up to C^256 are built step by step from the unit vectors; a longer chunk takes
+// (C^256)^q C^r, squaring only C^256, whose transient growth has decayed for the stable filters
+// this scan serves.
 template <int NA>
 __global__ void __launch_bounds__(256) allpole_transfer(const float* __restrict__ a, double* __restrict__ Mout,
                                                         int64_t lanes, int64_t T_c) {
@@ -123,33 +152,39 @@ __global__ void __launch_bounds__(kTile) allpole_fwd_chunk_end(const float* __re
   }
 }
 
-// 3. forward carries: entering state of every chunk, sequential over chunks per lane.
+// 3. forward carries: the entering state of every chunk, sequential over chunks per lane. Sixteen
+// threads per lane (one 16-lane DPP row): thread r holds state component r and row r of M, and
+// reads the other components by row broadcast. The chunk ends e_c do not depend on the carry and
+// are loaded kCarryPf chunks ahead.
+constexpr int kCarryPf = 8;
 template <int NA>
 __global__ void __launch_bounds__(256) allpole_fwd_carry(const double* __restrict__ M, const double* __restrict__ e,
                                                          const float* __restrict__ y0, double* __restrict__ S,
                                                          int64_t lanes, int64_t nchunk) {
-  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (lane >= lanes) return;
-  double m[NA][NA], s[NA], t[NA];
+  const int r = threadIdx.x & 15;
+  const int64_t lane = blockIdx.x * (int64_t)16 + (threadIdx.x >> 4);
+  const bool ld = lane < lanes && r < NA;
+  double m[NA];
 #pragma unroll
-  for (int r = 0; r < NA; ++r)
+  for (int c = 0; c < NA; ++c) m[c] = ld ? M[(lane * NA + r) * NA + c] : 0.0;
+  double s = (ld && y0) ? (double)y0[lane * NA + r] : 0.0;
+  double ev[kCarryPf];  // ev[k] = e of chunk cb + k (chunks 0 .. nchunk-2 have one)
 #pragma unroll
-    for (int c = 0; c < NA; ++c) m[r][c] = M[(lane * NA + r) * NA + c];
+  for (int k = 0; k < kCarryPf; ++k) ev[k] = (ld && k + 1 < nchunk) ? e[(k * lanes + lane) * NA + r] : 0.0;
+  for (int64_t cb = 0; cb < nchunk; cb += kCarryPf) {
 #pragma unroll
-  for (int k = 0; k < NA; ++k) s[k] = y0 ? (double)y0[lane * NA + k] : 0.0;
-  for (int64_t c = 0; c < nchunk; ++c) {
-#pragma unroll
-    for (int k = 0; k < NA; ++k) S[(c * lanes + lane) * NA + k] = s[k];
-    if (c + 1 < nchunk) {
-#pragma unroll
-      for (int r = 0; r < NA; ++r) {
-        double acc = e[(c * lanes + lane) * NA + r];
-#pragma unroll
-        for (int j = 0; j < NA; ++j) acc = fma(m[r][j], s[j], acc);
-        t[r] = acc;
+    for (int k = 0; k < kCarryPf; ++k) {
+      const int64_t c = cb + k;
+      if (c < nchunk) {  // uniform over the workgroup
+        if (ld) S[(c * lanes + lane) * NA + r] = s;
+        if (c + 1 < nchunk) {
+          double a0 = ev[k], a1 = 0.0;
+          row_dot2<NA>(m, s, a0, a1);
+          s = a0 + a1;
+        }
+        const int64_t cn = c + kCarryPf;
+        ev[k] = (ld && cn + 1 < nchunk) ? e[(cn * lanes + lane) * NA + r] : 0.0;
       }
-#pragma unroll
-      for (int k = 0; k < NA; ++k) s[k] = t[k];
     }
   }
 }
@@ -234,36 +269,41 @@ __global__ void __launch_bounds__(kTile) allpole_bwd_chunk_start(const float* __
 }
 
 // Backward 3. entering (from the right) states of every chunk: R_last = 0, R_{last-1} = f_last,
-// R_c = M R_{c+1} + f_{c+1}.
+// R_c = M R_{c+1} + f_{c+1}; the thread layout and prefetch of the forward carry.
 template <int NA>
 __global__ void __launch_bounds__(256) allpole_bwd_carry(const double* __restrict__ M, const double* __restrict__ f,
                                                          double* __restrict__ R, int64_t lanes, int64_t nchunk) {
-  const int64_t lane = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (lane >= lanes) return;
-  double m[NA][NA], s[NA], t[NA];
+  const int r = threadIdx.x & 15;
+  const int64_t lane = blockIdx.x * (int64_t)16 + (threadIdx.x >> 4);
+  const bool ld = lane < lanes && r < NA;
+  double m[NA];
 #pragma unroll
-  for (int r = 0; r < NA; ++r)
+  for (int c = 0; c < NA; ++c) m[c] = ld ? M[(lane * NA + r) * NA + c] : 0.0;
+  double s = 0.0;
+  double fv[kCarryPf];  // fv[k] = f of chunk nchunk-1 - (cb + k) (chunks 1 .. nchunk-1 have one)
 #pragma unroll
-    for (int c = 0; c < NA; ++c) m[r][c] = M[(lane * NA + r) * NA + c];
+  for (int k = 0; k < kCarryPf; ++k) {
+    const int64_t c = nchunk - 1 - k;
+    fv[k] = (ld && c >= 1) ? f[(c * lanes + lane) * NA + r] : 0.0;
+  }
+  for (int64_t cb = 0; cb < nchunk; cb += kCarryPf) {
 #pragma unroll
-  for (int k = 0; k < NA; ++k) s[k] = 0.0;
-  for (int64_t c = nchunk - 1; c >= 0; --c) {
-#pragma unroll
-    for (int k = 0; k < NA; ++k) R[(c * lanes + lane) * NA + k] = s[k];
-    if (c > 0) {
-      // exit of chunk c toward the left = entering state of chunk c-1
-      const bool last = (c == nchunk - 1);  // its entering state is zero, M is irrelevant
-#pragma unroll
-      for (int r = 0; r < NA; ++r) {
-        double acc = f[(c * lanes + lane) * NA + r];
-        if (!last) {
-#pragma unroll
-          for (int j = 0; j < NA; ++j) acc = fma(m[r][j], s[j], acc);
+    for (int k = 0; k < kCarryPf; ++k) {
+      const int64_t c = nchunk - 1 - (cb + k);
+      if (c >= 0) {  // uniform over the workgroup
+        if (ld) R[(c * lanes + lane) * NA + r] = s;
+        if (c > 0) {
+          if (c == nchunk - 1) {
+            s = fv[k];  // the last chunk enters from a zero state: its exit is f alone
+          } else {
+            double a0 = fv[k], a1 = 0.0;
+            row_dot2<NA>(m, s, a0, a1);
+            s = a0 + a1;
+          }
         }
-        t[r] = acc;
+        const int64_t cn = c - kCarryPf;
+        fv[k] = (ld && cn >= 1) ? f[(cn * lanes + lane) * NA + r] : 0.0;
       }
-#pragma unroll
-      for (int k = 0; k < NA; ++k) s[k] = t[k];
     }
   }
 }
@@ -633,6 +673,9 @@ struct Plan {
 Plan plan(int64_t lanes, int64_t L, int64_t na) {
   Plan p;
   p.T_c = allpole_chunk(lanes, L, na);
+  // a chunked sequence takes chunks of at most kColsT steps, whose transfer matrix is stepped
+  // column by column, unless that needs more than 65535 chunks (one grid row each)
+  if (p.T_c < L && p.T_c > kColsT && (L + kColsT - 1) / kColsT <= 65535) p.T_c = kColsT;
   p.nchunk = (L + p.T_c - 1) / p.T_c;
   const size_t f = 8;  // fp64 transfer matrices, carries and partials
   p.off_M = 0;
@@ -680,6 +723,17 @@ void bwd_lb(int64_t lanes, int64_t L, const float* g, const float* a, const floa
                      ga, gy0, lanes, L, p.nsuper);
 }
 
+// M = C^{T_c} (needed only when the sequence takes more than one chunk; a single chunk enters
+// from y0 directly)
+template <int NA>
+void transfer_launch(const Plan& p, const float* a, double* M, int64_t lanes, hipStream_t s) {
+  if (p.T_c <= kColsT)
+    hipLaunchKernelGGL((allpole_transfer_cols<NA>), dim3((unsigned)((lanes * NA + 63) / 64)), dim3(64), 0, s, a, M,
+                       lanes, (int)p.T_c);
+  else
+    hipLaunchKernelGGL((allpole_transfer<NA>), grid_for(lanes), dim3(256), 0, s, a, M, lanes, p.T_c);
+}
+
 size_t workspace_bytes_for(int64_t lanes, int64_t L, int64_t na) {
   return na <= kLbNA ? lb_plan(lanes, L, na).bytes : plan(lanes, L, na).bytes;
 }
@@ -695,12 +749,14 @@ int fwd_impl(int64_t lanes, int64_t L, const float* a, const float* w, const flo
   double* M = reinterpret_cast<double*>(ws + p.off_M);
   double* e = reinterpret_cast<double*>(ws + p.off_e);
   double* S = reinterpret_cast<double*>(ws + p.off_S);
-  hipLaunchKernelGGL((allpole_transfer<NA>), grid_for(lanes), dim3(256), 0, s, a, M, lanes, p.T_c);
   const unsigned groups = (unsigned)((lanes + kTile - 1) / kTile);
-  if (p.nchunk > 1)
+  if (p.nchunk > 1) {
+    transfer_launch<NA>(p, a, M, lanes, s);
     hipLaunchKernelGGL((allpole_fwd_chunk_end<NA>), dim3(groups, (unsigned)(p.nchunk - 1)), dim3(kTile), 0, s, a, w, e,
                        lanes, L, p.T_c, p.nchunk);
-  hipLaunchKernelGGL((allpole_fwd_carry<NA>), grid_for(lanes), dim3(256), 0, s, M, e, y0, S, lanes, p.nchunk);
+  }
+  hipLaunchKernelGGL((allpole_fwd_carry<NA>), dim3((unsigned)((lanes + 15) / 16)), dim3(256), 0, s, M, e, y0, S,
+                     lanes, p.nchunk);
   hipLaunchKernelGGL((allpole_fwd_apply<NA>), dim3(groups, (unsigned)p.nchunk), dim3(kTile), 0, s, a, w, S, y, lanes,
                      L, p.T_c, p.nchunk);
   return tsf_launch_status();
@@ -719,12 +775,14 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* a, const flo
   double* R = reinterpret_cast<double*>(ws + p.off_S);
   double* part = reinterpret_cast<double*>(ws + p.off_part);
   if (L > 0) {
-    hipLaunchKernelGGL((allpole_transfer<NA>), grid_for(lanes), dim3(256), 0, s, a, M, lanes, p.T_c);
     const unsigned groups = (unsigned)((lanes + kTile - 1) / kTile);
-    if (p.nchunk > 1)
+    if (p.nchunk > 1) {
+      transfer_launch<NA>(p, a, M, lanes, s);
       hipLaunchKernelGGL((allpole_bwd_chunk_start<NA>), dim3(groups, (unsigned)(p.nchunk - 1)), dim3(kTile), 0, s, a,
                          g, f, lanes, L, p.T_c, p.nchunk);
-    hipLaunchKernelGGL((allpole_bwd_carry<NA>), grid_for(lanes), dim3(256), 0, s, M, f, R, lanes, p.nchunk);
+    }
+    hipLaunchKernelGGL((allpole_bwd_carry<NA>), dim3((unsigned)((lanes + 15) / 16)), dim3(256), 0, s, M, f, R, lanes,
+                       p.nchunk);
     hipLaunchKernelGGL((allpole_bwd_apply<NA>), dim3(groups, (unsigned)p.nchunk), dim3(kTile), 0, s, a, g, y, R, gw,
                        part, lanes, L, p.T_c, p.nchunk);
   }

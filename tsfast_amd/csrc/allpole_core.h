@@ -144,6 +144,38 @@ TSF_DEV void companion_apply(double (&x)[NA], const double (&a)[NA]) {
   x[0] = y0;
 }
 
+// The value x holds in lane K (0..15) of this thread's 16-lane DPP row (row_newbcast: every lane
+// of the row reads lane K; an fp64 value moves as two 32-bit halves).
+template <int K>
+TSF_DEV uint32_t row_lane_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x150 + K, 0xF, 0xF, true);
+}
+template <int K>
+TSF_DEV double row_lane(double x) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint64_t lo = row_lane_u32<K>((uint32_t)b), hi = row_lane_u32<K>((uint32_t)(b >> 32));
+  return __longlong_as_double((long long)((hi << 32) | lo));
+}
+template <int K>
+TSF_DEV float row_lane(float x) {
+  return __uint_as_float(row_lane_u32<K>(__float_as_uint(x)));
+}
+
+// a0 + a1 + sum_{c < N} m[c] * (s of row lane c): one matrix row times a state vector spread over
+// a 16-lane DPP row (component c in lane c), in two interleaved partial sums so that consecutive
+// FMAs do not wait on each other. Called by all 16 lanes of the row together.
+template <int N, int C = 0>
+TSF_DEV void row_dot2(const double (&m)[N], double s, double& a0, double& a1) {
+  if constexpr (C < N) {
+    if constexpr (C % 2 == 0) {
+      a0 = fma(m[C], row_lane<C>(s), a0);
+    } else {
+      a1 = fma(m[C], row_lane<C>(s), a1);
+    }
+    row_dot2<N, C + 1>(m, s, a0, a1);
+  }
+}
+
 // Column `col` of both transfer matrices of one companion matrix (row 0 = -arow): Mc = C^32 and
 // Ms = C^(32 K), row-major NA x NA each. The column is C applied step by step to the unit vector
 // e_col in fp64: repeated squaring would compound rounding errors through the transient growth of

@@ -791,107 +791,223 @@ void bwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
 // summed over inputs): the grouped causal convolution of dynonet/core.py:219-222,
 //   w[b, j*O + o, t] = sum_{k < nb} b[o, j, k] u[b, t - k, j]     (u[b, -m, j] = u_tail[b, nb-1-m, j])
 // with w in the all-pole lane layout [B, I*O, L] (time contiguous). A workgroup takes one batch
-// row, one input channel and 256 steps: the steps' u values and their nb - 1 step halo go through
-// LDS once (u is channel-last, so a row of steps is strided), and each thread forms its step for
-// every output channel from the same nb registers; coefficients are uniform (scalar) loads.
-constexpr int kFirT = 256;
+// row, one input channel and kFirT steps, a thread kFirS consecutive steps: the steps' u values
+// and their halo go through LDS once (u is channel-last, so a row of steps is strided), each
+// thread keeps its window of them in registers and forms its steps for every output channel
+// from it. The tap count is padded to NBT (4, 8, 16, 32 or 64; the padding taps are zero), so
+// the inner loops are fixed; a block of kFirOB output channels' taps sits in LDS, read by every
+// thread at the same address.
+constexpr int kFirS = 4;                // steps per thread: one 16-byte row segment of w
+constexpr int kFirW = 256;              // threads per workgroup
+constexpr int kFirT = kFirS * kFirW;    // steps per workgroup
 constexpr int kFirMaxNB = 64;
+constexpr int kFirOB = 8;               // output channels per LDS round
+
+inline int fir_nbt(int64_t nb) { return nb <= 4 ? 4 : nb <= 8 ? 8 : nb <= 16 ? 16 : nb <= 32 ? 32 : 64; }
 
 struct FirTile {
   int64_t b, t0;
   int j;
 };
-TSF_DEV FirTile fir_tile(int64_t tiles_t, int I) {
+// workgroup -> (batch row, input channel, tile); the grid has at most INT32_MAX workgroups
+TSF_DEV FirTile fir_tile(unsigned tiles_t, unsigned I) {
   FirTile f;
-  const int64_t g = blockIdx.x;
-  const int64_t tt = g % tiles_t, rest = g / tiles_t;
+  const unsigned g = blockIdx.x, rest = g / tiles_t;
+  f.t0 = (int64_t)(g - rest * tiles_t) * kFirT;
   f.j = (int)(rest % I);
   f.b = rest / I;
-  f.t0 = tt * kFirT;
   return f;
 }
-// u_ext[b, t, j] for t in [-(nb - 1), L): u, then the carried tail (zero without it)
+// u_ext[b, t, j] for t in [-(nb - 1), L): u, then the carried tail (zero without it, and zero
+// outside both)
 TSF_DEV float fir_u(const float* __restrict__ u, const float* __restrict__ u_tail, int64_t b, int64_t t, int j,
                     int64_t L, int I, int nb) {
   if (t >= 0) return t < L ? u[(b * L + t) * I + j] : 0.0f;
   if (!u_tail || t < -(int64_t)(nb - 1)) return 0.0f;
   return u_tail[(b * (nb - 1) + (nb - 1 + t)) * I + j];
 }
-
-__global__ void __launch_bounds__(kFirT) gb_fir_fwd(const float* __restrict__ u, const float* __restrict__ bcoef,
-                                                    const float* __restrict__ u_tail, float* __restrict__ w,
-                                                    int64_t L, int I, int O, int nb, int64_t tiles_t) {
-  __shared__ float s_u[kFirT + kFirMaxNB - 1];
-  const FirTile f = fir_tile(tiles_t, I);
-  const int tid = threadIdx.x;
-  for (int i = tid; i < kFirT + nb - 1; i += kFirT) s_u[i] = fir_u(u, u_tail, f.b, f.t0 - (nb - 1) + i, f.j, L, I, nb);
-  __syncthreads();
-  const int64_t t = f.t0 + tid;
-  if (t >= L) return;
-  float uk[kFirMaxNB];  // uk[k] = u_ext[t - k]
+// s_u[i] = u_ext[t0 - (NBT - 1) + i], i < kFirT + NBT
+template <int NBT>
+TSF_DEV void fir_stage_u(float* s_u, const float* __restrict__ u, const float* __restrict__ u_tail, const FirTile& f,
+                         int64_t L, int I, int nb) {
+  for (int i = threadIdx.x; i < kFirT + NBT; i += kFirW)
+    s_u[i] = fir_u(u, u_tail, f.b, f.t0 - (NBT - 1) + i, f.j, L, I, nb);
+}
+// taps of output channels o0 .. o0 + kFirOB - 1 for input j, zero past nb and past O
+template <int NBT>
+TSF_DEV void fir_stage_b(float (*s_b)[NBT], const float* __restrict__ bcoef, int o0, int O, int I, int j, int nb) {
+  for (int e = threadIdx.x; e < kFirOB * NBT; e += kFirW) {
+    const int r = e / NBT, k = e - r * NBT;
+    s_b[r][k] = (o0 + r < O && k < nb) ? bcoef[((int64_t)(o0 + r) * I + j) * nb + k] : 0.0f;
+  }
+}
+// x[m] = s[4 * threadIdx.x + m], m < N (16-byte LDS reads; s is 16-byte aligned)
+template <int N>
+TSF_DEV void fir_window(float (&x)[N], const float* s) {
+  const float4* p = reinterpret_cast<const float4*>(s) + threadIdx.x;
 #pragma unroll
-  for (int k = 0; k < kFirMaxNB; ++k)
-    if (k < nb) uk[k] = s_u[tid + nb - 1 - k];
-  const int P = I * O;
-  for (int o = 0; o < O; ++o) {
-    const float* bk = bcoef + ((int64_t)o * I + f.j) * nb;
-    float acc = 0.0f;
+  for (int c = 0; c < (N + 3) / 4; ++c) {
+    const float4 q = p[c];
+    if (4 * c + 0 < N) x[4 * c + 0] = q.x;
+    if (4 * c + 1 < N) x[4 * c + 1] = q.y;
+    if (4 * c + 2 < N) x[4 * c + 2] = q.z;
+    if (4 * c + 3 < N) x[4 * c + 3] = q.w;
+  }
+}
+// whether rows of length L starting at p are 16-byte aligned (then every kFirS-step segment is)
+TSF_DEV bool fir_vec(const float* p, int64_t L) { return (L & 3) == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+// the kFirS steps t .. t + 3 of one row (one 16-byte store when the rows are aligned)
+TSF_DEV void fir_store(float* __restrict__ row, int64_t t, int64_t L, bool vec, const float (&v)[kFirS]) {
+  if (vec && t + kFirS <= L) {
+    *reinterpret_cast<float4*>(row + t) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
 #pragma unroll
-    for (int k = 0; k < kFirMaxNB; ++k)
-      if (k < nb) acc = fmaf(bk[k], uk[k], acc);
-    w[((f.b * P + (int64_t)f.j * O + o) * L) + t] = acc;
+    for (int i = 0; i < kFirS; ++i)
+      if (t + i < L) row[t + i] = v[i];
   }
 }
 
-// FIR adjoint, one workgroup per (batch row, input channel, 256 steps) as the forward:
+template <int NBT>
+__global__ void __launch_bounds__(kFirW) gb_fir_fwd(const float* __restrict__ u, const float* __restrict__ bcoef,
+                                                    const float* __restrict__ u_tail, float* __restrict__ w,
+                                                    int64_t L, int I, int O, int nb, unsigned tiles_t) {
+  __shared__ __align__(16) float s_u[kFirT + NBT];
+  __shared__ __align__(16) float s_b[kFirOB][NBT];
+  const FirTile f = fir_tile(tiles_t, (unsigned)I);
+  fir_stage_u<NBT>(s_u, u, u_tail, f, L, I, nb);
+  __syncthreads();
+  constexpr int NW = NBT + kFirS - 1;
+  float uw[NW];  // uw[m] = u_ext[t - (NBT - 1) + m]
+  fir_window<NW>(uw, s_u);
+  const int64_t t = f.t0 + kFirS * threadIdx.x;
+  const int64_t P = (int64_t)I * O;
+  const bool vec = fir_vec(w, L);
+  for (int o0 = 0; o0 < O; o0 += kFirOB) {
+    __syncthreads();  // the previous block's taps are read
+    fir_stage_b<NBT>(s_b, bcoef, o0, O, I, f.j, nb);
+    __syncthreads();
+    const int ob = (O - o0) < kFirOB ? (O - o0) : kFirOB;
+    for (int r = 0; r < ob; ++r) {
+      float acc[kFirS] = {};
+#pragma unroll
+      for (int k0 = 0; k0 < NBT; k0 += 4) {
+        const float4 bq = *reinterpret_cast<const float4*>(&s_b[r][k0]);
+        const float bk[4] = {bq.x, bq.y, bq.z, bq.w};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+          for (int i = 0; i < kFirS; ++i) acc[i] = fmaf(bk[kk], uw[i + NBT - 1 - (k0 + kk)], acc[i]);
+      }
+      fir_store(w + (f.b * P + (int64_t)f.j * O + o0 + r) * L, t, L, vec, acc);
+    }
+  }
+}
+
+// The sum over a wave's 64 lanes, left in lane 63 (DPP: within quads, across the 16-lane rows by
+// rotation, then row to row by broadcast).
+TSF_DEV float wave_sum_last(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // lane ^ 1
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // lane ^ 2
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));  // row rotate 4
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row rotate 8
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));  // row bcast 15
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));  // row bcast 31
+  return v;
+}
+
+// FIR adjoint, one workgroup per (batch row, input channel, kFirT steps) as the forward:
 //   gu[b, t, j]      = sum_o sum_k b[o, j, k] gw[b, j*O + o, t + k]      (gw zero from L on)
 //   gu_tail[b, m, j] = the same sum at t = m - (nb - 1) < 0
-//   part[., o, k]    = sum over the tile's steps of gw[b, j*O + o, t] u_ext[b, t - k, j]  (fp64)
-// Output channels go through LDS in blocks of kFirOB rows of gw (with the nb - 1 step halo on the
-// right); the grad-b partials are summed over tiles and batch rows by gb_fir_reduce.
-constexpr int kFirOB = 16;
-__global__ void __launch_bounds__(kFirT) gb_fir_bwd(const float* __restrict__ gw, const float* __restrict__ u,
+//   part[., o, k]    = sum over the tile's steps of gw[b, j*O + o, t] u_ext[b, t - k, j]
+// A block of kFirOB rows of gw (with the NBT - 1 step halo on the right) goes through LDS; each
+// thread forms its kFirS steps of gu and its share of every (o, k) partial from register windows,
+// the partials are summed over each wave (DPP) and then over the waves in a fixed order into fp64
+// part [B * tiles][I][O][nb], which gb_fir_reduce sums over batch rows and tiles.
+template <int NBT>
+__global__ void __launch_bounds__(kFirW) gb_fir_bwd(const float* __restrict__ gw, const float* __restrict__ u,
                                                     const float* __restrict__ bcoef, const float* __restrict__ u_tail,
                                                     float* __restrict__ gu, float* __restrict__ gu_tail,
                                                     double* __restrict__ part, int64_t L, int I, int O, int nb,
-                                                    int64_t tiles_t) {
-  __shared__ float s_u[kFirT + kFirMaxNB - 1];
-  __shared__ float s_g[kFirOB][kFirT + kFirMaxNB - 1];
-  const FirTile f = fir_tile(tiles_t, I);
-  const int tid = threadIdx.x;
-  const int P = I * O;
-  for (int i = tid; i < kFirT + nb - 1; i += kFirT) s_u[i] = fir_u(u, u_tail, f.b, f.t0 - (nb - 1) + i, f.j, L, I, nb);
-  const int64_t t = f.t0 + tid;
-  const int nt = (int)((L - f.t0) < kFirT ? (L - f.t0) : kFirT);  // steps of this tile
+                                                    unsigned tiles_t) {
+  constexpr int NS = kFirT + NBT;  // staged steps per row (the halo, rounded up)
+  __shared__ __align__(16) float s_u[NS];
+  __shared__ __align__(16) float s_g[kFirOB][NS];
+  __shared__ __align__(16) float s_b[kFirOB][NBT];
+  __shared__ float s_red[kFirW / 64][kFirOB][NBT];
+  const FirTile f = fir_tile(tiles_t, (unsigned)I);
+  const int tid = threadIdx.x, wave = tid >> 6;
+  fir_stage_u<NBT>(s_u, u, u_tail, f, L, I, nb);
+  const int64_t P = (int64_t)I * O;
+  const int64_t t = f.t0 + kFirS * tid;
   const bool tail = f.t0 == 0 && gu_tail && nb > 1 && tid < nb - 1;
-  float acc = 0.0f, acc_tail = 0.0f;
+  const bool vec = fir_vec(gw, L);
+  float gacc[kFirS] = {};
+  float acc_tail = 0.0f;
+  constexpr int NW = NBT + kFirS - 1;
+  float uw[NW];  // uw[m] = u_ext[t - (NBT - 1) + m]
   double* pw = part + (((f.b * tiles_t + f.t0 / kFirT) * I + f.j) * O) * nb;
   for (int o0 = 0; o0 < O; o0 += kFirOB) {
     const int ob = (O - o0) < kFirOB ? (O - o0) : kFirOB;
-    __syncthreads();  // the previous block's readers are done
-    for (int e = tid; e < ob * (kFirT + nb - 1); e += kFirT) {
-      const int r = e / (kFirT + nb - 1), i = e - r * (kFirT + nb - 1);
-      const int64_t tt = f.t0 + i;
-      s_g[r][i] = tt < L ? gw[(f.b * P + (int64_t)f.j * O + o0 + r) * L + tt] : 0.0f;
-    }
-    __syncthreads();
-    for (int r = 0; r < ob; ++r) {
-      const float* bk = bcoef + ((int64_t)(o0 + r) * I + f.j) * nb;
-      for (int k = 0; k < nb; ++k) acc = fmaf(bk[k], s_g[r][tid + k], acc);
-      if (tail) {
-        // gu_tail[m] with m = tid: t = m - (nb - 1), so gw index t + k >= 0 means k >= nb - 1 - m
-        for (int k = nb - 1 - tid; k < nb; ++k) acc_tail = fmaf(bk[k], s_g[r][tid - (nb - 1) + k], acc_tail);
+    __syncthreads();  // the previous block's rows, taps and wave sums are read
+    for (int r = 0; r < kFirOB; ++r) {
+      const float* grow = gw + (f.b * P + (int64_t)f.j * O + o0 + r) * L;
+      const bool live = r < ob;
+      if (vec) {
+        for (int q = tid; q < NS / 4; q += kFirW) {
+          const int64_t tq = f.t0 + 4 * q;
+          float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          if (live && tq < L) x = *reinterpret_cast<const float4*>(grow + tq);  // L % 4 == 0: all in range
+          reinterpret_cast<float4*>(&s_g[r][0])[q] = x;
+        }
+      } else {
+        for (int i = tid; i < NS; i += kFirW) s_g[r][i] = (live && f.t0 + i < L) ? grow[f.t0 + i] : 0.0f;
       }
     }
-    // grad-b partials of this block: one (o, k) per thread at a time, a dot product over the steps
-    for (int e = tid; e < ob * nb; e += kFirT) {
+    fir_stage_b<NBT>(s_b, bcoef, o0, O, I, f.j, nb);
+    __syncthreads();
+    if (o0 == 0) fir_window<NW>(uw, s_u);
+    for (int r = 0; r < ob; ++r) {
+      float gv[NW];  // gv[m] = gw[t + m]
+      fir_window<NW>(gv, &s_g[r][0]);
+      float p[NBT];
+#pragma unroll
+      for (int k0 = 0; k0 < NBT; k0 += 4) {
+        const float4 bq = *reinterpret_cast<const float4*>(&s_b[r][k0]);
+        const float bk[4] = {bq.x, bq.y, bq.z, bq.w};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int k = k0 + kk;
+          float pk = 0.0f;
+#pragma unroll
+          for (int i = 0; i < kFirS; ++i) {
+            gacc[i] = fmaf(bk[kk], gv[i + k], gacc[i]);
+            pk = fmaf(gv[i], uw[i + NBT - 1 - k], pk);
+          }
+          p[k] = pk;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < NBT; ++k) {
+        const float v = wave_sum_last(p[k]);
+        if ((tid & 63) == 63) s_red[wave][r][k] = v;
+      }
+      if (tail) {
+        // gu_tail[m] with m = tid: t = m - (nb - 1), so gw index t + k >= 0 means k >= nb - 1 - m
+        for (int k = nb - 1 - tid; k < nb; ++k) acc_tail = fmaf(s_b[r][k], s_g[r][tid - (nb - 1) + k], acc_tail);
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < ob * nb; e += kFirW) {
       const int r = e / nb, k = e - r * nb;
       double d = 0.0;
-      for (int i = 0; i < nt; ++i) d = fma((double)s_g[r][i], (double)s_u[i + nb - 1 - k], d);
+#pragma unroll
+      for (int wv = 0; wv < kFirW / 64; ++wv) d += (double)s_red[wv][r][k];
       pw[(o0 + r) * nb + k] = d;
     }
   }
-  if (t < L) gu[(f.b * L + t) * I + f.j] = acc;
+#pragma unroll
+  for (int i = 0; i < kFirS; ++i)
+    if (t + i < L) gu[(f.b * L + t + i) * I + f.j] = gacc[i];
   if (tail) gu_tail[(f.b * (nb - 1) + tid) * I + f.j] = acc_tail;
 }
 
@@ -920,6 +1036,8 @@ int fir_args_status(int64_t B, int64_t L, int64_t I, int64_t O, int64_t nb) {
   if (tiles > INT32_MAX || I * O > INT32_MAX / 2) return TSF_ERR_UNSUPPORTED;
   return TSF_OK;
 }
+
+#define TSF_FIR_NBT(X) X(4) X(8) X(16) X(32) X(64)
 
 #define TSF_GB_CASES(X) \
   X(1, 2) X(1, 4) X(1, 8) X(1, 16) X(2, 2) X(2, 4) X(2, 8) X(2, 16) X(3, 2) X(3, 4) X(3, 8) X(3, 16) X(4, 2) X(4, 4) X(4, 8) X(4, 16)
@@ -1006,8 +1124,17 @@ int tsfast_hip_gblock_fir_fwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_
   if (B == 0 || L == 0) return TSF_OK;
   if (!u || !b || !w) return TSF_ERR_ARG;
   const int64_t tiles_t = (L + kFirT - 1) / kFirT;
-  hipLaunchKernelGGL(gb_fir_fwd, dim3((unsigned)(B * I * tiles_t)), dim3(kFirT), 0, static_cast<hipStream_t>(stream),
-                     u, b, u_tail, w, L, (int)I, (int)O, (int)nb, tiles_t);
+  const dim3 grid((unsigned)(B * I * tiles_t));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (fir_nbt(nb)) {
+#define X(NBT_)                                                                                                    \
+  case NBT_:                                                                                                       \
+    hipLaunchKernelGGL((gb_fir_fwd<NBT_>), grid, dim3(kFirW), 0, s, u, b, u_tail, w, L, (int)I, (int)O, (int)nb, \
+                       (unsigned)tiles_t);                                                                         \
+    break;
+    TSF_FIR_NBT(X)
+#undef X
+  }
   return tsf_launch_status();
 }
 
@@ -1027,8 +1154,16 @@ int tsfast_hip_gblock_fir_bwd(int64_t B, int64_t L, int64_t I, int64_t O, int64_
   }
   if (!workspace || workspace_bytes < tsfast_hip_gblock_fir_workspace_bytes(B, L, I, O, nb)) return TSF_ERR_WORKSPACE;
   double* part = static_cast<double*>(workspace);
-  hipLaunchKernelGGL(gb_fir_bwd, dim3((unsigned)(B * I * tiles_t)), dim3(kFirT), 0, s, gw, u, b, u_tail, gu, gu_tail,
-                     part, L, (int)I, (int)O, (int)nb, tiles_t);
+  const dim3 grid((unsigned)(B * I * tiles_t));
+  switch (fir_nbt(nb)) {
+#define X(NBT_)                                                                                                 \
+  case NBT_:                                                                                                    \
+    hipLaunchKernelGGL((gb_fir_bwd<NBT_>), grid, dim3(kFirW), 0, s, gw, u, b, u_tail, gu, gu_tail, part, L,     \
+                       (int)I, (int)O, (int)nb, (unsigned)tiles_t);                                             \
+    break;
+    TSF_FIR_NBT(X)
+#undef X
+  }
   hipLaunchKernelGGL(gb_fir_reduce, dim3((unsigned)(O * I * nb)), dim3(256), 0, s, (const double*)part, gb, rows,
                      (int)I, (int)O, (int)nb);
   return tsf_launch_status();

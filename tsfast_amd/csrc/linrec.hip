@@ -1036,22 +1036,6 @@ constexpr int kSpread = 16;     // threads per group = the padded state size
 constexpr int kMaxSpreadNS = 16;
 constexpr int kSpreadPf = 8;    // steps fetched ahead by the chunk kernels
 
-template <int K>
-TSF_DEV uint32_t row_lane_u32(uint32_t x) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x150 + K, 0xF, 0xF, true);
-}
-// the value x holds in lane K (0..15) of this thread's 16-lane row
-template <int K>
-TSF_DEV double row_lane(double x) {
-  const uint64_t b = (uint64_t)__double_as_longlong(x);
-  const uint64_t lo = row_lane_u32<K>((uint32_t)b), hi = row_lane_u32<K>((uint32_t)(b >> 32));
-  return __longlong_as_double((long long)((hi << 32) | lo));
-}
-template <int K>
-TSF_DEV float row_lane(float x) {
-  return __uint_as_float(row_lane_u32<K>(__float_as_uint(x)));
-}
-
 // acc + sum_c p[c] * (s of lane c), c = 0 .. 15 in order
 template <int C = 0>
 TSF_DEV double spread_dot(const double (&p)[kSpread], double s, double acc) {
