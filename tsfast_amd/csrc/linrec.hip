@@ -544,8 +544,8 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const flo
 #define TSF_NS_CASES(X) X(1) X(2) X(3) X(4)
 
 // ------------------------------------------------------------------------------ n = 5..8
-// Two-pass path for state sizes above the single-pass kernels' look-back areas. One thread per
-// lane and chunk of kWideT steps, no waiting between workgroups:
+// Two-pass path for state sizes above the single-pass kernels' look-back areas. Two threads per
+// lane and chunk of kWideT steps (each owning half the state rows), no waiting between workgroups:
 //   forward:  chunk ends from a zero state (e) -> per lane, the entering state of every chunk by a
 //             sequential carry over the chunks with M = A^kWideT -> every chunk re-run from its
 //             entering state, writing x;
@@ -557,30 +557,6 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const flo
 constexpr int kWideT = 256;
 constexpr int kWidePf = 4;  // steps fetched ahead by the chunk kernels
 constexpr int kWideThreads = 256;
-
-template <int NS>
-TSF_DEV void load_matrix_f32(float (&m)[NS][NS], const float* __restrict__ A, int64_t lane) {
-  const float* a = A + lane * NS * NS;
-#pragma unroll
-  for (int r = 0; r < NS; ++r)
-#pragma unroll
-    for (int c = 0; c < NS; ++c) m[r][c] = a[r * NS + c];
-}
-
-// s <- m s + x (TR: m^T s + x), m fp32, s fp64
-template <int NS, bool TR>
-TSF_DEV void wide_step(const float (&m)[NS][NS], double (&s)[NS], const float* __restrict__ x) {
-  double t[NS];
-#pragma unroll
-  for (int r = 0; r < NS; ++r) {
-    double acc = (double)x[r];
-#pragma unroll
-    for (int c = 0; c < NS; ++c) acc = fma((double)(TR ? m[c][r] : m[r][c]), s[c], acc);
-    t[r] = acc;
-  }
-#pragma unroll
-  for (int r = 0; r < NS; ++r) s[r] = t[r];
-}
 
 // One step's NS floats of a lane's row, VEC floats per access (VEC divides NS; the host picks
 // VEC = 4 or 2 only when every row pointer is aligned to it).
@@ -601,20 +577,6 @@ TSF_DEV void ld_step(float (&d)[NS], const float* __restrict__ p) {
   } else {
 #pragma unroll
     for (int i = 0; i < NS; ++i) d[i] = p[i];
-  }
-}
-template <int NS, int VEC>
-TSF_DEV void st_step(float* __restrict__ p, const double (&s)[NS]) {
-  if constexpr (VEC == 4) {
-#pragma unroll
-    for (int i = 0; i < NS; i += 4)
-      *reinterpret_cast<float4*>(p + i) = make_float4((float)s[i], (float)s[i + 1], (float)s[i + 2], (float)s[i + 3]);
-  } else if constexpr (VEC == 2) {
-#pragma unroll
-    for (int i = 0; i < NS; i += 2) *reinterpret_cast<float2*>(p + i) = make_float2((float)s[i], (float)s[i + 1]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < NS; ++i) p[i] = (float)s[i];
   }
 }
 
@@ -652,36 +614,223 @@ __global__ void __launch_bounds__(64) lw_power(const float* __restrict__ A, doub
   for (int r = 0; r < NS; ++r) M[lane * NS * NS + r * NS + col] = x[r];
 }
 
+// The chunk kernels run two threads per lane (adjacent threads): thread h = threadIdx.x & 1 owns
+// state rows h * NH .. h * NH + NH - 1 (NH = ceil(n / 2); rows past n are zero padding), the
+// same rows of the step matrix P (A forward, A^T adjoint) split into the owned and the partner's
+// columns, and, in the adjoint re-run, the same rows of grad_A. A step reads the partner's
+// components by a DPP lane swap and sums the owned components' terms first. One thread per lane
+// held 228 VGPRs (the adjoint re-run 360, with the n x n fp64 grad_A accumulators): one or two
+// waves per SIMD, latency-bound.
+constexpr int half_rows(int ns) { return (ns + 1) / 2; }
+constexpr int kWideLanes = kWideThreads / 2;  // lanes per workgroup
+
+template <int NS, bool TR>
+TSF_DEV void half_matrix(float (&mo)[half_rows(NS)][half_rows(NS)], float (&mp)[half_rows(NS)][half_rows(NS)],
+                         const float* __restrict__ a, int own0, int par0) {
+  constexpr int NH = half_rows(NS);
+#pragma unroll
+  for (int i = 0; i < NH; ++i)
+#pragma unroll
+    for (int j = 0; j < NH; ++j) {
+      const int oi = own0 + i, oj = own0 + j, pi = par0 + i;
+      // P[r][c] = TR ? A[c][r] : A[r][c]; mo[i][j] = P[oj][oi], mp[i][j] = P[oj][pi]
+      mo[i][j] = (oi < NS && oj < NS) ? (TR ? a[oi * NS + oj] : a[oj * NS + oi]) : 0.0f;
+      mp[i][j] = (pi < NS && oj < NS) ? (TR ? a[pi * NS + oj] : a[oj * NS + pi]) : 0.0f;
+    }
+}
+// the partner's (lane ^ 1) values of s
+template <int NH>
+TSF_DEV void half_swap(double (&sp)[NH], const double (&s)[NH]) {
+#pragma unroll
+  for (int i = 0; i < NH; ++i) {
+    const uint64_t b = (uint64_t)__double_as_longlong(s[i]);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, 0xB1, 0xF, 0xF, false);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), 0xB1, 0xF, 0xF, false);
+    sp[i] = __longlong_as_double((long long)((hi << 32) | lo));
+  }
+}
+// owned rows of s <- P s + x; called by both threads of every pair together
+template <int NH>
+TSF_DEV void half_step(const float (&mo)[NH][NH], const float (&mp)[NH][NH], double (&s)[NH], const float (&x)[NH]) {
+  double sp[NH], t[NH];
+  half_swap<NH>(sp, s);
+#pragma unroll
+  for (int j = 0; j < NH; ++j) {
+    double acc = (double)x[j];
+#pragma unroll
+    for (int i = 0; i < NH; ++i) acc = fma((double)mo[i][j], s[i], acc);
+#pragma unroll
+    for (int i = 0; i < NH; ++i) acc = fma((double)mp[i][j], sp[i], acc);
+    t[j] = acc;
+  }
+#pragma unroll
+  for (int j = 0; j < NH; ++j) s[j] = t[j];
+}
+// access width of a thread's half of a step (its rows start own0 floats into the step)
+template <int NS, int VEC>
+constexpr int half_vec() {
+  return (VEC == 4 && half_rows(NS) % 4 == 0) ? 4 : (VEC >= 2 && half_rows(NS) % 2 == 0) ? 2 : 1;
+}
+// the owned rows of one step: p points at the step's row own0 (padding rows read as zero)
+template <int NS, int VH>
+TSF_DEV void ld_half(float (&d)[half_rows(NS)], const float* __restrict__ p, int own0) {
+  constexpr int NH = half_rows(NS);
+  if constexpr (VH > 1) {
+    ld_step<NH, VH>(d, p);  // NS even: no padding rows
+  } else {
+#pragma unroll
+    for (int i = 0; i < NH; ++i) d[i] = (own0 + i < NS) ? p[i] : 0.0f;
+  }
+}
+struct HalfIdx {
+  int h, ll, own0, par0;
+  int64_t lane, c, t0, t1;
+  bool live;
+};
+TSF_DEV HalfIdx half_idx(int64_t lanes, int64_t L, int NH) {
+  HalfIdx q;
+  q.h = threadIdx.x & 1;
+  q.ll = threadIdx.x >> 1;
+  q.own0 = q.h * NH;
+  q.par0 = (1 - q.h) * NH;
+  q.lane = blockIdx.x * (int64_t)kWideLanes + q.ll;
+  q.live = q.lane < lanes;
+  q.c = blockIdx.y;
+  q.t0 = q.c * kWideT;
+  q.t1 = (q.t0 + kWideT < L) ? q.t0 + kWideT : L;
+  return q;
+}
+
 // Forward chunk ends from a zero state: e [nchunks][lanes][NS]
 template <int NS, int VEC>
 __global__ void __launch_bounds__(kWideThreads) lw_sum_fwd(const float* __restrict__ A, const float* __restrict__ v,
                                                            double* __restrict__ e, int64_t lanes, int64_t L) {
-  const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
-  if (lane >= lanes) return;
-  const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
-  float m[NS][NS];
-  load_matrix_f32<NS>(m, A, lane);
-  double s[NS];
+  constexpr int NH = half_rows(NS), VH = half_vec<NS, VEC>();
+  const HalfIdx q = half_idx(lanes, L, NH);
+  if (!q.live) return;  // both threads of a pair
+  float mo[NH][NH], mp[NH][NH];
+  half_matrix<NS, false>(mo, mp, A + q.lane * NS * NS, q.own0, q.par0);
+  double s[NH];
 #pragma unroll
-  for (int r = 0; r < NS; ++r) s[r] = 0.0;
-  const float* row = v + lane * L * NS;
+  for (int i = 0; i < NH; ++i) s[i] = 0.0;
+  const float* row = v + q.lane * L * NS + q.own0;
   // kWidePf steps' loads in flight: step t + kWidePf is fetched while step t computes
-  float d[kWidePf][NS];
+  float d[kWidePf][NH];
 #pragma unroll
   for (int k = 0; k < kWidePf; ++k)
-    if (t0 + k < t1) ld_step<NS, VEC>(d[k], row + (t0 + k) * NS);
-  for (int64_t tb = t0; tb < t1; tb += kWidePf) {
+    if (q.t0 + k < q.t1) ld_half<NS, VH>(d[k], row + (q.t0 + k) * NS, q.own0);
+  for (int64_t tb = q.t0; tb < q.t1; tb += kWidePf) {
 #pragma unroll
     for (int k = 0; k < kWidePf; ++k) {
       const int64_t t = tb + k;
-      if (t < t1) {
-        wide_step<NS, false>(m, s, d[k]);
-        if (t + kWidePf < t1) ld_step<NS, VEC>(d[k], row + (t + kWidePf) * NS);
+      if (t < q.t1) {  // uniform over the workgroup (one chunk)
+        half_step<NH>(mo, mp, s, d[k]);
+        if (t + kWidePf < q.t1) ld_half<NS, VH>(d[k], row + (t + kWidePf) * NS, q.own0);
       }
     }
   }
 #pragma unroll
-  for (int r = 0; r < NS; ++r) e[(c * lanes + lane) * NS + r] = s[r];
+  for (int i = 0; i < NH; ++i)
+    if (q.own0 + i < NS) e[(q.c * lanes + q.lane) * NS + q.own0 + i] = s[i];
+}
+
+// Steps per output sub-block of the re-run kernels: a multiple of kWidePf whose NS-float steps fill
+// at most 64 floats, so one lane's sub-block is one contiguous row segment of <= 256 bytes.
+template <int NS>
+constexpr int wide_out_sb() {
+  return kWidePf * (64 / (kWidePf * NS));
+}
+
+// A re-run's outputs of sub-block tb (cnt steps) leave through LDS: each thread left its rows of
+// every step in its lane's LDS row, and each wave now writes its 32 lanes' row segments with
+// whole-segment (coalesced) stores, one lane at a time, so HBM sees full lines.
+template <int NS, int SB>
+TSF_DEV void half_write_segments(float* __restrict__ dst, const float (*s_o)[SB * NS + 1], int64_t lanes, int64_t L,
+                                 int64_t tb, int cnt) {
+  const int wl = threadIdx.x & 63, wlane0 = (threadIdx.x & ~63) >> 1;
+  const int64_t l0 = blockIdx.x * (int64_t)kWideLanes;
+  const int wseg = cnt * NS;
+#pragma unroll 8
+  for (int l = 0; l < 32; ++l) {
+    const int64_t ln = l0 + wlane0 + l;
+    if (ln < lanes && wl < wseg) dst[(ln * L + tb) * NS + wl] = s_o[wlane0 + l][wl];
+  }
+}
+
+// Every chunk re-run from its entering state, writing x.
+template <int NS, int VEC>
+__global__ void __launch_bounds__(kWideThreads) lw_apply_fwd(const float* __restrict__ A, const float* __restrict__ v,
+                                                             const double* __restrict__ carry, float* __restrict__ x,
+                                                             int64_t lanes, int64_t L) {
+  constexpr int NH = half_rows(NS), VH = half_vec<NS, VEC>();
+  constexpr int SB = wide_out_sb<NS>();
+  __shared__ float s_o[kWideLanes][SB * NS + 1];
+  const HalfIdx q = half_idx(lanes, L, NH);
+  float mo[NH][NH], mp[NH][NH];
+  double s[NH];
+  float d[kWidePf][NH];
+  const float* row = v + (q.live ? q.lane : 0) * L * NS + q.own0;
+  if (q.live) {
+    half_matrix<NS, false>(mo, mp, A + q.lane * NS * NS, q.own0, q.par0);
+#pragma unroll
+    for (int i = 0; i < NH; ++i) s[i] = (q.own0 + i < NS) ? carry[(q.c * lanes + q.lane) * NS + q.own0 + i] : 0.0;
+#pragma unroll
+    for (int k = 0; k < kWidePf; ++k)
+      if (q.t0 + k < q.t1) ld_half<NS, VH>(d[k], row + (q.t0 + k) * NS, q.own0);
+  }
+  for (int64_t tb = q.t0; tb < q.t1; tb += SB) {
+    const int cnt = (int)((q.t1 - tb) < SB ? (q.t1 - tb) : SB);
+    if (q.live) {
+      for (int kk = 0; kk < SB; kk += kWidePf) {
+#pragma unroll
+        for (int k = 0; k < kWidePf; ++k) {
+          const int64_t t = tb + kk + k;
+          if (t < q.t1) {
+            half_step<NH>(mo, mp, s, d[k]);
+#pragma unroll
+            for (int i = 0; i < NH; ++i)
+              if (q.own0 + i < NS) s_o[q.ll][(kk + k) * NS + q.own0 + i] = (float)s[i];
+            if (t + kWidePf < q.t1) ld_half<NS, VH>(d[k], row + (t + kWidePf) * NS, q.own0);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    half_write_segments<NS, SB>(x, s_o, lanes, L, tb, cnt);
+    __syncthreads();
+  }
+}
+
+// Adjoint chunk starts from a zero right-end state: f [nchunks][lanes][NS]
+template <int NS, int VEC>
+__global__ void __launch_bounds__(kWideThreads) lw_sum_bwd(const float* __restrict__ A, const float* __restrict__ g,
+                                                           double* __restrict__ f, int64_t lanes, int64_t L) {
+  constexpr int NH = half_rows(NS), VH = half_vec<NS, VEC>();
+  const HalfIdx q = half_idx(lanes, L, NH);
+  if (!q.live) return;  // both threads of a pair
+  float mo[NH][NH], mp[NH][NH];
+  half_matrix<NS, true>(mo, mp, A + q.lane * NS * NS, q.own0, q.par0);
+  double G[NH];
+#pragma unroll
+  for (int i = 0; i < NH; ++i) G[i] = 0.0;
+  const float* row = g + q.lane * L * NS + q.own0;
+  float d[kWidePf][NH];
+#pragma unroll
+  for (int k = 0; k < kWidePf; ++k)
+    if (q.t1 - 1 - k >= q.t0) ld_half<NS, VH>(d[k], row + (q.t1 - 1 - k) * NS, q.own0);
+  for (int64_t tb = q.t1 - 1; tb >= q.t0; tb -= kWidePf) {
+#pragma unroll
+    for (int k = 0; k < kWidePf; ++k) {
+      const int64_t t = tb - k;
+      if (t >= q.t0) {
+        half_step<NH>(mo, mp, G, d[k]);
+        if (t - kWidePf >= q.t0) ld_half<NS, VH>(d[k], row + (t - kWidePf) * NS, q.own0);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NH; ++i)
+    if (q.own0 + i < NS) f[(q.c * lanes + q.lane) * NS + q.own0 + i] = G[i];
 }
 
 // Entering state of every chunk: carry[c] = M carry[c-1] + e[c-1], carry[0] = x0 (or 0)
@@ -708,95 +857,6 @@ __global__ void __launch_bounds__(64) lw_carry_fwd(const double* __restrict__ M,
   }
 }
 
-// Steps per output sub-block of the re-run kernels: a multiple of kWidePf whose NS-float steps fill
-// at most 64 floats, so one lane's sub-block is one contiguous row segment of <= 256 bytes.
-template <int NS>
-constexpr int wide_out_sb() {
-  return kWidePf * (64 / (kWidePf * NS));
-}
-
-// Every chunk re-run from its entering state, writing x. Each thread leaves its outputs in its
-// LDS row; every wave then writes its 64 lanes' row segments with whole-segment (coalesced)
-// stores, one lane at a time, so HBM sees full lines instead of one step per lane per store.
-template <int NS, int VEC>
-__global__ void __launch_bounds__(kWideThreads) lw_apply_fwd(const float* __restrict__ A, const float* __restrict__ v,
-                                                             const double* __restrict__ carry, float* __restrict__ x,
-                                                             int64_t lanes, int64_t L) {
-  constexpr int SB = wide_out_sb<NS>();
-  __shared__ float s_o[kWideThreads][SB * NS + 1];
-  const int tid = threadIdx.x, wl = tid & 63, w0 = tid & ~63;
-  const int64_t l0 = blockIdx.x * (int64_t)kWideThreads, lane = l0 + tid;
-  const bool live = lane < lanes;
-  const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
-  float m[NS][NS];
-  double s[NS];
-  float d[kWidePf][NS];
-  const float* row = v + (live ? lane : 0) * L * NS;
-  if (live) {
-    load_matrix_f32<NS>(m, A, lane);
-#pragma unroll
-    for (int r = 0; r < NS; ++r) s[r] = carry[(c * lanes + lane) * NS + r];
-#pragma unroll
-    for (int k = 0; k < kWidePf; ++k)
-      if (t0 + k < t1) ld_step<NS, VEC>(d[k], row + (t0 + k) * NS);
-  }
-  for (int64_t tb = t0; tb < t1; tb += SB) {
-    const int cnt = (int)((t1 - tb) < SB ? (t1 - tb) : SB);
-    if (live) {
-      for (int kk = 0; kk < SB; kk += kWidePf) {
-#pragma unroll
-        for (int k = 0; k < kWidePf; ++k) {
-          const int64_t t = tb + kk + k;
-          if (t < t1) {
-            wide_step<NS, false>(m, s, d[k]);
-#pragma unroll
-            for (int r = 0; r < NS; ++r) s_o[tid][(kk + k) * NS + r] = (float)s[r];
-            if (t + kWidePf < t1) ld_step<NS, VEC>(d[k], row + (t + kWidePf) * NS);
-          }
-        }
-      }
-    }
-    __syncthreads();
-    const int wseg = cnt * NS;
-#pragma unroll 8
-    for (int l = 0; l < 64; ++l) {
-      const int64_t ln = l0 + w0 + l;
-      if (ln < lanes && wl < wseg) x[(ln * L + tb) * NS + wl] = s_o[w0 + l][wl];
-    }
-    __syncthreads();
-  }
-}
-
-// Adjoint chunk starts from a zero right-end state: f [nchunks][lanes][NS]
-template <int NS, int VEC>
-__global__ void __launch_bounds__(kWideThreads) lw_sum_bwd(const float* __restrict__ A, const float* __restrict__ g,
-                                                           double* __restrict__ f, int64_t lanes, int64_t L) {
-  const int64_t lane = blockIdx.x * (int64_t)kWideThreads + threadIdx.x;
-  if (lane >= lanes) return;
-  const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
-  float m[NS][NS];
-  load_matrix_f32<NS>(m, A, lane);
-  double G[NS];
-#pragma unroll
-  for (int r = 0; r < NS; ++r) G[r] = 0.0;
-  const float* row = g + lane * L * NS;
-  float d[kWidePf][NS];
-#pragma unroll
-  for (int k = 0; k < kWidePf; ++k)
-    if (t1 - 1 - k >= t0) ld_step<NS, VEC>(d[k], row + (t1 - 1 - k) * NS);
-  for (int64_t tb = t1 - 1; tb >= t0; tb -= kWidePf) {
-#pragma unroll
-    for (int k = 0; k < kWidePf; ++k) {
-      const int64_t t = tb - k;
-      if (t >= t0) {
-        wide_step<NS, true>(m, G, d[k]);
-        if (t - kWidePf >= t0) ld_step<NS, VEC>(d[k], row + (t - kWidePf) * NS);
-      }
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < NS; ++r) f[(c * lanes + lane) * NS + r] = G[r];
-}
 
 // Adjoint entering every chunk from the right: rc[c] = G at the first step of chunk c + 1 (zero
 // for the last chunk), rc[c-1] = f[c] + M rc[c]; then grad_x0 = A^T G_0 with G_0 = f[0] + M rc[0].
@@ -832,93 +892,98 @@ __global__ void __launch_bounds__(64) lw_carry_bwd(const float* __restrict__ A, 
 }
 
 // Every chunk re-run backwards from its right-end adjoint, writing grad_v and the chunk's grad_A
-// partial sum_t G_t x_{t-1}^T (x_{-1} = x0 or 0) into part [nchunks][lanes][NS * NS]. grad_v goes
-// out through LDS as whole row segments, like x in the forward re-run.
+// partial sum_t G_t x_{t-1}^T (x_{-1} = x0 or 0) into part [nchunks][lanes][NS * NS]: each thread
+// its rows of grad_A, with the columns of its own half of x_{t-1} first and the partner's half
+// (by DPP lane swap) second, so each thread loads half a row of x per step.
 template <int NS, int VEC>
 __global__ void __launch_bounds__(kWideThreads) lw_apply_bwd(const float* __restrict__ A, const float* __restrict__ g,
                                                              const float* __restrict__ out, const float* __restrict__ x0,
                                                              const double* __restrict__ rc, float* __restrict__ gv,
                                                              double* __restrict__ part, int64_t lanes, int64_t L) {
+  constexpr int NH = half_rows(NS), VH = half_vec<NS, VEC>();
   constexpr int SB = wide_out_sb<NS>();
-  constexpr int kPfB = 2;  // steps fetched ahead; SB is a multiple of it
+  constexpr int kPfB = 2;  // steps fetched ahead; SB is a multiple of it (4 and 8 measured no faster)
   static_assert(SB % kPfB == 0, "sub-blocks hold whole prefetch pairs");
-  __shared__ float s_o[kWideThreads][SB * NS + 1];
-  const int tid = threadIdx.x, wl = tid & 63, w0 = tid & ~63;
-  const int64_t l0 = blockIdx.x * (int64_t)kWideThreads, lane = l0 + tid;
-  const bool live = lane < lanes;
-  const int64_t c = blockIdx.y, t0 = c * kWideT, t1 = (t0 + kWideT < L) ? t0 + kWideT : L;
-  float m[NS][NS];
-  double G[NS], acc[NS][NS];
+  __shared__ float s_o[kWideLanes][SB * NS + 1];
+  const HalfIdx q = half_idx(lanes, L, NH);
+  float mo[NH][NH], mp[NH][NH];
+  double G[NH], acc[NH][2 * NH];  // acc[i][j]: column own0 + j (j < NH), par0 + j - NH (j >= NH)
 #pragma unroll
-  for (int r = 0; r < NS; ++r) {
-    G[r] = live ? rc[(c * lanes + lane) * NS + r] : 0.0;
+  for (int i = 0; i < NH; ++i) {
+    G[i] = (q.live && q.own0 + i < NS) ? rc[(q.c * lanes + q.lane) * NS + q.own0 + i] : 0.0;
 #pragma unroll
-    for (int q = 0; q < NS; ++q) acc[r][q] = 0.0;
+    for (int j = 0; j < 2 * NH; ++j) acc[i][j] = 0.0;
   }
-  const int64_t lrow = (live ? lane : 0) * L * NS;
+  const int64_t lrow = (q.live ? q.lane : 0) * L * NS + q.own0;
   const float* grow = g + lrow;
   const float* xrow = out + lrow;
-  // slot k of the ring holds g_t and x_{t-1} of a step t with (t - t0) % kPfB == k
-  float dg[kPfB][NS], dx[kPfB][NS];
+  // slot k of the ring holds the owned rows of g_t and of x_{t-1} of a step t with (t - t0) % kPfB == k
+  float dg[kPfB][NH], dx[kPfB][NH];
   auto fetch = [&](int k, int64_t t) __attribute__((always_inline)) {
-    ld_step<NS, VEC>(dg[k], grow + t * NS);
+    ld_half<NS, VH>(dg[k], grow + t * NS, q.own0);
     if (t > 0) {
-      ld_step<NS, VEC>(dx[k], xrow + (t - 1) * NS);
+      ld_half<NS, VH>(dx[k], xrow + (t - 1) * NS, q.own0);
     } else {
 #pragma unroll
-      for (int q = 0; q < NS; ++q) dx[k][q] = x0 ? x0[lane * NS + q] : 0.0f;
+      for (int i = 0; i < NH; ++i) dx[k][i] = (x0 && q.own0 + i < NS) ? x0[q.lane * NS + q.own0 + i] : 0.0f;
     }
   };
-  if (live) {
-    load_matrix_f32<NS>(m, A, lane);
-    if (((t1 - 1 - t0) & 1) == 0) {
-      fetch(0, t1 - 1);
-      if (t1 - 2 >= t0) fetch(1, t1 - 2);
-    } else {
-      fetch(1, t1 - 1);
-      if (t1 - 2 >= t0) fetch(0, t1 - 2);
+  const int64_t t0 = q.t0, t1 = q.t1;
+  if (q.live) {
+    half_matrix<NS, true>(mo, mp, A + q.lane * NS * NS, q.own0, q.par0);
+#pragma unroll
+    for (int i = 0; i < kPfB; ++i) {
+      const int64_t t = t1 - 1 - i;
+      if (t >= t0) fetch((int)((t - t0) % kPfB), t);
     }
   }
   const int64_t nsb = (t1 - t0 + SB - 1) / SB;
   for (int64_t j = nsb - 1; j >= 0; --j) {
     const int64_t tb = t0 + j * SB;
     const int cnt = (int)((t1 - tb) < SB ? (t1 - tb) : SB);
-    if (live) {
+    if (q.live) {
       for (int kk = SB - kPfB; kk >= 0; kk -= kPfB) {
 #pragma unroll
         for (int k = kPfB - 1; k >= 0; --k) {
           const int64_t t = tb + kk + k;
-          if (t < t1) {
-            wide_step<NS, true>(m, G, dg[k]);
-            float xp[NS];
+          if (t < t1) {  // uniform over the workgroup (one chunk)
+            half_step<NH>(mo, mp, G, dg[k]);
+            float xo[NH], xq[NH];  // x_{t-1}: owned rows, the partner's rows
 #pragma unroll
-            for (int r = 0; r < NS; ++r) {
-              s_o[tid][(kk + k) * NS + r] = (float)G[r];
-              xp[r] = dx[k][r];
+            for (int i = 0; i < NH; ++i) {
+              xo[i] = dx[k][i];
+              xq[i] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(xo[i]), 0xB1, 0xF, 0xF, false));
             }
+#pragma unroll
+            for (int i = 0; i < NH; ++i)
+              if (q.own0 + i < NS) s_o[q.ll][(kk + k) * NS + q.own0 + i] = (float)G[i];
             if (t - kPfB >= t0) fetch(k, t - kPfB);
 #pragma unroll
-            for (int r = 0; r < NS; ++r)
+            for (int i = 0; i < NH; ++i) {
 #pragma unroll
-              for (int q = 0; q < NS; ++q) acc[r][q] = fma(G[r], (double)xp[q], acc[r][q]);
+              for (int jj = 0; jj < NH; ++jj) acc[i][jj] = fma(G[i], (double)xo[jj], acc[i][jj]);
+#pragma unroll
+              for (int jj = 0; jj < NH; ++jj) acc[i][NH + jj] = fma(G[i], (double)xq[jj], acc[i][NH + jj]);
+            }
           }
         }
       }
     }
     __syncthreads();
-    const int wseg = cnt * NS;
-#pragma unroll 8
-    for (int l = 0; l < 64; ++l) {
-      const int64_t ln = l0 + w0 + l;
-      if (ln < lanes && wl < wseg) gv[(ln * L + tb) * NS + wl] = s_o[w0 + l][wl];
-    }
+    half_write_segments<NS, SB>(gv, s_o, lanes, L, tb, cnt);
     __syncthreads();
   }
-  if (live) {
+  if (q.live) {
+    double* prow = part + (q.c * lanes + q.lane) * NS * NS;
 #pragma unroll
-    for (int r = 0; r < NS; ++r)
+    for (int i = 0; i < NH; ++i)
+      if (q.own0 + i < NS) {
 #pragma unroll
-      for (int q = 0; q < NS; ++q) part[(c * lanes + lane) * NS * NS + r * NS + q] = acc[r][q];
+        for (int jj = 0; jj < NH; ++jj) {
+          if (q.own0 + jj < NS) prow[(q.own0 + i) * NS + q.own0 + jj] = acc[i][jj];
+          if (q.par0 + jj < NS) prow[(q.own0 + i) * NS + q.par0 + jj] = acc[i][NH + jj];
+        }
+      }
   }
 }
 
@@ -942,7 +1007,8 @@ LwPlan lw_plan(int64_t lanes, int64_t L, int64_t ns) {
 }
 
 inline bool lw_grid_fits(int64_t lanes, int64_t L) {
-  return (L + kWideT - 1) / kWideT <= 65535 && (lanes + kWideThreads - 1) / kWideThreads <= INT32_MAX;
+  // one grid row per chunk; two threads per lane, at most 2^32 - 1 threads per grid row
+  return (L + kWideT - 1) / kWideT <= 65535 && (lanes + kWideLanes - 1) / kWideLanes <= UINT32_MAX / kWideThreads;
 }
 
 template <int NS, int VEC>
@@ -952,7 +1018,7 @@ int wide_fwd_impl(int64_t lanes, int64_t L, const float* A, const float* v, cons
   double* e = reinterpret_cast<double*>(ws + p.off_e);
   double* carry = reinterpret_cast<double*>(ws + p.off_carry);
   double* M = reinterpret_cast<double*>(ws + p.off_M);
-  const dim3 grid((unsigned)((lanes + kWideThreads - 1) / kWideThreads), (unsigned)p.nchunks);
+  const dim3 grid((unsigned)((lanes + kWideLanes - 1) / kWideLanes), (unsigned)p.nchunks);
   const unsigned lb = (unsigned)((lanes + 63) / 64);
   hipLaunchKernelGGL((lw_power<NS>), dim3((unsigned)((lanes * NS + 63) / 64)), dim3(64), 0, s, A, M, lanes, kWideT, 0);
   hipLaunchKernelGGL((lw_sum_fwd<NS, VEC>), grid, dim3(kWideThreads), 0, s, A, v, e, lanes, L);
@@ -975,7 +1041,7 @@ int wide_bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, cons
   double* rc = reinterpret_cast<double*>(ws + p.off_carry);
   double* M = reinterpret_cast<double*>(ws + p.off_M);
   double* part = reinterpret_cast<double*>(ws + p.off_part);
-  const dim3 grid((unsigned)((lanes + kWideThreads - 1) / kWideThreads), (unsigned)p.nchunks);
+  const dim3 grid((unsigned)((lanes + kWideLanes - 1) / kWideLanes), (unsigned)p.nchunks);
   const unsigned lb = (unsigned)((lanes + 63) / 64);
   hipLaunchKernelGGL((lw_power<NS>), dim3((unsigned)((lanes * NS + 63) / 64)), dim3(64), 0, s, A, M, lanes, kWideT, 1);
   hipLaunchKernelGGL((lw_sum_bwd<NS, VEC>), grid, dim3(kWideThreads), 0, s, A, g, f, lanes, L);
