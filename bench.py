@@ -196,11 +196,14 @@ def allpole_inputs(device, P=64, B=64, L=16384, na=3):
 
 # --------------------------------------------------------------------------- timing
 def time_steps(step, steps, warmup):
-    """W untimed steps, then K timed steps between device synchronisations; step(ev) records
-    events at phase boundaries. Returns (ms per step, [mean ms per phase]). Python's cyclic
-    collector is run before and held off during the steps (as timeit does): a full collection
-    stalls the host for tens of milliseconds, starving the GPU of launches, and where it falls
-    depends on allocation counts that differ between a first and a later process."""
+    """W untimed steps, then K timed steps between device synchronisations, with nothing else in
+    them; then K more steps in which step(ev) records events at the phase boundaries, for the
+    per-phase times (an event record costs microseconds of host and device time, a measurable
+    share of the smallest configs' steps, so it stays out of the timed steps). Returns (ms per
+    timed step, [mean ms per phase]). Python's cyclic collector is run before and held off during
+    the steps (as timeit does): a full collection stalls the host for tens of milliseconds,
+    starving the GPU of launches, and where it falls depends on allocation counts that differ
+    between a first and a later process."""
     import torch
 
     gc.collect()
@@ -209,14 +212,17 @@ def time_steps(step, steps, warmup):
         for _ in range(warmup):
             step(None)
         torch.cuda.synchronize()
-        events = []
         t0 = time.perf_counter()
+        for _ in range(steps):
+            step(None)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        events = []
         for _ in range(steps):
             ev = []
             step(ev)
             events.append(ev)
         torch.cuda.synchronize()
-        t1 = time.perf_counter()
     finally:
         gc.enable()
     phases = []

@@ -127,12 +127,18 @@ def lookback_gave_up(ws: torch.Tensor) -> bool:
     return bool(ws[LOOKBACK_ERR_OFFSET : LOOKBACK_ERR_OFFSET + 4].view(torch.int32).item())
 
 
+_gpu_seen = False
+
+
 def _alarm(clear: bool) -> int:
     """1 if the library's look-back alarm word names a scan call that gave up and has not been
     reported, else 0 (-1 if the word is unavailable; 0 without a GPU, where no scan can have
     run); ``clear`` marks that call reported."""
-    if not torch.cuda.is_available():
-        return 0
+    global _gpu_seen
+    if not _gpu_seen:  # a GPU, once found, stays (the query costs more than the word's read)
+        if not torch.cuda.is_available():
+            return 0
+        _gpu_seen = True
     return load().tsfast_hip_lookback_gave_up(1 if clear else 0)
 
 
@@ -180,8 +186,9 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    """The current HIP stream of the tensor's device, as an integer handle."""
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """The current HIP stream of the tensor's device, as an integer handle (torch's raw-stream
+    query: a fraction of the cost of building a ``torch.cuda.Stream`` object on every call)."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 def require(t: torch.Tensor | None, name: str, dtypes: tuple, device: torch.device) -> None:
