@@ -90,6 +90,8 @@ _SHAPES = [
     (2, 5000, 8, 8, 8, 7),  # 64 pairs, many FIR tiles and all-pole chunks
     (2, 400, 9, 8, 8, 6),  # 72 pairs in one call (no grouping on this path)
     (3, 257, 2, 3, 64, 5),  # 64 taps, a ragged second FIR tile
+    (2, 2051, 2, 12, 12, 6),  # 12 outputs: two FIR channel blocks (8 + 4); 12 taps padded to 16; 3 FIR tiles
+    (1, 1030, 3, 9, 32, 5),  # 9 outputs (8 + 1), 32 taps, a 6-step last FIR tile, L % 4 = 2
 ]
 
 
