@@ -942,6 +942,9 @@ def main():
               else run_linrec if args.linrec else run_projected if args.projected else run_adjoint if args.adjoint
               else {1: run_diag, 2: run_diag, 3: run_mamba, 4: run_allpole, 5: run_diag}[args.config])
     ms, total_bytes, kernels, cpu = runner(args, line)
+    # the look-back scans' mode: bitwise reproducible (the library's default) or fast
+    # (TSFAST_HIP_REPRODUCIBLE=0: composition back to the nearest finished tile)
+    line["lookback_mode"] = "reproducible" if _lib._reproducible else "fast"
     mfma_peak = line.pop("_mfma_peak_tflops", None)
     if mfma_peak is not None:
         # a matrix-core workload: throughput in algorithmic TFLOP/s against the dense fp32 MFMA peak

@@ -45,15 +45,16 @@ extern "C" {
 const char* tsfast_hip_status_string(int status);
 
 /* Deterministic mode of the single-pass look-back scans (diag, selective, all-pole, linear
- * recurrence, G-block, projected), process-wide, read when a scan is launched. Off (0, the default):
- * a tile composes the published maps back to the nearest tile that has published its leaving
- * state, so which maps are composed depends on timing and results agree run to run to fp64
- * rounding. On: only every s-th tile in scan order publishes its leaving state and the others their
- * aggregates, so every launch composes the same maps in the same order and the outputs are bitwise
- * reproducible (the parameter-gradient sums of the projected scan excepted); a few to 20% slower.
- * No counterpart in the reference, whose kernels are deterministic by construction
- * (tsfast/models/architectures/mamba/mamba_triton.py:19-22); the Python backends set it from
- * torch.are_deterministic_algorithms_enabled(). */
+ * recurrence, G-block, projected), process-wide, read when a scan is launched. On (1, the
+ * default): anchor tiles in scan order publish their leaving state and the others their aggregates,
+ * so every launch composes the same maps in the same order and the outputs are bitwise reproducible
+ * (the parameter-gradient sums of the projected scan's fused backward excepted); 0-4% slower than
+ * off. Off (0): a tile composes the published maps back to the nearest tile that has published
+ * its leaving state, so which maps are composed depends on timing and results agree run to run to
+ * fp64 rounding. No counterpart in the reference, whose kernels are deterministic by construction
+ * (tsfast/models/architectures/mamba/mamba_triton.py:19-22); the Python backends keep it on unless
+ * reproducibility is switched off (tsfast_amd.set_reproducible(False) or
+ * TSFAST_HIP_REPRODUCIBLE=0) and torch.are_deterministic_algorithms_enabled() is false. */
 void tsfast_hip_set_deterministic(int on);
 int tsfast_hip_get_deterministic(void);
 /* Look-back failure reporting. Every look-back wait is bounded: a scan whose wait makes no

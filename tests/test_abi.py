@@ -179,3 +179,38 @@ def test_projected_supports_mirrors_the_library_size_check(lib, B, L, H, N, O):
 
     ok_lib = lib.tsfast_hip_projscan_workspace_bytes(B, L, H, N, O) >= 0
     assert (projected_hip.shape_reason(B, L, H, N, O) is None) == ok_lib
+
+
+def test_reproducible_by_default_and_switch(lib):
+    """The library starts in deterministic mode; the backends keep it there unless reproducibility
+    is switched off and torch's deterministic flag is off (no kernel is launched here)."""
+    import torch
+
+    _lib._det_mode = None
+    assert lib.tsfast_hip_get_deterministic() in (0, 1)
+    prev = _lib.set_reproducible(True)
+    try:
+        _lib.sync_deterministic()
+        assert lib.tsfast_hip_get_deterministic() == 1
+        _lib.set_reproducible(False)
+        _lib.sync_deterministic()
+        assert lib.tsfast_hip_get_deterministic() == 0
+        torch.use_deterministic_algorithms(True, warn_only=True)
+        try:
+            _lib.sync_deterministic()
+            assert lib.tsfast_hip_get_deterministic() == 1
+        finally:
+            torch.use_deterministic_algorithms(False)
+    finally:
+        _lib.set_reproducible(prev)
+        _lib.sync_deterministic()
+
+
+def test_library_default_is_deterministic(lib):
+    """A fresh process's library (C callers included) starts in deterministic mode."""
+    import subprocess
+    import sys
+
+    code = ("from tsfast_amd import _lib; import sys; "
+            "sys.exit(0 if _lib.load().tsfast_hip_get_deterministic() == 1 else 1)")
+    assert subprocess.run([sys.executable, "-c", code], cwd=ROOT).returncode == 0

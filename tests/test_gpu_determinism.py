@@ -1,17 +1,17 @@
-"""Bitwise run-to-run reproducibility of every HIP scan under torch.use_deterministic_algorithms
-(the reference's kernels are deterministic by construction,
-tsfast/models/architectures/mamba/mamba_triton.py:19-22).
+"""Bitwise run-to-run reproducibility of every HIP scan (the reference's kernels are deterministic
+by construction, tsfast/models/architectures/mamba/mamba_triton.py:19-22).
 
-In deterministic mode (tsfast_hip_set_deterministic, set by the backends from
-torch.are_deterministic_algorithms_enabled()) the look-back scans (diagonal, selective, all-pole,
-linear recurrence, G-block, projected) chain their tiles with anchored publication
-(csrc/lookback.h): a tile composes exactly the aggregates back to its anchor's published state,
-so which tiles happen to be finished when it looks back does not change a single bit. Sums over
-tiles run in fixed orders. Each test calls an op three times on the same inputs (a different
-amount of other GPU work queued before each call) and requires every output to be equal bit for
-bit, and the deterministic results to agree with the default mode's (which composes the nearest
-published maps) to fp32 rounding. Shapes span many super-chunks, so the walks cross several
-anchor spans.
+In deterministic mode (tsfast_hip_set_deterministic: on by default, kept on by the backends unless
+tsfast_amd.set_reproducible(False) and torch.are_deterministic_algorithms_enabled() is false) the
+look-back scans (diagonal, selective, all-pole, linear recurrence, G-block, projected) chain their
+tiles with anchored publication (csrc/lookback.h): a tile composes exactly the aggregates back to
+its anchor's published state, so which tiles happen to be finished when it looks back does not
+change a single bit. Sums over tiles run in fixed orders. Each test calls an op three times on the
+same inputs (a different amount of other GPU work queued before each call) under
+torch.use_deterministic_algorithms and requires every output to be equal bit for bit, and the
+results to agree with the fast mode's (reproducibility off: the nearest published maps) to fp32
+rounding. Shapes span many super-chunks, so the walks cross several anchor spans. One test repeats
+the diagonal scan in the library's default mode, with torch's flag off.
 """
 
 import math
@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 import torch
 
+from tsfast_amd import _lib
 from tsfast_amd.dynonet import allpole_hip, gblock_hip, linrec_hip
 from tsfast_amd.mamba import conv_hip, mamba_hip
 from tsfast_amd.scan_backends import diagonal_hip, projected_hip, selective_hip
@@ -55,7 +56,9 @@ def _repeat(fn, *args, reps=3):
 
 
 def _default_mode(fn, *args):
+    """The op in the fast mode (reproducibility off, torch's flag off)."""
     torch.use_deterministic_algorithms(False)
+    prev = _lib.set_reproducible(False)
     try:
         res = fn(*args)
         res = res if isinstance(res, (tuple, list)) else (res,)
@@ -63,6 +66,7 @@ def _default_mode(fn, *args):
         torch.cuda.synchronize()
         return res
     finally:
+        _lib.set_reproducible(prev)
         torch.use_deterministic_algorithms(True, warn_only=True)
 
 
@@ -222,18 +226,50 @@ def test_mamba_and_conv_bitwise_repeatable(gpu):
     _assert_same(_repeat(conv, x, tail, w, bias, gyc))
 
 
-def test_backends_follow_torch_deterministic_setting(gpu):
-    """A look-back scan launched under torch.use_deterministic_algorithms(True) runs in the
-    library's deterministic mode, and in the default mode otherwise."""
-    from tsfast_amd import _lib
-
+def test_backends_follow_the_reproducibility_settings(gpu):
+    """A look-back scan runs in the library's deterministic mode by default and under
+    torch.use_deterministic_algorithms(True) whatever set_reproducible says; only with both off
+    does it take the fast mode."""
     lam = torch.full((4, 8), 0.9, device=gpu)
     v = torch.randn(4, 100, 8, device=gpu)
     diagonal_hip.forward(lam, v, None)
     assert _lib.load().tsfast_hip_get_deterministic() == 1
+    prev = _lib.set_reproducible(False)
+    try:
+        diagonal_hip.forward(lam, v, None)  # torch's flag is on (fixture)
+        assert _lib.load().tsfast_hip_get_deterministic() == 1
+        torch.use_deterministic_algorithms(False)
+        diagonal_hip.forward(lam, v, None)
+        assert _lib.load().tsfast_hip_get_deterministic() == 0
+        _lib.set_reproducible(True)
+        diagonal_hip.forward(lam, v, None)
+        assert _lib.load().tsfast_hip_get_deterministic() == 1
+    finally:
+        _lib.set_reproducible(prev)
+
+
+def test_default_mode_is_bitwise_repeatable(gpu):
+    """Without torch's flag, the library's default mode alone makes the look-back scans repeat bit
+    for bit (diagonal scan over many super-chunks, forward and backward)."""
     torch.use_deterministic_algorithms(False)
-    diagonal_hip.forward(lam, v, None)
-    assert _lib.load().tsfast_hip_get_deterministic() == 0
+    g = torch.Generator().manual_seed(11)
+    lam = (torch.rand(8, 256, generator=g) * 0.099 + 0.9).to(gpu)
+    v = torch.randn(8, 20000, 256, generator=g).to(gpu)
+    gv = torch.randn(8, 20000, 256, generator=g).to(gpu)
+    x0 = torch.randn(8, 256, generator=g).to(gpu)
+
+    def call(lam, v, gv, x0):
+        out = diagonal_hip.forward(lam, v, x0)
+        return (out, *diagonal_hip.backward(gv, lam, out, x0))
+
+    noise = torch.randn(1 << 22, device=gpu)
+    outs = []
+    for r in range(3):
+        for _ in range(r * 3):
+            noise.mul_(1.0001)
+        outs.append([t.clone() for t in call(lam, v, gv, x0)])
+    torch.cuda.synchronize()
+    _assert_same(outs)
 
 
 def test_nss_adjoint_scan_bitwise_repeatable(gpu):

@@ -11,9 +11,12 @@ Mamba / dynoNet all-pole dispatch points (``mamba``, ``dynonet``) — and adds o
 - ``dynonet.allpole_hip``: ``supports(a, w, y0)``, ``run(a, w, y0)``.
 
 Every kernel is hand-written HIP in ``csrc/`` compiled into ``libtsfast_hip.so`` (C ABI in
-``include/tsfast_hip.h``) and loaded with ctypes by ``_lib``.
+``include/tsfast_hip.h``) and loaded with ctypes by ``_lib``. The look-back scans are bitwise
+reproducible by default, like the reference's kernels; ``set_reproducible(False)`` trades that for
+0-4% of speed.
 """
 
+from ._lib import set_reproducible  # noqa: F401
 from .dispatch import BACKENDS, get_backend, set_backend, use_backend  # noqa: F401
 
 __version__ = "0.1.0"

@@ -104,14 +104,26 @@ def load() -> ctypes.CDLL:
 
 
 _det_mode: int | None = None
+_reproducible = os.environ.get("TSFAST_HIP_REPRODUCIBLE", "1") not in ("", "0")
+
+
+def set_reproducible(on: bool) -> bool:
+    """Whether the look-back scans compose their tiles in a fixed order (bitwise reproducible
+    outputs, the default; 0-4% slower) or back to the nearest finished tile (results agree run to
+    run to fp64 rounding). Under ``torch.use_deterministic_algorithms(True)`` they are reproducible
+    either way. Also set by the environment variable ``TSFAST_HIP_REPRODUCIBLE`` (``0`` = off).
+    Returns the previous setting."""
+    global _reproducible
+    prev, _reproducible = _reproducible, bool(on)
+    return prev
 
 
 def sync_deterministic() -> None:
-    """Put the library's look-back scans in deterministic mode exactly when
-    ``torch.are_deterministic_algorithms_enabled()`` (bitwise reproducible outputs at some cost
-    in speed); called before every look-back scan is launched."""
+    """Put the library's look-back scans in deterministic mode unless reproducibility is switched
+    off (``set_reproducible``) and ``torch.are_deterministic_algorithms_enabled()`` is false;
+    called before every look-back scan is launched."""
     global _det_mode
-    want = 1 if torch.are_deterministic_algorithms_enabled() else 0
+    want = 1 if (_reproducible or torch.are_deterministic_algorithms_enabled()) else 0
     if want != _det_mode:
         load().tsfast_hip_set_deterministic(want)
         _det_mode = want

@@ -971,7 +971,7 @@ void diag_fwd_launch(const DiagTile& t, const T* lam, const T* v, const T* x0, T
   auto* inc = reinterpret_cast<W*>(agg + t.nsuper * t.lanes);
   lookback_reset_launch(ws, lookback_bytes(t, sizeof(W)) / 8, s);
   hipLaunchKernelGGL((diag_fwd<T, TC>), dim3(persistent_grid(t, diag_fwd<T, TC>, occ)), dim3(64 * t.K), 0, s, lam, v,
-                     x0, out, agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper, lb_spacing_for(kAnchorSpacing));
+                     x0, out, agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper, lb_spacing_for(anchor_spacing_for_groups(t.groups)));
 }
 
 template <typename T, int TC>
@@ -985,7 +985,7 @@ void diag_bwd_launch(const DiagTile& t, const T* g, const T* lam, const T* out, 
   lookback_reset_launch(ws, lookback_bytes(t, sizeof(W)) / 8, s);
   hipLaunchKernelGGL((diag_bwd<T, TC>), dim3(persistent_grid(t, diag_bwd<T, TC>, occ)), dim3(64 * t.K), 0, s, lam, g,
                      out, x0, agg, inc, reinterpret_cast<unsigned*>(ws), gv, part, glam, gx0, t.lanes, L, N, t.groups,
-                     t.K, t.nsuper, lb_spacing_for(kAnchorSpacing));
+                     t.K, t.nsuper, lb_spacing_for(anchor_spacing_for_groups(t.groups)));
   if (t.nsuper > 1)
     hipLaunchKernelGGL(diag_sum_parts<T>, dim3((unsigned)t.groups), dim3(64 * kMaxWaves), 0, s, (const W*)part, glam,
                        t.lanes, t.nsuper);
@@ -999,7 +999,7 @@ void sel_fwd_launch(const DiagTile& t, const float* a, const float* v, const flo
   auto* inc = reinterpret_cast<double*>(agg + t.nsuper * t.lanes);
   lookback_reset_launch(ws, lookback_bytes(t, 8) / 8, s);
   hipLaunchKernelGGL((sel_fwd<TC>), dim3(persistent_grid(t, sel_fwd<TC>, occ)), dim3(64 * t.K), 0, s, a, v, x0, out,
-                     agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper, lb_spacing_for(kAnchorSpacing));
+                     agg, inc, reinterpret_cast<unsigned*>(ws), t.lanes, L, N, t.groups, t.K, t.nsuper, lb_spacing_for(anchor_spacing_for_groups(t.groups)));
 }
 
 void sel_bwd_launch(const DiagTile& t, const float* g, const float* a, const float* out, const float* x0, float* glam,
@@ -1010,7 +1010,7 @@ void sel_bwd_launch(const DiagTile& t, const float* g, const float* a, const flo
   lookback_reset_launch(ws, lookback_bytes(t, 8) / 8, s);
   hipLaunchKernelGGL((sel_bwd<16>), dim3(persistent_grid(t, sel_bwd<16>, occ)), dim3(64 * t.K), 0, s, a, g, out, x0,
                      agg, inc, reinterpret_cast<unsigned*>(ws), glam, gv, gx0, t.lanes, L, N, t.groups, t.K,
-                     t.nsuper, lb_spacing_for(kAnchorSpacing));
+                     t.nsuper, lb_spacing_for(anchor_spacing_for_groups(t.groups)));
 }
 
 }  // namespace

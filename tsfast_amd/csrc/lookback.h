@@ -70,7 +70,12 @@ struct LbCfg {
 };
 TSF_DEV bool lb_pub_agg(int64_t j, LbCfg c) { return lb_pub_agg(j, c.spacing); }
 TSF_DEV bool lb_pub_inc(int64_t j, LbCfg c) { return lb_pub_inc(j, c.spacing); }
-constexpr int kAnchorSpacing = 8;  // deterministic-mode spacing of the look-backs whose window moves
+// Deterministic-mode anchor spacing of the look-backs whose window moves. Spacing 1 (every tile an
+// anchor: a chained scan, each tile waiting for its predecessor's state) is cheapest when many
+// lane groups run side by side, so each group's chain is short; few, long chains want the
+// longer spans.
+constexpr int kAnchorSpacing = 8;
+inline int anchor_spacing_for_groups(int64_t groups) { return groups >= 128 ? 1 : kAnchorSpacing; }
 
 // Give-up flag: the word kErrWord words after the tile counter (inside the kCounterBytes header
 // of the workspace, byte offset 64) is set to 1 by any look-back that gives up after kSpinMax

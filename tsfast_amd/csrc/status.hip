@@ -12,7 +12,8 @@ thread_local char g_msg[256];
 }
 
 namespace {
-std::atomic<int> g_deterministic{0};
+// Bitwise-reproducible look-back scans by default (tsfast_hip_set_deterministic)
+std::atomic<int> g_deterministic{1};
 // Polls without progress before a look-back gives up (lookback.h kSpinMax).
 std::atomic<uint32_t> g_spin_limit{1u << 20};
 // The alarm word: 4 bytes of mapped, coherent host memory (visible to every device), allocated
