@@ -47,15 +47,15 @@ TSF_DEV double2 quiet_nan<double2>() {
 }
 
 // What a tile publishes, in scan order j = 0, 1, ... (the last tile publishes nothing):
-//  * spacing 0 (default): every tile but the first publishes its aggregate (agg) and every tile
-//    the state leaving it (inc). A look-back stops at the nearest published inc, so the maps it
-//    composes depend on which tiles have finished: results agree run to run to fp64 rounding.
-//  * spacing s > 0 (deterministic mode): an anchor tile (j % s == 0) publishes only its inc, every
-//    other tile only its agg. A look-back then composes exactly the aggregates of tiles a+1 .. j-1
-//    onto inc_a (a = the last anchor before j) in the same order on every run, so the entering
-//    states and everything computed from them are bitwise reproducible; a tile waits for its
-//    anchor's look-back, which costs time when the anchor runs concurrently. s must not exceed
-//    the slots a look-back examines.
+//  * spacing 0 (the fast mode): every tile but the first publishes its aggregate (agg) and every
+//    tile the state leaving it (inc). A look-back stops at the nearest published inc, so the maps
+//    it composes depend on which tiles have finished: results agree run to run to fp64 rounding.
+//  * spacing s > 0 (deterministic mode, the library's default): an anchor tile (j % s == 0)
+//    publishes only its inc, every other tile only its agg. A look-back then composes exactly the
+//    aggregates of tiles a+1 .. j-1 onto inc_a (a = the last anchor before j) in the same order on
+//    every run, so the entering states and everything computed from them are bitwise
+//    reproducible; a tile waits for its anchor's look-back, which costs time when the anchor runs
+//    concurrently. s must not exceed the slots a look-back examines.
 TSF_DEV bool lb_pub_agg(int64_t j, int spacing) { return spacing == 0 ? j > 0 : j % spacing != 0; }
 TSF_DEV bool lb_pub_inc(int64_t j, int spacing) { return spacing == 0 || j % spacing == 0; }
 
