@@ -3,8 +3,8 @@
 Counterparts of ``tsfast/models/architectures/dynonet/core.py``:
 
 * ``linear_recurrence`` (``:103-127``): ``x_t = A x_{t-1} + v_t`` with constant ``A [..., n, n]``
-  and its matrix adjoint. On GPU the ``"hip"`` family serves state sizes n <= 8 (a single-pass
-  scan for n <= 4, a two-pass scan above); otherwise the ``tsfast_hip::linear_recurrence`` op
+  and its matrix adjoint. On GPU the ``"hip"`` family serves state sizes n <= 16 (a single-pass
+  scan for n <= 4, two-pass scans above); otherwise the ``tsfast_hip::linear_recurrence`` op
   runs the blocked torch scan of :mod:`tsfast_amd.blocked_scan` (the reference runs a
   log-doubling scan, ``:23-37``).
 * ``allpole``: the all-pole branch of ``LinearDynamicalOperator.forward`` (``:221-248``), the
@@ -140,9 +140,10 @@ def linear_dynamical_operator(
 
     ``u [B, L, I]``, ``b_coeff [O, I, nb]``, ``a_coeff [O, I, na]``; ``state`` is the reference's
     ``{"u": FIR tail [B, nb-1, I], "x": IIR states [B, I*O, na]}`` (zeros if None). The fused
-    G-block kernel runs FIR, all-pole and the sum over inputs in one pass when it serves the
-    inputs; otherwise the reference's three stages run (grouped ``conv1d`` with flipped taps,
-    the all-pole op per pair, the sum over inputs). Returns ``y [B, L, O]`` and, with
+    G-block backend runs FIR, all-pole and the sum over inputs when it serves the inputs (one
+    pass for na <= 4, this library's FIR and all-pole ops for higher orders); otherwise the
+    reference's three stages run (grouped ``conv1d`` with flipped taps, the all-pole op per pair,
+    the sum over inputs). Returns ``y [B, L, O]`` and, with
     ``return_state``, the new state.
     """
     B, L, I = u.shape
