@@ -830,12 +830,23 @@ TSF_DEV float fir_u(const float* __restrict__ u, const float* __restrict__ u_tai
   if (!u_tail || t < -(int64_t)(nb - 1)) return 0.0f;
   return u_tail[(b * (nb - 1) + (nb - 1 + t)) * I + j];
 }
-// s_u[i] = u_ext[t0 - (NBT - 1) + i], i < kFirT + NBT
+// s_u[i] = u_ext[t0 - (NBT - 1) + i], i < kFirT + NBT: every load issued before the first LDS
+// store, so the thread waits on them together rather than one round trip at a time
 template <int NBT>
 TSF_DEV void fir_stage_u(float* s_u, const float* __restrict__ u, const float* __restrict__ u_tail, const FirTile& f,
                          int64_t L, int I, int nb) {
-  for (int i = threadIdx.x; i < kFirT + NBT; i += kFirW)
-    s_u[i] = fir_u(u, u_tail, f.b, f.t0 - (NBT - 1) + i, f.j, L, I, nb);
+  constexpr int NU = (kFirT + NBT + kFirW - 1) / kFirW;
+  float v[NU];
+#pragma unroll
+  for (int c = 0; c < NU; ++c) {
+    const int i = threadIdx.x + c * kFirW;
+    v[c] = i < kFirT + NBT ? fir_u(u, u_tail, f.b, f.t0 - (NBT - 1) + i, f.j, L, I, nb) : 0.0f;
+  }
+#pragma unroll
+  for (int c = 0; c < NU; ++c) {
+    const int i = threadIdx.x + c * kFirW;
+    if (i < kFirT + NBT) s_u[i] = v[c];
+  }
 }
 // taps of output channels o0 .. o0 + kFirOB - 1 for input j, zero past nb and past O
 template <int NBT>
@@ -953,19 +964,47 @@ __global__ void __launch_bounds__(kFirW) gb_fir_bwd(const float* __restrict__ gw
   for (int o0 = 0; o0 < O; o0 += kFirOB) {
     const int ob = (O - o0) < kFirOB ? (O - o0) : kFirOB;
     __syncthreads();  // the previous block's rows, taps and wave sums are read
-    for (int r = 0; r < kFirOB; ++r) {
-      const float* grow = gw + (f.b * P + (int64_t)f.j * O + o0 + r) * L;
-      const bool live = r < ob;
-      if (vec) {
-        for (int q = tid; q < NS / 4; q += kFirW) {
+    // the block's gw rows: every load issued before the first LDS store
+    if (vec) {
+      constexpr int NQ = (NS / 4 + kFirW - 1) / kFirW;  // 16-byte pieces per thread and row
+      float4 x[kFirOB][NQ];
+#pragma unroll
+      for (int r = 0; r < kFirOB; ++r) {
+        const float* grow = gw + (f.b * P + (int64_t)f.j * O + o0 + r) * L;
+#pragma unroll
+        for (int c = 0; c < NQ; ++c) {
+          const int q = tid + c * kFirW;
           const int64_t tq = f.t0 + 4 * q;
-          float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          if (live && tq < L) x = *reinterpret_cast<const float4*>(grow + tq);  // L % 4 == 0: all in range
-          reinterpret_cast<float4*>(&s_g[r][0])[q] = x;
+          x[r][c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          if (r < ob && q < NS / 4 && tq < L) x[r][c] = *reinterpret_cast<const float4*>(grow + tq);  // L % 4 == 0
         }
-      } else {
-        for (int i = tid; i < NS; i += kFirW) s_g[r][i] = (live && f.t0 + i < L) ? grow[f.t0 + i] : 0.0f;
       }
+#pragma unroll
+      for (int r = 0; r < kFirOB; ++r)
+#pragma unroll
+        for (int c = 0; c < NQ; ++c) {
+          const int q = tid + c * kFirW;
+          if (q < NS / 4) reinterpret_cast<float4*>(&s_g[r][0])[q] = x[r][c];
+        }
+    } else {
+      constexpr int NE = (NS + kFirW - 1) / kFirW;
+      float x[kFirOB][NE];
+#pragma unroll
+      for (int r = 0; r < kFirOB; ++r) {
+        const float* grow = gw + (f.b * P + (int64_t)f.j * O + o0 + r) * L;
+#pragma unroll
+        for (int c = 0; c < NE; ++c) {
+          const int i = tid + c * kFirW;
+          x[r][c] = (r < ob && i < NS && f.t0 + i < L) ? grow[f.t0 + i] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kFirOB; ++r)
+#pragma unroll
+        for (int c = 0; c < NE; ++c) {
+          const int i = tid + c * kFirW;
+          if (i < NS) s_g[r][i] = x[r][c];
+        }
     }
     fir_stage_b<NBT>(s_b, bcoef, o0, O, I, f.j, nb);
     __syncthreads();
