@@ -57,20 +57,20 @@ MEASURED_TRAFFIC = {
         "bwd": (3_103_900_000, "profiles/mamba_scan_config3_traffic.md"),
     },
     (2, "f32"): {
-        "fwd": (1_139_400_000, "profiles/diag_scan_config2_traffic.md"),
-        "bwd": (1_686_700_000, "profiles/diag_scan_config2_traffic.md"),
+        "fwd": (1_109_100_000, "profiles/diag_scan_config2_traffic.md"),
+        "bwd": (1_656_200_000, "profiles/diag_scan_config2_traffic.md"),
     },
     ("selective", "f32"): {
-        "fwd": (1_631_000_000, "profiles/selective_scan_traffic.md"),
-        "bwd": (2_727_900_000, "profiles/selective_scan_traffic.md"),
+        "fwd": (1_624_700_000, "profiles/selective_scan_traffic.md"),
+        "bwd": (2_713_100_000, "profiles/selective_scan_traffic.md"),
     },
     (4, "f32"): {
-        "fwd": (672_000_000, "profiles/allpole_scan_config4_traffic.md"),
-        "bwd": (961_100_000, "profiles/allpole_scan_config4_traffic.md"),
+        "fwd": (668_600_000, "profiles/allpole_scan_config4_traffic.md"),
+        "bwd": (959_800_000, "profiles/allpole_scan_config4_traffic.md"),
     },
     ("linrec", "f32"): {
-        "fwd": (2_122_100_000, "profiles/linrec_config4route_traffic.md"),
-        "bwd": (3_258_500_000, "profiles/linrec_config4route_traffic.md"),
+        "fwd": (2_120_800_000, "profiles/linrec_config4route_traffic.md"),
+        "bwd": (3_283_900_000, "profiles/linrec_config4route_traffic.md"),
     },
 }
 
