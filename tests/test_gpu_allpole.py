@@ -150,3 +150,28 @@ def test_allpole_reference_coefficient_draws(gpu, B, P, L, na, with_y0):
     assert O.rel_err(_np(a_d.grad), ga.reshape(B, P, na).sum(0)) < TOL, "ga"
     if y0 is not None:
         assert O.rel_err(_np(y0_d.grad).reshape(lanes, na), gy0) < TOL, "gy0"
+
+
+def test_allpole_long_chunks_square_the_transfer(gpu):
+    """A sequence of more than 65535 x 256 steps takes all-pole chunks longer than 256 steps (one
+    grid row per chunk), whose transfer matrix is C^256 squared up (allpole_transfer) rather than
+    stepped column by column: one lane, na 5, against scipy's lfilter (the textbook form the
+    oracle is pinned to) for y and the adjoint G = the same filter run backwards, with
+    grad a_i = -sum_t G_t y_{t-i} and grad w = G."""
+    from scipy.signal import lfilter
+
+    g = torch.Generator().manual_seed(17)
+    L, na = 65535 * 256 + 4097, 5
+    a = _stable_poles(1, na, g)
+    w = torch.randn(1, L, generator=g)
+    gy = torch.randn(1, L, generator=g)
+    ag, wg = a.to(gpu).requires_grad_(), w.to(gpu).requires_grad_()
+    y = allpole_hip.run(ag, wg, None)
+    y.backward(gy.to(gpu))
+    den = np.concatenate(([1.0], a[0].double().numpy()))
+    y_ref = lfilter([1.0], den, w[0].double().numpy())
+    G = lfilter([1.0], den, gy[0].double().numpy()[::-1])[::-1]
+    ga_ref = np.array([-(G[i:] * y_ref[: L - i]).sum() for i in range(1, na + 1)])
+    assert O.rel_err(_np(y)[0], y_ref) < TOL
+    assert O.rel_err(_np(wg.grad)[0], G) < TOL
+    assert O.rel_err(_np(ag.grad)[0], ga_ref) < TOL
