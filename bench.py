@@ -702,27 +702,34 @@ def projected_inputs(device, B=64, L=4096, H=32, N=256, O=32, seed=4):
 
 
 def run_projected(args, line):
-    """The fused projected complex diagonal scan (LRU / S5 layer core) at config 2's shape, with the
-    reference's unfused stack (complex_in_proj -> diagonal_recurrence -> real_out_proj, HIP scan
-    backend, autograd) timed in the same run. Both projections run on the fp32 matrix cores, so
-    the roofline is fp32 MFMA."""
+    """The projected complex diagonal scan (LRU / S5 layer core) at config 2's shape (or the widths
+    --widths names) as projected_diagonal_recurrence runs it: the fused kernels within their widths
+    (H, O <= 32, N <= 256), the wide route beyond (one GEMM per projection around the diagonal scan
+    kernels, split-K weight gradients). The reference's unfused stack (complex_in_proj ->
+    diagonal_recurrence -> real_out_proj, HIP scan backend, autograd) is timed in the same run. The
+    projections run on the fp32 matrix cores, so the roofline is fp32 MFMA."""
     import torch
 
     from tsfast_amd import scan
     from tsfast_amd.scan_backends import projected_hip
 
-    u, W_re, W_im, lam, C_re, C_im, gy = projected_inputs("cuda")
-    B, L, H = u.shape
-    N, O = lam.shape[0], C_re.shape[0]
+    H, N, O = (int(v) for v in args.widths.split(","))
+    u, W_re, W_im, lam, C_re, C_im, gy = projected_inputs("cuda", H=H, N=N, O=O)
+    B, L = u.shape[:2]
+    bl = B * L
+    fused = projected_hip.shape_reason(B, L, H, N, O) is None
+    fwd_f = 2 * bl * 2 * N * (H + O)  # in-projection and read-out
+    # g_x, grad C, grad W, g_u; the fused backward also recomputes v (the wide route saves x)
+    bwd_f = 2 * bl * 2 * N * (2 * O + (3 if fused else 2) * H)
+    train_op = projected_hip._scan_train_op if fused else projected_hip._wide_train_op
+    bwd_op = projected_hip._scan_bwd_op if fused else projected_hip._wide_bwd_op
 
     def step(ev):
         mark(ev)
-        y, x_last, saved = projected_hip._scan_train_op(u, W_re, W_im, lam, C_re, C_im, None)
+        y, x_last, saved = train_op(u, W_re, W_im, lam, C_re, C_im, None)
         mark(ev)
-        projected_hip._scan_bwd_op(gy, None, saved, u, W_re, W_im, lam, C_re, C_im, None)
+        bwd_op(gy, None, saved, u, W_re, W_im, lam, C_re, C_im, None)
         mark(ev)
-
-    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
 
     def unfused(ev):
         ins = [t.detach().requires_grad_() for t in (u, W_re, W_im, lam, C_re, C_im)]
@@ -733,15 +740,15 @@ def run_projected(args, line):
         torch.autograd.backward(y, gy)
         mark(ev)
 
+    ms, (fwd_ms, bwd_ms) = time_steps(step, args.steps, args.warmup)
     ums, (ufwd, ubwd) = time_steps(unfused, max(args.steps // 2, 2), 2)
-    bl = B * L
-    fwd_f = 2 * bl * 2 * N * (H + O)  # in-projection and read-out
-    bwd_f = 2 * bl * 2 * N * (2 * O + 3 * H)  # g_x, v recompute, grad C, grad W, g_u
+    route = "fused" if fused else "wide route (GEMMs around the diagonal scan kernels, split-K weight gradients)"
     line.update(
-        metric="fwd+bwd ms + achieved fp32 TFLOP/s, fused projected complex diagonal scan (LRU/S5 layer core)",
+        metric=f"fwd+bwd ms + achieved fp32 TFLOP/s, projected complex diagonal scan (LRU/S5 layer core), {route}",
         unit="TFLOP/s",
-        config={"workload": f"fused complex_in_proj -> diagonal_recurrence -> real_out_proj fwd+bwd: batch {B}, "
-                            f"L {L}, N {N} complex states, H {H} inputs, O {O} outputs (BASELINE config 2 scan)",
+        config={"workload": f"{route} complex_in_proj -> diagonal_recurrence -> real_out_proj fwd+bwd: batch {B}, "
+                            f"L {L}, N {N} complex states, H {H} inputs, O {O} outputs"
+                            + (" (BASELINE config 2 scan)" if (H, N, O) == (32, 256, 32) else ""),
                 "B": B, "L": L, "N": N, "H": H, "O": O},
         fwd_ms=round(fwd_ms, 4),
         bwd_ms=round(bwd_ms, 4),
@@ -750,8 +757,12 @@ def run_projected(args, line):
         algorithmic_flops={"fwd": fwd_f, "bwd": bwd_f},
         _mfma_peak_tflops=157.3,
     )
-    kernels = {"fwd": ("projscan_fwd (in-projection, scan, read-out on fp32 MFMA)", fwd_ms, fwd_f),
-               "bwd": ("projscan_bwd + projscan_bwd_reduce", bwd_ms, bwd_f)}
+    if fused:
+        kernels = {"fwd": ("projscan_fwd (in-projection, scan, read-out on fp32 MFMA)", fwd_ms, fwd_f),
+                   "bwd": ("projscan_bwd + projscan_bwd_reduce", bwd_ms, bwd_f)}
+    else:
+        kernels = {"fwd": ("wide forward: 2 GEMMs + diag_fwd", fwd_ms, fwd_f),
+                   "bwd": ("wide backward: 2 GEMMs + diag_bwd + 2 split-K weight-gradient GEMMs", bwd_ms, bwd_f)}
     return ms, fwd_f + bwd_f, kernels, None
 
 
@@ -887,6 +898,9 @@ def main():
                     help="measure the constant-matrix linear_recurrence on config 4's companion-matrix route")
     ap.add_argument("--projected", action="store_true",
                     help="measure the fused projected complex diagonal scan (LRU/S5 core) at config 2's shape")
+    ap.add_argument("--widths", default="32,256,32",
+                    help="with --projected: the layer's H,N,O (config 2's scan is 32,256,32); widths beyond the "
+                         "fused kernel's (H, O <= 32, N <= 256) run the wide route")
     ap.add_argument("--adjoint", action="store_true",
                     help="measure the chunked NSS adjoint scan (n 32, the reference's chunking)")
     ap.add_argument("--order", type=int, default=3,

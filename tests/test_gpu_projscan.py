@@ -8,7 +8,10 @@ max relative error <= 1e-5 on y, the returned state and all seven gradients.
 
 Shapes cover every (H, O) kernel instantiation, N that is not a multiple of 64, L that is not a
 multiple of the 64-step forward tile or the 32-step backward tile, L = 1, several look-back
-chunks per row, and config 2 (N 256, H = O = 32) at full length with the batch reduced.
+chunks per row, and config 2 (N 256, H = O = 32) at full length with the batch reduced. Widths
+beyond the fused kernel's (H or O > 32, N > 256) take the wide route (packed GEMMs around the
+diagonal scan kernels, split-K weight gradients) and are held to the same bar, with B L large
+enough for the split-K products, a remainder row block included.
 """
 
 import numpy as np
@@ -35,6 +38,15 @@ _SHAPES = [
     (1, 1000, 1, 1, 1),
     (5, 513, 12, 192, 8),
     (4, 4096, 32, 256, 32),  # config 2, batch reduced
+]
+# wider than the fused kernel: the wide route
+_WIDE_SHAPES = [
+    (2, 7, 33, 4, 2),
+    (2, 300, 48, 64, 40),
+    (2, 257, 16, 300, 8),
+    (3, 130, 33, 256, 33),
+    (1, 9001, 64, 96, 48),  # split-K over 2 row blocks and a one-row remainder
+    (2, 8192, 128, 512, 128),  # the widths of a large LRU / S5 layer, 16 row blocks
 ]
 
 
@@ -100,6 +112,48 @@ def test_projscan_matches_oracle(gpu, shape, with_x0):
     y, xl, grads = _run(gpu, u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl)
     torch.cuda.synchronize()
     _check(y, xl, grads, u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl)
+
+
+@pytest.mark.parametrize("shape", _WIDE_SHAPES)
+@pytest.mark.parametrize("with_x0", [True, False])
+def test_projscan_wide_route_matches_oracle(gpu, shape, with_x0):
+    B, L, H, N, O_ = shape
+    assert projected_hip.shape_reason(B, L, H, N, O_) is not None
+    u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl = _make(*shape, seed=sum(shape))
+    x0 = x0 if with_x0 else None
+    print(f"projscan wide shape={shape} x0={with_x0}", flush=True)
+    y, xl, grads = _run(gpu, u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl)
+    torch.cuda.synchronize()
+    _check(y, xl, grads, u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl)
+
+
+def test_projscan_wide_route_inference_and_chunks(gpu):
+    """Wide route: the no-grad op gives the training forward's outputs bit for bit, and carrying
+    the returned state through four chunks equals one call."""
+    u, W_re, W_im, lam, C_re, C_im, *_ = _make(2, 1024, 40, 300, 36, seed=12)
+    d = [t.to(gpu) for t in (u, W_re, W_im, lam, C_re, C_im)]
+    with torch.no_grad():
+        y0, xl0 = projected_hip.run(*d, None)
+        state, ys = None, []
+        for k in range(4):
+            yk, state = projected_hip.run(d[0][:, 256 * k : 256 * (k + 1)].contiguous(), *d[1:], state)
+            ys.append(yk)
+    y1, xl1, x = projected_hip._wide_train_op(*d, None)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1) and torch.equal(xl0, xl1) and x.shape == (2, 1024, 300)
+    assert O.rel_err(_np(torch.cat(ys, 1)), _np(y0)) < TOL
+    assert O.rel_err(_np(state), _np(xl0)) < TOL
+
+
+def test_projscan_wide_route_empty_sequence(gpu):
+    u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl = _make(2, 0, 40, 8, 3, seed=9)
+    y, xl, grads = _run(gpu, u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 0, 3)
+    assert torch.equal(xl.cpu(), x0)
+    assert torch.equal(grads[6].cpu(), g_xl)
+    for gw in grads[1:6]:
+        assert not gw.cpu().any()
 
 
 def test_projscan_without_state_gradient(gpu):
