@@ -264,7 +264,9 @@ int tsfast_hip_linrec_bwd(int64_t lanes, int64_t L, int64_t n, const float* g, c
  * and S5.forward (architectures/s5.py:180-198) call it, plus the returned state x[..., -1, :].
  * Layout: u [B, L, H] float32; w_re/w_im [N, H]; lam [N] complex64 (interleaved re, im);
  * c_re/c_im [O, N]; x0 and x_last [B, N] complex64; y [B, L, O] float32; all contiguous.
- * Limits: H <= 32, N <= 256, O <= 32 and B * L * H * 4 < 2^31, else TSF_ERR_UNSUPPORTED.
+ * Limits: H <= 32, N <= 256, O <= 32 and B * L * H * 4 < 2^31, else TSF_ERR_UNSUPPORTED. Wider
+ * layers run as two GEMMs around tsfast_hip_diag_fwd / tsfast_hip_diag_bwd (the Python backend's
+ * wide route), which have no width limits.
  * saved (may be NULL) receives the state entering each 32-step sub-chunk, [B, ceil(L/32), N]
  * complex64 (tsfast_hip_projscan_saved_floats floats), for the backward pass. The workspace holds
  * the look-back words, re-initialised by each call on its stream: two calls in flight must not
