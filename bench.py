@@ -356,8 +356,13 @@ def run_diag(args, line):
     line.update(config={"workload": workload, "M": M, "L": L, "N": N, "io_dtype": "complex64" if cplx else "f32"},
                 fwd_ms=round(fwd_ms, 4), bwd_ms=round(bwd_ms, 4))
     line["dtype"] = "c128" if cplx else "f64"  # fp32/complex64 I/O, fp64 state inside
-    kernels = {"fwd": ("diag_fwd look-back scan + workspace reset", fwd_ms, fwd_b),
-               "bwd": ("diag_bwd look-back scan + reset + glam lane sums", bwd_ms, bwd_b)}
+    # the kernels csrc/diag.hip picks for these shapes (whole_tile): config 1 runs whole-sequence
+    # tiles both ways, config 5's 64-chunk forward too, and the rest the look-back
+    whole_fwd = "diag_whole_fwd (whole-sequence tiles, one launch)"
+    look_fwd = "diag_fwd look-back scan + workspace reset"
+    kernels = {"fwd": (whole_fwd if cfg in (1, 5) else look_fwd, fwd_ms, fwd_b),
+               "bwd": ("diag_whole_bwd (whole-sequence tiles, one launch)" if cfg == 1
+                       else "diag_bwd look-back scan + reset + glam lane sums", bwd_ms, bwd_b)}
     cpu = None
     if not args.no_cpu:
         def cpu_leg():

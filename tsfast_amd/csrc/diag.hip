@@ -927,10 +927,15 @@ struct WholeTile {
 inline WholeTile whole_tile(int64_t lanes, int64_t L, int tc, bool bwd) {
   const int64_t chunks = (L + tc - 1) / tc;
   if ((lanes + 63) / 64 >= 256) return chunks <= 16 ? WholeTile{64, 16} : WholeTile{};
-  if (chunks <= 16) return {16, 16};
-  // 64 chunks of 16 lanes: forward only, and only while one round of workgroups covers the
-  // lanes (the backward of so long a chunk run reloads its values, slower than the look-back)
-  if (!bwd && chunks <= 64 && (lanes + 15) / 16 <= 256) return {16, 64};
+  // the forward narrows its groups to 8 lanes while that keeps within one workgroup per CU (8-lane
+  // groups measured 4-9% faster on configs 5 and 1, 4-lane groups no faster than 8); the
+  // backward stays at 16 lanes (narrower groups measured 12% slower on config 1)
+  const int lg = (!bwd && (lanes + 7) / 8 <= 256) ? 8 : 16;
+  if (chunks <= 16) return {lg, 16};
+  // 64 chunks of 16 or 8 lanes: forward only, and only while one round of workgroups covers the
+  // lanes (the backward of so long a chunk run reloads its values, slower than the look-back; a
+  // 4-lane backward that keeps them measured 29% slower on config 5 at one wave per SIMD)
+  if (!bwd && chunks <= 64 && (lanes + lg - 1) / lg <= 256) return {lg, 64};
   return {};
 }
 inline bool whole_both(int64_t lanes, int64_t L, bool cplx) {
@@ -942,24 +947,27 @@ template <typename T, int TC>
 void whole_fwd_launch(const WholeTile& w, int64_t lanes, int64_t L, int64_t N, const T* lam, const T* v, const T* x0,
                       T* out, unsigned* ws, hipStream_t s) {
   const dim3 grid((unsigned)((lanes + w.lg - 1) / w.lg)), block((unsigned)(w.lg * ((L + TC - 1) / TC)));
-  if (w.lg == 64)
-    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 64, 16>), grid, block, 0, s, lam, v, x0, out, ws, lanes, L, N);
-  else if (w.kmax == 16)
-    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 16, 16>), grid, block, 0, s, lam, v, x0, out, ws, lanes, L, N);
-  else
-    hipLaunchKernelGGL((diag_whole_fwd<T, TC, 16, 64>), grid, block, 0, s, lam, v, x0, out, ws, lanes, L, N);
+#define TSF_WHOLE_FWD(LG, KMAX) \
+  if (w.lg == LG && w.kmax == KMAX) { \
+    hipLaunchKernelGGL((diag_whole_fwd<T, TC, LG, KMAX>), grid, block, 0, s, lam, v, x0, out, ws, lanes, L, N); \
+    return; \
+  }
+  TSF_WHOLE_FWD(64, 16) TSF_WHOLE_FWD(16, 16) TSF_WHOLE_FWD(8, 16) TSF_WHOLE_FWD(16, 64) TSF_WHOLE_FWD(8, 64)
+#undef TSF_WHOLE_FWD
 }
 
 template <typename T, int TC>
 void whole_bwd_launch(const WholeTile& w, int64_t lanes, int64_t L, int64_t N, const T* lam, const T* g, const T* out,
                       const T* x0, T* gv, T* glam, T* gx0, unsigned* ws, hipStream_t s) {
   const dim3 grid((unsigned)((lanes + w.lg - 1) / w.lg)), block((unsigned)(w.lg * ((L + TC - 1) / TC)));
-  if (w.lg == 64)
-    hipLaunchKernelGGL((diag_whole_bwd<T, TC, 64, 16>), grid, block, 0, s, lam, g, out, x0, gv, glam, gx0, ws, lanes,
-                       L, N);
-  else
-    hipLaunchKernelGGL((diag_whole_bwd<T, TC, 16, 16>), grid, block, 0, s, lam, g, out, x0, gv, glam, gx0, ws, lanes,
-                       L, N);
+#define TSF_WHOLE_BWD(LG, KMAX) \
+  if (w.lg == LG && w.kmax == KMAX) { \
+    hipLaunchKernelGGL((diag_whole_bwd<T, TC, LG, KMAX>), grid, block, 0, s, lam, g, out, x0, gv, glam, gx0, ws, \
+                       lanes, L, N); \
+    return; \
+  }
+  TSF_WHOLE_BWD(64, 16) TSF_WHOLE_BWD(16, 16)
+#undef TSF_WHOLE_BWD
 }
 
 template <typename T, int TC>
