@@ -644,8 +644,10 @@ TSF_DEV void half_swap(double (&sp)[NH], const double (&s)[NH]) {
 #pragma unroll
   for (int i = 0; i < NH; ++i) {
     const uint64_t b = (uint64_t)__double_as_longlong(s[i]);
-    const uint64_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, 0xB1, 0xF, 0xF, false);
-    const uint64_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), 0xB1, 0xF, 0xF, false);
+    // quad_perm [1,0,3,2] reads a lane of every pair, so no lane keeps its old value: mov_dpp
+    // (no old operand) spares the zeroing move update_dpp(0, ...) would need per word
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)b, 0xB1, 0xF, 0xF, false);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), 0xB1, 0xF, 0xF, false);
     sp[i] = __longlong_as_double((long long)((hi << 32) | lo));
   }
 }
@@ -714,21 +716,24 @@ __global__ void __launch_bounds__(kWideThreads) lw_sum_fwd(const float* __restri
 #pragma unroll
   for (int i = 0; i < NH; ++i) s[i] = 0.0;
   const float* row = v + q.lane * L * NS + q.own0;
-  // kWidePf steps' loads in flight: step t + kWidePf is fetched while step t computes
+  // kWidePf steps' loads in flight: step t + kWidePf is fetched while step t computes. The whole
+  // blocks run without per-step branches: a fetch past the chunk's end re-reads its last step
+  // (never used), and the remaining n % kWidePf steps follow the loop.
+  const int64_t t0 = q.t0, tl = q.t1 - 1, n = q.t1 - q.t0, nfull = n - n % kWidePf;
   float d[kWidePf][NH];
 #pragma unroll
-  for (int k = 0; k < kWidePf; ++k)
-    if (q.t0 + k < q.t1) ld_half<NS, VH>(d[k], row + (q.t0 + k) * NS, q.own0);
-  for (int64_t tb = q.t0; tb < q.t1; tb += kWidePf) {
+  for (int k = 0; k < kWidePf; ++k) ld_half<NS, VH>(d[k], row + (t0 + k < tl ? t0 + k : tl) * NS, q.own0);
+  for (int64_t tb = t0; tb < t0 + nfull; tb += kWidePf) {
 #pragma unroll
     for (int k = 0; k < kWidePf; ++k) {
-      const int64_t t = tb + k;
-      if (t < q.t1) {  // uniform over the workgroup (one chunk)
-        half_step<NH>(mo, mp, s, d[k]);
-        if (t + kWidePf < q.t1) ld_half<NS, VH>(d[k], row + (t + kWidePf) * NS, q.own0);
-      }
+      half_step<NH>(mo, mp, s, d[k]);
+      const int64_t tn = tb + k + kWidePf;
+      ld_half<NS, VH>(d[k], row + (tn < tl ? tn : tl) * NS, q.own0);
     }
   }
+#pragma unroll
+  for (int k = 0; k < kWidePf - 1; ++k)
+    if (k < n - nfull) half_step<NH>(mo, mp, s, d[k]);
 #pragma unroll
   for (int i = 0; i < NH; ++i)
     if (q.own0 + i < NS) e[(q.c * lanes + q.lane) * NS + q.own0 + i] = s[i];
@@ -778,9 +783,25 @@ __global__ void __launch_bounds__(kWideThreads) lw_apply_fwd(const float* __rest
     for (int k = 0; k < kWidePf; ++k)
       if (q.t0 + k < q.t1) ld_half<NS, VH>(d[k], row + (q.t0 + k) * NS, q.own0);
   }
+  const int64_t tl = q.t1 - 1;
   for (int64_t tb = q.t0; tb < q.t1; tb += SB) {
     const int cnt = (int)((q.t1 - tb) < SB ? (q.t1 - tb) : SB);
-    if (q.live) {
+    if (q.live && cnt == SB) {
+      // a whole sub-block without per-step branches (which made the compiler copy the prefetch
+      // ring between register sets every step): a fetch past the chunk's end re-reads its last step
+#pragma unroll
+      for (int kk = 0; kk < SB; kk += kWidePf) {
+#pragma unroll
+        for (int k = 0; k < kWidePf; ++k) {
+          half_step<NH>(mo, mp, s, d[k]);
+#pragma unroll
+          for (int i = 0; i < NH; ++i)
+            if (q.own0 + i < NS) s_o[q.ll][(kk + k) * NS + q.own0 + i] = (float)s[i];
+          const int64_t tn = tb + kk + k + kWidePf;
+          ld_half<NS, VH>(d[k], row + (tn < tl ? tn : tl) * NS, q.own0);
+        }
+      }
+    } else if (q.live) {
       for (int kk = 0; kk < SB; kk += kWidePf) {
 #pragma unroll
         for (int k = 0; k < kWidePf; ++k) {
@@ -814,20 +835,24 @@ __global__ void __launch_bounds__(kWideThreads) lw_sum_bwd(const float* __restri
 #pragma unroll
   for (int i = 0; i < NH; ++i) G[i] = 0.0;
   const float* row = g + q.lane * L * NS + q.own0;
+  // as lw_sum_fwd, from the chunk's last step down: whole blocks without per-step branches (a
+  // fetch before the chunk's start re-reads its first step), then the remaining steps
+  const int64_t t0 = q.t0, tl = q.t1 - 1, n = q.t1 - q.t0, nblk = (n - n % kWidePf) / kWidePf;
   float d[kWidePf][NH];
 #pragma unroll
-  for (int k = 0; k < kWidePf; ++k)
-    if (q.t1 - 1 - k >= q.t0) ld_half<NS, VH>(d[k], row + (q.t1 - 1 - k) * NS, q.own0);
-  for (int64_t tb = q.t1 - 1; tb >= q.t0; tb -= kWidePf) {
+  for (int k = 0; k < kWidePf; ++k) ld_half<NS, VH>(d[k], row + (tl - k > t0 ? tl - k : t0) * NS, q.own0);
+  for (int64_t it = 0; it < nblk; ++it) {
+    const int64_t tb = tl - it * kWidePf;
 #pragma unroll
     for (int k = 0; k < kWidePf; ++k) {
-      const int64_t t = tb - k;
-      if (t >= q.t0) {
-        half_step<NH>(mo, mp, G, d[k]);
-        if (t - kWidePf >= q.t0) ld_half<NS, VH>(d[k], row + (t - kWidePf) * NS, q.own0);
-      }
+      half_step<NH>(mo, mp, G, d[k]);
+      const int64_t tn = tb - k - kWidePf;
+      ld_half<NS, VH>(d[k], row + (tn > t0 ? tn : t0) * NS, q.own0);
     }
   }
+#pragma unroll
+  for (int k = 0; k < kWidePf - 1; ++k)
+    if (k < n - nblk * kWidePf) half_step<NH>(mo, mp, G, d[k]);
 #pragma unroll
   for (int i = 0; i < NH; ++i)
     if (q.own0 + i < NS) f[(q.c * lanes + q.lane) * NS + q.own0 + i] = G[i];
@@ -941,30 +966,53 @@ __global__ void __launch_bounds__(kWideThreads) lw_apply_bwd(const float* __rest
   for (int64_t j = nsb - 1; j >= 0; --j) {
     const int64_t tb = t0 + j * SB;
     const int cnt = (int)((t1 - tb) < SB ? (t1 - tb) : SB);
-    if (q.live) {
+    // one step of the re-run: G, its store to the tile, grad_A += G_t x_{t-1}^T (x_{t-1}: the
+    // owned rows and, by a DPP swap, the partner's)
+    auto step = [&](int k, int slot) __attribute__((always_inline)) {
+      half_step<NH>(mo, mp, G, dg[k]);
+      float xo[NH], xq[NH];
+#pragma unroll
+      for (int i = 0; i < NH; ++i) {
+        xo[i] = dx[k][i];
+        xq[i] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(xo[i]), 0xB1, 0xF, 0xF, false));
+      }
+#pragma unroll
+      for (int i = 0; i < NH; ++i)
+        if (q.own0 + i < NS) s_o[q.ll][slot * NS + q.own0 + i] = (float)G[i];
+      return [&, xo, xq]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NH; ++i) {
+#pragma unroll
+          for (int jj = 0; jj < NH; ++jj) acc[i][jj] = fma(G[i], (double)xo[jj], acc[i][jj]);
+#pragma unroll
+          for (int jj = 0; jj < NH; ++jj) acc[i][NH + jj] = fma(G[i], (double)xq[jj], acc[i][NH + jj]);
+        }
+      };
+    };
+    // (odd n keeps the guarded loop: its padded half rows took the branch-free form past 256 VGPRs)
+    if (NS % 2 == 0 && q.live && cnt == SB && tb > 0) {
+      // a whole sub-block without per-step branches: a fetch before the chunk's start re-reads its
+      // first step (never used); every fetched step is >= 1 here (t0 > 0, or tb >= SB > kPfB), so
+      // x_{t-1} is a row of out
+      for (int kk = SB - kPfB; kk >= 0; kk -= kPfB) {
+#pragma unroll
+        for (int k = kPfB - 1; k >= 0; --k) {
+          auto grad_a = step(k, kk + k);
+          const int64_t tn = tb + kk + k - kPfB, tc = tn > t0 ? tn : t0;
+          ld_half<NS, VH>(dg[k], grow + tc * NS, q.own0);
+          ld_half<NS, VH>(dx[k], xrow + (tc - 1) * NS, q.own0);
+          grad_a();
+        }
+      }
+    } else if (q.live) {
       for (int kk = SB - kPfB; kk >= 0; kk -= kPfB) {
 #pragma unroll
         for (int k = kPfB - 1; k >= 0; --k) {
           const int64_t t = tb + kk + k;
           if (t < t1) {  // uniform over the workgroup (one chunk)
-            half_step<NH>(mo, mp, G, dg[k]);
-            float xo[NH], xq[NH];  // x_{t-1}: owned rows, the partner's rows
-#pragma unroll
-            for (int i = 0; i < NH; ++i) {
-              xo[i] = dx[k][i];
-              xq[i] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(xo[i]), 0xB1, 0xF, 0xF, false));
-            }
-#pragma unroll
-            for (int i = 0; i < NH; ++i)
-              if (q.own0 + i < NS) s_o[q.ll][(kk + k) * NS + q.own0 + i] = (float)G[i];
+            auto grad_a = step(k, kk + k);
             if (t - kPfB >= t0) fetch(k, t - kPfB);
-#pragma unroll
-            for (int i = 0; i < NH; ++i) {
-#pragma unroll
-              for (int jj = 0; jj < NH; ++jj) acc[i][jj] = fma(G[i], (double)xo[jj], acc[i][jj]);
-#pragma unroll
-              for (int jj = 0; jj < NH; ++jj) acc[i][NH + jj] = fma(G[i], (double)xq[jj], acc[i][NH + jj]);
-            }
+            grad_a();
           }
         }
       }
