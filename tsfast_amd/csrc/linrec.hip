@@ -1214,21 +1214,27 @@ __global__ void __launch_bounds__(256) lsp_sum_fwd(const float* __restrict__ A, 
   const bool ld = q.live && q.r < n;
   double p[kSpread];
   spread_row(p, A, q.lane, n, q.r, q.live, false);
-  const float* row = v + (q.live ? q.lane : 0) * L * n + q.r;
+  // whole blocks of kSpreadPf steps without per-step branches (which made the compiler copy the
+  // prefetch ring between register sets every step): every load is unconditional, a fetch past
+  // the chunk's end re-reads its last step (never used) and threads r >= n read component n - 1
+  // (their inputs are taken as zero); the remaining steps follow the loop
+  const float* row = v + (q.live ? q.lane : 0) * L * n + (q.r < n ? q.r : n - 1);
+  const int64_t t0 = q.t0, tl = q.t1 - 1, cnt = q.t1 - q.t0, nfull = cnt - cnt % kSpreadPf;
   float d[kSpreadPf];
 #pragma unroll
-  for (int k = 0; k < kSpreadPf; ++k) d[k] = (ld && q.t0 + k < q.t1) ? row[(q.t0 + k) * n] : 0.0f;
+  for (int k = 0; k < kSpreadPf; ++k) d[k] = row[(t0 + k < tl ? t0 + k : tl) * n];
   double s = 0.0;
-  for (int64_t tb = q.t0; tb < q.t1; tb += kSpreadPf) {
+  for (int64_t tb = t0; tb < t0 + nfull; tb += kSpreadPf) {
 #pragma unroll
     for (int k = 0; k < kSpreadPf; ++k) {
-      const int64_t t = tb + k;
-      if (t < q.t1) {  // uniform over the workgroup (one chunk)
-        s = spread_dot(p, s, (double)d[k]);
-        d[k] = (ld && t + kSpreadPf < q.t1) ? row[(t + kSpreadPf) * n] : 0.0f;
-      }
+      s = spread_dot(p, s, ld ? (double)d[k] : 0.0);
+      const int64_t tn = tb + k + kSpreadPf;
+      d[k] = row[(tn < tl ? tn : tl) * n];
     }
   }
+#pragma unroll
+  for (int k = 0; k < kSpreadPf - 1; ++k)
+    if (k < cnt - nfull) s = spread_dot(p, s, ld ? (double)d[k] : 0.0);
   if (ld) e[(q.c * lanes + q.lane) * n + q.r] = s;
 }
 
@@ -1258,24 +1264,30 @@ __global__ void __launch_bounds__(256) lsp_apply_fwd(const float* __restrict__ A
   const bool ld = q.live && q.r < n;
   double p[kSpread];
   spread_row(p, A, q.lane, n, q.r, q.live, false);
-  const int64_t off = (q.live ? q.lane : 0) * L * n + q.r;
+  const int64_t off = (q.live ? q.lane : 0) * L * n + (q.r < n ? q.r : n - 1);
   const float* row = v + off;
   float* orow = x + off;
+  // as lsp_sum_fwd: whole blocks without per-step branches, then the remaining steps
+  const int64_t t0 = q.t0, tl = q.t1 - 1, cnt = q.t1 - q.t0, nfull = cnt - cnt % kSpreadPf;
   float d[kSpreadPf];
 #pragma unroll
-  for (int k = 0; k < kSpreadPf; ++k) d[k] = (ld && q.t0 + k < q.t1) ? row[(q.t0 + k) * n] : 0.0f;
+  for (int k = 0; k < kSpreadPf; ++k) d[k] = row[(t0 + k < tl ? t0 + k : tl) * n];
   double s = ld ? carry[(q.c * lanes + q.lane) * n + q.r] : 0.0;
-  for (int64_t tb = q.t0; tb < q.t1; tb += kSpreadPf) {
+  for (int64_t tb = t0; tb < t0 + nfull; tb += kSpreadPf) {
 #pragma unroll
     for (int k = 0; k < kSpreadPf; ++k) {
-      const int64_t t = tb + k;
-      if (t < q.t1) {
-        s = spread_dot(p, s, (double)d[k]);
-        if (ld) orow[t * n] = (float)s;
-        d[k] = (ld && t + kSpreadPf < q.t1) ? row[(t + kSpreadPf) * n] : 0.0f;
-      }
+      s = spread_dot(p, s, ld ? (double)d[k] : 0.0);
+      if (ld) orow[(tb + k) * n] = (float)s;
+      const int64_t tn = tb + k + kSpreadPf;
+      d[k] = row[(tn < tl ? tn : tl) * n];
     }
   }
+#pragma unroll
+  for (int k = 0; k < kSpreadPf - 1; ++k)
+    if (k < cnt - nfull) {
+      s = spread_dot(p, s, ld ? (double)d[k] : 0.0);
+      if (ld) orow[(t0 + nfull + k) * n] = (float)s;
+    }
 }
 
 // Adjoint chunk starts from a zero right-end state: f [nchunks][lanes][n]
@@ -1285,21 +1297,25 @@ __global__ void __launch_bounds__(256) lsp_sum_bwd(const float* __restrict__ A, 
   const bool ld = q.live && q.r < n;
   double p[kSpread];
   spread_row(p, A, q.lane, n, q.r, q.live, true);
-  const float* row = g + (q.live ? q.lane : 0) * L * n + q.r;
+  // as lsp_sum_fwd from the chunk's last step down (a fetch before its start re-reads its first)
+  const float* row = g + (q.live ? q.lane : 0) * L * n + (q.r < n ? q.r : n - 1);
+  const int64_t t0 = q.t0, tl = q.t1 - 1, cnt = q.t1 - q.t0, nblk = (cnt - cnt % kSpreadPf) / kSpreadPf;
   float d[kSpreadPf];
 #pragma unroll
-  for (int k = 0; k < kSpreadPf; ++k) d[k] = (ld && q.t1 - 1 - k >= q.t0) ? row[(q.t1 - 1 - k) * n] : 0.0f;
+  for (int k = 0; k < kSpreadPf; ++k) d[k] = row[(tl - k > t0 ? tl - k : t0) * n];
   double G = 0.0;
-  for (int64_t tb = q.t1 - 1; tb >= q.t0; tb -= kSpreadPf) {
+  for (int64_t it = 0; it < nblk; ++it) {
+    const int64_t tb = tl - it * kSpreadPf;
 #pragma unroll
     for (int k = 0; k < kSpreadPf; ++k) {
-      const int64_t t = tb - k;
-      if (t >= q.t0) {
-        G = spread_dot(p, G, (double)d[k]);
-        d[k] = (ld && t - kSpreadPf >= q.t0) ? row[(t - kSpreadPf) * n] : 0.0f;
-      }
+      G = spread_dot(p, G, ld ? (double)d[k] : 0.0);
+      const int64_t tn = tb - k - kSpreadPf;
+      d[k] = row[(tn > t0 ? tn : t0) * n];
     }
   }
+#pragma unroll
+  for (int k = 0; k < kSpreadPf - 1; ++k)
+    if (k < cnt - nblk * kSpreadPf) G = spread_dot(p, G, ld ? (double)d[k] : 0.0);
   if (ld) f[(q.c * lanes + q.lane) * n + q.r] = G;
 }
 
@@ -1339,33 +1355,41 @@ __global__ void __launch_bounds__(256) lsp_apply_bwd(const float* __restrict__ A
   spread_row(p, A, q.lane, n, q.r, q.live, true);
 #pragma unroll
   for (int c = 0; c < kSpread; ++c) acc[c] = 0.0;
-  const int64_t off = (q.live ? q.lane : 0) * L * n + q.r;
+  const int64_t off = (q.live ? q.lane : 0) * L * n + (q.r < n ? q.r : n - 1);
   const float* grow = g + off;
   const float* xrow = out + off;
   float* orow = gv + off;
   const float x_init = (ld && x0) ? x0[q.lane * n + q.r] : 0.0f;  // x_{-1}
-  // slot k holds g_t and x_{t-1} of a step t with (t1 - 1 - t) % kSpreadPf == k
+  // slot k holds g_t and x_{t-1} of a step t with (t1 - 1 - t) % kSpreadPf == k. Every load is
+  // unconditional (as lsp_sum_bwd: fetches before the chunk's start re-read its first step, threads
+  // r >= n read component n - 1, masked on use); x_{t-1} of step 0 is x_init.
   float dg[kSpreadPf], dx[kSpreadPf];
+  const int64_t t0 = q.t0, tl = q.t1 - 1, cnt = q.t1 - q.t0, nblk = (cnt - cnt % kSpreadPf) / kSpreadPf;
   auto fetch = [&](int k, int64_t t) __attribute__((always_inline)) {
-    dg[k] = ld ? grow[t * n] : 0.0f;
-    dx[k] = !ld ? 0.0f : t > 0 ? xrow[(t - 1) * n] : x_init;
+    const int64_t tc = t > t0 ? t : t0;
+    dg[k] = grow[tc * n];
+    const float xv = xrow[(tc > 0 ? tc - 1 : 0) * n];
+    dx[k] = tc > 0 ? xv : x_init;
+  };
+  double G = ld ? rc[(q.c * lanes + q.lane) * n + q.r] : 0.0;
+  auto step = [&](int k, int64_t t) __attribute__((always_inline)) {
+    G = spread_dot(p, G, ld ? (double)dg[k] : 0.0);
+    if (ld) orow[t * n] = (float)G;
+    spread_outer(acc, G, ld ? dx[k] : 0.0f);
   };
 #pragma unroll
-  for (int k = 0; k < kSpreadPf; ++k)
-    if (q.t1 - 1 - k >= q.t0) fetch(k, q.t1 - 1 - k);
-  double G = ld ? rc[(q.c * lanes + q.lane) * n + q.r] : 0.0;
-  for (int64_t tb = q.t1 - 1; tb >= q.t0; tb -= kSpreadPf) {
+  for (int k = 0; k < kSpreadPf; ++k) fetch(k, tl - k);
+  for (int64_t it = 0; it < nblk; ++it) {
+    const int64_t tb = tl - it * kSpreadPf;
 #pragma unroll
     for (int k = 0; k < kSpreadPf; ++k) {
-      const int64_t t = tb - k;
-      if (t >= q.t0) {
-        G = spread_dot(p, G, (double)dg[k]);
-        if (ld) orow[t * n] = (float)G;
-        spread_outer(acc, G, dx[k]);
-        if (t - kSpreadPf >= q.t0) fetch(k, t - kSpreadPf);
-      }
+      step(k, tb - k);
+      fetch(k, tb - k - kSpreadPf);
     }
   }
+#pragma unroll
+  for (int k = 0; k < kSpreadPf - 1; ++k)
+    if (k < cnt - nblk * kSpreadPf) step(k, tl - nblk * kSpreadPf - k);
   if (ld) {
     double* pr = part + ((q.c * lanes + q.lane) * n + q.r) * n;
 #pragma unroll
