@@ -27,6 +27,8 @@
 //             tile's G. grad a = -sum G_t y_{t-i} and grad b = sum G_t u_{t-k} are reduced per
 //             tile; gu (sum of c over o) and the tail gradient go through LDS.
 // Orders na <= 4, nb <= 16 (taps padded to NBT in {2, 4, 8, 16} with zeros), I * O <= 64.
+#include <type_traits>
+
 #include "common.h"
 #include "tsfast_hip.h"
 
@@ -289,6 +291,18 @@ TSF_DEV float* part_b_area(LdsTile* lds, int wv) {
   return reinterpret_cast<float*>(reinterpret_cast<double*>(&lds[wv][0][0]) + 64 * NA);
 }
 
+// Runs body(whole) with whole a compile-time true for a whole tile (n == kTileT steps, every
+// chunk but the sequence's last) and false otherwise. A loop whose steps are each guarded by
+// `i < n` makes the compiler merge the recurrence state at every step (register copies on every
+// step); the whole-tile instance has no guards.
+template <typename F>
+TSF_DEV void whole_or_part(int n, F&& body) {
+  if (n == kTileT)
+    body(std::true_type{});
+  else
+    body(std::false_type{});
+}
+
 template <int NA, int NBT>
 __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     const float* __restrict__ gy, const float* __restrict__ g_xlast, const float* __restrict__ u,
@@ -362,15 +376,17 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
       load_g_window(gw);
 #pragma unroll
       for (int q = 0; q < NA; ++q) sG[q] = sC[q] = 0.0;
+      whole_or_part(n, [&](auto whole) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = kTileT - 1; i >= 0; --i)
-        if (i < n) {
-          float h = 0.0f;
+        for (int i = kTileT - 1; i >= 0; --i)
+          if (decltype(whole)::value || i < n) {
+            float h = 0.0f;
 #pragma unroll
-          for (int kk = 0; kk < NBT; ++kk) h = fmaf(bk[kk], gw[i + kk], h);
-          step<NA>(av, sG, (double)gw[i]);
-          step<NA>(av, sC, (double)h);
-        }
+            for (int kk = 0; kk < NBT; ++kk) h = fmaf(bk[kk], gw[i + kk], h);
+            step<NA>(av, sG, (double)gw[i]);
+            step<NA>(av, sC, (double)h);
+          }
+      });
     }
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
@@ -442,9 +458,11 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
         for (int i = 0; i < kUW; ++i) s_uw[k][lid][i] = uw[i];
       }
       fir<NBT>(xb, uw, bk);
+      whole_or_part(n, [&](auto whole) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < kTileT; ++i)
-        if (i < n) step<NA>(av, s, (double)xb[i]);
+        for (int i = 0; i < kTileT; ++i)
+          if (decltype(whole)::value || i < n) step<NA>(av, s, (double)xb[i]);
+      });
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -471,9 +489,11 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
     if (n > 0) {
 #pragma unroll
       for (int q = 0; q < NA; ++q) s[q] = vk[q];
+      whole_or_part(n, [&](auto whole) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < kTileT; ++i)
-        if (i < n) xb[i] = (float)step<NA>(av, s, (double)xb[i]);
+        for (int i = 0; i < kTileT; ++i)
+          if (decltype(whole)::value || i < n) xb[i] = (float)step<NA>(av, s, (double)xb[i]);
+      });
     }
     // --- adjoint sweep: G, c, grad a, grad b, head taps and the tail gradient
     double ga[NA];
@@ -488,19 +508,21 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
       load_g_window(gw);
       // pass 1, right to left: G, c (into xb) and grad a; G_t then goes into gw[i + NBT - 1],
       // the window slot no later step reads (step i' < i reads gw[i' .. i' + NBT - 1])
+      whole_or_part(n, [&](auto whole) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = kTileT - 1; i >= 0; --i)
-        if (i < n) {
-          const double yu = xb[i];
+        for (int i = kTileT - 1; i >= 0; --i)
+          if (decltype(whole)::value || i < n) {
+            const double yu = xb[i];
 #pragma unroll
-          for (int q = 0; q < NA; ++q) ga[q] = fma(sG[q], yu, ga[q]);  // sG_q = G_{t+1+q} before the step
-          float h = 0.0f;
+            for (int q = 0; q < NA; ++q) ga[q] = fma(sG[q], yu, ga[q]);  // sG_q = G_{t+1+q} before the step
+            float h = 0.0f;
 #pragma unroll
-          for (int kk = 0; kk < NBT; ++kk) h = fmaf(bk[kk], gw[i + kk], h);
-          const float G = (float)step<NA>(av, sG, (double)gw[i]);
-          xb[i] = (float)step<NA>(av, sC, (double)h);  // c_t, the pair's input gradient at t
-          gw[i + NBT - 1] = G;
-        }
+            for (int kk = 0; kk < NBT; ++kk) h = fmaf(bk[kk], gw[i + kk], h);
+            const float G = (float)step<NA>(av, sG, (double)gw[i]);
+            xb[i] = (float)step<NA>(av, sC, (double)h);  // c_t, the pair's input gradient at t
+            gw[i + NBT - 1] = G;
+          }
+      });
       // gu[b, t, j] = sum_o c_{j*O+o}[t] through the wave's LDS tile
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -529,20 +551,22 @@ __global__ void __launch_bounds__(64 * kLbWaves) gblock_bwd_lb(
         } else {
           load_u_window<NBT>(uw, u, u_tail, g, t0, L, I, nb);
         }
+        whole_or_part(n, [&](auto whole) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < kTileT; ++i)
-          if (i < n) {
-            const float G = gw[i + NBT - 1];
+          for (int i = 0; i < kTileT; ++i)
+            if (decltype(whole)::value || i < n) {
+              const float G = gw[i + NBT - 1];
 #pragma unroll
-            for (int kk = 0; kk < NBT; ++kk) gbk[kk] = fmaf(G, uw[i + NBT - 1 - kk], gbk[kk]);
-            if (t0 == 0) {
-              // u_tail[m] (time m - (nb - 1)) met b_kk at steps i = m - (nb - 1) + kk >= 0
+              for (int kk = 0; kk < NBT; ++kk) gbk[kk] = fmaf(G, uw[i + NBT - 1 - kk], gbk[kk]);
+              if (t0 == 0) {
+                // u_tail[m] (time m - (nb - 1)) met b_kk at steps i = m - (nb - 1) + kk >= 0
 #pragma unroll
-              for (int kk = 1; kk < NBT; ++kk)
-                if (i < kk && i - kk + NBT - 1 >= 0) gt[i - kk + NBT - 1] = fmaf(bk[kk], G, gt[i - kk + NBT - 1]);
-              if (i < NA && live) gh[lane * NA + i] = G;  // G_0 .. G_{NA-1} for the x0 head taps
+                for (int kk = 1; kk < NBT; ++kk)
+                  if (i < kk && i - kk + NBT - 1 >= 0) gt[i - kk + NBT - 1] = fmaf(bk[kk], G, gt[i - kk + NBT - 1]);
+                if (i < NA && live) gh[lane * NA + i] = G;  // G_0 .. G_{NA-1} for the x0 head taps
+              }
             }
-          }
+        });
       }
       if (t0 == 0 && gu_tail && nb > 1) {
         // gt[m'] holds tail position m' - (NBT - 1) + (nb - 1) = m; only m' >= NBT - nb are real
