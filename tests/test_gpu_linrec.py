@@ -62,6 +62,11 @@ _SHAPES = [
     (300, 256, 6),  # exactly one chunk, two lane blocks
     (600, 3000, 8),  # three lane blocks (the last partial) x twelve chunks (the last ragged)
     (520, 1500, 5),  # three lane blocks x six chunks
+    # chunks that end off a prefetch block (4 steps) and off an output sub-block: the remainder
+    # after the whole blocks, and chunk 0's guarded re-run with x0 at step 0
+    (9, 263, 8),  # a 7-step second chunk
+    (4, 5, 6),  # one 5-step chunk, shorter than a sub-block
+    (2, 514, 7),  # odd n, a 2-step third chunk
     # n = 9..16: spread path (16 lanes of a workgroup, one 16-thread group each)
     (5, 40, 9),
     (33, 1000, 12),  # three lane groups (the last with one lane), ragged last chunk
@@ -71,6 +76,8 @@ _SHAPES = [
     (40, 600, 13),
     (20, 256, 10),  # exactly one chunk
     (16, 2000, 15),  # exactly one workgroup of lanes
+    (6, 262, 12),  # a 6-step second chunk, shorter than one 8-step prefetch block
+    (5, 1283, 16),  # a 3-step last chunk after five whole ones
 ]
 
 
