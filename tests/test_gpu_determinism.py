@@ -194,6 +194,29 @@ def test_projected_scan_repeatable(gpu):
             assert ((a - b).abs().max() / b.abs().max()).item() < 1e-5, f"output {i}: composition vs fused"
 
 
+def test_projected_wide_route_bitwise_repeatable(gpu):
+    """Beyond the fused widths the projected scan runs GEMMs around the diagonal scan kernels and
+    takes its weight gradients as split-K products summed in a fixed order: every output and
+    gradient repeats bit for bit, and matches the fast mode's to 1e-6."""
+    g = torch.Generator().manual_seed(12)
+    B, L, H, N, O = 2, 9000, 48, 300, 40
+    assert projected_hip.shape_reason(B, L, H, N, O) is not None
+    u = torch.randn(B, L, H, generator=g)
+    W_re, W_im = torch.randn(N, H, generator=g) / math.sqrt(H), torch.randn(N, H, generator=g) / math.sqrt(H)
+    lam = torch.polar(torch.rand(N, generator=g) * 0.099 + 0.9, torch.rand(N, generator=g) * 0.3)
+    C_re, C_im = torch.randn(O, N, generator=g) / 16, torch.randn(O, N, generator=g) / 16
+    gy = torch.randn(B, L, O, generator=g)
+    x0 = torch.randn(B, N, dtype=torch.complex64, generator=g)
+    g_xl = torch.randn(B, N, dtype=torch.complex64, generator=g)
+    ins = [t.to(gpu) for t in (u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl)]
+
+    def call(u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl):
+        y, x_last, x = projected_hip._wide_train_op(u, W_re, W_im, lam, C_re, C_im, x0)
+        return (y, x_last, *projected_hip._wide_bwd_op(gy, g_xl, x, u, W_re, W_im, lam, C_re, C_im, x0))
+
+    _assert_same(_repeat(call, *ins))
+
+
 def test_mamba_and_conv_bitwise_repeatable(gpu):
     """No look-back here (one workgroup walks a whole sequence); the channel and batch sums run in
     fixed orders."""
