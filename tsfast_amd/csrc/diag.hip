@@ -413,9 +413,10 @@ __global__ void __launch_bounds__(1024) diag_bwd(const T* __restrict__ lam, cons
 // LG-lane group's whole sequence (threads k*LG .. k*LG + LG-1 the k-th chunk): no look-back, no
 // workspace words and no reset launch, so each direction is a single kernel. After one barrier
 // every chunk composes the summaries of the chunks before it (forward) or after it (backward)
-// from LDS into its entering state, at most K - 1 fp64 folds. Narrow groups (LG = 16) give a
-// small scan more workgroups than there are lane groups of 64; whole_group() hands each XCD a
-// contiguous range of groups, so the groups whose rows share a 128-byte line share an L2.
+// from LDS into its entering state, at most K - 1 fp64 folds. Narrow groups (LG = 16, or 8 in the
+// forward) give a small scan more workgroups than there are lane groups of 64; whole_group()
+// hands each XCD a contiguous range of groups, so the groups whose rows share a 128-byte line
+// share an L2.
 TSF_DEV int64_t whole_group() {
   const unsigned total = gridDim.x;
   unsigned lin = blockIdx.x;
@@ -917,9 +918,10 @@ unsigned persistent_grid(const DiagTile& t, F kern, int* cache) {
 
 // Whole-sequence tiling (diag_whole_fwd / diag_whole_bwd): TC steps per chunk; lane groups of 64
 // (256-byte row segments of fp32) when they already give every CU a workgroup, else of 16 (four
-// times the workgroups; 64-byte segments, paired in L2). A workgroup holds up to 1024 threads:
-// 16 chunks of 64 lanes, or 64 chunks of 16 lanes (16 chunks when they cover the sequence, so
-// that 256 threads may keep a chunk's values in registers). Longer sequences take the look-back.
+// times the workgroups; 64-byte segments, paired in L2) or, in the forward, of 8 while that stays
+// within one workgroup per CU. A workgroup holds up to 1024 threads: 16 chunks of 64 lanes, or up
+// to 64 chunks of 16 or 8 lanes (the backward 16 chunks of 16 lanes, so that 256 threads may keep
+// a chunk's values in registers). Longer sequences take the look-back.
 constexpr int whole_tc(bool cplx, bool bwd) { return cplx ? (bwd ? 16 : 32) : 64; }
 struct WholeTile {
   int lg = 0, kmax = 0;  // kmax == 0: the sequence is too long for one workgroup
