@@ -153,10 +153,12 @@ def test_compile_linear_dynamical_operator_with_state(gpu):
     _compare(section, leaves)
 
 
-def test_compile_projected_diagonal_recurrence(gpu):
-    """The fused LRU/S5 layer core (tsfast_hip::projected_scan_train / _bwd) under fullgraph."""
+@pytest.mark.parametrize("widths", [(6, 40, 5), (40, 300, 36)], ids=["fused", "wide"])
+def test_compile_projected_diagonal_recurrence(gpu, widths):
+    """The LRU/S5 layer core under fullgraph: the fused ops (tsfast_hip::projected_scan_train /
+    _bwd) and, beyond their widths, the wide route's (projected_scan_wide_train / _bwd)."""
     g = torch.Generator().manual_seed(9)
-    B, L, H, N, O = 2, 400, 6, 40, 5
+    (B, L), (H, N, O) = (2, 400), widths
     leaves = [t.to(gpu).requires_grad_() for t in (
         torch.randn(B, L, H, generator=g), torch.randn(N, H, generator=g) / H**0.5, torch.randn(N, H, generator=g) / H**0.5,
         torch.polar(torch.rand(N, generator=g) * 0.099 + 0.9, torch.rand(N, generator=g) * 0.3),
