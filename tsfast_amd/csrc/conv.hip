@@ -193,19 +193,39 @@ __global__ void __launch_bounds__(kCh) conv_silu_fwd_kernel(const TIO* __restric
   TIO* orow = out + b * L * D;
   TileRegs2<TIO, TR> rg;
   tile_issue<TIO, TR, VECL>(rg, xrow, t0, L, c0, D, sxl, sxd);
+  const bool all_live = c0 + kCh <= D;  // uniform over the workgroup
   for (int64_t jb = 0; jb < nrow; jb += TR) {
     __syncthreads();
     tile_commit<TIO, TR>(rg, s_x);
     __syncthreads();
     if (jb + TR < nrow) tile_issue<TIO, TR, VECL>(rg, xrow, t0 + jb + TR, L, c0, D, sxl, sxd);
+    if (all_live && jb + TR <= nrow) {
+      // a whole tile of a fully live workgroup: no per-step exit or store mask. Groups of K steps
+      // (TR is a multiple of K, so a step's ring slot is its place in the group) in a loop that is
+      // not unrolled: unrolled over the whole tile, the compiler hoisted the later steps' reads
+      // and offsets (130 VGPRs against 51)
+      const uint32_t o0 = (uint32_t)((t0 + jb) * D + d);
+#pragma unroll 1
+      for (int i0 = 0; i0 < TR; i0 += K) {
 #pragma unroll
-    for (int i = 0; i < TR; ++i) {
-      if (jb + i >= nrow) break;  // uniform over the workgroup
-      xr[i % K] = to_f32(s_x[i][tid]);
-      float p = bv;
+        for (int r = 0; r < K; ++r) {
+          xr[r] = to_f32(s_x[i0 + r][tid]);
+          float p = bv;
 #pragma unroll
-      for (int k = 0; k < K; ++k) p = fmaf(wk[k], xr[(i + 1 + k) % K], p);
-      if (live) st32(orow, (uint32_t)((t0 + jb + i) * D + d), from_f32<TIO>(silu_f(p)));
+          for (int k = 0; k < K; ++k) p = fmaf(wk[k], xr[(r + 1 + k) % K], p);
+          st32(orow, o0 + (uint32_t)((i0 + r) * D), from_f32<TIO>(silu_f(p)));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TR; ++i) {
+        if (jb + i >= nrow) break;  // uniform over the workgroup
+        xr[i % K] = to_f32(s_x[i][tid]);
+        float p = bv;
+#pragma unroll
+        for (int k = 0; k < K; ++k) p = fmaf(wk[k], xr[(i + 1 + k) % K], p);
+        if (live) st32(orow, (uint32_t)((t0 + jb + i) * D + d), from_f32<TIO>(silu_f(p)));
+      }
     }
   }
 }
