@@ -764,11 +764,11 @@ __global__ void __launch_bounds__(256) mamba_reduce_bc(const TIO* __restrict__ p
 // one kind (NS a multiple of V = 16 / sizeof(TIO)): thread (row, q) adds columns V q .. V q + V - 1
 // of every tile's [2*NS] row, in tile order, and writes them to gBt (V q < NS) or gCt.
 template <typename TIO>
-__global__ void __launch_bounds__(256) mamba_reduce_bc_vec(const TIO* __restrict__ part, TIO* __restrict__ gBt,
-                                                           TIO* __restrict__ gCt, int64_t nT, int64_t BL, int NS) {
+TSF_DEV void reduce_bc_vec(const TIO* __restrict__ part, TIO* __restrict__ gBt, TIO* __restrict__ gCt, int64_t nT,
+                           int64_t BL, int NS, unsigned block) {
   constexpr int V = 16 / sizeof(TIO);
   const int QR = 2 * NS / V;  // vectors per row
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // over BL * QR
+  const int64_t i = block * (int64_t)blockDim.x + threadIdx.x;  // over BL * QR
   if (i >= BL * QR) return;
   const int64_t row = i / QR;
   const int q = (int)(i % QR);
@@ -792,14 +792,37 @@ __global__ void __launch_bounds__(256) mamba_reduce_bc_vec(const TIO* __restrict
   *reinterpret_cast<uint4*>(dst) = o;
 }
 
-// Sum [B, X] partials over the batch into [X] (gA with X = D*N, gDp with X = D).
-__global__ void __launch_bounds__(256) mamba_reduce_batch(const float* __restrict__ part, float* __restrict__ dst,
-                                                          int64_t B, int64_t X) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+// Sum [B, X] partials over the batch into [X] (gA with X = D*N, gDp with X = D), in batch order.
+TSF_DEV void reduce_batch(const float* __restrict__ part, float* __restrict__ dst, int64_t B, int64_t X,
+                          unsigned block) {
+  const int64_t i = block * (int64_t)blockDim.x + threadIdx.x;
   if (i >= X) return;
   float s = 0.0f;
   for (int64_t b = 0; b < B; ++b) s += part[b * X + i];
   dst[i] = s;
+}
+__global__ void __launch_bounds__(256) mamba_reduce_batch(const float* __restrict__ part, float* __restrict__ dst,
+                                                          int64_t B, int64_t X) {
+  reduce_batch(part, dst, B, X, blockIdx.x);
+}
+
+// The backward's three sums in one launch (each a few microseconds of work, so the launches
+// themselves were most of their time): blocks [0, nb_bc) the grad B_t / grad C_t sum over channel
+// tiles (reduce_bc_vec), the next nb_a blocks grad A over the batch, the rest grad Dp.
+template <typename TIO>
+__global__ void __launch_bounds__(256) mamba_reduce_all(const TIO* __restrict__ part, TIO* __restrict__ gBt,
+                                                        TIO* __restrict__ gCt, int64_t nT, int64_t BL, int NS,
+                                                        unsigned nb_bc, const float* __restrict__ gA_part,
+                                                        float* __restrict__ gA, const float* __restrict__ gDp_part,
+                                                        float* __restrict__ gDp, int64_t B, int64_t XA, int64_t XD,
+                                                        unsigned nb_a) {
+  if (blockIdx.x < nb_bc) {
+    reduce_bc_vec<TIO>(part, gBt, gCt, nT, BL, NS, blockIdx.x);
+  } else if (blockIdx.x - nb_bc < nb_a) {
+    reduce_batch(gA_part, gA, B, XA, blockIdx.x - nb_bc);
+  } else {
+    reduce_batch(gDp_part, gDp, B, XD, blockIdx.x - nb_bc - nb_a);
+  }
 }
 
 template <typename TIO, int NS>
@@ -868,9 +891,13 @@ int launch_bwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
   constexpr int V = 16 / sizeof(TIO);
   if (BLN > 0 && N == NS && NS % V == 0) {
     const int64_t items = B * L * (2 * NS / V);
-    hipLaunchKernelGGL((mamba_reduce_bc_vec<TIO>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, gBC_part,
-                       (TIO*)gBt, (TIO*)gCt, nT, B * L, NS);
-  } else if (BLN > 0) {
+    const unsigned nb_bc = (unsigned)((items + 255) / 256), nb_a = (unsigned)((D * N + 255) / 256),
+                   nb_d = (unsigned)((D + 255) / 256);
+    hipLaunchKernelGGL((mamba_reduce_all<TIO>), dim3(nb_bc + nb_a + nb_d), dim3(256), 0, s, gBC_part, (TIO*)gBt,
+                       (TIO*)gCt, nT, B * L, NS, nb_bc, gA_part, gA, gDp_part, gDp, B, D * N, D, nb_a);
+    return tsf_launch_status();
+  }
+  if (BLN > 0) {
     hipLaunchKernelGGL((mamba_reduce_bc<TIO>), dim3((unsigned)((BLN + 255) / 256)), dim3(256), 0, s, gBC_part,
                        (TIO*)gBt, (TIO*)gCt, nT, B * L, (int)N, NS);
   }
