@@ -693,8 +693,9 @@ void fwd_lb(int64_t lanes, int64_t L, const float* a, const float* w, const floa
   const LbPlan p = lb_plan(lanes, L, NA);
   double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
   double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-  hipLaunchKernelGGL((allpole_transfer2<NA>), transfer_grid(lanes, NA), dim3(64), 0, s, a, Mc, Ms, lanes, p.K);
-  lookback_reset_launch(ws, 2 * p.nsuper * lanes * NA, s);
+  const ResetJob rj = reset_job(ws, 2 * p.nsuper * lanes * NA, 64);
+  hipLaunchKernelGGL((allpole_transfer2<NA>), dim3(transfer_grid(lanes, NA).x + rj.blocks), dim3(64), 0, s, a, Mc, Ms,
+                     lanes, p.K, rj);
   const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(allpole_fwd_lb<NA>, 64 * p.K, occ);
   hipLaunchKernelGGL((allpole_fwd_lb<NA>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, a, w,
                      y0, y, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
@@ -711,8 +712,9 @@ void bwd_lb(int64_t lanes, int64_t L, const float* g, const float* a, const floa
   if (L > 0) {
     double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
     double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-    hipLaunchKernelGGL((allpole_transfer2<NA>), transfer_grid(lanes, NA), dim3(64), 0, s, a, Mc, Ms, lanes, p.K);
-    lookback_reset_launch(ws, 2 * p.nsuper * lanes * NA, s);
+    const ResetJob rj = reset_job(ws, 2 * p.nsuper * lanes * NA, 64);
+    hipLaunchKernelGGL((allpole_transfer2<NA>), dim3(transfer_grid(lanes, NA).x + rj.blocks), dim3(64), 0, s, a, Mc,
+                       Ms, lanes, p.K, rj);
     const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(allpole_bwd_lb<NA>, 64 * p.K, occ);
     hipLaunchKernelGGL((allpole_bwd_lb<NA>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, a, g,
                        y, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),

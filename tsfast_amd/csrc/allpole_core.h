@@ -204,10 +204,15 @@ TSF_DEV void companion_powers_col(const float* __restrict__ arow, double* __rest
 }
 
 // Both transfer matrices per lane ([lanes][NA][NA] each), a [lanes, NA].
-// One thread per (lane, column).
+// One thread per (lane, column); the last rj.blocks workgroups run the scan's look-back reset.
 template <int NA>
 __global__ void __launch_bounds__(64) allpole_transfer2(const float* __restrict__ a, double* __restrict__ Mc,
-                                                        double* __restrict__ Ms, int64_t lanes, int K) {
+                                                        double* __restrict__ Ms, int64_t lanes, int K, ResetJob rj) {
+  const unsigned tb = gridDim.x - rj.blocks;
+  if (blockIdx.x >= tb) {
+    run_reset(rj, blockIdx.x - tb);
+    return;
+  }
   const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (idx >= lanes * NA) return;
   const int64_t lane = idx / NA;

@@ -124,11 +124,17 @@ TSF_DEV void load_pair_coeffs(double (&av)[NA], float (&bk)[NBT], const float* _
 }
 
 // Transfer matrices per lane from its pair's coefficients a [O, I, NA] (lane = b * Pp + j * O + o;
-// padding lanes take pair 0's). One thread per (lane, column).
+// padding lanes take pair 0's). One thread per (lane, column); the last rj.blocks workgroups run
+// the scan's look-back reset.
 template <int NA>
 __global__ void __launch_bounds__(64) gblock_transfer(const float* __restrict__ acoef, double* __restrict__ Mc,
                                                       double* __restrict__ Ms, int64_t lanes, int I, int O, int Pp,
-                                                      int K) {
+                                                      int K, ResetJob rj) {
+  const unsigned tb = gridDim.x - rj.blocks;
+  if (blockIdx.x >= tb) {
+    run_reset(rj, blockIdx.x - tb);
+    return;
+  }
   const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (idx >= lanes * NA) return;
   const int64_t lane = idx / NA;
@@ -767,9 +773,9 @@ void fwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
   static int occ[kMaxNA + 1];
   double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
   double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-  hipLaunchKernelGGL((gblock_transfer<NA>), transfer_grid(p.lanes, NA), dim3(64), 0, s, acoef, Mc, Ms, p.lanes, I, O,
-                     p.pp, p.lb.K);
-  lookback_reset_launch(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, s);
+  const ResetJob rj = reset_job(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, 64);
+  hipLaunchKernelGGL((gblock_transfer<NA>), dim3(transfer_grid(p.lanes, NA).x + rj.blocks), dim3(64), 0, s, acoef, Mc,
+                     Ms, p.lanes, I, O, p.pp, p.lb.K, rj);
   const int64_t tiles = p.lb.groups * p.lb.nsuper, cap = resident_wgs(gblock_fwd_lb<NA, NBT>, 64 * p.lb.K, occ);
   hipLaunchKernelGGL((gblock_fwd_lb<NA, NBT>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.lb.K), 0, s, u,
                      bcoef, acoef, u_tail, x0, y, x_last, saved, (const double*)Mc, (const double*)Ms,
@@ -790,9 +796,9 @@ void bwd_impl(const GbPlan& p, int64_t B, int64_t L, int I, int O, int nb, const
   if (L > 0) {
     double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
     double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-    hipLaunchKernelGGL((gblock_transfer<NA>), transfer_grid(p.lanes, NA), dim3(64), 0, s, acoef, Mc, Ms, p.lanes, I, O,
-                       p.pp, p.lb.K);
-    lookback_reset_launch(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, s);
+    const ResetJob rj = reset_job(ws, p.lb.nsuper * p.lanes * 2 * NA * 2, 64);
+    hipLaunchKernelGGL((gblock_transfer<NA>), dim3(transfer_grid(p.lanes, NA).x + rj.blocks), dim3(64), 0, s, acoef, Mc,
+                       Ms, p.lanes, I, O, p.pp, p.lb.K, rj);
     const int64_t tiles = p.lb.groups * p.lb.nsuper, cap = resident_wgs(gblock_bwd_lb<NA, NBT>, 64 * p.lb.K, occ);
     hipLaunchKernelGGL((gblock_bwd_lb<NA, NBT>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.lb.K), 0, s,
                        gy, g_xlast, u, bcoef, acoef, u_tail, x0, saved, (const double*)Mc, (const double*)Ms,

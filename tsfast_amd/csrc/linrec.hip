@@ -49,9 +49,16 @@ constexpr int steps_per_chunk() {
 // fp64. (Repeated squaring would compound rounding errors through the transient growth of
 // non-normal powers, which for companion matrices with poles near the unit circle reach 1e5
 // before they decay; step-by-step application keeps them at the level of the recurrence itself.)
+// The last rj.blocks workgroups run the scan's look-back reset instead.
 template <int NS>
 __global__ void __launch_bounds__(256) linrec_transfer(const float* __restrict__ A, double* __restrict__ Mc,
-                                                       double* __restrict__ Ms, int64_t lanes, int K, int transpose) {
+                                                       double* __restrict__ Ms, int64_t lanes, int K, int transpose,
+                                                       ResetJob rj) {
+  const unsigned tb = gridDim.x - rj.blocks;
+  if (blockIdx.x >= tb) {
+    run_reset(rj, blockIdx.x - tb);
+    return;
+  }
   const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (idx >= lanes * NS) return;
   const int64_t lane = idx / NS;
@@ -506,8 +513,9 @@ int fwd_impl(int64_t lanes, int64_t L, const float* A, const float* v, const flo
   const LrPlan p = lr_plan(lanes, L, NS);
   double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
   double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
-  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes * NS)), dim3(256), 0, s, A, Mc, Ms, lanes, p.K, 0);
-  lookback_reset_launch(ws, 2 * p.nsuper * lanes * NS, s);
+  const ResetJob rj = reset_job(ws, 2 * p.nsuper * lanes * NS, 256);
+  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes * NS) + rj.blocks), dim3(256), 0, s, A, Mc, Ms, lanes,
+                     p.K, 0, rj);
   const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(linrec_fwd_lb<NS>, 64 * p.K, occ);
   hipLaunchKernelGGL((linrec_fwd_lb<NS>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, A, v, x0,
                      x, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),
@@ -529,8 +537,9 @@ int bwd_impl(int64_t lanes, int64_t L, const float* g, const float* A, const flo
   double* Mc = reinterpret_cast<double*>(ws + p.off_Mc);
   double* Ms = reinterpret_cast<double*>(ws + p.off_Ms);
   double* part = reinterpret_cast<double*>(ws + p.off_part);
-  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes * NS)), dim3(256), 0, s, A, Mc, Ms, lanes, p.K, 1);
-  lookback_reset_launch(ws, 2 * p.nsuper * lanes * NS, s);
+  const ResetJob rj = reset_job(ws, 2 * p.nsuper * lanes * NS, 256);
+  hipLaunchKernelGGL((linrec_transfer<NS>), dim3(blocks_for(lanes * NS) + rj.blocks), dim3(256), 0, s, A, Mc, Ms, lanes,
+                     p.K, 1, rj);
   const int64_t tiles = p.groups * p.nsuper, cap = resident_wgs(linrec_bwd_lb<NS>, 64 * p.K, occ);
   hipLaunchKernelGGL((linrec_bwd_lb<NS>), dim3((unsigned)(tiles < cap ? tiles : cap)), dim3(64 * p.K), 0, s, A, g, out,
                      x0, gv, gx0, (const double*)Mc, (const double*)Ms, reinterpret_cast<double*>(ws + p.off_agg),

@@ -101,18 +101,28 @@ TSF_DEV unsigned take_tile(unsigned* counter) {
 
 // Resets the look-back words to kUnset and the tile counter to zero before every scan (a
 // kernel rather than a memset node, so that a captured graph replays it reliably).
-__global__ void __launch_bounds__(256) lookback_reset(uint64_t* __restrict__ words, int64_t n,
-                                                      unsigned* __restrict__ counter, unsigned* alarm,
-                                                      uint32_t epoch) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) words[i] = kUnset;
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    counter[0] = 0u;
-    counter[kErrWord] = 0u;
-    counter[kEpochWord] = epoch;
-    *reinterpret_cast<uint64_t*>(counter + kAlarmWord) = reinterpret_cast<uint64_t>(alarm);
+// A reset as a job of `blocks` workgroups: lookback_reset runs it alone, and a kernel launched
+// right before a scan (the transfer-matrix kernels) can run it in extra workgroups of its own
+// launch, which saves a launch per scan call.
+struct ResetJob {
+  uint64_t* words;
+  int64_t n;
+  unsigned* counter;
+  unsigned* alarm;
+  uint32_t epoch;
+  unsigned blocks;
+};
+TSF_DEV void run_reset(const ResetJob& r, unsigned block) {
+  const int64_t stride = (int64_t)r.blocks * blockDim.x;
+  for (int64_t i = block * (int64_t)blockDim.x + threadIdx.x; i < r.n; i += stride) r.words[i] = kUnset;
+  if (block == 0 && threadIdx.x == 0) {
+    r.counter[0] = 0u;
+    r.counter[kErrWord] = 0u;
+    r.counter[kEpochWord] = r.epoch;
+    *reinterpret_cast<uint64_t*>(r.counter + kAlarmWord) = reinterpret_cast<uint64_t>(r.alarm);
   }
 }
+__global__ void __launch_bounds__(256) lookback_reset(ResetJob r) { run_reset(r, blockIdx.x); }
 
 
 // Host side. A workspace starts with the tile counter (kCounterBytes), followed by the published
@@ -137,11 +147,17 @@ inline LbCfg lb_spacing_for(int deterministic_spacing) {
   return LbCfg{tsf_deterministic() ? deterministic_spacing : 0, tsf_lookback_spin_limit()};
 }
 
-void lookback_reset_launch(char* ws, int64_t words, hipStream_t s) {
-  int64_t blocks = (words + 255) / 256;
+// The reset of a scan call's workspace (the tile counter, then `words` published words) as a job
+// of workgroups of `threads` threads (at most 2^19 threads in all, striding over the words).
+inline ResetJob reset_job(char* ws, int64_t words, int threads) {
+  int64_t blocks = (words + threads - 1) / threads;
+  const int64_t cap = (int64_t)(1 << 19) / threads;
   if (blocks < 1) blocks = 1;
-  if (blocks > 2048) blocks = 2048;
-  hipLaunchKernelGGL(lookback_reset, dim3((unsigned)blocks), dim3(256), 0, s,
-                     reinterpret_cast<uint64_t*>(ws + kCounterBytes), words, reinterpret_cast<unsigned*>(ws),
-                     tsf_lookback_alarm(), tsf_next_epoch());
+  if (blocks > cap) blocks = cap;
+  return ResetJob{reinterpret_cast<uint64_t*>(ws + kCounterBytes), words, reinterpret_cast<unsigned*>(ws),
+                  tsf_lookback_alarm(), tsf_next_epoch(), (unsigned)blocks};
+}
+void lookback_reset_launch(char* ws, int64_t words, hipStream_t s) {
+  const ResetJob r = reset_job(ws, words, 256);
+  hipLaunchKernelGGL(lookback_reset, dim3(r.blocks), dim3(256), 0, s, r);
 }
