@@ -163,9 +163,9 @@ def test_gblock_bitwise_repeatable(gpu):
 def test_projected_scan_repeatable(gpu):
     """Every output and gradient is bitwise repeatable: y and the returned state from the fused
     forward's anchored look-back, and all seven gradients from the backward, which in this mode
-    differentiates the three-step composition (the fused backward's parameter gradients are
-    sums a workgroup accumulates over the tiles it takes from a counter, whose order depends on
-    timing). The deterministic gradients also agree with the fused backward's to 1e-5."""
+    recomputes the states and runs the wide route's backward (the fused backward's parameter
+    gradients are sums a workgroup accumulates over the tiles it takes from a counter, whose order
+    depends on timing). The deterministic gradients also agree with the fused backward's to 1e-5."""
     g = torch.Generator().manual_seed(6)
     B, L, H, N, O = 4, 8192, 32, 256, 32
     u = torch.randn(B, L, H, generator=g)
@@ -174,11 +174,12 @@ def test_projected_scan_repeatable(gpu):
     C_re, C_im = torch.randn(O, N, generator=g) / 16, torch.randn(O, N, generator=g) / 16
     gy = torch.randn(B, L, O, generator=g)
     x0 = torch.randn(B, N, dtype=torch.complex64, generator=g)
-    ins = [t.to(gpu) for t in (u, W_re, W_im, lam, C_re, C_im, x0, gy)]
+    gxl = torch.randn(B, N, dtype=torch.complex64, generator=g)
+    ins = [t.to(gpu) for t in (u, W_re, W_im, lam, C_re, C_im, x0, gy, gxl)]
 
-    def call(u, W_re, W_im, lam, C_re, C_im, x0, gy):
+    def call(u, W_re, W_im, lam, C_re, C_im, x0, gy, gxl):
         y, x_last, saved = projected_hip._scan_train_op(u, W_re, W_im, lam, C_re, C_im, x0)
-        return (y, x_last, *projected_hip.backward(gy, None, saved, u, W_re, W_im, lam, C_re, C_im, x0))
+        return (y, x_last, *projected_hip.backward(gy, gxl, saved, u, W_re, W_im, lam, C_re, C_im, x0))
 
     fused = _default_mode(call, *ins)  # the fused backward kernel
     noise = torch.randn(1 << 22, device=gpu)
@@ -191,7 +192,7 @@ def test_projected_scan_repeatable(gpu):
     _assert_same(outs)
     for i, (a, b) in enumerate(zip(outs[0], fused)):
         if b.numel():
-            assert ((a - b).abs().max() / b.abs().max()).item() < 1e-5, f"output {i}: composition vs fused"
+            assert ((a - b).abs().max() / b.abs().max()).item() < 1e-5, f"output {i}: deterministic vs fused"
 
 
 def test_projected_wide_route_bitwise_repeatable(gpu):

@@ -109,3 +109,22 @@ def test_wide_route_empty_sequence(oracle_scan):
     grads = projected_hip._wide_backward(gy, g_xl, x, u, W_re, W_im, lam, C_re, C_im, x0)
     assert torch.equal(grads[6], g_xl)
     assert all(not t.any() for t in grads[1:6])
+
+
+@pytest.mark.parametrize("with_x0", [True, False])
+def test_deterministic_backward_matches_oracle(oracle_scan, with_x0):
+    """The backward used under torch.use_deterministic_algorithms recomputes the states with the
+    wide route and runs its backward: the same seven gradients as the oracle's."""
+    u, W_re, W_im, lam, C_re, C_im, x0, gy, g_xl = _make(2, 37, 6, 10, 5, seed=4)
+    x0 = x0 if with_x0 else None
+    got = projected_hip._deterministic_bwd(gy, g_xl, u, W_re, W_im, lam, C_re, C_im, x0)
+    _, want_x = O.projscan_forward(*(t.numpy() if t is not None else None for t in (u, W_re, W_im, lam, C_re, C_im, x0)))
+    want = O.projscan_backward(
+        gy.numpy(), g_xl.numpy(), u.numpy(), W_re.numpy(), W_im.numpy(), lam.numpy(), C_re.numpy(), C_im.numpy(),
+        want_x, None if x0 is None else x0.numpy(),
+    )
+    for name, gg, gw in zip(("g_u", "g_W_re", "g_W_im", "g_lam", "g_C_re", "g_C_im", "g_x0"), got, want):
+        if gw is None:
+            assert gg.numel() == 0, name
+        else:
+            assert O.rel_err(gg.numpy(), gw) < 1e-5, name

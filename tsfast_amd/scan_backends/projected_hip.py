@@ -145,36 +145,15 @@ def _(u, W_re, W_im, lam, C_re, C_im, x0):
     return _fake_outs(u, lam, C_re, train=True)
 
 
-def _composition_bwd(gy, g_xlast, u, W_re, W_im, lam, C_re, C_im, x0):
-    """Every gradient of the projected scan through the three-step composition
-    ``complex_in_proj -> diagonal_recurrence -> real_out_proj`` (the reference's own formulation,
-    ``models/_core/scan.py:221-243, 272-313``), differentiated by autograd. Used under
-    ``torch.use_deterministic_algorithms(True)``: the fused backward adds its parameter gradients
-    (grad W, grad lam, grad C) per workgroup over the tiles the workgroup takes from a counter,
-    and which tiles those are depends on timing, while the composition's GEMMs and the diagonal
-    scan's anchored look-back give the same bits on every run."""
-    from ..scan import complex_in_proj, diagonal_recurrence, real_out_proj
-
-    B, L, _ = u.shape
-    if L == 0:
-        zeros = [torch.zeros_like(t) for t in (u, W_re, W_im, lam, C_re, C_im)]
-        g_x0 = lam.new_empty(0)
-        if x0 is not None:
-            g_x0 = g_xlast.clone() if g_xlast is not None else torch.zeros_like(x0)
-        return (*zeros, g_x0)
-    with torch.enable_grad():
-        leaves = [t.detach().requires_grad_() for t in (u, W_re, W_im, lam, C_re, C_im)]
-        if x0 is not None:
-            leaves.append(x0.detach().requires_grad_())
-        x = diagonal_recurrence(leaves[3], complex_in_proj(leaves[0], leaves[1], leaves[2]),
-                                leaves[6] if x0 is not None else None)
-        outs, ups = [real_out_proj(x, leaves[4], leaves[5])], [gy]
-        if g_xlast is not None:
-            outs.append(x[:, -1, :])
-            ups.append(g_xlast)
-        grads = torch.autograd.grad(outs, leaves, ups, allow_unused=True)
-    grads = [torch.zeros_like(t) if g is None else g for g, t in zip(grads, leaves)]
-    return (*grads[:6], grads[6] if x0 is not None else lam.new_empty(0))
+def _deterministic_bwd(gy, g_xlast, u, W_re, W_im, lam, C_re, C_im, x0):
+    """Every gradient of the projected scan through the wide route: the states recomputed by one
+    GEMM and the diagonal scan kernels, then ``_wide_backward`` (GEMMs, the adjoint scan kernels and
+    the fixed-order split-K weight sums). Used under ``torch.use_deterministic_algorithms(True)``:
+    the fused backward adds its parameter gradients (grad W, grad lam, grad C) per workgroup over
+    the tiles the workgroup takes from a counter, and which tiles those are depends on timing,
+    while every step here gives the same bits on every run (the diagonal scan's look-back is
+    anchored in this mode)."""
+    return _wide_backward(gy, g_xlast, _wide_states(u, W_re, W_im, lam, x0), u, W_re, W_im, lam, C_re, C_im, x0)
 
 
 @torch.library.custom_op("tsfast_hip::projected_scan_bwd", mutates_args=())
@@ -225,10 +204,10 @@ def _(gy, g_xlast, saved, u, W_re, W_im, lam, C_re, C_im, x0):
 def backward(gy, g_xlast, saved, u, W_re, W_im, lam, C_re, C_im, x0):
     """Every gradient of the projected scan: ``(g_u, g_W_re, g_W_im, g_lam, g_C_re, g_C_im,
     g_x0)`` (``g_x0`` empty when ``x0`` is None). The fused backward kernel, or under
-    ``torch.use_deterministic_algorithms(True)`` the composition's autograd
-    (``_composition_bwd``), whose bits do not depend on timing."""
+    ``torch.use_deterministic_algorithms(True)`` the wide route's recompute and backward
+    (``_deterministic_bwd``), whose bits do not depend on timing."""
     if torch.are_deterministic_algorithms_enabled():
-        return _composition_bwd(*_dense(gy, g_xlast, u, W_re, W_im, lam, C_re, C_im, x0))
+        return _deterministic_bwd(*_dense(gy, g_xlast, u, W_re, W_im, lam, C_re, C_im, x0))
     return _scan_bwd_op(gy, g_xlast, saved, u, W_re, W_im, lam, C_re, C_im, x0)
 
 
@@ -293,6 +272,14 @@ def _fresh(t):
     return t.clone(memory_format=torch.contiguous_format)
 
 
+def _wide_states(u, W_re, W_im, lam, x0):
+    """The states x [B, L, N] (B L > 0): v by one GEMM, then the diagonal scan kernels."""
+    B, L, _ = u.shape
+    N = lam.shape[0]
+    v = torch.view_as_complex(F.linear(u, _w_cat(W_re, W_im)).view(B, L, N, 2))
+    return diagonal_hip.forward(lam.expand(B, N).contiguous(), v, x0)
+
+
 def _wide_forward(u, W_re, W_im, lam, C_re, C_im, x0):
     """``(y, x_last, x)``: v by one GEMM, the states by the diagonal scan kernels, y by one GEMM."""
     B, L, H = u.shape
@@ -300,9 +287,7 @@ def _wide_forward(u, W_re, W_im, lam, C_re, C_im, x0):
     if B * L == 0:
         x_last = x0.clone() if x0 is not None else lam.new_zeros(B, N)
         return u.new_zeros(B, L, O), x_last, lam.new_empty(B, L, N)
-    v = torch.view_as_complex(F.linear(u, _w_cat(W_re, W_im)).view(B, L, N, 2))
-    x = diagonal_hip.forward(lam.expand(B, N).contiguous(), v, x0)
-    del v
+    x = _wide_states(u, W_re, W_im, lam, x0)
     y = F.linear(torch.view_as_real(x).view(B, L, 2 * N), _c_cat(C_re, C_im))
     return y, _fresh(x[:, -1]), x
 
