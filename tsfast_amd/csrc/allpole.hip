@@ -330,18 +330,25 @@ __global__ void __launch_bounds__(kTile) allpole_bwd_apply(const float* __restri
   const int64_t t0 = c * T_c;
   const int64_t len = (L - t0) < T_c ? (L - t0) : T_c;
   const int64_t last = ((len - 1) / kTileT) * kTileT;
+  // Above order 8 the next tile is not prefetched during the recurrence: its 64 registers would
+  // take the kernel to one wave per SIMD.
+  constexpr bool kPf = NA <= 8;
   TileRegs rgg, rgy;
-  {
+  if (kPf) {
     const int n0 = (int)((len - last) < kTileT ? (len - last) : kTileT);
     tile_fetch(rgg, g, lanes, L, l0, t0 + last, n0, tid);
     tile_fetch(rgy, y, lanes, L, l0, t0 + last, n0, tid);
   }
   for (int64_t tt = last; tt >= 0; tt -= kTileT) {
     const int n = (int)((len - tt) < kTileT ? (len - tt) : kTileT);
+    if (!kPf) {
+      tile_fetch(rgg, g, lanes, L, l0, t0 + tt, n, tid);
+      tile_fetch(rgy, y, lanes, L, l0, t0 + tt, n, tid);
+    }
     tile_put(rgg, tg, tid);
     tile_put(rgy, ty, tid);
     __syncthreads();
-    if (tt > 0) {
+    if (kPf && tt > 0) {
       tile_fetch(rgg, g, lanes, L, l0, t0 + tt - kTileT, kTileT, tid);
       tile_fetch(rgy, y, lanes, L, l0, t0 + tt - kTileT, kTileT, tid);
     }

@@ -40,13 +40,20 @@ struct TileRegs {
   float v[kTile / 2];
 };
 // `lid` is the thread's lane within its wave (the tile belongs to one wave).
+// The row pointer starts from a per-thread base that passes through an empty asm and steps by two
+// rows per access, so the compiler cannot hoist the 32 row addresses (64 VGPRs per matrix) out of
+// a kernel's tile loop.
 TSF_DEV void tile_fetch(TileRegs& rg, const float* __restrict__ src, int64_t lanes, int64_t L, int64_t l0, int64_t c0,
                         int ncol, int lid) {
   const int col = lid & (kTileT - 1), half = lid >> 5;
+  const float* p = src + ((l0 + half) * L + c0 + col);
+  asm volatile("" : "+v"(p));
+  const bool cok = col < ncol;
 #pragma unroll
   for (int r2 = 0; r2 < kTile / 2; ++r2) {
     const int64_t lane = l0 + 2 * r2 + half;
-    rg.v[r2] = (lane < lanes && col < ncol) ? src[lane * L + c0 + col] : 0.0f;
+    rg.v[r2] = (lane < lanes && cok) ? *p : 0.0f;
+    p += 2 * L;
   }
 }
 TSF_DEV void tile_put(const TileRegs& rg, float (*tile)[kTileT + 1], int lid) {
@@ -57,11 +64,14 @@ TSF_DEV void tile_put(const TileRegs& rg, float (*tile)[kTileT + 1], int lid) {
 TSF_DEV void tile_store(float (*tile)[kTileT + 1], float* __restrict__ dst, int64_t lanes, int64_t L, int64_t l0,
                         int64_t c0, int ncol, int lid) {
   const int col = lid & (kTileT - 1), half = lid >> 5;
+  float* p = dst + ((l0 + half) * L + c0 + col);
+  asm volatile("" : "+v"(p));
 #pragma unroll 8
   for (int r2 = 0; r2 < kTile / 2; ++r2) {
     const int r = 2 * r2 + half;
     const int64_t lane = l0 + r;
-    if (lane < lanes && col < ncol) dst[lane * L + c0 + col] = tile[r][col];
+    if (lane < lanes && col < ncol) *p = tile[r][col];
+    p += 2 * L;
   }
 }
 
