@@ -2,7 +2,8 @@
 
 The oracle (oracle/scan_oracle.py::gblock_forward/backward) is pinned against float64 autograd
 through the reference's own formulation (grouped conv1d, a sequential all-pole loop, the sum
-over inputs; tests/test_oracle.py). Shapes cover every tap padding (nb 1..16 -> 2, 4, 8, 16),
+over inputs; tests/test_oracle.py). Shapes cover every tap padding of the fused kernels (nb 1..16 -> 2, 4, 8, 16; 9..16 taps through
+the op itself, since the operator stages them),
 every order na 1..4, pair counts that divide 64 (64 / (I*O) batch rows per tile) and that do
 not (a batch row padded to the next power of two: 3, 15, 24 and 40 pairs), more than 64 pairs
 (run as groups of inputs, and of outputs past 64), sequences shorter than na and than one chunk,
@@ -98,11 +99,24 @@ _SHAPES = [
 @pytest.mark.parametrize("with_state", [True, False])
 @pytest.mark.parametrize("shape", _SHAPES)
 def test_gblock_matches_oracle(gpu, shape, with_state):
+    _check_against_oracle(gpu, shape, with_state, gblock_hip.run)
+
+
+# 9..16 taps take the staged path in gblock_hip.run (faster there than the fused kernels' 16-tap
+# instances); C callers reach the fused kernels with them, so they are checked through the op
+@pytest.mark.parametrize("with_state", [True, False])
+@pytest.mark.parametrize("shape", [(2, 5000, 4, 4, 16, 4), (2, 5000, 3, 5, 16, 4), (3, 700, 2, 4, 12, 3)])
+def test_gblock_fused_kernel_wide_taps_matches_oracle(gpu, shape, with_state):
+    assert not gblock_hip._fused(shape[5], shape[4])
+    _check_against_oracle(gpu, shape, with_state, lambda *ts: gblock_hip._gblock_op(*ts)[:2])
+
+
+def _check_against_oracle(gpu, shape, with_state, call):
     B, L, I, O_, nb, na = shape
     u, b, a, ut, x0, gy, gxl = _make(*shape, seed=sum(shape), with_state=with_state)
     ts = [t.to(gpu).requires_grad_() if t is not None else None for t in (u, b, a, ut, x0)]
     assert gblock_hip.supports(*ts) is None
-    y, x_last = gblock_hip.run(*ts)
+    y, x_last = call(*ts)
     torch.autograd.backward([y, x_last], [gy.to(gpu), gxl.to(gpu)])
     z = lambda t, shp: np.zeros(shp) if t is None else _np(t)  # noqa: E731
     args = (_np(u), _np(b), _np(a), z(ut, (B, nb - 1, I)), z(x0, (B, I * O_, na)))

@@ -12,10 +12,10 @@ outputs from per-super-chunk states the forward saves (a few MB).
 ``dynonet_gblock_bwd`` custom ops. Shapes follow the reference: ``u [B, L, I]``, ``b_coeff
 [O, I, nb]``, ``a_coeff [O, I, na]``, ``u_tail [B, nb-1, I]``, ``x0 [B, I*O, na]`` (pairs input-major,
 newest first); ``y [B, L, O]``, ``x_last [B, I*O, na]``. float32, any number of channel pairs.
-Orders ``na <= 4`` with ``nb <= 16`` run the fused kernels: one launch per direction serves up to
+Orders ``na <= 4`` with ``nb <= 8`` run the fused kernels: one launch per direction serves up to
 64 pairs (a batch row's pairs padded to a power of two inside the kernels); a larger block runs as
 groups of whole inputs (and, past 64 outputs, of outputs) of at most 64 pairs each, whose outputs
-and gradients add up. Orders ``5 <= na <= 16`` (or ``nb`` up to 64) run the three stages on this
+and gradients add up. Orders ``5 <= na <= 16`` (or ``9 <= nb <= 64``) run the three stages on this
 library's kernels: the FIR stage (``tsfast_hip::dynonet_fir``, writing ``w`` in the all-pole lane
 layout), the all-pole op on the pair lanes (``allpole_hip``), and a sum over inputs.
 """
@@ -29,7 +29,7 @@ import torch
 from .. import _lib
 
 _MAX_NA = 4  # orders of the fused kernels
-_MAX_NB = 16
+_MAX_NB = 8  # taps the operator fuses (the kernels take up to 16; 9..16 ran 1.5x slower than staged)
 _MAX_PAIRS = 64  # pairs one launch serves (a tile of 64 lanes holds whole batch rows)
 _MAX_NA_STAGED = 16  # orders of the staged path (the all-pole kernels' range)
 _MAX_NB_STAGED = 64  # taps of the FIR kernel
