@@ -63,7 +63,9 @@ def _run_hip(t, gout, ghlast, dev, use_ghlast):
 @pytest.mark.parametrize(
     "B,L,D,N",
     [(4, 50, 32, 16), (2, 33, 16, 8), (1, 7, 8, 32), (2, 64, 20, 16), (2, 40, 24, 12), (3, 100, 130, 4),
-     (2, 37, 70, 64), (2, 16, 64, 1)],
+     (2, 37, 70, 64), (2, 16, 64, 1),
+     # from 32 states the backward takes 16-channel tiles: several whole tiles, and a partial one
+     (2, 75, 48, 32), (1, 130, 40, 20)],
 )
 @pytest.mark.parametrize("io", ["fp32", "bf16"])
 @pytest.mark.parametrize("with_h0,use_ghlast", [(True, True), (False, False)])

@@ -28,8 +28,9 @@
 //        G_t = gy_t C_t + lam_{t+1} G_{t+1}
 //    backwards through the chunk, so exp is evaluated once per element per pass; the gate
 //    gradient reads the forward's saved pre-gate output y instead of recomputing sum_n h C.
-//  * grad B_t / grad C_t (sums over channels) are reduced over the 32 channels of the tile in
-//    LDS and written as partials [D/32, B, L, 2*NS] in the I/O type (the reference keeps its
+//  * grad B_t / grad C_t (sums over channels) are reduced over the channels of the tile (32; 16
+//    in the backward from N = 32, see bwd_dt) in LDS and written as partials [D/DT, B, L, 2*NS]
+//    in the I/O type (the reference keeps its
 //    per-block partials in the I/O dtype too); a second kernel sums the partials in fp32 in a
 //    fixed order (no atomics: deterministic run to run).
 // The next chunk's inputs are loaded into registers while the current chunk computes.
@@ -847,12 +848,20 @@ int launch_fwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
 // the grad-B/C partials, measured 16% slower at config 3: with one workgroup per CU nothing runs
 // while its waves wait at the chunk barriers.)
 constexpr int kBwdDT = TSF_MAMBA_BWD_DT;
+// From 32 states a launch takes 16-channel tiles: at 32 channels their per-chunk LDS (86 KB at
+// N = 32) fits one workgroup per CU, one wave per SIMD; at 16 channels two (backward -13% at
+// N = 32, -12% at N = 64 on config 3's B, L, D). At N = 16 the 32-channel tile stays faster
+// (the narrower tile doubles the grad-B/C partials; +10%).
+template <int NS>
+constexpr int bwd_dt() {
+  return NS >= 32 ? 16 : kBwdDT;
+}
 
 // Backward workspace: grad-B/C partials [nT, B, L, 2*NS] in the I/O type (padded to 256 bytes),
 // then the fp32 per-row partials of gA [B, D, N] and gDp [B, D].
 template <int NS>
 int64_t bwd_partial_bytes(int64_t B, int64_t L, int64_t D, int64_t esz) {
-  const int64_t nT = (D + kBwdDT - 1) / kBwdDT;
+  const int64_t nT = (D + bwd_dt<NS>() - 1) / bwd_dt<NS>();
   return (nT * B * L * 2 * NS * esz + 255) / 256 * 256;
 }
 template <int NS>
@@ -880,12 +889,12 @@ int launch_bwd(int64_t B, int64_t L, int64_t D, int64_t N, const void* draw, con
                float* gDp, float* gh0, void* workspace, hipStream_t s) {
   using C = MCfg<NS>;
   const int64_t NC = (L + C::CHK - 1) / C::CHK;
-  const int64_t nT = (D + kBwdDT - 1) / kBwdDT;
+  const int64_t nT = (D + bwd_dt<NS>() - 1) / bwd_dt<NS>();
   TIO* gBC_part = static_cast<TIO*>(workspace);
   float* gA_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + bwd_partial_bytes<NS>(B, L, D, sizeof(TIO)));
   float* gDp_part = gA_part + B * D * N;
   if (B > 0 && D > 0)
-    launch_bwd_tile<TIO, NS, kBwdDT>(B, L, D, N, NC, draw, A, Bt, Ct, u, z, Dp, h0, chk, gout, ghlast, gdraw, gu, gz,
+    launch_bwd_tile<TIO, NS, bwd_dt<NS>()>(B, L, D, N, NC, draw, A, Bt, Ct, u, z, Dp, h0, chk, gout, ghlast, gdraw, gu, gz,
                                      gA_part, gDp_part, gBC_part, gh0, s);
   const int64_t BLN = B * L * N;
   constexpr int V = 16 / sizeof(TIO);
@@ -1048,9 +1057,10 @@ int tsfast_hip_mamba_bwd(int64_t B, int64_t L, int64_t D, int64_t N, int io_dtyp
                          float* gA, void* gBt, void* gCt, void* gu, void* gz, float* gDp, float* gh0, void* workspace,
                          int64_t workspace_bytes, void* stream) {
   if (B < 0 || L < 0 || D < 0 || N < 1) return TSF_ERR_ARG;
-  if ((D + 31) / 32 * B > INT32_MAX) return TSF_ERR_UNSUPPORTED;  // one-dimensional grid
   const int ns = ns_for(N);
   if (ns == 0) return TSF_ERR_UNSUPPORTED;
+  const int64_t dt = ns >= 32 ? bwd_dt<32>() : kBwdDT;  // the backward's channel tile
+  if ((D + dt - 1) / dt * B > INT32_MAX) return TSF_ERR_UNSUPPORTED;  // one-dimensional grid
   if (!A || !Dp || !gA || !gDp) return TSF_ERR_ARG;
   if (L > 0 && (!draw || !Bt || !Ct || !u || !z || !gout || !gdraw || !gBt || !gCt || !gu || !gz)) return TSF_ERR_ARG;
   if (h0 && !gh0) return TSF_ERR_ARG;

@@ -92,8 +92,9 @@ def supports(draw, A, Bt, Ct, u, z, Dp, h0) -> str | None:
         return f"A.shape {tuple(A.shape)} incompatible with draw {tuple(draw.shape)}"
     if N < 1:
         return f"state size N={N} below 1"
-    if -(-D // 32) * B > 2**31 - 1:
-        return f"{B} batch rows x {-(-D // 32)} channel tiles exceed the kernels' one-dimensional grid"
+    dt = 16 if min(N, _MAX_N) > 16 else 32  # the backward's channel tile (the forward's is 32)
+    if -(-D // dt) * B > 2**31 - 1:
+        return f"{B} batch rows x {-(-D // dt)} channel tiles exceed the kernels' one-dimensional grid"
     if not _rows_fit(L, D, min(N, _MAX_N)):
         return f"one batch row (L={L}, D={D}, N={N}) exceeds the kernels' 2 GiB per-row addressing"
     if tuple(u.shape) != (B, L, D) or tuple(z.shape) != (B, L, D):
