@@ -720,6 +720,13 @@ void bwd_reg(int vec, int64_t B, int64_t L, int64_t D, const void* x, int64_t sx
     launch_bwd<TIO, K, 1>(B, L, D, x, sxb, sxl, sxd, tail, w, bias, gy, gx, gtail, gw, gb, part, s);
 }
 
+// fp32 I/O from this many taps takes the LDS-tiled backward (the bf16 kernels' family) instead of
+// the register-tile one, whose 6- to 8-tap instances run one wave per SIMD: at B 16, L 4096,
+// D 1536 the tiled backward measured 264 / 272 / 285 us at K 5 / 6 / 8 against 287 / 364 /
+// 430 us, and 262 / 273 us against 250 / 264 us at K 3 / 4.
+#ifndef TSF_CONV_F32_TILED_K
+#define TSF_CONV_F32_TILED_K 5
+#endif
 #define TSF_CONV_K_SWITCH(K, CALL) \
   switch (K) {                     \
     case 2: CALL(2); break;        \
@@ -806,7 +813,12 @@ int tsfast_hip_conv_silu_bwd(int64_t B, int64_t L, int64_t D, int64_t K, int io_
   }
   if (const int st = conv_layout_status(L, D, sxl, sxd, io_dtype == TSF_DTYPE_BF16 ? 2 : 4)) return st;
   float* part = static_cast<float*>(workspace);
-  if (io_dtype == TSF_DTYPE_F32) {
+  if (io_dtype == TSF_DTYPE_F32 && K >= TSF_CONV_F32_TILED_K) {
+    const bool vec = vec_rows<float>(x, D, sxb, sxl, sxd, gy, gx);
+#define CALL(KK) bwd_k<float, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, gy, gx, gtail, gw, gb, part, s)
+    TSF_CONV_K_SWITCH(K, CALL)
+#undef CALL
+  } else if (io_dtype == TSF_DTYPE_F32) {
     const int vec = vec_for<float>(x, D, sxb, sxl, sxd, gy) == 4 && ((uintptr_t)gx % 16 == 0) ? 4 : 1;
 #define CALL(KK) bwd_reg<float, KK>(vec, B, L, D, x, sxb, sxl, sxd, tail, weight, bias, gy, gx, gtail, gw, gb, part, s)
     TSF_CONV_K_SWITCH(K, CALL)
